@@ -1,0 +1,172 @@
+#!/usr/bin/env python3
+"""Headline benchmark: quantized CSR SpMM on one MI355X.
+
+Default workload = BASELINE.json configs[2] (the metric's "1M cells, N=64"): 4-bit packed
+quantized CSR, 1,000,000 cells x 33,538 genes, row nnz ~ LogNormal(mean 1,500, sigma 0.6),
+Zipf(1.1) gene popularity, per-gene scale/offset, fp16 W 33,538 x 64 ~ N(0, 0.02), fp32 Y.
+Inputs are generated seeded on the GPU and are resident in HBM before timing starts.
+
+One step = one cx_qcsr_spmm_fwd launch over the whole matrix. Prints ONE JSON line:
+metric/value (nnz/s), ms_per_step, roofline of the kernel (achieved algorithmic GB/s from
+HIP events on the launch stream vs 8 TB/s), and the CPU baseline (the oracle's row-parallel
+fp32 restatement timed on this host on a bounded row sample).
+
+  python bench.py [--steps K] [--warmup W] [--config c3|c3n128|c2|c4|c5] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def host_cores() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def time_launches(torch, launch, steps: int, warmup: int, stream):
+    """Runs `launch` warmup + steps times on `stream`; returns (wall ms/step, event ms list)."""
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        launch()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    ev = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return wall_ms, ev
+
+
+def cpu_baseline_qcsr(m, w, sample_rows: int, threads: int) -> dict:
+    import numpy as np
+
+    from oracle import pyoracle
+
+    pyoracle.build()
+    rows = min(sample_rows, m.rows)
+    # download only the sampled rows' slices
+    rp = m.row_ptr[: rows + 1].cpu().numpy()
+    nnz = int(rp[-1])
+    prp = m.packed_row_ptr[: rows + 1].cpu().numpy()
+    cols = m.col_idx[:nnz].cpu().numpy()
+    packed = m.packed_values[: int(prp[-1]) + 16].cpu().numpy()
+    scales = m.column_scales.cpu().numpy()
+    offsets = m.column_offsets.cpu().numpy()
+    wn = w.cpu().numpy()
+    args = (m.bits, m.decode_policy, rows, m.cols, rp, prp, cols, packed, scales, offsets, None, wn)
+    pyoracle.qcsr_spmm_f32_mt(*args, threads=threads)  # warm caches / page-in
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        pyoracle.qcsr_spmm_f32_mt(*args, threads=threads)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": nnz / t, "unit": "nnz/s", "cores": threads, "kind": "port",
+            "sample": f"first {rows} of {m.rows} rows ({nnz} nnz), median of 3 after 1 warmup; "
+                      f"oracle or_qcsr_spmm_f32_mt (decode + fp32 FMA, AVX2, row-parallel)",
+            "seconds": t}
+
+
+def bench_qcsr(args, torch, cfg, n_out: int) -> dict:
+    from cellerator_amd import qcsr_spmm
+    from cellerator_amd.synth import dense_normal, generate_qcsr
+
+    t0 = time.perf_counter()
+    m = generate_qcsr(cfg)
+    w = dense_normal((m.cols, n_out), 0.02, torch.float16, seed=cfg.seed + n_out)
+    out = torch.empty((m.rows, n_out), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    log(f"generated {cfg.name}: nnz={m.nnz} in {time.perf_counter() - t0:.1f}s")
+    stream = torch.cuda.current_stream()
+
+    def launch():
+        qcsr_spmm(m, w, out=out, stream=stream)
+
+    wall_ms, ev = time_launches(torch, launch, args.steps, args.warmup, stream)
+    kern_ms = statistics.mean(ev)
+    alg_bytes = m.nbytes_algorithmic(n_out, 2)
+    achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
+    flops = 2.0 * m.nnz * n_out
+    res = {
+        "metric": "quantized CSR SpMM nnz/s + effective HBM GB/s (% roofline), 1M cells, N=64",
+        "value": m.nnz / (wall_ms * 1e-3),
+        "unit": "nnz/s",
+        "ms_per_step": wall_ms,
+        "dtype": f"u{m.bits}-codes/f16-W/f32-accumulate" if m.bits else "f32",
+        "config": {"workload": cfg.name, "rows": m.rows, "genes": m.cols, "nnz": m.nnz,
+                   "bits": m.bits, "n_out": n_out, "rhs": "fp16",
+                   "nnz_per_row_mean": m.nnz / m.rows, "seed": hex(cfg.seed)},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "qcsr_spmm_rowwave", "kernel_ms_mean": kern_ms,
+                     "kernel_ms_median": statistics.median(ev),
+                     "algorithmic_bytes": alg_bytes,
+                     "fp32_fma_tflops": flops / (kern_ms * 1e-3) / 1e12,
+                     "valu_fp32_peak_tflops_nonpacked": 78.6},
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline_qcsr(m, w, args.cpu_rows, host_cores())
+    return res
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c3", choices=["c3", "c3n128", "c2"])
+    ap.add_argument("--rows", type=int, default=0, help="override the row count (smaller runs)")
+    ap.add_argument("--cpu-rows", type=int, default=100_000)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: every box in this build has one MI355X and the "
+              "projection shards by rows with no exchange (see DESIGN.md); run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    from cellerator_amd.synth import C2, C3
+
+    cfg, n_out = {"c3": (C3, 64), "c3n128": (C3, 128), "c2": (C2, 64)}[args.config]
+    if args.rows:
+        cfg = cfg.scaled(args.rows)
+    res = bench_qcsr(args, torch, cfg, n_out)
+    line = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"),
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": res.pop("ms_per_step"), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": res.pop("dtype"), "data": "synthetic (seeded, generated on GPU)",
+            **res}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

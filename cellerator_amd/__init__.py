@@ -1,0 +1,12 @@
+"""MI355X-native engine for Cellerator's sparse expression-matrix projection hot path.
+
+Hand-written gfx950 HIP kernels behind a C-ABI (include/cellerator_amd.h):
+quantized CSR SpMM, Blocked-ELL SpMM on bf16 MFMA, and the CP-BP warp-tile
+feature-weighted row reduction. This package is the Python host mirror of that ABI;
+PyTorch supplies device memory and streams only.
+"""
+from .engine import (BellMatrix, CpbpTiles, QcsrMatrix, bell_pack_rhs, bell_spmm,  # noqa: F401
+                     bell_spmm_packed, cpbp_reduce, csr_spmv, qcsr_spmm)
+
+__all__ = ["QcsrMatrix", "BellMatrix", "CpbpTiles", "qcsr_spmm", "bell_spmm", "bell_pack_rhs",
+           "bell_spmm_packed", "cpbp_reduce", "csr_spmv"]

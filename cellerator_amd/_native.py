@@ -1,0 +1,171 @@
+"""ctypes bindings of the engine's C-ABI (include/cellerator_amd.h) and of the synthetic
+input library (include/cellerator_amd_synth.h).
+
+The libraries are built in-tree by ``cellerator_amd.build`` (``__graft_entry__.build()``).
+Loading fails loudly when a library is missing: there is no CPU fallback for any
+operation of the engine.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ENGINE_PATH = PKG / "libcellerator_amd.so"
+SYNTH_PATH = PKG / "libcx_synth.so"
+
+# cellerator_dtype (include/cellerator_amd.h)
+DTYPE_F16, DTYPE_F32, DTYPE_U8, DTYPE_U32, DTYPE_BF16 = 1, 2, 3, 4, 5
+DECODE_PER_GENE_AFFINE, DECODE_COLUMN_SCALE_ROW_OFFSET = 1, 2
+STATUS_NAMES = {0: "SUCCESS", 1: "INVALID_ARGUMENT", 2: "INVALID_SHAPE", 3: "UNSUPPORTED",
+                4: "HIP_ERROR", 5: "INTERNAL_ERROR"}
+
+p_void = C.c_void_p
+u32, u64, i32, i64 = C.c_uint32, C.c_uint64, C.c_int32, C.c_int64
+
+
+class CxQcsrMatrix(C.Structure):
+    _fields_ = [
+        ("rows", u32), ("cols", u32), ("nnz", u64), ("bits", u32), ("decode_policy", u32),
+        ("row_ptr", p_void), ("packed_row_ptr", p_void), ("col_idx", p_void),
+        ("packed_values", p_void), ("column_scales", p_void), ("column_offsets", p_void),
+        ("row_offsets", p_void), ("values", p_void), ("value_dtype", u32), ("reserved", u32),
+    ]
+
+
+class CxBellMatrix(C.Structure):
+    _fields_ = [
+        ("rows", u32), ("cols", u32), ("block_size", u32), ("ell_cols", u32),
+        ("block_col_idx", p_void), ("values", p_void), ("value_dtype", u32), ("bits", u32),
+        ("decode_policy", u32), ("row_stride_bytes", u32), ("packed_values", p_void),
+        ("column_scales", p_void), ("column_offsets", p_void), ("row_offsets", p_void),
+    ]
+
+
+class CxCpbpTiles(C.Structure):
+    _fields_ = [
+        ("row_count", u32), ("feature_count", u32), ("feature_block_count", u32),
+        ("tile_row_width", u32), ("tile_count", u32), ("tile_block_count", u32),
+        ("row_block_entry_count", u32), ("nnz_count", u32), ("value_dtype", u32),
+        ("reserved", u32),
+        ("feature_block_offsets", p_void), ("feature_permutation", p_void),
+        ("tile_block_offsets", p_void), ("tile_block_ids", p_void),
+        ("tile_block_cell_masks", p_void), ("block_row_entry_offsets", p_void),
+        ("row_block_gene_masks", p_void), ("row_block_value_offsets", p_void),
+        ("values", p_void), ("row_permutation", p_void),
+    ]
+
+
+class CxsQcsrParams(C.Structure):
+    _fields_ = [
+        ("seed", u64), ("rows", u32), ("cols", u32), ("row_dist", u32), ("bits", u32),
+        ("nnz_mean", C.c_double), ("nnz_sigma", C.c_double), ("nnz_min", u32),
+        ("nnz_max", u32), ("zipf_s", C.c_double), ("nb_mean", C.c_double),
+        ("nb_size", C.c_double),
+    ]
+
+
+# ---- public context ABI structs (include/Cellerator/abi.h layout) ----
+class CelleratorExecutionConfig(C.Structure):
+    _fields_ = [("version", u32), ("size", C.c_size_t), ("device", i32), ("stream", p_void),
+                ("scratch", p_void), ("scratch_bytes", C.c_size_t)]
+
+
+class CelleratorTensorDesc(C.Structure):
+    _fields_ = [("version", u32), ("size", C.c_size_t), ("data", p_void), ("dtype", C.c_int),
+                ("rank", u32), ("shape", u64 * 4), ("stride", i64 * 4)]
+
+
+class CelleratorSparseLayoutDesc(C.Structure):
+    _fields_ = [
+        ("version", u32), ("size", C.c_size_t), ("layout", C.c_int), ("rows", u32),
+        ("cols", u32), ("nnz", u32), ("block_size", u32), ("ell_cols", u32),
+        ("row_stride_bytes", u32), ("bits", u32), ("decode_policy", u32),
+        ("value_dtype", C.c_int), ("major_ptr", p_void), ("minor_idx", p_void),
+        ("block_col_idx", p_void), ("values", p_void), ("packed_values", p_void),
+        ("column_scales", p_void), ("column_offsets", p_void), ("row_offsets", p_void),
+    ]
+
+
+# Every symbol include/cellerator_amd.h declares, with its ctypes signature.
+ENGINE_SIGNATURES = {
+    "cx_qcsr_spmm_fwd": (C.c_int, [C.POINTER(CxQcsrMatrix), p_void, u32, i64, i64, p_void, i64, p_void]),
+    "cx_bell_spmm_fwd": (C.c_int, [C.POINTER(CxBellMatrix), p_void, u32, i64, i64, p_void, i64, p_void]),
+    "cx_bell_pack_rhs": (C.c_int, [p_void, i64, u32, u32, p_void, p_void]),
+    "cx_bell_spmm_fwd_packed": (C.c_int, [C.POINTER(CxBellMatrix), p_void, i64, p_void, i64, p_void]),
+    "cx_cpbp_reduce": (C.c_int, [C.POINTER(CxCpbpTiles), p_void, u64, p_void, u64, p_void]),
+    "cx_csr_spmv_fwd": (C.c_int, [u32, p_void, p_void, p_void, u32, p_void, p_void, p_void]),
+    "cx_last_error": (C.c_char_p, []),
+    "cx_build_info": (C.c_char_p, []),
+    "cellerator_status_string": (C.c_char_p, [C.c_int]),
+    "cellerator_last_error": (C.c_char_p, []),
+    "cellerator_context_create": (C.c_int, [C.POINTER(CelleratorExecutionConfig), C.POINTER(p_void)]),
+    "cellerator_context_synchronize": (C.c_int, [p_void]),
+    "cellerator_context_destroy": (None, [p_void]),
+    "cellerator_saved_state_destroy": (None, [p_void]),
+    "cellerator_sparse_projection_forward": (
+        C.c_int, [p_void, C.POINTER(CelleratorSparseLayoutDesc), C.POINTER(CelleratorTensorDesc),
+                  C.POINTER(CelleratorTensorDesc), C.POINTER(p_void)]),
+}
+
+SYNTH_SIGNATURES = {
+    "cxs_qcsr_create": (C.c_int, [C.POINTER(CxsQcsrParams), C.POINTER(p_void)]),
+    "cxs_destroy": (None, [p_void]),
+    "cxs_qcsr_count": (C.c_int, [p_void, p_void, p_void]),
+    "cxs_qcsr_fill": (C.c_int, [p_void, p_void, p_void, p_void, p_void, p_void]),
+    "cxs_qcsr_calibrate": (C.c_int, [p_void, p_void, p_void, p_void, p_void, p_void]),
+    "cxs_qcsr_encode": (C.c_int, [p_void, p_void, p_void, p_void, p_void, p_void, p_void, p_void,
+                                  p_void]),
+    "cxs_dense_normal": (C.c_int, [u64, u64, C.c_float, u32, p_void, p_void]),
+    "cxs_bell_generate": (C.c_int, [u64, u32, u32, u32, u32, u32, u32, u32, C.c_float, C.c_double,
+                                    C.c_double, p_void, p_void, p_void]),
+    "cxs_last_error": (C.c_char_p, []),
+}
+
+_engine = None
+_synth = None
+
+
+class EngineError(RuntimeError):
+    """A C-ABI entry point returned a non-success status."""
+
+    def __init__(self, name: str, status: int, message: str):
+        super().__init__(f"{name} -> {STATUS_NAMES.get(status, status)}: {message}")
+        self.status = status
+
+
+def _bind(path: Path, signatures: dict) -> C.CDLL:
+    if not path.exists():
+        raise ImportError(
+            f"{path.name} is not built; run __graft_entry__.build() (python -m cellerator_amd.build)")
+    lib = C.CDLL(str(path))
+    for name, (res, args) in signatures.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def engine() -> C.CDLL:
+    global _engine
+    if _engine is None:
+        _engine = _bind(ENGINE_PATH, ENGINE_SIGNATURES)
+    return _engine
+
+
+def synth() -> C.CDLL:
+    global _synth
+    if _synth is None:
+        _synth = _bind(SYNTH_PATH, SYNTH_SIGNATURES)
+    return _synth
+
+
+def check(name: str, status: int) -> None:
+    if status != 0:
+        msg = engine().cx_last_error().decode()
+        raise EngineError(name, status, msg)
+
+
+def check_synth(name: str, status: int) -> None:
+    if status != 0:
+        raise RuntimeError(f"{name}: {synth().cxs_last_error().decode()}")

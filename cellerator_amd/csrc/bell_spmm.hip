@@ -1,0 +1,301 @@
+// bell_spmm.hip -- Blocked-ELL SpMM on gfx950.
+//
+// MFMA path (bf16 values, bf16 weights, 32x32 blocks, N a multiple of 64):
+//   * the weight panel is packed once per weight generation (cx_bell_pack_rhs) from
+//     row-major K x N into [K/32][N][32]: for every 32-gene block column and output
+//     column the 32 gene weights are contiguous, which is the K-contiguous operand form
+//     the matrix cores read (the role of the reference's packed dense operand,
+//     src/compute/math/packed_dense_operand.cu:131-260);
+//   * one workgroup owns one 32-row block; wave w owns output columns [64w, 64w+64)
+//     as two 32x32 fp32 accumulator tiles;
+//   * per valid ELL slot each lane loads its 16-byte A fragment (8 bf16 of one row of
+//     the 32x32 value block) and 16-byte B fragments straight from the packed panel,
+//     and issues v_mfma_f32_32x32x16_bf16 (two K steps of 16 per block); empty slots
+//     (0xffffffff) are skipped without touching their values;
+//   * row blocks are visited in an XCD-major order so consecutive row blocks of the
+//     schedule share one XCD's L2 (the weight panel is re-read from L2, not HBM).
+// Generic path (any other dtype / block size / N, quantized BELL): one wave per row,
+// lanes over output columns, slots in order, decoded with the codec exactly as
+// quantized_blocked_ell_spmm_fwd_kernel_ does
+// (src/compute/sparse/project/kernels/quantized_blocked_ell_spmm_fwd_kernel_.cuh:1-39).
+#include "cx_common.hpp"
+
+typedef __bf16 cx_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float cx_floatx16 __attribute__((ext_vector_type(16)));
+
+namespace cx {
+namespace {
+
+constexpr std::uint32_t kInvalidBlock = 0xffffffffu;
+
+struct BellArgs {
+    const std::uint32_t *block_col_idx;
+    const void *values;
+    const std::uint8_t *packed;
+    const float *scales;
+    const float *offsets;
+    const float *row_offsets;
+    const void *rhs;
+    std::int64_t rhs_ld;
+    float *out;
+    std::int64_t out_ld;
+    std::uint32_t rows;
+    std::uint32_t cols;
+    std::uint32_t block_size;
+    std::uint32_t ell_cols;
+    std::uint32_t row_stride_bytes;
+};
+
+// Row block handled by workgroup `wg` of `count`: XCD-major so that the row blocks a
+// single XCD processes are contiguous in the matrix (dispatch places wg on XCD wg % 8).
+__device__ __forceinline__ std::uint32_t xcd_major(std::uint32_t wg, std::uint32_t count) {
+    constexpr std::uint32_t kXcds = 8;
+    const std::uint32_t per = count / kXcds;
+    const std::uint32_t full = per * kXcds;
+    if (wg >= full) return wg; // ragged tail keeps its natural index
+    return (wg % kXcds) * per + wg / kXcds;
+}
+
+template<int kN>
+__global__ __launch_bounds__(kN) void bell_spmm_mfma(BellArgs a, const std::uint16_t *packed_rhs) {
+    constexpr int kTilesPerWave = 2; // 64 output columns per wave
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    const std::uint32_t row_blocks = (a.rows + 31u) / 32u;
+    const std::uint32_t rb = xcd_major(blockIdx.x, gridDim.x);
+    if (rb >= row_blocks) return;
+    const std::uint32_t width = a.ell_cols / 32u;
+    const std::uint32_t *slots = a.block_col_idx + static_cast<std::uint64_t>(rb) * width;
+
+    const int m = lane % 32;         // A row / B,D column within the tile
+    const int kq = (lane / 32) * 8;  // first K element of this lane's fragment
+    const std::uint32_t row = rb * 32u + static_cast<std::uint32_t>(m);
+    const bool row_ok = row < a.rows;
+    const std::uint16_t *arow = static_cast<const std::uint16_t *>(a.values)
+        + static_cast<std::uint64_t>(row_ok ? row : 0u) * a.ell_cols + kq;
+    const int n0 = wave * 64;
+
+    cx_floatx16 acc[kTilesPerWave];
+#pragma unroll
+    for (int t = 0; t < kTilesPerWave; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
+
+    for (std::uint32_t s = 0; s < width; ++s) {
+        const std::uint32_t bc = slots[s];
+        if (bc == kInvalidBlock) continue;
+        cx_bf16x8 afrag[2];
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+            uint4 raw = make_uint4(0u, 0u, 0u, 0u);
+            if (row_ok) raw = *reinterpret_cast<const uint4 *>(arow + s * 32u + kc * 16);
+            __builtin_memcpy(&afrag[kc], &raw, 16);
+        }
+        const std::uint16_t *panel = packed_rhs + static_cast<std::uint64_t>(bc) * kN * 32;
+#pragma unroll
+        for (int t = 0; t < kTilesPerWave; ++t) {
+            const std::uint16_t *bcol = panel + static_cast<std::uint64_t>(n0 + t * 32 + m) * 32 + kq;
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc) {
+                const uint4 raw = *reinterpret_cast<const uint4 *>(bcol + kc * 16);
+                cx_bf16x8 bfrag;
+                __builtin_memcpy(&bfrag, &raw, 16);
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afrag[kc], bfrag, acc[t], 0, 0, 0);
+            }
+        }
+    }
+
+    // D layout: lane holds column (lane % 32); element i is row 8*(i/4) + 4*(lane/32) + i%4.
+#pragma unroll
+    for (int t = 0; t < kTilesPerWave; ++t) {
+        const int col = n0 + t * 32 + m;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const std::uint32_t r = rb * 32u + 8u * (i / 4) + 4u * (lane / 32) + (i % 4);
+            if (r < a.rows) a.out[static_cast<std::int64_t>(r) * a.out_ld + col] = acc[t][i];
+        }
+    }
+}
+
+__global__ void pack_rhs_kernel(const std::uint16_t *rhs, std::int64_t rhs_ld, std::uint32_t k,
+                                std::uint32_t n, std::uint16_t *packed) {
+    // one thread per packed element: (kb, col, kk)
+    const std::uint64_t idx = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x;
+    const std::uint32_t kblocks = (k + 31u) / 32u;
+    const std::uint64_t total = static_cast<std::uint64_t>(kblocks) * n * 32u;
+    if (idx >= total) return;
+    const std::uint32_t kk = static_cast<std::uint32_t>(idx % 32u);
+    const std::uint32_t col = static_cast<std::uint32_t>((idx / 32u) % n);
+    const std::uint32_t kb = static_cast<std::uint32_t>(idx / (32ull * n));
+    const std::uint32_t gene = kb * 32u + kk;
+    packed[idx] = gene < k ? rhs[static_cast<std::int64_t>(gene) * rhs_ld + col] : 0;
+}
+
+template<typename T>
+__device__ __forceinline__ float load_as_float(const void *p, std::uint64_t i, std::uint32_t dtype) {
+    if (dtype == CELLERATOR_DTYPE_F32) return static_cast<const float *>(p)[i];
+    const std::uint16_t bits = static_cast<const std::uint16_t *>(p)[i];
+    return dtype == CELLERATOR_DTYPE_BF16 ? bf2f(bits) : h2f(bits);
+}
+
+// Reference-semantics kernel: row per wave, lanes over output columns, slots in order.
+__global__ __launch_bounds__(256) void bell_spmm_generic(BellArgs a, std::uint32_t value_dtype,
+                                                         std::uint32_t rhs_dtype, std::uint32_t bits,
+                                                         std::uint32_t policy, std::int64_t n) {
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const std::uint32_t row = (blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+    if (row >= a.rows) return;
+    const std::uint32_t bs = a.block_size;
+    const std::uint32_t width = a.ell_cols / bs;
+    const std::uint32_t rb = row / bs;
+    const float row_offset = (bits != 0u && policy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET
+                              && a.row_offsets != nullptr) ? a.row_offsets[row] : 0.0f;
+    for (std::int64_t c0 = 0; c0 < n; c0 += kWave) {
+        const std::int64_t c = c0 + lane;
+        float acc = 0.0f;
+        for (std::uint32_t s = 0; s < width; ++s) {
+            const std::uint32_t bc = a.block_col_idx[static_cast<std::uint64_t>(rb) * width + s];
+            if (bc == kInvalidBlock) continue;
+            for (std::uint32_t kk = 0; kk < bs; ++kk) {
+                const std::uint64_t col = static_cast<std::uint64_t>(bc) * bs + kk;
+                if (col >= a.cols) break;
+                const std::uint32_t slot = s * bs + kk;
+                float x;
+                if (bits != 0u) {
+                    const std::uint32_t cpb = 8u / bits;
+                    const std::uint8_t byte = a.packed[static_cast<std::uint64_t>(row) * a.row_stride_bytes
+                                                       + slot / cpb];
+                    const std::uint32_t code = (byte >> ((slot % cpb) * bits)) & ((1u << bits) - 1u);
+                    const float scale = a.scales != nullptr ? a.scales[col] : 1.0f;
+                    const float offset = policy == CX_DECODE_PER_GENE_AFFINE
+                        ? (a.offsets != nullptr ? a.offsets[col] : 0.0f)
+                        : row_offset;
+                    x = __builtin_fmaf(static_cast<float>(code), scale, offset);
+                } else {
+                    x = load_as_float<float>(a.values, static_cast<std::uint64_t>(row) * a.ell_cols + slot,
+                                             value_dtype);
+                }
+                if (c < n) {
+                    const float w = load_as_float<float>(a.rhs, col * a.rhs_ld + c, rhs_dtype);
+                    acc = __builtin_fmaf(x, w, acc);
+                }
+            }
+        }
+        if (c < n) a.out[static_cast<std::int64_t>(row) * a.out_ld + c] = acc;
+    }
+}
+
+int validate_bell(const cx_bell_matrix *m, const void *rhs, std::int64_t rhs_ld,
+                  std::int64_t out_cols, const float *out, std::int64_t out_ld) {
+    if (m == nullptr || rhs == nullptr || out == nullptr)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "Blocked-ELL: null matrix, rhs or output");
+    if (out_cols <= 0 || out_ld < out_cols || rhs_ld < out_cols)
+        return fail(CX_STATUS_INVALID_SHAPE, "Blocked-ELL: bad output columns or leading dimension");
+    if (m->block_size == 0u || m->ell_cols == 0u || m->ell_cols % m->block_size != 0u)
+        return fail(CX_STATUS_INVALID_SHAPE, "Blocked-ELL: ell_cols must be a positive multiple of block_size");
+    if (m->rows != 0u && m->block_col_idx == nullptr)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "Blocked-ELL: null block_col_idx");
+    if (m->bits != 0u) {
+        if (!(m->bits == 1u || m->bits == 2u || m->bits == 4u || m->bits == 8u))
+            return fail(CX_STATUS_UNSUPPORTED, "quantized Blocked-ELL bits must be 1, 2, 4 or 8");
+        if (m->row_stride_bytes == 0u || m->packed_values == nullptr)
+            return fail(CX_STATUS_INVALID_ARGUMENT, "quantized Blocked-ELL needs packed values and a row stride");
+        if (m->decode_policy == CX_DECODE_PER_GENE_AFFINE && m->column_scales == nullptr)
+            return fail(CX_STATUS_INVALID_ARGUMENT, "per-gene affine decode needs column scales");
+        if (m->decode_policy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET && m->row_offsets == nullptr)
+            return fail(CX_STATUS_INVALID_ARGUMENT, "column-scale/row-offset decode needs row offsets");
+        if (m->decode_policy != CX_DECODE_PER_GENE_AFFINE
+            && m->decode_policy != CX_DECODE_COLUMN_SCALE_ROW_OFFSET)
+            return fail(CX_STATUS_UNSUPPORTED, "unknown Blocked-ELL decode policy");
+    } else {
+        if (m->values == nullptr) return fail(CX_STATUS_INVALID_ARGUMENT, "Blocked-ELL: null values");
+        if (m->value_dtype != CELLERATOR_DTYPE_BF16 && m->value_dtype != CELLERATOR_DTYPE_F16
+            && m->value_dtype != CELLERATOR_DTYPE_F32)
+            return fail(CX_STATUS_UNSUPPORTED, "Blocked-ELL values must be BF16, F16 or F32");
+    }
+    return CX_STATUS_SUCCESS;
+}
+
+BellArgs make_args(const cx_bell_matrix *m, const void *rhs, std::int64_t rhs_ld, float *out,
+                   std::int64_t out_ld) {
+    BellArgs a{};
+    a.block_col_idx = m->block_col_idx;
+    a.values = m->values;
+    a.packed = m->packed_values;
+    a.scales = m->column_scales;
+    a.offsets = m->column_offsets;
+    a.row_offsets = m->row_offsets;
+    a.rhs = rhs;
+    a.rhs_ld = rhs_ld;
+    a.out = out;
+    a.out_ld = out_ld;
+    a.rows = m->rows;
+    a.cols = m->cols;
+    a.block_size = m->block_size;
+    a.ell_cols = m->ell_cols;
+    a.row_stride_bytes = m->row_stride_bytes;
+    return a;
+}
+
+} // namespace
+} // namespace cx
+
+extern "C" int cx_bell_spmm_fwd(const cx_bell_matrix *m, const void *rhs, uint32_t rhs_dtype,
+                                int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
+                                void *stream) {
+    using namespace cx;
+    clear_error();
+    int rc = validate_bell(m, rhs, rhs_ld, out_cols, out, out_ld);
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    if (rhs_dtype != CELLERATOR_DTYPE_F32 && rhs_dtype != CELLERATOR_DTYPE_F16
+        && rhs_dtype != CELLERATOR_DTYPE_BF16)
+        return fail(CX_STATUS_UNSUPPORTED, "Blocked-ELL rhs must be F32, F16 or BF16");
+    if (m->rows == 0u) return CX_STATUS_SUCCESS;
+    const BellArgs a = make_args(m, rhs, rhs_ld, out, out_ld);
+    const std::uint64_t threads = static_cast<std::uint64_t>(m->rows) * kWave;
+    hipLaunchKernelGGL(bell_spmm_generic, dim3(static_cast<unsigned>((threads + 255) / 256)),
+                       dim3(256), 0, static_cast<hipStream_t>(stream), a, m->value_dtype,
+                       rhs_dtype, m->bits, m->decode_policy, out_cols);
+    return check_launch("bell_spmm_generic");
+}
+
+extern "C" int cx_bell_pack_rhs(const uint16_t *rhs_bf16, int64_t rhs_ld, uint32_t k, uint32_t n,
+                                uint16_t *packed, void *stream) {
+    using namespace cx;
+    clear_error();
+    if (rhs_bf16 == nullptr || packed == nullptr)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_bell_pack_rhs: null rhs or packed output");
+    if (k == 0u || n == 0u || rhs_ld < static_cast<int64_t>(n))
+        return fail(CX_STATUS_INVALID_SHAPE, "cx_bell_pack_rhs: bad shape");
+    const std::uint64_t total = static_cast<std::uint64_t>((k + 31u) / 32u) * n * 32u;
+    hipLaunchKernelGGL(pack_rhs_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256),
+                       0, static_cast<hipStream_t>(stream), rhs_bf16, rhs_ld, k, n, packed);
+    return check_launch("cx_bell_pack_rhs");
+}
+
+extern "C" int cx_bell_spmm_fwd_packed(const cx_bell_matrix *m, const uint16_t *packed_rhs,
+                                       int64_t out_cols, float *out, int64_t out_ld,
+                                       void *stream) {
+    using namespace cx;
+    clear_error();
+    int rc = validate_bell(m, packed_rhs, out_cols, out_cols, out, out_ld);
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    if (m->bits != 0u || m->value_dtype != CELLERATOR_DTYPE_BF16 || m->block_size != 32u)
+        return fail(CX_STATUS_UNSUPPORTED,
+                    "MFMA Blocked-ELL needs unquantized BF16 values and 32x32 blocks");
+    if (out_cols != 64 && out_cols != 128 && out_cols != 256)
+        return fail(CX_STATUS_UNSUPPORTED, "MFMA Blocked-ELL supports 64, 128 or 256 output columns");
+    if ((reinterpret_cast<std::uintptr_t>(m->values) & 15u) != 0u
+        || (reinterpret_cast<std::uintptr_t>(packed_rhs) & 15u) != 0u)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "MFMA Blocked-ELL operands must be 16-byte aligned");
+    if (m->rows == 0u) return CX_STATUS_SUCCESS;
+    const BellArgs a = make_args(m, packed_rhs, out_cols, out, out_ld);
+    const unsigned row_blocks = (m->rows + 31u) / 32u;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (out_cols) {
+    case 64: hipLaunchKernelGGL(bell_spmm_mfma<64>, dim3(row_blocks), dim3(64), 0, s, a, packed_rhs); break;
+    case 128: hipLaunchKernelGGL(bell_spmm_mfma<128>, dim3(row_blocks), dim3(128), 0, s, a, packed_rhs); break;
+    default: hipLaunchKernelGGL(bell_spmm_mfma<256>, dim3(row_blocks), dim3(256), 0, s, a, packed_rhs); break;
+    }
+    return check_launch("bell_spmm_mfma");
+}

@@ -1,0 +1,321 @@
+// qcsr_spmm.hip -- quantized CSR SpMM on gfx950: Y = decode(X) . W, fp32 accumulate.
+//
+// Semantics (parity contract): each stored code is decoded exactly as the reference
+// codec does, value = fma(float(code), scale, offset) with one rounding
+// (include/Cellerator/quantized/access.cuh:81-91, numeric.cuh:34-36); the fp16 weight is
+// widened exactly; products and sums are fp32, as csr_spmm_fwd_kernel_ computes them
+// (src/compute/sparse/project/kernels/csr_spmm_fwd_kernel_.cuh:13-19) but in a fixed
+// per-row order of our own (partial sums per lane group, then a butterfly).
+//
+// Layout of the fast path ("row per wavefront, lanes over output columns"):
+//   * one wave64 owns one cell row;
+//   * the row's entries are streamed 64 at a time: lane i loads col_idx[i] and its
+//     code (coalesced), decodes it in registers with the per-gene scale/offset, and
+//     stages (gene, value) in LDS;
+//   * the wave then consumes the staged entries kEps at a time: lane group g takes
+//     entry s + g, each of its kLpe lanes loads 16 B of that gene's weight row
+//     (8 fp16 or 4 fp32 output columns) and issues fused multiply-adds
+//     (v_fma_mix_f32 for fp16 weights: widening folded into the FMA);
+//   * at the end of the row the kEps group partials are summed with a xor butterfly
+//     and group 0 writes the row's N outputs (one 16/32 B store per lane).
+// Any other shape (N not 32/64/128, unaligned operands) takes the generic kernel: one
+// wave per row, lanes over output columns, entries in nnz order.
+#include "cx_common.hpp"
+
+namespace cx {
+namespace {
+
+enum class ValueMode : int { quantized = 0, f16 = 1, f32 = 2 };
+
+struct QcsrArgs {
+    const std::int32_t *row_ptr;
+    const std::int32_t *packed_row_ptr;
+    const std::int32_t *col_idx;
+    const std::uint8_t *packed;
+    const float *scales;
+    const float *offsets;
+    const float *row_offsets;
+    const void *values;
+    const void *rhs;
+    std::int64_t rhs_ld;
+    float *out;
+    std::int64_t out_ld;
+    std::uint32_t rows;
+    std::uint32_t cols;
+};
+
+constexpr int kWavesPerBlock = 4;
+
+// Decoded value of entry `i` (global nnz index) of row `row` whose packed codes start
+// at `pbase`. Returns the gene through `col`.
+template<int kBits, int kPolicy, ValueMode kMode>
+__device__ __forceinline__ float load_entry(const QcsrArgs &a, std::int64_t i,
+                                            std::int64_t begin, const std::uint8_t *pbase,
+                                            float row_offset, int &col) {
+    col = a.col_idx[i];
+    if constexpr (kMode == ValueMode::quantized) {
+        constexpr int kCpb = 8 / kBits;
+        constexpr unsigned kMask = (1u << kBits) - 1u;
+        const std::int64_t local = i - begin;
+        const unsigned byte = pbase[local / kCpb];
+        const unsigned code = (byte >> (static_cast<unsigned>(local % kCpb) * kBits)) & kMask;
+        const float scale = a.scales != nullptr ? a.scales[col] : 1.0f;
+        const float offset = kPolicy == CX_DECODE_PER_GENE_AFFINE
+            ? (a.offsets != nullptr ? a.offsets[col] : 0.0f)
+            : row_offset;
+        return __builtin_fmaf(static_cast<float>(code), scale, offset);
+    } else if constexpr (kMode == ValueMode::f16) {
+        return h2f(static_cast<const std::uint16_t *>(a.values)[i]);
+    } else {
+        return static_cast<const float *>(a.values)[i];
+    }
+}
+
+template<typename RhsT, int kCpl>
+__device__ __forceinline__ void fma_row(float (&acc)[kCpl], float x, const RhsT *w) {
+    if constexpr (sizeof(RhsT) == 2) {
+        static_assert(kCpl == 8, "fp16 rows are read 16 B per lane");
+        const uint4 raw = *reinterpret_cast<const uint4 *>(w);
+        const unsigned words[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            acc[2 * k] = __builtin_fmaf(x, h2f(static_cast<std::uint16_t>(words[k] & 0xffffu)),
+                                        acc[2 * k]);
+            acc[2 * k + 1] = __builtin_fmaf(x, h2f(static_cast<std::uint16_t>(words[k] >> 16)),
+                                            acc[2 * k + 1]);
+        }
+    } else {
+        static_assert(kCpl == 4, "fp32 rows are read 16 B per lane");
+        const float4 v = *reinterpret_cast<const float4 *>(w);
+        acc[0] = __builtin_fmaf(x, v.x, acc[0]);
+        acc[1] = __builtin_fmaf(x, v.y, acc[1]);
+        acc[2] = __builtin_fmaf(x, v.z, acc[2]);
+        acc[3] = __builtin_fmaf(x, v.w, acc[3]);
+    }
+}
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+template<int kBits, int kPolicy, ValueMode kMode, typename RhsT, int kN>
+__global__ __launch_bounds__(kWave *kWavesPerBlock) void qcsr_spmm_rowwave(QcsrArgs a) {
+    constexpr int kCpl = 16 / static_cast<int>(sizeof(RhsT)); // output columns per lane
+    constexpr int kLpe = kN / kCpl;                           // lanes per entry
+    constexpr int kEps = kWave / kLpe;                        // entries per step
+    static_assert(kN % kCpl == 0 && kLpe <= kWave && kWave % kLpe == 0, "bad shape");
+
+    __shared__ int2 stage[kWavesPerBlock][kWave];
+
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const std::uint32_t row = blockIdx.x * kWavesPerBlock + wave;
+    if (row >= a.rows) return;
+
+    const int g = lane / kLpe;
+    const int j = lane % kLpe;
+    const std::int64_t begin = a.row_ptr[row];
+    const std::int64_t end = a.row_ptr[row + 1];
+    const std::uint8_t *pbase = nullptr;
+    float row_offset = 0.0f;
+    if constexpr (kMode == ValueMode::quantized) {
+        pbase = a.packed + a.packed_row_ptr[row];
+        if constexpr (kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET)
+            row_offset = a.row_offsets != nullptr ? a.row_offsets[row] : 0.0f;
+    }
+    const RhsT *rhs = static_cast<const RhsT *>(a.rhs) + j * kCpl;
+
+    float acc[kCpl];
+#pragma unroll
+    for (int k = 0; k < kCpl; ++k) acc[k] = 0.0f;
+
+    for (std::int64_t c0 = begin; c0 < end; c0 += kWave) {
+        const std::int64_t i = c0 + lane;
+        int col = 0;
+        float x = 0.0f;
+        if (i < end) x = load_entry<kBits, kPolicy, kMode>(a, i, begin, pbase, row_offset, col);
+        stage[wave][lane] = make_int2(col, __float_as_int(x));
+        wave_sync();
+        const int count = end - c0 < kWave ? static_cast<int>(end - c0) : kWave;
+        if (count == kWave) {
+#pragma unroll
+            for (int s = 0; s < kWave; s += kEps) {
+                const int2 e = stage[wave][s + g];
+                fma_row<RhsT, kCpl>(acc, __int_as_float(e.y),
+                                    rhs + static_cast<std::int64_t>(e.x) * a.rhs_ld);
+            }
+        } else {
+            for (int s = 0; s < count; s += kEps) {
+                if (s + g < count) {
+                    const int2 e = stage[wave][s + g];
+                    fma_row<RhsT, kCpl>(acc, __int_as_float(e.y),
+                                        rhs + static_cast<std::int64_t>(e.x) * a.rhs_ld);
+                }
+            }
+        }
+        wave_sync();
+    }
+
+    // Sum the kEps group partials: lanes of equal j differ in the bits above log2(kLpe).
+    constexpr int kFirstBit = __builtin_ctz(kLpe);
+#pragma unroll
+    for (int k = 0; k < kCpl; ++k) {
+        if constexpr (kFirstBit < 6) acc[k] = xor_reduce<kFirstBit, 5>(acc[k]);
+    }
+    if (g == 0) {
+        float *dst = a.out + static_cast<std::int64_t>(row) * a.out_ld + j * kCpl;
+#pragma unroll
+        for (int k = 0; k < kCpl; k += 4)
+            *reinterpret_cast<float4 *>(dst + k) = make_float4(acc[k], acc[k + 1], acc[k + 2],
+                                                               acc[k + 3]);
+    }
+}
+
+// Generic shape: one wave per row, lanes over output columns in chunks of 64, entries
+// consumed in nnz order (wave-uniform decode).
+template<int kBits, int kPolicy, ValueMode kMode, typename RhsT>
+__global__ __launch_bounds__(kWave *kWavesPerBlock) void qcsr_spmm_generic(QcsrArgs a,
+                                                                           std::int64_t n) {
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const std::uint32_t row = blockIdx.x * kWavesPerBlock + wave;
+    if (row >= a.rows) return;
+    const std::int64_t begin = a.row_ptr[row];
+    const std::int64_t end = a.row_ptr[row + 1];
+    const std::uint8_t *pbase = nullptr;
+    float row_offset = 0.0f;
+    if constexpr (kMode == ValueMode::quantized) {
+        pbase = a.packed + a.packed_row_ptr[row];
+        if constexpr (kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET)
+            row_offset = a.row_offsets != nullptr ? a.row_offsets[row] : 0.0f;
+    }
+    const RhsT *rhs = static_cast<const RhsT *>(a.rhs);
+    for (std::int64_t c0 = 0; c0 < n; c0 += kWave) {
+        const std::int64_t c = c0 + lane;
+        float acc = 0.0f;
+        for (std::int64_t i = begin; i < end; ++i) {
+            int col = 0;
+            const float x = load_entry<kBits, kPolicy, kMode>(a, i, begin, pbase, row_offset, col);
+            if (c < n) {
+                const RhsT w = rhs[static_cast<std::int64_t>(col) * a.rhs_ld + c];
+                float wf;
+                if constexpr (sizeof(RhsT) == 2) wf = h2f(w);
+                else wf = w;
+                acc = __builtin_fmaf(x, wf, acc);
+            }
+        }
+        if (c < n) a.out[static_cast<std::int64_t>(row) * a.out_ld + c] = acc;
+    }
+}
+
+template<int kBits, int kPolicy, ValueMode kMode, typename RhsT>
+int launch_rhs(const QcsrArgs &a, std::int64_t n, bool aligned, hipStream_t stream) {
+    const unsigned blocks = (a.rows + kWavesPerBlock - 1) / kWavesPerBlock;
+    const dim3 grid(blocks), block(kWave * kWavesPerBlock);
+    constexpr int kCpl = 16 / static_cast<int>(sizeof(RhsT));
+    if (aligned && n == 64) {
+        hipLaunchKernelGGL((qcsr_spmm_rowwave<kBits, kPolicy, kMode, RhsT, 64>), grid, block, 0,
+                           stream, a);
+    } else if (aligned && n == 128) {
+        hipLaunchKernelGGL((qcsr_spmm_rowwave<kBits, kPolicy, kMode, RhsT, 128>), grid, block, 0,
+                           stream, a);
+    } else if (aligned && n == 32 && kCpl == 8) {
+        hipLaunchKernelGGL((qcsr_spmm_rowwave<kBits, kPolicy, kMode, RhsT, 32>), grid, block, 0,
+                           stream, a);
+    } else {
+        hipLaunchKernelGGL((qcsr_spmm_generic<kBits, kPolicy, kMode, RhsT>), grid, block, 0,
+                           stream, a, n);
+    }
+    return check_launch("qcsr_spmm");
+}
+
+template<int kBits, int kPolicy, ValueMode kMode>
+int launch_mode(const QcsrArgs &a, std::uint32_t rhs_dtype, std::int64_t n, bool aligned,
+                hipStream_t stream) {
+    if (rhs_dtype == CELLERATOR_DTYPE_F16)
+        return launch_rhs<kBits, kPolicy, kMode, std::uint16_t>(a, n, aligned, stream);
+    return launch_rhs<kBits, kPolicy, kMode, float>(a, n, aligned, stream);
+}
+
+template<int kPolicy>
+int launch_bits(const QcsrArgs &a, std::uint32_t bits, std::uint32_t rhs_dtype, std::int64_t n,
+                bool aligned, hipStream_t stream) {
+    switch (bits) {
+    case 1: return launch_mode<1, kPolicy, ValueMode::quantized>(a, rhs_dtype, n, aligned, stream);
+    case 2: return launch_mode<2, kPolicy, ValueMode::quantized>(a, rhs_dtype, n, aligned, stream);
+    case 4: return launch_mode<4, kPolicy, ValueMode::quantized>(a, rhs_dtype, n, aligned, stream);
+    case 8: return launch_mode<8, kPolicy, ValueMode::quantized>(a, rhs_dtype, n, aligned, stream);
+    default: return fail(CX_STATUS_UNSUPPORTED, "quantized CSR bits must be 1, 2, 4 or 8");
+    }
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0u; }
+
+} // namespace
+} // namespace cx
+
+extern "C" int cx_qcsr_spmm_fwd(const cx_qcsr_matrix *m, const void *rhs, uint32_t rhs_dtype,
+                                int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
+                                void *stream) {
+    using namespace cx;
+    clear_error();
+    if (m == nullptr || out == nullptr || rhs == nullptr)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd: null matrix, rhs or output");
+    if (rhs_dtype != CELLERATOR_DTYPE_F16 && rhs_dtype != CELLERATOR_DTYPE_F32)
+        return fail(CX_STATUS_UNSUPPORTED, "cx_qcsr_spmm_fwd: rhs dtype must be F16 or F32");
+    if (out_cols <= 0 || rhs_ld < out_cols || out_ld < out_cols)
+        return fail(CX_STATUS_INVALID_SHAPE,
+                    "cx_qcsr_spmm_fwd: out_cols must be positive and <= both leading dimensions");
+    if (m->rows == 0u) return CX_STATUS_SUCCESS;
+    if (m->row_ptr == nullptr || (m->nnz != 0u && m->col_idx == nullptr))
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd: null row_ptr or col_idx");
+    if (m->nnz > static_cast<std::uint64_t>(INT32_MAX))
+        return fail(CX_STATUS_INVALID_SHAPE, "cx_qcsr_spmm_fwd: nnz exceeds int32 row offsets");
+    if (m->bits != 0u) {
+        if (m->packed_row_ptr == nullptr || (m->nnz != 0u && m->packed_values == nullptr))
+            return fail(CX_STATUS_INVALID_ARGUMENT,
+                        "cx_qcsr_spmm_fwd: quantized matrix needs packed_row_ptr and packed_values");
+        if (m->decode_policy != CX_DECODE_PER_GENE_AFFINE
+            && m->decode_policy != CX_DECODE_COLUMN_SCALE_ROW_OFFSET)
+            return fail(CX_STATUS_UNSUPPORTED, "cx_qcsr_spmm_fwd: unknown decode policy");
+    } else {
+        if (m->nnz != 0u && m->values == nullptr)
+            return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd: null values");
+        if (m->value_dtype != CELLERATOR_DTYPE_F16 && m->value_dtype != CELLERATOR_DTYPE_F32)
+            return fail(CX_STATUS_UNSUPPORTED, "cx_qcsr_spmm_fwd: value dtype must be F16 or F32");
+    }
+    if (static_cast<const void *>(out) == rhs)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd: output aliases the rhs");
+
+    QcsrArgs a{};
+    a.row_ptr = m->row_ptr;
+    a.packed_row_ptr = m->packed_row_ptr;
+    a.col_idx = m->col_idx;
+    a.packed = m->packed_values;
+    a.scales = m->column_scales;
+    a.offsets = m->column_offsets;
+    a.row_offsets = m->row_offsets;
+    a.values = m->values;
+    a.rhs = rhs;
+    a.rhs_ld = rhs_ld;
+    a.out = out;
+    a.out_ld = out_ld;
+    a.rows = m->rows;
+    a.cols = m->cols;
+    const std::size_t esize = rhs_dtype == CELLERATOR_DTYPE_F16 ? 2u : 4u;
+    const bool aligned = aligned16(rhs) && aligned16(out) && (rhs_ld * esize) % 16 == 0
+        && (out_ld * 4) % 16 == 0;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (m->bits == 0u) {
+        if (m->value_dtype == CELLERATOR_DTYPE_F16)
+            return launch_mode<0, CX_DECODE_PER_GENE_AFFINE, ValueMode::f16>(a, rhs_dtype,
+                                                                               out_cols, aligned, s);
+        return launch_mode<0, CX_DECODE_PER_GENE_AFFINE, ValueMode::f32>(a, rhs_dtype, out_cols,
+                                                                          aligned, s);
+    }
+    if (m->decode_policy == CX_DECODE_PER_GENE_AFFINE)
+        return launch_bits<CX_DECODE_PER_GENE_AFFINE>(a, m->bits, rhs_dtype, out_cols, aligned, s);
+    return launch_bits<CX_DECODE_COLUMN_SCALE_ROW_OFFSET>(a, m->bits, rhs_dtype, out_cols, aligned,
+                                                          s);
+}

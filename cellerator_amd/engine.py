@@ -1,0 +1,240 @@
+"""Python host mirror of the engine's launch layer: device-resident matrix containers
+and one function per C-ABI entry point. PyTorch only provides device memory and
+streams; every operation runs the HIP kernels of libcellerator_amd.so.
+
+Containers mirror the reference's types:
+  QcsrMatrix -- cellerator::quantized::csr_matrix (include/Cellerator/quantized/layout.cuh:12-39)
+  BellMatrix -- cellerator::quantized::blocked_ell::matrix (quantized/blocked_ell.cuh:18-35)
+                and the plain Blocked-ELL of blocked_ell_spmm_fwd_f16_f32
+  CpbpTiles  -- cellpack::warp_tile_view + feature_weighted_row_reduction_plan_view
+                (components/CellPack/include/CellPack/warp_tiles.hh:41-79,
+                 feature_weighted_row_reduction.hh:16-26)
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+
+from . import _native as N
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream) -> int:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+
+
+def _require_cuda(*tensors: Optional[torch.Tensor]) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("engine operands must be device tensors")
+
+
+_DTYPE_CODE = {torch.float16: N.DTYPE_F16, torch.float32: N.DTYPE_F32, torch.bfloat16: N.DTYPE_BF16}
+
+
+@dataclass
+class QcsrMatrix:
+    rows: int
+    cols: int
+    bits: int  # 1, 2, 4, 8; 0 = unquantized `values`
+    row_ptr: torch.Tensor  # int32 [rows + 1]
+    col_idx: torch.Tensor  # int32 [nnz]
+    packed_row_ptr: Optional[torch.Tensor] = None  # int32 [rows + 1]
+    packed_values: Optional[torch.Tensor] = None  # uint8
+    column_scales: Optional[torch.Tensor] = None  # float32 [cols]
+    column_offsets: Optional[torch.Tensor] = None  # float32 [cols]
+    row_offsets: Optional[torch.Tensor] = None  # float32 [rows]
+    values: Optional[torch.Tensor] = None  # f16/f32 [nnz] when bits == 0
+    decode_policy: int = N.DECODE_PER_GENE_AFFINE
+    meta: dict = field(default_factory=dict)
+
+    @property
+    def nnz(self) -> int:
+        return int(self.col_idx.numel())
+
+    def descriptor(self) -> N.CxQcsrMatrix:
+        d = N.CxQcsrMatrix()
+        d.rows, d.cols, d.nnz = self.rows, self.cols, self.nnz
+        d.bits, d.decode_policy = self.bits, self.decode_policy
+        d.row_ptr, d.col_idx = _ptr(self.row_ptr), _ptr(self.col_idx)
+        d.packed_row_ptr, d.packed_values = _ptr(self.packed_row_ptr), _ptr(self.packed_values)
+        d.column_scales, d.column_offsets = _ptr(self.column_scales), _ptr(self.column_offsets)
+        d.row_offsets, d.values = _ptr(self.row_offsets), _ptr(self.values)
+        d.value_dtype = _DTYPE_CODE[self.values.dtype] if self.values is not None else 0
+        return d
+
+    def nbytes_algorithmic(self, rhs_cols: int, rhs_bytes: int = 2) -> int:
+        """Bytes the SpMM must move once: row_ptr (+ packed_row_ptr), col_idx, codes or
+        values, per-gene metadata, the weight panel and the fp32 output."""
+        b = self.row_ptr.numel() * 4 + self.col_idx.numel() * 4
+        if self.bits:
+            b += self.packed_row_ptr.numel() * 4 + self.packed_values.numel()
+            b += sum(t.numel() * 4 for t in (self.column_scales, self.column_offsets,
+                                             self.row_offsets) if t is not None)
+        else:
+            b += self.values.numel() * self.values.element_size()
+        return b + self.cols * rhs_cols * rhs_bytes + self.rows * rhs_cols * 4
+
+
+def qcsr_spmm(m: QcsrMatrix, rhs: torch.Tensor, out: Optional[torch.Tensor] = None,
+              stream=None) -> torch.Tensor:
+    """Y = decode(X) . rhs (fp32). rhs: [cols, N] f16/f32, row-major (leading dim = stride)."""
+    _require_cuda(m.row_ptr, m.col_idx, rhs)
+    if rhs.dim() != 2 or rhs.shape[0] != m.cols or rhs.stride(1) != 1:
+        raise ValueError("rhs must be [cols, N] with unit column stride")
+    n = rhs.shape[1]
+    if out is None:
+        out = torch.empty((m.rows, n), dtype=torch.float32, device=rhs.device)
+    d = m.descriptor()
+    N.check("cx_qcsr_spmm_fwd", N.engine().cx_qcsr_spmm_fwd(
+        C.byref(d), rhs.data_ptr(), _DTYPE_CODE[rhs.dtype], rhs.stride(0), n, out.data_ptr(),
+        out.stride(0), _stream(stream)))
+    return out
+
+
+@dataclass
+class BellMatrix:
+    rows: int
+    cols: int
+    block_size: int
+    ell_cols: int
+    block_col_idx: torch.Tensor  # uint32 as int32 storage [rows/bs, ell_cols/bs]
+    values: Optional[torch.Tensor] = None  # [rows, ell_cols] bf16/f16/f32
+    bits: int = 0
+    decode_policy: int = N.DECODE_PER_GENE_AFFINE
+    row_stride_bytes: int = 0
+    packed_values: Optional[torch.Tensor] = None
+    column_scales: Optional[torch.Tensor] = None
+    column_offsets: Optional[torch.Tensor] = None
+    row_offsets: Optional[torch.Tensor] = None
+    meta: dict = field(default_factory=dict)
+
+    def descriptor(self) -> N.CxBellMatrix:
+        d = N.CxBellMatrix()
+        d.rows, d.cols, d.block_size, d.ell_cols = self.rows, self.cols, self.block_size, self.ell_cols
+        d.block_col_idx = _ptr(self.block_col_idx)
+        d.values = _ptr(self.values)
+        d.value_dtype = _DTYPE_CODE[self.values.dtype] if self.values is not None else 0
+        d.bits, d.decode_policy, d.row_stride_bytes = self.bits, self.decode_policy, self.row_stride_bytes
+        d.packed_values = _ptr(self.packed_values)
+        d.column_scales, d.column_offsets = _ptr(self.column_scales), _ptr(self.column_offsets)
+        d.row_offsets = _ptr(self.row_offsets)
+        return d
+
+
+def bell_spmm(m: BellMatrix, rhs: torch.Tensor, out: Optional[torch.Tensor] = None,
+              stream=None) -> torch.Tensor:
+    """Reference-semantics Blocked-ELL SpMM with a row-major rhs [cols, N]."""
+    _require_cuda(m.block_col_idx, rhs)
+    n = rhs.shape[1]
+    if out is None:
+        out = torch.empty((m.rows, n), dtype=torch.float32, device=rhs.device)
+    d = m.descriptor()
+    N.check("cx_bell_spmm_fwd", N.engine().cx_bell_spmm_fwd(
+        C.byref(d), rhs.data_ptr(), _DTYPE_CODE[rhs.dtype], rhs.stride(0), n, out.data_ptr(),
+        out.stride(0), _stream(stream)))
+    return out
+
+
+def bell_pack_rhs(rhs: torch.Tensor, stream=None) -> torch.Tensor:
+    """Packs a bf16 [K, N] row-major weight panel into the MFMA operand layout."""
+    _require_cuda(rhs)
+    if rhs.dtype != torch.bfloat16 or rhs.dim() != 2 or rhs.stride(1) != 1:
+        raise ValueError("rhs must be a row-major bf16 [K, N] tensor")
+    k, n = rhs.shape
+    packed = torch.empty(((k + 31) // 32) * n * 32, dtype=torch.bfloat16, device=rhs.device)
+    N.check("cx_bell_pack_rhs", N.engine().cx_bell_pack_rhs(
+        rhs.data_ptr(), rhs.stride(0), k, n, packed.data_ptr(), _stream(stream)))
+    return packed
+
+
+def bell_spmm_packed(m: BellMatrix, packed_rhs: torch.Tensor, n: int,
+                     out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """MFMA Blocked-ELL SpMM against a packed bf16 panel (bell_pack_rhs)."""
+    _require_cuda(m.block_col_idx, packed_rhs)
+    if out is None:
+        out = torch.empty((m.rows, n), dtype=torch.float32, device=packed_rhs.device)
+    d = m.descriptor()
+    N.check("cx_bell_spmm_fwd_packed", N.engine().cx_bell_spmm_fwd_packed(
+        C.byref(d), packed_rhs.data_ptr(), n, out.data_ptr(), out.stride(0), _stream(stream)))
+    return out
+
+
+@dataclass
+class CpbpTiles:
+    row_count: int
+    feature_count: int
+    tile_row_width: int
+    feature_block_offsets: torch.Tensor  # u32 (int32 storage)
+    feature_permutation: torch.Tensor
+    tile_block_offsets: torch.Tensor
+    tile_block_ids: torch.Tensor
+    tile_block_cell_masks: torch.Tensor  # u32 (int32) or u64 (int64) storage
+    block_row_entry_offsets: torch.Tensor
+    row_block_gene_masks: torch.Tensor
+    row_block_value_offsets: torch.Tensor
+    values: torch.Tensor  # f16 / f32
+    row_permutation: torch.Tensor
+    meta: dict = field(default_factory=dict)
+
+    @property
+    def tile_count(self) -> int:
+        return int(self.tile_block_offsets.numel()) - 1
+
+    def descriptor(self) -> N.CxCpbpTiles:
+        d = N.CxCpbpTiles()
+        d.row_count, d.feature_count = self.row_count, self.feature_count
+        d.feature_block_count = int(self.feature_block_offsets.numel()) - 1
+        d.tile_row_width, d.tile_count = self.tile_row_width, self.tile_count
+        d.tile_block_count = int(self.tile_block_ids.numel())
+        d.row_block_entry_count = int(self.row_block_gene_masks.numel())
+        d.nnz_count = int(self.values.numel())
+        d.value_dtype = _DTYPE_CODE[self.values.dtype]
+        for name in ("feature_block_offsets", "feature_permutation", "tile_block_offsets",
+                     "tile_block_ids", "tile_block_cell_masks", "block_row_entry_offsets",
+                     "row_block_gene_masks", "row_block_value_offsets", "values",
+                     "row_permutation"):
+            setattr(d, name, _ptr(getattr(self, name)))
+        return d
+
+    def nbytes_algorithmic(self) -> int:
+        """Bytes of every tile array, the plan subset, the weights and the output once
+        (the reference bench's accounting, feature_weighted_row_reduction_bench.cu:356-368)."""
+        arrays = (self.feature_block_offsets, self.feature_permutation, self.tile_block_offsets,
+                  self.tile_block_ids, self.tile_block_cell_masks, self.block_row_entry_offsets,
+                  self.row_block_gene_masks, self.row_block_value_offsets, self.values,
+                  self.row_permutation)
+        b = sum(t.numel() * t.element_size() for t in arrays)
+        return b + self.feature_count * 4 + self.row_count * 4
+
+
+def cpbp_reduce(t: CpbpTiles, weights: torch.Tensor, out: Optional[torch.Tensor] = None,
+                stream=None) -> torch.Tensor:
+    _require_cuda(weights, t.values)
+    if out is None:
+        out = torch.empty(t.row_count, dtype=torch.float32, device=weights.device)
+    d = t.descriptor()
+    N.check("cx_cpbp_reduce", N.engine().cx_cpbp_reduce(
+        C.byref(d), weights.data_ptr(), weights.numel(), out.data_ptr(), out.numel(),
+        _stream(stream)))
+    return out
+
+
+def csr_spmv(row_ptr: torch.Tensor, col_idx: torch.Tensor, values: torch.Tensor,
+             x: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    _require_cuda(row_ptr, col_idx, values, x)
+    rows = row_ptr.numel() - 1
+    if out is None:
+        out = torch.empty(rows, dtype=torch.float32, device=x.device)
+    N.check("cx_csr_spmv_fwd", N.engine().cx_csr_spmv_fwd(
+        rows, row_ptr.data_ptr(), col_idx.data_ptr(), values.data_ptr(), _DTYPE_CODE[values.dtype],
+        x.data_ptr(), out.data_ptr(), _stream(stream)))
+    return out

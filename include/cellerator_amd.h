@@ -1,0 +1,302 @@
+/*
+ * cellerator_amd.h -- C-ABI of the MI355X projection engine (libcellerator_amd.so).
+ *
+ * Two layers, both plain C (pointers, sizes, POD descriptors; no C++ or torch types):
+ *
+ *  1. The thin launch layer (cx_*). One entry point per hot-path operation; each
+ *     validates its descriptor on the host, then enqueues hand-written gfx950
+ *     kernels on the caller's hipStream_t (passed as void*). Nothing synchronises,
+ *     nothing allocates on the launch path. These replace the reference's launchers:
+ *       cx_qcsr_spmm_fwd  <- sparse_project::csr_spmm_fwd_f16_f32
+ *                            (src/compute/sparse/project/project.hh:12-23, project.cu:31-48)
+ *                            generalised to the quantized csr_matrix container
+ *                            (include/Cellerator/quantized/layout.cuh:12-39) decoded by
+ *                            dequantize_code (include/Cellerator/quantized/access.cuh:81-91)
+ *       cx_bell_spmm_fwd  <- sparse_project::blocked_ell_spmm_fwd_f16_f32 and
+ *                            quantized_blocked_ell_spmm_fwd_f32
+ *                            (src/compute/sparse/project/project.hh:25-62, project.cu:50-168)
+ *       cx_cpbp_reduce    <- cellpack::evaluate_feature_weighted_row_reduction_tiles_cuda
+ *                            (components/CellPack/include/CellPack/feature_weighted_row_reduction_cuda.hh:17-22,
+ *                             components/CellPack/src/feature_weighted_row_reduction_cuda.cu:238-262)
+ *
+ *  2. The public context ABI (cellerator_*), layout-compatible with the reference's
+ *     include/Cellerator/abi.h:11-152 for the structs and functions of the projection
+ *     forward path, with two additive enum values: CELLERATOR_DTYPE_BF16 and
+ *     CELLERATOR_LAYOUT_QUANTIZED_CSR.
+ *
+ * Status codes are shared by both layers and equal the reference's cellerator_status
+ * values (include/Cellerator/abi.h:14-21). The thread-local message of the last failure
+ * is returned by cx_last_error() / cellerator_last_error().
+ */
+#ifndef CELLERATOR_AMD_H
+#define CELLERATOR_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------------- */
+/* Shared enums                                                                    */
+/* ------------------------------------------------------------------------------- */
+
+#define CELLERATOR_ABI_VERSION 1u
+#define CELLERATOR_TENSOR_MAX_RANK 4u
+
+/* include/Cellerator/abi.h:14-21 */
+typedef enum cellerator_status {
+    CELLERATOR_STATUS_SUCCESS = 0,
+    CELLERATOR_STATUS_INVALID_ARGUMENT = 1,
+    CELLERATOR_STATUS_INVALID_SHAPE = 2,
+    CELLERATOR_STATUS_UNSUPPORTED = 3,
+    CELLERATOR_STATUS_CUDA_ERROR = 4, /* a HIP runtime error on this engine */
+    CELLERATOR_STATUS_INTERNAL_ERROR = 5
+} cellerator_status;
+
+#define CX_STATUS_SUCCESS CELLERATOR_STATUS_SUCCESS
+#define CX_STATUS_INVALID_ARGUMENT CELLERATOR_STATUS_INVALID_ARGUMENT
+#define CX_STATUS_INVALID_SHAPE CELLERATOR_STATUS_INVALID_SHAPE
+#define CX_STATUS_UNSUPPORTED CELLERATOR_STATUS_UNSUPPORTED
+#define CX_STATUS_HIP_ERROR CELLERATOR_STATUS_CUDA_ERROR
+#define CX_STATUS_INTERNAL_ERROR CELLERATOR_STATUS_INTERNAL_ERROR
+
+/* include/Cellerator/abi.h:23-29, plus BF16 (additive). */
+typedef enum cellerator_dtype {
+    CELLERATOR_DTYPE_INVALID = 0,
+    CELLERATOR_DTYPE_F16 = 1,
+    CELLERATOR_DTYPE_F32 = 2,
+    CELLERATOR_DTYPE_U8 = 3,
+    CELLERATOR_DTYPE_U32 = 4,
+    CELLERATOR_DTYPE_BF16 = 5
+} cellerator_dtype;
+
+/* include/Cellerator/quantized/blocked_ell.cuh:10-14 */
+#define CX_DECODE_PER_GENE_AFFINE 1u
+#define CX_DECODE_COLUMN_SCALE_ROW_OFFSET 2u
+
+/* ------------------------------------------------------------------------------- */
+/* 1. Thin launch layer                                                            */
+/* ------------------------------------------------------------------------------- */
+
+/* Quantized (or plain) CSR cells x genes matrix. Field meaning follows
+ * cellerator::quantized::csr_matrix (include/Cellerator/quantized/layout.cuh:24-37):
+ * row_ptr are nnz offsets, packed_row_ptr are byte offsets of each row's unpadded
+ * packed codes (layout.cuh:106-129), codes are little-endian within a byte
+ * (format.cuh:39-48). bits == 0 selects unquantized values: `values` of
+ * `value_dtype` (F16 or F32), one per nnz, as csr_spmm_fwd_f16_f32 consumes. */
+typedef struct cx_qcsr_matrix {
+    uint32_t rows;
+    uint32_t cols;
+    uint64_t nnz;
+    uint32_t bits;          /* 1, 2, 4, 8; 0 = unquantized `values` */
+    uint32_t decode_policy; /* CX_DECODE_* (ignored when bits == 0) */
+    const int32_t *row_ptr;        /* rows + 1 */
+    const int32_t *packed_row_ptr; /* rows + 1 (ignored when bits == 0) */
+    const int32_t *col_idx;        /* nnz */
+    const uint8_t *packed_values;  /* packed_row_ptr[rows] bytes */
+    const float *column_scales;    /* cols or NULL (-> 1) */
+    const float *column_offsets;   /* cols or NULL (-> 0); per_gene_affine */
+    const float *row_offsets;      /* rows or NULL (-> 0); column_scale_row_offset */
+    const void *values;            /* nnz of value_dtype when bits == 0 */
+    uint32_t value_dtype;          /* cellerator_dtype, bits == 0 only */
+    uint32_t reserved;
+} cx_qcsr_matrix;
+
+/* Y[rows x out_cols] (fp32, row stride out_ld) = decode(A) . RHS[cols x out_cols]
+ * (row stride rhs_ld, dtype F16 or F32; F16 widens exactly). fp32 multiply and
+ * fp32 accumulation, deterministic (fixed per-row summation order).
+ * Replaces csr_spmm_fwd_f16_f32 (src/compute/sparse/project/project.hh:12-23). */
+int cx_qcsr_spmm_fwd(const cx_qcsr_matrix *a, const void *rhs, uint32_t rhs_dtype,
+                     int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
+                     void *stream);
+
+/* Blocked-ELL matrix (include/Cellerator/quantized/blocked_ell.cuh:18-35 and the
+ * cs::sparse::blocked_ell layout consumed by blocked_ell_spmm_fwd_kernel_):
+ * block_col_idx is (rows/block_size) x (ell_cols/block_size), 0xffffffff marks an
+ * empty slot; values are row-major rows x ell_cols. bits != 0 selects the quantized
+ * form (packed codes, row stride row_stride_bytes). */
+typedef struct cx_bell_matrix {
+    uint32_t rows;
+    uint32_t cols;
+    uint32_t block_size;
+    uint32_t ell_cols;
+    const uint32_t *block_col_idx;
+    const void *values;  /* rows x ell_cols of value_dtype (BF16, F16 or F32) */
+    uint32_t value_dtype;
+    uint32_t bits;       /* 0 = plain values; 1, 2, 4, 8 = packed codes */
+    uint32_t decode_policy;
+    uint32_t row_stride_bytes;
+    const uint8_t *packed_values;
+    const float *column_scales;
+    const float *column_offsets;
+    const float *row_offsets;
+} cx_bell_matrix;
+
+/* Y = X_bell . RHS with a row-major RHS (F32, F16 or BF16), any block size and N, plain
+ * (BF16/F16/F32) or quantized values: fp32 accumulation in slot order per output
+ * element, the semantics of blocked_ell_spmm_fwd_kernel_ / quantized_blocked_ell_spmm_fwd_kernel_
+ * (src/compute/sparse/project/kernels/blocked_ell_spmm_fwd_kernel_.cuh:1-33,
+ *  quantized_blocked_ell_spmm_fwd_kernel_.cuh:1-39). Replaces
+ * blocked_ell_spmm_fwd_f16_f32 / quantized_blocked_ell_spmm_fwd_f32
+ * (src/compute/sparse/project/project.cu:50-168). */
+int cx_bell_spmm_fwd(const cx_bell_matrix *a, const void *rhs, uint32_t rhs_dtype,
+                     int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
+                     void *stream);
+
+/* Packs a row-major bf16 RHS [k x n] into the matrix-core operand panel
+ * [ceil(k/32)][n][32] (genes of one 32-gene block column contiguous per output column,
+ * zero-padded past k): the Blocked-ELL counterpart of pack_dense_operand_cuda
+ * (include/Cellerator/compute/math/packed_dense_operand.hh:16-70). `packed` holds
+ * ceil(k/32) * n * 32 bf16. Done once per weight generation. */
+int cx_bell_pack_rhs(const uint16_t *rhs_bf16, int64_t rhs_ld, uint32_t k, uint32_t n,
+                     uint16_t *packed, void *stream);
+
+/* MFMA Blocked-ELL: bf16 32x32 value blocks x packed bf16 panel -> fp32 Y, N in
+ * {64, 128, 256}, v_mfma_f32_32x32x16_bf16 with fp32 accumulation. Same result
+ * contract as cx_bell_spmm_fwd within fp32 reordered-sum tolerance. */
+int cx_bell_spmm_fwd_packed(const cx_bell_matrix *a, const uint16_t *packed_rhs,
+                            int64_t out_cols, float *out, int64_t out_ld, void *stream);
+
+/* CP-BP warp-tile projection (components/CellPack/include/CellPack/warp_tiles.hh:41-79)
+ * plus the plan subset of feature_weighted_row_reduction_plan_view
+ * (components/CellPack/include/CellPack/feature_weighted_row_reduction.hh:16-26).
+ * tile_row_width <= 32 uses u32 cell masks (the reference's v1 contract);
+ * 32 < tile_row_width <= 64 uses u64 cell masks (the wave64 projection).
+ * values are F16 (reference storage_t) or F32. */
+typedef struct cx_cpbp_tiles {
+    uint32_t row_count;
+    uint32_t feature_count;
+    uint32_t feature_block_count;
+    uint32_t tile_row_width;
+    uint32_t tile_count;
+    uint32_t tile_block_count;
+    uint32_t row_block_entry_count;
+    uint32_t nnz_count;
+    uint32_t value_dtype;
+    uint32_t reserved;
+    const uint32_t *feature_block_offsets; /* feature_block_count + 1 */
+    const uint32_t *feature_permutation;   /* feature_count: execution -> canonical */
+    const uint32_t *tile_block_offsets;    /* tile_count + 1 */
+    const uint32_t *tile_block_ids;        /* tile_block_count */
+    const void *tile_block_cell_masks;     /* tile_block_count of u32 or u64 */
+    const uint32_t *block_row_entry_offsets; /* tile_block_count + 1 */
+    const uint32_t *row_block_gene_masks;    /* row_block_entry_count */
+    const uint32_t *row_block_value_offsets; /* row_block_entry_count + 1 */
+    const void *values;                      /* nnz_count */
+    const uint32_t *row_permutation;         /* row_count: execution -> canonical row */
+} cx_cpbp_tiles;
+
+/* row_values[row_permutation[exec_row]] = sum over the row's stored values of
+ * fp32(value) * feature_weights[canonical feature], fp32 accumulation. Output in
+ * canonical partition-local row order, as the reference kernel writes it
+ * (feature_weighted_row_reduction_cuda.cu:180-218). Validates the metadata and output
+ * aliasing on the host first (:57-178). */
+int cx_cpbp_reduce(const cx_cpbp_tiles *tiles, const float *feature_weights,
+                   uint64_t feature_weight_capacity, float *row_values,
+                   uint64_t row_capacity, void *stream);
+
+/* N = 1 CSR comparator: csr_spmv_fwd_f16_f32 (src/compute/sparse/ops/ops.hh:83-90);
+ * y[r] = sum fp32(values) * x[col]. values F16 or F32. */
+int cx_csr_spmv_fwd(uint32_t rows, const uint32_t *row_ptr, const uint32_t *col_idx,
+                    const void *values, uint32_t value_dtype, const float *x, float *y,
+                    void *stream);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *cx_last_error(void);
+/* Engine build identity, e.g. "cellerator_amd gfx950". */
+const char *cx_build_info(void);
+
+/* ------------------------------------------------------------------------------- */
+/* 2. Public context ABI (include/Cellerator/abi.h:31-152)                          */
+/* ------------------------------------------------------------------------------- */
+
+typedef enum cellerator_sparse_layout {
+    CELLERATOR_LAYOUT_CSR = 1,
+    CELLERATOR_LAYOUT_BLOCKED_ELL = 2,
+    CELLERATOR_LAYOUT_SLICED_ELL = 3,
+    CELLERATOR_LAYOUT_QUANTIZED_BLOCKED_ELL = 4,
+    CELLERATOR_LAYOUT_QUANTIZED_CSR = 5 /* additive: packed codes + major_ptr/minor_idx */
+} cellerator_sparse_layout;
+
+typedef enum cellerator_saved_state_kind {
+    CELLERATOR_SAVED_STATE_NONE = 0,
+    CELLERATOR_SAVED_STATE_SPARSE_PROJECTION = 1,
+    CELLERATOR_SAVED_STATE_ROW_SCALE = 2,
+    CELLERATOR_SAVED_STATE_RECONSTRUCTION_LOSS = 3
+} cellerator_saved_state_kind;
+
+typedef struct cellerator_context cellerator_context;
+typedef struct cellerator_saved_state cellerator_saved_state;
+
+typedef struct cellerator_execution_config {
+    uint32_t version;
+    size_t size;
+    int32_t device;
+    void *stream;
+    void *scratch;
+    size_t scratch_bytes;
+} cellerator_execution_config;
+
+typedef struct cellerator_tensor_desc {
+    uint32_t version;
+    size_t size;
+    void *data;
+    cellerator_dtype dtype;
+    uint32_t rank;
+    uint64_t shape[CELLERATOR_TENSOR_MAX_RANK];
+    int64_t stride[CELLERATOR_TENSOR_MAX_RANK];
+} cellerator_tensor_desc;
+
+/* For CELLERATOR_LAYOUT_QUANTIZED_CSR, major_ptr holds the rows + 1 nnz offsets,
+ * minor_idx the gene of each nnz, packed_values the codes, and block_col_idx (unused by
+ * CSR layouts) carries the rows + 1 packed row byte offsets that build_packed_row_ptr
+ * produces (include/Cellerator/quantized/layout.cuh:106-129). */
+typedef struct cellerator_sparse_layout_desc {
+    uint32_t version;
+    size_t size;
+    cellerator_sparse_layout layout;
+    uint32_t rows;
+    uint32_t cols;
+    uint32_t nnz;
+    uint32_t block_size;
+    uint32_t ell_cols;
+    uint32_t row_stride_bytes;
+    uint32_t bits;
+    uint32_t decode_policy;
+    cellerator_dtype value_dtype;
+    const uint32_t *major_ptr;
+    const uint32_t *minor_idx;
+    const uint32_t *block_col_idx;
+    const void *values;
+    const uint8_t *packed_values;
+    const float *column_scales;
+    const float *column_offsets;
+    const float *row_offsets;
+} cellerator_sparse_layout_desc;
+
+const char *cellerator_status_string(cellerator_status status);
+const char *cellerator_last_error(void);
+
+cellerator_status cellerator_context_create(const cellerator_execution_config *config,
+                                            cellerator_context **out_context);
+cellerator_status cellerator_context_synchronize(cellerator_context *context);
+void cellerator_context_destroy(cellerator_context *context);
+void cellerator_saved_state_destroy(cellerator_saved_state *saved_state);
+
+/* rhs: F32 (reference contract) or F16/BF16 rank-2 [cols x N] row-major;
+ * out: F32 rank-2 [rows x N] row-major. Layouts: CSR (F16/F32 values), BLOCKED_ELL
+ * (F16/BF16/F32 values), QUANTIZED_BLOCKED_ELL, QUANTIZED_CSR. SLICED_ELL returns
+ * UNSUPPORTED, as the reference does (src/abi/abi.cu:326-328). */
+cellerator_status cellerator_sparse_projection_forward(cellerator_context *context,
+                                                       const cellerator_sparse_layout_desc *layout,
+                                                       const cellerator_tensor_desc *rhs,
+                                                       cellerator_tensor_desc *out,
+                                                       cellerator_saved_state **saved_state);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CELLERATOR_AMD_H */
