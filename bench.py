@@ -121,7 +121,7 @@ def bench_qcsr(args, torch, cfg, n_out: int) -> dict:
                    "bits": m.bits, "n_out": n_out, "rhs": "fp16",
                    "nnz_per_row_mean": m.nnz / m.rows, "seed": hex(cfg.seed)},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(cfg.name),
                      "kernel": "qcsr_spmm_rowwave", "kernel_ms_mean": kern_ms,
                      "kernel_ms_median": statistics.median(ev),
                      "algorithmic_bytes": alg_bytes,
@@ -133,6 +133,34 @@ def bench_qcsr(args, torch, cfg, n_out: int) -> dict:
     return res
 
 
+def load_traffic(workload: str):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel calibration), or
+    None when no summary exists for this workload."""
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        entry = json.loads(f.read_text()).get(workload)
+    except (OSError, ValueError):
+        return None
+    return None if entry is None else entry.get("hbm_bytes_per_launch")
+
+
+def calibrate_copy(nbytes: int, reps: int) -> int:
+    """Plain device-to-device copy of known size: the reference point that scales the
+    FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    import torch
+
+    src = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": src.numel() * 4, "reps": reps}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -142,6 +170,8 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=0, help="override the row count (smaller runs)")
     ap.add_argument("--cpu-rows", type=int, default=100_000)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="run only a plain copy of BYTES (rocprofv3 counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every box in this build has one MI355X and the "
@@ -153,6 +183,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy, max(args.steps, 1))
     from cellerator_amd.synth import C2, C3
 
     cfg, n_out = {"c3": (C3, 64), "c3n128": (C3, 128), "c2": (C2, 64)}[args.config]
