@@ -56,12 +56,49 @@ class CxCpbpTiles(C.Structure):
     ]
 
 
+class CxCpbpPlan(C.Structure):
+    _fields_ = [("feature_count", u32), ("feature_block_count", u32),
+                ("feature_permutation", p_void), ("feature_block_offsets", p_void)]
+
+
+class CxCpbpCsr(C.Structure):
+    _fields_ = [("rows", u32), ("value_size_bytes", u32), ("row_offsets", p_void),
+                ("canonical_features", p_void), ("values", p_void)]
+
+
+class CxCpbpOrderConfig(C.Structure):
+    _fields_ = [("kind", u32), ("window_size", u32), ("group_width", u32), ("reserved", u32),
+                ("seed", u64), ("global_row_begin", u64)]
+
+
+class CxCpbpTileRequirements(C.Structure):
+    _fields_ = [("row_count", u32), ("feature_count", u32), ("feature_block_count", u32),
+                ("tile_row_width", u32), ("tile_count", u32), ("tile_block_count", u32),
+                ("row_block_entry_count", u32), ("nnz_count", u32), ("value_size_bytes", u32),
+                ("cell_mask_bytes", u32)]
+
+
+class CxCpbpTileBuffers(C.Structure):
+    _fields_ = [("tile_block_offsets", p_void), ("tile_block_ids", p_void),
+                ("tile_block_cell_masks", p_void), ("block_row_entry_offsets", p_void),
+                ("row_block_gene_masks", p_void), ("row_block_value_offsets", p_void),
+                ("values", p_void), ("row_permutation", p_void), ("primary_keys", p_void)]
+
+
 class CxsQcsrParams(C.Structure):
     _fields_ = [
         ("seed", u64), ("rows", u32), ("cols", u32), ("row_dist", u32), ("bits", u32),
         ("nnz_mean", C.c_double), ("nnz_sigma", C.c_double), ("nnz_min", u32),
         ("nnz_max", u32), ("zipf_s", C.c_double), ("nb_mean", C.c_double),
         ("nb_size", C.c_double),
+    ]
+
+
+class CxsCpbpParams(C.Structure):
+    _fields_ = [
+        ("seed", u64), ("rows", u32), ("genes", u32), ("modules", u32), ("module_size", u32),
+        ("min_active", u32), ("max_active", u32), ("active_genes", u32), ("background", u32),
+        ("nb_mean", C.c_double), ("nb_size", C.c_double),
     ]
 
 
@@ -95,6 +132,12 @@ ENGINE_SIGNATURES = {
     "cx_bell_spmm_fwd_packed": (C.c_int, [C.POINTER(CxBellMatrix), p_void, i64, p_void, i64, p_void]),
     "cx_cpbp_reduce": (C.c_int, [C.POINTER(CxCpbpTiles), p_void, u64, p_void, u64, p_void]),
     "cx_csr_spmv_fwd": (C.c_int, [u32, p_void, p_void, p_void, u32, p_void, p_void, p_void]),
+    "cx_cpbp_builder_create": (C.c_int, [C.POINTER(CxCpbpPlan), C.POINTER(CxCpbpCsr),
+                                         C.POINTER(CxCpbpOrderConfig), u32, C.POINTER(p_void)]),
+    "cx_cpbp_builder_requirements": (C.c_int, [p_void, C.POINTER(CxCpbpTileRequirements)]),
+    "cx_cpbp_builder_export": (C.c_int, [p_void, C.POINTER(CxCpbpTileBuffers)]),
+    "cx_cpbp_builder_destroy": (None, [p_void]),
+    "cx_cpbp_build_last_error": (C.c_char_p, []),
     "cx_last_error": (C.c_char_p, []),
     "cx_build_info": (C.c_char_p, []),
     "cellerator_status_string": (C.c_char_p, [C.c_int]),
@@ -119,6 +162,8 @@ SYNTH_SIGNATURES = {
     "cxs_dense_normal": (C.c_int, [u64, u64, C.c_float, u32, p_void, p_void]),
     "cxs_bell_generate": (C.c_int, [u64, u32, u32, u32, u32, u32, u32, u32, C.c_float, C.c_double,
                                     C.c_double, p_void, p_void, p_void]),
+    "cxs_cpbp_count": (C.c_int, [C.POINTER(CxsCpbpParams), p_void, u32]),
+    "cxs_cpbp_fill": (C.c_int, [C.POINTER(CxsCpbpParams), p_void, p_void, p_void, u32]),
     "cxs_last_error": (C.c_char_p, []),
 }
 

@@ -32,6 +32,7 @@ ENGINE_SOURCES = [
     "cpbp_reduce.hip",
     "csr_spmv.hip",
     "abi.cpp",
+    "cpbp_build.cpp",
 ]
 SYNTH_SOURCES = ["synth.hip"]
 

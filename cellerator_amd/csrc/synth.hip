@@ -8,6 +8,8 @@
 #include <cstdint>
 #include <cstdio>
 #include <vector>
+#include <thread>
+#include <atomic>
 
 #include "cellerator_amd_synth.h"
 
@@ -50,7 +52,7 @@ __host__ __device__ inline std::uint32_t lowbias32(std::uint32_t x) {
 // Independent streams of one seed.
 enum Stream : std::uint64_t {
     kTarget = 1, kInclude = 2, kCount = 3, kPerm = 4, kDense = 5, kBellRow = 6,
-    kBellValue = 7, kBellPattern = 8
+    kBellValue = 7, kBellPattern = 8, kCpbpRow = 9, kCpbpValue = 10
 };
 
 __host__ __device__ inline std::uint64_t stream_base(std::uint64_t seed, std::uint64_t stream) {
@@ -377,11 +379,134 @@ int upload(T **dst, const std::vector<T> &src) {
                      "hipMemcpy");
 }
 
+
+// ---- CP-BP structured-support matrix, generated on host threads ----
+// Row r: k ~ U{min_active..max_active} distinct modules (module m = genes
+// [m*module_size, (m+1)*module_size)), active_genes of each chosen module without
+// replacement, then `background` genes uniform over the axis excluding genes already
+// present; genes sorted ascending; value = log1p(1 + NB(nb_mean, nb_size)) (a stored entry
+// is never zero). Every draw is a splitmix64 of (seed stream, row, draw index), so the
+// matrix does not depend on the thread count.
+inline std::uint64_t cpbp_draw(std::uint64_t row_key, std::uint64_t i) {
+    return splitmix64(row_key ^ (i * 0xd1b54a32d192ed03ull));
+}
+
+int host_nb_draw(const std::vector<std::uint32_t> &cdf, std::uint32_t u) {
+    int lo = 0, hi = kCountMax;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (u < cdf[mid]) hi = mid;
+        else lo = mid + 1;
+    }
+    return lo;
+}
+
+int cpbp_check(const cxs_cpbp_params *p) {
+    if (p == nullptr) return fail("null CP-BP parameters");
+    if (p->modules == 0u || p->module_size == 0u || p->module_size > 1024u
+        || static_cast<std::uint64_t>(p->modules) * p->module_size > p->genes)
+        return fail("modules must fit the gene axis (module_size <= 1024)");
+    if (p->min_active == 0u || p->min_active > p->max_active || p->max_active > p->modules)
+        return fail("active module range must be within [1, modules]");
+    if (p->active_genes > p->module_size) return fail("active genes exceed the module size");
+    if (static_cast<std::uint64_t>(p->max_active) * p->active_genes + p->background > p->genes / 2)
+        return fail("a row may hold at most half of the gene axis");
+    if (p->nb_mean <= 0.0 || p->nb_size <= 0.0) return fail("bad NB moments");
+    return 0;
+}
+
+std::uint32_t cpbp_active(const cxs_cpbp_params *p, std::uint64_t key) {
+    return p->min_active
+        + static_cast<std::uint32_t>(cpbp_draw(key, 0) % (p->max_active - p->min_active + 1u));
+}
+
+template<typename Fn>
+void host_parallel(std::uint32_t count, std::uint32_t threads, Fn fn) {
+    threads = std::max(1u, std::min(threads, count));
+    std::vector<std::thread> pool;
+    const std::uint32_t per = count / threads, extra = count % threads;
+    std::uint32_t begin = 0;
+    for (std::uint32_t t = 0; t < threads; ++t) {
+        const std::uint32_t end = begin + per + (t < extra ? 1u : 0u);
+        pool.emplace_back([=] { fn(begin, end); });
+        begin = end;
+    }
+    for (auto &th : pool) th.join();
+}
+
 } // namespace
 
 extern "C" {
 
 const char *cxs_last_error(void) { return g_error; }
+
+int cxs_cpbp_count(const cxs_cpbp_params *p, std::uint32_t *row_nnz, std::uint32_t threads) {
+    if (int rc = cpbp_check(p)) return rc;
+    if (row_nnz == nullptr && p->rows != 0u) return fail("null row_nnz");
+    const std::uint64_t base = stream_base(p->seed, kCpbpRow);
+    host_parallel(p->rows, threads, [&](std::uint32_t lo, std::uint32_t hi) {
+        for (std::uint32_t r = lo; r < hi; ++r)
+            row_nnz[r] = cpbp_active(p, splitmix64(base ^ r)) * p->active_genes + p->background;
+    });
+    return 0;
+}
+
+int cxs_cpbp_fill(const cxs_cpbp_params *p, const std::uint32_t *row_offsets,
+                  std::uint32_t *features, float *values, std::uint32_t threads) {
+    if (int rc = cpbp_check(p)) return rc;
+    if (p->rows != 0u && (row_offsets == nullptr || features == nullptr || values == nullptr))
+        return fail("null CP-BP output");
+    const std::uint64_t base = stream_base(p->seed, kCpbpRow);
+    const std::uint64_t vbase = stream_base(p->seed, kCpbpValue);
+    const std::vector<std::uint32_t> cdf = nb_cdf_table(p->nb_mean, p->nb_size);
+    const std::vector<float> lut = log1p_table();
+    std::atomic<int> bad{0};
+    host_parallel(p->rows, threads, [&](std::uint32_t lo, std::uint32_t hi) {
+        std::vector<std::uint8_t> present(p->genes, 0u);
+        std::vector<std::uint32_t> genes, mods, local(p->module_size);
+        for (std::uint32_t r = lo; r < hi; ++r) {
+            const std::uint64_t key = splitmix64(base ^ r);
+            const std::uint32_t k = cpbp_active(p, key);
+            std::uint64_t draw = 1;
+            mods.clear();
+            genes.clear();
+            while (mods.size() < k) {
+                const std::uint32_t m = static_cast<std::uint32_t>(cpbp_draw(key, draw++) % p->modules);
+                if (std::find(mods.begin(), mods.end(), m) == mods.end()) mods.push_back(m);
+            }
+            for (std::uint32_t m : mods) {
+                for (std::uint32_t t = 0; t < p->module_size; ++t) local[t] = t;
+                for (std::uint32_t t = 0; t < p->active_genes; ++t) {
+                    const std::uint32_t j = t + static_cast<std::uint32_t>(
+                        cpbp_draw(key, draw++) % (p->module_size - t));
+                    std::swap(local[t], local[j]);
+                    const std::uint32_t g = m * p->module_size + local[t];
+                    genes.push_back(g);
+                    present[g] = 1u;
+                }
+            }
+            for (std::uint32_t t = 0; t < p->background;) {
+                const std::uint32_t g = static_cast<std::uint32_t>(cpbp_draw(key, draw++) % p->genes);
+                if (present[g]) continue;
+                present[g] = 1u;
+                genes.push_back(g);
+                ++t;
+            }
+            std::sort(genes.begin(), genes.end());
+            const std::uint32_t off = row_offsets[r];
+            if (row_offsets[r + 1] - off != genes.size()) { bad = 1; continue; }
+            const std::uint64_t vkey = splitmix64(vbase ^ r);
+            for (std::size_t i = 0; i < genes.size(); ++i) {
+                const std::uint32_t u = static_cast<std::uint32_t>(splitmix64(vkey ^ genes[i]) >> 32);
+                features[off + i] = genes[i];
+                values[off + i] = lut[1 + host_nb_draw(cdf, u)];
+                present[genes[i]] = 0u;
+            }
+        }
+    });
+    return bad ? fail("row_offsets disagree with cxs_cpbp_count") : 0;
+}
+
 
 int cxs_qcsr_create(const cxs_qcsr_params *params, cxs_generator **out) {
     if (params == nullptr || out == nullptr) return fail("null argument");

@@ -147,3 +147,55 @@ def generate_bell(cfg: BellConfig, device="cuda") -> BellMatrix:
         values.data_ptr(), s))
     return BellMatrix(cfg.rows, cfg.cols, cfg.block_size, ell_cols, idx, values=values,
                       meta={"config": cfg.name})
+
+
+@dataclass(frozen=True)
+class CpbpConfig:
+    name: str
+    rows: int
+    genes: int = 20_000
+    modules: int = 200
+    module_size: int = 100
+    min_active: int = 3
+    max_active: int = 8
+    active_genes: int = 60  # 60% of a module's genes
+    background: int = 50
+    nb_mean: float = 2.0
+    nb_size: float = 0.5
+    block_width: int = 25  # module-aligned feature blocks (4 per module)
+    tile_row_width: int = 64
+    window_size: int = 1024
+    seed: int = 0xCE11E7A700000005
+
+    def scaled(self, rows: int) -> "CpbpConfig":
+        return CpbpConfig(**{**self.__dict__, "rows": rows, "name": f"{self.name}@{rows}"})
+
+
+# BASELINE.json configs[4]
+C5 = CpbpConfig("C5 CP-BP 2M x 20k, 64-row tiles", 2_000_000)
+
+
+def generate_cpbp_host(cfg: CpbpConfig, threads: int | None = None):
+    """Canonical CSR (row_offsets uint32, features uint32, values float32) of config 5,
+    generated on host threads (include/cellerator_amd_synth.h)."""
+    import os
+
+    import numpy as np
+
+    lib = N.synth()
+    p = N.CxsCpbpParams(cfg.seed, cfg.rows, cfg.genes, cfg.modules, cfg.module_size,
+                        cfg.min_active, cfg.max_active, cfg.active_genes, cfg.background,
+                        cfg.nb_mean, cfg.nb_size)
+    nthreads = threads or min(16, os.cpu_count() or 1)
+    counts = np.zeros(cfg.rows, np.uint32)
+    N.check_synth("cxs_cpbp_count", lib.cxs_cpbp_count(C.byref(p), counts.ctypes.data, nthreads))
+    offs = np.zeros(cfg.rows + 1, np.uint64)
+    np.cumsum(counts, out=offs[1:])
+    if offs[-1] >= 2**32:
+        raise ValueError(f"{cfg.name}: nnz {int(offs[-1])} exceeds uint32 offsets")
+    offs = offs.astype(np.uint32)
+    feats = np.zeros(int(offs[-1]), np.uint32)
+    vals = np.zeros(int(offs[-1]), np.float32)
+    N.check_synth("cxs_cpbp_fill", lib.cxs_cpbp_fill(C.byref(p), offs.ctypes.data, feats.ctypes.data,
+                                                      vals.ctypes.data, nthreads))
+    return offs, feats, vals

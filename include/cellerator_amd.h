@@ -197,6 +197,91 @@ int cx_cpbp_reduce(const cx_cpbp_tiles *tiles, const float *feature_weights,
                    uint64_t feature_weight_capacity, float *row_values,
                    uint64_t row_capacity, void *stream);
 
+/* ---- CP-BP construction (host): canonical CSR -> records -> local order -> tiles ----
+ * Replaces the host producers apply_frozen_plan_host + build_cell_block_records_host +
+ * build_local_cell_order_host + build_warp_tiles_host
+ * (components/CellPack/include/CellPack/apply_plan.hh, cell_block_records.hh,
+ *  local_cell_ordering.hh:13-67, warp_tiles.hh:131-150) for one row partition, and
+ * extends the tile width to 64 rows (u64 cell masks). Runs on host threads; nothing here
+ * touches the GPU. */
+
+/* frozen_packing_plan subset (components/CellPack/include/CellPack/packing_plan.hh:39-128):
+ * feature_permutation[execution] = canonical feature; blocks hold 1..32 execution
+ * features. */
+typedef struct cx_cpbp_plan {
+    uint32_t feature_count;
+    uint32_t feature_block_count;
+    const uint32_t *feature_permutation;   /* feature_count */
+    const uint32_t *feature_block_offsets; /* feature_block_count + 1 */
+} cx_cpbp_plan;
+
+/* plan_application_source_view subset (apply_plan.hh): canonical rows, canonical feature
+ * ids strictly increasing per row, values of value_size_bytes (2 = f16, 4 = f32). */
+typedef struct cx_cpbp_csr {
+    uint32_t rows;
+    uint32_t value_size_bytes;
+    const uint32_t *row_offsets;        /* rows + 1 */
+    const uint32_t *canonical_features; /* row_offsets[rows] */
+    const void *values;                 /* row_offsets[rows] */
+} cx_cpbp_csr;
+
+/* local_cell_order_kind (local_cell_ordering.hh:15-20) */
+#define CX_CPBP_ORDER_INFERRED_MINHASH 1u
+#define CX_CPBP_ORDER_ORIGINAL 2u
+#define CX_CPBP_ORDER_DETERMINISTIC_RANDOM 3u
+#define CX_CPBP_ORDER_ROW_NNZ_DESCENDING 4u
+
+/* local_cell_order_config (local_cell_ordering.hh:22-27) plus the partition's global
+ * row begin used by the deterministic_random keys. group_width is the tile width. */
+typedef struct cx_cpbp_order_config {
+    uint32_t kind;
+    uint32_t window_size; /* reference default 1024 */
+    uint32_t group_width; /* 1..64; window_size % group_width == 0 */
+    uint32_t reserved;
+    uint64_t seed;        /* reference default 0x6a09e667f3bcc909 */
+    uint64_t global_row_begin;
+} cx_cpbp_order_config;
+
+/* Exact output sizes (warp_tile_requirements, warp_tiles.hh:15-22, in elements). */
+typedef struct cx_cpbp_tile_requirements {
+    uint32_t row_count;
+    uint32_t feature_count;
+    uint32_t feature_block_count;
+    uint32_t tile_row_width;
+    uint32_t tile_count;            /* tile_block_offsets holds tile_count + 1 */
+    uint32_t tile_block_count;      /* block_row_entry_offsets holds this + 1 */
+    uint32_t row_block_entry_count; /* row_block_value_offsets holds this + 1 */
+    uint32_t nnz_count;
+    uint32_t value_size_bytes;
+    uint32_t cell_mask_bytes;       /* 4 (width <= 32) or 8 */
+} cx_cpbp_tile_requirements;
+
+/* Caller-owned host outputs (warp_tile_buffers, warp_tiles.hh:24-38, plus the order). */
+typedef struct cx_cpbp_tile_buffers {
+    uint32_t *tile_block_offsets;
+    uint32_t *tile_block_ids;
+    void *tile_block_cell_masks; /* u32 or u64 per cell_mask_bytes */
+    uint32_t *block_row_entry_offsets;
+    uint32_t *row_block_gene_masks;
+    uint32_t *row_block_value_offsets;
+    void *values;
+    uint32_t *row_permutation;   /* execution row -> canonical partition-local row */
+    uint64_t *primary_keys;      /* optional: local-order primary key per canonical row */
+} cx_cpbp_tile_buffers;
+
+typedef struct cx_cpbp_builder cx_cpbp_builder;
+
+/* Validates and builds everything on `threads` host threads (0 -> 1); the result is
+ * identical for every thread count. Errors: CX_STATUS_*, message in
+ * cx_cpbp_build_last_error(). */
+int cx_cpbp_builder_create(const cx_cpbp_plan *plan, const cx_cpbp_csr *csr,
+                           const cx_cpbp_order_config *config, uint32_t threads,
+                           cx_cpbp_builder **out);
+int cx_cpbp_builder_requirements(const cx_cpbp_builder *builder, cx_cpbp_tile_requirements *out);
+int cx_cpbp_builder_export(const cx_cpbp_builder *builder, const cx_cpbp_tile_buffers *buffers);
+void cx_cpbp_builder_destroy(cx_cpbp_builder *builder);
+const char *cx_cpbp_build_last_error(void);
+
 /* N = 1 CSR comparator: csr_spmv_fwd_f16_f32 (src/compute/sparse/ops/ops.hh:83-90);
  * y[r] = sum fp32(values) * x[col]. values F16 or F32. */
 int cx_csr_spmv_fwd(uint32_t rows, const uint32_t *row_ptr, const uint32_t *col_idx,

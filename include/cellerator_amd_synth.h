@@ -77,6 +77,30 @@ int cxs_bell_generate(uint64_t seed, uint32_t rows, uint32_t cols, uint32_t bloc
                       uint32_t max_blocks, float density, double nb_mean, double nb_size,
                       uint32_t *block_col_idx, uint16_t *values_bf16, void *stream);
 
+/* CP-BP structured-support matrix, generated on `threads` host threads
+ * (identical output for any count). Row r activates k ~ U{min_active..max_active} distinct
+ * modules (module m = genes [m*module_size, (m+1)*module_size)), takes active_genes of each
+ * without replacement, adds `background` genes uniform over the axis excluding genes already
+ * present, sorts; value = log1p(1 + NB(nb_mean, nb_size)) fp32. Pass 1 gives row sizes,
+ * pass 2 fills canonical features and values at the caller's exclusive-scan offsets. */
+typedef struct cxs_cpbp_params {
+    uint64_t seed;
+    uint32_t rows;
+    uint32_t genes;
+    uint32_t modules;
+    uint32_t module_size;
+    uint32_t min_active;
+    uint32_t max_active;
+    uint32_t active_genes;
+    uint32_t background;
+    double nb_mean;
+    double nb_size;
+} cxs_cpbp_params;
+
+int cxs_cpbp_count(const cxs_cpbp_params *params, uint32_t *row_nnz, uint32_t threads);
+int cxs_cpbp_fill(const cxs_cpbp_params *params, const uint32_t *row_offsets, uint32_t *features,
+                  float *values, uint32_t threads);
+
 const char *cxs_last_error(void);
 
 #ifdef __cplusplus
