@@ -133,6 +133,129 @@ def bench_qcsr(args, torch, cfg, n_out: int) -> dict:
     return res
 
 
+def bench_bell(args, torch, cfg) -> dict:
+    """Config 4: Blocked-ELL bf16 SpMM on MFMA (cx_bell_spmm_fwd_packed), N = 256."""
+    import numpy as np
+
+    from cellerator_amd import bell_pack_rhs, bell_spmm_packed
+    from cellerator_amd.synth import dense_normal, generate_bell
+
+    t0 = time.perf_counter()
+    m = generate_bell(cfg)
+    n_out = cfg.n_out
+    w = dense_normal((m.cols, n_out), 0.02, torch.bfloat16, seed=cfg.seed + n_out)
+    packed = bell_pack_rhs(w)
+    out = torch.empty((m.rows, n_out), dtype=torch.float32, device="cuda")
+    valid_blocks = int((m.block_col_idx != -1).sum().item())
+    torch.cuda.synchronize()
+    log(f"generated {cfg.name}: {valid_blocks} valid 32x32 blocks in {time.perf_counter() - t0:.1f}s")
+    stream = torch.cuda.current_stream()
+
+    def launch():
+        bell_spmm_packed(m, packed, n_out, out=out, stream=stream)
+
+    wall_ms, ev = time_launches(torch, launch, args.steps, args.warmup, stream)
+    kern_ms = statistics.mean(ev)
+    bs = m.block_size
+    alg_bytes = (valid_blocks * bs * bs * 2 + m.block_col_idx.numel() * 4 + m.cols * n_out * 2
+                 + m.rows * n_out * 4)
+    flops = 2.0 * valid_blocks * bs * bs * n_out
+    achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
+    res = {
+        "metric": "Blocked-ELL bf16 SpMM on MFMA: effective HBM GB/s (% roofline) and MFMA TFLOP/s, 500k x 20k, N=256",
+        "value": valid_blocks * bs * bs / (wall_ms * 1e-3), "unit": "stored block elements/s",
+        "ms_per_step": wall_ms, "dtype": "bf16-values/bf16-W/f32-accumulate",
+        "config": {"workload": cfg.name, "rows": m.rows, "genes": m.cols, "block_size": bs,
+                   "valid_blocks": valid_blocks, "ell_width": cfg.ell_width, "n_out": n_out,
+                   "seed": hex(cfg.seed)},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(cfg.name),
+                     "kernel": "bell_spmm_mfma<256>", "kernel_ms_mean": kern_ms,
+                     "kernel_ms_median": statistics.median(ev), "algorithmic_bytes": alg_bytes,
+                     "mfma_tflops": flops / (kern_ms * 1e-3) / 1e12,
+                     "mfma_frac_of_bf16_dense_peak": flops / (kern_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS},
+    }
+    if not args.no_cpu:
+        from oracle import pyoracle
+        pyoracle.build()
+        rb = min(min(args.cpu_rows, 4096) // bs, m.rows // bs)
+        rows = rb * bs
+        idx = m.block_col_idx[:rb].cpu().numpy()
+        vals = m.values[:rows].view(torch.int16).cpu().numpy().view(np.uint16)
+        wn = w.view(torch.int16).cpu().numpy().view(np.uint16)
+        t1 = time.perf_counter()
+        pyoracle.bell_spmm_referee(rows, m.cols, bs, m.ell_cols, idx, vals, wn,
+                                   value_type=pyoracle.BF16, rhs_type=pyoracle.BF16,
+                                   want_magnitude=False)
+        t = time.perf_counter() - t1
+        nvalid = int((idx != np.uint32(0xFFFFFFFF).astype(idx.dtype)).sum())
+        res["cpu_baseline"] = {"value": nvalid * bs * bs / t, "unit": "stored block elements/s",
+                               "cores": 1, "kind": "port",
+                               "sample": f"first {rows} of {m.rows} rows ({nvalid} blocks), one pass of "
+                                         f"the oracle's float64 Blocked-ELL referee (single thread)",
+                               "seconds": t}
+    return res
+
+
+def bench_cpbp(args, torch, cfg) -> dict:
+    """Config 5: CP-BP feature-weighted row reduction on 64-row tiles (cx_cpbp_reduce)."""
+    import numpy as np
+
+    from cellerator_amd import cpbp, cpbp_reduce
+    from cellerator_amd.synth import dense_normal, generate_cpbp_host
+
+    t0 = time.perf_counter()
+    offs, feats, vals = generate_cpbp_host(cfg, threads=host_cores())
+    plan = cpbp.contiguous_plan(cfg.genes, cfg.block_width)
+    host = cpbp.build_tiles(plan, offs, feats, vals, group_width=cfg.tile_row_width,
+                            window_size=cfg.window_size, threads=host_cores())
+    tiles = cpbp.to_device(plan, host)
+    weights = dense_normal((cfg.genes,), 1.0, torch.float32, seed=cfg.seed + 1)
+    out = torch.empty(cfg.rows, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    nnz = int(offs[-1])
+    log(f"generated and tiled {cfg.name}: nnz={nnz}, descriptors={host.req['tile_block_count']} "
+        f"in {time.perf_counter() - t0:.1f}s")
+    del host
+    stream = torch.cuda.current_stream()
+
+    def launch():
+        cpbp_reduce(tiles, weights, out=out, stream=stream)
+
+    wall_ms, ev = time_launches(torch, launch, args.steps, args.warmup, stream)
+    kern_ms = statistics.mean(ev)
+    alg_bytes = tiles.nbytes_algorithmic()
+    achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
+    res = {
+        "metric": "CP-BP feature-weighted row reduction: nnz/s + effective HBM GB/s (% roofline), 2M cells, 64-row tiles",
+        "value": nnz / (wall_ms * 1e-3), "unit": "nnz/s", "ms_per_step": wall_ms,
+        "dtype": "f32-values/f32-weights/f32-accumulate",
+        "config": {"workload": cfg.name, "rows": cfg.rows, "genes": cfg.genes, "nnz": nnz,
+                   "tile_row_width": cfg.tile_row_width, "block_width": cfg.block_width,
+                   "tile_blocks": tiles.descriptor().tile_block_count,
+                   "row_block_entries": tiles.descriptor().row_block_entry_count, "seed": hex(cfg.seed)},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(cfg.name),
+                     "kernel": "cpbp_reduce_kernel<u64,f32>", "kernel_ms_mean": kern_ms,
+                     "kernel_ms_median": statistics.median(ev), "algorithmic_bytes": alg_bytes},
+    }
+    if not args.no_cpu:
+        from oracle import pyoracle
+        pyoracle.build()
+        rows = min(args.cpu_rows, cfg.rows)
+        sub_offs = offs[:rows + 1]
+        n = int(sub_offs[-1])
+        wn = weights.cpu().numpy()
+        t1 = time.perf_counter()
+        pyoracle.cpbp_canonical(sub_offs, feats[:n], vals[:n], wn)
+        t = time.perf_counter() - t1
+        res["cpu_baseline"] = {"value": n / t, "unit": "nnz/s", "cores": 1, "kind": "port",
+                               "sample": f"first {rows} of {cfg.rows} rows ({n} nnz), one pass of the "
+                                         f"oracle's canonical referee (fp32 accumulate, single thread)",
+                               "seconds": t}
+    return res
+
+
 def load_traffic(workload: str):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc
     summary (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel calibration), or
@@ -166,7 +289,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c3", choices=["c3", "c3n128", "c2"])
+    ap.add_argument("--config", default="c3", choices=["c3", "c3n128", "c2", "c4", "c5"])
     ap.add_argument("--rows", type=int, default=0, help="override the row count (smaller runs)")
     ap.add_argument("--cpu-rows", type=int, default=100_000)
     ap.add_argument("--no-cpu", action="store_true")
@@ -187,10 +310,17 @@ def main() -> int:
         return calibrate_copy(args.calibrate_copy, max(args.steps, 1))
     from cellerator_amd.synth import C2, C3
 
-    cfg, n_out = {"c3": (C3, 64), "c3n128": (C3, 128), "c2": (C2, 64)}[args.config]
-    if args.rows:
-        cfg = cfg.scaled(args.rows)
-    res = bench_qcsr(args, torch, cfg, n_out)
+    if args.config in ("c4", "c5"):
+        from cellerator_amd.synth import C4, C5
+        cfg = C4 if args.config == "c4" else C5
+        if args.rows:
+            cfg = cfg.scaled(args.rows)
+        res = (bench_bell if args.config == "c4" else bench_cpbp)(args, torch, cfg)
+    else:
+        cfg, n_out = {"c3": (C3, 64), "c3n128": (C3, 128), "c2": (C2, 64)}[args.config]
+        if args.rows:
+            cfg = cfg.scaled(args.rows)
+        res = bench_qcsr(args, torch, cfg, n_out)
     line = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"),
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": res.pop("ms_per_step"), "higher_is_better": True, "scaling": "weak",
