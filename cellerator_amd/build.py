@@ -2,9 +2,13 @@
 
 Outputs (git-ignored, shipped to the GPU box with the tree):
   cellerator_amd/libcellerator_amd.so   -- HIP kernels + C-ABI (include/cellerator_amd.h)
-                                           + the C++ operation-core backend
   cellerator_amd/libcx_synth.so         -- seeded synthetic single-cell inputs on the GPU
                                            (bench/test support, include/cellerator_amd_synth.h)
+  cellerator_amd/libcellerator_amd_cpmath.so
+                                        -- CP-Math operation-core candidates (cpmath/), built
+                                           with g++ against the Cellerator headers when they
+                                           are present (CELLERATOR_INCLUDE, default
+                                           /root/reference/include); links the engine library
 
 Every HIP translation unit is compiled with packed-FP32 instruction selection disabled
 (`-Xclang -target-feature -Xclang -packed-fp32-ops`); the host pass warns that it does
@@ -37,6 +41,8 @@ ENGINE_SOURCES = [
 SYNTH_SOURCES = ["synth.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CXX = os.environ.get("CXX", "g++")
+CELLERATOR_INCLUDE = Path(os.environ.get("CELLERATOR_INCLUDE", "/root/reference/include"))
 COMMON = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -73,6 +79,28 @@ def _link(objs: list[Path], out: Path) -> None:
     os.replace(tmp, out)
 
 
+def build_cpmath(verbose: bool = True) -> Path | None:
+    """Builds the CP-Math candidate library where the Cellerator headers are available;
+    elsewhere a previously built library is left in place."""
+    out = PKG / "libcellerator_amd_cpmath.so"
+    header = CELLERATOR_INCLUDE / "Cellerator/compute/math/operation_core/operation_core.hh"
+    if not header.exists():
+        if verbose:
+            print(f"Cellerator headers not found under {CELLERATOR_INCLUDE}: "
+                  f"{out.name} not rebuilt", file=sys.stderr)
+        return out if out.exists() else None
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [CXX, "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra",
+           f"-I{CELLERATOR_INCLUDE}", f"-I{ROOT / 'include'}",
+           str(PKG / "cpmath" / "cpmath_backend.cc"), "-o", str(tmp),
+           f"-L{PKG}", "-lcellerator_amd", "-Wl,-rpath,$ORIGIN"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"CP-Math backend build failed:\n{res.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def build(verbose: bool = True) -> dict[str, Path]:
     """Compiles every HIP/C++ source (always, also when a library exists) and links."""
     BUILD.mkdir(exist_ok=True)
@@ -88,9 +116,11 @@ def build(verbose: bool = True) -> dict[str, Path]:
     _link([BUILD / (Path(n).stem + ".o") for n in ENGINE_SOURCES], engine)
     _link([BUILD / (Path(n).stem + ".o") for n in SYNTH_SOURCES], synth)
     shutil.rmtree(BUILD, ignore_errors=True)
+    cpmath = build_cpmath(verbose)
     if verbose:
-        print(f"built {engine.name} and {synth.name} for {ARCH}")
-    return {"engine": engine, "synth": synth}
+        extra = f" and {cpmath.name}" if cpmath is not None else ""
+        print(f"built {engine.name}, {synth.name} for {ARCH}{extra}")
+    return {"engine": engine, "synth": synth, "cpmath": cpmath}
 
 
 if __name__ == "__main__":

@@ -1,0 +1,495 @@
+// CP-Math operation-core backend: candidate records, prepare (freezes the binding contract
+// from a declared projection) and run (checks the launch against the prepared projection,
+// then calls the engine's C-ABI on the launch stream). The interface is described in
+// cpmath_backend.hh.
+#include "cpmath_backend.hh"
+
+#include <cstring>
+#include <mutex>
+
+namespace cellerator_amd::cpmath {
+namespace {
+
+using execution::i64;
+using execution::numeric_type;
+using execution::u32;
+using execution::u64;
+using code = core::operation_status_code;
+
+constexpr u32 projection_capacity = 64u;
+// The MFMA Blocked-ELL path packs W into the launch workspace: ceil(genes/32)*32 * N * 2
+// bytes, at most this many (65,536 genes x 256 columns of bf16).
+constexpr u64 mfma_panel_limit = 65536ull * 256ull * 2ull;
+
+struct projection_state {
+    bool live = false;
+    projection_declaration declaration{};
+    execution::operand_axis_contract inputs[2]{};
+    execution::operand_axis_contract outputs[1]{};
+    execution::output_axis_contract orders[2]{};
+    execution::output_effect_contract effects[1]{};
+    u32 order_count = 0u;
+};
+
+projection_state projections[projection_capacity];
+std::mutex projections_mutex;
+thread_local char engine_error[512] = "";
+
+constexpr core::operation_status fail(code c, const char *message) noexcept {
+    return {c, execution::binding_validation_code::ok, message};
+}
+
+constexpr core::operation_status bad_launch(const char *message) noexcept {
+    return {code::invalid_launch_bindings,
+        execution::binding_validation_code::invalid_operand, message};
+}
+
+core::operation_status engine_failed(int rc) noexcept {
+    const char *text = cx_last_error();
+    std::strncpy(engine_error, text != nullptr ? text : "", sizeof(engine_error) - 1u);
+    engine_error[sizeof(engine_error) - 1u] = '\0';
+    return rc == CX_STATUS_HIP_ERROR
+        ? fail(code::execution_failed, "engine kernel launch failed (see last_engine_error)")
+        : fail(code::execution_failed, "engine rejected the launch (see last_engine_error)");
+}
+
+// ---- numeric policies ----------------------------------------------------------------
+
+bool common_numeric(const core::numeric_policy &n) noexcept {
+    return n.output_storage == numeric_type::f32 && n.multiply == numeric_type::f32
+        && n.accumulation == numeric_type::f32 && n.scalar == numeric_type::f32
+        && n.bias == numeric_type::invalid
+        && n.rounding == core::rounding_policy::nearest_even
+        && n.saturation == core::saturation_policy::none;
+}
+
+bool supports_quantized_csr(const core::numeric_policy &n) noexcept {
+    if (!common_numeric(n)) return false;
+    if (n.dense_storage != numeric_type::f16 && n.dense_storage != numeric_type::f32)
+        return false;
+    if (n.sparse_storage == numeric_type::u8)
+        return n.quantization == core::quantization_granularity::module;
+    return (n.sparse_storage == numeric_type::f16 || n.sparse_storage == numeric_type::f32)
+        && n.quantization == core::quantization_granularity::none;
+}
+
+bool plain_storage(numeric_type t) noexcept {
+    return t == numeric_type::bf16 || t == numeric_type::f16 || t == numeric_type::f32;
+}
+
+bool supports_blocked_ell(const core::numeric_policy &n) noexcept {
+    return common_numeric(n) && plain_storage(n.sparse_storage)
+        && plain_storage(n.dense_storage)
+        && n.quantization == core::quantization_granularity::none;
+}
+
+bool supports_cpbp(const core::numeric_policy &n) noexcept {
+    return common_numeric(n)
+        && (n.sparse_storage == numeric_type::f16 || n.sparse_storage == numeric_type::f32)
+        && n.dense_storage == numeric_type::f32
+        && n.quantization == core::quantization_granularity::none;
+}
+
+std::uint32_t engine_dtype(numeric_type t) noexcept {
+    switch (t) {
+    case numeric_type::f16: return CELLERATOR_DTYPE_F16;
+    case numeric_type::bf16: return CELLERATOR_DTYPE_BF16;
+    case numeric_type::f32: return CELLERATOR_DTYPE_F32;
+    default: return CELLERATOR_DTYPE_INVALID;
+    }
+}
+
+// ---- launch checks --------------------------------------------------------------------
+
+const projection_state *state_of(const core::prepared_operation &prepared) noexcept {
+    if (prepared.persistent.data == nullptr
+        || prepared.persistent.bytes != sizeof(projection_state))
+        return nullptr;
+    const auto *state = static_cast<const projection_state *>(prepared.persistent.data);
+    if (!state->live
+        || !execution::same_handle(state->declaration.key.runtime, prepared.projection.runtime))
+        return nullptr;
+    return state;
+}
+
+bool on_launch_device(const execution::device_location &where, const execution::launch_bindings &l) noexcept {
+    return (where.residency == execution::residency_kind::device
+               || where.residency == execution::residency_kind::managed)
+        && where.device_ordinal == l.stream.device_ordinal;
+}
+
+// The sparse operand must carry the prepared projection and its structure, with the
+// engine's physical view of `view_bytes` as projection data.
+const void *physical_view(const projection_state &s, const execution::launch_bindings &l,
+                          u64 view_bytes) noexcept {
+    const execution::biological_operand_view &op = l.inputs[0];
+    if (op.kind != execution::operand_kind::sparse_relation) return nullptr;
+    const execution::sparse_relation_view &rel = op.storage.relation;
+    if (!execution::same_handle(rel.projection, s.declaration.key.runtime)
+        || !execution::same_handle(rel.structure, s.declaration.structure.identity)
+        || rel.epoch.value != s.declaration.structure.epoch.value
+        || rel.projection_bytes != view_bytes)
+        return nullptr;
+    return rel.projection_data;
+}
+
+const execution::value_plane *value_plane_of(const projection_state &s,
+                                             const core::prepared_operation &p,
+                                             const execution::launch_bindings &l) noexcept {
+    if (l.value_count != 1u || l.values == nullptr || l.values[0].plane == nullptr) return nullptr;
+    const execution::value_plane *plane = l.values[0].plane;
+    if (!execution::same_handle(plane->structure, s.declaration.structure.identity)
+        || plane->numeric.storage != p.numeric.sparse_storage
+        || !on_launch_device(plane->location, l))
+        return nullptr;
+    return plane;
+}
+
+// Row-major matrix [rows x cols] (rank 2, unit inner stride) or vector [rows] (rank 1).
+bool dense_shape(const execution::dense_tensor_view &v, numeric_type type, u32 rank, u64 rows,
+                 u64 cols, const execution::launch_bindings &l) noexcept {
+    if (v.value_type != type || v.rank != rank || v.shape[0] != rows || v.data == nullptr
+        || !on_launch_device(v.location, l))
+        return false;
+    if (rank == 1u) return v.stride[0] == 1;
+    return v.shape[1] == cols && v.stride[1] == 1 && v.stride[0] >= static_cast<i64>(cols);
+}
+
+// ---- run functions --------------------------------------------------------------------
+
+core::operation_status run_quantized_csr(const core::prepared_operation &p,
+                                         const execution::launch_bindings &l) noexcept {
+    const projection_state *s = state_of(p);
+    if (s == nullptr) return fail(code::execution_failed, "prepared operation has no live projection state");
+    const projection_declaration &d = s->declaration;
+    const void *view = physical_view(*s, l, sizeof(cx_qcsr_matrix));
+    if (view == nullptr) return bad_launch("sparse operand does not carry the prepared quantized CSR view");
+    cx_qcsr_matrix a;
+    std::memcpy(&a, view, sizeof(a));
+    if (a.rows != d.rows || a.cols != d.cols || a.bits != p.projection.variant
+        || a.nnz != d.structure.logical_edge_count)
+        return bad_launch("quantized CSR view differs from the declared projection");
+    if (a.packed_values != nullptr || a.values != nullptr || a.column_scales != nullptr
+        || a.column_offsets != nullptr || a.row_offsets != nullptr)
+        return bad_launch("values and quantization metadata travel in the value plane");
+    const execution::value_plane *plane = value_plane_of(*s, p, l);
+    if (plane == nullptr || plane->element_count != a.nnz)
+        return bad_launch("one value plane of the structure with nnz elements is required");
+    const execution::quantization_descriptor &q = plane->quantization;
+    if (a.bits != 0u) {
+        if (q.kind != execution::quantization_kind::per_module || q.group_count != a.cols
+            || q.scale_type != numeric_type::f32
+            || (q.offsets != nullptr && q.offset_type != numeric_type::f32))
+            return bad_launch("quantized values need per-gene f32 scales (and offsets)");
+        a.decode_policy = CX_DECODE_PER_GENE_AFFINE;
+        a.packed_values = static_cast<const uint8_t *>(plane->values);
+        a.column_scales = static_cast<const float *>(q.scales);
+        a.column_offsets = static_cast<const float *>(q.offsets);
+    } else {
+        if (q.kind != execution::quantization_kind::none)
+            return bad_launch("plain CSR values must not be quantized");
+        a.values = plane->values;
+        a.value_dtype = engine_dtype(plane->numeric.storage);
+    }
+    const execution::dense_tensor_view &w = l.inputs[1].storage.dense;
+    execution::dense_tensor_view y = l.outputs[0].storage.dense;
+    if (l.inputs[1].kind != execution::operand_kind::dense_tensor
+        || !dense_shape(w, p.numeric.dense_storage, 2u, d.cols, d.output_columns, l))
+        return bad_launch("W must be a row-major [genes x N] tensor of the dense storage type");
+    if (!dense_shape(y, numeric_type::f32, 2u, d.rows, d.output_columns, l))
+        return bad_launch("Y must be a row-major f32 [cells x N] tensor");
+    const int rc = cx_qcsr_spmm_fwd(&a, w.data, engine_dtype(w.value_type), w.stride[0],
+                                    d.output_columns, static_cast<float *>(y.data), y.stride[0],
+                                    l.stream.stream);
+    return rc == CX_STATUS_SUCCESS ? core::operation_status{} : engine_failed(rc);
+}
+
+core::operation_status run_blocked_ell(const core::prepared_operation &p,
+                                       const execution::launch_bindings &l) noexcept {
+    const projection_state *s = state_of(p);
+    if (s == nullptr) return fail(code::execution_failed, "prepared operation has no live projection state");
+    const projection_declaration &d = s->declaration;
+    const void *view = physical_view(*s, l, sizeof(cx_bell_matrix));
+    if (view == nullptr) return bad_launch("sparse operand does not carry the prepared Blocked-ELL view");
+    cx_bell_matrix a;
+    std::memcpy(&a, view, sizeof(a));
+    if (a.rows != d.rows || a.cols != d.cols || a.block_size != d.block_size || a.bits != 0u)
+        return bad_launch("Blocked-ELL view differs from the declared projection");
+    if (a.values != nullptr || a.packed_values != nullptr || a.column_scales != nullptr
+        || a.column_offsets != nullptr || a.row_offsets != nullptr)
+        return bad_launch("Blocked-ELL values travel in the value plane");
+    const execution::value_plane *plane = value_plane_of(*s, p, l);
+    if (plane == nullptr || plane->layout != execution::value_layout_kind::projection_local_order
+        || plane->quantization.kind != execution::quantization_kind::none
+        || plane->element_count != static_cast<u64>(a.rows) * a.ell_cols)
+        return bad_launch("one projection-order value plane of rows x ell_cols values is required");
+    a.values = plane->values;
+    a.value_dtype = engine_dtype(plane->numeric.storage);
+    const execution::dense_tensor_view &w = l.inputs[1].storage.dense;
+    const execution::dense_tensor_view &y = l.outputs[0].storage.dense;
+    if (l.inputs[1].kind != execution::operand_kind::dense_tensor
+        || !dense_shape(w, p.numeric.dense_storage, 2u, d.cols, d.output_columns, l))
+        return bad_launch("W must be a row-major [genes x N] tensor of the dense storage type");
+    if (!dense_shape(y, numeric_type::f32, 2u, d.rows, d.output_columns, l))
+        return bad_launch("Y must be a row-major f32 [cells x N] tensor");
+    int rc;
+    if (core::same_stable_id(p.kernel, blocked_ell_mfma_kernel_id)) {
+        auto *panel = static_cast<uint16_t *>(l.workspace.data);
+        rc = cx_bell_pack_rhs(static_cast<const uint16_t *>(w.data), w.stride[0], d.cols,
+                              d.output_columns, panel, l.stream.stream);
+        if (rc == CX_STATUS_SUCCESS)
+            rc = cx_bell_spmm_fwd_packed(&a, panel, d.output_columns,
+                                         static_cast<float *>(y.data), y.stride[0],
+                                         l.stream.stream);
+    } else {
+        rc = cx_bell_spmm_fwd(&a, w.data, engine_dtype(w.value_type), w.stride[0],
+                              d.output_columns, static_cast<float *>(y.data), y.stride[0],
+                              l.stream.stream);
+    }
+    return rc == CX_STATUS_SUCCESS ? core::operation_status{} : engine_failed(rc);
+}
+
+core::operation_status run_cpbp(const core::prepared_operation &p,
+                                const execution::launch_bindings &l) noexcept {
+    const projection_state *s = state_of(p);
+    if (s == nullptr) return fail(code::execution_failed, "prepared operation has no live projection state");
+    const projection_declaration &d = s->declaration;
+    const void *view = physical_view(*s, l, sizeof(cx_cpbp_tiles));
+    if (view == nullptr) return bad_launch("sparse operand does not carry the prepared CP-BP tile view");
+    cx_cpbp_tiles t;
+    std::memcpy(&t, view, sizeof(t));
+    if (t.row_count != d.rows || t.feature_count != d.cols
+        || t.nnz_count != d.structure.logical_edge_count)
+        return bad_launch("CP-BP tile view differs from the declared projection");
+    if (t.values != nullptr) return bad_launch("CP-BP values travel in the value plane");
+    const execution::value_plane *plane = value_plane_of(*s, p, l);
+    if (plane == nullptr || plane->layout != execution::value_layout_kind::projection_local_order
+        || plane->quantization.kind != execution::quantization_kind::none
+        || plane->element_count != t.nnz_count)
+        return bad_launch("one projection-order value plane of nnz values is required");
+    t.values = plane->values;
+    t.value_dtype = engine_dtype(plane->numeric.storage);
+    const execution::dense_tensor_view &w = l.inputs[1].storage.dense;
+    const execution::dense_tensor_view &y = l.outputs[0].storage.dense;
+    if (l.inputs[1].kind != execution::operand_kind::dense_tensor
+        || !dense_shape(w, numeric_type::f32, 1u, d.cols, 0u, l))
+        return bad_launch("feature weights must be a contiguous f32 [genes] tensor");
+    if (!dense_shape(y, numeric_type::f32, 1u, d.rows, 0u, l))
+        return bad_launch("row values must be a contiguous f32 [cells] tensor");
+    const int rc = cx_cpbp_reduce(&t, static_cast<const float *>(w.data), d.cols,
+                                  static_cast<float *>(y.data), d.rows, l.stream.stream);
+    return rc == CX_STATUS_SUCCESS ? core::operation_status{} : engine_failed(rc);
+}
+
+// ---- prepare --------------------------------------------------------------------------
+
+projection_state *find_live(execution::projection_handle handle) noexcept {
+    for (projection_state &s : projections)
+        if (s.live && execution::same_handle(s.declaration.key.runtime, handle)) return &s;
+    return nullptr;
+}
+
+u64 mfma_panel_bytes(const projection_declaration &d) noexcept {
+    return (static_cast<u64>(d.cols) + 31u) / 32u * 32u * d.output_columns * 2u;
+}
+
+bool mfma_eligible(const projection_declaration &d, const core::numeric_policy &n) noexcept {
+    return n.sparse_storage == numeric_type::bf16 && n.dense_storage == numeric_type::bf16
+        && d.block_size == 32u
+        && (d.output_columns == 64u || d.output_columns == 128u || d.output_columns == 256u)
+        && mfma_panel_bytes(d) <= mfma_panel_limit;
+}
+
+core::operation_status prepare(
+    const core::operation_candidate &candidate,
+    const core::operation_problem &problem,
+    const core::structure_set_key &structures,
+    const core::projection_key &projection,
+    const core::numeric_policy &numeric,
+    const core::prepare_policy &policy,
+    core::prepared_operation *prepared) noexcept {
+    if (prepared == nullptr) return fail(code::invalid_argument, "prepare needs an output record");
+    std::lock_guard<std::mutex> lock(projections_mutex);
+    projection_state *state = find_live(projection.runtime);
+    if (state == nullptr)
+        return fail(code::unsupported_projection, "projection was not declared to the engine backend");
+    const projection_declaration &d = state->declaration;
+    if (!execution::same_identity(d.key.persistent, projection.persistent)
+        || d.key.kind != projection.kind || d.key.schema_version != projection.schema_version
+        || d.key.variant != projection.variant || candidate.projection != projection.kind)
+        return fail(code::unsupported_projection, "projection key differs from its declaration");
+    if (structures.count != 1u
+        || !execution::same_handle(structures.structures[0].runtime, d.structure.identity)
+        || structures.structures[0].epoch.value != d.structure.epoch.value
+        || !execution::same_identity(structures.structures[0].persistent, d.persistent_structure))
+        return {code::stale_structure, execution::binding_validation_code::stale_structure,
+            "structure key differs from the declared projection's structure"};
+    if (problem.input_count != 2u || problem.output_count != 1u)
+        return fail(code::unsupported_problem,
+            "operation takes one sparse and one dense input and one output");
+    if (projection.kind == core::projection_kind::csr
+        && (projection.variant != 0u) != (numeric.sparse_storage == numeric_type::u8))
+        return fail(code::unsupported_numeric_policy,
+            "code width in the projection variant disagrees with the sparse storage type");
+
+    core::stable_id kernel = candidate.identity;
+    core::run_function run = run_quantized_csr;
+    u64 workspace = 0u;
+    if (candidate.operation == core::operation_kind::weighted_relation_reduce) {
+        run = run_cpbp;
+    } else if (projection.kind == core::projection_kind::blocked_ell) {
+        const bool mfma = mfma_eligible(d, numeric);
+        kernel = mfma ? blocked_ell_mfma_kernel_id : blocked_ell_generic_kernel_id;
+        workspace = mfma ? mfma_panel_bytes(d) : 0u;
+        run = run_blocked_ell;
+    }
+    if (policy.transient_memory_limit != 0u && workspace > policy.transient_memory_limit)
+        return fail(code::capability_rejected, "candidate exceeds memory policy");
+
+    *prepared = core::prepared_operation{};
+    prepared->problem = problem;
+    prepared->structures = structures;
+    prepared->projection = projection;
+    prepared->numeric = numeric;
+    prepared->kernel = kernel;
+    prepared->backend = core::backend_kind::native_direct;
+    prepared->capability_flags = candidate.capability_flags;
+    prepared->persistent = {state, sizeof(*state)};
+    prepared->binding_contract.structures[0] = {d.structure.identity, d.structure.epoch};
+    prepared->binding_contract.inputs = state->inputs;
+    prepared->binding_contract.outputs = state->outputs;
+    prepared->binding_contract.output_orders = state->orders;
+    prepared->binding_contract.output_effects = state->effects;
+    prepared->binding_contract.input_count = 2u;
+    prepared->binding_contract.output_count = 1u;
+    prepared->binding_contract.output_order_count = state->order_count;
+    prepared->binding_contract.structure_count = 1u;
+    prepared->binding_contract.output_effect_count = 1u;
+    prepared->binding_contract.workspace = {workspace, 256u, 0u};
+    prepared->run = run;
+    return {};
+}
+
+core::operation_candidate candidate(core::stable_id id, const char *name,
+                                    core::operation_kind operation,
+                                    core::projection_kind projection,
+                                    core::numeric_support_function supports,
+                                    u64 transient_bytes) noexcept {
+    core::operation_candidate c{};
+    c.identity = id;
+    c.name = name;
+    c.operation = operation;
+    c.projection = projection;
+    c.backend = core::backend_kind::native_direct;
+    // Fixed per-row / per-tile summation order, and launches that neither allocate nor
+    // synchronize.
+    c.capability_flags = core::candidate_deterministic | core::candidate_graph_capture;
+    c.persistent_bytes = 0u;  // no device-resident state beyond the caller's operands
+    c.transient_bytes = transient_bytes;
+    c.supports_numeric = supports;
+    c.prepare = prepare;
+    return c;
+}
+
+} // namespace
+
+core::operation_status declare_projection(const projection_declaration &d) noexcept {
+    const core::projection_key &k = d.key;
+    if (!execution::valid_identity(k.persistent) || !execution::valid_handle(k.runtime)
+        || k.schema_version != physical_view_schema)
+        return fail(code::invalid_argument, "projection key is incomplete or of another schema");
+    const bool multiply = k.kind == core::projection_kind::csr
+        || k.kind == core::projection_kind::blocked_ell;
+    if (!multiply && k.kind != core::projection_kind::native_row_masked)
+        return fail(code::unsupported_projection, "engine backend serves csr, blocked_ell and native_row_masked");
+    if (execution::validate_relation_structure(d.structure) != execution::lifetime_validation_code::ok
+        || !execution::valid_identity(d.persistent_structure))
+        return fail(code::stale_structure, "relation structure is invalid");
+    if (d.rows == 0u || d.cols == 0u)
+        return fail(code::invalid_argument, "projection needs rows and genes");
+    if (multiply && (d.output_columns == 0u || !execution::valid_axis_identity(d.output_axis)))
+        return fail(code::invalid_argument, "multiply projection needs an output axis and N");
+    if (!multiply && d.output_columns != 0u)
+        return fail(code::invalid_argument, "the row reduction has no output columns");
+    if (k.kind == core::projection_kind::csr && k.variant != 0u && k.variant != 1u
+        && k.variant != 2u && k.variant != 4u && k.variant != 8u)
+        return fail(code::unsupported_projection, "quantized CSR code width must be 1, 2, 4 or 8");
+    if (k.kind == core::projection_kind::blocked_ell && d.block_size == 0u)
+        return fail(code::invalid_argument, "Blocked-ELL projection needs its block size");
+
+    std::lock_guard<std::mutex> lock(projections_mutex);
+    if (find_live(k.runtime) != nullptr)
+        return fail(code::duplicate_candidate, "projection is already declared");
+    projection_state *slot = nullptr;
+    for (projection_state &s : projections)
+        if (!s.live) { slot = &s; break; }
+    if (slot == nullptr) return fail(code::registry_full, "projection table is full");
+
+    *slot = projection_state{};
+    slot->declaration = d;
+    const execution::axis_identity cells = d.structure.source_axis;
+    const execution::axis_identity genes = d.structure.destination_axis;
+    slot->inputs[0].kind = execution::operand_kind::sparse_relation;
+    slot->inputs[0].rank = 2u;
+    slot->inputs[0].axes[0] = cells;
+    slot->inputs[0].axes[1] = genes;
+    slot->inputs[1].kind = execution::operand_kind::dense_tensor;
+    slot->outputs[0].kind = execution::operand_kind::dense_tensor;
+    slot->orders[0].input_axis = cells;
+    slot->orders[0].output_axis = cells;
+    slot->orders[0].transition = execution::order_transition_kind::preserve;
+    slot->orders[0].axis_index = 0u;
+    if (multiply) {
+        slot->inputs[1].rank = 2u;
+        slot->inputs[1].axes[0] = genes;
+        slot->inputs[1].axes[1] = d.output_axis;
+        slot->outputs[0].rank = 2u;
+        slot->outputs[0].axes[0] = cells;
+        slot->outputs[0].axes[1] = d.output_axis;
+        slot->orders[1].input_axis = d.output_axis;
+        slot->orders[1].output_axis = d.output_axis;
+        slot->orders[1].transition = execution::order_transition_kind::preserve;
+        slot->orders[1].axis_index = 1u;
+        slot->order_count = 2u;
+    } else {
+        slot->inputs[1].rank = 1u;
+        slot->inputs[1].axes[0] = genes;
+        slot->outputs[0].rank = 1u;
+        slot->outputs[0].axes[0] = cells;
+        slot->order_count = 1u;
+    }
+    slot->effects[0] = {execution::output_update_kind::overwrite, false, false, 0u,
+        execution::invalid_scalar_binding_id, execution::invalid_scalar_binding_id};
+    slot->live = true;
+    return {};
+}
+
+core::operation_status retire_projection(execution::projection_handle projection) noexcept {
+    std::lock_guard<std::mutex> lock(projections_mutex);
+    projection_state *s = find_live(projection);
+    if (s == nullptr) return fail(code::invalid_argument, "projection is not declared");
+    s->live = false;
+    return {};
+}
+
+core::operation_candidate quantized_csr_candidate() noexcept {
+    return candidate(quantized_csr_candidate_id, "cellerator-amd-quantized-csr-spmm",
+        core::operation_kind::sparse_dense_multiply, core::projection_kind::csr,
+        supports_quantized_csr, 0u);
+}
+
+core::operation_candidate blocked_ell_candidate() noexcept {
+    return candidate(blocked_ell_candidate_id, "cellerator-amd-blocked-ell-spmm",
+        core::operation_kind::sparse_dense_multiply, core::projection_kind::blocked_ell,
+        supports_blocked_ell, mfma_panel_limit);
+}
+
+core::operation_candidate cpbp_candidate() noexcept {
+    return candidate(cpbp_candidate_id, "cellerator-amd-cpbp-row-reduction",
+        core::operation_kind::weighted_relation_reduce, core::projection_kind::native_row_masked,
+        supports_cpbp, 0u);
+}
+
+const char *last_engine_error() noexcept { return engine_error; }
+
+} // namespace cellerator_amd::cpmath

@@ -1,0 +1,81 @@
+// CP-Math operation-core backend for the MI355X engine: three native candidates that a
+// Cellerator build registers in its candidate_registry
+// (include/Cellerator/compute/math/operation_core/operation_core.hh:195-212) and then
+// prepares and runs through prepare_candidate / run_prepared_operation
+// (src/compute/math/operation_core/operation_core.cc:136-242).
+//
+//   quantized_csr_candidate   sparse_dense_multiply    x csr               x native_direct
+//   blocked_ell_candidate     sparse_dense_multiply    x blocked_ell       x native_direct
+//   cpbp_candidate            weighted_relation_reduce x native_row_masked x native_direct
+//
+// This file compiles against the reference's public headers (types and inline validators
+// only) and links against libcellerator_amd.so, whose C-ABI (include/cellerator_amd.h)
+// launches the HIP kernels. It calls no function of the reference's own libraries.
+//
+// Flow. The operation core's prepare callback receives keys only, so the axes and shapes
+// an operation binds are declared once per projection with declare_projection(); prepare
+// finds the declaration by its projection handle and freezes the binding contract from it.
+// The prepared_operation borrows that declaration (persistent state): retire it only
+// after every prepared operation made from it is gone.
+//
+// Operands of a launch (execution::launch_bindings, launch_bindings.hh:85-97):
+//   inputs[0]  sparse_relation (axes cells x genes). projection_data points to the
+//              engine's typed physical view of the structure -- cx_qcsr_matrix,
+//              cx_bell_matrix or cx_cpbp_tiles -- with every value pointer NULL, and
+//              projection_bytes == sizeof of that view.
+//   values[0]  the value plane of that structure: quantized codes (u8 storage, per-gene
+//              affine as quantization_kind::per_module with one group per gene) or plain
+//              f16 / bf16 / f32 values.
+//   inputs[1]  dense_tensor: W [genes x N] row-major (multiply) or w [genes] (reduce).
+//   outputs[0] dense_tensor f32: Y [cells x N] row-major, or y [cells] in canonical order.
+// The stream is launch.stream.stream (a hipStream_t, NULL = the null stream). Run
+// launches kernels only: it neither allocates, synchronizes nor queries the device.
+#pragma once
+
+#include <Cellerator/compute/math/operation_core/operation_core.hh>
+
+#include <cstdint>
+
+#include "cellerator_amd.h"
+
+namespace cellerator_amd::cpmath {
+
+namespace core = cellerator::compute::math::core;
+namespace execution = cellerator::execution;
+
+// projection_key.schema_version of the engine's physical views.
+inline constexpr std::uint16_t physical_view_schema = 1u;
+
+// Candidate identities; kernel identities of the prepared dispatch.
+inline constexpr core::stable_id quantized_csr_candidate_id{0x4358414d44514353ull, 1u};
+inline constexpr core::stable_id blocked_ell_candidate_id{0x4358414d4442454cull, 1u};
+inline constexpr core::stable_id cpbp_candidate_id{0x4358414d44435042ull, 1u};
+inline constexpr core::stable_id blocked_ell_mfma_kernel_id{0x4358414d4442454cull, 2u};
+inline constexpr core::stable_id blocked_ell_generic_kernel_id{0x4358414d4442454cull, 3u};
+
+// projection_key.variant of a quantized CSR projection: the code width in bits (1, 2, 4,
+// 8), or 0 for plain f16 / f32 values.
+//
+// What the caller states once per projection.
+struct projection_declaration {
+    core::projection_key key{};                 // handle, persistent id, kind, schema, variant
+    execution::relation_structure structure{};  // source axis = cells, destination = genes
+    execution::structure_id persistent_structure{};
+    execution::axis_identity output_axis{};     // the N axis of W and Y (multiply only)
+    std::uint32_t rows = 0u;                    // cells
+    std::uint32_t cols = 0u;                    // genes
+    std::uint32_t output_columns = 0u;          // N (multiply); 0 for the reduction
+    std::uint32_t block_size = 0u;              // Blocked-ELL block edge; 0 otherwise
+};
+
+core::operation_status declare_projection(const projection_declaration &declaration) noexcept;
+core::operation_status retire_projection(execution::projection_handle projection) noexcept;
+
+core::operation_candidate quantized_csr_candidate() noexcept;
+core::operation_candidate blocked_ell_candidate() noexcept;
+core::operation_candidate cpbp_candidate() noexcept;
+
+// Engine error text behind the last execution_failed status of this thread.
+const char *last_engine_error() noexcept;
+
+} // namespace cellerator_amd::cpmath

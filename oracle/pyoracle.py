@@ -39,6 +39,20 @@ def build() -> Path:
     return LIB_PATH
 
 
+REFERENCE_ROOT = Path("/root/reference")
+REF_DIR = HERE / "_ref"
+
+
+def build_reference() -> bool:
+    """Where the reference tree is present, compiles its host-only operation core from
+    source into oracle/_ref/ together with the CP-Math test harness (`make ref`).
+    Elsewhere (the GPU box) the prebuilt files are used as they are."""
+    if not (REFERENCE_ROOT / "src/compute/math/operation_core/operation_core.cc").exists():
+        return False
+    subprocess.run(["make", "-s", "-C", str(HERE), "ref", f"REF={REFERENCE_ROOT}"], check=True)
+    return True
+
+
 def lib() -> C.CDLL:
     global _lib
     if _lib is None:

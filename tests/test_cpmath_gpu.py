@@ -1,0 +1,233 @@
+"""GPU: the engine's CP-Math candidates prepared and run through the reference's own
+operation core (register -> find -> prepare -> run_prepared_operation), checked bitwise
+against the same kernels called directly through the C-ABI and against the oracle.
+Also: rebinding a prepared operation to new W / Y without re-preparing, and capture of
+the run in a HIP graph replayed with fresh inputs."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from tests.cpmath import harness as H
+from tests.helpers import check_against_referee, quantized_fixture, to_device_qcsr
+
+pytestmark = pytest.mark.gpu
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def qcsr_case(m, w, y, bits_view=None):
+    """HCase for a device QcsrMatrix `m`: the view keeps the structure arrays only."""
+    import torch
+
+    d = m.descriptor()
+    view = type(d).from_buffer_copy(d)
+    view.packed_values = view.values = view.column_scales = view.column_offsets = None
+    view.row_offsets = None
+    view.decode_policy = 0
+    quantized = m.bits != 0
+    vals = m.packed_values if quantized else m.values
+    dense = H.NT_F16 if w.dtype == torch.float16 else H.NT_F32
+    sparse = H.NT_U8 if quantized else (H.NT_F16 if vals.dtype == torch.float16 else H.NT_F32)
+    c = H.HCase(kind=H.KIND_QCSR, view=C.addressof(view), view_bytes=C.sizeof(view),
+                variant=m.bits, rows=m.rows, cols=m.cols, out_cols=w.shape[1], block_size=0,
+                sparse_type=sparse, dense_type=dense, nnz=m.nnz, values=vals.data_ptr(),
+                value_count=m.nnz, value_bytes=vals.numel() * vals.element_size(),
+                scales=_ptr(m.column_scales), offsets=_ptr(m.column_offsets), w=w.data_ptr(),
+                w_ld=w.stride(0), y=y.data_ptr(), y_ld=y.stride(0),
+                stream=torch.cuda.current_stream().cuda_stream, device=torch.cuda.current_device())
+    c._keep = (view, m, w, y)
+    return c
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantized_csr_through_reference_core(oracle, bits):
+    import torch
+
+    from cellerator_amd import qcsr_spmm
+    rng = np.random.default_rng(40 + bits)
+    fx = quantized_fixture(oracle, rng, 900, 1700, 60.0, bits, oracle.PER_GENE_AFFINE,
+                           empty_every=13)
+    m = to_device_qcsr(fx)
+    w_host = (rng.standard_normal((fx["cols"], 64)) * 0.02).astype(np.float16)
+    w = torch.from_numpy(w_host).cuda()
+    y = torch.full((fx["rows"], 64), float("nan"), device="cuda")
+    r = H.run(qcsr_case(m, w, y))
+    assert (r.prepare_status, r.status) == (H.OK, H.OK), (r.message, r.engine)
+    torch.cuda.synchronize()
+    direct = qcsr_spmm(m, w)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), direct.view(torch.int32))
+    ref, mag = oracle.qcsr_spmm_referee(bits, fx["policy"], fx["rows"], fx["cols"], fx["row_ptr"],
+                                        fx["packed_row_ptr"], fx["col_idx"], fx["packed"],
+                                        fx["scales"], fx["offsets"], None, w_host)
+    check_against_referee(oracle, ref, mag, y.cpu().numpy())
+
+
+def test_rebinding_without_reprepare(oracle):
+    import torch
+
+    from cellerator_amd import qcsr_spmm
+    rng = np.random.default_rng(7)
+    fx = quantized_fixture(oracle, rng, 500, 800, 40.0, 4, oracle.PER_GENE_AFFINE)
+    m = to_device_qcsr(fx)
+    w1 = (torch.randn(fx["cols"], 128, device="cuda") * 0.02).half()
+    w2 = (torch.randn(fx["cols"], 128, device="cuda") * 0.02).half()
+    y1 = torch.empty(fx["rows"], 128, device="cuda")
+    y2 = torch.empty(fx["rows"], 128, device="cuda")
+    c = qcsr_case(m, w1, y1)
+    c.w2, c.y2 = w2.data_ptr(), y2.data_ptr()
+    r = H.run(c)
+    assert (r.status, r.second_status) == (H.OK, H.OK), r.message
+    torch.cuda.synchronize()
+    assert torch.equal(y1, qcsr_spmm(m, w1))
+    assert torch.equal(y2, qcsr_spmm(m, w2))
+
+
+def test_plain_f32_csr_through_reference_core():
+    import torch
+
+    from cellerator_amd import QcsrMatrix, qcsr_spmm
+    # tests/sparse_ops_runtime_test.cu:140-161: 3x3 x 3x2 -> {201, 402, 430, 860, 5, 10}
+    row_ptr = torch.tensor([0, 2, 4, 5], dtype=torch.int32).cuda()
+    col_idx = torch.tensor([0, 2, 1, 2, 0], dtype=torch.int32).cuda()
+    vals = torch.tensor([1, 2, 3, 4, 5], dtype=torch.float32).cuda()
+    m = QcsrMatrix(3, 3, 0, row_ptr, col_idx, values=vals)
+    w = torch.tensor([[1, 2], [10, 20], [100, 200]], dtype=torch.float32).cuda()
+    y = torch.zeros(3, 2, device="cuda")
+    r = H.run(qcsr_case(m, w, y))
+    assert r.status == H.OK, r.message
+    torch.cuda.synchronize()
+    assert y.cpu().numpy().ravel().tolist() == [201.0, 402.0, 430.0, 860.0, 5.0, 10.0]
+    assert torch.equal(y, qcsr_spmm(m, w))
+
+
+def bell_case(m, w, y, workspace=None):
+    import torch
+
+    d = m.descriptor()
+    view = type(d).from_buffer_copy(d)
+    view.values = None
+    dense = {torch.bfloat16: H.NT_BF16, torch.float16: H.NT_F16, torch.float32: H.NT_F32}
+    vals = m.values
+    c = H.HCase(kind=H.KIND_BELL, view=C.addressof(view), view_bytes=C.sizeof(view), variant=0,
+                rows=m.rows, cols=m.cols, out_cols=w.shape[1], block_size=m.block_size,
+                sparse_type=dense[vals.dtype], dense_type=dense[w.dtype],
+                nnz=m.rows * m.ell_cols, values=vals.data_ptr(), value_count=vals.numel(),
+                value_bytes=vals.numel() * vals.element_size(), w=w.data_ptr(),
+                w_ld=w.stride(0), y=y.data_ptr(), y_ld=y.stride(0),
+                workspace=_ptr(workspace),
+                workspace_bytes=0 if workspace is None else workspace.numel(),
+                stream=torch.cuda.current_stream().cuda_stream, device=torch.cuda.current_device())
+    c._keep = (view, m, w, y, workspace)
+    return c
+
+
+def _bell(n_rows_blocks=40, cols=1000, width=9, seed=3):
+    import torch
+
+    from cellerator_amd import BellMatrix
+    from tests.test_bell_gpu import _bf16_round, random_bell
+    rng = np.random.default_rng(seed)
+    idx, vals = random_bell(rng, 32 * n_rows_blocks, cols, 32, width)
+    vbits = _bf16_round(vals)
+    m = BellMatrix(32 * n_rows_blocks, cols, 32, width * 32,
+                   torch.from_numpy(idx.view(np.int32)).cuda(),
+                   values=torch.from_numpy(vbits.view(np.int16)).view(torch.bfloat16).cuda())
+    return m, rng
+
+
+@pytest.mark.parametrize("n", [64, 256])
+def test_blocked_ell_mfma_through_reference_core(n):
+    import torch
+
+    from cellerator_amd import bell_pack_rhs, bell_spmm_packed
+    m, rng = _bell()
+    w = (torch.randn(m.cols, n, device="cuda") * 0.02).bfloat16()
+    y = torch.empty(m.rows, n, device="cuda")
+    ws = torch.empty(((m.cols + 31) // 32) * 32 * n * 2, dtype=torch.uint8, device="cuda")
+    r = H.run(bell_case(m, w, y, ws))
+    assert (r.prepare_status, r.status) == (H.OK, H.OK), (r.message, r.engine)
+    assert r.kernel_high == 2 and r.workspace_bytes == ws.numel()
+    torch.cuda.synchronize()
+    direct = bell_spmm_packed(m, bell_pack_rhs(w), n)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), direct.view(torch.int32))
+
+
+def test_blocked_ell_generic_through_reference_core():
+    import torch
+
+    from cellerator_amd import bell_spmm
+    m, rng = _bell(seed=5)
+    w = torch.randn(m.cols, 96, device="cuda") * 0.02
+    y = torch.empty(m.rows, 96, device="cuda")
+    r = H.run(bell_case(m, w, y))
+    assert (r.prepare_status, r.status) == (H.OK, H.OK), (r.message, r.engine)
+    assert r.kernel_high == 3
+    torch.cuda.synchronize()
+    assert torch.equal(y, bell_spmm(m, w))
+
+
+def test_cpbp_through_reference_core(oracle):
+    import torch
+
+    from cellerator_amd import cpbp, cpbp_reduce
+    from tests.test_cpbp_build import random_csr, random_plan
+    rng = np.random.default_rng(17)
+    plan = random_plan(rng, 700)
+    offs, feats, vals = random_csr(rng, 1500, 700, 30.0, np.float32)
+    t = cpbp.build_tiles(plan, offs, feats, vals, group_width=64, window_size=256)
+    dev = cpbp.to_device(plan, t)
+    w = torch.from_numpy(rng.standard_normal(700).astype(np.float32)).cuda()
+    y = torch.empty(1500, device="cuda")
+    d = dev.descriptor()
+    view = type(d).from_buffer_copy(d)
+    view.values = None
+    c = H.HCase(kind=H.KIND_CPBP, view=C.addressof(view), view_bytes=C.sizeof(view), variant=0,
+                rows=1500, cols=700, out_cols=0, block_size=0, sparse_type=H.NT_F32,
+                dense_type=H.NT_F32, nnz=int(t.req["nnz_count"]), values=dev.values.data_ptr(),
+                value_count=dev.values.numel(), value_bytes=dev.values.numel() * 4,
+                w=w.data_ptr(), w_ld=1, y=y.data_ptr(), y_ld=1,
+                stream=torch.cuda.current_stream().cuda_stream, device=torch.cuda.current_device())
+    r = H.run(c)
+    assert (r.prepare_status, r.status) == (H.OK, H.OK), (r.message, r.engine)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), cpbp_reduce(dev, w).view(torch.int32))
+    ref, mag = oracle.cpbp_canonical_f64(offs, feats, vals, w.cpu().numpy())
+    assert np.all(np.abs(y.cpu().numpy() - ref) <= 1e-5 + 1e-5 * np.abs(ref) + 2.0 ** -22 * mag)
+
+
+def test_graph_capture_replays_match_eager(oracle):
+    """The prepared run captured in a HIP graph (candidate_graph_capture), replayed with
+    new W contents, eager work and synchronizations between replays."""
+    import torch
+
+    from cellerator_amd import qcsr_spmm
+    rng = np.random.default_rng(23)
+    fx = quantized_fixture(oracle, rng, 700, 1200, 50.0, 4, oracle.PER_GENE_AFFINE)
+    m = to_device_qcsr(fx)
+    w = (torch.randn(fx["cols"], 64, device="cuda") * 0.02).half()
+    y = torch.empty(fx["rows"], 64, device="cuda")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up launch outside capture
+        assert H.run(qcsr_case(m, w, y)).status == H.OK
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        r = H.run(qcsr_case(m, w, y))
+    assert r.status == H.OK, r.message
+    for step in range(4):
+        w.copy_((torch.randn(fx["cols"], 64, device="cuda") * 0.02).half())
+        y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        eager = qcsr_spmm(m, w)
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager), f"replay {step} differs"
