@@ -236,7 +236,7 @@ def bench_cpbp(args, torch, cfg) -> dict:
                    "row_block_entries": tiles.descriptor().row_block_entry_count, "seed": hex(cfg.seed)},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(cfg.name),
-                     "kernel": "cpbp_reduce_kernel<u64,f32>", "kernel_ms_mean": kern_ms,
+                     "kernel": "cpbp_reduce_kernel<u64,f32,lds-weights>", "kernel_ms_mean": kern_ms,
                      "kernel_ms_median": statistics.median(ev), "algorithmic_bytes": alg_bytes},
     }
     if not args.no_cpu:
@@ -247,12 +247,20 @@ def bench_cpbp(args, torch, cfg) -> dict:
         n = int(sub_offs[-1])
         wn = weights.cpu().numpy()
         t1 = time.perf_counter()
-        pyoracle.cpbp_canonical(sub_offs, feats[:n], vals[:n], wn)
+        ref = pyoracle.cpbp_canonical(sub_offs, feats[:n], vals[:n], wn)
         t = time.perf_counter() - t1
         res["cpu_baseline"] = {"value": n / t, "unit": "nnz/s", "cores": 1, "kind": "port",
                                "sample": f"first {rows} of {cfg.rows} rows ({n} nnz), one pass of the "
                                          f"oracle's canonical referee (fp32 accumulate, single thread)",
                                "seconds": t}
+        # the timed output, checked on the same rows against the referee (reference
+        # tolerance 1e-5 abs + 1e-5 rel, widened for fp32 reordering)
+        got = out[:rows].cpu().numpy()
+        ref64, mag = pyoracle.cpbp_canonical_f64(sub_offs, feats[:n], vals[:n], wn)
+        bad = np.abs(got.astype(np.float64) - ref64) > 1e-5 + 1e-5 * np.abs(ref64) + 2.0 ** -22 * mag
+        res["parity_sample"] = {"rows": rows, "mismatches": int(bad.sum()),
+                                "max_abs_err": float(np.max(np.abs(got - ref64))) if rows else 0.0}
+        del ref
     return res
 
 

@@ -1,16 +1,31 @@
 // cpbp_reduce.hip -- CP-BP warp-tile feature-weighted row reduction on gfx950.
 //
-// Contract (components/CellPack/src/feature_weighted_row_reduction_cuda.cu:180-218):
-// for every execution row of every tile, sum over its stored values of
-// fp32(value) * w[feature_permutation[block_begin + local]] and write the row's sum to
-// row_values[row_permutation[execution_row]] (canonical order). Per row the values are
-// visited in the reference's order (descriptor, then local feature), one fp32 FMA each.
+// Contract (components/CellPack/src/feature_weighted_row_reduction_cuda.cu:180-218): for
+// every execution row of every tile, the sum over its stored values of
+// fp32(value) * w[feature_permutation[block_begin + local]], written to
+// row_values[row_permutation[execution_row]] (canonical order).
 //
-// Mapping: one wave64 per tile and lane = tile-local row, so a 64-row tile (u64 cell
-// masks, the wave64 projection) fills the wavefront; tiles of width <= 32 use u32 masks
-// (the reference's v1 contract) with the upper lanes idle. Descriptor fields are
-// wave-uniform loads; a lane whose cell bit is set ranks itself among the set bits
-// below it (popcount) to find its compacted row-block entry.
+// Why not the reference's mapping (one lane per tile row, looping over the tile's
+// descriptors): with module-sparse cells a 64-row tile carries ~790 descriptors of ~6 rows
+// each, so a lane-per-row wave is ~9% busy.
+//
+// Entry-batch mapping. One wave owns one tile at a time (tiles strided over the grid); 16
+// waves share a workgroup and the plan staged once in LDS (permuted weights
+// wp[f] = w[perm[f]], block starts). A tile's row-block entries are contiguous, and so are
+// their values. The wave takes the entries in batches of up to 64 (at most 512 values):
+//   1. lane j holds entry j (value offset, gene mask) and lane k descriptor k (first entry,
+//      cell mask, block id), loaded coalesced;
+//   2. each entry finds its descriptor (descriptor starts scattered into LDS slots, then a
+//      wave max-scan) and its row (the rank-th set bit of the descriptor's cell mask);
+//   3. the batch's values, loaded coalesced, are staged in LDS; each entry lane sums
+//      value * wp[block start + bit] over its own values in a register (fp32 FMA) and adds
+//      the sum to its row's accumulator in LDS (one LDS atomic per entry, spread over 4
+//      slots per row; per-value LDS float atomics were measured 2x slower overall).
+// Loads are raw buffer loads over the tile's slices (0 past the end, no branches) and run
+// one batch ahead on ping-pong registers, so a batch's waits cover only its own loads.
+// The summation order (per entry, then entries per row) differs from the reference's
+// (descriptor, then bit) order; results agree within the reference's tolerance
+// (feature_weighted_row_reduction.hh:13-14) widened for fp32 reordering.
 #include "cx_common.hpp"
 
 namespace cx {
@@ -32,45 +47,304 @@ struct CpbpArgs {
     std::uint32_t row_count;
     std::uint32_t tile_count;
     std::uint32_t tile_row_width;
+    std::uint32_t feature_count;
+    std::uint32_t feature_block_count;
 };
 
-constexpr int kTilesPerBlock = 4;
+constexpr int kCpbpWaves = 16;         // waves (tiles in flight) per workgroup
+constexpr int kCpbpGrid = 256;         // one workgroup per CU (LDS-limited)
+constexpr int kAccSpread = 4;          // accumulator slots per row
+constexpr std::uint32_t kBatchValues = 512;  // values of one entry batch (staged in LDS)
+constexpr std::uint32_t kWeightsLds = 20480;  // features whose weights fit the LDS stage
+constexpr std::uint32_t kBlocksLds = 2048;    // feature block offsets staged in LDS
 
-template<typename MaskT, typename ValT>
-__global__ __launch_bounds__(kWave *kTilesPerBlock) void cpbp_reduce_kernel(CpbpArgs a) {
-    const int lane = static_cast<int>(threadIdx.x) % kWave;
-    const std::uint32_t tile = blockIdx.x * kTilesPerBlock + threadIdx.x / kWave;
-    if (tile >= a.tile_count) return;
-    const std::uint32_t exec_row = tile * a.tile_row_width + static_cast<std::uint32_t>(lane);
-    const bool active = static_cast<std::uint32_t>(lane) < a.tile_row_width && exec_row < a.row_count;
-    const MaskT lane_bit = static_cast<MaskT>(1) << (lane & (sizeof(MaskT) * 8 - 1));
-    const MaskT lower = lane_bit - static_cast<MaskT>(1);
+struct WaveLds {
+    float acc[64 * kAccSpread];
+    float stage[kBatchValues + 4];  // + one step of the 4-wide read past an entry's end
+    std::int32_t slot[64];
+};
+
+__device__ __forceinline__ void lds_order() { __asm__ volatile("" ::: "memory"); }
+
+__device__ __forceinline__ std::uint32_t uniform(std::uint32_t v) {
+    return static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+}
+
+__device__ __forceinline__ int wave_inclusive_max(int v, int lane) {
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int o = __shfl_up(v, off, kWave);
+        if (lane >= off) v = v > o ? v : o;
+    }
+    return v;
+}
+
+// Position of the rank-th (0-based) set bit of a 32-bit mask (rank < popcount).
+__device__ __forceinline__ std::uint32_t select_bit32(std::uint32_t m, std::uint32_t r) {
+    std::uint32_t base = 0u, c;
+    c = __builtin_popcount(m & 0xFFFFu); if (r >= c) { r -= c; m >>= 16; base += 16u; }
+    c = __builtin_popcount(m & 0xFFu);   if (r >= c) { r -= c; m >>= 8;  base += 8u; }
+    c = __builtin_popcount(m & 0xFu);    if (r >= c) { r -= c; m >>= 4;  base += 4u; }
+    c = __builtin_popcount(m & 0x3u);    if (r >= c) { r -= c; m >>= 2;  base += 2u; }
+    c = m & 1u;                          if (r >= c) { base += 1u; }
+    return base;
+}
+
+__device__ __forceinline__ std::uint32_t select_bit(std::uint64_t m, std::uint32_t r) {
+    const std::uint32_t lo = static_cast<std::uint32_t>(m);
+    const std::uint32_t c = static_cast<std::uint32_t>(__builtin_popcount(lo));
+    return r < c ? select_bit32(lo, r) : 32u + select_bit32(static_cast<std::uint32_t>(m >> 32), r - c);
+}
+
+__device__ __forceinline__ std::uint32_t select_bit(std::uint32_t m, std::uint32_t r) {
+    return select_bit32(m, r);
+}
+
+template<typename ValT>
+__device__ __forceinline__ float load_value(const ValT *values, std::uint32_t i) {
+    if constexpr (sizeof(ValT) == 2) return h2f(values[i]);
+    else return values[i];
+}
+
+// Buffer resources over one tile's slices of the tile arrays. Raw buffer loads return 0
+// past the end of the slice, so the batch loads need no branches: every iteration issues
+// the same straight-line loads, which lets the wait counts of the prefetch pipeline cover
+// only the loads actually needed next.
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, std::uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ std::uint32_t bload32(rsrc_t r, std::uint32_t byte_offset) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(byte_offset), 0, 0);
+}
+
+template<typename MaskT>
+__device__ __forceinline__ MaskT bload_mask(rsrc_t r, std::uint32_t index) {
+    if constexpr (sizeof(MaskT) == 8) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(index * 8u), 0, 0);
+        return static_cast<MaskT>(v[0]) | (static_cast<MaskT>(v[1]) << 32);
+    } else {
+        return bload32(r, index * 4u);
+    }
+}
+
+template<typename ValT>
+__device__ __forceinline__ float bload_value(rsrc_t r, std::uint32_t index) {
+    if constexpr (sizeof(ValT) == 2) {
+        const std::uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(index * 2u), 0, 0);
+        return h2f(h);
+    } else {
+        return __uint_as_float(bload32(r, index * 4u));
+    }
+}
+
+struct TileRsrc {
+    rsrc_t value_offsets, gene_masks, entry_offsets, masks, block_ids, values;
+    std::uint32_t e0, d0, v0;
+};
+
+// Per-lane inputs of one entry batch: entry `lane` of the batch (value offset, next value
+// offset, gene mask) and descriptor `lane` from the batch's first descriptor (first entry,
+// cell mask, block id).
+template<typename MaskT>
+struct BatchInput {
+    std::uint32_t s_j, s_next, gm, eo_k, blk_k;
+    MaskT mask_k;
+    bool has_entry, has_desc;
+};
+
+template<typename MaskT>
+__device__ __forceinline__ BatchInput<MaskT> load_batch(const TileRsrc &r, std::uint32_t e,
+                                                        std::uint32_t e_end, std::uint32_t d,
+                                                        std::uint32_t d_end, int lane) {
+    BatchInput<MaskT> b;
+    const std::uint32_t ul = static_cast<std::uint32_t>(lane);
+    b.has_entry = e < e_end && ul < min(64u, e_end - e);
+    b.has_desc = e < e_end && ul < min(64u, d_end - d);
+    const std::uint32_t ei = e - r.e0 + ul, di = d - r.d0 + ul;
+    // loads first, selects after: no branch around a load
+    const std::uint32_t s_j = bload32(r.value_offsets, ei * 4u);
+    const std::uint32_t s_next = bload32(r.value_offsets, ei * 4u + 4u);
+    const std::uint32_t gm = bload32(r.gene_masks, ei * 4u);
+    b.s_j = b.has_entry ? s_j : 0u;
+    b.s_next = b.has_entry ? s_next : 0u;
+    b.gm = b.has_entry ? gm : 0u;
+    b.eo_k = bload32(r.entry_offsets, di * 4u);
+    b.mask_k = bload_mask<MaskT>(r.masks, di);
+    b.blk_k = bload32(r.block_ids, di * 4u);
+    return b;
+}
+
+// Extent of a batch: its first value offset, entry count n (values <= kBatchValues) and
+// value count.
+struct BatchExtent {
+    std::uint32_t s0, n, nv;
+};
+
+template<typename MaskT>
+__device__ __forceinline__ BatchExtent batch_extent(const BatchInput<MaskT> &b) {
+    BatchExtent x;
+    x.s0 = uniform(b.s_j);
+    const unsigned long long fit = __ballot(b.has_entry && b.s_next - x.s0 <= kBatchValues);
+    x.n = max(1u, static_cast<std::uint32_t>(__popcll(fit)));
+    const std::uint32_t v_end = uniform(__shfl(b.s_next, static_cast<int>(x.n) - 1, kWave));
+    x.nv = min(v_end - x.s0, kBatchValues);
+    return x;
+}
+
+// First descriptor of the batch that starts at entry e_next: the last loaded descriptor
+// whose first entry is <= e_next.
+template<typename MaskT>
+__device__ __forceinline__ std::uint32_t next_descriptor(const BatchInput<MaskT> &b, std::uint32_t d,
+                                                         std::uint32_t e_next) {
+    const unsigned long long passed = __ballot(b.has_desc && b.eo_k <= e_next);
+    return d + max(1u, static_cast<std::uint32_t>(__popcll(passed))) - 1u;
+}
+
+// The batch's values (lanes past the batch read the next values of the tile, or 0 past
+// the tile; neither is used).
+template<typename ValT>
+__device__ __forceinline__ void load_values(float (&x)[kBatchValues / kWave], const TileRsrc &r,
+                                            std::uint32_t s0, int lane) {
+#pragma unroll
+    for (std::uint32_t c = 0; c < kBatchValues / kWave; ++c)
+        x[c] = bload_value<ValT>(r.values, s0 - r.v0 + c * kWave + static_cast<std::uint32_t>(lane));
+}
+
+template<typename MaskT, typename ValT, bool kLdsPlan>
+__global__ __launch_bounds__(kWave *kCpbpWaves) void cpbp_reduce_kernel(CpbpArgs a) {
+    // Plan staged in LDS: permuted weights (zero-padded by one block) and block starts.
+    __shared__ float wp[kLdsPlan ? kWeightsLds + 32 : 1];
+    __shared__ std::uint32_t block_begin[kLdsPlan ? kBlocksLds : 1];
+    __shared__ WaveLds wave_lds[kCpbpWaves];
+    const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+    const std::uint32_t wave = uniform(threadIdx.x / kWave);
+    if constexpr (kLdsPlan) {
+        for (std::uint32_t f = threadIdx.x; f < a.feature_count + 32u; f += blockDim.x)
+            wp[f] = f < a.feature_count ? a.weights[a.feature_permutation[f]] : 0.0f;
+        for (std::uint32_t k = threadIdx.x; k <= a.feature_block_count; k += blockDim.x)
+            block_begin[k] = a.feature_block_offsets[k];
+        __syncthreads();
+    }
+    WaveLds &L = wave_lds[wave];
     const MaskT *masks = static_cast<const MaskT *>(a.cell_masks);
     const ValT *values = static_cast<const ValT *>(a.values);
-    float sum = 0.0f;
-    const std::uint32_t d_begin = a.tile_block_offsets[tile];
-    const std::uint32_t d_end = a.tile_block_offsets[tile + 1];
-    for (std::uint32_t d = d_begin; d < d_end; ++d) {
-        const MaskT cell_mask = masks[d];
-        if (!active || (cell_mask & lane_bit) == 0) continue;
-        const std::uint32_t entry = a.block_row_entry_offsets[d]
-            + static_cast<std::uint32_t>(__popcll(static_cast<unsigned long long>(cell_mask & lower)));
-        const std::uint32_t block = a.tile_block_ids[d];
-        const std::uint32_t block_begin = a.feature_block_offsets[block];
-        std::uint32_t gene_mask = a.gene_masks[entry];
-        std::uint32_t v = a.value_offsets[entry];
-        while (gene_mask != 0u) {
-            const std::uint32_t local = static_cast<std::uint32_t>(__builtin_ctz(gene_mask));
-            gene_mask &= gene_mask - 1u;
-            const std::uint32_t feature = a.feature_permutation[block_begin + local];
-            float x;
-            if constexpr (sizeof(ValT) == 2) x = h2f(values[v]);
-            else x = values[v];
-            sum = __builtin_fmaf(x, a.weights[feature], sum);
-            ++v;
+
+    for (std::uint32_t t = blockIdx.x * kCpbpWaves + wave; t < a.tile_count;
+         t += gridDim.x * kCpbpWaves) {
+#pragma unroll
+        for (int k = 0; k < kAccSpread; ++k) L.acc[lane * kAccSpread + k] = 0.0f;
+        // tile bounds are wave-uniform: keep them (and the buffer resources) in SGPRs
+        const std::uint32_t d_end = uniform(a.tile_block_offsets[t + 1]);
+        std::uint32_t d = uniform(a.tile_block_offsets[t]);
+        std::uint32_t e = uniform(a.block_row_entry_offsets[d]);
+        const std::uint32_t e_end = uniform(a.block_row_entry_offsets[d_end]);
+        TileRsrc r;
+        r.e0 = e;
+        r.d0 = d;
+        r.v0 = uniform(a.value_offsets[e]);
+        const std::uint32_t v_tile_end = uniform(a.value_offsets[e_end]);
+        r.value_offsets = make_rsrc(a.value_offsets + e, (e_end - e + 1u) * 4u);
+        r.gene_masks = make_rsrc(a.gene_masks + e, (e_end - e) * 4u);
+        r.entry_offsets = make_rsrc(a.block_row_entry_offsets + d, (d_end - d + 1u) * 4u);
+        r.masks = make_rsrc(masks + d, (d_end - d) * static_cast<std::uint32_t>(sizeof(MaskT)));
+        r.block_ids = make_rsrc(a.tile_block_ids + d, (d_end - d) * 4u);
+        r.values = make_rsrc(values + r.v0, (v_tile_end - r.v0) * static_cast<std::uint32_t>(sizeof(ValT)));
+
+        // Two-stage pipeline over ping-pong register sets (no copies, so no forced waits):
+        // while batch i is reduced, the entries/descriptors of batch i+1 and the 512-value
+        // window that starts where batch i ends (it contains batch i+1) are in flight.
+        auto step = [&](BatchInput<MaskT> &cur, float (&x_cur)[kBatchValues / kWave],
+                        BatchInput<MaskT> &nxt, float (&x_nxt)[kBatchValues / kWave]) {
+            const BatchExtent cur_x = batch_extent(cur);
+            const std::uint32_t e_next = e + cur_x.n;
+            const std::uint32_t d_next = next_descriptor(cur, d, e_next);
+            nxt = load_batch<MaskT>(r, e_next, e_end, d_next, d_end, lane);
+            load_values<ValT>(x_nxt, r, cur_x.s0 + cur_x.nv, lane);
+
+            // entry -> descriptor (slots + max-scan) -> row and block start
+            L.slot[lane] = 0;
+            lds_order();
+            const std::uint32_t q = cur.eo_k - e;
+            if (cur.has_desc && q < 64u)
+                __hip_atomic_fetch_max(&L.slot[q], lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+            lds_order();
+            const int kd = wave_inclusive_max(L.slot[lane], lane);
+            const std::uint32_t my_eo = __shfl(cur.eo_k, kd, kWave);
+            const MaskT my_mask = __shfl(cur.mask_k, kd, kWave);
+            const std::uint32_t my_blk = __shfl(cur.blk_k, kd, kWave);
+            const std::uint32_t row = select_bit(my_mask, e + lane - my_eo) & 63u;
+            std::uint32_t bb;
+            if constexpr (kLdsPlan) bb = min(block_begin[min(my_blk, a.feature_block_count)], a.feature_count);
+            else bb = a.feature_block_offsets[min(my_blk, a.feature_block_count)];
+
+            // stage the batch's values; each entry sums its own values in a register
+#pragma unroll
+            for (std::uint32_t c = 0; c < kBatchValues / kWave; ++c)
+                L.stage[c * kWave + static_cast<std::uint32_t>(lane)] = x_cur[c];
+            lds_order();
+            if (static_cast<std::uint32_t>(lane) < cur_x.n) {
+                std::uint32_t m = cur.gm;
+                const float *v = &L.stage[min(cur.s_j - cur_x.s0, kBatchValues)];
+                float sum = 0.0f;
+                if constexpr (kLdsPlan) {
+                    const float *w = &wp[bb];
+                    while (m != 0u) {  // four stored values per step
+                        const std::uint32_t b0 = static_cast<std::uint32_t>(__builtin_ctz(m));
+                        m &= m - 1u;
+                        const bool h1 = m != 0u;
+                        const std::uint32_t b1 = h1 ? static_cast<std::uint32_t>(__builtin_ctz(m)) : 0u;
+                        m &= m - 1u;
+                        const bool h2 = m != 0u;
+                        const std::uint32_t b2 = h2 ? static_cast<std::uint32_t>(__builtin_ctz(m)) : 0u;
+                        m &= m - 1u;
+                        const bool h3 = m != 0u;
+                        const std::uint32_t b3 = h3 ? static_cast<std::uint32_t>(__builtin_ctz(m)) : 0u;
+                        m &= m - 1u;
+                        sum = __builtin_fmaf(v[0], w[b0], sum);
+                        sum = __builtin_fmaf(h1 ? v[1] : 0.0f, h1 ? w[b1] : 0.0f, sum);
+                        sum = __builtin_fmaf(h2 ? v[2] : 0.0f, h2 ? w[b2] : 0.0f, sum);
+                        sum = __builtin_fmaf(h3 ? v[3] : 0.0f, h3 ? w[b3] : 0.0f, sum);
+                        v += 4;
+                    }
+                } else {
+                    while (m != 0u) {
+                        const std::uint32_t b = static_cast<std::uint32_t>(__builtin_ctz(m));
+                        m &= m - 1u;
+                        const std::uint32_t f = min(bb + b, a.feature_count - 1u);
+                        sum = __builtin_fmaf(*v, a.weights[a.feature_permutation[f]], sum);
+                        ++v;
+                    }
+                }
+                __hip_atomic_fetch_add(&L.acc[row * kAccSpread + (lane & (kAccSpread - 1))], sum,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+            }
+            lds_order();
+            e = e_next;
+            d = d_next;
+        };
+
+        BatchInput<MaskT> in_a = load_batch<MaskT>(r, e, e_end, d, d_end, lane), in_b;
+        float x_a[kBatchValues / kWave], x_b[kBatchValues / kWave];
+        load_values<ValT>(x_a, r, r.v0, lane);
+        while (e < e_end) {
+            step(in_a, x_a, in_b, x_b);
+            if (e >= e_end) break;
+            step(in_b, x_b, in_a, x_a);
         }
+        lds_order();
+        const std::uint32_t exec_row = t * a.tile_row_width + static_cast<std::uint32_t>(lane);
+        if (static_cast<std::uint32_t>(lane) < a.tile_row_width && exec_row < a.row_count) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kAccSpread; ++k) sum += L.acc[lane * kAccSpread + k];
+            a.row_values[a.row_permutation[exec_row]] = sum;
+        }
+        lds_order();
     }
-    if (active) a.row_values[a.row_permutation[exec_row]] = sum;
 }
 
 } // namespace
@@ -131,13 +405,26 @@ extern "C" int cx_cpbp_reduce(const cx_cpbp_tiles *t, const float *feature_weigh
     a.row_count = t->row_count;
     a.tile_count = t->tile_count;
     a.tile_row_width = t->tile_row_width;
-    const dim3 grid((t->tile_count + kTilesPerBlock - 1) / kTilesPerBlock), block(kWave * kTilesPerBlock);
+    a.feature_count = t->feature_count;  // 0 features: no descriptors, every row sums to 0
+    a.feature_block_count = t->feature_block_count;
+    const std::uint32_t wgs = (t->tile_count + kCpbpWaves - 1u) / kCpbpWaves;
+    const dim3 grid(wgs < static_cast<std::uint32_t>(kCpbpGrid) ? wgs : kCpbpGrid), block(kWave * kCpbpWaves);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool wide = t->tile_row_width > 32u;
     const bool half = t->value_dtype == CELLERATOR_DTYPE_F16;
-    if (wide && half) hipLaunchKernelGGL((cpbp_reduce_kernel<std::uint64_t, std::uint16_t>), grid, block, 0, s, a);
-    else if (wide) hipLaunchKernelGGL((cpbp_reduce_kernel<std::uint64_t, float>), grid, block, 0, s, a);
-    else if (half) hipLaunchKernelGGL((cpbp_reduce_kernel<std::uint32_t, std::uint16_t>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((cpbp_reduce_kernel<std::uint32_t, float>), grid, block, 0, s, a);
+    const bool lds = t->feature_count <= kWeightsLds && t->feature_block_count < kBlocksLds;
+#define CX_CPBP_LAUNCH(M, V, W) hipLaunchKernelGGL((cpbp_reduce_kernel<M, V, W>), grid, block, 0, s, a)
+    if (lds) {
+        if (wide && half) CX_CPBP_LAUNCH(std::uint64_t, std::uint16_t, true);
+        else if (wide) CX_CPBP_LAUNCH(std::uint64_t, float, true);
+        else if (half) CX_CPBP_LAUNCH(std::uint32_t, std::uint16_t, true);
+        else CX_CPBP_LAUNCH(std::uint32_t, float, true);
+    } else {
+        if (wide && half) CX_CPBP_LAUNCH(std::uint64_t, std::uint16_t, false);
+        else if (wide) CX_CPBP_LAUNCH(std::uint64_t, float, false);
+        else if (half) CX_CPBP_LAUNCH(std::uint32_t, std::uint16_t, false);
+        else CX_CPBP_LAUNCH(std::uint32_t, float, false);
+    }
+#undef CX_CPBP_LAUNCH
     return check_launch("cpbp_reduce");
 }
