@@ -92,19 +92,24 @@ def cpu_baseline_qcsr(m, w, sample_rows: int, threads: int) -> dict:
 
 
 def bench_qcsr(args, torch, cfg, n_out: int) -> dict:
-    from cellerator_amd import qcsr_spmm
+    from cellerator_amd import _native as N
+    from cellerator_amd import qcsr_pack_gene_affine, qcsr_spmm
     from cellerator_amd.synth import dense_normal, generate_qcsr
 
     t0 = time.perf_counter()
     m = generate_qcsr(cfg)
     w = dense_normal((m.cols, n_out), 0.02, torch.float16, seed=cfg.seed + n_out)
     out = torch.empty((m.rows, n_out), dtype=torch.float32, device="cuda")
+    # per-gene (scale, offset) interleaved once per metadata generation (untimed, like a
+    # packed weight panel); decodes bit-identically to the separate arrays
+    pairs = bool(m.bits) and m.decode_policy == N.DECODE_PER_GENE_AFFINE and not args.separate_meta
+    mt = qcsr_pack_gene_affine(m) if pairs else m
     torch.cuda.synchronize()
     log(f"generated {cfg.name}: nnz={m.nnz} in {time.perf_counter() - t0:.1f}s")
     stream = torch.cuda.current_stream()
 
     def launch():
-        qcsr_spmm(m, w, out=out, stream=stream)
+        qcsr_spmm(mt, w, out=out, stream=stream)
 
     wall_ms, ev = time_launches(torch, launch, args.steps, args.warmup, stream)
     kern_ms = statistics.mean(ev)
@@ -122,7 +127,8 @@ def bench_qcsr(args, torch, cfg, n_out: int) -> dict:
                    "nnz_per_row_mean": m.nnz / m.rows, "seed": hex(cfg.seed)},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(cfg.name),
-                     "kernel": "qcsr_spmm_rowwave", "kernel_ms_mean": kern_ms,
+                     "kernel": "qcsr_spmm_rowwave" + ("<gene-affine pairs>" if pairs else ""),
+                     "kernel_ms_mean": kern_ms,
                      "kernel_ms_median": statistics.median(ev),
                      "algorithmic_bytes": alg_bytes,
                      "fp32_fma_tflops": flops / (kern_ms * 1e-3) / 1e12,
@@ -130,7 +136,25 @@ def bench_qcsr(args, torch, cfg, n_out: int) -> dict:
     }
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline_qcsr(m, w, args.cpu_rows, host_cores())
+        res["parity_sample"] = parity_sample_qcsr(m, w, out, min(args.cpu_rows, 2000))
     return res
+
+
+def parity_sample_qcsr(m, w, out, rows: int) -> dict:
+    """The timed output's first rows against the oracle's float64 referee, at the tests'
+    tolerance (1e-4 abs-scaled + 1e-4 relative)."""
+    from oracle import pyoracle
+
+    rp = m.row_ptr[: rows + 1].cpu().numpy()
+    prp = m.packed_row_ptr[: rows + 1].cpu().numpy()
+    nnz = int(rp[-1])
+    ref, mag = pyoracle.qcsr_spmm_referee(
+        m.bits, m.decode_policy, rows, m.cols, rp, prp, m.col_idx[:nnz].cpu().numpy(),
+        m.packed_values[: int(prp[-1]) + 16].cpu().numpy(), m.column_scales.cpu().numpy(),
+        m.column_offsets.cpu().numpy(), None, w.cpu().numpy())
+    cmp = pyoracle.compare(ref, out[:rows].cpu().numpy(), 1e-4, 1e-4, mag)
+    return {"rows": rows, "within_tolerance": bool(cmp["within_tolerance"]),
+            "max_relative_error": float(cmp["max_relative_error"])}
 
 
 def bench_bell(args, torch, cfg) -> dict:
@@ -301,6 +325,8 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=0, help="override the row count (smaller runs)")
     ap.add_argument("--cpu-rows", type=int, default=100_000)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--separate-meta", action="store_true",
+                    help="C2/C3: time the separate scale/offset arrays instead of interleaved pairs")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="run only a plain copy of BYTES (rocprofv3 counter calibration)")
     args = ap.parse_args()

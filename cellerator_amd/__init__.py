@@ -6,7 +6,7 @@ feature-weighted row reduction. This package is the Python host mirror of that A
 PyTorch supplies device memory and streams only.
 """
 from .engine import (BellMatrix, CpbpTiles, QcsrMatrix, bell_pack_rhs, bell_spmm,  # noqa: F401
-                     bell_spmm_packed, cpbp_reduce, csr_spmv, qcsr_spmm)
+                     bell_spmm_packed, cpbp_reduce, csr_spmv, qcsr_pack_gene_affine, qcsr_spmm)
 
 __all__ = ["QcsrMatrix", "BellMatrix", "CpbpTiles", "qcsr_spmm", "bell_spmm", "bell_pack_rhs",
-           "bell_spmm_packed", "cpbp_reduce", "csr_spmv"]
+           "bell_spmm_packed", "cpbp_reduce", "csr_spmv", "qcsr_pack_gene_affine"]

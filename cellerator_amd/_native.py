@@ -16,7 +16,7 @@ SYNTH_PATH = PKG / "libcx_synth.so"
 
 # cellerator_dtype (include/cellerator_amd.h)
 DTYPE_F16, DTYPE_F32, DTYPE_U8, DTYPE_U32, DTYPE_BF16 = 1, 2, 3, 4, 5
-DECODE_PER_GENE_AFFINE, DECODE_COLUMN_SCALE_ROW_OFFSET = 1, 2
+DECODE_PER_GENE_AFFINE, DECODE_COLUMN_SCALE_ROW_OFFSET, DECODE_PER_GENE_AFFINE_PAIRS = 1, 2, 3
 STATUS_NAMES = {0: "SUCCESS", 1: "INVALID_ARGUMENT", 2: "INVALID_SHAPE", 3: "UNSUPPORTED",
                 4: "HIP_ERROR", 5: "INTERNAL_ERROR"}
 
@@ -127,6 +127,7 @@ class CelleratorSparseLayoutDesc(C.Structure):
 # Every symbol include/cellerator_amd.h declares, with its ctypes signature.
 ENGINE_SIGNATURES = {
     "cx_qcsr_spmm_fwd": (C.c_int, [C.POINTER(CxQcsrMatrix), p_void, u32, i64, i64, p_void, i64, p_void]),
+    "cx_qcsr_pack_gene_affine": (C.c_int, [p_void, p_void, u32, p_void, p_void]),
     "cx_bell_spmm_fwd": (C.c_int, [C.POINTER(CxBellMatrix), p_void, u32, i64, i64, p_void, i64, p_void]),
     "cx_bell_pack_rhs": (C.c_int, [p_void, i64, u32, u32, p_void, p_void]),
     "cx_bell_spmm_fwd_packed": (C.c_int, [C.POINTER(CxBellMatrix), p_void, i64, p_void, i64, p_void]),

@@ -59,11 +59,17 @@ __device__ __forceinline__ float load_entry(const QcsrArgs &a, std::int64_t i,
         const std::int64_t local = i - begin;
         const unsigned byte = pbase[local / kCpb];
         const unsigned code = (byte >> (static_cast<unsigned>(local % kCpb) * kBits)) & kMask;
-        const float scale = a.scales != nullptr ? a.scales[col] : 1.0f;
-        const float offset = kPolicy == CX_DECODE_PER_GENE_AFFINE
-            ? (a.offsets != nullptr ? a.offsets[col] : 0.0f)
-            : row_offset;
-        return __builtin_fmaf(static_cast<float>(code), scale, offset);
+        if constexpr (kPolicy == CX_DECODE_PER_GENE_AFFINE_PAIRS) {
+            // interleaved (scale, offset): one 8-byte gather
+            const float2 so = reinterpret_cast<const float2 *>(a.scales)[col];
+            return __builtin_fmaf(static_cast<float>(code), so.x, so.y);
+        } else {
+            const float scale = a.scales != nullptr ? a.scales[col] : 1.0f;
+            const float offset = kPolicy == CX_DECODE_PER_GENE_AFFINE
+                ? (a.offsets != nullptr ? a.offsets[col] : 0.0f)
+                : row_offset;
+            return __builtin_fmaf(static_cast<float>(code), scale, offset);
+        }
     } else if constexpr (kMode == ValueMode::f16) {
         return h2f(static_cast<const std::uint16_t *>(a.values)[i]);
     } else {
@@ -250,6 +256,13 @@ int launch_bits(const QcsrArgs &a, std::uint32_t bits, std::uint32_t rhs_dtype, 
     }
 }
 
+__global__ void pack_gene_affine_kernel(const float *scales, const float *offsets, std::uint32_t cols,
+                                        float2 *pairs) {
+    const std::uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= cols) return;
+    pairs[c] = make_float2(scales != nullptr ? scales[c] : 1.0f, offsets != nullptr ? offsets[c] : 0.0f);
+}
+
 bool aligned16(const void *p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0u; }
 
 } // namespace
@@ -277,8 +290,15 @@ extern "C" int cx_qcsr_spmm_fwd(const cx_qcsr_matrix *m, const void *rhs, uint32
             return fail(CX_STATUS_INVALID_ARGUMENT,
                         "cx_qcsr_spmm_fwd: quantized matrix needs packed_row_ptr and packed_values");
         if (m->decode_policy != CX_DECODE_PER_GENE_AFFINE
-            && m->decode_policy != CX_DECODE_COLUMN_SCALE_ROW_OFFSET)
+            && m->decode_policy != CX_DECODE_COLUMN_SCALE_ROW_OFFSET
+            && m->decode_policy != CX_DECODE_PER_GENE_AFFINE_PAIRS)
             return fail(CX_STATUS_UNSUPPORTED, "cx_qcsr_spmm_fwd: unknown decode policy");
+        if (m->decode_policy == CX_DECODE_PER_GENE_AFFINE_PAIRS
+            && (m->column_scales == nullptr || m->column_offsets != nullptr
+                || (reinterpret_cast<std::uintptr_t>(m->column_scales) & 7u) != 0u))
+            return fail(CX_STATUS_INVALID_ARGUMENT,
+                        "cx_qcsr_spmm_fwd: interleaved metadata needs 8-byte aligned (scale, offset) "
+                        "pairs in column_scales and NULL column_offsets");
     } else {
         if (m->nnz != 0u && m->values == nullptr)
             return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd: null values");
@@ -316,6 +336,23 @@ extern "C" int cx_qcsr_spmm_fwd(const cx_qcsr_matrix *m, const void *rhs, uint32
     }
     if (m->decode_policy == CX_DECODE_PER_GENE_AFFINE)
         return launch_bits<CX_DECODE_PER_GENE_AFFINE>(a, m->bits, rhs_dtype, out_cols, aligned, s);
+    if (m->decode_policy == CX_DECODE_PER_GENE_AFFINE_PAIRS)
+        return launch_bits<CX_DECODE_PER_GENE_AFFINE_PAIRS>(a, m->bits, rhs_dtype, out_cols, aligned, s);
     return launch_bits<CX_DECODE_COLUMN_SCALE_ROW_OFFSET>(a, m->bits, rhs_dtype, out_cols, aligned,
                                                           s);
+}
+
+extern "C" int cx_qcsr_pack_gene_affine(const float *scales, const float *offsets, uint32_t cols,
+                                        float *pairs, void *stream) {
+    using namespace cx;
+    clear_error();
+    if (pairs == nullptr || (reinterpret_cast<std::uintptr_t>(pairs) & 7u) != 0u)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_pack_gene_affine: pairs must be 8-byte aligned");
+    if (pairs == scales || pairs == offsets)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_pack_gene_affine: pairs aliases an input");
+    if (cols == 0u) return CX_STATUS_SUCCESS;
+    hipLaunchKernelGGL(pack_gene_affine_kernel, dim3((cols + 255u) / 256u), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), scales, offsets, cols,
+                       reinterpret_cast<float2 *>(pairs));
+    return check_launch("cx_qcsr_pack_gene_affine");
 }

@@ -100,6 +100,21 @@ def qcsr_spmm(m: QcsrMatrix, rhs: torch.Tensor, out: Optional[torch.Tensor] = No
     return out
 
 
+def qcsr_pack_gene_affine(m: QcsrMatrix, stream=None) -> QcsrMatrix:
+    """The same matrix with its per-gene (scale, offset) interleaved into one array
+    (decode policy CX_DECODE_PER_GENE_AFFINE_PAIRS): decodes bit-identically with one
+    8-byte metadata gather per code. Built once per metadata generation."""
+    if m.bits == 0 or m.decode_policy != N.DECODE_PER_GENE_AFFINE:
+        raise ValueError("interleaved metadata applies to quantized per-gene-affine matrices")
+    _require_cuda(m.row_ptr)
+    pairs = torch.empty(2 * m.cols, dtype=torch.float32, device=m.row_ptr.device)
+    N.check("cx_qcsr_pack_gene_affine", N.engine().cx_qcsr_pack_gene_affine(
+        _ptr(m.column_scales), _ptr(m.column_offsets), m.cols, pairs.data_ptr(), _stream(stream)))
+    return QcsrMatrix(m.rows, m.cols, m.bits, m.row_ptr, m.col_idx, packed_row_ptr=m.packed_row_ptr,
+                      packed_values=m.packed_values, column_scales=pairs, column_offsets=None,
+                      decode_policy=N.DECODE_PER_GENE_AFFINE_PAIRS, meta=dict(m.meta))
+
+
 @dataclass
 class BellMatrix:
     rows: int

@@ -75,6 +75,12 @@ typedef enum cellerator_dtype {
 /* include/Cellerator/quantized/blocked_ell.cuh:10-14 */
 #define CX_DECODE_PER_GENE_AFFINE 1u
 #define CX_DECODE_COLUMN_SCALE_ROW_OFFSET 2u
+/* Engine addition (no counterpart in the reference): per-gene affine decode with the
+ * metadata interleaved, column_scales -> cols (scale, offset) float pairs (8-byte
+ * aligned), column_offsets = NULL. Decodes bit-identically to CX_DECODE_PER_GENE_AFFINE;
+ * one 8-byte gather per stored code instead of two 4-byte ones. Built once per metadata
+ * generation by cx_qcsr_pack_gene_affine. */
+#define CX_DECODE_PER_GENE_AFFINE_PAIRS 3u
 
 /* ------------------------------------------------------------------------------- */
 /* 1. Thin launch layer                                                            */
@@ -111,6 +117,13 @@ typedef struct cx_qcsr_matrix {
 int cx_qcsr_spmm_fwd(const cx_qcsr_matrix *a, const void *rhs, uint32_t rhs_dtype,
                      int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
                      void *stream);
+
+/* Interleaves per-gene metadata for CX_DECODE_PER_GENE_AFFINE_PAIRS:
+ * pairs[2c] = scales[c] (1 if scales is NULL), pairs[2c+1] = offsets[c] (0 if NULL),
+ * for c < cols; pairs (device, 8-byte aligned) holds 2 * cols floats. No counterpart in
+ * the reference: it prepares the layout the decode reads in one gather. */
+int cx_qcsr_pack_gene_affine(const float *scales, const float *offsets, uint32_t cols,
+                             float *pairs, void *stream);
 
 /* Blocked-ELL matrix (include/Cellerator/quantized/blocked_ell.cuh:18-35 and the
  * cs::sparse::blocked_ell layout consumed by blocked_ell_spmm_fwd_kernel_):

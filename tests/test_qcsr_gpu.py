@@ -204,3 +204,45 @@ def test_public_abi_quantized_csr(oracle):
     lay.layout = 3  # SLICED_ELL -> UNSUPPORTED, as the reference
     assert lib.cellerator_sparse_projection_forward(ctx, C.byref(lay), C.byref(r), C.byref(o), None) == 3
     lib.cellerator_context_destroy(ctx)
+
+
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+@pytest.mark.parametrize("n,rhs_dtype", [(64, np.float16), (128, np.float16), (32, np.float16),
+                                         (64, np.float32), (100, np.float32)])
+def test_interleaved_gene_affine_is_bit_identical(oracle, bits, n, rhs_dtype):
+    """CX_DECODE_PER_GENE_AFFINE_PAIRS decodes exactly like the separate scale/offset
+    arrays: outputs equal bitwise on the fast (32/64/128) and generic shapes."""
+    torch = _torch()
+    from cellerator_amd import qcsr_pack_gene_affine, qcsr_spmm
+    rng = np.random.default_rng(500 + bits * 10 + n)
+    fx = quantized_fixture(oracle, rng, 301, 1200, 90.0, bits, oracle.PER_GENE_AFFINE, empty_every=7)
+    m = to_device_qcsr(fx)
+    mp = qcsr_pack_gene_affine(m)
+    pairs = mp.column_scales.view(-1, 2).cpu().numpy()
+    assert np.array_equal(pairs[:, 0], fx["scales"]) and np.array_equal(pairs[:, 1], fx["offsets"])
+    rhs = torch.from_numpy((rng.standard_normal((1200, n)) * 0.02).astype(rhs_dtype)).cuda()
+    a = qcsr_spmm(m, rhs)
+    b = qcsr_spmm(mp, rhs)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+
+
+def test_interleaved_gene_affine_defaults_and_errors():
+    """NULL scales/offsets pack to (1, 0); the pairs policy rejects separate offsets."""
+    torch = _torch()
+    from cellerator_amd import QcsrMatrix, qcsr_pack_gene_affine, qcsr_spmm
+    from cellerator_amd import _native as N
+    m = QcsrMatrix(2, 4, 4, torch.tensor([0, 1, 2], dtype=torch.int32).cuda(),
+                   torch.tensor([0, 3], dtype=torch.int32).cuda(),
+                   packed_row_ptr=torch.tensor([0, 1, 2], dtype=torch.int32).cuda(),
+                   packed_values=torch.tensor([5, 9] + [0] * 14, dtype=torch.uint8).cuda())
+    mp = qcsr_pack_gene_affine(m)
+    assert mp.column_scales.cpu().tolist() == [1.0, 0.0] * 4
+    w = torch.arange(16, dtype=torch.float32).reshape(4, 4).cuda()
+    assert torch.equal(qcsr_spmm(mp, w), qcsr_spmm(m, w))
+    bad = QcsrMatrix(2, 4, 4, m.row_ptr, m.col_idx, packed_row_ptr=m.packed_row_ptr,
+                     packed_values=m.packed_values, column_scales=mp.column_scales,
+                     column_offsets=torch.zeros(4).cuda(),
+                     decode_policy=N.DECODE_PER_GENE_AFFINE_PAIRS)
+    with pytest.raises(N.EngineError, match="INVALID_ARGUMENT"):
+        qcsr_spmm(bad, w)
