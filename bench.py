@@ -161,7 +161,7 @@ def bench_bell(args, torch, cfg) -> dict:
     """Config 4: Blocked-ELL bf16 SpMM on MFMA (cx_bell_spmm_fwd_packed), N = 256."""
     import numpy as np
 
-    from cellerator_amd import bell_pack_rhs, bell_spmm_packed
+    from cellerator_amd import bell_pack_rhs, bell_plan_groups, bell_spmm_grouped, bell_spmm_packed
     from cellerator_amd.synth import dense_normal, generate_bell
 
     t0 = time.perf_counter()
@@ -171,12 +171,19 @@ def bench_bell(args, torch, cfg) -> dict:
     packed = bell_pack_rhs(w)
     out = torch.empty((m.rows, n_out), dtype=torch.float32, device="cuda")
     valid_blocks = int((m.block_col_idx != -1).sum().item())
+    # row-block grouping planned once per projection (untimed, like the packed panel)
+    groups = None if args.ungrouped else bell_plan_groups(m)
     torch.cuda.synchronize()
-    log(f"generated {cfg.name}: {valid_blocks} valid 32x32 blocks in {time.perf_counter() - t0:.1f}s")
+    log(f"generated {cfg.name}: {valid_blocks} valid 32x32 blocks in {time.perf_counter() - t0:.1f}s"
+        + ("" if groups is None else f"; {groups.group_count} groups cover {groups.grouped_row_blocks} "
+                                     f"row blocks, {groups.single_count} single"))
     stream = torch.cuda.current_stream()
 
     def launch():
-        bell_spmm_packed(m, packed, n_out, out=out, stream=stream)
+        if groups is None:
+            bell_spmm_packed(m, packed, n_out, out=out, stream=stream)
+        else:
+            bell_spmm_grouped(m, packed, groups, n_out, out=out, stream=stream)
 
     wall_ms, ev = time_launches(torch, launch, args.steps, args.warmup, stream)
     kern_ms = statistics.mean(ev)
@@ -191,10 +198,14 @@ def bench_bell(args, torch, cfg) -> dict:
         "ms_per_step": wall_ms, "dtype": "bf16-values/bf16-W/f32-accumulate",
         "config": {"workload": cfg.name, "rows": m.rows, "genes": m.cols, "block_size": bs,
                    "valid_blocks": valid_blocks, "ell_width": cfg.ell_width, "n_out": n_out,
-                   "seed": hex(cfg.seed)},
+                   "seed": hex(cfg.seed),
+                   "row_block_groups": None if groups is None else {
+                       "groups": groups.group_count, "grouped_row_blocks": groups.grouped_row_blocks,
+                       "single_row_blocks": groups.single_count}},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(cfg.name),
-                     "kernel": "bell_spmm_mfma<256>", "kernel_ms_mean": kern_ms,
+                     "kernel": "bell_spmm_mfma<256>" if groups is None else "bell_spmm_mfma_grouped<256> (+ singles)",
+                     "kernel_ms_mean": kern_ms,
                      "kernel_ms_median": statistics.median(ev), "algorithmic_bytes": alg_bytes,
                      "mfma_tflops": flops / (kern_ms * 1e-3) / 1e12,
                      "mfma_frac_of_bf16_dense_peak": flops / (kern_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS},
@@ -213,6 +224,11 @@ def bench_bell(args, torch, cfg) -> dict:
                                    want_magnitude=False)
         t = time.perf_counter() - t1
         nvalid = int((idx != np.uint32(0xFFFFFFFF).astype(idx.dtype)).sum())
+        ref, mag = pyoracle.bell_spmm_referee(rows, m.cols, bs, m.ell_cols, idx, vals, wn,
+                                              value_type=pyoracle.BF16, rhs_type=pyoracle.BF16)
+        cmp = pyoracle.compare(ref, out[:rows].cpu().numpy(), 1e-4, 1e-4, mag)
+        res["parity_sample"] = {"rows": rows, "within_tolerance": bool(cmp["within_tolerance"]),
+                                "max_relative_error": float(cmp["max_relative_error"])}
         res["cpu_baseline"] = {"value": nvalid * bs * bs / t, "unit": "stored block elements/s",
                                "cores": 1, "kind": "port",
                                "sample": f"first {rows} of {m.rows} rows ({nvalid} blocks), one pass of "
@@ -325,6 +341,8 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=0, help="override the row count (smaller runs)")
     ap.add_argument("--cpu-rows", type=int, default=100_000)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--ungrouped", action="store_true",
+                    help="C4: time the per-row-block MFMA kernel without the row-block grouping")
     ap.add_argument("--separate-meta", action="store_true",
                     help="C2/C3: time the separate scale/offset arrays instead of interleaved pairs")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",

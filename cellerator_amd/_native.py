@@ -42,6 +42,11 @@ class CxBellMatrix(C.Structure):
     ]
 
 
+class CxBellGroups(C.Structure):
+    _fields_ = [("group_count", u32), ("grouped_row_blocks", u32), ("single_count", u32),
+                ("reserved", u32), ("order", p_void), ("group_offsets", p_void)]
+
+
 class CxCpbpTiles(C.Structure):
     _fields_ = [
         ("row_count", u32), ("feature_count", u32), ("feature_block_count", u32),
@@ -131,6 +136,11 @@ ENGINE_SIGNATURES = {
     "cx_bell_spmm_fwd": (C.c_int, [C.POINTER(CxBellMatrix), p_void, u32, i64, i64, p_void, i64, p_void]),
     "cx_bell_pack_rhs": (C.c_int, [p_void, i64, u32, u32, p_void, p_void]),
     "cx_bell_spmm_fwd_packed": (C.c_int, [C.POINTER(CxBellMatrix), p_void, i64, p_void, i64, p_void]),
+    "cx_bell_plan_groups": (C.c_int, [p_void, u32, u32, u32, p_void, p_void, C.POINTER(u32),
+                                      C.POINTER(u32)]),
+    "cx_bell_plan_last_error": (C.c_char_p, []),
+    "cx_bell_spmm_fwd_grouped": (C.c_int, [C.POINTER(CxBellMatrix), p_void, C.POINTER(CxBellGroups),
+                                           i64, p_void, i64, p_void]),
     "cx_cpbp_reduce": (C.c_int, [C.POINTER(CxCpbpTiles), p_void, u64, p_void, u64, p_void]),
     "cx_csr_spmv_fwd": (C.c_int, [u32, p_void, p_void, p_void, u32, p_void, p_void, p_void]),
     "cx_cpbp_builder_create": (C.c_int, [C.POINTER(CxCpbpPlan), C.POINTER(CxCpbpCsr),

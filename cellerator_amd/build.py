@@ -37,6 +37,7 @@ ENGINE_SOURCES = [
     "csr_spmv.hip",
     "abi.cpp",
     "cpbp_build.cpp",
+    "bell_plan.cpp",
 ]
 SYNTH_SOURCES = ["synth.hip"]
 

@@ -56,24 +56,65 @@ __device__ __forceinline__ std::uint32_t xcd_major(std::uint32_t wg, std::uint32
     return (wg % kXcds) * per + wg / kXcds;
 }
 
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, std::uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ cx_bf16x8 load_frag(rsrc_t r, std::uint32_t byte_offset) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(byte_offset), 0, 0);
+    cx_bf16x8 f;
+    __builtin_memcpy(&f, &v, 16);
+    return f;
+}
+
+// Operand fragments of one ELL slot for one wave: A (this lane's row, two K halves) and
+// B (two 32-column tiles x two K halves).
+struct SlotFrags {
+    cx_bf16x8 a[2];
+    cx_bf16x8 b[2][2];
+};
+
 template<int kN>
-__global__ __launch_bounds__(kN) void bell_spmm_mfma(BellArgs a, const std::uint16_t *packed_rhs) {
+__global__ __launch_bounds__(kN) void bell_spmm_mfma(BellArgs a, const std::uint16_t *packed_rhs,
+                                                     std::uint32_t panel_bytes,
+                                                     const std::uint32_t *rb_list) {
     constexpr int kTilesPerWave = 2; // 64 output columns per wave
     const int lane = static_cast<int>(threadIdx.x) % kWave;
     const int wave = static_cast<int>(threadIdx.x) / kWave;
     const std::uint32_t row_blocks = (a.rows + 31u) / 32u;
-    const std::uint32_t rb = xcd_major(blockIdx.x, gridDim.x);
+    // a listed subset of row blocks (the planner's singletons), or all in XCD-major order
+    const std::uint32_t rb = rb_list != nullptr ? rb_list[blockIdx.x] : xcd_major(blockIdx.x, gridDim.x);
     if (rb >= row_blocks) return;
     const std::uint32_t width = a.ell_cols / 32u;
     const std::uint32_t *slots = a.block_col_idx + static_cast<std::uint64_t>(rb) * width;
 
     const int m = lane % 32;         // A row / B,D column within the tile
     const int kq = (lane / 32) * 8;  // first K element of this lane's fragment
-    const std::uint32_t row = rb * 32u + static_cast<std::uint32_t>(m);
-    const bool row_ok = row < a.rows;
-    const std::uint16_t *arow = static_cast<const std::uint16_t *>(a.values)
-        + static_cast<std::uint64_t>(row_ok ? row : 0u) * a.ell_cols + kq;
     const int n0 = wave * 64;
+    // A: this row block's value rows (rows past the matrix read as 0 from the buffer)
+    const std::uint32_t rows_here = min(32u, a.rows - rb * 32u);
+    const rsrc_t ra = make_rsrc(static_cast<const std::uint16_t *>(a.values)
+                                    + static_cast<std::uint64_t>(rb) * 32u * a.ell_cols,
+                                rows_here * a.ell_cols * 2u);
+    const rsrc_t rbp = make_rsrc(packed_rhs, panel_bytes);
+    const std::uint32_t a_lane = (static_cast<std::uint32_t>(m) * a.ell_cols + static_cast<std::uint32_t>(kq)) * 2u;
+    const std::uint32_t b_lane = (static_cast<std::uint32_t>(n0 + m) * 32u + static_cast<std::uint32_t>(kq)) * 2u;
+
+    auto load_slot = [&](SlotFrags &f, std::uint32_t s, std::uint32_t bc) {
+        const std::uint32_t ao = a_lane + s * 64u;
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) f.a[kc] = load_frag(ra, ao + static_cast<std::uint32_t>(kc) * 32u);
+        const std::uint32_t bo = bc * static_cast<std::uint32_t>(kN) * 64u + b_lane;
+#pragma unroll
+        for (int t = 0; t < kTilesPerWave; ++t)
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc)
+                f.b[t][kc] = load_frag(rbp, bo + static_cast<std::uint32_t>(t) * 32u * 64u
+                                                + static_cast<std::uint32_t>(kc) * 32u);
+    };
 
     cx_floatx16 acc[kTilesPerWave];
 #pragma unroll
@@ -81,27 +122,45 @@ __global__ __launch_bounds__(kN) void bell_spmm_mfma(BellArgs a, const std::uint
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
 
-    for (std::uint32_t s = 0; s < width; ++s) {
-        const std::uint32_t bc = slots[s];
-        if (bc == kInvalidBlock) continue;
-        cx_bf16x8 afrag[2];
+    auto mfma_slot = [&](const SlotFrags &f) {
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-            uint4 raw = make_uint4(0u, 0u, 0u, 0u);
-            if (row_ok) raw = *reinterpret_cast<const uint4 *>(arow + s * 32u + kc * 16);
-            __builtin_memcpy(&afrag[kc], &raw, 16);
-        }
-        const std::uint16_t *panel = packed_rhs + static_cast<std::uint64_t>(bc) * kN * 32;
+        for (int t = 0; t < kTilesPerWave; ++t)
 #pragma unroll
-        for (int t = 0; t < kTilesPerWave; ++t) {
-            const std::uint16_t *bcol = panel + static_cast<std::uint64_t>(n0 + t * 32 + m) * 32 + kq;
-#pragma unroll
-            for (int kc = 0; kc < 2; ++kc) {
-                const uint4 raw = *reinterpret_cast<const uint4 *>(bcol + kc * 16);
-                cx_bf16x8 bfrag;
-                __builtin_memcpy(&bfrag, &raw, 16);
-                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afrag[kc], bfrag, acc[t], 0, 0, 0);
-            }
+            for (int kc = 0; kc < 2; ++kc)
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[kc], f.b[t][kc], acc[t], 0, 0, 0);
+    };
+
+    // Valid slots of each 64-slot chunk are walked in order; the next valid slot's
+    // fragments load (ping-pong registers) while the current slot's MFMAs run. Empty
+    // slots (0xffffffff) are never read.
+    for (std::uint32_t base = 0; base < width; base += kWave) {
+        const std::uint32_t cnt = min(static_cast<std::uint32_t>(kWave), width - base);
+        const std::uint32_t sid = static_cast<std::uint32_t>(lane) < cnt ? slots[base + lane] : kInvalidBlock;
+        unsigned long long valid = __ballot(sid != kInvalidBlock);
+        if (valid == 0ull) continue;
+        SlotFrags f0, f1;
+        std::uint32_t s = static_cast<std::uint32_t>(__builtin_ctzll(valid));
+        load_slot(f0, base + s, static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(sid), static_cast<int>(s))));
+        valid &= valid - 1ull;
+        // The prefetch is issued unconditionally (the last one re-reads the current slot):
+        // with no branch around it, each wait covers only the slot about to be used.
+        for (;;) {
+            const bool more0 = valid != 0ull;
+            if (more0) s = static_cast<std::uint32_t>(__builtin_ctzll(valid));
+            load_slot(f1, base + s, static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(sid), static_cast<int>(s))));
+            valid &= valid - 1ull;
+            __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of these MFMAs
+            mfma_slot(f0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (!more0) break;
+            const bool more1 = valid != 0ull;
+            if (more1) s = static_cast<std::uint32_t>(__builtin_ctzll(valid));
+            load_slot(f0, base + s, static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(sid), static_cast<int>(s))));
+            valid &= valid - 1ull;
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_slot(f1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (!more1) break;
         }
     }
 
@@ -109,6 +168,136 @@ __global__ __launch_bounds__(kN) void bell_spmm_mfma(BellArgs a, const std::uint
 #pragma unroll
     for (int t = 0; t < kTilesPerWave; ++t) {
         const int col = n0 + t * 32 + m;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const std::uint32_t r = rb * 32u + 8u * (i / 4) + 4u * (lane / 32) + (i % 4);
+            if (r < a.rows) a.out[static_cast<std::int64_t>(r) * a.out_ld + col] = acc[t][i];
+        }
+    }
+}
+
+
+// Grouped MFMA path. One workgroup per planner group of 2..4 row blocks whose valid
+// block-column lists are prefixes of the longest member's (cx_bell_plan_groups). Wave w owns
+// member w across all N output columns (N/32 accumulator tiles). At step k every member
+// uses the group's k-th block column, so its N x 32 panel slice is loaded from the packed
+// panel once per group, into LDS (column stride 80 B: 8 consecutive lanes' 16-byte reads
+// hit distinct banks), double-buffered; each wave reads its B fragments from LDS and its own
+// A fragment (its k-th valid slot) from global memory.
+constexpr int kGroupWaves = 4;
+constexpr int kPanelColStride = 80;
+
+template<int kN>
+__global__ __launch_bounds__(kWave *kGroupWaves) void bell_spmm_mfma_grouped(
+    BellArgs a, const std::uint16_t *packed_rhs, std::uint32_t panel_bytes,
+    const std::uint32_t *order, const std::uint32_t *group_offsets) {
+    constexpr int kTiles = kN / 32;
+    constexpr int kSlice = kN * kPanelColStride;
+    constexpr int kChunks = kN * 4;  // 16-byte chunks of one N x 32 bf16 slice
+    __shared__ __attribute__((aligned(16))) unsigned char bslice[2][kSlice];
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const std::uint32_t wave = static_cast<std::uint32_t>(
+        __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave)));
+    const std::uint32_t g0 = group_offsets[blockIdx.x], g1 = group_offsets[blockIdx.x + 1];
+    const std::uint32_t members = g1 - g0;
+    const std::uint32_t leader = order[g1 - 1u];
+    const bool active = wave < members;
+    const std::uint32_t rb = active ? order[g0 + wave] : leader;
+    const std::uint32_t width = a.ell_cols / 32u;
+    const std::uint32_t lead_sid = static_cast<std::uint32_t>(lane) < width
+        ? a.block_col_idx[static_cast<std::uint64_t>(leader) * width + lane] : kInvalidBlock;
+    const std::uint32_t own_sid = static_cast<std::uint32_t>(lane) < width
+        ? a.block_col_idx[static_cast<std::uint64_t>(rb) * width + lane] : kInvalidBlock;
+    unsigned long long lead_valid = __ballot(lead_sid != kInvalidBlock);
+    unsigned long long own_valid = active ? __ballot(own_sid != kInvalidBlock) : 0ull;
+    const std::uint32_t steps = static_cast<std::uint32_t>(__popcll(lead_valid));
+    const std::uint32_t own_steps = static_cast<std::uint32_t>(__popcll(own_valid));
+
+    const int m = lane % 32;
+    const int kq = (lane / 32) * 8;
+    const std::uint32_t rows_here = min(32u, a.rows - rb * 32u);
+    const rsrc_t ra = make_rsrc(static_cast<const std::uint16_t *>(a.values)
+                                    + static_cast<std::uint64_t>(rb) * 32u * a.ell_cols,
+                                rows_here * a.ell_cols * 2u);
+    const rsrc_t rbp = make_rsrc(packed_rhs, panel_bytes);
+    const std::uint32_t a_lane = (static_cast<std::uint32_t>(m) * a.ell_cols + static_cast<std::uint32_t>(kq)) * 2u;
+
+    cx_floatx16 acc[kTiles];
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
+
+    // next block column of the group / next own valid slot
+    auto next_lead = [&]() {
+        const std::uint32_t s = static_cast<std::uint32_t>(__builtin_ctzll(lead_valid));
+        lead_valid &= lead_valid - 1ull;
+        return static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lead_sid), static_cast<int>(s)));
+    };
+    auto next_own = [&]() {
+        const std::uint32_t s = own_valid != 0ull ? static_cast<std::uint32_t>(__builtin_ctzll(own_valid)) : 0u;
+        own_valid &= own_valid - 1ull;
+        return s;
+    };
+    struct BRegs { uint4 c[kChunks / (kWave * kGroupWaves)]; };
+    auto load_b = [&](BRegs &b, std::uint32_t bc) {
+#pragma unroll
+        for (int i = 0; i < kChunks / (kWave * kGroupWaves); ++i) {
+            const std::uint32_t c = threadIdx.x + static_cast<std::uint32_t>(i) * kWave * kGroupWaves;
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(
+                rbp, static_cast<int>(bc * static_cast<std::uint32_t>(kN) * 64u + c * 16u), 0, 0);
+            __builtin_memcpy(&b.c[i], &v, 16);
+        }
+    };
+    auto store_b = [&](const BRegs &b, int buf) {
+#pragma unroll
+        for (int i = 0; i < kChunks / (kWave * kGroupWaves); ++i) {
+            const std::uint32_t c = threadIdx.x + static_cast<std::uint32_t>(i) * kWave * kGroupWaves;
+            *reinterpret_cast<uint4 *>(&bslice[buf][(c / 4u) * kPanelColStride + (c % 4u) * 16u]) = b.c[i];
+        }
+    };
+    auto load_a = [&](cx_bf16x8 (&af)[2], std::uint32_t s) {
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) af[kc] = load_frag(ra, a_lane + s * 64u + static_cast<std::uint32_t>(kc) * 32u);
+    };
+    auto mfma_step = [&](const cx_bf16x8 (&af)[2], int buf) {
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc) {
+                cx_bf16x8 bf;
+                __builtin_memcpy(&bf, &bslice[buf][(t * 32 + m) * kPanelColStride + (kq + kc * 16) * 2], 16);
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kc], bf, acc[t], 0, 0, 0);
+            }
+    };
+
+    if (steps != 0u) {
+        BRegs b;
+        cx_bf16x8 a0[2], a1[2];
+        load_b(b, next_lead());
+        load_a(a0, next_own());
+        store_b(b, 0);
+        __syncthreads();
+        // step k reads buffer k % 2 and A set k % 2; loads for step k+1 are in flight
+        std::uint32_t k = 0;
+        for (;;) {
+            if (k + 1u < steps) { load_b(b, next_lead()); load_a(a1, next_own()); }
+            if (active && k < own_steps) mfma_step(a0, 0);
+            if (k + 1u < steps) store_b(b, 1);
+            __syncthreads();
+            if (++k >= steps) break;
+            if (k + 1u < steps) { load_b(b, next_lead()); load_a(a0, next_own()); }
+            if (active && k < own_steps) mfma_step(a1, 1);
+            if (k + 1u < steps) store_b(b, 0);
+            __syncthreads();
+            if (++k >= steps) break;
+        }
+    }
+
+    if (!active) return;
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+        const int col = t * 32 + m;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const std::uint32_t r = rb * 32u + 8u * (i / 4) + 4u * (lane / 32) + (i % 4);
@@ -292,10 +481,72 @@ extern "C" int cx_bell_spmm_fwd_packed(const cx_bell_matrix *m, const uint16_t *
     const BellArgs a = make_args(m, packed_rhs, out_cols, out, out_ld);
     const unsigned row_blocks = (m->rows + 31u) / 32u;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    const std::uint64_t panel = static_cast<std::uint64_t>((m->cols + 31u) / 32u) * static_cast<std::uint64_t>(out_cols) * 64u;
+    const std::uint64_t block_rows = static_cast<std::uint64_t>(32u) * m->ell_cols * 2u;
+    if (panel > 0xFFFFFFFFull || block_rows > 0xFFFFFFFFull)
+        return fail(CX_STATUS_INVALID_SHAPE, "MFMA Blocked-ELL: packed panel or row block exceeds 4 GiB");
+    const std::uint32_t pb = static_cast<std::uint32_t>(panel);
+    const std::uint32_t *none = nullptr;
     switch (out_cols) {
-    case 64: hipLaunchKernelGGL(bell_spmm_mfma<64>, dim3(row_blocks), dim3(64), 0, s, a, packed_rhs); break;
-    case 128: hipLaunchKernelGGL(bell_spmm_mfma<128>, dim3(row_blocks), dim3(128), 0, s, a, packed_rhs); break;
-    default: hipLaunchKernelGGL(bell_spmm_mfma<256>, dim3(row_blocks), dim3(256), 0, s, a, packed_rhs); break;
+    case 64: hipLaunchKernelGGL(bell_spmm_mfma<64>, dim3(row_blocks), dim3(64), 0, s, a, packed_rhs, pb, none); break;
+    case 128: hipLaunchKernelGGL(bell_spmm_mfma<128>, dim3(row_blocks), dim3(128), 0, s, a, packed_rhs, pb, none); break;
+    default: hipLaunchKernelGGL(bell_spmm_mfma<256>, dim3(row_blocks), dim3(256), 0, s, a, packed_rhs, pb, none); break;
     }
     return check_launch("bell_spmm_mfma");
+}
+
+extern "C" int cx_bell_spmm_fwd_grouped(const cx_bell_matrix *m, const uint16_t *packed_rhs,
+                                        const cx_bell_groups *groups, int64_t out_cols,
+                                        float *out, int64_t out_ld, void *stream) {
+    using namespace cx;
+    clear_error();
+    int rc = validate_bell(m, packed_rhs, out_cols, out_cols, out, out_ld);
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    if (groups == nullptr) return fail(CX_STATUS_INVALID_ARGUMENT, "grouped Blocked-ELL: null groups");
+    if (m->bits != 0u || m->value_dtype != CELLERATOR_DTYPE_BF16 || m->block_size != 32u)
+        return fail(CX_STATUS_UNSUPPORTED,
+                    "MFMA Blocked-ELL needs unquantized BF16 values and 32x32 blocks");
+    if (out_cols != 64 && out_cols != 128 && out_cols != 256)
+        return fail(CX_STATUS_UNSUPPORTED, "MFMA Blocked-ELL supports 64, 128 or 256 output columns");
+    if ((reinterpret_cast<std::uintptr_t>(m->values) & 15u) != 0u
+        || (reinterpret_cast<std::uintptr_t>(packed_rhs) & 15u) != 0u)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "MFMA Blocked-ELL operands must be 16-byte aligned");
+    const std::uint32_t row_blocks = (m->rows + 31u) / 32u;
+    if (static_cast<std::uint64_t>(groups->grouped_row_blocks) + groups->single_count != row_blocks
+        || (groups->group_count != 0u
+            && (groups->group_offsets == nullptr || groups->grouped_row_blocks < 2u * groups->group_count
+                || groups->grouped_row_blocks > 4ull * groups->group_count))
+        || (row_blocks != 0u && groups->order == nullptr))
+        return fail(CX_STATUS_INVALID_SHAPE, "grouped Blocked-ELL: groups do not cover the row blocks");
+    if (groups->group_count != 0u && m->ell_cols / 32u > 64u)
+        return fail(CX_STATUS_UNSUPPORTED, "grouped Blocked-ELL supports at most 64 slots per row block");
+    if (m->rows == 0u) return CX_STATUS_SUCCESS;
+    const BellArgs a = make_args(m, packed_rhs, out_cols, out, out_ld);
+    const std::uint64_t panel = static_cast<std::uint64_t>((m->cols + 31u) / 32u) * static_cast<std::uint64_t>(out_cols) * 64u;
+    if (panel > 0xFFFFFFFFull || static_cast<std::uint64_t>(32u) * m->ell_cols * 2u > 0xFFFFFFFFull)
+        return fail(CX_STATUS_INVALID_SHAPE, "MFMA Blocked-ELL: packed panel or row block exceeds 4 GiB");
+    const std::uint32_t pb = static_cast<std::uint32_t>(panel);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 gblock(kWave * kGroupWaves);
+    if (groups->group_count != 0u) {
+        const dim3 ggrid(groups->group_count);
+        switch (out_cols) {
+        case 64: hipLaunchKernelGGL(bell_spmm_mfma_grouped<64>, ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets); break;
+        case 128: hipLaunchKernelGGL(bell_spmm_mfma_grouped<128>, ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets); break;
+        default: hipLaunchKernelGGL(bell_spmm_mfma_grouped<256>, ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets); break;
+        }
+        rc = check_launch("bell_spmm_mfma_grouped");
+        if (rc != CX_STATUS_SUCCESS) return rc;
+    }
+    if (groups->single_count != 0u) {
+        const std::uint32_t *singles = groups->order + groups->grouped_row_blocks;
+        const dim3 sgrid(groups->single_count);
+        switch (out_cols) {
+        case 64: hipLaunchKernelGGL(bell_spmm_mfma<64>, sgrid, dim3(64), 0, s, a, packed_rhs, pb, singles); break;
+        case 128: hipLaunchKernelGGL(bell_spmm_mfma<128>, sgrid, dim3(128), 0, s, a, packed_rhs, pb, singles); break;
+        default: hipLaunchKernelGGL(bell_spmm_mfma<256>, sgrid, dim3(256), 0, s, a, packed_rhs, pb, singles); break;
+        }
+        rc = check_launch("bell_spmm_mfma");
+    }
+    return rc;
 }

@@ -184,6 +184,58 @@ def bell_spmm_packed(m: BellMatrix, packed_rhs: torch.Tensor, n: int,
 
 
 @dataclass
+class BellGroups:
+    """Row-block groups of a Blocked-ELL matrix for the grouped MFMA path (host-planned once
+    per projection; see cx_bell_plan_groups)."""
+    group_count: int
+    grouped_row_blocks: int
+    single_count: int
+    order: torch.Tensor          # int32 [row_blocks] (uint32 ids)
+    group_offsets: torch.Tensor  # int32 [group_count + 1]
+
+    def descriptor(self) -> N.CxBellGroups:
+        return N.CxBellGroups(self.group_count, self.grouped_row_blocks, self.single_count, 0,
+                              _ptr(self.order), _ptr(self.group_offsets))
+
+
+def bell_plan_groups(m: BellMatrix, max_group: int = 4) -> BellGroups:
+    """Groups row blocks whose valid block-column lists are prefixes of one another (host
+    planner on a host copy of block_col_idx; the result is uploaded to m's device)."""
+    import numpy as np
+
+    rb = (m.rows + m.block_size - 1) // m.block_size
+    slots = m.ell_cols // m.block_size
+    idx = np.ascontiguousarray(m.block_col_idx.cpu().numpy().view(np.uint32).reshape(rb, slots))
+    order = np.zeros(rb, np.uint32)
+    offs = np.zeros(rb + 1, np.uint32)
+    gc, sc = C.c_uint32(), C.c_uint32()
+    lib = N.engine()
+    st = lib.cx_bell_plan_groups(idx.ctypes.data if idx.size else None, rb, slots, max_group,
+                                 order.ctypes.data if order.size else None, offs.ctypes.data,
+                                 C.byref(gc), C.byref(sc))
+    if st != 0:
+        raise N.EngineError("cx_bell_plan_groups", st, lib.cx_bell_plan_last_error().decode())
+    grouped = int(offs[gc.value]) if gc.value else 0
+    dev = m.block_col_idx.device
+    return BellGroups(gc.value, grouped, sc.value,
+                      torch.from_numpy(order.view(np.int32)).to(dev),
+                      torch.from_numpy(offs[: gc.value + 1].view(np.int32).copy()).to(dev))
+
+
+def bell_spmm_grouped(m: BellMatrix, packed_rhs: torch.Tensor, groups: BellGroups, n: int,
+                      out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """MFMA Blocked-ELL with a planned row-block grouping; same contract as bell_spmm_packed."""
+    _require_cuda(m.block_col_idx, packed_rhs)
+    if out is None:
+        out = torch.empty((m.rows, n), dtype=torch.float32, device=packed_rhs.device)
+    d, g = m.descriptor(), groups.descriptor()
+    N.check("cx_bell_spmm_fwd_grouped", N.engine().cx_bell_spmm_fwd_grouped(
+        C.byref(d), packed_rhs.data_ptr(), C.byref(g), n, out.data_ptr(), out.stride(0),
+        _stream(stream)))
+    return out
+
+
+@dataclass
 class CpbpTiles:
     row_count: int
     feature_count: int

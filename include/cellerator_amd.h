@@ -172,6 +172,38 @@ int cx_bell_pack_rhs(const uint16_t *rhs_bf16, int64_t rhs_ld, uint32_t k, uint3
 int cx_bell_spmm_fwd_packed(const cx_bell_matrix *a, const uint16_t *packed_rhs,
                             int64_t out_cols, float *out, int64_t out_ld, void *stream);
 
+/* Row-block groups for the grouped MFMA path (engine addition, no counterpart in the
+ * reference; a persistent preprocessing of the Blocked-ELL projection, like the packed
+ * panel). order[0 .. grouped_row_blocks) holds group_count groups of 2..4 row blocks
+ * (group g = order[group_offsets[g] .. group_offsets[g+1]), longest member last) whose valid
+ * block-column lists are prefixes of the longest member's; order[grouped_row_blocks ..)
+ * holds single_count row blocks run one per workgroup. order and group_offsets are device
+ * arrays. */
+typedef struct cx_bell_groups {
+    uint32_t group_count;
+    uint32_t grouped_row_blocks;
+    uint32_t single_count;
+    uint32_t reserved;
+    const uint32_t *order;         /* ceil(rows/32) row block ids */
+    const uint32_t *group_offsets; /* group_count + 1 */
+} cx_bell_groups;
+
+/* Host planner for cx_bell_groups: block_col_idx (HOST copy, row_blocks x slots, 0xffffffff
+ * = empty) -> order (row_blocks), group_offsets (row_blocks + 1 capacity), counts. Groups hold
+ * up to max_group (1..4) row blocks. Deterministic. */
+int cx_bell_plan_groups(const uint32_t *block_col_idx, uint32_t row_blocks, uint32_t slots,
+                        uint32_t max_group, uint32_t *order, uint32_t *group_offsets,
+                        uint32_t *group_count, uint32_t *single_count);
+const char *cx_bell_plan_last_error(void);
+
+/* Same result contract as cx_bell_spmm_fwd_packed: per group, each N x 32 panel slice is
+ * loaded once (into LDS) for all members; per output element the MFMA accumulation runs in
+ * the same slot order as the ungrouped kernel. Up to 64 slots per row block when groups
+ * are present. */
+int cx_bell_spmm_fwd_grouped(const cx_bell_matrix *a, const uint16_t *packed_rhs,
+                             const cx_bell_groups *groups, int64_t out_cols, float *out,
+                             int64_t out_ld, void *stream);
+
 /* CP-BP warp-tile projection (components/CellPack/include/CellPack/warp_tiles.hh:41-79)
  * plus the plan subset of feature_weighted_row_reduction_plan_view
  * (components/CellPack/include/CellPack/feature_weighted_row_reduction.hh:16-26).

@@ -111,3 +111,57 @@ def test_generated_c4_sample(oracle):
                                         w.view(torch.int16).cpu().numpy().view(np.uint16),
                                         value_type=oracle.BF16, rhs_type=oracle.BF16)
     check_against_referee(oracle, ref, mag, out.cpu().numpy())
+
+
+@pytest.mark.parametrize("n", [64, 128, 256])
+@pytest.mark.parametrize("scatter", [False, True])
+def test_grouped_mfma_equals_ungrouped_and_referee(oracle, n, scatter):
+    """Grouped path (planner groups + singletons) is bitwise equal to the per-row-block MFMA
+    kernel (same slot order per output) and within tolerance of the float64 referee, with
+    valid slots contiguous or scattered among empty ones."""
+    import torch
+
+    from cellerator_amd import (BellMatrix, bell_pack_rhs, bell_plan_groups, bell_spmm_grouped,
+                                bell_spmm_packed)
+    from tests.test_bell_plan import patterned
+    rng = np.random.default_rng(900 + n + scatter)
+    rb, slots, cols = 60, 16, 32 * 500 - 7  # K not a multiple of 32
+    idx = patterned(rng, rb=rb, slots=slots, patterns=5, scatter_invalid=scatter)
+    idx[:, :][idx != 0xFFFFFFFF] %= (cols + 31) // 32
+    # keep each row's valid columns distinct after the modulo
+    for r in range(rb):
+        v = idx[r][idx[r] != 0xFFFFFFFF]
+        if len(set(v.tolist())) != len(v):
+            idx[r] = 0xFFFFFFFF
+    rows = rb * 32 - 5  # ragged last row block
+    vals = rng.standard_normal((rb * 32, slots * 32)).astype(np.float32)
+    vals *= rng.random(vals.shape) < 0.35
+    vbits = _bf16_round(vals)
+    w = (rng.standard_normal((cols, n)) * 0.02).astype(np.float32)
+    wbits = _bf16_round(w)
+    m = BellMatrix(rows, cols, 32, slots * 32, torch.from_numpy(idx.view(np.int32)).cuda(),
+                   values=torch.from_numpy(vbits.view(np.int16)).view(torch.bfloat16).cuda())
+    rhs = torch.from_numpy(wbits.view(np.int16)).view(torch.bfloat16).cuda()
+    packed = bell_pack_rhs(rhs)
+    groups = bell_plan_groups(m)
+    assert groups.group_count > 0 and groups.grouped_row_blocks + groups.single_count == rb
+    a = bell_spmm_packed(m, packed, n)
+    b = bell_spmm_grouped(m, packed, groups, n)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    ref, mag = oracle.bell_spmm_referee(rows, cols, 32, slots * 32, idx, vbits[:rows], wbits,
+                                        value_type=oracle.BF16, rhs_type=oracle.BF16)
+    check_against_referee(oracle, ref, mag, b.cpu().numpy())
+
+
+def test_grouped_rejects_groups_that_do_not_cover():
+    import torch
+
+    from cellerator_amd import BellGroups, BellMatrix, bell_pack_rhs, bell_spmm_grouped
+    from cellerator_amd._native import EngineError
+    idx = torch.zeros((2, 1), dtype=torch.int32).cuda()
+    m = BellMatrix(64, 32, 32, 32, idx, values=torch.zeros((64, 32), dtype=torch.bfloat16).cuda())
+    packed = bell_pack_rhs(torch.zeros((32, 64), dtype=torch.bfloat16).cuda())
+    bad = BellGroups(0, 0, 1, torch.zeros(2, dtype=torch.int32).cuda(), torch.zeros(1, dtype=torch.int32).cuda())
+    with pytest.raises(EngineError, match="INVALID_SHAPE"):
+        bell_spmm_grouped(m, packed, bad, 64)
