@@ -181,24 +181,31 @@ __global__ __launch_bounds__(kN) void bell_spmm_mfma(BellArgs a, const std::uint
 // block-column lists are prefixes of the longest member's (cx_bell_plan_groups). Wave w owns
 // member w across all N output columns (N/32 accumulator tiles). At step k every member
 // uses the group's k-th block column, so its N x 32 panel slice is loaded from the packed
-// panel once per group, into LDS (column stride 80 B: 8 consecutive lanes' 16-byte reads
-// hit distinct banks), double-buffered; each wave reads its B fragments from LDS and its own
-// A fragment (its k-th valid slot) from global memory.
+// panel once per group into an LDS ring of three slices (column stride 80 B: 8 consecutive
+// lanes' 16-byte reads hit distinct banks). Panel slices run two steps ahead (ping-pong
+// registers, then LDS), the members' A fragments (their k-th valid slot) one step ahead.
 constexpr int kGroupWaves = 4;
 constexpr int kPanelColStride = 80;
+constexpr int kRing = 3;
 
 template<int kN>
-__global__ __launch_bounds__(kWave *kGroupWaves) void bell_spmm_mfma_grouped(
-    BellArgs a, const std::uint16_t *packed_rhs, std::uint32_t panel_bytes,
-    const std::uint32_t *order, const std::uint32_t *group_offsets) {
+__global__ __launch_bounds__(kWave *kGroupWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void bell_spmm_mfma_grouped(BellArgs a, const std::uint16_t *packed_rhs, std::uint32_t panel_bytes,
+                            const std::uint32_t *order, const std::uint32_t *group_offsets,
+                            std::uint32_t group_count, std::uint32_t grouped_row_blocks) {
     constexpr int kTiles = kN / 32;
     constexpr int kSlice = kN * kPanelColStride;
     constexpr int kChunks = kN * 4;  // 16-byte chunks of one N x 32 bf16 slice
-    __shared__ __attribute__((aligned(16))) unsigned char bslice[2][kSlice];
+    constexpr int kThreads = kWave * kGroupWaves;
+    constexpr int kLoadIters = (kChunks + kThreads - 1) / kThreads;
+    __shared__ __attribute__((aligned(16))) unsigned char bslice[kRing][kSlice];
     const int lane = static_cast<int>(threadIdx.x) % kWave;
     const std::uint32_t wave = static_cast<std::uint32_t>(
         __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave)));
-    const std::uint32_t g0 = group_offsets[blockIdx.x], g1 = group_offsets[blockIdx.x + 1];
+    // workgroups past the groups take the single row blocks, one each
+    const bool single = blockIdx.x >= group_count;
+    const std::uint32_t g0 = single ? grouped_row_blocks + (blockIdx.x - group_count) : group_offsets[blockIdx.x];
+    const std::uint32_t g1 = single ? g0 + 1u : group_offsets[blockIdx.x + 1];
     const std::uint32_t members = g1 - g0;
     const std::uint32_t leader = order[g1 - 1u];
     const bool active = wave < members;
@@ -228,69 +235,81 @@ __global__ __launch_bounds__(kWave *kGroupWaves) void bell_spmm_mfma_grouped(
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
 
-    // next block column of the group / next own valid slot
+    // the group's next block column (after the last one: repeats it; never stored)
+    std::uint32_t last_bc = 0u;
     auto next_lead = [&]() {
-        const std::uint32_t s = static_cast<std::uint32_t>(__builtin_ctzll(lead_valid));
-        lead_valid &= lead_valid - 1ull;
-        return static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lead_sid), static_cast<int>(s)));
+        if (lead_valid != 0ull) {
+            const std::uint32_t s = static_cast<std::uint32_t>(__builtin_ctzll(lead_valid));
+            lead_valid &= lead_valid - 1ull;
+            last_bc = static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lead_sid), static_cast<int>(s)));
+        }
+        return last_bc;
     };
     auto next_own = [&]() {
         const std::uint32_t s = own_valid != 0ull ? static_cast<std::uint32_t>(__builtin_ctzll(own_valid)) : 0u;
         own_valid &= own_valid - 1ull;
         return s;
     };
-    struct BRegs { uint4 c[kChunks / (kWave * kGroupWaves)]; };
+    struct BRegs { uint4 c[kLoadIters]; };
     auto load_b = [&](BRegs &b, std::uint32_t bc) {
 #pragma unroll
-        for (int i = 0; i < kChunks / (kWave * kGroupWaves); ++i) {
-            const std::uint32_t c = threadIdx.x + static_cast<std::uint32_t>(i) * kWave * kGroupWaves;
+        for (int i = 0; i < kLoadIters; ++i) {
+            const std::uint32_t c = threadIdx.x + static_cast<std::uint32_t>(i) * kThreads;
+            const std::uint32_t cc = c < static_cast<std::uint32_t>(kChunks) ? c : 0u;
             const auto v = __builtin_amdgcn_raw_buffer_load_b128(
-                rbp, static_cast<int>(bc * static_cast<std::uint32_t>(kN) * 64u + c * 16u), 0, 0);
+                rbp, static_cast<int>(bc * static_cast<std::uint32_t>(kN) * 64u + cc * 16u), 0, 0);
             __builtin_memcpy(&b.c[i], &v, 16);
         }
     };
-    auto store_b = [&](const BRegs &b, int buf) {
+    auto store_b = [&](const BRegs &b, std::uint32_t slot) {
 #pragma unroll
-        for (int i = 0; i < kChunks / (kWave * kGroupWaves); ++i) {
-            const std::uint32_t c = threadIdx.x + static_cast<std::uint32_t>(i) * kWave * kGroupWaves;
-            *reinterpret_cast<uint4 *>(&bslice[buf][(c / 4u) * kPanelColStride + (c % 4u) * 16u]) = b.c[i];
+        for (int i = 0; i < kLoadIters; ++i) {
+            const std::uint32_t c = threadIdx.x + static_cast<std::uint32_t>(i) * kThreads;
+            if (c < static_cast<std::uint32_t>(kChunks))
+                *reinterpret_cast<uint4 *>(&bslice[slot][(c / 4u) * kPanelColStride + (c % 4u) * 16u]) = b.c[i];
         }
     };
     auto load_a = [&](cx_bf16x8 (&af)[2], std::uint32_t s) {
 #pragma unroll
         for (int kc = 0; kc < 2; ++kc) af[kc] = load_frag(ra, a_lane + s * 64u + static_cast<std::uint32_t>(kc) * 32u);
     };
-    auto mfma_step = [&](const cx_bf16x8 (&af)[2], int buf) {
+    auto mfma_step = [&](const cx_bf16x8 (&af)[2], std::uint32_t slot) {
 #pragma unroll
         for (int t = 0; t < kTiles; ++t)
 #pragma unroll
             for (int kc = 0; kc < 2; ++kc) {
                 cx_bf16x8 bf;
-                __builtin_memcpy(&bf, &bslice[buf][(t * 32 + m) * kPanelColStride + (kq + kc * 16) * 2], 16);
+                __builtin_memcpy(&bf, &bslice[slot][(t * 32 + m) * kPanelColStride + (kq + kc * 16) * 2], 16);
                 acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kc], bf, acc[t], 0, 0, 0);
             }
     };
 
     if (steps != 0u) {
-        BRegs b;
+        BRegs r0, r1;
         cx_bf16x8 a0[2], a1[2];
-        load_b(b, next_lead());
+        load_b(r0, next_lead());   // slice 0
+        load_b(r1, next_lead());   // slice 1 (in flight through step 0)
         load_a(a0, next_own());
-        store_b(b, 0);
+        store_b(r0, 0u);
         __syncthreads();
-        // step k reads buffer k % 2 and A set k % 2; loads for step k+1 are in flight
-        std::uint32_t k = 0;
+        // At step k: LDS slot k%3 holds slice k; registers hold slice k+1 (issued one step
+        // earlier); slice k+2 and A(k+1) are issued now; slice k+1 is stored after the MFMAs.
+        std::uint32_t k = 0, slot = 0;
+        auto step = [&](BRegs &mine_next, BRegs &free_regs, cx_bf16x8 (&a_cur)[2], cx_bf16x8 (&a_nxt)[2]) {
+            load_b(free_regs, next_lead());     // slice k+2
+            load_a(a_nxt, next_own());          // A(k+1)
+            if (active && k < own_steps) mfma_step(a_cur, slot);
+            const std::uint32_t nslot = slot + 1u == static_cast<std::uint32_t>(kRing) ? 0u : slot + 1u;
+            if (k + 1u < steps) store_b(mine_next, nslot);  // slice k+1
+            __syncthreads();
+            slot = nslot;
+            ++k;
+        };
         for (;;) {
-            if (k + 1u < steps) { load_b(b, next_lead()); load_a(a1, next_own()); }
-            if (active && k < own_steps) mfma_step(a0, 0);
-            if (k + 1u < steps) store_b(b, 1);
-            __syncthreads();
-            if (++k >= steps) break;
-            if (k + 1u < steps) { load_b(b, next_lead()); load_a(a0, next_own()); }
-            if (active && k < own_steps) mfma_step(a1, 1);
-            if (k + 1u < steps) store_b(b, 0);
-            __syncthreads();
-            if (++k >= steps) break;
+            step(r1, r0, a0, a1);
+            if (k >= steps) break;
+            step(r0, r1, a1, a0);
+            if (k >= steps) break;
         }
     }
 
@@ -518,7 +537,7 @@ extern "C" int cx_bell_spmm_fwd_grouped(const cx_bell_matrix *m, const uint16_t 
                 || groups->grouped_row_blocks > 4ull * groups->group_count))
         || (row_blocks != 0u && groups->order == nullptr))
         return fail(CX_STATUS_INVALID_SHAPE, "grouped Blocked-ELL: groups do not cover the row blocks");
-    if (groups->group_count != 0u && m->ell_cols / 32u > 64u)
+    if (m->ell_cols / 32u > 64u)
         return fail(CX_STATUS_UNSUPPORTED, "grouped Blocked-ELL supports at most 64 slots per row block");
     if (m->rows == 0u) return CX_STATUS_SUCCESS;
     const BellArgs a = make_args(m, packed_rhs, out_cols, out, out_ld);
@@ -528,25 +547,13 @@ extern "C" int cx_bell_spmm_fwd_grouped(const cx_bell_matrix *m, const uint16_t 
     const std::uint32_t pb = static_cast<std::uint32_t>(panel);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const dim3 gblock(kWave * kGroupWaves);
-    if (groups->group_count != 0u) {
-        const dim3 ggrid(groups->group_count);
-        switch (out_cols) {
-        case 64: hipLaunchKernelGGL(bell_spmm_mfma_grouped<64>, ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets); break;
-        case 128: hipLaunchKernelGGL(bell_spmm_mfma_grouped<128>, ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets); break;
-        default: hipLaunchKernelGGL(bell_spmm_mfma_grouped<256>, ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets); break;
-        }
-        rc = check_launch("bell_spmm_mfma_grouped");
-        if (rc != CX_STATUS_SUCCESS) return rc;
+    const dim3 ggrid(groups->group_count + groups->single_count);
+    const std::uint32_t gc = groups->group_count, grb = groups->grouped_row_blocks;
+    switch (out_cols) {
+    case 64: hipLaunchKernelGGL(bell_spmm_mfma_grouped<64>, ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb); break;
+    case 128: hipLaunchKernelGGL(bell_spmm_mfma_grouped<128>, ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb); break;
+    default: hipLaunchKernelGGL(bell_spmm_mfma_grouped<256>, ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb); break;
     }
-    if (groups->single_count != 0u) {
-        const std::uint32_t *singles = groups->order + groups->grouped_row_blocks;
-        const dim3 sgrid(groups->single_count);
-        switch (out_cols) {
-        case 64: hipLaunchKernelGGL(bell_spmm_mfma<64>, sgrid, dim3(64), 0, s, a, packed_rhs, pb, singles); break;
-        case 128: hipLaunchKernelGGL(bell_spmm_mfma<128>, sgrid, dim3(128), 0, s, a, packed_rhs, pb, singles); break;
-        default: hipLaunchKernelGGL(bell_spmm_mfma<256>, sgrid, dim3(256), 0, s, a, packed_rhs, pb, singles); break;
-        }
-        rc = check_launch("bell_spmm_mfma");
-    }
+    rc = check_launch("bell_spmm_mfma_grouped");
     return rc;
 }

@@ -198,8 +198,8 @@ const char *cx_bell_plan_last_error(void);
 
 /* Same result contract as cx_bell_spmm_fwd_packed: per group, each N x 32 panel slice is
  * loaded once (into LDS) for all members; per output element the MFMA accumulation runs in
- * the same slot order as the ungrouped kernel. Up to 64 slots per row block when groups
- * are present. */
+ * the same slot order as the ungrouped kernel. One launch: single row blocks run as
+ * one-member groups. At most 64 slots per row block. */
 int cx_bell_spmm_fwd_grouped(const cx_bell_matrix *a, const uint16_t *packed_rhs,
                              const cx_bell_groups *groups, int64_t out_cols, float *out,
                              int64_t out_ld, void *stream);
