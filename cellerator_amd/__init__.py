@@ -5,9 +5,10 @@ quantized CSR SpMM, Blocked-ELL SpMM on bf16 MFMA, and the CP-BP warp-tile
 feature-weighted row reduction. This package is the Python host mirror of that ABI;
 PyTorch supplies device memory and streams only.
 """
-from .engine import (BellGroups, BellMatrix, CpbpTiles, QcsrMatrix, bell_pack_rhs,  # noqa: F401
-                     bell_plan_groups, bell_spmm, bell_spmm_grouped, bell_spmm_packed, cpbp_reduce, csr_spmv, qcsr_pack_gene_affine, qcsr_spmm)
+from .engine import (BellGroups, BellMatrix, CpbpTiles, Epilogue, QcsrMatrix,  # noqa: F401
+                     bell_pack_rhs, bell_plan_groups, bell_spmm, bell_spmm_grouped,
+                     bell_spmm_packed, cpbp_reduce, csr_spmv, qcsr_pack_gene_affine, qcsr_spmm)
 
-__all__ = ["QcsrMatrix", "BellMatrix", "BellGroups", "CpbpTiles", "bell_plan_groups",
+__all__ = ["QcsrMatrix", "BellMatrix", "BellGroups", "CpbpTiles", "Epilogue", "bell_plan_groups",
            "bell_spmm_grouped", "qcsr_spmm", "bell_spmm", "bell_pack_rhs",
            "bell_spmm_packed", "cpbp_reduce", "csr_spmv", "qcsr_pack_gene_affine"]

@@ -17,6 +17,9 @@ SYNTH_PATH = PKG / "libcx_synth.so"
 # cellerator_dtype (include/cellerator_amd.h)
 DTYPE_F16, DTYPE_F32, DTYPE_U8, DTYPE_U32, DTYPE_BF16 = 1, 2, 3, 4, 5
 DECODE_PER_GENE_AFFINE, DECODE_COLUMN_SCALE_ROW_OFFSET, DECODE_PER_GENE_AFFINE_PAIRS = 1, 2, 3
+# CX_EPILOGUE_* = the reference's epilogue_kind values
+(EPILOGUE_NONE, EPILOGUE_BIAS, EPILOGUE_RELU, EPILOGUE_GELU_ERF, EPILOGUE_GELU_TANH,
+ EPILOGUE_BIAS_RELU, EPILOGUE_BIAS_GELU_ERF, EPILOGUE_BIAS_GELU_TANH) = range(8)
 STATUS_NAMES = {0: "SUCCESS", 1: "INVALID_ARGUMENT", 2: "INVALID_SHAPE", 3: "UNSUPPORTED",
                 4: "HIP_ERROR", 5: "INTERNAL_ERROR"}
 
@@ -40,6 +43,11 @@ class CxBellMatrix(C.Structure):
         ("decode_policy", u32), ("row_stride_bytes", u32), ("packed_values", p_void),
         ("column_scales", p_void), ("column_offsets", p_void), ("row_offsets", p_void),
     ]
+
+
+class CxSpmmEpilogue(C.Structure):
+    _fields_ = [("kind", u32), ("reserved", u32), ("alpha", C.c_float), ("beta", C.c_float),
+                ("bias", p_void), ("initial", p_void), ("initial_ld", i64)]
 
 
 class CxBellGroups(C.Structure):
@@ -132,15 +140,24 @@ class CelleratorSparseLayoutDesc(C.Structure):
 # Every symbol include/cellerator_amd.h declares, with its ctypes signature.
 ENGINE_SIGNATURES = {
     "cx_qcsr_spmm_fwd": (C.c_int, [C.POINTER(CxQcsrMatrix), p_void, u32, i64, i64, p_void, i64, p_void]),
+    "cx_qcsr_spmm_fwd_epilogue": (C.c_int, [C.POINTER(CxQcsrMatrix), p_void, u32, i64, i64, p_void,
+                                            i64, C.POINTER(CxSpmmEpilogue), p_void]),
     "cx_qcsr_pack_gene_affine": (C.c_int, [p_void, p_void, u32, p_void, p_void]),
     "cx_bell_spmm_fwd": (C.c_int, [C.POINTER(CxBellMatrix), p_void, u32, i64, i64, p_void, i64, p_void]),
+    "cx_bell_spmm_fwd_epilogue": (C.c_int, [C.POINTER(CxBellMatrix), p_void, u32, i64, i64, p_void,
+                                            i64, C.POINTER(CxSpmmEpilogue), p_void]),
     "cx_bell_pack_rhs": (C.c_int, [p_void, i64, u32, u32, p_void, p_void]),
     "cx_bell_spmm_fwd_packed": (C.c_int, [C.POINTER(CxBellMatrix), p_void, i64, p_void, i64, p_void]),
+    "cx_bell_spmm_fwd_packed_epilogue": (C.c_int, [C.POINTER(CxBellMatrix), p_void, i64, p_void, i64,
+                                                   C.POINTER(CxSpmmEpilogue), p_void]),
     "cx_bell_plan_groups": (C.c_int, [p_void, u32, u32, u32, p_void, p_void, C.POINTER(u32),
                                       C.POINTER(u32)]),
     "cx_bell_plan_last_error": (C.c_char_p, []),
     "cx_bell_spmm_fwd_grouped": (C.c_int, [C.POINTER(CxBellMatrix), p_void, C.POINTER(CxBellGroups),
                                            i64, p_void, i64, p_void]),
+    "cx_bell_spmm_fwd_grouped_epilogue": (C.c_int, [C.POINTER(CxBellMatrix), p_void,
+                                                    C.POINTER(CxBellGroups), i64, p_void, i64,
+                                                    C.POINTER(CxSpmmEpilogue), p_void]),
     "cx_cpbp_reduce": (C.c_int, [C.POINTER(CxCpbpTiles), p_void, u64, p_void, u64, p_void]),
     "cx_csr_spmv_fwd": (C.c_int, [u32, p_void, p_void, p_void, u32, p_void, p_void, p_void]),
     "cx_cpbp_builder_create": (C.c_int, [C.POINTER(CxCpbpPlan), C.POINTER(CxCpbpCsr),

@@ -24,10 +24,10 @@ constexpr u64 mfma_panel_limit = 65536ull * 256ull * 2ull;
 struct projection_state {
     bool live = false;
     projection_declaration declaration{};
-    execution::operand_axis_contract inputs[2]{};
+    execution::operand_axis_contract inputs[3]{};  // sparse, dense, bias (epilogue only)
     execution::operand_axis_contract outputs[1]{};
     execution::output_axis_contract orders[2]{};
-    execution::output_effect_contract effects[1]{};
+    execution::output_effect_contract effects[2]{};  // overwrite, affine_accumulate
     u32 order_count = 0u;
 };
 
@@ -53,18 +53,48 @@ core::operation_status engine_failed(int rc) noexcept {
         : fail(code::execution_failed, "engine rejected the launch (see last_engine_error)");
 }
 
+// ---- epilogue operations --------------------------------------------------------------
+
+struct epilogue_request {
+    std::uint32_t kind = CX_EPILOGUE_NONE;
+    bool affine = false;
+    bool bias = false;
+};
+
+// problem.operation -> epilogue; false for a malformed epilogue operation id.
+bool parse_operation(const core::stable_id &operation, epilogue_request *out) noexcept {
+    *out = epilogue_request{};
+    if (operation.low != spmm_epilogue_family) return true;  // the plain product
+    const u64 kind = operation.high & 0xffu;
+    if ((operation.high & ~(0xffull | spmm_affine_flag)) != 0u || kind > CX_EPILOGUE_BIAS_GELU_TANH)
+        return false;
+    out->kind = static_cast<std::uint32_t>(kind);
+    out->affine = (operation.high & spmm_affine_flag) != 0u;
+    out->bias = kind == CX_EPILOGUE_BIAS || kind == CX_EPILOGUE_BIAS_RELU
+        || kind == CX_EPILOGUE_BIAS_GELU_ERF || kind == CX_EPILOGUE_BIAS_GELU_TANH;
+    return true;
+}
+
+bool is_epilogue_operation(const core::stable_id &operation) noexcept {
+    return operation.low == spmm_epilogue_family;
+}
+
 // ---- numeric policies ----------------------------------------------------------------
 
 bool common_numeric(const core::numeric_policy &n) noexcept {
     return n.output_storage == numeric_type::f32 && n.multiply == numeric_type::f32
         && n.accumulation == numeric_type::f32 && n.scalar == numeric_type::f32
-        && n.bias == numeric_type::invalid
         && n.rounding == core::rounding_policy::nearest_even
         && n.saturation == core::saturation_policy::none;
 }
 
+// Multiplies take an optional f32 bias (epilogue); the reduction takes none.
+bool multiply_numeric(const core::numeric_policy &n) noexcept {
+    return common_numeric(n) && (n.bias == numeric_type::invalid || n.bias == numeric_type::f32);
+}
+
 bool supports_quantized_csr(const core::numeric_policy &n) noexcept {
-    if (!common_numeric(n)) return false;
+    if (!multiply_numeric(n)) return false;
     if (n.dense_storage != numeric_type::f16 && n.dense_storage != numeric_type::f32)
         return false;
     if (n.sparse_storage == numeric_type::u8)
@@ -78,13 +108,13 @@ bool plain_storage(numeric_type t) noexcept {
 }
 
 bool supports_blocked_ell(const core::numeric_policy &n) noexcept {
-    return common_numeric(n) && plain_storage(n.sparse_storage)
+    return multiply_numeric(n) && plain_storage(n.sparse_storage)
         && plain_storage(n.dense_storage)
         && n.quantization == core::quantization_granularity::none;
 }
 
 bool supports_cpbp(const core::numeric_policy &n) noexcept {
-    return common_numeric(n)
+    return common_numeric(n) && n.bias == numeric_type::invalid
         && (n.sparse_storage == numeric_type::f16 || n.sparse_storage == numeric_type::f32)
         && n.dense_storage == numeric_type::f32
         && n.quantization == core::quantization_granularity::none;
@@ -155,6 +185,51 @@ bool dense_shape(const execution::dense_tensor_view &v, numeric_type type, u32 r
     return v.shape[1] == cols && v.stride[1] == 1 && v.stride[0] >= static_cast<i64>(cols);
 }
 
+// Launch-time epilogue of a prepared multiply: the bias operand (inputs[2]) and, for the
+// affine effect, alpha / beta from the scalar bindings with Y itself as C.
+bool scalar_value_of(const execution::launch_bindings &l, u32 id, float *value) noexcept {
+    for (u32 i = 0u; i < l.scalars.count && i < execution::maximum_scalar_bindings; ++i) {
+        const execution::scalar_binding &b = l.scalars.values[i];
+        if (b.binding_id != id) continue;
+        if (b.type == numeric_type::f32) {
+            const std::uint32_t bits = static_cast<std::uint32_t>(b.bits);
+            std::memcpy(value, &bits, sizeof(bits));
+            return true;
+        }
+        if (b.type == numeric_type::f64) {
+            double d;
+            std::memcpy(&d, &b.bits, sizeof(d));
+            *value = static_cast<float>(d);
+            return true;
+        }
+        return false;
+    }
+    return false;
+}
+
+const char *bind_epilogue(const core::prepared_operation &p, const projection_declaration &d,
+                          const execution::launch_bindings &l,
+                          const execution::dense_tensor_view &y, cx_spmm_epilogue *ep) noexcept {
+    epilogue_request e;
+    if (!parse_operation(p.problem.operation, &e)) return "malformed epilogue operation";
+    *ep = cx_spmm_epilogue{};
+    ep->kind = e.kind;
+    ep->alpha = 1.0f;
+    if (e.bias) {
+        if (l.input_count != 3u || l.inputs[2].kind != execution::operand_kind::dense_tensor
+            || !dense_shape(l.inputs[2].storage.dense, numeric_type::f32, 1u, d.output_columns, 0u, l))
+            return "bias must be a contiguous f32 [N] tensor";
+        ep->bias = static_cast<const float *>(l.inputs[2].storage.dense.data);
+    }
+    if (e.affine) {
+        if (!scalar_value_of(l, alpha_binding, &ep->alpha) || !scalar_value_of(l, beta_binding, &ep->beta))
+            return "affine accumulation needs f32 or f64 alpha and beta scalars";
+        ep->initial = static_cast<const float *>(y.data);
+        ep->initial_ld = y.stride[0];
+    }
+    return nullptr;
+}
+
 // ---- run functions --------------------------------------------------------------------
 
 core::operation_status run_quantized_csr(const core::prepared_operation &p,
@@ -198,9 +273,11 @@ core::operation_status run_quantized_csr(const core::prepared_operation &p,
         return bad_launch("W must be a row-major [genes x N] tensor of the dense storage type");
     if (!dense_shape(y, numeric_type::f32, 2u, d.rows, d.output_columns, l))
         return bad_launch("Y must be a row-major f32 [cells x N] tensor");
-    const int rc = cx_qcsr_spmm_fwd(&a, w.data, engine_dtype(w.value_type), w.stride[0],
-                                    d.output_columns, static_cast<float *>(y.data), y.stride[0],
-                                    l.stream.stream);
+    cx_spmm_epilogue ep;
+    if (const char *why = bind_epilogue(p, d, l, y, &ep)) return bad_launch(why);
+    const int rc = cx_qcsr_spmm_fwd_epilogue(&a, w.data, engine_dtype(w.value_type), w.stride[0],
+                                             d.output_columns, static_cast<float *>(y.data),
+                                             y.stride[0], &ep, l.stream.stream);
     return rc == CX_STATUS_SUCCESS ? core::operation_status{} : engine_failed(rc);
 }
 
@@ -232,19 +309,21 @@ core::operation_status run_blocked_ell(const core::prepared_operation &p,
         return bad_launch("W must be a row-major [genes x N] tensor of the dense storage type");
     if (!dense_shape(y, numeric_type::f32, 2u, d.rows, d.output_columns, l))
         return bad_launch("Y must be a row-major f32 [cells x N] tensor");
+    cx_spmm_epilogue ep;
+    if (const char *why = bind_epilogue(p, d, l, y, &ep)) return bad_launch(why);
     int rc;
     if (core::same_stable_id(p.kernel, blocked_ell_mfma_kernel_id)) {
         auto *panel = static_cast<uint16_t *>(l.workspace.data);
         rc = cx_bell_pack_rhs(static_cast<const uint16_t *>(w.data), w.stride[0], d.cols,
                               d.output_columns, panel, l.stream.stream);
         if (rc == CX_STATUS_SUCCESS)
-            rc = cx_bell_spmm_fwd_packed(&a, panel, d.output_columns,
-                                         static_cast<float *>(y.data), y.stride[0],
-                                         l.stream.stream);
+            rc = cx_bell_spmm_fwd_packed_epilogue(&a, panel, d.output_columns,
+                                                  static_cast<float *>(y.data), y.stride[0], &ep,
+                                                  l.stream.stream);
     } else {
-        rc = cx_bell_spmm_fwd(&a, w.data, engine_dtype(w.value_type), w.stride[0],
-                              d.output_columns, static_cast<float *>(y.data), y.stride[0],
-                              l.stream.stream);
+        rc = cx_bell_spmm_fwd_epilogue(&a, w.data, engine_dtype(w.value_type), w.stride[0],
+                                       d.output_columns, static_cast<float *>(y.data),
+                                       y.stride[0], &ep, l.stream.stream);
     }
     return rc == CX_STATUS_SUCCESS ? core::operation_status{} : engine_failed(rc);
 }
@@ -324,9 +403,19 @@ core::operation_status prepare(
         || !execution::same_identity(structures.structures[0].persistent, d.persistent_structure))
         return {code::stale_structure, execution::binding_validation_code::stale_structure,
             "structure key differs from the declared projection's structure"};
-    if (problem.input_count != 2u || problem.output_count != 1u)
+    epilogue_request epilogue;
+    if (!parse_operation(problem.operation, &epilogue))
+        return fail(code::unsupported_problem, "unknown epilogue in the operation identity");
+    const bool reduce = candidate.operation == core::operation_kind::weighted_relation_reduce;
+    if (reduce && is_epilogue_operation(problem.operation))
+        return fail(code::unsupported_problem, "the row reduction has no epilogue");
+    if (epilogue.bias != (numeric.bias == numeric_type::f32))
+        return fail(code::unsupported_numeric_policy,
+            "a bias epilogue needs numeric bias f32, and only a bias epilogue may declare one");
+    const u32 input_count = epilogue.bias ? 3u : 2u;
+    if (problem.input_count != input_count || problem.output_count != 1u)
         return fail(code::unsupported_problem,
-            "operation takes one sparse and one dense input and one output");
+            "operation takes one sparse and one dense input (plus the bias) and one output");
     if (projection.kind == core::projection_kind::csr
         && (projection.variant != 0u) != (numeric.sparse_storage == numeric_type::u8))
         return fail(code::unsupported_numeric_policy,
@@ -335,7 +424,7 @@ core::operation_status prepare(
     core::stable_id kernel = candidate.identity;
     core::run_function run = run_quantized_csr;
     u64 workspace = 0u;
-    if (candidate.operation == core::operation_kind::weighted_relation_reduce) {
+    if (reduce) {
         run = run_cpbp;
     } else if (projection.kind == core::projection_kind::blocked_ell) {
         const bool mfma = mfma_eligible(d, numeric);
@@ -359,8 +448,8 @@ core::operation_status prepare(
     prepared->binding_contract.inputs = state->inputs;
     prepared->binding_contract.outputs = state->outputs;
     prepared->binding_contract.output_orders = state->orders;
-    prepared->binding_contract.output_effects = state->effects;
-    prepared->binding_contract.input_count = 2u;
+    prepared->binding_contract.output_effects = &state->effects[epilogue.affine ? 1 : 0];
+    prepared->binding_contract.input_count = input_count;
     prepared->binding_contract.output_count = 1u;
     prepared->binding_contract.output_order_count = state->order_count;
     prepared->binding_contract.structure_count = 1u;
@@ -443,6 +532,9 @@ core::operation_status declare_projection(const projection_declaration &d) noexc
         slot->inputs[1].rank = 2u;
         slot->inputs[1].axes[0] = genes;
         slot->inputs[1].axes[1] = d.output_axis;
+        slot->inputs[2].kind = execution::operand_kind::dense_tensor;
+        slot->inputs[2].rank = 1u;
+        slot->inputs[2].axes[0] = d.output_axis;
         slot->outputs[0].rank = 2u;
         slot->outputs[0].axes[0] = cells;
         slot->outputs[0].axes[1] = d.output_axis;
@@ -460,6 +552,8 @@ core::operation_status declare_projection(const projection_declaration &d) noexc
     }
     slot->effects[0] = {execution::output_update_kind::overwrite, false, false, 0u,
         execution::invalid_scalar_binding_id, execution::invalid_scalar_binding_id};
+    slot->effects[1] = {execution::output_update_kind::affine_accumulate, true, false, 0u,
+        alpha_binding, beta_binding};
     slot->live = true;
     return {};
 }

@@ -30,6 +30,17 @@
 //   outputs[0] dense_tensor f32: Y [cells x N] row-major, or y [cells] in canonical order.
 // The stream is launch.stream.stream (a hipStream_t, NULL = the null stream). Run
 // launches kernels only: it neither allocates, synchronizes nor queries the device.
+//
+// Fused epilogues (the two multiply candidates). operation_problem names the operation's
+// semantics, so an epilogue travels in problem.operation = spmm_operation(kind, affine):
+//   kind    the reference's epilogue_kind (operation.hh:49-58, CX_EPILOGUE_*): bias kinds
+//           bind inputs[2] = bias, a dense f32 [N] tensor on the output axis
+//           (numeric_policy.bias = f32, problem.input_count = 3); the others take none
+//           (numeric_policy.bias = invalid, input_count = 2);
+//   affine  output effect affine_accumulate: Y = act(alpha * A.W + beta * Y + bias) in
+//           place, alpha and beta bound per launch as f32 (or f64) scalars with binding ids
+//           alpha_binding and beta_binding. Otherwise the effect is overwrite.
+// Any other problem.operation is the plain product (kind none, overwrite).
 #pragma once
 
 #include <Cellerator/compute/math/operation_core/operation_core.hh>
@@ -52,6 +63,16 @@ inline constexpr core::stable_id blocked_ell_candidate_id{0x4358414d4442454cull,
 inline constexpr core::stable_id cpbp_candidate_id{0x4358414d44435042ull, 1u};
 inline constexpr core::stable_id blocked_ell_mfma_kernel_id{0x4358414d4442454cull, 2u};
 inline constexpr core::stable_id blocked_ell_generic_kernel_id{0x4358414d4442454cull, 3u};
+
+// problem.operation of a multiply with a fused epilogue (see the file comment).
+inline constexpr std::uint64_t spmm_epilogue_family = 0x4358414d44455049ull;
+inline constexpr std::uint64_t spmm_affine_flag = 0x100u;
+inline constexpr std::uint32_t alpha_binding = 0u;
+inline constexpr std::uint32_t beta_binding = 1u;
+
+constexpr core::stable_id spmm_operation(std::uint32_t kind, bool affine) noexcept {
+    return {spmm_epilogue_family, static_cast<std::uint64_t>(kind) | (affine ? spmm_affine_flag : 0u)};
+}
 
 // projection_key.variant of a quantized CSR projection: the code width in bits (1, 2, 4,
 // 8), or 0 for plain f16 / f32 values.

@@ -44,6 +44,7 @@ struct BellArgs {
     std::uint32_t block_size;
     std::uint32_t ell_cols;
     std::uint32_t row_stride_bytes;
+    Epilogue ep;
 };
 
 // Row block handled by workgroup `wg` of `count`: XCD-major so that the row blocks a
@@ -171,7 +172,9 @@ __global__ __launch_bounds__(kN) void bell_spmm_mfma(BellArgs a, const std::uint
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const std::uint32_t r = rb * 32u + 8u * (i / 4) + 4u * (lane / 32) + (i % 4);
-            if (r < a.rows) a.out[static_cast<std::int64_t>(r) * a.out_ld + col] = acc[t][i];
+            if (r < a.rows)
+                a.out[static_cast<std::int64_t>(r) * a.out_ld + col] =
+                    a.ep.active ? epilogue_value(a.ep, acc[t][i], r, col) : acc[t][i];
         }
     }
 }
@@ -320,7 +323,9 @@ void bell_spmm_mfma_grouped(BellArgs a, const std::uint16_t *packed_rhs, std::ui
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const std::uint32_t r = rb * 32u + 8u * (i / 4) + 4u * (lane / 32) + (i % 4);
-            if (r < a.rows) a.out[static_cast<std::int64_t>(r) * a.out_ld + col] = acc[t][i];
+            if (r < a.rows)
+                a.out[static_cast<std::int64_t>(r) * a.out_ld + col] =
+                    a.ep.active ? epilogue_value(a.ep, acc[t][i], r, col) : acc[t][i];
         }
     }
 }
@@ -389,7 +394,9 @@ __global__ __launch_bounds__(256) void bell_spmm_generic(BellArgs a, std::uint32
                 }
             }
         }
-        if (c < n) a.out[static_cast<std::int64_t>(row) * a.out_ld + c] = acc;
+        if (c < n)
+            a.out[static_cast<std::int64_t>(row) * a.out_ld + c] =
+                a.ep.active ? epilogue_value(a.ep, acc, row, c) : acc;
     }
 }
 
@@ -425,8 +432,9 @@ int validate_bell(const cx_bell_matrix *m, const void *rhs, std::int64_t rhs_ld,
 }
 
 BellArgs make_args(const cx_bell_matrix *m, const void *rhs, std::int64_t rhs_ld, float *out,
-                   std::int64_t out_ld) {
+                   std::int64_t out_ld, const Epilogue &ep) {
     BellArgs a{};
+    a.ep = ep;
     a.block_col_idx = m->block_col_idx;
     a.values = m->values;
     a.packed = m->packed_values;
@@ -451,15 +459,26 @@ BellArgs make_args(const cx_bell_matrix *m, const void *rhs, std::int64_t rhs_ld
 extern "C" int cx_bell_spmm_fwd(const cx_bell_matrix *m, const void *rhs, uint32_t rhs_dtype,
                                 int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
                                 void *stream) {
+    return cx_bell_spmm_fwd_epilogue(m, rhs, rhs_dtype, rhs_ld, out_cols, out, out_ld, nullptr,
+                                     stream);
+}
+
+extern "C" int cx_bell_spmm_fwd_epilogue(const cx_bell_matrix *m, const void *rhs,
+                                         uint32_t rhs_dtype, int64_t rhs_ld, int64_t out_cols,
+                                         float *out, int64_t out_ld,
+                                         const cx_spmm_epilogue *epilogue, void *stream) {
     using namespace cx;
     clear_error();
     int rc = validate_bell(m, rhs, rhs_ld, out_cols, out, out_ld);
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    Epilogue ep;
+    rc = make_epilogue(epilogue, m->rows, out_cols, out, out_ld, &ep, "cx_bell_spmm_fwd");
     if (rc != CX_STATUS_SUCCESS) return rc;
     if (rhs_dtype != CELLERATOR_DTYPE_F32 && rhs_dtype != CELLERATOR_DTYPE_F16
         && rhs_dtype != CELLERATOR_DTYPE_BF16)
         return fail(CX_STATUS_UNSUPPORTED, "Blocked-ELL rhs must be F32, F16 or BF16");
     if (m->rows == 0u) return CX_STATUS_SUCCESS;
-    const BellArgs a = make_args(m, rhs, rhs_ld, out, out_ld);
+    const BellArgs a = make_args(m, rhs, rhs_ld, out, out_ld, ep);
     const std::uint64_t threads = static_cast<std::uint64_t>(m->rows) * kWave;
     hipLaunchKernelGGL(bell_spmm_generic, dim3(static_cast<unsigned>((threads + 255) / 256)),
                        dim3(256), 0, static_cast<hipStream_t>(stream), a, m->value_dtype,
@@ -484,9 +503,19 @@ extern "C" int cx_bell_pack_rhs(const uint16_t *rhs_bf16, int64_t rhs_ld, uint32
 extern "C" int cx_bell_spmm_fwd_packed(const cx_bell_matrix *m, const uint16_t *packed_rhs,
                                        int64_t out_cols, float *out, int64_t out_ld,
                                        void *stream) {
+    return cx_bell_spmm_fwd_packed_epilogue(m, packed_rhs, out_cols, out, out_ld, nullptr, stream);
+}
+
+extern "C" int cx_bell_spmm_fwd_packed_epilogue(const cx_bell_matrix *m,
+                                                const uint16_t *packed_rhs, int64_t out_cols,
+                                                float *out, int64_t out_ld,
+                                                const cx_spmm_epilogue *epilogue, void *stream) {
     using namespace cx;
     clear_error();
     int rc = validate_bell(m, packed_rhs, out_cols, out_cols, out, out_ld);
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    Epilogue ep;
+    rc = make_epilogue(epilogue, m->rows, out_cols, out, out_ld, &ep, "cx_bell_spmm_fwd_packed");
     if (rc != CX_STATUS_SUCCESS) return rc;
     if (m->bits != 0u || m->value_dtype != CELLERATOR_DTYPE_BF16 || m->block_size != 32u)
         return fail(CX_STATUS_UNSUPPORTED,
@@ -497,7 +526,7 @@ extern "C" int cx_bell_spmm_fwd_packed(const cx_bell_matrix *m, const uint16_t *
         || (reinterpret_cast<std::uintptr_t>(packed_rhs) & 15u) != 0u)
         return fail(CX_STATUS_INVALID_ARGUMENT, "MFMA Blocked-ELL operands must be 16-byte aligned");
     if (m->rows == 0u) return CX_STATUS_SUCCESS;
-    const BellArgs a = make_args(m, packed_rhs, out_cols, out, out_ld);
+    const BellArgs a = make_args(m, packed_rhs, out_cols, out, out_ld, ep);
     const unsigned row_blocks = (m->rows + 31u) / 32u;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const std::uint64_t panel = static_cast<std::uint64_t>((m->cols + 31u) / 32u) * static_cast<std::uint64_t>(out_cols) * 64u;
@@ -517,9 +546,21 @@ extern "C" int cx_bell_spmm_fwd_packed(const cx_bell_matrix *m, const uint16_t *
 extern "C" int cx_bell_spmm_fwd_grouped(const cx_bell_matrix *m, const uint16_t *packed_rhs,
                                         const cx_bell_groups *groups, int64_t out_cols,
                                         float *out, int64_t out_ld, void *stream) {
+    return cx_bell_spmm_fwd_grouped_epilogue(m, packed_rhs, groups, out_cols, out, out_ld, nullptr,
+                                             stream);
+}
+
+extern "C" int cx_bell_spmm_fwd_grouped_epilogue(const cx_bell_matrix *m,
+                                                 const uint16_t *packed_rhs,
+                                                 const cx_bell_groups *groups, int64_t out_cols,
+                                                 float *out, int64_t out_ld,
+                                                 const cx_spmm_epilogue *epilogue, void *stream) {
     using namespace cx;
     clear_error();
     int rc = validate_bell(m, packed_rhs, out_cols, out_cols, out, out_ld);
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    Epilogue ep;
+    rc = make_epilogue(epilogue, m->rows, out_cols, out, out_ld, &ep, "cx_bell_spmm_fwd_grouped");
     if (rc != CX_STATUS_SUCCESS) return rc;
     if (groups == nullptr) return fail(CX_STATUS_INVALID_ARGUMENT, "grouped Blocked-ELL: null groups");
     if (m->bits != 0u || m->value_dtype != CELLERATOR_DTYPE_BF16 || m->block_size != 32u)
@@ -540,7 +581,7 @@ extern "C" int cx_bell_spmm_fwd_grouped(const cx_bell_matrix *m, const uint16_t 
     if (m->ell_cols / 32u > 64u)
         return fail(CX_STATUS_UNSUPPORTED, "grouped Blocked-ELL supports at most 64 slots per row block");
     if (m->rows == 0u) return CX_STATUS_SUCCESS;
-    const BellArgs a = make_args(m, packed_rhs, out_cols, out, out_ld);
+    const BellArgs a = make_args(m, packed_rhs, out_cols, out, out_ld, ep);
     const std::uint64_t panel = static_cast<std::uint64_t>((m->cols + 31u) / 32u) * static_cast<std::uint64_t>(out_cols) * 64u;
     if (panel > 0xFFFFFFFFull || static_cast<std::uint64_t>(32u) * m->ell_cols * 2u > 0xFFFFFFFFull)
         return fail(CX_STATUS_INVALID_SHAPE, "MFMA Blocked-ELL: packed panel or row block exceeds 4 GiB");

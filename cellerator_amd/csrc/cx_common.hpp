@@ -39,6 +39,46 @@ __device__ __forceinline__ float bf2f(std::uint16_t bits) {
     return __uint_as_float(static_cast<std::uint32_t>(bits) << 16);
 }
 
+// Device form of cx_spmm_epilogue. `active` == 0 means a plain store of the accumulator.
+struct Epilogue {
+    const float *bias;
+    const float *initial;
+    std::int64_t initial_ld;
+    float alpha;
+    float beta;
+    std::uint32_t kind;
+    std::uint32_t active;
+};
+
+// Validates `ep` (NULL = none) for an fp32 output of rows x cols at `out` (leading
+// dimension out_ld) and fills `dev`; `who` prefixes the error text.
+int make_epilogue(const cx_spmm_epilogue *ep, std::uint64_t rows, std::int64_t cols,
+                  const float *out, std::int64_t out_ld, Epilogue *dev, const char *who);
+
+__device__ __forceinline__ bool bias_kind(std::uint32_t kind) {
+    return kind == CX_EPILOGUE_BIAS || kind == CX_EPILOGUE_BIAS_RELU
+        || kind == CX_EPILOGUE_BIAS_GELU_ERF || kind == CX_EPILOGUE_BIAS_GELU_TANH;
+}
+
+// act(alpha * acc + beta * C[row, col] + bias[col]) in fp32, in the referee's order
+// (src/compute/math/referee.cc:81-97): scale and accumulate, add the bias, then activate.
+__device__ __forceinline__ float epilogue_value(const Epilogue &e, float acc, std::int64_t row,
+                                                std::int64_t col) {
+    float v = e.alpha == 0.0f ? 0.0f : e.alpha * acc;
+    if (e.beta != 0.0f) v = __builtin_fmaf(e.beta, e.initial[row * e.initial_ld + col], v);
+    if (bias_kind(e.kind)) v += e.bias[col];
+    switch (e.kind) {
+    case CX_EPILOGUE_RELU:
+    case CX_EPILOGUE_BIAS_RELU: return fmaxf(v, 0.0f);
+    case CX_EPILOGUE_GELU_ERF:
+    case CX_EPILOGUE_BIAS_GELU_ERF: return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+    case CX_EPILOGUE_GELU_TANH:
+    case CX_EPILOGUE_BIAS_GELU_TANH:
+        return 0.5f * v * (1.0f + tanhf(0.79788456080286536f * (v + 0.044715f * v * v * v)));
+    default: return v;
+    }
+}
+
 // Sum over the lanes that differ only in the bits of `mask_bits` (xor butterfly).
 template<int kFirstBit, int kLastBit>
 __device__ __forceinline__ float xor_reduce(float v) {

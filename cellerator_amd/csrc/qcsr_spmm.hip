@@ -42,6 +42,7 @@ struct QcsrArgs {
     std::int64_t out_ld;
     std::uint32_t rows;
     std::uint32_t cols;
+    Epilogue ep;
 };
 
 constexpr int kWavesPerBlock = 4;
@@ -171,6 +172,10 @@ __global__ __launch_bounds__(kWave *kWavesPerBlock) void qcsr_spmm_rowwave(QcsrA
     }
     if (g == 0) {
         float *dst = a.out + static_cast<std::int64_t>(row) * a.out_ld + j * kCpl;
+        if (a.ep.active) {
+#pragma unroll
+            for (int k = 0; k < kCpl; ++k) acc[k] = epilogue_value(a.ep, acc[k], row, j * kCpl + k);
+        }
 #pragma unroll
         for (int k = 0; k < kCpl; k += 4)
             *reinterpret_cast<float4 *>(dst + k) = make_float4(acc[k], acc[k + 1], acc[k + 2],
@@ -211,7 +216,9 @@ __global__ __launch_bounds__(kWave *kWavesPerBlock) void qcsr_spmm_generic(QcsrA
                 acc = __builtin_fmaf(x, wf, acc);
             }
         }
-        if (c < n) a.out[static_cast<std::int64_t>(row) * a.out_ld + c] = acc;
+        if (c < n)
+            a.out[static_cast<std::int64_t>(row) * a.out_ld + c] =
+                a.ep.active ? epilogue_value(a.ep, acc, row, c) : acc;
     }
 }
 
@@ -271,6 +278,14 @@ bool aligned16(const void *p) { return (reinterpret_cast<std::uintptr_t>(p) & 15
 extern "C" int cx_qcsr_spmm_fwd(const cx_qcsr_matrix *m, const void *rhs, uint32_t rhs_dtype,
                                 int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
                                 void *stream) {
+    return cx_qcsr_spmm_fwd_epilogue(m, rhs, rhs_dtype, rhs_ld, out_cols, out, out_ld, nullptr,
+                                     stream);
+}
+
+extern "C" int cx_qcsr_spmm_fwd_epilogue(const cx_qcsr_matrix *m, const void *rhs,
+                                         uint32_t rhs_dtype, int64_t rhs_ld, int64_t out_cols,
+                                         float *out, int64_t out_ld,
+                                         const cx_spmm_epilogue *epilogue, void *stream) {
     using namespace cx;
     clear_error();
     if (m == nullptr || out == nullptr || rhs == nullptr)
@@ -307,8 +322,12 @@ extern "C" int cx_qcsr_spmm_fwd(const cx_qcsr_matrix *m, const void *rhs, uint32
     }
     if (static_cast<const void *>(out) == rhs)
         return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd: output aliases the rhs");
+    Epilogue ep;
+    const int erc = make_epilogue(epilogue, m->rows, out_cols, out, out_ld, &ep, "cx_qcsr_spmm_fwd");
+    if (erc != CX_STATUS_SUCCESS) return erc;
 
     QcsrArgs a{};
+    a.ep = ep;
     a.row_ptr = m->row_ptr;
     a.packed_row_ptr = m->packed_row_ptr;
     a.col_idx = m->col_idx;

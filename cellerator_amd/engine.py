@@ -84,9 +84,35 @@ class QcsrMatrix:
         return b + self.cols * rhs_cols * rhs_bytes + self.rows * rhs_cols * 4
 
 
+@dataclass
+class Epilogue:
+    """Fused SpMM epilogue: Y = act(alpha * (A . W) + beta * C + bias), kind = one of the
+    reference's epilogue_kind values (N.EPILOGUE_*). `initial` (C, f32 [rows, N]) is read only
+    when beta != 0 and may be the output itself (in-place update); `bias` is f32 [N] for the
+    bias kinds."""
+    kind: int = N.EPILOGUE_NONE
+    alpha: float = 1.0
+    beta: float = 0.0
+    bias: Optional[torch.Tensor] = None
+    initial: Optional[torch.Tensor] = None
+
+    def descriptor(self, out: torch.Tensor) -> N.CxSpmmEpilogue:
+        for t in (self.bias, self.initial):
+            if t is not None and (t.dtype != torch.float32 or t.device != out.device):
+                raise ValueError("epilogue tensors must be f32 on the output's device")
+        if self.bias is not None and not self.bias.is_contiguous():
+            raise ValueError("bias must be contiguous")
+        if self.initial is not None and (self.initial.dim() != 2 or self.initial.stride(1) != 1):
+            raise ValueError("initial must be a row-major [rows, N] tensor")
+        return N.CxSpmmEpilogue(self.kind, 0, self.alpha, self.beta, _ptr(self.bias),
+                                _ptr(self.initial),
+                                self.initial.stride(0) if self.initial is not None else 0)
+
+
 def qcsr_spmm(m: QcsrMatrix, rhs: torch.Tensor, out: Optional[torch.Tensor] = None,
-              stream=None) -> torch.Tensor:
-    """Y = decode(X) . rhs (fp32). rhs: [cols, N] f16/f32, row-major (leading dim = stride)."""
+              stream=None, epilogue: Optional[Epilogue] = None) -> torch.Tensor:
+    """Y = decode(X) . rhs (fp32), optionally through a fused epilogue.
+    rhs: [cols, N] f16/f32, row-major (leading dim = stride)."""
     _require_cuda(m.row_ptr, m.col_idx, rhs)
     if rhs.dim() != 2 or rhs.shape[0] != m.cols or rhs.stride(1) != 1:
         raise ValueError("rhs must be [cols, N] with unit column stride")
@@ -94,9 +120,15 @@ def qcsr_spmm(m: QcsrMatrix, rhs: torch.Tensor, out: Optional[torch.Tensor] = No
     if out is None:
         out = torch.empty((m.rows, n), dtype=torch.float32, device=rhs.device)
     d = m.descriptor()
-    N.check("cx_qcsr_spmm_fwd", N.engine().cx_qcsr_spmm_fwd(
-        C.byref(d), rhs.data_ptr(), _DTYPE_CODE[rhs.dtype], rhs.stride(0), n, out.data_ptr(),
-        out.stride(0), _stream(stream)))
+    if epilogue is None:
+        N.check("cx_qcsr_spmm_fwd", N.engine().cx_qcsr_spmm_fwd(
+            C.byref(d), rhs.data_ptr(), _DTYPE_CODE[rhs.dtype], rhs.stride(0), n, out.data_ptr(),
+            out.stride(0), _stream(stream)))
+    else:
+        e = epilogue.descriptor(out)
+        N.check("cx_qcsr_spmm_fwd_epilogue", N.engine().cx_qcsr_spmm_fwd_epilogue(
+            C.byref(d), rhs.data_ptr(), _DTYPE_CODE[rhs.dtype], rhs.stride(0), n, out.data_ptr(),
+            out.stride(0), C.byref(e), _stream(stream)))
     return out
 
 
@@ -146,16 +178,22 @@ class BellMatrix:
 
 
 def bell_spmm(m: BellMatrix, rhs: torch.Tensor, out: Optional[torch.Tensor] = None,
-              stream=None) -> torch.Tensor:
+              stream=None, epilogue: Optional[Epilogue] = None) -> torch.Tensor:
     """Reference-semantics Blocked-ELL SpMM with a row-major rhs [cols, N]."""
     _require_cuda(m.block_col_idx, rhs)
     n = rhs.shape[1]
     if out is None:
         out = torch.empty((m.rows, n), dtype=torch.float32, device=rhs.device)
     d = m.descriptor()
-    N.check("cx_bell_spmm_fwd", N.engine().cx_bell_spmm_fwd(
-        C.byref(d), rhs.data_ptr(), _DTYPE_CODE[rhs.dtype], rhs.stride(0), n, out.data_ptr(),
-        out.stride(0), _stream(stream)))
+    if epilogue is None:
+        N.check("cx_bell_spmm_fwd", N.engine().cx_bell_spmm_fwd(
+            C.byref(d), rhs.data_ptr(), _DTYPE_CODE[rhs.dtype], rhs.stride(0), n, out.data_ptr(),
+            out.stride(0), _stream(stream)))
+    else:
+        e = epilogue.descriptor(out)
+        N.check("cx_bell_spmm_fwd_epilogue", N.engine().cx_bell_spmm_fwd_epilogue(
+            C.byref(d), rhs.data_ptr(), _DTYPE_CODE[rhs.dtype], rhs.stride(0), n, out.data_ptr(),
+            out.stride(0), C.byref(e), _stream(stream)))
     return out
 
 
@@ -172,14 +210,21 @@ def bell_pack_rhs(rhs: torch.Tensor, stream=None) -> torch.Tensor:
 
 
 def bell_spmm_packed(m: BellMatrix, packed_rhs: torch.Tensor, n: int,
-                     out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+                     out: Optional[torch.Tensor] = None, stream=None,
+                     epilogue: Optional[Epilogue] = None) -> torch.Tensor:
     """MFMA Blocked-ELL SpMM against a packed bf16 panel (bell_pack_rhs)."""
     _require_cuda(m.block_col_idx, packed_rhs)
     if out is None:
         out = torch.empty((m.rows, n), dtype=torch.float32, device=packed_rhs.device)
     d = m.descriptor()
-    N.check("cx_bell_spmm_fwd_packed", N.engine().cx_bell_spmm_fwd_packed(
-        C.byref(d), packed_rhs.data_ptr(), n, out.data_ptr(), out.stride(0), _stream(stream)))
+    if epilogue is None:
+        N.check("cx_bell_spmm_fwd_packed", N.engine().cx_bell_spmm_fwd_packed(
+            C.byref(d), packed_rhs.data_ptr(), n, out.data_ptr(), out.stride(0), _stream(stream)))
+    else:
+        e = epilogue.descriptor(out)
+        N.check("cx_bell_spmm_fwd_packed_epilogue", N.engine().cx_bell_spmm_fwd_packed_epilogue(
+            C.byref(d), packed_rhs.data_ptr(), n, out.data_ptr(), out.stride(0), C.byref(e),
+            _stream(stream)))
     return out
 
 
@@ -223,15 +268,22 @@ def bell_plan_groups(m: BellMatrix, max_group: int = 4) -> BellGroups:
 
 
 def bell_spmm_grouped(m: BellMatrix, packed_rhs: torch.Tensor, groups: BellGroups, n: int,
-                      out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+                      out: Optional[torch.Tensor] = None, stream=None,
+                      epilogue: Optional[Epilogue] = None) -> torch.Tensor:
     """MFMA Blocked-ELL with a planned row-block grouping; same contract as bell_spmm_packed."""
     _require_cuda(m.block_col_idx, packed_rhs)
     if out is None:
         out = torch.empty((m.rows, n), dtype=torch.float32, device=packed_rhs.device)
     d, g = m.descriptor(), groups.descriptor()
-    N.check("cx_bell_spmm_fwd_grouped", N.engine().cx_bell_spmm_fwd_grouped(
-        C.byref(d), packed_rhs.data_ptr(), C.byref(g), n, out.data_ptr(), out.stride(0),
-        _stream(stream)))
+    if epilogue is None:
+        N.check("cx_bell_spmm_fwd_grouped", N.engine().cx_bell_spmm_fwd_grouped(
+            C.byref(d), packed_rhs.data_ptr(), C.byref(g), n, out.data_ptr(), out.stride(0),
+            _stream(stream)))
+    else:
+        e = epilogue.descriptor(out)
+        N.check("cx_bell_spmm_fwd_grouped_epilogue", N.engine().cx_bell_spmm_fwd_grouped_epilogue(
+            C.byref(d), packed_rhs.data_ptr(), C.byref(g), n, out.data_ptr(), out.stride(0),
+            C.byref(e), _stream(stream)))
     return out
 
 

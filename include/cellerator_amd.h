@@ -82,9 +82,44 @@ typedef enum cellerator_dtype {
  * generation by cx_qcsr_pack_gene_affine. */
 #define CX_DECODE_PER_GENE_AFFINE_PAIRS 3u
 
+/* Fused SpMM epilogue kinds: the values of the reference's epilogue_kind
+ * (include/Cellerator/compute/math/operation.hh:49-58). */
+#define CX_EPILOGUE_NONE 0u
+#define CX_EPILOGUE_BIAS 1u
+#define CX_EPILOGUE_RELU 2u
+#define CX_EPILOGUE_GELU_ERF 3u
+#define CX_EPILOGUE_GELU_TANH 4u
+#define CX_EPILOGUE_BIAS_RELU 5u
+#define CX_EPILOGUE_BIAS_GELU_ERF 6u
+#define CX_EPILOGUE_BIAS_GELU_TANH 7u
+
 /* ------------------------------------------------------------------------------- */
 /* 1. Thin launch layer                                                            */
 /* ------------------------------------------------------------------------------- */
+
+/* Fused epilogue of an SpMM: every output element is
+ *     Y[r,c] = act(alpha * (A . W)[r,c] + beta * C[r,c] + bias[c])
+ * applied to the fp32 accumulator before its single store. This is the alpha / beta /
+ * epilogue part of spmm_request (include/Cellerator/compute/math/operation.hh:136-164)
+ * as the CPU referee applies it (src/compute/math/referee.cc:75-97,170-250): beta * C,
+ * plus alpha * the product, then the bias (bias kinds only), then the activation --
+ * ReLU max(v, 0); exact GELU 0.5 v (1 + erf(v / sqrt 2)); tanh GELU
+ * 0.5 v (1 + tanh(0.7978845608 (v + 0.044715 v^3))). Computed in fp32 (the referee
+ * uses double). alpha == 0 skips the product: the contract's epilogue-only case
+ * (src/compute/math/operation.cc:282-292). A NULL epilogue, or kind NONE with alpha 1
+ * and beta 0, is the plain product (bit-identical to the entry without an epilogue). */
+typedef struct cx_spmm_epilogue {
+    uint32_t kind;          /* CX_EPILOGUE_* */
+    uint32_t reserved;      /* must be 0 */
+    float alpha;
+    float beta;
+    const float *bias;      /* out_cols f32 values for the bias kinds; NULL otherwise */
+    const float *initial;   /* C: rows x out_cols f32, row-major, leading dimension
+                               initial_ld; read only when beta != 0. May be the output
+                               itself with initial_ld == out_ld (in-place update); must
+                               not otherwise overlap the output. */
+    int64_t initial_ld;
+} cx_spmm_epilogue;
 
 /* Quantized (or plain) CSR cells x genes matrix. Field meaning follows
  * cellerator::quantized::csr_matrix (include/Cellerator/quantized/layout.cuh:24-37):
@@ -117,6 +152,13 @@ typedef struct cx_qcsr_matrix {
 int cx_qcsr_spmm_fwd(const cx_qcsr_matrix *a, const void *rhs, uint32_t rhs_dtype,
                      int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
                      void *stream);
+
+/* cx_qcsr_spmm_fwd with a fused epilogue (cx_spmm_epilogue; NULL = none): the
+ * spmm_request alpha / beta / epilogue (operation.hh:136-164) on the quantized CSR path.
+ * Same kernels and summation order; the epilogue runs on each output element once. */
+int cx_qcsr_spmm_fwd_epilogue(const cx_qcsr_matrix *a, const void *rhs, uint32_t rhs_dtype,
+                              int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
+                              const cx_spmm_epilogue *epilogue, void *stream);
 
 /* Interleaves per-gene metadata for CX_DECODE_PER_GENE_AFFINE_PAIRS:
  * pairs[2c] = scales[c] (1 if scales is NULL), pairs[2c+1] = offsets[c] (0 if NULL),
@@ -158,6 +200,12 @@ int cx_bell_spmm_fwd(const cx_bell_matrix *a, const void *rhs, uint32_t rhs_dtyp
                      int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
                      void *stream);
 
+/* cx_bell_spmm_fwd with a fused epilogue (cx_spmm_epilogue; NULL = none), the
+ * spmm_request alpha / beta / epilogue (operation.hh:136-164). */
+int cx_bell_spmm_fwd_epilogue(const cx_bell_matrix *a, const void *rhs, uint32_t rhs_dtype,
+                              int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
+                              const cx_spmm_epilogue *epilogue, void *stream);
+
 /* Packs a row-major bf16 RHS [k x n] into the matrix-core operand panel
  * [ceil(k/32)][n][32] (genes of one 32-gene block column contiguous per output column,
  * zero-padded past k): the Blocked-ELL counterpart of pack_dense_operand_cuda
@@ -171,6 +219,11 @@ int cx_bell_pack_rhs(const uint16_t *rhs_bf16, int64_t rhs_ld, uint32_t k, uint3
  * contract as cx_bell_spmm_fwd within fp32 reordered-sum tolerance. */
 int cx_bell_spmm_fwd_packed(const cx_bell_matrix *a, const uint16_t *packed_rhs,
                             int64_t out_cols, float *out, int64_t out_ld, void *stream);
+
+/* cx_bell_spmm_fwd_packed with a fused epilogue (cx_spmm_epilogue; NULL = none). */
+int cx_bell_spmm_fwd_packed_epilogue(const cx_bell_matrix *a, const uint16_t *packed_rhs,
+                                     int64_t out_cols, float *out, int64_t out_ld,
+                                     const cx_spmm_epilogue *epilogue, void *stream);
 
 /* Row-block groups for the grouped MFMA path (engine addition, no counterpart in the
  * reference; a persistent preprocessing of the Blocked-ELL projection, like the packed
@@ -203,6 +256,12 @@ const char *cx_bell_plan_last_error(void);
 int cx_bell_spmm_fwd_grouped(const cx_bell_matrix *a, const uint16_t *packed_rhs,
                              const cx_bell_groups *groups, int64_t out_cols, float *out,
                              int64_t out_ld, void *stream);
+
+/* cx_bell_spmm_fwd_grouped with a fused epilogue (cx_spmm_epilogue; NULL = none). */
+int cx_bell_spmm_fwd_grouped_epilogue(const cx_bell_matrix *a, const uint16_t *packed_rhs,
+                                      const cx_bell_groups *groups, int64_t out_cols,
+                                      float *out, int64_t out_ld,
+                                      const cx_spmm_epilogue *epilogue, void *stream);
 
 /* CP-BP warp-tile projection (components/CellPack/include/CellPack/warp_tiles.hh:41-79)
  * plus the plan subset of feature_weighted_row_reduction_plan_view

@@ -38,6 +38,12 @@ typedef struct h_case {
     uint64_t workspace_bytes;
     void *stream;
     int32_t device, reserved2;
+    // fused epilogue (multiply only): operation = spmm_operation(epilogue_kind, affine) when
+    // fused != 0; bias (f32 [out_cols]) binds inputs[2] for the bias kinds; alpha / beta are
+    // the affine effect's scalar bindings.
+    uint32_t fused, epilogue_kind, affine, reserved3;
+    const void *bias;
+    float alpha, beta;
 } h_case;
 
 typedef struct h_result {
@@ -60,7 +66,8 @@ enum mutation : int32_t {
     bad_numeric = 6, wrong_projection_kind = 7, undeclared_projection = 8, swapped_axes = 9,
     output_aliases_input = 10, wrong_view_bytes = 11, values_in_view = 12, wrong_device = 15,
     wrong_dense_type = 16, wrong_output_shape = 17, tight_memory_policy = 18,
-    retired_projection = 19
+    retired_projection = 19, missing_scalars = 20, bias_numeric_mismatch = 21,
+    f64_scalars = 22
 };
 
 ex::axis_identity axis(uint32_t base) {
@@ -128,6 +135,10 @@ extern "C" int h_run(const h_case *c, h_result *r) {
     problem.kind = candidate->operation;
     problem.operation = {0x71u, 0x72u};
     problem.input_count = 2u;
+    if (c->fused != 0u) {
+        problem.operation = cp::spmm_operation(c->epilogue_kind, c->affine != 0u);
+        if (c->bias != nullptr) problem.input_count = 3u;
+    }
     problem.output_count = 1u;
     problem.logical_work_items = c->rows;
     core::structure_set_key keys{};
@@ -145,7 +156,9 @@ extern "C" int h_run(const h_case *c, h_result *r) {
     numeric.multiply = ex::numeric_type::f32;
     numeric.accumulation = c->mutation == bad_numeric ? ex::numeric_type::f16 : ex::numeric_type::f32;
     numeric.scalar = ex::numeric_type::f32;
-    numeric.bias = ex::numeric_type::invalid;
+    numeric.bias = c->bias != nullptr ? ex::numeric_type::f32 : ex::numeric_type::invalid;
+    if (c->mutation == bias_numeric_mismatch)
+        numeric.bias = c->bias != nullptr ? ex::numeric_type::invalid : ex::numeric_type::f32;
     numeric.quantization = quantized ? core::quantization_granularity::module
                                      : core::quantization_granularity::none;
     core::prepare_policy policy{};
@@ -192,7 +205,7 @@ extern "C" int h_run(const h_case *c, h_result *r) {
     const ex::value_binding values[1] = {
         {&plane, {c->mutation == stale_generation ? 4u : 3u}}};
 
-    ex::biological_operand_view inputs[2]{};
+    ex::biological_operand_view inputs[3]{};
     inputs[0].kind = ex::operand_kind::sparse_relation;
     ex::sparse_relation_view &rel = inputs[0].storage.relation;
     rel.source_axis = cells;
@@ -226,6 +239,14 @@ extern "C" int h_run(const h_case *c, h_result *r) {
         y.rank = 2u; y.axes[0] = cells; y.axes[1] = outs;
         y.shape[0] = c->rows; y.shape[1] = c->out_cols; y.stride[0] = c->y_ld; y.stride[1] = 1;
     }
+    if (c->bias != nullptr) {
+        inputs[2].kind = ex::operand_kind::dense_tensor;
+        ex::dense_tensor_view &b = inputs[2].storage.dense;
+        b.data = const_cast<void *>(c->bias);
+        b.location = device_at(c->device);
+        b.value_type = ex::numeric_type::f32;
+        b.rank = 1u; b.axes[0] = outs; b.shape[0] = c->out_cols; b.stride[0] = 1;
+    }
     if (c->mutation == swapped_axes) { w.axes[0] = outs; if (w.rank == 2u) w.axes[1] = genes; }
     if (c->mutation == wrong_output_shape) y.shape[0] += 1u;
 
@@ -233,7 +254,23 @@ extern "C" int h_run(const h_case *c, h_result *r) {
     launch.structures = structures;
     launch.structure_count = c->mutation == structure_count ? 2u : 1u;
     launch.inputs = inputs;
-    launch.input_count = 2u;
+    launch.input_count = c->bias != nullptr ? 3u : 2u;
+    if (c->affine != 0u && c->mutation != missing_scalars) {
+        const bool wide = c->mutation == f64_scalars;
+        const float scalars[2] = {c->alpha, c->beta};
+        for (uint32_t i = 0; i < 2u; ++i) {
+            ex::scalar_binding &b = launch.scalars.values[i];
+            b.binding_id = i == 0u ? cp::alpha_binding : cp::beta_binding;
+            b.type = wide ? ex::numeric_type::f64 : ex::numeric_type::f32;
+            if (wide) {
+                const double v = scalars[i];
+                std::memcpy(&b.bits, &v, sizeof(v));
+            } else {
+                std::memcpy(&b.bits, &scalars[i], sizeof(float));
+            }
+        }
+        launch.scalars.count = 2u;
+    }
     launch.outputs = outputs;
     launch.output_count = 1u;
     launch.values = values;

@@ -30,7 +30,9 @@ MUTATIONS = dict(none=0, stale_epoch=1, structure_count=2, short_workspace=4,
                  undeclared_projection=8, swapped_axes=9, output_aliases_input=10,
                  wrong_view_bytes=11, values_in_view=12, wrong_device=15,
                  wrong_dense_type=16, wrong_output_shape=17, tight_memory_policy=18,
-                 retired_projection=19)
+                 retired_projection=19, missing_scalars=20, bias_numeric_mismatch=21,
+                 f64_scalars=22)
+B_MISSING_SCALAR = 15
 
 p = C.c_void_p
 
@@ -44,7 +46,10 @@ class HCase(C.Structure):
                 ("value_count", C.c_uint64), ("value_bytes", C.c_uint64), ("scales", p),
                 ("offsets", p), ("w", p), ("w_ld", C.c_int64), ("y", p), ("y_ld", C.c_int64),
                 ("w2", p), ("y2", p), ("workspace", p), ("workspace_bytes", C.c_uint64),
-                ("stream", p), ("device", C.c_int32), ("reserved2", C.c_int32)]
+                ("stream", p), ("device", C.c_int32), ("reserved2", C.c_int32),
+                ("fused", C.c_uint32), ("epilogue_kind", C.c_uint32), ("affine", C.c_uint32),
+                ("reserved3", C.c_uint32), ("bias", p), ("alpha", C.c_float),
+                ("beta", C.c_float)]
 
 
 class HResult(C.Structure):

@@ -132,3 +132,51 @@ def test_bad_code_width_is_not_declared():
     c.mutation = 0
     assert H.lib().h_run(C.byref(c), C.byref(res)) == 1
     assert res.prepare_status == H.UNSUPPORTED_PROJECTION
+
+
+# ---------------------------------------------------------------- fused epilogues
+
+def _fused(case, kind, affine=False, bias=True):
+    case.fused, case.epilogue_kind, case.affine = 1, kind, int(affine)
+    case.alpha, case.beta = 0.5, 2.0
+    if kind in (1, 5, 6, 7) and bias:
+        case.bias = FAKE + 0x8000
+    return case
+
+
+@pytest.mark.parametrize("kind", ["qcsr", "bell"])
+@pytest.mark.parametrize("epilogue", range(8))
+@pytest.mark.parametrize("affine", [False, True])
+def test_epilogue_prepares_on_multiplies(kind, epilogue, affine):
+    r = H.run(_fused(CASES[kind](), epilogue, affine), "retired_projection")
+    assert r.prepare_status == H.OK, r.message
+
+
+def test_epilogue_on_the_reduction_is_unsupported():
+    r = H.run(_fused(cpbp_case(), 2))
+    assert r.prepare_status == H.UNSUPPORTED_PROBLEM
+
+
+def test_unknown_epilogue_kind_is_unsupported():
+    r = H.run(_fused(qcsr_case(), 9))
+    assert r.prepare_status == H.UNSUPPORTED_PROBLEM
+
+
+@pytest.mark.parametrize("kind", [1, 2])
+def test_bias_numeric_must_match_the_epilogue(kind):
+    """numeric_policy.bias = f32 exactly when the epilogue adds a bias."""
+    r = H.run(_fused(qcsr_case(), kind), "bias_numeric_mismatch")
+    assert r.prepare_status == H.UNSUPPORTED_NUMERIC
+
+
+def test_bias_kind_without_a_bias_operand_is_unsupported():
+    # input_count 2 with a bias epilogue (numeric bias left invalid as well)
+    r = H.run(_fused(qcsr_case(), 5, bias=False))
+    assert r.prepare_status == H.UNSUPPORTED_NUMERIC
+
+
+def test_affine_effect_needs_both_scalars():
+    """The core itself rejects an affine_accumulate launch without alpha / beta bindings."""
+    r = H.run(_fused(bell_case(), 0, affine=True), "missing_scalars")
+    assert r.prepare_status == H.OK
+    assert (r.status, r.binding) == (H.INVALID_LAUNCH, H.B_MISSING_SCALAR)

@@ -231,3 +231,66 @@ def test_graph_capture_replays_match_eager(oracle):
         eager = qcsr_spmm(m, w)
         torch.cuda.synchronize()
         assert torch.equal(y, eager), f"replay {step} differs"
+
+
+@pytest.mark.parametrize("kind,affine", [(7, False), (6, True), (2, True), (0, True)])
+def test_quantized_csr_epilogue_through_reference_core(oracle, kind, affine):
+    """problem.operation = spmm_operation(kind, affine): bias through inputs[2], alpha / beta
+    through scalar bindings with Y updated in place; bitwise equal to the C-ABI call with the
+    same epilogue, and within tolerance of the referee."""
+    import torch
+
+    from cellerator_amd import Epilogue, qcsr_spmm
+    rng = np.random.default_rng(80 + kind)
+    fx = quantized_fixture(oracle, rng, 400, 900, 50.0, 4, oracle.PER_GENE_AFFINE)
+    m = to_device_qcsr(fx)
+    w_host = (rng.standard_normal((fx["cols"], 64)) * 0.05).astype(np.float16)
+    w = torch.from_numpy(w_host).cuda()
+    c0 = rng.standard_normal((fx["rows"], 64)).astype(np.float32)
+    bias = (rng.standard_normal(64) * 0.5).astype(np.float32) if kind in (1, 5, 6, 7) else None
+    bias_dev = None if bias is None else torch.from_numpy(bias).cuda()
+    alpha, beta = (0.5, -1.5) if affine else (1.0, 0.0)
+    y = torch.from_numpy(c0.copy()).cuda()
+    c = qcsr_case(m, w, y)
+    c.fused, c.epilogue_kind, c.affine = 1, kind, int(affine)
+    c.alpha, c.beta = alpha, beta
+    c.bias = _ptr(bias_dev)
+    r = H.run(c, "f64_scalars" if kind == 2 else "none")
+    assert (r.prepare_status, r.status) == (H.OK, H.OK), (r.message, r.engine)
+    torch.cuda.synchronize()
+    direct = torch.from_numpy(c0.copy()).cuda()
+    qcsr_spmm(m, w, out=direct, epilogue=Epilogue(kind, alpha, beta, bias_dev,
+                                                  direct if affine else None))
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), direct.view(torch.int32))
+    decoded = oracle.decode_csr(4, fx["policy"], fx["row_ptr"], fx["packed_row_ptr"],
+                                fx["col_idx"], fx["packed"], fx["scales"], fx["offsets"], None)
+    ref = oracle.spmm_referee(fx["rows"], fx["cols"], 64, fx["row_ptr"], fx["col_idx"], decoded,
+                              w_host, alpha=alpha, beta=beta, c0=c0 if beta else None,
+                              epilogue=kind, bias=bias)
+    cmp = oracle.compare(ref, y.cpu().numpy(), 1e-4, 1e-4)
+    assert cmp["status"] == 0 and cmp["within_tolerance"], cmp
+
+
+def test_blocked_ell_epilogue_through_reference_core():
+    import torch
+
+    from cellerator_amd import Epilogue, bell_pack_rhs, bell_spmm_packed
+    m, rng = _bell(seed=9)
+    n = 128
+    w = (torch.randn(m.cols, n, device="cuda") * 0.02).bfloat16()
+    bias = torch.randn(n, device="cuda")
+    c0 = torch.randn(m.rows, n, device="cuda")
+    y = c0.clone()
+    ws = torch.empty(((m.cols + 31) // 32) * 32 * n * 2, dtype=torch.uint8, device="cuda")
+    c = bell_case(m, w, y, ws)
+    c.fused, c.epilogue_kind, c.affine, c.alpha, c.beta = 1, 6, 1, 2.0, 0.25
+    c.bias = bias.data_ptr()
+    r = H.run(c)
+    assert (r.prepare_status, r.status) == (H.OK, H.OK), (r.message, r.engine)
+    torch.cuda.synchronize()
+    direct = c0.clone()
+    bell_spmm_packed(m, bell_pack_rhs(w), n, out=direct,
+                     epilogue=Epilogue(6, 2.0, 0.25, bias, direct))
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), direct.view(torch.int32))
