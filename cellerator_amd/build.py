@@ -32,6 +32,8 @@ ARCH = "gfx950"
 ENGINE_SOURCES = [
     "cx_runtime.hip",
     "qcsr_spmm.hip",
+    "qcsr_backward.hip",
+    "sort.hip",
     "bell_spmm.hip",
     "cpbp_reduce.hip",
     "csr_spmv.hip",

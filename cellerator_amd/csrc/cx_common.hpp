@@ -39,6 +39,15 @@ __device__ __forceinline__ float bf2f(std::uint16_t bits) {
     return __uint_as_float(static_cast<std::uint32_t>(bits) << 16);
 }
 
+// Device primitives of sort.hip (stream-ordered; workspace sized by the *_bytes helpers).
+std::uint64_t scan_workspace_bytes(std::uint64_t n);
+int exclusive_scan_u32(const std::uint32_t *in, std::uint32_t *out, std::uint64_t n,
+                       void *workspace, hipStream_t stream);
+std::uint64_t sort_pairs_workspace_bytes(std::uint64_t count, std::uint32_t key_bits);
+int sort_pairs(const std::uint32_t *keys_in, const std::uint32_t *vals_in, std::uint32_t *keys_out,
+               std::uint32_t *vals_out, std::uint64_t count, std::uint32_t key_bits,
+               void *workspace, std::uint64_t workspace_bytes, hipStream_t stream);
+
 // Device form of cx_spmm_epilogue. `active` == 0 means a plain store of the accumulator.
 struct Epilogue {
     const float *bias;

@@ -20,63 +20,10 @@
 //     and group 0 writes the row's N outputs (one 16/32 B store per lane).
 // Any other shape (N not 32/64/128, unaligned operands) takes the generic kernel: one
 // wave per row, lanes over output columns, entries in nnz order.
-#include "cx_common.hpp"
+#include "qcsr_common.hpp"
 
 namespace cx {
 namespace {
-
-enum class ValueMode : int { quantized = 0, f16 = 1, f32 = 2 };
-
-struct QcsrArgs {
-    const std::int32_t *row_ptr;
-    const std::int32_t *packed_row_ptr;
-    const std::int32_t *col_idx;
-    const std::uint8_t *packed;
-    const float *scales;
-    const float *offsets;
-    const float *row_offsets;
-    const void *values;
-    const void *rhs;
-    std::int64_t rhs_ld;
-    float *out;
-    std::int64_t out_ld;
-    std::uint32_t rows;
-    std::uint32_t cols;
-    Epilogue ep;
-};
-
-constexpr int kWavesPerBlock = 4;
-
-// Decoded value of entry `i` (global nnz index) of row `row` whose packed codes start
-// at `pbase`. Returns the gene through `col`.
-template<int kBits, int kPolicy, ValueMode kMode>
-__device__ __forceinline__ float load_entry(const QcsrArgs &a, std::int64_t i,
-                                            std::int64_t begin, const std::uint8_t *pbase,
-                                            float row_offset, int &col) {
-    col = a.col_idx[i];
-    if constexpr (kMode == ValueMode::quantized) {
-        constexpr int kCpb = 8 / kBits;
-        constexpr unsigned kMask = (1u << kBits) - 1u;
-        const std::int64_t local = i - begin;
-        const unsigned byte = pbase[local / kCpb];
-        const unsigned code = (byte >> (static_cast<unsigned>(local % kCpb) * kBits)) & kMask;
-        if constexpr (kPolicy == CX_DECODE_PER_GENE_AFFINE_PAIRS) {
-            // interleaved (scale, offset): one 8-byte gather
-            const float2 so = reinterpret_cast<const float2 *>(a.scales)[col];
-            return __builtin_fmaf(static_cast<float>(code), so.x, so.y);
-        } else {
-            const float scale = a.scales != nullptr ? a.scales[col] : 1.0f;
-            const float offset = kPolicy == CX_DECODE_PER_GENE_AFFINE
-                ? (a.offsets != nullptr ? a.offsets[col] : 0.0f)
-                : row_offset;
-            return __builtin_fmaf(static_cast<float>(code), scale, offset);
-        }
-    } else if constexpr (kMode == ValueMode::f16) {
-        return h2f(static_cast<const std::uint16_t *>(a.values)[i]);
-    } else {
-        return static_cast<const float *>(a.values)[i];
-    }
-}
 
 template<typename RhsT, int kCpl>
 __device__ __forceinline__ void fma_row(float (&acc)[kCpl], float x, const RhsT *w) {
@@ -99,11 +46,6 @@ __device__ __forceinline__ void fma_row(float (&acc)[kCpl], float x, const RhsT 
         acc[2] = __builtin_fmaf(x, v.z, acc[2]);
         acc[3] = __builtin_fmaf(x, v.w, acc[3]);
     }
-}
-
-__device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
 }
 
 template<int kBits, int kPolicy, ValueMode kMode, typename RhsT, int kN>

@@ -147,6 +147,96 @@ def qcsr_pack_gene_affine(m: QcsrMatrix, stream=None) -> QcsrMatrix:
                       decode_policy=N.DECODE_PER_GENE_AFFINE_PAIRS, meta=dict(m.meta))
 
 
+def qcsr_transpose(m: QcsrMatrix, stream=None) -> QcsrMatrix:
+    """A^T (genes x cells) as a plain f32 CSR, values decoded exactly as the forward decodes
+    them; feeds qcsr_spmm (A^T . B) and qcsr_spmm_bwd_rhs. Built once per structure and
+    value generation (device radix sort, deterministic)."""
+    _require_cuda(m.row_ptr)
+    d = m.descriptor()
+    lib = N.engine()
+    ws_bytes = C.c_uint64()
+    N.check("cx_qcsr_transpose_workspace", lib.cx_qcsr_transpose_workspace(C.byref(d), C.byref(ws_bytes)))
+    dev = m.row_ptr.device
+    nnz = m.nnz
+    ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=dev)
+    t_row_ptr = torch.empty(m.cols + 1, dtype=torch.int32, device=dev)
+    t_col_idx = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)
+    t_values = torch.empty(max(nnz, 1), dtype=torch.float32, device=dev)
+    N.check("cx_qcsr_transpose", lib.cx_qcsr_transpose(
+        C.byref(d), t_row_ptr.data_ptr(), t_col_idx.data_ptr(), t_values.data_ptr(),
+        ws.data_ptr(), ws_bytes.value, _stream(stream)))
+    # The workspace may be released once the build is ordered before later work: on the
+    # current stream torch's allocator guarantees that; on another stream keep it alive.
+    meta = {} if stream is None else {"transpose_workspace": ws}
+    return QcsrMatrix(m.cols, m.rows, 0, t_row_ptr, t_col_idx[:nnz], values=t_values[:nnz],
+                      meta=meta)
+
+
+def qcsr_spmm_bwd_values(m: QcsrMatrix, grad_out: torch.Tensor, rhs: torch.Tensor,
+                         out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """grad_values[i] = <grad_out[row_i, :], rhs[col_i, :]> for every stored entry (f32)."""
+    _require_cuda(m.row_ptr, grad_out, rhs)
+    if grad_out.dtype != torch.float32 or grad_out.stride(1) != 1 or rhs.stride(1) != 1:
+        raise ValueError("grad_out must be row-major f32 and rhs row-major")
+    n = rhs.shape[1]
+    if grad_out.shape != (m.rows, n) or rhs.shape[0] != m.cols:
+        raise ValueError("grad_out must be [rows, N] and rhs [cols, N]")
+    if out is None:
+        out = torch.empty(max(m.nnz, 1), dtype=torch.float32, device=rhs.device)[: m.nnz]
+    d = m.descriptor()
+    N.check("cx_qcsr_spmm_bwd_values", N.engine().cx_qcsr_spmm_bwd_values(
+        C.byref(d), grad_out.data_ptr(), grad_out.stride(0), rhs.data_ptr(), _DTYPE_CODE[rhs.dtype],
+        rhs.stride(0), n, out.data_ptr(), _stream(stream)))
+    return out
+
+
+def qcsr_spmm_bwd_rhs(transposed: QcsrMatrix, grad_out: torch.Tensor,
+                      out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """grad_rhs = A^T . grad_out with `transposed` from qcsr_transpose(A) (f32 [cols, N])."""
+    _require_cuda(transposed.row_ptr, grad_out)
+    if grad_out.dtype != torch.float32 or grad_out.stride(1) != 1 or grad_out.shape[0] != transposed.cols:
+        raise ValueError("grad_out must be row-major f32 [rows of A, N]")
+    n = grad_out.shape[1]
+    if out is None:
+        out = torch.empty((transposed.rows, n), dtype=torch.float32, device=grad_out.device)
+    d = transposed.descriptor()
+    N.check("cx_qcsr_spmm_bwd_rhs", N.engine().cx_qcsr_spmm_bwd_rhs(
+        C.byref(d), grad_out.data_ptr(), grad_out.stride(0), n, out.data_ptr(), out.stride(0),
+        _stream(stream)))
+    return out
+
+
+def sort_pairs(keys: torch.Tensor, values: Optional[torch.Tensor] = None, key_bits: int = 32,
+               stream=None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Stable device radix sort of int32-stored u32 keys (low key_bits bits) with u32 values
+    (None: the identity permutation). Returns (sorted keys, permuted values)."""
+    _require_cuda(keys)
+    count = keys.numel()
+    lib = N.engine()
+    ws_bytes = C.c_uint64()
+    N.check("cx_sort_pairs_workspace", lib.cx_sort_pairs_workspace(count, key_bits, C.byref(ws_bytes)))
+    ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=keys.device)
+    ko = torch.empty(max(count, 1), dtype=torch.int32, device=keys.device)
+    vo = torch.empty(max(count, 1), dtype=torch.int32, device=keys.device)
+    N.check("cx_sort_pairs", lib.cx_sort_pairs(
+        keys.data_ptr(), _ptr(values), ko.data_ptr(), vo.data_ptr(), count, key_bits, ws.data_ptr(),
+        ws_bytes.value, _stream(stream)))
+    return ko[:count], vo[:count]
+
+
+def exclusive_scan_u32(x: torch.Tensor, stream=None) -> torch.Tensor:
+    """Exclusive prefix sum of int32-stored u32 values (modulo 2^32)."""
+    _require_cuda(x)
+    lib = N.engine()
+    ws_bytes = C.c_uint64()
+    N.check("cx_exclusive_scan_u32_workspace", lib.cx_exclusive_scan_u32_workspace(x.numel(), C.byref(ws_bytes)))
+    ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=x.device)
+    out = torch.empty_like(x)
+    N.check("cx_exclusive_scan_u32", lib.cx_exclusive_scan_u32(
+        x.data_ptr(), out.data_ptr(), x.numel(), ws.data_ptr(), ws_bytes.value, _stream(stream)))
+    return out
+
+
 @dataclass
 class BellMatrix:
     rows: int

@@ -167,6 +167,55 @@ int cx_qcsr_spmm_fwd_epilogue(const cx_qcsr_matrix *a, const void *rhs, uint32_t
 int cx_qcsr_pack_gene_affine(const float *scales, const float *offsets, uint32_t cols,
                              float *pairs, void *stream);
 
+/* ---- transpose and backward of the CSR SpMM ------------------------------------ */
+
+/* Device bytes of workspace cx_qcsr_transpose needs for `a`. */
+int cx_qcsr_transpose_workspace(const cx_qcsr_matrix *a, uint64_t *bytes);
+
+/* Builds A^T (cols x rows) as a plain f32 CSR on the device: t_row_ptr[cols + 1],
+ * t_col_idx[nnz] (cell rows, ascending within each gene row), t_values[nnz] (each entry
+ * decoded exactly as the forward decodes it). Viewed as a cx_qcsr_matrix {rows = a.cols,
+ * cols = a.rows, bits = 0, value_dtype = F32}, it computes A^T . B with cx_qcsr_spmm_fwd --
+ * the referee's transpose_sparse product (src/compute/math/referee.cc:170-232) -- and the
+ * backward grad_W (cx_qcsr_spmm_bwd_rhs). Deterministic: a stable device radix sort of the
+ * column indices (no atomics). Built once per structure and value generation; no
+ * counterpart in the reference, whose backward scatters with atomics instead. */
+int cx_qcsr_transpose(const cx_qcsr_matrix *a, int32_t *t_row_ptr, int32_t *t_col_idx,
+                      float *t_values, void *workspace, uint64_t workspace_bytes, void *stream);
+
+/* grad_values[i] = sum_{c < out_cols} grad_out[row_i, c] * rhs[col_i, c] for every stored
+ * entry i: the gradient of Y = A . RHS with respect to A's (decoded) values. Replaces
+ * csr_spmm_bwd_values_f16_f32 (src/compute/sparse/ops/ops.hh:111-120,
+ * kernels/base_sparse/csr_spmm_bwd_values_kernel_.cuh), whose kernel reads grad_out with the
+ * rhs leading dimension; here each operand has its own. Reads only A's structure. fp32
+ * products and sums in a fixed order; rhs F16 or F32, grad_out F32. */
+int cx_qcsr_spmm_bwd_values(const cx_qcsr_matrix *a, const float *grad_out,
+                            int64_t grad_out_ld, const void *rhs, uint32_t rhs_dtype,
+                            int64_t rhs_ld, int64_t out_cols, float *grad_values, void *stream);
+
+/* grad_rhs[cols x out_cols] = A^T . grad_out, with `transposed` the f32 transpose built by
+ * cx_qcsr_transpose: the forward row-wave SpMM on A^T, every element written once in a fixed
+ * order. Replaces csr_spmm_bwd_rhs_f16_f32 (src/compute/sparse/ops/ops.hh:122-133,
+ * kernels/base_sparse/csr_spmm_bwd_rhs_kernel_.cuh), which zero-fills grad_rhs and adds
+ * with float atomics. */
+int cx_qcsr_spmm_bwd_rhs(const cx_qcsr_matrix *transposed, const float *grad_out,
+                         int64_t grad_out_ld, int64_t out_cols, float *grad_rhs,
+                         int64_t grad_rhs_ld, void *stream);
+
+/* Stable LSD radix sort of (key, value) u32 pairs on the device, on the keys' low key_bits
+ * bits (8 bits per pass); vals_in == NULL sorts the identity permutation (value = input
+ * position). Outputs must not alias inputs. Deterministic. Engine utility behind the
+ * transpose (no counterpart in the reference, which uses CUB). */
+int cx_sort_pairs_workspace(uint64_t count, uint32_t key_bits, uint64_t *bytes);
+int cx_sort_pairs(const uint32_t *keys_in, const uint32_t *vals_in, uint32_t *keys_out,
+                  uint32_t *vals_out, uint64_t count, uint32_t key_bits, void *workspace,
+                  uint64_t workspace_bytes, void *stream);
+
+/* Exclusive prefix sum of u32 values on the device (wraps modulo 2^32). */
+int cx_exclusive_scan_u32_workspace(uint64_t count, uint64_t *bytes);
+int cx_exclusive_scan_u32(const uint32_t *in, uint32_t *out, uint64_t count, void *workspace,
+                          uint64_t workspace_bytes, void *stream);
+
 /* Blocked-ELL matrix (include/Cellerator/quantized/blocked_ell.cuh:18-35 and the
  * cs::sparse::blocked_ell layout consumed by blocked_ell_spmm_fwd_kernel_):
  * block_col_idx is (rows/block_size) x (ell_cols/block_size), 0xffffffff marks an

@@ -518,3 +518,23 @@ int or_cpbp_within_tolerance(float reference, float candidate, double abs_tol,
     if (!isfinite(rv) || !isfinite(cv)) return 0;
     return fabs(cv - rv) <= abs_tol + rel_tol * fabs(rv);
 }
+
+/* csr_spmm_bwd_values_kernel_
+ * (src/compute/sparse/ops/kernels/base_sparse/csr_spmm_bwd_values_kernel_.cuh:1-19) */
+int or_spmm_bwd_values(uint32_t rows, const int32_t *row_ptr, const int32_t *col_idx,
+                       const float *grad_out, uint64_t grad_out_ld, const void *rhs,
+                       int rhs_type, uint64_t rhs_ld, uint64_t n, double *grad_values) {
+    if (rows != 0u && (row_ptr == NULL || grad_out == NULL || rhs == NULL)) return -1;
+    if (grad_out_ld < n || rhs_ld < n) return -2;
+    for (uint32_t r = 0; r < rows; ++r) {
+        const float *g = grad_out + (uint64_t)r * grad_out_ld;
+        for (int32_t i = row_ptr[r]; i < row_ptr[r + 1]; ++i) {
+            const uint64_t base = (uint64_t)col_idx[i] * rhs_ld;
+            double acc = 0.0;
+            for (uint64_t c = 0; c < n; ++c)
+                acc += (double)g[c] * read_typed_f(rhs, rhs_type, base + c);
+            grad_values[i] = acc;
+        }
+    }
+    return 0;
+}

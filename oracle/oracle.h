@@ -31,6 +31,13 @@
  *         36-feature plan fixture shape of
  *         components/CellPack/tests/feature_weighted_row_reduction_cuda_test.cu:69-151;
  *         brute force: dense mat-vec in float64.
+ *   or_spmm_bwd_values
+ *       - reference KAT {5,500,110,1100,17} (tests/sparse_ops_runtime_test.cu:140-161,566-582);
+ *       - adjoint identity: sum_i grad_values[i] * x_i == <grad_out, X . W> (Frobenius),
+ *         with X . W from the pinned referee, on random inputs (a transposed operand or a
+ *         wrong row/column index breaks it).
+ *   grad_rhs = X^T . grad_out is or_spmm_referee with transpose_sparse = 1, pinned by the
+ *       reference KAT {26,32,9,12,14,20} (tests/sparse_ops_runtime_test.cu:584-604).
  *   or_compare
  *       - restates compare_spmm_reference (include/Cellerator/compute/math/referee.hh:143-211);
  *         pinned by planted-error tests in tests/test_oracle.py.
@@ -154,6 +161,14 @@ int or_cpbp_tiles(uint32_t row_count, uint32_t tile_count, uint32_t tile_row_wid
                   const uint32_t *block_row_entry_offsets, const uint32_t *row_block_gene_masks,
                   const uint32_t *row_block_value_offsets, const void *values, int value_type,
                   const uint32_t *row_permutation, const float *weights, float *out);
+/* ---- backward of the CSR SpMM ----
+ * csr_spmm_bwd_values_kernel_ (src/compute/sparse/ops/kernels/base_sparse/
+ * csr_spmm_bwd_values_kernel_.cuh:1-19): grad_values[i] = sum_c grad_out[row_i, c] *
+ * rhs[col_i, c], accumulated in float64 over c in order. Each operand has its own leading
+ * dimension (the reference kernel reads both with rhs_ld). */
+int or_spmm_bwd_values(uint32_t rows, const int32_t *row_ptr, const int32_t *col_idx,
+                       const float *grad_out, uint64_t grad_out_ld, const void *rhs,
+                       int rhs_type, uint64_t rhs_ld, uint64_t n, double *grad_values);
 /* float64 canonical sum, for tolerance checks that do not depend on order. */
 int or_cpbp_canonical_f64(uint32_t rows, const uint32_t *row_offsets,
                           const uint32_t *canonical_features, const void *values,

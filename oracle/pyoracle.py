@@ -96,6 +96,9 @@ def lib() -> C.CDLL:
         _lib.or_cpbp_tiles.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32] + [
             C.c_void_p] * 9 + [C.c_int] + [C.c_void_p] * 3
         _lib.or_cpbp_within_tolerance.argtypes = [C.c_float, C.c_float, C.c_double, C.c_double]
+        _lib.or_spmm_bwd_values.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p,
+                                            C.c_uint64, C.c_void_p, C.c_int, C.c_uint64,
+                                            C.c_uint64, C.c_void_p]
     return _lib
 
 
@@ -266,6 +269,23 @@ def bell_spmm_referee(rows, cols, block_size, ell_cols, block_col_idx, values, r
     if rc != 0:
         raise ValueError(f"bell_spmm_referee failed ({rc})")
     return out.reshape(rows, n), (None if mag is None else mag.reshape(rows, n))
+
+
+# ---------------------------------------------------------------- backward
+def spmm_bwd_values(row_ptr, col_idx, grad_out, rhs) -> np.ndarray:
+    """float64 grad_values of Y = X . rhs (csr_spmm_bwd_values_kernel_); grad_out f32
+    [rows, n], rhs f16/f32 [cols, n], both row-major."""
+    row_ptr, col_idx = _c(row_ptr, np.int32), _c(col_idx, np.int32)
+    grad_out = _c(grad_out, np.float32)
+    rhs = np.ascontiguousarray(rhs)
+    n = grad_out.shape[1]
+    out = np.zeros(len(col_idx), dtype=np.float64)
+    rc = lib().or_spmm_bwd_values(len(row_ptr) - 1, _p(row_ptr), _p(col_idx), _p(grad_out),
+                                  grad_out.shape[1], _p(rhs), _TYPE_OF[rhs.dtype], rhs.shape[1],
+                                  n, _p(out))
+    if rc != 0:
+        raise ValueError(f"spmm_bwd_values failed ({rc})")
+    return out
 
 
 # ---------------------------------------------------------------- CP-BP

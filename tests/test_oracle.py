@@ -273,3 +273,46 @@ def test_bell_referee_brute_force(oracle):
     out, _ = oracle.bell_spmm_referee(rows, cols, bs, width * bs, idx, vals, rhs,
                                       value_type=oracle.F32)
     assert np.allclose(out, dense @ rhs.astype(np.float64), rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------- backward
+
+_BWD_ROW_PTR = np.array([0, 2, 4, 5], np.int32)
+_BWD_COLS = np.array([0, 2, 1, 2, 0], np.int32)
+_BWD_VALUES = np.array([1, 2, 3, 4, 5], np.float16)
+_BWD_RHS = np.array([[1, 2], [10, 20], [100, 200]], np.float32)
+_BWD_GRAD = np.array([[1, 2], [3, 4], [5, 6]], np.float32)
+
+
+def test_bwd_values_reference_kat(oracle):
+    """tests/sparse_ops_runtime_test.cu:566-582: {5, 500, 110, 1100, 17}."""
+    gv = oracle.spmm_bwd_values(_BWD_ROW_PTR, _BWD_COLS, _BWD_GRAD, _BWD_RHS)
+    assert gv.tolist() == [5.0, 500.0, 110.0, 1100.0, 17.0]
+
+
+def test_bwd_rhs_reference_kat(oracle):
+    """tests/sparse_ops_runtime_test.cu:584-604: X^T . grad = {26,32, 9,12, 14,20}."""
+    g = oracle.spmm_referee(3, 3, 2, _BWD_ROW_PTR, _BWD_COLS, _BWD_VALUES, _BWD_GRAD,
+                            transpose_sparse=True)
+    assert g.ravel().tolist() == [26.0, 32.0, 9.0, 12.0, 14.0, 20.0]
+
+
+@pytest.mark.parametrize("rhs_dtype", [np.float32, np.float16])
+def test_bwd_values_adjoint_identity(oracle, rhs_dtype):
+    """sum_i grad_values[i] x_i = <G, X . W>: the gradient is the adjoint of the forward."""
+    from tests.helpers import random_csr
+    rng = np.random.default_rng(31)
+    rows, cols, n = 70, 90, 13
+    row_ptr, col_idx = random_csr(rng, rows, cols, 9.0, empty_every=6)
+    x = rng.standard_normal(len(col_idx)).astype(np.float32)
+    w = rng.standard_normal((cols, n)).astype(rhs_dtype)
+    g = rng.standard_normal((rows, n)).astype(np.float32)
+    gv = oracle.spmm_bwd_values(row_ptr, col_idx, g, w)
+    y = oracle.spmm_referee(rows, cols, n, row_ptr, col_idx, x, w)
+    lhs = float(np.dot(gv, x.astype(np.float64)))
+    rhs = float(np.sum(g.astype(np.float64) * y))
+    assert abs(lhs - rhs) <= 1e-9 * max(1.0, abs(rhs))
+    # and per entry against the dense product G . W^T sampled at the pattern
+    dense = g.astype(np.float64) @ w.astype(np.float64).T
+    rows_of = np.repeat(np.arange(rows), np.diff(row_ptr))
+    assert np.allclose(gv, dense[rows_of, col_idx], rtol=1e-12, atol=1e-12)
