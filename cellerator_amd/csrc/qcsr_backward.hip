@@ -333,7 +333,8 @@ extern "C" int cx_qcsr_spmm_bwd_values(const cx_qcsr_matrix *m, const float *gra
 
 extern "C" int cx_qcsr_spmm_bwd_rhs(const cx_qcsr_matrix *transposed, const float *grad_out,
                                     int64_t grad_out_ld, int64_t out_cols, float *grad_rhs,
-                                    int64_t grad_rhs_ld, void *stream) {
+                                    int64_t grad_rhs_ld, void *workspace,
+                                    uint64_t workspace_bytes, void *stream) {
     using namespace cx;
     clear_error();
     if (transposed == nullptr)
@@ -341,6 +342,8 @@ extern "C" int cx_qcsr_spmm_bwd_rhs(const cx_qcsr_matrix *transposed, const floa
     if (transposed->bits != 0u || transposed->value_dtype != CELLERATOR_DTYPE_F32)
         return fail(CX_STATUS_INVALID_ARGUMENT,
                     "cx_qcsr_spmm_bwd_rhs: expects the f32 transpose built by cx_qcsr_transpose");
-    return cx_qcsr_spmm_fwd(transposed, grad_out, CELLERATOR_DTYPE_F32, grad_out_ld, out_cols,
-                            grad_rhs, grad_rhs_ld, stream);
+    // gene rows of an expression matrix are heavily skewed: the balanced form
+    return cx_qcsr_spmm_fwd_balanced(transposed, grad_out, CELLERATOR_DTYPE_F32, grad_out_ld,
+                                     out_cols, grad_rhs, grad_rhs_ld, nullptr, workspace,
+                                     workspace_bytes, stream);
 }

@@ -48,24 +48,27 @@ __device__ __forceinline__ void fma_row(float (&acc)[kCpl], float x, const RhsT 
     }
 }
 
-template<int kBits, int kPolicy, ValueMode kMode, typename RhsT, int kN>
-__global__ __launch_bounds__(kWave *kWavesPerBlock) void qcsr_spmm_rowwave(QcsrArgs a) {
-    constexpr int kCpl = 16 / static_cast<int>(sizeof(RhsT)); // output columns per lane
-    constexpr int kLpe = kN / kCpl;                           // lanes per entry
-    constexpr int kEps = kWave / kLpe;                        // entries per step
+// Shape constants of the row-wave fast path: kCpl output columns per lane (16 B of W),
+// kLpe lanes per entry, kEps entries per step.
+template<typename RhsT, int kN>
+struct WaveShape {
+    static constexpr int kCpl = 16 / static_cast<int>(sizeof(RhsT));
+    static constexpr int kLpe = kN / kCpl;
+    static constexpr int kEps = kWave / kLpe;
     static_assert(kN % kCpl == 0 && kLpe <= kWave && kWave % kLpe == 0, "bad shape");
+};
 
-    __shared__ int2 stage[kWavesPerBlock][kWave];
-
-    const int wave = static_cast<int>(threadIdx.x) / kWave;
-    const int lane = static_cast<int>(threadIdx.x) % kWave;
-    const std::uint32_t row = blockIdx.x * kWavesPerBlock + wave;
-    if (row >= a.rows) return;
-
+// Accumulates entries [sb, se) of row `row` (whose entries start at nnz offset `begin`)
+// into this lane's kCpl partial output columns; `stage` is the wave's 64 staging slots.
+template<int kBits, int kPolicy, ValueMode kMode, typename RhsT, int kN>
+__device__ __forceinline__ void accumulate_segment(const QcsrArgs &a, int2 *stage, std::uint32_t row,
+                                                   std::int64_t begin, std::int64_t sb,
+                                                   std::int64_t se, int lane,
+                                                   float (&acc)[WaveShape<RhsT, kN>::kCpl]) {
+    using S = WaveShape<RhsT, kN>;
+    constexpr int kCpl = S::kCpl, kLpe = S::kLpe, kEps = S::kEps;
     const int g = lane / kLpe;
     const int j = lane % kLpe;
-    const std::int64_t begin = a.row_ptr[row];
-    const std::int64_t end = a.row_ptr[row + 1];
     const std::uint8_t *pbase = nullptr;
     float row_offset = 0.0f;
     if constexpr (kMode == ValueMode::quantized) {
@@ -74,30 +77,25 @@ __global__ __launch_bounds__(kWave *kWavesPerBlock) void qcsr_spmm_rowwave(QcsrA
             row_offset = a.row_offsets != nullptr ? a.row_offsets[row] : 0.0f;
     }
     const RhsT *rhs = static_cast<const RhsT *>(a.rhs) + j * kCpl;
-
-    float acc[kCpl];
-#pragma unroll
-    for (int k = 0; k < kCpl; ++k) acc[k] = 0.0f;
-
-    for (std::int64_t c0 = begin; c0 < end; c0 += kWave) {
+    for (std::int64_t c0 = sb; c0 < se; c0 += kWave) {
         const std::int64_t i = c0 + lane;
         int col = 0;
         float x = 0.0f;
-        if (i < end) x = load_entry<kBits, kPolicy, kMode>(a, i, begin, pbase, row_offset, col);
-        stage[wave][lane] = make_int2(col, __float_as_int(x));
+        if (i < se) x = load_entry<kBits, kPolicy, kMode>(a, i, begin, pbase, row_offset, col);
+        stage[lane] = make_int2(col, __float_as_int(x));
         wave_sync();
-        const int count = end - c0 < kWave ? static_cast<int>(end - c0) : kWave;
+        const int count = se - c0 < kWave ? static_cast<int>(se - c0) : kWave;
         if (count == kWave) {
 #pragma unroll
             for (int s = 0; s < kWave; s += kEps) {
-                const int2 e = stage[wave][s + g];
+                const int2 e = stage[s + g];
                 fma_row<RhsT, kCpl>(acc, __int_as_float(e.y),
                                     rhs + static_cast<std::int64_t>(e.x) * a.rhs_ld);
             }
         } else {
             for (int s = 0; s < count; s += kEps) {
                 if (s + g < count) {
-                    const int2 e = stage[wave][s + g];
+                    const int2 e = stage[s + g];
                     fma_row<RhsT, kCpl>(acc, __int_as_float(e.y),
                                         rhs + static_cast<std::int64_t>(e.x) * a.rhs_ld);
                 }
@@ -105,23 +103,132 @@ __global__ __launch_bounds__(kWave *kWavesPerBlock) void qcsr_spmm_rowwave(QcsrA
         }
         wave_sync();
     }
+}
 
-    // Sum the kEps group partials: lanes of equal j differ in the bits above log2(kLpe).
+// Sums the kEps group partials: lanes of equal j differ in the bits above log2(kLpe).
+template<int kLpe, int kCpl>
+__device__ __forceinline__ void reduce_groups(float (&acc)[kCpl]) {
     constexpr int kFirstBit = __builtin_ctz(kLpe);
 #pragma unroll
     for (int k = 0; k < kCpl; ++k) {
         if constexpr (kFirstBit < 6) acc[k] = xor_reduce<kFirstBit, 5>(acc[k]);
     }
-    if (g == 0) {
-        float *dst = a.out + static_cast<std::int64_t>(row) * a.out_ld + j * kCpl;
-        if (a.ep.active) {
+}
+
+// Group-0 lane j: columns [j kCpl, j kCpl + kCpl) of row `row`, through the epilogue.
+template<int kCpl>
+__device__ __forceinline__ void store_row(const QcsrArgs &a, std::uint32_t row, int j,
+                                          float (&acc)[kCpl]) {
+    float *dst = a.out + static_cast<std::int64_t>(row) * a.out_ld + j * kCpl;
+    if (a.ep.active) {
 #pragma unroll
-            for (int k = 0; k < kCpl; ++k) acc[k] = epilogue_value(a.ep, acc[k], row, j * kCpl + k);
+        for (int k = 0; k < kCpl; ++k) acc[k] = epilogue_value(a.ep, acc[k], row, j * kCpl + k);
+    }
+#pragma unroll
+    for (int k = 0; k < kCpl; k += 4)
+        *reinterpret_cast<float4 *>(dst + k) = make_float4(acc[k], acc[k + 1], acc[k + 2], acc[k + 3]);
+}
+
+template<int kBits, int kPolicy, ValueMode kMode, typename RhsT, int kN>
+__global__ __launch_bounds__(kWave *kWavesPerBlock) void qcsr_spmm_rowwave(QcsrArgs a) {
+    using S = WaveShape<RhsT, kN>;
+    __shared__ int2 stage[kWavesPerBlock][kWave];
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const std::uint32_t row = blockIdx.x * kWavesPerBlock + wave;
+    if (row >= a.rows) return;
+    const std::int64_t begin = a.row_ptr[row];
+    const std::int64_t end = a.row_ptr[row + 1];
+    float acc[S::kCpl];
+#pragma unroll
+    for (int k = 0; k < S::kCpl; ++k) acc[k] = 0.0f;
+    accumulate_segment<kBits, kPolicy, kMode, RhsT, kN>(a, stage[wave], row, begin, begin, end, lane, acc);
+    reduce_groups<S::kLpe, S::kCpl>(acc);
+    if (lane < S::kLpe) store_row<S::kCpl>(a, row, lane, acc);
+}
+
+// ---- load-balanced form: equal nnz chunks, one wave per chunk ----------------------------
+
+struct Balance {
+    std::int64_t nnz;
+    float *partials;       // [chunks][2][kN]: slot 0 = row begun before the chunk, 1 = row
+                           // continuing past it
+    std::uint32_t chunk;   // entries per chunk
+    std::uint32_t chunks;
+};
+
+// First row a chunk starting at entry `cb` visits: the row holding entry cb, or the first
+// of the (possibly empty) rows that start at cb.
+__device__ __forceinline__ std::uint32_t first_row_of_chunk(const std::int32_t *row_ptr,
+                                                            std::uint32_t rows, std::int64_t cb) {
+    std::uint32_t lo = 0u, hi = rows;  // first r with row_ptr[r] >= cb
+    while (lo < hi) {
+        const std::uint32_t mid = lo + (hi - lo) / 2u;
+        if (row_ptr[mid] < cb) lo = mid + 1u;
+        else hi = mid;
+    }
+    if (lo == rows || row_ptr[lo] > cb) --lo;
+    return lo;
+}
+
+// Chunk k covers entries [k chunk, (k + 1) chunk) (the last one also the empty rows at the
+// end). Rows wholly inside the chunk are stored (through the epilogue); the parts of rows
+// that cross a chunk edge go to the chunk's partial slots for qcsr_spmm_fixup.
+template<int kBits, int kPolicy, ValueMode kMode, typename RhsT, int kN>
+__global__ __launch_bounds__(kWave *kWavesPerBlock) void qcsr_spmm_balanced(QcsrArgs a, Balance b) {
+    using S = WaveShape<RhsT, kN>;
+    __shared__ int2 stage[kWavesPerBlock][kWave];
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const std::uint32_t k = blockIdx.x * kWavesPerBlock + wave;
+    if (k >= b.chunks) return;
+    const bool last = k + 1u == b.chunks;
+    const std::int64_t cb = static_cast<std::int64_t>(k) * b.chunk;
+    const std::int64_t ce = last ? b.nnz : cb + b.chunk;
+    for (std::uint32_t r = first_row_of_chunk(a.row_ptr, a.rows, cb); r < a.rows; ++r) {
+        const std::int64_t rb = a.row_ptr[r], re = a.row_ptr[r + 1];
+        if (!last && rb >= ce) break;
+        float acc[S::kCpl];
+#pragma unroll
+        for (int c = 0; c < S::kCpl; ++c) acc[c] = 0.0f;
+        accumulate_segment<kBits, kPolicy, kMode, RhsT, kN>(a, stage[wave], r, rb, rb > cb ? rb : cb,
+                                                            re < ce ? re : ce, lane, acc);
+        reduce_groups<S::kLpe, S::kCpl>(acc);
+        if (lane < S::kLpe) {
+            if (rb >= cb && re <= ce) {
+                store_row<S::kCpl>(a, r, lane, acc);
+            } else {
+                float *dst = b.partials + (static_cast<std::int64_t>(k) * 2 + (rb < cb ? 0 : 1)) * kN
+                    + lane * S::kCpl;
+#pragma unroll
+                for (int c = 0; c < S::kCpl; c += 4)
+                    *reinterpret_cast<float4 *>(dst + c) = make_float4(acc[c], acc[c + 1], acc[c + 2], acc[c + 3]);
+            }
         }
-#pragma unroll
-        for (int k = 0; k < kCpl; k += 4)
-            *reinterpret_cast<float4 *>(dst + k) = make_float4(acc[k], acc[k + 1], acc[k + 2],
-                                                               acc[k + 3]);
+    }
+}
+
+// One wave per chunk k: if the row holding k's first entry began in an earlier chunk and
+// ends in k, sum its partials in chunk order (tail of its first chunk, then the heads of
+// the following chunks up to k) and store it through the epilogue.
+template<int kN>
+__global__ __launch_bounds__(kWave *kWavesPerBlock) void qcsr_spmm_fixup(QcsrArgs a, Balance b) {
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const std::uint32_t k = blockIdx.x * kWavesPerBlock + wave;
+    if (k >= b.chunks) return;
+    const bool last = k + 1u == b.chunks;
+    const std::int64_t cb = static_cast<std::int64_t>(k) * b.chunk;
+    const std::int64_t ce = last ? b.nnz : cb + b.chunk;
+    const std::uint32_t r = first_row_of_chunk(a.row_ptr, a.rows, cb);
+    if (r >= a.rows) return;  // row_ptr[0] != 0: nothing here is well defined
+    const std::int64_t rb = a.row_ptr[r], re = a.row_ptr[r + 1];
+    if (!(rb < cb && re <= ce)) return;
+    const std::uint32_t k0 = static_cast<std::uint32_t>(rb / b.chunk);
+    for (int c = lane; c < kN; c += kWave) {
+        float v = b.partials[(static_cast<std::int64_t>(k0) * 2 + 1) * kN + c];
+        for (std::uint32_t q = k0 + 1u; q <= k; ++q) v += b.partials[static_cast<std::int64_t>(q) * 2 * kN + c];
+        a.out[static_cast<std::int64_t>(r) * a.out_ld + c] = a.ep.active ? epilogue_value(a.ep, v, r, c) : v;
     }
 }
 
@@ -164,11 +271,24 @@ __global__ __launch_bounds__(kWave *kWavesPerBlock) void qcsr_spmm_generic(QcsrA
     }
 }
 
+template<int kBits, int kPolicy, ValueMode kMode, typename RhsT, int kN>
+int launch_balanced(const QcsrArgs &a, const Balance &b, hipStream_t stream) {
+    const dim3 grid((b.chunks + kWavesPerBlock - 1) / kWavesPerBlock), block(kWave * kWavesPerBlock);
+    hipLaunchKernelGGL((qcsr_spmm_balanced<kBits, kPolicy, kMode, RhsT, kN>), grid, block, 0, stream, a, b);
+    hipLaunchKernelGGL((qcsr_spmm_fixup<kN>), grid, block, 0, stream, a, b);
+    return check_launch("qcsr_spmm_balanced");
+}
+
 template<int kBits, int kPolicy, ValueMode kMode, typename RhsT>
-int launch_rhs(const QcsrArgs &a, std::int64_t n, bool aligned, hipStream_t stream) {
+int launch_rhs(const QcsrArgs &a, std::int64_t n, bool aligned, const Balance *bal,
+               hipStream_t stream) {
     const unsigned blocks = (a.rows + kWavesPerBlock - 1) / kWavesPerBlock;
     const dim3 grid(blocks), block(kWave * kWavesPerBlock);
     constexpr int kCpl = 16 / static_cast<int>(sizeof(RhsT));
+    if (bal != nullptr && aligned && n == 64)
+        return launch_balanced<kBits, kPolicy, kMode, RhsT, 64>(a, *bal, stream);
+    if (bal != nullptr && aligned && n == 128)
+        return launch_balanced<kBits, kPolicy, kMode, RhsT, 128>(a, *bal, stream);
     if (aligned && n == 64) {
         hipLaunchKernelGGL((qcsr_spmm_rowwave<kBits, kPolicy, kMode, RhsT, 64>), grid, block, 0,
                            stream, a);
@@ -187,20 +307,20 @@ int launch_rhs(const QcsrArgs &a, std::int64_t n, bool aligned, hipStream_t stre
 
 template<int kBits, int kPolicy, ValueMode kMode>
 int launch_mode(const QcsrArgs &a, std::uint32_t rhs_dtype, std::int64_t n, bool aligned,
-                hipStream_t stream) {
+                const Balance *bal, hipStream_t stream) {
     if (rhs_dtype == CELLERATOR_DTYPE_F16)
-        return launch_rhs<kBits, kPolicy, kMode, std::uint16_t>(a, n, aligned, stream);
-    return launch_rhs<kBits, kPolicy, kMode, float>(a, n, aligned, stream);
+        return launch_rhs<kBits, kPolicy, kMode, std::uint16_t>(a, n, aligned, bal, stream);
+    return launch_rhs<kBits, kPolicy, kMode, float>(a, n, aligned, bal, stream);
 }
 
 template<int kPolicy>
 int launch_bits(const QcsrArgs &a, std::uint32_t bits, std::uint32_t rhs_dtype, std::int64_t n,
-                bool aligned, hipStream_t stream) {
+                bool aligned, const Balance *bal, hipStream_t stream) {
     switch (bits) {
-    case 1: return launch_mode<1, kPolicy, ValueMode::quantized>(a, rhs_dtype, n, aligned, stream);
-    case 2: return launch_mode<2, kPolicy, ValueMode::quantized>(a, rhs_dtype, n, aligned, stream);
-    case 4: return launch_mode<4, kPolicy, ValueMode::quantized>(a, rhs_dtype, n, aligned, stream);
-    case 8: return launch_mode<8, kPolicy, ValueMode::quantized>(a, rhs_dtype, n, aligned, stream);
+    case 1: return launch_mode<1, kPolicy, ValueMode::quantized>(a, rhs_dtype, n, aligned, bal, stream);
+    case 2: return launch_mode<2, kPolicy, ValueMode::quantized>(a, rhs_dtype, n, aligned, bal, stream);
+    case 4: return launch_mode<4, kPolicy, ValueMode::quantized>(a, rhs_dtype, n, aligned, bal, stream);
+    case 8: return launch_mode<8, kPolicy, ValueMode::quantized>(a, rhs_dtype, n, aligned, bal, stream);
     default: return fail(CX_STATUS_UNSUPPORTED, "quantized CSR bits must be 1, 2, 4 or 8");
     }
 }
@@ -213,6 +333,25 @@ __global__ void pack_gene_affine_kernel(const float *scales, const float *offset
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0u; }
+
+// Entries per chunk of the balanced form: about 65,536 chunks, at least 1,024 entries each,
+// a multiple of 64.
+std::uint32_t balance_chunk(std::uint64_t nnz) {
+    std::uint64_t c = (nnz + 65535u) / 65536u;
+    c = (c + 63u) / 64u * 64u;
+    return static_cast<std::uint32_t>(c < 1024u ? 1024u : c);
+}
+
+std::uint64_t balance_bytes(std::uint64_t nnz, std::int64_t out_cols) {
+    if (nnz == 0u || out_cols <= 0) return 0u;
+    const std::uint64_t chunk = balance_chunk(nnz);
+    return (nnz + chunk - 1u) / chunk * 2u * static_cast<std::uint64_t>(out_cols) * 4u;
+}
+
+// Shared body of the forward entries; `bal_ws` (may be NULL) selects the balanced form.
+int qcsr_forward(const cx_qcsr_matrix *m, const void *rhs, std::uint32_t rhs_dtype, std::int64_t rhs_ld,
+                 std::int64_t out_cols, float *out, std::int64_t out_ld, const cx_spmm_epilogue *epilogue,
+                 void *bal_ws, std::uint64_t bal_bytes, void *stream);
 
 } // namespace
 } // namespace cx
@@ -228,8 +367,37 @@ extern "C" int cx_qcsr_spmm_fwd_epilogue(const cx_qcsr_matrix *m, const void *rh
                                          uint32_t rhs_dtype, int64_t rhs_ld, int64_t out_cols,
                                          float *out, int64_t out_ld,
                                          const cx_spmm_epilogue *epilogue, void *stream) {
+    cx::clear_error();
+    return cx::qcsr_forward(m, rhs, rhs_dtype, rhs_ld, out_cols, out, out_ld, epilogue, nullptr, 0u,
+                            stream);
+}
+
+extern "C" int cx_qcsr_spmm_balanced_workspace(const cx_qcsr_matrix *m, int64_t out_cols,
+                                               uint64_t *bytes) {
     using namespace cx;
     clear_error();
+    if (m == nullptr || bytes == nullptr)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_balanced_workspace: null argument");
+    *bytes = balance_bytes(m->nnz, out_cols);
+    return CX_STATUS_SUCCESS;
+}
+
+extern "C" int cx_qcsr_spmm_fwd_balanced(const cx_qcsr_matrix *m, const void *rhs,
+                                         uint32_t rhs_dtype, int64_t rhs_ld, int64_t out_cols,
+                                         float *out, int64_t out_ld,
+                                         const cx_spmm_epilogue *epilogue, void *workspace,
+                                         uint64_t workspace_bytes, void *stream) {
+    cx::clear_error();
+    return cx::qcsr_forward(m, rhs, rhs_dtype, rhs_ld, out_cols, out, out_ld, epilogue, workspace,
+                            workspace_bytes, stream);
+}
+
+namespace cx {
+namespace {
+
+int qcsr_forward(const cx_qcsr_matrix *m, const void *rhs, std::uint32_t rhs_dtype, std::int64_t rhs_ld,
+                 std::int64_t out_cols, float *out, std::int64_t out_ld, const cx_spmm_epilogue *epilogue,
+                 void *bal_ws, std::uint64_t bal_bytes, void *stream) {
     if (m == nullptr || out == nullptr || rhs == nullptr)
         return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd: null matrix, rhs or output");
     if (rhs_dtype != CELLERATOR_DTYPE_F16 && rhs_dtype != CELLERATOR_DTYPE_F32)
@@ -288,20 +456,37 @@ extern "C" int cx_qcsr_spmm_fwd_epilogue(const cx_qcsr_matrix *m, const void *rh
     const bool aligned = aligned16(rhs) && aligned16(out) && (rhs_ld * esize) % 16 == 0
         && (out_ld * 4) % 16 == 0;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    Balance balance{};
+    const Balance *bal = nullptr;
+    if (bal_ws != nullptr && m->nnz != 0u) {
+        if (bal_bytes < balance_bytes(m->nnz, out_cols))
+            return fail(CX_STATUS_INVALID_ARGUMENT,
+                        "cx_qcsr_spmm_fwd_balanced: workspace smaller than cx_qcsr_spmm_balanced_workspace");
+        if ((reinterpret_cast<std::uintptr_t>(bal_ws) & 15u) != 0u)
+            return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd_balanced: workspace must be 16-byte aligned");
+        balance.nnz = static_cast<std::int64_t>(m->nnz);
+        balance.partials = static_cast<float *>(bal_ws);
+        balance.chunk = balance_chunk(m->nnz);
+        balance.chunks = static_cast<std::uint32_t>((m->nnz + balance.chunk - 1u) / balance.chunk);
+        bal = &balance;
+    }
     if (m->bits == 0u) {
         if (m->value_dtype == CELLERATOR_DTYPE_F16)
             return launch_mode<0, CX_DECODE_PER_GENE_AFFINE, ValueMode::f16>(a, rhs_dtype,
-                                                                               out_cols, aligned, s);
+                                                                               out_cols, aligned, bal, s);
         return launch_mode<0, CX_DECODE_PER_GENE_AFFINE, ValueMode::f32>(a, rhs_dtype, out_cols,
-                                                                          aligned, s);
+                                                                          aligned, bal, s);
     }
     if (m->decode_policy == CX_DECODE_PER_GENE_AFFINE)
-        return launch_bits<CX_DECODE_PER_GENE_AFFINE>(a, m->bits, rhs_dtype, out_cols, aligned, s);
+        return launch_bits<CX_DECODE_PER_GENE_AFFINE>(a, m->bits, rhs_dtype, out_cols, aligned, bal, s);
     if (m->decode_policy == CX_DECODE_PER_GENE_AFFINE_PAIRS)
-        return launch_bits<CX_DECODE_PER_GENE_AFFINE_PAIRS>(a, m->bits, rhs_dtype, out_cols, aligned, s);
+        return launch_bits<CX_DECODE_PER_GENE_AFFINE_PAIRS>(a, m->bits, rhs_dtype, out_cols, aligned, bal, s);
     return launch_bits<CX_DECODE_COLUMN_SCALE_ROW_OFFSET>(a, m->bits, rhs_dtype, out_cols, aligned,
-                                                          s);
+                                                          bal, s);
 }
+
+} // namespace
+} // namespace cx
 
 extern "C" int cx_qcsr_pack_gene_affine(const float *scales, const float *offsets, uint32_t cols,
                                         float *pairs, void *stream) {

@@ -200,8 +200,35 @@ def qcsr_spmm_bwd_rhs(transposed: QcsrMatrix, grad_out: torch.Tensor,
     if out is None:
         out = torch.empty((transposed.rows, n), dtype=torch.float32, device=grad_out.device)
     d = transposed.descriptor()
+    ws = _balanced_workspace(d, n, grad_out.device)
     N.check("cx_qcsr_spmm_bwd_rhs", N.engine().cx_qcsr_spmm_bwd_rhs(
         C.byref(d), grad_out.data_ptr(), grad_out.stride(0), n, out.data_ptr(), out.stride(0),
+        ws.data_ptr(), ws.numel(), _stream(stream)))
+    return out
+
+
+def _balanced_workspace(d, n: int, device) -> torch.Tensor:
+    nbytes = C.c_uint64()
+    N.check("cx_qcsr_spmm_balanced_workspace",
+            N.engine().cx_qcsr_spmm_balanced_workspace(C.byref(d), n, C.byref(nbytes)))
+    return torch.empty(max(nbytes.value, 16), dtype=torch.uint8, device=device)
+
+
+def qcsr_spmm_balanced(m: QcsrMatrix, rhs: torch.Tensor, out: Optional[torch.Tensor] = None,
+                       stream=None, epilogue: Optional[Epilogue] = None) -> torch.Tensor:
+    """qcsr_spmm in the load-balanced (equal nnz chunks) form, for skewed row lengths."""
+    _require_cuda(m.row_ptr, m.col_idx, rhs)
+    if rhs.dim() != 2 or rhs.shape[0] != m.cols or rhs.stride(1) != 1:
+        raise ValueError("rhs must be [cols, N] with unit column stride")
+    n = rhs.shape[1]
+    if out is None:
+        out = torch.empty((m.rows, n), dtype=torch.float32, device=rhs.device)
+    d = m.descriptor()
+    ws = _balanced_workspace(d, n, rhs.device)
+    e = epilogue.descriptor(out) if epilogue is not None else None
+    N.check("cx_qcsr_spmm_fwd_balanced", N.engine().cx_qcsr_spmm_fwd_balanced(
+        C.byref(d), rhs.data_ptr(), _DTYPE_CODE[rhs.dtype], rhs.stride(0), n, out.data_ptr(),
+        out.stride(0), C.byref(e) if e is not None else None, ws.data_ptr(), ws.numel(),
         _stream(stream)))
     return out
 

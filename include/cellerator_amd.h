@@ -160,6 +160,20 @@ int cx_qcsr_spmm_fwd_epilogue(const cx_qcsr_matrix *a, const void *rhs, uint32_t
                               int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
                               const cx_spmm_epilogue *epilogue, void *stream);
 
+/* Load-balanced form of cx_qcsr_spmm_fwd_epilogue for skewed row lengths (the transpose of an
+ * expression matrix has genes stored in nearly every cell): the nnz range is cut into equal
+ * chunks (about 65,536 of at least 1,024 entries), one wave per chunk. Rows inside a chunk
+ * are stored directly; the pieces of rows crossing a chunk edge are written to `workspace`
+ * and summed by a second kernel in chunk order, so results are deterministic (per element
+ * the summation order differs from the row-wave form's). Applies to N = 64 or 128 with
+ * aligned operands; other shapes run the row-wave form. workspace (16-byte aligned) holds
+ * cx_qcsr_spmm_balanced_workspace bytes; no counterpart in the reference. */
+int cx_qcsr_spmm_balanced_workspace(const cx_qcsr_matrix *a, int64_t out_cols, uint64_t *bytes);
+int cx_qcsr_spmm_fwd_balanced(const cx_qcsr_matrix *a, const void *rhs, uint32_t rhs_dtype,
+                              int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
+                              const cx_spmm_epilogue *epilogue, void *workspace,
+                              uint64_t workspace_bytes, void *stream);
+
 /* Interleaves per-gene metadata for CX_DECODE_PER_GENE_AFFINE_PAIRS:
  * pairs[2c] = scales[c] (1 if scales is NULL), pairs[2c+1] = offsets[c] (0 if NULL),
  * for c < cols; pairs (device, 8-byte aligned) holds 2 * cols floats. No counterpart in
@@ -194,13 +208,14 @@ int cx_qcsr_spmm_bwd_values(const cx_qcsr_matrix *a, const float *grad_out,
                             int64_t rhs_ld, int64_t out_cols, float *grad_values, void *stream);
 
 /* grad_rhs[cols x out_cols] = A^T . grad_out, with `transposed` the f32 transpose built by
- * cx_qcsr_transpose: the forward row-wave SpMM on A^T, every element written once in a fixed
- * order. Replaces csr_spmm_bwd_rhs_f16_f32 (src/compute/sparse/ops/ops.hh:122-133,
+ * cx_qcsr_transpose: cx_qcsr_spmm_fwd_balanced on A^T (workspace sized by
+ * cx_qcsr_spmm_balanced_workspace(transposed, out_cols)), every element in a fixed order. Replaces csr_spmm_bwd_rhs_f16_f32 (src/compute/sparse/ops/ops.hh:122-133,
  * kernels/base_sparse/csr_spmm_bwd_rhs_kernel_.cuh), which zero-fills grad_rhs and adds
  * with float atomics. */
 int cx_qcsr_spmm_bwd_rhs(const cx_qcsr_matrix *transposed, const float *grad_out,
                          int64_t grad_out_ld, int64_t out_cols, float *grad_rhs,
-                         int64_t grad_rhs_ld, void *stream);
+                         int64_t grad_rhs_ld, void *workspace, uint64_t workspace_bytes,
+                         void *stream);
 
 /* Stable LSD radix sort of (key, value) u32 pairs on the device, on the keys' low key_bits
  * bits (8 bits per pass); vals_in == NULL sorts the identity permutation (value = input

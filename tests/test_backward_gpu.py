@@ -166,7 +166,8 @@ def test_bwd_rhs_and_transposed_product_match_referee(oracle, bits, policy, n):
     """grad_rhs = A^T . G equals the referee's transpose_sparse product (referee.cc:170-232),
     and the transposed matrix also serves A^T . B through the plain forward."""
     torch = _torch()
-    from cellerator_amd import QcsrMatrix, qcsr_spmm, qcsr_spmm_bwd_rhs, qcsr_transpose
+    from cellerator_amd import (QcsrMatrix, qcsr_spmm, qcsr_spmm_balanced, qcsr_spmm_bwd_rhs,
+                                qcsr_transpose)
     rng = np.random.default_rng(bits * 10 + policy + n)
     rows, cols = 2100, 500
     if bits == 0:
@@ -183,15 +184,123 @@ def test_bwd_rhs_and_transposed_product_match_referee(oracle, bits, policy, n):
     g = rng.standard_normal((rows, n)).astype(np.float32)
     t = qcsr_transpose(m)
     gr = qcsr_spmm_bwd_rhs(t, torch.from_numpy(g).cuda())
-    direct = qcsr_spmm(t, torch.from_numpy(g).cuda())
+    direct = qcsr_spmm_balanced(t, torch.from_numpy(g).cuda())
+    rowwave = qcsr_spmm(t, torch.from_numpy(g).cuda())
     torch.cuda.synchronize()
     ref = oracle.spmm_referee(cols, rows, n, row_ptr, col_idx, decoded, g, transpose_sparse=True)
     absx = np.abs(decoded.astype(np.float64))
     mag = oracle.spmm_referee(cols, rows, n, row_ptr, col_idx, absx, np.abs(g).astype(np.float64),
                               transpose_sparse=True)
     check_against_referee(oracle, ref, mag, gr.cpu().numpy())
+    check_against_referee(oracle, ref, mag, rowwave.cpu().numpy())
     assert torch.equal(gr.view(torch.int32), direct.view(torch.int32))
     # run to run: the same bits (no atomics)
     again = qcsr_spmm_bwd_rhs(qcsr_transpose(m), torch.from_numpy(g).cuda())
     torch.cuda.synchronize()
     assert torch.equal(gr.view(torch.int32), again.view(torch.int32))
+
+
+# ---------------------------------------------------------------- load-balanced form
+
+def _rows_from_lengths(oracle, rng, lengths, cols, bits=4, policy=1):
+    """A quantized CSR with the given row lengths (columns sorted, distinct)."""
+    from tests.helpers import quantized_fixture
+    lengths = np.asarray(lengths, np.int64)
+    fx = quantized_fixture(oracle, rng, len(lengths), cols, 1.0, bits, policy)
+    row_ptr = np.zeros(len(lengths) + 1, np.int64)
+    row_ptr[1:] = np.cumsum(lengths)
+    col_idx = np.concatenate([np.sort(rng.choice(cols, size=int(c), replace=False)) for c in lengths
+                              if c] or [np.zeros(0, np.int64)]).astype(np.int32)
+    qmax = (1 << bits) - 1
+    codes = rng.integers(0, qmax + 1, len(col_idx))
+    values = (fx["offsets"][col_idx] + fx["scales"][col_idx] * codes).astype(np.float32) \
+        if policy == 1 else None
+    row_ptr = row_ptr.astype(np.int32)
+    packed_row_ptr = oracle.build_packed_row_ptr(bits, row_ptr)
+    packed = oracle.pack_csr(bits, policy, row_ptr, packed_row_ptr, col_idx, values, fx["scales"],
+                             fx["offsets"], None)
+    fx.update(row_ptr=row_ptr, packed_row_ptr=packed_row_ptr, col_idx=col_idx, packed=packed)
+    return fx
+
+
+# chunk = 1,024 entries at these sizes: rows ending exactly on a chunk edge, empty rows on
+# an edge, a row spanning several chunks, trailing empty rows, a last partial chunk
+EDGE_LENGTHS = [1024, 0, 0, 3000, 1, 0, 2047, 5000, 0, 1023, 1, 0, 0, 4100, 7, 0, 0]
+
+
+@pytest.mark.parametrize("n,rhs_dtype", [(64, np.float16), (128, np.float32), (64, np.float32)])
+def test_balanced_matches_referee_on_chunk_edges(oracle, n, rhs_dtype):
+    torch = _torch()
+    from cellerator_amd import Epilogue, qcsr_spmm, qcsr_spmm_balanced
+    rng = np.random.default_rng(n)
+    fx = _rows_from_lengths(oracle, rng, EDGE_LENGTHS, 6000)
+    m = to_device_qcsr(fx)
+    w = (rng.standard_normal((6000, n)) * 0.05).astype(rhs_dtype)
+    wt = torch.from_numpy(w).cuda()
+    out = qcsr_spmm_balanced(m, wt)
+    plain = qcsr_spmm(m, wt)
+    again = qcsr_spmm_balanced(m, wt)
+    torch.cuda.synchronize()
+    ref, mag = oracle.qcsr_spmm_referee(4, 1, len(EDGE_LENGTHS), 6000, fx["row_ptr"],
+                                        fx["packed_row_ptr"], fx["col_idx"], fx["packed"],
+                                        fx["scales"], fx["offsets"], None, w)
+    check_against_referee(oracle, ref, mag + 1e-30, out.cpu().numpy())
+    check_against_referee(oracle, ref, mag + 1e-30, plain.cpu().numpy())
+    assert torch.equal(out.view(torch.int32), again.view(torch.int32))
+    # with an epilogue, in place
+    bias = torch.randn(n, device="cuda")
+    c0 = torch.randn(len(EDGE_LENGTHS), n, device="cuda")
+    y = c0.clone()
+    qcsr_spmm_balanced(m, wt, out=y, epilogue=Epilogue(7, 0.5, 2.0, bias, y))
+    torch.cuda.synchronize()
+    decoded = oracle.decode_csr(4, 1, fx["row_ptr"], fx["packed_row_ptr"], fx["col_idx"], fx["packed"],
+                                fx["scales"], fx["offsets"], None)
+    ref_e = oracle.spmm_referee(len(EDGE_LENGTHS), 6000, n, fx["row_ptr"], fx["col_idx"], decoded, w,
+                                alpha=0.5, beta=2.0, c0=c0.cpu().numpy(), epilogue=7,
+                                bias=bias.cpu().numpy())
+    cmp = oracle.compare(ref_e, y.cpu().numpy(), 1e-4, 1e-4)
+    assert cmp["status"] == 0 and cmp["within_tolerance"], cmp
+
+
+def test_balanced_single_row_and_empty_matrix(oracle):
+    torch = _torch()
+    from cellerator_amd import Epilogue, QcsrMatrix, qcsr_spmm_balanced
+    rng = np.random.default_rng(3)
+    fx = _rows_from_lengths(oracle, rng, [9000], 9500, bits=8)
+    w = (rng.standard_normal((9500, 64)) * 0.05).astype(np.float16)
+    out = qcsr_spmm_balanced(to_device_qcsr(fx), torch.from_numpy(w).cuda())
+    torch.cuda.synchronize()
+    ref, mag = oracle.qcsr_spmm_referee(8, 1, 1, 9500, fx["row_ptr"], fx["packed_row_ptr"],
+                                        fx["col_idx"], fx["packed"], fx["scales"], fx["offsets"],
+                                        None, w)
+    check_against_referee(oracle, ref, mag, out.cpu().numpy())
+    empty = QcsrMatrix(5, 7, 0, torch.zeros(6, dtype=torch.int32).cuda(),
+                       torch.zeros(0, dtype=torch.int32).cuda(),
+                       values=torch.zeros(0, dtype=torch.float32).cuda())
+    bias = torch.arange(64, dtype=torch.float32, device="cuda")
+    y = torch.full((5, 64), float("nan"), device="cuda")
+    qcsr_spmm_balanced(empty, torch.ones(7, 64, device="cuda"), out=y,
+                       epilogue=Epilogue(5, 1.0, 0.0, bias - 10.0))
+    torch.cuda.synchronize()
+    assert torch.equal(y, torch.relu(bias - 10.0).expand(5, 64))
+
+
+def test_balanced_skewed_random_matches_row_wave(oracle):
+    """Lognormal rows with a few very long ones: balanced and row-wave agree within fp32
+    reordering, both within the referee's tolerance."""
+    torch = _torch()
+    from cellerator_amd import qcsr_spmm, qcsr_spmm_balanced
+    rng = np.random.default_rng(12)
+    lengths = np.minimum(rng.lognormal(3.0, 1.5, 3000).astype(np.int64), 3999)
+    lengths[[5, 700, 2999]] = [3999, 3500, 3998]
+    fx = _rows_from_lengths(oracle, rng, lengths, 4000, bits=4, policy=1)
+    w = (rng.standard_normal((4000, 128)) * 0.05).astype(np.float16)
+    m = to_device_qcsr(fx)
+    a = qcsr_spmm_balanced(m, torch.from_numpy(w).cuda())
+    b = qcsr_spmm(m, torch.from_numpy(w).cuda())
+    torch.cuda.synchronize()
+    ref, mag = oracle.qcsr_spmm_referee(4, 1, 3000, 4000, fx["row_ptr"], fx["packed_row_ptr"],
+                                        fx["col_idx"], fx["packed"], fx["scales"], fx["offsets"],
+                                        None, w)
+    check_against_referee(oracle, ref, mag + 1e-30, a.cpu().numpy())
+    check_against_referee(oracle, ref, mag + 1e-30, b.cpu().numpy())
