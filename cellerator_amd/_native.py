@@ -180,6 +180,13 @@ ENGINE_SIGNATURES = {
     "cx_cpbp_builder_export": (C.c_int, [p_void, C.POINTER(CxCpbpTileBuffers)]),
     "cx_cpbp_builder_destroy": (None, [p_void]),
     "cx_cpbp_build_last_error": (C.c_char_p, []),
+    "cx_cpbp_device_builder_create": (C.c_int, [C.POINTER(CxCpbpPlan), C.POINTER(CxCpbpCsr),
+                                                C.POINTER(CxCpbpOrderConfig), p_void,
+                                                C.POINTER(p_void)]),
+    "cx_cpbp_device_builder_requirements": (C.c_int, [p_void, C.POINTER(CxCpbpTileRequirements)]),
+    "cx_cpbp_device_builder_export": (C.c_int, [p_void, C.POINTER(CxCpbpTileBuffers), p_void]),
+    "cx_cpbp_device_builder_destroy": (None, [p_void]),
+    "cx_cpbp_device_build_last_error": (C.c_char_p, []),
     "cx_last_error": (C.c_char_p, []),
     "cx_build_info": (C.c_char_p, []),
     "cellerator_status_string": (C.c_char_p, [C.c_int]),

@@ -39,6 +39,7 @@ ENGINE_SOURCES = [
     "csr_spmv.hip",
     "abi.cpp",
     "cpbp_build.cpp",
+    "cpbp_build_device.hip",
     "bell_plan.cpp",
 ]
 SYNTH_SOURCES = ["synth.hip"]

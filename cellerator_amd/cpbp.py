@@ -112,6 +112,76 @@ def build_tiles(plan: Plan, row_offsets: np.ndarray, canonical_features: np.ndar
         lib.cx_cpbp_builder_destroy(handle)
 
 
+def build_tiles_device(plan: Plan, row_offsets, canonical_features, values, *,
+                       kind: int = ORDER_INFERRED_MINHASH, window_size: int = 1024,
+                       group_width: int = 64, seed: int = DEFAULT_ORDER_SEED,
+                       global_row_begin: int = 0, stream=None):
+    """Device construction of the tiles (cx_cpbp_device_builder_*): inputs are torch device
+    tensors (int32 storage of u32 row offsets / canonical features, f16 or f32 values) or
+    numpy arrays (uploaded first). Returns (CpbpTiles on the device, primary keys). The
+    result is bit-identical to build_tiles + to_device."""
+    import torch
+
+    from .engine import CpbpTiles, _stream
+
+    def dev_u32(a):
+        if isinstance(a, torch.Tensor):
+            return a.contiguous()
+        return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).cuda()
+
+    ro, cf = dev_u32(row_offsets), dev_u32(canonical_features)
+    vals = values if isinstance(values, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(values)).cuda()
+    if vals.dtype not in (torch.float16, torch.float32):
+        raise ValueError("CP-BP values must be float16 or float32")
+    perm = dev_u32(plan.feature_permutation)
+    boffs = dev_u32(plan.feature_block_offsets)
+    lib = N.engine()
+    cplan = N.CxCpbpPlan(plan.feature_count, plan.feature_block_count, perm.data_ptr(), boffs.data_ptr())
+    csr = N.CxCpbpCsr(ro.numel() - 1, vals.element_size(), ro.data_ptr(), cf.data_ptr(), vals.data_ptr())
+    cfg = N.CxCpbpOrderConfig(kind, window_size, group_width, 0, seed, global_row_begin)
+    handle = C.c_void_p()
+    s = _stream(stream)
+    st = lib.cx_cpbp_device_builder_create(C.byref(cplan), C.byref(csr), C.byref(cfg), s, C.byref(handle))
+    if st != 0:
+        raise N.EngineError("cx_cpbp_device_builder_create", st,
+                            lib.cx_cpbp_device_build_last_error().decode())
+    try:
+        req = N.CxCpbpTileRequirements()
+        N.check("cx_cpbp_device_builder_requirements",
+                lib.cx_cpbp_device_builder_requirements(handle, C.byref(req)))
+
+        def buf(n, dtype):
+            return torch.empty(max(n, 1), dtype=dtype, device=vals.device)[:n]
+
+        mask_dtype = torch.int64 if req.cell_mask_bytes == 8 else torch.int32
+        t = CpbpTiles(
+            row_count=req.row_count, feature_count=req.feature_count,
+            tile_row_width=req.tile_row_width, feature_block_offsets=boffs,
+            feature_permutation=perm,
+            tile_block_offsets=buf(req.tile_count + 1, torch.int32),
+            tile_block_ids=buf(req.tile_block_count, torch.int32),
+            tile_block_cell_masks=buf(req.tile_block_count, mask_dtype),
+            block_row_entry_offsets=buf(req.tile_block_count + 1, torch.int32),
+            row_block_gene_masks=buf(req.row_block_entry_count, torch.int32),
+            row_block_value_offsets=buf(req.row_block_entry_count + 1, torch.int32),
+            values=buf(req.nnz_count, vals.dtype), row_permutation=buf(req.row_count, torch.int32),
+            meta={"tile_requirements": {f: getattr(req, f) for f, _ in req._fields_}})
+        primary = buf(req.row_count, torch.int64)
+        ptr = lambda x: x.data_ptr() if x.numel() else None  # noqa: E731
+        bufs = N.CxCpbpTileBuffers(
+            ptr(t.tile_block_offsets), ptr(t.tile_block_ids), ptr(t.tile_block_cell_masks),
+            ptr(t.block_row_entry_offsets), ptr(t.row_block_gene_masks),
+            ptr(t.row_block_value_offsets), ptr(t.values), ptr(t.row_permutation), ptr(primary))
+        st = lib.cx_cpbp_device_builder_export(handle, C.byref(bufs), s)
+        if st != 0:
+            raise N.EngineError("cx_cpbp_device_builder_export", st,
+                                lib.cx_cpbp_device_build_last_error().decode())
+        torch.cuda.current_stream().synchronize() if stream is None else None
+        return t, primary
+    finally:
+        lib.cx_cpbp_device_builder_destroy(handle)
+
+
 def to_device(plan: Plan, tiles: HostTiles, device="cuda"):
     """Uploads the tiles and the plan subset the kernel reads as a CpbpTiles."""
     import torch

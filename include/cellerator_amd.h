@@ -450,6 +450,27 @@ int cx_cpbp_builder_export(const cx_cpbp_builder *builder, const cx_cpbp_tile_bu
 void cx_cpbp_builder_destroy(cx_cpbp_builder *builder);
 const char *cx_cpbp_build_last_error(void);
 
+/* Device construction of the same projection: plan and CSR arrays (cx_cpbp_plan,
+ * cx_cpbp_csr) are DEVICE pointers; the result is bit-identical to cx_cpbp_builder_create's
+ * for the same inputs and config. Replaces the reference's CUDA producers
+ * (components/CellPack/include/CellPack/{apply_plan,cell_block_records_cuda,
+ * local_cell_ordering_cuda,warp_tiles_cuda}.hh: apply_frozen_plan_cuda,
+ * build_cell_block_records_cuda, build_local_cell_order_cuda, build_warp_tiles_cuda) with the
+ * engine's radix sort and scans. create validates on the device, enqueues the construction on
+ * `stream` and synchronizes it (twice, to size the intermediates, which it allocates);
+ * export fills caller-allocated DEVICE buffers (sizes from requirements) on `stream`
+ * without synchronizing. A one-time preprocessing step, not a launch-path call. */
+typedef struct cx_cpbp_device_builder cx_cpbp_device_builder;
+int cx_cpbp_device_builder_create(const cx_cpbp_plan *device_plan, const cx_cpbp_csr *device_csr,
+                                  const cx_cpbp_order_config *config, void *stream,
+                                  cx_cpbp_device_builder **out);
+int cx_cpbp_device_builder_requirements(const cx_cpbp_device_builder *builder,
+                                        cx_cpbp_tile_requirements *out);
+int cx_cpbp_device_builder_export(const cx_cpbp_device_builder *builder,
+                                  const cx_cpbp_tile_buffers *device_buffers, void *stream);
+void cx_cpbp_device_builder_destroy(cx_cpbp_device_builder *builder);
+const char *cx_cpbp_device_build_last_error(void);
+
 /* N = 1 CSR comparator: csr_spmv_fwd_f16_f32 (src/compute/sparse/ops/ops.hh:83-90);
  * y[r] = sum fp32(values) * x[col]. values F16 or F32. */
 int cx_csr_spmv_fwd(uint32_t rows, const uint32_t *row_ptr, const uint32_t *col_idx,
