@@ -98,6 +98,36 @@ class CxCpbpTileBuffers(C.Structure):
                 ("values", p_void), ("row_permutation", p_void), ("primary_keys", p_void)]
 
 
+class CxCpk1Expected(C.Structure):
+    _fields_ = [("global_row_begin", u64), ("row_count", u32), ("feature_count", u32),
+                ("reserved0", u32), ("feature_axis_fingerprint", u64),
+                ("feature_axis_fingerprint_version", u32), ("reserved1", u32),
+                ("row_domain_identity", u64), ("payload_identity", u64)]
+
+
+class CxCpk1View(C.Structure):
+    _fields_ = [("payload_identity", u64), ("image_base", p_void), ("image_bytes", u64),
+                ("global_row_begin", u64), ("full_row_count", u32), ("row_group_count", u32),
+                ("row_group_width", u32), ("maximum_feature_block_width", u32),
+                ("feature_axis_fingerprint", u64), ("feature_axis_fingerprint_version", u32),
+                ("row_domain_kind", u32), ("row_domain_identity", u64),
+                ("feature_block_geometry_identity", u64), ("ordering_identity", u64),
+                ("tile_identity", u64), ("order", CxCpbpOrderConfig),
+                ("inverse_feature_permutation", p_void), ("feature_to_block", p_void),
+                ("feature_to_local", p_void), ("row_group_offsets", p_void),
+                ("inverse_row_permutation", p_void), ("tiles", CxCpbpTiles)]
+
+
+class CxCpk1Metadata(C.Structure):
+    _fields_ = [("feature_axis_fingerprint", u64), ("feature_axis_fingerprint_version", u32),
+                ("row_domain_kind", u32), ("row_domain_identity", u64),
+                ("evaluation_source_identity", u64), ("sampling_provenance_identity", u64),
+                ("cost_policy_identity", u64), ("objective_kind", u32), ("full_row_count", u32),
+                ("maximum_feature_block_width", u32), ("row_group_width", u32),
+                ("row_group_count", u32), ("reserved", u32), ("row_group_offsets", p_void),
+                ("global_row_begin", u64), ("order", CxCpbpOrderConfig)]
+
+
 class CxsQcsrParams(C.Structure):
     _fields_ = [
         ("seed", u64), ("rows", u32), ("cols", u32), ("row_dist", u32), ("bits", u32),
@@ -173,6 +203,13 @@ ENGINE_SIGNATURES = {
                                                     C.POINTER(CxBellGroups), i64, p_void, i64,
                                                     C.POINTER(CxSpmmEpilogue), p_void]),
     "cx_cpbp_reduce": (C.c_int, [C.POINTER(CxCpbpTiles), p_void, u64, p_void, u64, p_void]),
+    "cx_cpk1_image_bytes": (C.c_int, [C.POINTER(CxCpbpTileRequirements), u32, C.POINTER(u64)]),
+    "cx_cpk1_write": (C.c_int, [C.POINTER(CxCpbpPlan), C.POINTER(CxCpk1Metadata),
+                                C.POINTER(CxCpbpTileRequirements), C.POINTER(CxCpbpTileBuffers),
+                                p_void, u64, C.POINTER(CxCpk1View)]),
+    "cx_cpk1_validate": (C.c_int, [p_void, u64, C.POINTER(CxCpk1Expected), C.POINTER(CxCpk1View)]),
+    "cx_cpk1_rebind": (C.c_int, [C.POINTER(CxCpk1View), p_void, u64, C.POINTER(CxCpk1View)]),
+    "cx_cpk1_last_error": (C.c_char_p, []),
     "cx_csr_spmv_fwd": (C.c_int, [u32, p_void, p_void, p_void, u32, p_void, p_void, p_void]),
     "cx_cpbp_builder_create": (C.c_int, [C.POINTER(CxCpbpPlan), C.POINTER(CxCpbpCsr),
                                          C.POINTER(CxCpbpOrderConfig), u32, C.POINTER(p_void)]),

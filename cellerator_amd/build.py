@@ -40,6 +40,7 @@ ENGINE_SOURCES = [
     "abi.cpp",
     "cpbp_build.cpp",
     "cpbp_build_device.hip",
+    "cpk1.cpp",
     "bell_plan.cpp",
 ]
 SYNTH_SOURCES = ["synth.hip"]

@@ -471,6 +471,98 @@ int cx_cpbp_device_builder_export(const cx_cpbp_device_builder *builder,
 void cx_cpbp_device_builder_destroy(cx_cpbp_device_builder *builder);
 const char *cx_cpbp_device_build_last_error(void);
 
+/* ---- CPK1 persistent packing payload --------------------------------------------
+ * The reference's pointer-free image of one packed partition
+ * (components/CellPack/include/CellPack/persistent_packing_payload.hh:9-96,
+ * components/CellPack/src/persistent_packing_payload.cc): a 352-byte header and fifteen
+ * 64-byte-aligned sections. CPK1 v1 holds u32 cell masks (tile widths 1..32) and f16
+ * values. Load = validate on the host, upload the bytes in one copy, rebind the view to
+ * the device copy, and pass view.tiles to cx_cpbp_reduce. */
+
+/* persistent_packing_payload_compatibility (persistent_packing_payload.hh:23-31) */
+typedef struct cx_cpk1_expected {
+    uint64_t global_row_begin;
+    uint32_t row_count;
+    uint32_t feature_count;
+    uint32_t reserved0;
+    uint64_t feature_axis_fingerprint;
+    uint32_t feature_axis_fingerprint_version;
+    uint32_t reserved1;
+    uint64_t row_domain_identity;
+    uint64_t payload_identity;
+} cx_cpk1_expected;
+
+/* persistent_packing_payload_view (persistent_packing_payload.hh:35-56), with the tile
+ * arrays as a cx_cpbp_tiles (value_dtype F16, u32 cell masks). Pointers point into the
+ * image: host after validate, device after rebind. */
+typedef struct cx_cpk1_view {
+    uint64_t payload_identity;
+    const void *image_base;
+    uint64_t image_bytes;
+    uint64_t global_row_begin;
+    uint32_t full_row_count;
+    uint32_t row_group_count;
+    uint32_t row_group_width;
+    uint32_t maximum_feature_block_width;
+    uint64_t feature_axis_fingerprint;
+    uint32_t feature_axis_fingerprint_version;
+    uint32_t row_domain_kind;
+    uint64_t row_domain_identity;
+    uint64_t feature_block_geometry_identity;
+    uint64_t ordering_identity;
+    uint64_t tile_identity;
+    cx_cpbp_order_config order;
+    const uint32_t *inverse_feature_permutation;
+    const uint32_t *feature_to_block;
+    const uint32_t *feature_to_local;
+    const uint32_t *row_group_offsets;
+    const uint32_t *inverse_row_permutation;
+    cx_cpbp_tiles tiles;
+} cx_cpk1_view;
+
+/* What the image records about the plan, its row domain and the local order, beyond the
+ * tiles themselves (the frozen packing plan identity and local_cell_order_config the
+ * reference's writer reads, build_persistent_packing_payload_host,
+ * persistent_packing_payload.cc:483-571). row_group_offsets NULL = uniform groups of
+ * row_group_width over full_row_count; maximum_feature_block_width 0 = the widest block. */
+typedef struct cx_cpk1_metadata {
+    uint64_t feature_axis_fingerprint;
+    uint32_t feature_axis_fingerprint_version;
+    uint32_t row_domain_kind;          /* 1 full dataset, 2 sampled rows */
+    uint64_t row_domain_identity;
+    uint64_t evaluation_source_identity;
+    uint64_t sampling_provenance_identity;
+    uint64_t cost_policy_identity;
+    uint32_t objective_kind;           /* 1 total bytes, 2 row-active block references, 3 weighted */
+    uint32_t full_row_count;
+    uint32_t maximum_feature_block_width;
+    uint32_t row_group_width;
+    uint32_t row_group_count;
+    uint32_t reserved;
+    const uint32_t *row_group_offsets; /* row_group_count + 1, or NULL */
+    uint64_t global_row_begin;
+    cx_cpbp_order_config order;        /* kind, window_size, group_width (= tile width), seed */
+} cx_cpk1_metadata;
+
+/* Image bytes for tiles of `req` with row_group_count row groups. */
+int cx_cpk1_image_bytes(const cx_cpbp_tile_requirements *req, uint32_t row_group_count,
+                        uint64_t *bytes);
+/* Writes the image of HOST plan and tile arrays (cx_cpbp_builder_export's layout) into
+ * `image` (host, capacity bytes), computes the geometry, ordering, tile and payload
+ * identities, then validates it into `out` (build_persistent_packing_payload_host). */
+int cx_cpk1_write(const cx_cpbp_plan *plan, const cx_cpk1_metadata *meta,
+                  const cx_cpbp_tile_requirements *req, const cx_cpbp_tile_buffers *tiles,
+                  void *image, uint64_t capacity, cx_cpk1_view *out);
+/* validate_persistent_packing_payload_host: header, identity (FNV-1a over the image),
+ * layout, the caller's expected identity, plan and tile arrays. HOST image. */
+int cx_cpk1_validate(const void *image, uint64_t image_bytes, const cx_cpk1_expected *expected,
+                     cx_cpk1_view *out);
+/* rebind_persistent_packing_payload: the view of an equal-sized copy at new_base (e.g. a
+ * device upload); no copy, allocation or dereference of new_base. */
+int cx_cpk1_rebind(const cx_cpk1_view *validated, const void *new_base, uint64_t new_bytes,
+                   cx_cpk1_view *out);
+const char *cx_cpk1_last_error(void);
+
 /* N = 1 CSR comparator: csr_spmv_fwd_f16_f32 (src/compute/sparse/ops/ops.hh:83-90);
  * y[r] = sum fp32(values) * x[col]. values F16 or F32. */
 int cx_csr_spmv_fwd(uint32_t rows, const uint32_t *row_ptr, const uint32_t *col_idx,
