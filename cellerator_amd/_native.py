@@ -176,6 +176,13 @@ ENGINE_SIGNATURES = {
     "cx_qcsr_transpose_workspace": (C.c_int, [C.POINTER(CxQcsrMatrix), C.POINTER(u64)]),
     "cx_qcsr_transpose": (C.c_int, [C.POINTER(CxQcsrMatrix), p_void, p_void, p_void, p_void, u64,
                                     p_void]),
+    "cx_qcsr_transpose_panelled_workspace": (C.c_int, [C.POINTER(CxQcsrMatrix), u32, C.POINTER(u64)]),
+    "cx_qcsr_transpose_panelled": (C.c_int, [C.POINTER(CxQcsrMatrix), u32, p_void, p_void, p_void,
+                                             p_void, u64, p_void]),
+    "cx_qcsr_spmm_bwd_rhs_panelled_workspace": (C.c_int, [C.POINTER(CxQcsrMatrix), u32, i64,
+                                                          C.POINTER(u64)]),
+    "cx_qcsr_spmm_bwd_rhs_panelled": (C.c_int, [C.POINTER(CxQcsrMatrix), u32, p_void, i64, i64,
+                                                p_void, i64, p_void, u64, p_void]),
     "cx_qcsr_spmm_bwd_values": (C.c_int, [C.POINTER(CxQcsrMatrix), p_void, i64, p_void, u32, i64,
                                           i64, p_void, p_void]),
     "cx_qcsr_spmm_bwd_rhs": (C.c_int, [C.POINTER(CxQcsrMatrix), p_void, i64, i64, p_void, i64,

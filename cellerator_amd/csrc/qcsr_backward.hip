@@ -234,9 +234,45 @@ std::uint32_t key_bits_for(std::uint32_t cols) {
 
 std::uint64_t align256(std::uint64_t b) { return (b + 255u) & ~static_cast<std::uint64_t>(255u); }
 
-std::uint64_t transpose_workspace(const cx_qcsr_matrix *m) {
-    return align256(m->nnz * 4u) + sort_pairs_workspace_bytes(m->nnz, key_bits_for(m->cols));
+// Rows of the (panelled) transpose: panel p, gene g -> row p * cols + g.
+std::uint64_t panel_count(const cx_qcsr_matrix *m, std::uint32_t panel_rows) {
+    return panel_rows == 0u ? 1u : (static_cast<std::uint64_t>(m->rows) + panel_rows - 1u) / panel_rows;
 }
+
+std::uint64_t transpose_workspace(const cx_qcsr_matrix *m, std::uint32_t panel_rows) {
+    const std::uint64_t out_rows = panel_count(m, panel_rows) * m->cols;
+    std::uint64_t bytes = align256(m->nnz * 4u)
+        + sort_pairs_workspace_bytes(m->nnz, key_bits_for(static_cast<std::uint32_t>(out_rows)));
+    if (panel_rows != 0u) bytes += align256(m->nnz * 4u);  // the computed keys
+    return bytes;
+}
+
+// key[i] = panel(row of i) * cols + col[i], one wave per row (coalesced).
+__global__ __launch_bounds__(256) void panel_key_kernel(const std::int32_t *row_ptr, const std::int32_t *col_idx,
+                                                        std::uint32_t rows, std::uint32_t cols,
+                                                        std::uint32_t panel_rows, std::uint32_t *key) {
+    const std::uint32_t row = (blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    if (row >= rows) return;
+    const std::uint32_t base = (row / panel_rows) * cols;
+    for (std::int64_t i = row_ptr[row] + lane; i < row_ptr[row + 1]; i += kWave)
+        key[i] = base + static_cast<std::uint32_t>(col_idx[i]);
+}
+
+// grad_rhs[g, c] = sum over panels p (in order) of z[(p * cols + g) * n + c].
+__global__ void panel_reduce_kernel(const float *z, std::uint32_t panels, std::uint32_t cols,
+                                    std::int64_t n, float *out, std::int64_t out_ld) {
+    const std::uint64_t i = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x;
+    if (i >= static_cast<std::uint64_t>(cols) * n) return;
+    const std::uint64_t g = i / n, c = i % n;
+    float v = 0.0f;
+    for (std::uint32_t p = 0; p < panels; ++p) v += z[(static_cast<std::uint64_t>(p) * cols + g) * n + c];
+    out[g * out_ld + c] = v;
+}
+
+int transpose_impl(const cx_qcsr_matrix *m, std::uint32_t panel_rows, std::int32_t *t_row_ptr,
+                   std::int32_t *t_col_idx, float *t_values, void *workspace,
+                   std::uint64_t workspace_bytes, hipStream_t s);
 
 bool aligned16(const void *p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0u; }
 
@@ -244,39 +280,81 @@ bool aligned16(const void *p) { return (reinterpret_cast<std::uintptr_t>(p) & 15
 } // namespace cx
 
 extern "C" int cx_qcsr_transpose_workspace(const cx_qcsr_matrix *m, uint64_t *bytes) {
+    return cx_qcsr_transpose_panelled_workspace(m, 0u, bytes);
+}
+
+extern "C" int cx_qcsr_transpose_panelled_workspace(const cx_qcsr_matrix *m, uint32_t panel_rows,
+                                                    uint64_t *bytes) {
     using namespace cx;
     clear_error();
     if (bytes == nullptr) return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_transpose_workspace: null bytes");
     const int rc = validate_matrix(m, "cx_qcsr_transpose_workspace: null matrix");
     if (rc != CX_STATUS_SUCCESS) return rc;
-    *bytes = transpose_workspace(m);
+    *bytes = transpose_workspace(m, panel_rows);
     return CX_STATUS_SUCCESS;
 }
 
 extern "C" int cx_qcsr_transpose(const cx_qcsr_matrix *m, int32_t *t_row_ptr, int32_t *t_col_idx,
                                  float *t_values, void *workspace, uint64_t workspace_bytes,
                                  void *stream) {
-    using namespace cx;
-    clear_error();
+    cx::clear_error();
+    return cx::transpose_impl(m, 0u, t_row_ptr, t_col_idx, t_values, workspace, workspace_bytes,
+                              static_cast<hipStream_t>(stream));
+}
+
+extern "C" int cx_qcsr_transpose_panelled(const cx_qcsr_matrix *m, uint32_t panel_rows,
+                                          int32_t *t_row_ptr, int32_t *t_col_idx, float *t_values,
+                                          void *workspace, uint64_t workspace_bytes, void *stream) {
+    cx::clear_error();
+    if (panel_rows == 0u)
+        return cx::fail(CX_STATUS_INVALID_SHAPE, "cx_qcsr_transpose_panelled: panel_rows must be positive");
+    return cx::transpose_impl(m, panel_rows, t_row_ptr, t_col_idx, t_values, workspace, workspace_bytes,
+                              static_cast<hipStream_t>(stream));
+}
+
+namespace cx {
+namespace {
+
+int transpose_impl(const cx_qcsr_matrix *m, std::uint32_t panel_rows, std::int32_t *t_row_ptr,
+                   std::int32_t *t_col_idx, float *t_values, void *workspace,
+                   std::uint64_t workspace_bytes, hipStream_t s) {
     int rc = validate_matrix(m, "cx_qcsr_transpose: null matrix");
     if (rc != CX_STATUS_SUCCESS) return rc;
     if (m->cols == 0u) return fail(CX_STATUS_INVALID_SHAPE, "cx_qcsr_transpose: the matrix has no columns");
+    const std::uint64_t out_rows = panel_count(m, panel_rows) * m->cols;
+    if (out_rows >= 0xFFFFFFFFull)
+        return fail(CX_STATUS_INVALID_SHAPE, "cx_qcsr_transpose: panels x genes exceeds u32 row ids");
     if (t_row_ptr == nullptr || (m->nnz != 0u && (t_col_idx == nullptr || t_values == nullptr)))
         return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_transpose: null output");
-    if (workspace_bytes < transpose_workspace(m) || (workspace == nullptr && workspace_bytes != 0u))
+    if (workspace_bytes < transpose_workspace(m, panel_rows) || (workspace == nullptr && workspace_bytes != 0u))
         return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_transpose: workspace smaller than cx_qcsr_transpose_workspace");
-    hipStream_t s = static_cast<hipStream_t>(stream);
     const std::uint32_t nnz = static_cast<std::uint32_t>(m->nnz);
     auto *ws = static_cast<unsigned char *>(workspace);
-    auto *sorted_genes = reinterpret_cast<std::uint32_t *>(ws);
+    auto *sorted_keys = reinterpret_cast<std::uint32_t *>(ws);
+    ws += align256(m->nnz * 4u);
+    std::uint64_t left = workspace_bytes - align256(m->nnz * 4u);
+    const std::uint32_t *keys = reinterpret_cast<const std::uint32_t *>(m->col_idx);
+    if (panel_rows != 0u) {
+        auto *computed = reinterpret_cast<std::uint32_t *>(ws);
+        ws += align256(m->nnz * 4u);
+        left -= align256(m->nnz * 4u);
+        if (nnz != 0u) {
+            const std::uint64_t threads = static_cast<std::uint64_t>(m->rows) * kWave;
+            hipLaunchKernelGGL(panel_key_kernel, dim3(static_cast<unsigned>((threads + 255u) / 256u)), dim3(256),
+                               0, s, m->row_ptr, m->col_idx, m->rows, m->cols, panel_rows, computed);
+            rc = check_launch("qcsr_transpose_panel_keys");
+            if (rc != CX_STATUS_SUCCESS) return rc;
+        }
+        keys = computed;
+    }
     if (nnz != 0u) {
-        rc = sort_pairs(reinterpret_cast<const std::uint32_t *>(m->col_idx), nullptr, sorted_genes,
-                        reinterpret_cast<std::uint32_t *>(t_col_idx), nnz, key_bits_for(m->cols),
-                        ws + align256(m->nnz * 4u), workspace_bytes - align256(m->nnz * 4u), s);
+        rc = sort_pairs(keys, nullptr, sorted_keys, reinterpret_cast<std::uint32_t *>(t_col_idx), nnz,
+                        key_bits_for(static_cast<std::uint32_t>(out_rows)), ws, left, s);
         if (rc != CX_STATUS_SUCCESS) return rc;
     }
-    hipLaunchKernelGGL(transpose_row_ptr_kernel, dim3((m->cols + 1u + 255u) / 256u), dim3(256), 0, s,
-                       sorted_genes, nnz, m->cols, t_row_ptr);
+    const std::uint32_t rows_out = static_cast<std::uint32_t>(out_rows);
+    hipLaunchKernelGGL(transpose_row_ptr_kernel, dim3((rows_out + 1u + 255u) / 256u), dim3(256), 0, s,
+                       sorted_keys, nnz, rows_out, t_row_ptr);
     rc = check_launch("qcsr_transpose_row_ptr");
     if (rc != CX_STATUS_SUCCESS || nnz == 0u) return rc;
 
@@ -304,6 +382,9 @@ extern "C" int cx_qcsr_transpose(const cx_qcsr_matrix *m, int32_t *t_row_ptr, in
         return finalize_bits<CX_DECODE_PER_GENE_AFFINE_PAIRS>(a, m->bits, nnz, t_col_idx, t_values, s);
     return finalize_bits<CX_DECODE_COLUMN_SCALE_ROW_OFFSET>(a, m->bits, nnz, t_col_idx, t_values, s);
 }
+
+} // namespace
+} // namespace cx
 
 extern "C" int cx_qcsr_spmm_bwd_values(const cx_qcsr_matrix *m, const float *grad_out,
                                        int64_t grad_out_ld, const void *rhs, uint32_t rhs_dtype,
@@ -346,4 +427,52 @@ extern "C" int cx_qcsr_spmm_bwd_rhs(const cx_qcsr_matrix *transposed, const floa
     return cx_qcsr_spmm_fwd_balanced(transposed, grad_out, CELLERATOR_DTYPE_F32, grad_out_ld,
                                      out_cols, grad_rhs, grad_rhs_ld, nullptr, workspace,
                                      workspace_bytes, stream);
+}
+
+extern "C" int cx_qcsr_spmm_bwd_rhs_panelled_workspace(const cx_qcsr_matrix *panelled, uint32_t panels,
+                                                      int64_t out_cols, uint64_t *bytes) {
+    using namespace cx;
+    clear_error();
+    if (panelled == nullptr || bytes == nullptr)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_bwd_rhs_panelled_workspace: null argument");
+    if (panels == 0u || out_cols <= 0 || panelled->rows % panels != 0u)
+        return fail(CX_STATUS_INVALID_SHAPE, "cx_qcsr_spmm_bwd_rhs_panelled_workspace: bad panels or columns");
+    std::uint64_t balanced = 0u;
+    const int rc = cx_qcsr_spmm_balanced_workspace(panelled, out_cols, &balanced);
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    *bytes = align256(static_cast<std::uint64_t>(panelled->rows) * static_cast<std::uint64_t>(out_cols) * 4u)
+        + align256(balanced);
+    return CX_STATUS_SUCCESS;
+}
+
+extern "C" int cx_qcsr_spmm_bwd_rhs_panelled(const cx_qcsr_matrix *panelled, uint32_t panels,
+                                             const float *grad_out, int64_t grad_out_ld, int64_t out_cols,
+                                             float *grad_rhs, int64_t grad_rhs_ld, void *workspace,
+                                             uint64_t workspace_bytes, void *stream) {
+    using namespace cx;
+    clear_error();
+    if (panelled == nullptr || grad_rhs == nullptr)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_bwd_rhs_panelled: null argument");
+    if (panelled->bits != 0u || panelled->value_dtype != CELLERATOR_DTYPE_F32)
+        return fail(CX_STATUS_INVALID_ARGUMENT,
+                    "cx_qcsr_spmm_bwd_rhs_panelled: expects the f32 transpose built by cx_qcsr_transpose_panelled");
+    std::uint64_t need = 0u;
+    int rc = cx_qcsr_spmm_bwd_rhs_panelled_workspace(panelled, panels, out_cols, &need);
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    if (workspace == nullptr || workspace_bytes < need || (reinterpret_cast<std::uintptr_t>(workspace) & 15u) != 0u)
+        return fail(CX_STATUS_INVALID_ARGUMENT,
+                    "cx_qcsr_spmm_bwd_rhs_panelled: workspace (16-byte aligned) smaller than the query");
+    if (grad_rhs_ld < out_cols) return fail(CX_STATUS_INVALID_SHAPE, "cx_qcsr_spmm_bwd_rhs_panelled: bad grad_rhs_ld");
+    const std::uint32_t genes = panelled->rows / panels;
+    auto *z = static_cast<float *>(workspace);
+    const std::uint64_t z_bytes = align256(static_cast<std::uint64_t>(panelled->rows) * out_cols * 4u);
+    rc = cx_qcsr_spmm_fwd_balanced(panelled, grad_out, CELLERATOR_DTYPE_F32, grad_out_ld, out_cols, z, out_cols,
+                                   nullptr, static_cast<unsigned char *>(workspace) + z_bytes,
+                                   workspace_bytes - z_bytes, stream);
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    const std::uint64_t total = static_cast<std::uint64_t>(genes) * static_cast<std::uint64_t>(out_cols);
+    if (total == 0u) return CX_STATUS_SUCCESS;
+    hipLaunchKernelGGL(panel_reduce_kernel, dim3(static_cast<unsigned>((total + 255u) / 256u)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), z, panels, genes, out_cols, grad_rhs, grad_rhs_ld);
+    return check_launch("qcsr_bwd_rhs_panel_reduce");
 }

@@ -172,6 +172,32 @@ def qcsr_transpose(m: QcsrMatrix, stream=None) -> QcsrMatrix:
                       meta=meta)
 
 
+def qcsr_transpose_panelled(m: QcsrMatrix, panel_rows: int = 8192, stream=None) -> QcsrMatrix:
+    """A^T with rows ordered by (cell panel, gene): rows = ceil(rows / panel_rows) * cols.
+    meta["panels"] holds the panel count for qcsr_spmm_bwd_rhs."""
+    _require_cuda(m.row_ptr)
+    d = m.descriptor()
+    lib = N.engine()
+    ws_bytes = C.c_uint64()
+    N.check("cx_qcsr_transpose_panelled_workspace",
+            lib.cx_qcsr_transpose_panelled_workspace(C.byref(d), panel_rows, C.byref(ws_bytes)))
+    dev = m.row_ptr.device
+    panels = (m.rows + panel_rows - 1) // panel_rows
+    nnz = m.nnz
+    ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=dev)
+    t_row_ptr = torch.empty(panels * m.cols + 1, dtype=torch.int32, device=dev)
+    t_col_idx = torch.empty(max(nnz, 1), dtype=torch.int32, device=dev)
+    t_values = torch.empty(max(nnz, 1), dtype=torch.float32, device=dev)
+    N.check("cx_qcsr_transpose_panelled", lib.cx_qcsr_transpose_panelled(
+        C.byref(d), panel_rows, t_row_ptr.data_ptr(), t_col_idx.data_ptr(), t_values.data_ptr(),
+        ws.data_ptr(), ws_bytes.value, _stream(stream)))
+    meta = {"panels": panels, "panel_rows": panel_rows}
+    if stream is not None:
+        meta["transpose_workspace"] = ws
+    return QcsrMatrix(panels * m.cols, m.rows, 0, t_row_ptr, t_col_idx[:nnz], values=t_values[:nnz],
+                      meta=meta)
+
+
 def qcsr_spmm_bwd_values(m: QcsrMatrix, grad_out: torch.Tensor, rhs: torch.Tensor,
                          out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
     """grad_values[i] = <grad_out[row_i, :], rhs[col_i, :]> for every stored entry (f32)."""
@@ -192,14 +218,28 @@ def qcsr_spmm_bwd_values(m: QcsrMatrix, grad_out: torch.Tensor, rhs: torch.Tenso
 
 def qcsr_spmm_bwd_rhs(transposed: QcsrMatrix, grad_out: torch.Tensor,
                       out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
-    """grad_rhs = A^T . grad_out with `transposed` from qcsr_transpose(A) (f32 [cols, N])."""
+    """grad_rhs = A^T . grad_out with `transposed` from qcsr_transpose(A) or
+    qcsr_transpose_panelled(A) (f32 [cols, N])."""
     _require_cuda(transposed.row_ptr, grad_out)
     if grad_out.dtype != torch.float32 or grad_out.stride(1) != 1 or grad_out.shape[0] != transposed.cols:
         raise ValueError("grad_out must be row-major f32 [rows of A, N]")
     n = grad_out.shape[1]
+    panels = transposed.meta.get("panels", 1)
+    d = transposed.descriptor()
+    if panels > 1:
+        genes = transposed.rows // panels
+        if out is None:
+            out = torch.empty((genes, n), dtype=torch.float32, device=grad_out.device)
+        nbytes = C.c_uint64()
+        N.check("cx_qcsr_spmm_bwd_rhs_panelled_workspace",
+                N.engine().cx_qcsr_spmm_bwd_rhs_panelled_workspace(C.byref(d), panels, n, C.byref(nbytes)))
+        ws = torch.empty(max(nbytes.value, 16), dtype=torch.uint8, device=grad_out.device)
+        N.check("cx_qcsr_spmm_bwd_rhs_panelled", N.engine().cx_qcsr_spmm_bwd_rhs_panelled(
+            C.byref(d), panels, grad_out.data_ptr(), grad_out.stride(0), n, out.data_ptr(),
+            out.stride(0), ws.data_ptr(), ws.numel(), _stream(stream)))
+        return out
     if out is None:
         out = torch.empty((transposed.rows, n), dtype=torch.float32, device=grad_out.device)
-    d = transposed.descriptor()
     ws = _balanced_workspace(d, n, grad_out.device)
     N.check("cx_qcsr_spmm_bwd_rhs", N.engine().cx_qcsr_spmm_bwd_rhs(
         C.byref(d), grad_out.data_ptr(), grad_out.stride(0), n, out.data_ptr(), out.stride(0),

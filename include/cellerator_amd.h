@@ -197,6 +197,28 @@ int cx_qcsr_transpose_workspace(const cx_qcsr_matrix *a, uint64_t *bytes);
 int cx_qcsr_transpose(const cx_qcsr_matrix *a, int32_t *t_row_ptr, int32_t *t_col_idx,
                       float *t_values, void *workspace, uint64_t workspace_bytes, void *stream);
 
+/* Panelled transpose for grad_rhs at large row counts: rows ordered by (cell panel, gene), a
+ * panel being panel_rows consecutive cells, i.e. row p * cols + g holds the cells of gene g
+ * inside panel p, ascending (a.cols * ceil(a.rows / panel_rows) rows, t_row_ptr one more).
+ * While the balanced SpMM walks it, the grad_out rows of one panel (panel_rows x N x 4 bytes)
+ * stay in L2 instead of being gathered from all of grad_out for every gene. */
+int cx_qcsr_transpose_panelled_workspace(const cx_qcsr_matrix *a, uint32_t panel_rows,
+                                         uint64_t *bytes);
+int cx_qcsr_transpose_panelled(const cx_qcsr_matrix *a, uint32_t panel_rows, int32_t *t_row_ptr,
+                               int32_t *t_col_idx, float *t_values, void *workspace,
+                               uint64_t workspace_bytes, void *stream);
+
+/* grad_rhs = A^T . grad_out on a panelled transpose of `panels` panels: the balanced SpMM
+ * writes one partial row per (panel, gene) into the workspace, then a reduction sums each
+ * gene's partials in panel order (deterministic). workspace: 16-byte aligned, the query's
+ * bytes (partials + balanced-SpMM scratch). */
+int cx_qcsr_spmm_bwd_rhs_panelled_workspace(const cx_qcsr_matrix *panelled, uint32_t panels,
+                                            int64_t out_cols, uint64_t *bytes);
+int cx_qcsr_spmm_bwd_rhs_panelled(const cx_qcsr_matrix *panelled, uint32_t panels,
+                                  const float *grad_out, int64_t grad_out_ld, int64_t out_cols,
+                                  float *grad_rhs, int64_t grad_rhs_ld, void *workspace,
+                                  uint64_t workspace_bytes, void *stream);
+
 /* grad_values[i] = sum_{c < out_cols} grad_out[row_i, c] * rhs[col_i, c] for every stored
  * entry i: the gradient of Y = A . RHS with respect to A's (decoded) values. Replaces
  * csr_spmm_bwd_values_f16_f32 (src/compute/sparse/ops/ops.hh:111-120,

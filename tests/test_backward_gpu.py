@@ -304,3 +304,61 @@ def test_balanced_skewed_random_matches_row_wave(oracle):
                                         None, w)
     check_against_referee(oracle, ref, mag + 1e-30, a.cpu().numpy())
     check_against_referee(oracle, ref, mag + 1e-30, b.cpu().numpy())
+
+
+# ---------------------------------------------------------------- panelled transpose
+
+@pytest.mark.parametrize("panel_rows", [1, 64, 500, 5000])
+def test_panelled_transpose_is_blockwise_scipy_transpose(oracle, panel_rows):
+    torch = _torch()
+    import scipy.sparse as sp
+
+    from cellerator_amd import qcsr_transpose_panelled
+    rng = np.random.default_rng(panel_rows)
+    rows, cols = 1234, 300
+    fx = quantized_fixture(oracle, rng, rows, cols, 20.0, 4, 1, empty_every=7)
+    decoded = oracle.decode_csr(4, 1, fx["row_ptr"], fx["packed_row_ptr"], fx["col_idx"], fx["packed"],
+                                fx["scales"], fx["offsets"], None)
+    t = qcsr_transpose_panelled(to_device_qcsr(fx), panel_rows)
+    torch.cuda.synchronize()
+    panels = (rows + panel_rows - 1) // panel_rows
+    assert (t.rows, t.cols, t.meta["panels"]) == (panels * cols, rows, panels)
+    ids = sp.csr_matrix((np.arange(1, len(fx["col_idx"]) + 1), fx["col_idx"], fx["row_ptr"]),
+                        shape=(rows, cols))
+    ptr, idx, val = [0], [], []
+    for p in range(panels):
+        block = ids[p * panel_rows:(p + 1) * panel_rows].T.tocsr()
+        block.sort_indices()
+        for g in range(cols):
+            s, e = block.indptr[g], block.indptr[g + 1]
+            idx.extend((block.indices[s:e] + p * panel_rows).tolist())
+            val.extend(block.data[s:e].tolist())
+            ptr.append(len(idx))
+    assert np.array_equal(t.row_ptr.cpu().numpy(), np.array(ptr))
+    assert np.array_equal(t.col_idx.cpu().numpy(), np.array(idx))
+    expect = decoded[np.array(val, np.int64) - 1]
+    assert np.array_equal(t.values.cpu().numpy().view(np.uint32), expect.view(np.uint32))
+
+
+@pytest.mark.parametrize("panel_rows,n", [(256, 64), (1000, 128), (3000, 64), (64, 48)])
+def test_panelled_bwd_rhs_matches_referee(oracle, panel_rows, n):
+    torch = _torch()
+    from cellerator_amd import qcsr_spmm_bwd_rhs, qcsr_transpose_panelled
+    rng = np.random.default_rng(panel_rows + n)
+    rows, cols = 2500, 400
+    fx = quantized_fixture(oracle, rng, rows, cols, 30.0, 8, 1, empty_every=9)
+    decoded = oracle.decode_csr(8, 1, fx["row_ptr"], fx["packed_row_ptr"], fx["col_idx"], fx["packed"],
+                                fx["scales"], fx["offsets"], None)
+    g = rng.standard_normal((rows, n)).astype(np.float32)
+    gt = torch.from_numpy(g).cuda()
+    t = qcsr_transpose_panelled(to_device_qcsr(fx), panel_rows)
+    a = qcsr_spmm_bwd_rhs(t, gt)
+    b = qcsr_spmm_bwd_rhs(t, gt)
+    torch.cuda.synchronize()
+    ref = oracle.spmm_referee(cols, rows, n, fx["row_ptr"], fx["col_idx"], decoded, g,
+                              transpose_sparse=True)
+    mag = oracle.spmm_referee(cols, rows, n, fx["row_ptr"], fx["col_idx"],
+                              np.abs(decoded).astype(np.float64), np.abs(g).astype(np.float64),
+                              transpose_sparse=True)
+    check_against_referee(oracle, ref, mag, a.cpu().numpy())
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
