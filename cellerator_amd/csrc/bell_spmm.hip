@@ -64,8 +64,12 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void *base, std::uint32_t byte
                                              static_cast<int>(bytes), 0x00020000);
 }
 
-__device__ __forceinline__ cx_bf16x8 load_frag(rsrc_t r, std::uint32_t byte_offset) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(byte_offset), 0, 0);
+// 16 bytes at voffset (per lane) + soffset (wave-uniform, kept in an SGPR so the per-step
+// address needs no VALU arithmetic).
+__device__ __forceinline__ cx_bf16x8 load_frag(rsrc_t r, std::uint32_t byte_offset,
+                                               std::uint32_t uniform_offset = 0u) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(byte_offset),
+                                                         static_cast<int>(uniform_offset), 0);
     cx_bf16x8 f;
     __builtin_memcpy(&f, &v, 16);
     return f;
@@ -185,8 +189,8 @@ __global__ __launch_bounds__(kN) void bell_spmm_mfma(BellArgs a, const std::uint
 // member w across all N output columns (N/32 accumulator tiles). At step k every member
 // uses the group's k-th block column, so its N x 32 panel slice is loaded from the packed
 // panel once per group into an LDS ring of three slices (column stride 80 B: 8 consecutive
-// lanes' 16-byte reads hit distinct banks). Panel slices run two steps ahead (ping-pong
-// registers, then LDS), the members' A fragments (their k-th valid slot) one step ahead.
+// lanes' 16-byte reads hit distinct banks). Panel slices are issued three steps before use
+// (three register sets, then LDS), the members' A fragments (their k-th valid slot) two.
 constexpr int kGroupWaves = 4;
 constexpr int kPanelColStride = 80;
 constexpr int kRing = 3;
@@ -205,10 +209,13 @@ void bell_spmm_mfma_grouped(BellArgs a, const std::uint16_t *packed_rhs, std::ui
     const int lane = static_cast<int>(threadIdx.x) % kWave;
     const std::uint32_t wave = static_cast<std::uint32_t>(
         __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave)));
-    // workgroups past the groups take the single row blocks, one each
-    const bool single = blockIdx.x >= group_count;
-    const std::uint32_t g0 = single ? grouped_row_blocks + (blockIdx.x - group_count) : group_offsets[blockIdx.x];
-    const std::uint32_t g1 = single ? g0 + 1u : group_offsets[blockIdx.x + 1];
+    // XCD-major: each XCD takes a contiguous range of the planner's order, whose neighbouring
+    // groups share block columns, so the panel slices in use stay in that XCD's L2.
+    // Workgroups past the groups take the single row blocks, one each.
+    const std::uint32_t wg = xcd_major(blockIdx.x, gridDim.x);
+    const bool single = wg >= group_count;
+    const std::uint32_t g0 = single ? grouped_row_blocks + (wg - group_count) : group_offsets[wg];
+    const std::uint32_t g1 = single ? g0 + 1u : group_offsets[wg + 1];
     const std::uint32_t members = g1 - g0;
     const std::uint32_t leader = order[g1 - 1u];
     const bool active = wave < members;
@@ -260,7 +267,7 @@ void bell_spmm_mfma_grouped(BellArgs a, const std::uint16_t *packed_rhs, std::ui
             const std::uint32_t c = threadIdx.x + static_cast<std::uint32_t>(i) * kThreads;
             const std::uint32_t cc = c < static_cast<std::uint32_t>(kChunks) ? c : 0u;
             const auto v = __builtin_amdgcn_raw_buffer_load_b128(
-                rbp, static_cast<int>(bc * static_cast<std::uint32_t>(kN) * 64u + cc * 16u), 0, 0);
+                rbp, static_cast<int>(cc * 16u), static_cast<int>(bc * static_cast<std::uint32_t>(kN) * 64u), 0);
             __builtin_memcpy(&b.c[i], &v, 16);
         }
     };
@@ -274,7 +281,8 @@ void bell_spmm_mfma_grouped(BellArgs a, const std::uint16_t *packed_rhs, std::ui
     };
     auto load_a = [&](cx_bf16x8 (&af)[2], std::uint32_t s) {
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc) af[kc] = load_frag(ra, a_lane + s * 64u + static_cast<std::uint32_t>(kc) * 32u);
+        for (int kc = 0; kc < 2; ++kc)
+            af[kc] = load_frag(ra, a_lane + static_cast<std::uint32_t>(kc) * 32u, s * 64u);
     };
     auto mfma_step = [&](const cx_bf16x8 (&af)[2], std::uint32_t slot) {
 #pragma unroll
@@ -288,30 +296,36 @@ void bell_spmm_mfma_grouped(BellArgs a, const std::uint16_t *packed_rhs, std::ui
     };
 
     if (steps != 0u) {
-        BRegs r0, r1;
-        cx_bf16x8 a0[2], a1[2];
-        load_b(r0, next_lead());   // slice 0
-        load_b(r1, next_lead());   // slice 1 (in flight through step 0)
+        // Slices and A fragments both run two steps ahead: slice j lives in register set
+        // j % 3 from its issue (step j - 3) until it is stored to LDS slot j % 3 (end of step
+        // j - 1); A(j) lives in a[j % 3] from step j - 2. Both stream from L2/HBM, and a step
+        // (16 MFMAs per wave at N = 256) is far shorter than their latency.
+        BRegs b0, b1, b2;
+        cx_bf16x8 a0[2], a1[2], a2[2];
+        load_b(b0, next_lead());   // slice 0
+        load_b(b1, next_lead());   // slice 1
+        load_b(b2, next_lead());   // slice 2
         load_a(a0, next_own());
-        store_b(r0, 0u);
+        load_a(a1, next_own());
+        store_b(b0, 0u);
         __syncthreads();
-        // At step k: LDS slot k%3 holds slice k; registers hold slice k+1 (issued one step
-        // earlier); slice k+2 and A(k+1) are issued now; slice k+1 is stored after the MFMAs.
         std::uint32_t k = 0, slot = 0;
-        auto step = [&](BRegs &mine_next, BRegs &free_regs, cx_bf16x8 (&a_cur)[2], cx_bf16x8 (&a_nxt)[2]) {
-            load_b(free_regs, next_lead());     // slice k+2
-            load_a(a_nxt, next_own());          // A(k+1)
+        auto step = [&](BRegs &free_regs, BRegs &to_store, cx_bf16x8 (&a_cur)[2], cx_bf16x8 (&a_new)[2]) {
+            load_b(free_regs, next_lead());     // slice k+3 (its set held slice k, stored last step)
+            load_a(a_new, next_own());          // A(k+2)
             if (active && k < own_steps) mfma_step(a_cur, slot);
             const std::uint32_t nslot = slot + 1u == static_cast<std::uint32_t>(kRing) ? 0u : slot + 1u;
-            if (k + 1u < steps) store_b(mine_next, nslot);  // slice k+1
+            if (k + 1u < steps) store_b(to_store, nslot);  // slice k+1
             __syncthreads();
             slot = nslot;
             ++k;
         };
         for (;;) {
-            step(r1, r0, a0, a1);
+            step(b0, b1, a0, a2);
             if (k >= steps) break;
-            step(r0, r1, a1, a0);
+            step(b1, b2, a1, a0);
+            if (k >= steps) break;
+            step(b2, b0, a2, a1);
             if (k >= steps) break;
         }
     }
