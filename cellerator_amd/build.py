@@ -33,6 +33,7 @@ ENGINE_SOURCES = [
     "cx_runtime.hip",
     "qcsr_spmm.hip",
     "qcsr_backward.hip",
+    "qcsr_parts.hip",
     "sort.hip",
     "bell_spmm.hip",
     "cpbp_reduce.hip",

@@ -1,0 +1,379 @@
+// qcsr_parts.hip -- quantized CSR SpMM with the weight panel streamed through LDS by gene
+// part (fp16 weights, N = 64, column-sorted rows).
+//
+// Same value semantics as qcsr_spmm.hip (decode fma(float(code), scale, offset), exact fp16
+// widening, fp32 products and sums); only the summation order differs, and it is fixed.
+//
+// Why: gathering a 128-byte weight row per nonzero through the texture path, plus an
+// 8-byte metadata gather per code, keeps the row-wave kernel far below HBM speed. LDS
+// serves the same 16-byte-per-lane gathers at about twice the rate, and the per-gene
+// metadata of a part sits beside its weight rows.
+//
+// Layout: one workgroup of kWaves waves per CU (LDS-bound) owns kWaves x kRw rows. A
+// prologue ranks the block's rows by length and deals them to the waves in snake order,
+// so every wave carries about the same number of nonzeros. The workgroup walks the genes in
+// parts of kPartGenes:
+//   * the part's fp16 weight rows (128 B each) and (scale, offset) pairs are copied into
+//     LDS by buffer loads that write LDS directly;
+//   * each wave then visits its rows in turn. Columns within a row are sorted, so the row's
+//     entries in the part are the run starting at the row's cursor. The wave keeps the next
+//     64 (gene, code) pairs of every row in one register (gene in the low 24 bits), decodes
+//     the run from the LDS metadata, stages (LDS offset of the weight row, value), and lets
+//     lane group g = lane / 8 take entry s + g while lane j = lane % 8 reads 16 B of that
+//     weight row and issues 8 v_fma_mix_f32 into the row's 8 partial sums;
+//   * after the visits of a part, every row window with fewer than kRefill entries left is
+//     refilled; those loads complete behind the next part's copy into LDS.
+// After the last part the 8 lane groups' partials of each row are reduce-scattered
+// (permlane32 swap, permlane16 swap, DPP row rotate), leaving one column per lane.
+// Rows whose cursor cannot advance (a column out of order across parts, or outside
+// [0, cols)) are recomputed at the end on a plain per-row path that skips columns outside
+// [0, cols); valid sorted input never takes it.
+#include "qcsr_common.hpp"
+
+namespace cx {
+namespace {
+
+constexpr int kPartGenes = 1024;                 // 128 KB of fp16 weight rows per part
+constexpr std::uint32_t kGeneMask = 0xffffffu;   // window register: gene | code << 24
+constexpr std::uint32_t kNoGene = kGeneMask;     // never inside a part
+constexpr std::uint32_t kNoRow = 0xffffffffu;
+constexpr int kRefill = 48;                      // refill a row's window below this many
+
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, std::uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), 0x00020000);
+}
+
+template<int kWaves, int kRw>
+struct PartsShared {
+    uint4 w[kPartGenes * 8];          // [gene][16-byte quarter-rows]: fp16 weights
+    float2 meta[kPartGenes];          // (scale, offset) per gene of the part
+    int2 stage[kWaves][kWave];        // per wave: (LDS byte offset of the row, value)
+    int len[kWaves * kRw];            // prologue: row lengths
+    std::uint32_t rows[kWaves * kRw]; // prologue: row of (wave, slot)
+};
+
+// Output column held by `lane` after reduce_scatter: 8 (lane % 8) + 4 bit3 + 2 bit4 + bit5.
+__device__ __forceinline__ int scatter_column(int lane) {
+    return 8 * (lane & 7) + 4 * ((lane >> 3) & 1) + 2 * ((lane >> 4) & 1) + ((lane >> 5) & 1);
+}
+
+// Sums the 8 lane groups' partials of columns 8 j + k (k < 8, j = lane % 8) and leaves
+// each lane with the total of scatter_column(lane).
+__device__ __forceinline__ float reduce_scatter(const float (&p)[8], int lane) {
+    float q[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        // lanes 32..63 of p[2m] trade places with lanes 0..31 of p[2m+1]
+        const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(p[2 * m]),
+                                                        __float_as_uint(p[2 * m + 1]), false, false);
+        q[m] = __uint_as_float(s[0]) + __uint_as_float(s[1]);  // bit5 = 0: slot 2m, 1: 2m+1
+    }
+    float r[2];
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+        const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(q[2 * n]),
+                                                        __float_as_uint(q[2 * n + 1]), false, false);
+        r[n] = __uint_as_float(s[0]) + __uint_as_float(s[1]);  // bit4 selects q[2n + bit4]
+    }
+    const bool hi = (lane & 8) != 0;
+    const float keep = hi ? r[1] : r[0];
+    const float send = hi ? r[0] : r[1];
+    // row_ror:8 inside each 16-lane row pairs lane l with l ^ 8
+    const float got = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), 0x128, 0xf, 0xf, false));
+    return keep + got;
+}
+
+// A row's register window: entries [base, base + 64) as the raw column index and the byte
+// holding the entry's code (`base` - `begin` is a multiple of the codes per byte, so lane
+// i's code sits at byte i / cpb, shift (i % cpb) * bits). Lanes past the row end are not
+// loaded; every reader bounds the lanes by the row end.
+struct Window {
+    std::uint32_t col;
+    std::uint32_t byte;
+};
+
+// `pb` is the packed byte of entry `base`; `entries` / `bytes` are the matrix totals. The
+// loads are buffer loads from descriptors built in scalar registers with a constant lane
+// offset, so they write the window registers directly (no address registers that would
+// have to wait for earlier loads), and the descriptor bounds stop them at the end of the
+// matrix arrays (those lanes read zeros; readers bound lanes by the row end anyway).
+template<int kBits>
+__device__ __forceinline__ void load_window(Window &w, const QcsrArgs &a, int base, int pb, int lane,
+                                            int entries, int bytes) {
+    constexpr int kCpb = 8 / kBits;
+    const int n = entries - base < kWave ? entries - base : kWave;
+    const int nb = bytes - pb < kWave / kCpb ? bytes - pb : kWave / kCpb;
+    const rsrc_t rc = make_rsrc(a.col_idx + base, static_cast<std::uint32_t>(n) * 4u);
+    const rsrc_t rp = make_rsrc(a.packed + pb, static_cast<std::uint32_t>(nb));
+    w.col = static_cast<std::uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rc, lane * 4, 0, 0));
+    w.byte = __builtin_amdgcn_raw_buffer_load_b8(rp, lane / kCpb, 0, 0);
+}
+
+using lds_ptr = __attribute__((address_space(3))) void *;
+
+// The weight rows and metadata of genes [lo, hi) into LDS. The weight rows go straight from
+// memory to LDS (buffer loads with the lds flag: wave instruction k of wave w fills 1 KB,
+// 8 rows, at no register cost); loads past the part's last row return zeros. Interleaved
+// (scale, offset) pairs go the same way; the other decode policies build their pairs in
+// registers.
+template<int kPolicy, int kWaves, typename Shared>
+__device__ __forceinline__ void load_part(Shared &sh, const QcsrArgs &a, int lo, int hi, int wave, int lane,
+                                          int tid) {
+    constexpr int kChunks = kPartGenes * 8 / kWave;  // 1 KB wave loads per part
+    static_assert(kChunks % kWaves == 0, "part chunks must divide among the waves");
+    const int span = hi - lo;
+    const std::uint32_t row_bytes = static_cast<std::uint32_t>(a.rhs_ld) * 2u;
+    const rsrc_t rw = make_rsrc(static_cast<const std::uint16_t *>(a.rhs) + static_cast<std::int64_t>(lo) * a.rhs_ld,
+                                static_cast<std::uint32_t>(span - 1) * row_bytes + 128u);
+#pragma unroll
+    for (int k = 0; k < kChunks / kWaves; ++k) {
+        const int chunk = k * kWaves + wave;
+        const int idx = chunk * kWave + lane;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rw, (lds_ptr)(&sh.w[chunk * kWave]), 16,
+            static_cast<std::uint32_t>(idx / 8) * row_bytes + static_cast<std::uint32_t>(idx % 8) * 16u, 0, 0, 0);
+    }
+    if constexpr (kPolicy == CX_DECODE_PER_GENE_AFFINE_PAIRS) {
+        constexpr int kMetaChunks = kPartGenes * 8 / (kWave * 16);  // 2 pairs per lane
+        if (wave < kMetaChunks) {
+            const rsrc_t rm = make_rsrc(reinterpret_cast<const float2 *>(a.scales) + lo,
+                                        static_cast<std::uint32_t>(span) * 8u);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_ptr)(&sh.meta[wave * 2 * kWave]), 16,
+                                                     static_cast<std::uint32_t>(wave * kWave + lane) * 16u, 0, 0, 0);
+        }
+    } else {
+        for (int g = tid; g < span; g += kWaves * kWave) {
+            float2 md;
+            md.x = a.scales != nullptr ? a.scales[lo + g] : 1.0f;
+            md.y = kPolicy == CX_DECODE_PER_GENE_AFFINE && a.offsets != nullptr ? a.offsets[lo + g] : 0.0f;
+            sh.meta[g] = md;
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the LDS writes of the loads above
+}
+
+__device__ __forceinline__ void fma8(float (&p)[8], float x, uint4 w) {
+    const std::uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        p[2 * k] = __builtin_fmaf(x, h2f(static_cast<std::uint16_t>(words[k] & 0xffffu)), p[2 * k]);
+        p[2 * k + 1] = __builtin_fmaf(x, h2f(static_cast<std::uint16_t>(words[k] >> 16)), p[2 * k + 1]);
+    }
+}
+
+// Plain per-row path for rows the part walk could not finish: lane c accumulates column
+// c over the row's entries in storage order; columns outside [0, cols) contribute nothing.
+template<int kBits, int kPolicy>
+__device__ float row_fallback(const QcsrArgs &a, std::uint32_t row, int lane) {
+    const std::int64_t begin = a.row_ptr[row], end = a.row_ptr[row + 1];
+    const std::uint8_t *pbase = a.packed + a.packed_row_ptr[row];
+    const float row_offset = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET && a.row_offsets != nullptr
+        ? a.row_offsets[row] : 0.0f;
+    const std::uint16_t *rhs = static_cast<const std::uint16_t *>(a.rhs);
+    float acc = 0.0f;
+    for (std::int64_t i = begin; i < end; ++i) {
+        const std::uint32_t col = static_cast<std::uint32_t>(a.col_idx[i]);
+        if (col >= a.cols) continue;
+        int c = 0;
+        const float x = load_entry<kBits, kPolicy, ValueMode::quantized>(a, i, begin, pbase, row_offset, c);
+        acc = __builtin_fmaf(x, h2f(rhs[static_cast<std::int64_t>(col) * a.rhs_ld + lane]), acc);
+    }
+    return acc;
+}
+
+template<int kBits, int kPolicy, int kWaves, int kRw>
+__global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_parts(QcsrArgs a) {
+    constexpr int kBlockRows = kWaves * kRw;
+    constexpr int kCpb = 8 / kBits;
+    static_assert(kBlockRows <= kWaves * kWave && kRw <= kWave, "bad part-kernel shape");
+    __shared__ PartsShared<kWaves, kRw> sh;
+    const int tid = static_cast<int>(threadIdx.x);
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
+    const int grp = lane >> 3;
+    const int j = lane & 7;
+    const std::uint32_t first = blockIdx.x * static_cast<std::uint32_t>(kBlockRows);
+    const std::uint32_t code_shift = static_cast<std::uint32_t>((lane % kCpb) * kBits);
+
+    // Balanced assignment: rank the block's rows by length (descending, ties by index) and
+    // deal rank r to slot r / kWaves of wave (r / kWaves even ? r % kWaves
+    // : kWaves - 1 - r % kWaves).
+    if (tid < kBlockRows) {
+        const std::uint32_t row = first + static_cast<std::uint32_t>(tid);
+        sh.len[tid] = row < a.rows ? a.row_ptr[row + 1] - a.row_ptr[row] : -1;
+    }
+    __syncthreads();
+    if (tid < kBlockRows) {
+        const int len = sh.len[tid];
+        int rank = 0;
+#pragma unroll 4
+        for (int u = 0; u < kBlockRows; ++u) {
+            const int lu = sh.len[u];
+            rank += lu > len || (lu == len && u < tid) ? 1 : 0;
+        }
+        const int round = rank / kWaves, pos = rank % kWaves;
+        const int w = (round & 1) != 0 ? kWaves - 1 - pos : pos;
+        const std::uint32_t row = first + static_cast<std::uint32_t>(tid);
+        sh.rows[w * kRw + round] = row < a.rows ? row : kNoRow;
+    }
+    __syncthreads();
+
+    // Matrix totals (window loads stop at them).
+    const int nnz = __builtin_amdgcn_readfirstlane(a.row_ptr[a.rows]);
+    const int nbytes = __builtin_amdgcn_readfirstlane(a.packed_row_ptr[a.rows]);
+
+    // Per-row state (wave-uniform, kept in scalar registers): cursor, end, window base,
+    // packed byte of the window base, row offset (column-scale/row-offset decode).
+    int cur[kRw], end[kRw], base[kRw], pb[kRw];
+    float roff[kRw];
+    float acc[kRw][8];
+    Window win[kRw];
+#pragma unroll
+    for (int rw = 0; rw < kRw; ++rw) {
+        const std::uint32_t row = __builtin_amdgcn_readfirstlane(sh.rows[wave * kRw + rw]);
+        cur[rw] = end[rw] = pb[rw] = 0;
+        roff[rw] = 0.0f;
+        if (row != kNoRow) {
+            cur[rw] = __builtin_amdgcn_readfirstlane(a.row_ptr[row]);
+            end[rw] = __builtin_amdgcn_readfirstlane(a.row_ptr[row + 1]);
+            pb[rw] = __builtin_amdgcn_readfirstlane(a.packed_row_ptr[row]);
+            if constexpr (kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET)
+                roff[rw] = a.row_offsets != nullptr
+                    ? __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(a.row_offsets[row])))
+                    : 0.0f;
+        }
+        base[rw] = cur[rw];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[rw][k] = 0.0f;
+        win[rw].col = kNoGene;
+        win[rw].byte = 0u;
+        if (cur[rw] < end[rw]) load_window<kBits>(win[rw], a, base[rw], pb[rw], lane, nnz, nbytes);
+    }
+
+    const int cols = static_cast<int>(a.cols);
+    const int parts = (cols + kPartGenes - 1) / kPartGenes;
+    for (int part = 0; part < parts; ++part) {
+        const int lo = part * kPartGenes;
+        const int hi = lo + kPartGenes < cols ? lo + kPartGenes : cols;
+        const std::uint32_t span = static_cast<std::uint32_t>(hi - lo);
+        __syncthreads();  // every wave is done reading part - 1
+        load_part<kPolicy, kWaves>(sh, a, lo, hi, wave, lane, tid);  // also completes the refills
+        __syncthreads();
+#pragma unroll
+        for (int rw = 0; rw < kRw; ++rw) {
+            if (cur[rw] >= end[rw]) continue;
+            for (;;) {
+                const int start = cur[rw] - base[rw];  // 0 <= start < 64
+                const int lim = end[rw] - base[rw];    // lanes >= lim are past the row end
+                const std::uint32_t g = win[rw].col - static_cast<std::uint32_t>(lo);
+                const bool in = lane >= start && lane < lim && g < span;
+                const std::uint64_t run = ~(__builtin_amdgcn_ballot_w64(in) >> start);
+                const int cnt = run == 0u ? kWave - start : __builtin_ctzll(run);
+                if (cnt == 0) break;
+                const int stop = start + cnt;
+                if (lane >= start && lane < stop) {
+                    const float2 md = sh.meta[g];
+                    const float code = static_cast<float>((win[rw].byte >> code_shift) & ((1u << kBits) - 1u));
+                    const float off = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET ? roff[rw] : md.y;
+                    sh.stage[wave][lane] = make_int2(static_cast<int>(g) * 128,
+                                                     __float_as_int(__builtin_fmaf(code, md.x, off)));
+                }
+                wave_sync();
+                const char *wbase = reinterpret_cast<const char *>(sh.w) + j * 16;
+                int s = start;
+                for (; s + 16 <= stop; s += 16) {  // two steps in flight
+                    const int2 e0 = sh.stage[wave][s + grp];
+                    const int2 e1 = sh.stage[wave][s + 8 + grp];
+                    const uint4 w0 = *reinterpret_cast<const uint4 *>(wbase + e0.x);
+                    const uint4 w1 = *reinterpret_cast<const uint4 *>(wbase + e1.x);
+                    fma8(acc[rw], __int_as_float(e0.y), w0);
+                    fma8(acc[rw], __int_as_float(e1.y), w1);
+                }
+                if (s + 8 <= stop) {
+                    const int2 e = sh.stage[wave][s + grp];
+                    fma8(acc[rw], __int_as_float(e.y), *reinterpret_cast<const uint4 *>(wbase + e.x));
+                    s += 8;
+                }
+                if (s + grp < stop) {
+                    const int2 e = sh.stage[wave][s + grp];
+                    fma8(acc[rw], __int_as_float(e.y), *reinterpret_cast<const uint4 *>(wbase + e.x));
+                }
+                wave_sync();
+                cur[rw] += cnt;
+                if (cur[rw] - base[rw] < kWave || cur[rw] >= end[rw]) break;
+                // window used up inside the part: load the next 64 entries now
+                base[rw] = cur[rw];
+                pb[rw] += kWave / kCpb;
+                load_window<kBits>(win[rw], a, base[rw], pb[rw], lane, nnz, nbytes);
+            }
+        }
+        // Refill the windows that are running low for the next part (from the cursor rounded
+        // down to a code byte). Issued after all visits, the loads write the window registers
+        // directly and complete behind the next part's copy into LDS.
+#pragma unroll
+        for (int rw = 0; rw < kRw; ++rw) {
+            if (base[rw] + kWave < end[rw] && base[rw] + kWave - cur[rw] < kRefill) {
+                const int step = (cur[rw] - base[rw]) / kCpb;
+                base[rw] += step * kCpb;
+                pb[rw] += step;
+                load_window<kBits>(win[rw], a, base[rw], pb[rw], lane, nnz, nbytes);
+            }
+        }
+    }
+
+    const int col = scatter_column(lane);
+#pragma unroll
+    for (int rw = 0; rw < kRw; ++rw) {
+        const std::uint32_t row = __builtin_amdgcn_readfirstlane(sh.rows[wave * kRw + rw]);
+        if (row == kNoRow) continue;
+        if (cur[rw] < end[rw]) {
+            // unfinished: recompute the row on the plain path (lane = column)
+            const float v = row_fallback<kBits, kPolicy>(a, row, lane);
+            a.out[static_cast<std::int64_t>(row) * a.out_ld + lane] = a.ep.active ? epilogue_value(a.ep, v, row, lane) : v;
+            continue;
+        }
+        const float v = reduce_scatter(acc[rw], lane);
+        a.out[static_cast<std::int64_t>(row) * a.out_ld + col] = a.ep.active ? epilogue_value(a.ep, v, row, col) : v;
+    }
+}
+
+template<int kBits, int kPolicy>
+int launch_bits_parts(const QcsrArgs &a, hipStream_t stream) {
+    constexpr int kWaves = 16, kRw = 8;
+    const unsigned rows_per_block = kWaves * kRw;
+    const dim3 grid((a.rows + rows_per_block - 1) / rows_per_block), block(kWaves * kWave);
+    hipLaunchKernelGGL((qcsr_spmm_parts<kBits, kPolicy, kWaves, kRw>), grid, block, 0, stream, a);
+    return check_launch("qcsr_spmm_parts");
+}
+
+template<int kPolicy>
+int launch_policy_parts(const QcsrArgs &a, std::uint32_t bits, hipStream_t stream) {
+    switch (bits) {
+    case 1: return launch_bits_parts<1, kPolicy>(a, stream);
+    case 2: return launch_bits_parts<2, kPolicy>(a, stream);
+    case 4: return launch_bits_parts<4, kPolicy>(a, stream);
+    default: return launch_bits_parts<8, kPolicy>(a, stream);
+    }
+}
+
+} // namespace
+
+bool qcsr_parts_applicable(const QcsrArgs &a, std::uint32_t bits, std::uint32_t rhs_dtype,
+                           std::int64_t out_cols, bool aligned) {
+    return bits != 0u && rhs_dtype == CELLERATOR_DTYPE_F16 && out_cols == 64 && aligned
+        && a.cols < kGeneMask && a.rows > 0u && a.cols > 0u
+        && a.rhs_ld <= (INT32_MAX / 2) / kPartGenes;
+}
+
+int launch_qcsr_parts(const QcsrArgs &a, std::uint32_t bits, std::uint32_t policy, hipStream_t stream) {
+    if (policy == CX_DECODE_PER_GENE_AFFINE_PAIRS)
+        return launch_policy_parts<CX_DECODE_PER_GENE_AFFINE_PAIRS>(a, bits, stream);
+    if (policy == CX_DECODE_PER_GENE_AFFINE)
+        return launch_policy_parts<CX_DECODE_PER_GENE_AFFINE>(a, bits, stream);
+    return launch_policy_parts<CX_DECODE_COLUMN_SCALE_ROW_OFFSET>(a, bits, stream);
+}
+
+} // namespace cx

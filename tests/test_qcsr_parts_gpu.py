@@ -1,0 +1,168 @@
+"""GPU parity of the gene-part quantized CSR kernel (qcsr_parts.hip).
+
+cx_qcsr_spmm_fwd takes this kernel for quantized codes with fp16 weights and N = 64: the
+weight panel is streamed through LDS in parts of 1,024 genes, each row keeps a cursor, and
+rows the part walk cannot finish (columns out of order across parts, or outside
+[0, cols)) are recomputed on a plain per-row path. These cases pin each of those paths
+against the float64 referee on the same inputs: many parts, rows longer than a 64-entry
+window inside one part, skewed row lengths across workgroups (the balanced row
+assignment), unsorted and duplicated columns, and out-of-range columns (which contribute
+nothing on this path).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests.helpers import check_against_referee, quantized_fixture, to_device_qcsr
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(m, rhs_np):
+    import torch
+
+    from cellerator_amd import qcsr_spmm
+    out = qcsr_spmm(m, torch.from_numpy(rhs_np).cuda())
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def _referee(oracle, fx, rhs):
+    return oracle.qcsr_spmm_referee(fx["bits"], fx["policy"], fx["rows"], fx["cols"], fx["row_ptr"],
+                                    fx["packed_row_ptr"], fx["col_idx"], fx["packed"], fx["scales"],
+                                    fx["offsets"], fx["row_offsets"], rhs)
+
+
+def _skewed_fixture(oracle, rng, rows, cols, bits, policy):
+    """Row lengths from 0 to several thousand (a few rows span every part, several rows
+    are empty), sorted unique columns."""
+    fx = quantized_fixture(oracle, rng, rows, cols, 10.0, bits, policy)
+    lengths = np.minimum(rng.lognormal(np.log(400.0), 1.1, rows).astype(np.int64), cols)
+    lengths[rng.choice(rows, rows // 15, replace=False)] = 0
+    lengths[rng.choice(rows, 3, replace=False)] = cols  # dense rows: every gene
+    row_ptr = np.zeros(rows + 1, np.int64)
+    row_ptr[1:] = np.cumsum(lengths)
+    col_idx = np.empty(int(row_ptr[-1]), np.int32)
+    for r in range(rows):
+        if lengths[r]:
+            col_idx[row_ptr[r]:row_ptr[r + 1]] = np.sort(rng.choice(cols, lengths[r], replace=False))
+    return _rebuild(oracle, rng, fx, row_ptr.astype(np.int32), col_idx)
+
+
+def _rebuild(oracle, rng, fx, row_ptr, col_idx):
+    """Same metadata, new structure: fresh codes packed by the oracle."""
+    bits, policy, rows = fx["bits"], fx["policy"], fx["rows"]
+    codes = rng.integers(0, (1 << bits), len(col_idx))
+    if policy == oracle.PER_GENE_AFFINE:
+        values = (fx["offsets"][col_idx] + fx["scales"][col_idx] * codes).astype(np.float32)
+    else:
+        row_of = np.repeat(np.arange(rows), np.diff(row_ptr))
+        values = (fx["row_offsets"][row_of] + fx["scales"][col_idx] * codes).astype(np.float32)
+    packed_row_ptr = oracle.build_packed_row_ptr(bits, row_ptr)
+    packed = oracle.pack_csr(bits, policy, row_ptr, packed_row_ptr, col_idx, values, fx["scales"],
+                             fx["offsets"], fx["row_offsets"])
+    return dict(fx, row_ptr=row_ptr, col_idx=col_idx, packed_row_ptr=packed_row_ptr, packed=packed)
+
+
+@pytest.mark.parametrize("bits,policy", [(4, 1), (8, 1), (2, 2), (1, 1)])
+def test_many_parts_skewed_rows(oracle, bits, policy):
+    """5 parts (the last one partial), 3 workgroups of 128 rows plus a ragged one, rows from
+    empty to all 4,700 genes (windows refilled inside a part)."""
+    rng = np.random.default_rng(900 + bits * 10 + policy)
+    fx = _skewed_fixture(oracle, rng, 400, 4700, bits, policy)
+    rhs = (rng.standard_normal((4700, 64)) * 0.02).astype(np.float16)
+    ref, mag = _referee(oracle, fx, rhs)
+    check_against_referee(oracle, ref, mag, _run(to_device_qcsr(fx), rhs))
+
+
+def test_interleaved_pairs_through_parts(oracle):
+    """The pairs policy copies (scale, offset) into LDS by direct loads: equal bitwise to
+    the separate arrays across several parts."""
+    import torch
+
+    from cellerator_amd import qcsr_pack_gene_affine, qcsr_spmm
+    rng = np.random.default_rng(931)
+    fx = _skewed_fixture(oracle, rng, 300, 3100, 4, oracle.PER_GENE_AFFINE)
+    m = to_device_qcsr(fx)
+    rhs = torch.from_numpy((rng.standard_normal((3100, 64)) * 0.02).astype(np.float16)).cuda()
+    a = qcsr_spmm(m, rhs)
+    b = qcsr_spmm(qcsr_pack_gene_affine(m), rhs)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    ref, mag = _referee(oracle, fx, rhs.cpu().numpy())
+    check_against_referee(oracle, ref, mag, a.cpu().numpy())
+
+
+def test_unsorted_and_duplicate_columns(oracle):
+    """Rows whose columns go back across a part boundary take the per-row path; columns out
+    of order inside one part and repeated columns stay on the part walk. Every row must
+    match the referee, which sums entries in storage order."""
+    rng = np.random.default_rng(947)
+    fx = _skewed_fixture(oracle, rng, 260, 3000, 4, 1)
+    row_ptr, col_idx = fx["row_ptr"], fx["col_idx"].copy()
+    for r in range(0, 260, 3):  # reverse every third row: out of order across parts
+        s, e = row_ptr[r], row_ptr[r + 1]
+        col_idx[s:e] = col_idx[s:e][::-1]
+    for r in range(1, 260, 7):  # swap neighbours inside a part, duplicate a column
+        s, e = row_ptr[r], row_ptr[r + 1]
+        seg = col_idx[s:e]
+        inside = [i for i in range(len(seg) - 1) if seg[i] // 1024 == seg[i + 1] // 1024]
+        if inside:
+            i = inside[len(inside) // 2]
+            seg[i], seg[i + 1] = seg[i + 1], seg[i]
+        if len(seg) > 2:
+            seg[-1] = seg[-2]
+    fx = _rebuild(oracle, rng, fx, row_ptr, col_idx)
+    rhs = (rng.standard_normal((3000, 64)) * 0.02).astype(np.float16)
+    ref, mag = _referee(oracle, fx, rhs)
+    check_against_referee(oracle, ref, mag, _run(to_device_qcsr(fx), rhs))
+
+
+def test_out_of_range_columns_contribute_nothing(oracle):
+    """Columns >= cols or negative are skipped on this path. The expected output is the
+    referee's on one extra gene whose weight row is zero, with those entries pointed at it."""
+    rng = np.random.default_rng(953)
+    cols = 2100
+    fx = _skewed_fixture(oracle, rng, 200, cols, 4, 1)
+    col_idx = fx["col_idx"].copy()
+    bad = rng.choice(len(col_idx), 40, replace=False)
+    col_idx[bad[:20]] = cols + 5
+    col_idx[bad[20:]] = -3
+    rhs = (rng.standard_normal((cols, 64)) * 0.02).astype(np.float16)
+    # device matrix: the out-of-range columns as they are
+    dev = dict(fx, col_idx=col_idx)
+    got = _run(to_device_qcsr(dev), rhs)
+    # referee: cols + 1 genes, the bad entries on gene `cols` whose weight row is zero
+    ref_cols = col_idx.copy()
+    ref_cols[bad] = cols
+    ext = dict(fx, cols=cols + 1, col_idx=ref_cols,
+               scales=np.append(fx["scales"], np.float32(0.25)),
+               offsets=np.append(fx["offsets"], np.float32(0.0)))
+    rhs_ext = np.vstack([rhs, np.zeros((1, 64), np.float16)])
+    ref, mag = _referee(oracle, ext, rhs_ext)
+    check_against_referee(oracle, ref, mag, got)
+
+
+def test_generated_c3_rows_with_epilogue(oracle):
+    """GPU-generated C3-distributed rows (33,538 genes: 33 parts) through the part walk with
+    a fused bias + ReLU epilogue, against the referee followed by the same epilogue."""
+    import torch
+
+    from cellerator_amd import Epilogue, qcsr_pack_gene_affine, qcsr_spmm
+    from cellerator_amd._native import EPILOGUE_BIAS_RELU
+    from cellerator_amd.synth import C3, dense_normal, generate_qcsr
+    from tests.helpers import qcsr_to_host
+    m = generate_qcsr(C3.scaled(700))
+    w = dense_normal((m.cols, 64), 0.02, torch.float16, seed=C3.seed + 1)
+    bias = torch.linspace(-0.05, 0.05, 64, device="cuda", dtype=torch.float32)
+    out = qcsr_spmm(qcsr_pack_gene_affine(m), w, epilogue=Epilogue(kind=EPILOGUE_BIAS_RELU, bias=bias))
+    torch.cuda.synchronize()
+    h = qcsr_to_host(m)
+    ref, mag = oracle.qcsr_spmm_referee(4, 1, m.rows, m.cols, h["row_ptr"], h["packed_row_ptr"],
+                                        h["col_idx"], h["packed"], h["scales"], h["offsets"], None,
+                                        w.cpu().numpy())
+    expect = np.maximum(ref.reshape(m.rows, 64) + bias.cpu().numpy().astype(np.float64), 0.0)
+    got = out.cpu().numpy().astype(np.float64)
+    tol = 1e-4 * np.abs(expect) + 1e-4 * mag.reshape(m.rows, 64)  # the suite's bound
+    assert np.all(np.abs(got - expect) <= tol)
