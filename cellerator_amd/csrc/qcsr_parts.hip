@@ -50,7 +50,7 @@ template<int kWaves, int kRw>
 struct PartsShared {
     uint4 w[kPartGenes * 8];          // [gene][16-byte quarter-rows]: fp16 weights
     float2 meta[kPartGenes];          // (scale, offset) per gene of the part
-    int2 stage[kWaves][kWave];        // per wave: (LDS byte offset of the row, value)
+    int2 stage[kWaves][2][kWave];     // per wave, two rows: (LDS byte offset of the row, value)
     int len[kWaves * kRw];            // prologue: row lengths
     std::uint32_t rows[kWaves * kRw]; // prologue: row of (wave, slot)
 };
@@ -104,10 +104,12 @@ template<int kBits>
 __device__ __forceinline__ void load_window(Window &w, const QcsrArgs &a, int base, int pb, int lane,
                                             int entries, int bytes) {
     constexpr int kCpb = 8 / kBits;
-    const int n = entries - base < kWave ? entries - base : kWave;
-    const int nb = bytes - pb < kWave / kCpb ? bytes - pb : kWave / kCpb;
-    const rsrc_t rc = make_rsrc(a.col_idx + base, static_cast<std::uint32_t>(n) * 4u);
-    const rsrc_t rp = make_rsrc(a.packed + pb, static_cast<std::uint32_t>(nb));
+    const std::uint32_t ub = static_cast<std::uint32_t>(base), upb = static_cast<std::uint32_t>(pb);
+    const std::uint32_t n = static_cast<std::uint32_t>(entries) - ub < kWave ? static_cast<std::uint32_t>(entries) - ub : kWave;
+    const std::uint32_t nb = static_cast<std::uint32_t>(bytes) - upb < kWave / kCpb
+        ? static_cast<std::uint32_t>(bytes) - upb : kWave / kCpb;
+    const rsrc_t rc = make_rsrc(a.col_idx + ub, n * 4u);
+    const rsrc_t rp = make_rsrc(a.packed + upb, nb);
     w.col = static_cast<std::uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rc, lane * 4, 0, 0));
     w.byte = __builtin_amdgcn_raw_buffer_load_b8(rp, lane / kCpb, 0, 0);
 }
@@ -188,10 +190,10 @@ template<int kBits, int kPolicy, int kWaves, int kRw>
 __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_parts(QcsrArgs a) {
     constexpr int kBlockRows = kWaves * kRw;
     constexpr int kCpb = 8 / kBits;
-    static_assert(kBlockRows <= kWaves * kWave && kRw <= kWave, "bad part-kernel shape");
+    static_assert(kBlockRows <= kWaves * kWave && kRw <= kWave && kRw % 2 == 0, "bad part-kernel shape");
     __shared__ PartsShared<kWaves, kRw> sh;
     const int tid = static_cast<int>(threadIdx.x);
-    const int wave = tid / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int lane = tid % kWave;
     const int grp = lane >> 3;
     const int j = lane & 7;
@@ -253,6 +255,72 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_parts(QcsrArgs a) {
         if (cur[rw] < end[rw]) load_window<kBits>(win[rw], a, base[rw], pb[rw], lane, nnz, nbytes);
     }
 
+    const char *wbase = reinterpret_cast<const char *>(sh.w) + j * 16;
+
+    // Run of row rw's window lanes from the cursor whose genes lie in [lo, lo + span), cut
+    // at the row end: window lanes [start, start + cnt); g = gene - lo per lane.
+    auto segment = [&](int rw, int lo, std::uint32_t span, int &start, int &cnt, std::uint32_t &g) {
+        start = cur[rw] - base[rw];  // 0 <= start < 64
+        g = win[rw].col - static_cast<std::uint32_t>(lo);
+        const std::uint64_t run = ~(__builtin_amdgcn_ballot_w64(g < span) >> start);
+        const int in_run = run == 0u ? kWave - start : __builtin_ctzll(run);
+        cnt = in_run < end[rw] - cur[rw] ? in_run : end[rw] - cur[rw];
+    };
+    // Decodes the run into stage slot `slot`: (LDS byte offset of the weight row, value).
+    auto decode = [&](int rw, int slot, int start, int cnt, std::uint32_t g) {
+        if (static_cast<std::uint32_t>(lane - start) < static_cast<std::uint32_t>(cnt)) {
+            const float2 md = sh.meta[g];
+            const float code = static_cast<float>((win[rw].byte >> code_shift) & ((1u << kBits) - 1u));
+            const float off = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET ? roff[rw] : md.y;
+            sh.stage[wave][slot][lane] = make_int2(static_cast<int>(g) * 128,
+                                                   __float_as_int(__builtin_fmaf(code, md.x, off)));
+        }
+    };
+    // `pairs` two-entry steps from ep, then the run's last cnt % 16 entries: lane group grp
+    // takes staged entry s + grp, lane j reads 16 B of its weight row.
+    auto steps = [&](int rw, const int2 *ep, int pairs, int cnt) {
+        for (int k = pairs; k > 0; --k, ep += 16) {
+            const int2 e0 = ep[0], e1 = ep[8];
+            const uint4 w0 = *reinterpret_cast<const uint4 *>(wbase + e0.x);
+            const uint4 w1 = *reinterpret_cast<const uint4 *>(wbase + e1.x);
+            fma8(acc[rw], __int_as_float(e0.y), w0);
+            fma8(acc[rw], __int_as_float(e1.y), w1);
+        }
+        if ((cnt & 8) != 0) {
+            const int2 e = ep[0];
+            fma8(acc[rw], __int_as_float(e.y), *reinterpret_cast<const uint4 *>(wbase + e.x));
+            ep += 8;
+        }
+        if (grp < (cnt & 7)) {
+            const int2 e = ep[0];
+            fma8(acc[rw], __int_as_float(e.y), *reinterpret_cast<const uint4 *>(wbase + e.x));
+        }
+    };
+    // Moves row rw's cursor past a run ending at window lane `stop`; when the run used the
+    // window up inside the part, loads the next 64 entries and returns true.
+    auto advance = [&](int rw, int stop, int cnt) -> bool {
+        cur[rw] += cnt;
+        if (stop < kWave || cur[rw] >= end[rw]) return false;
+        base[rw] = cur[rw];
+        pb[rw] += kWave / kCpb;
+        load_window<kBits>(win[rw], a, base[rw], pb[rw], lane, nnz, nbytes);
+        return true;
+    };
+    // The rest of row rw's part after a window reload, one row at a time.
+    auto visit_rest = [&](int rw, int lo, std::uint32_t span) {
+        for (;;) {
+            int start, cnt;
+            std::uint32_t g;
+            segment(rw, lo, span, start, cnt, g);
+            if (cnt == 0) return;
+            decode(rw, 0, start, cnt, g);
+            wave_sync();
+            steps(rw, &sh.stage[wave][0][start + grp], cnt >> 4, cnt);
+            wave_sync();
+            if (!advance(rw, start + cnt, cnt)) return;
+        }
+    };
+
     const int cols = static_cast<int>(a.cols);
     const int parts = (cols + kPartGenes - 1) / kPartGenes;
     for (int part = 0; part < parts; ++part) {
@@ -262,53 +330,39 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_parts(QcsrArgs a) {
         __syncthreads();  // every wave is done reading part - 1
         load_part<kPolicy, kWaves>(sh, a, lo, hi, wave, lane, tid);  // also completes the refills
         __syncthreads();
+        // Rows are visited in pairs so two independent decode / step chains are in flight.
 #pragma unroll
-        for (int rw = 0; rw < kRw; ++rw) {
-            if (cur[rw] >= end[rw]) continue;
-            for (;;) {
-                const int start = cur[rw] - base[rw];  // 0 <= start < 64
-                const int lim = end[rw] - base[rw];    // lanes >= lim are past the row end
-                const std::uint32_t g = win[rw].col - static_cast<std::uint32_t>(lo);
-                const bool in = lane >= start && lane < lim && g < span;
-                const std::uint64_t run = ~(__builtin_amdgcn_ballot_w64(in) >> start);
-                const int cnt = run == 0u ? kWave - start : __builtin_ctzll(run);
-                if (cnt == 0) break;
-                const int stop = start + cnt;
-                if (lane >= start && lane < stop) {
-                    const float2 md = sh.meta[g];
-                    const float code = static_cast<float>((win[rw].byte >> code_shift) & ((1u << kBits) - 1u));
-                    const float off = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET ? roff[rw] : md.y;
-                    sh.stage[wave][lane] = make_int2(static_cast<int>(g) * 128,
-                                                     __float_as_int(__builtin_fmaf(code, md.x, off)));
-                }
-                wave_sync();
-                const char *wbase = reinterpret_cast<const char *>(sh.w) + j * 16;
-                int s = start;
-                for (; s + 16 <= stop; s += 16) {  // two steps in flight
-                    const int2 e0 = sh.stage[wave][s + grp];
-                    const int2 e1 = sh.stage[wave][s + 8 + grp];
-                    const uint4 w0 = *reinterpret_cast<const uint4 *>(wbase + e0.x);
-                    const uint4 w1 = *reinterpret_cast<const uint4 *>(wbase + e1.x);
-                    fma8(acc[rw], __int_as_float(e0.y), w0);
-                    fma8(acc[rw], __int_as_float(e1.y), w1);
-                }
-                if (s + 8 <= stop) {
-                    const int2 e = sh.stage[wave][s + grp];
-                    fma8(acc[rw], __int_as_float(e.y), *reinterpret_cast<const uint4 *>(wbase + e.x));
-                    s += 8;
-                }
-                if (s + grp < stop) {
-                    const int2 e = sh.stage[wave][s + grp];
-                    fma8(acc[rw], __int_as_float(e.y), *reinterpret_cast<const uint4 *>(wbase + e.x));
-                }
-                wave_sync();
-                cur[rw] += cnt;
-                if (cur[rw] - base[rw] < kWave || cur[rw] >= end[rw]) break;
-                // window used up inside the part: load the next 64 entries now
-                base[rw] = cur[rw];
-                pb[rw] += kWave / kCpb;
-                load_window<kBits>(win[rw], a, base[rw], pb[rw], lane, nnz, nbytes);
+        for (int ra = 0; ra < kRw; ra += 2) {
+            const int rb = ra + 1;
+            int sa = 0, ca = 0, sb = 0, cb = 0;
+            std::uint32_t ga = 0u, gb = 0u;
+            if (cur[ra] < end[ra]) segment(ra, lo, span, sa, ca, ga);
+            if (cur[rb] < end[rb]) segment(rb, lo, span, sb, cb, gb);
+            decode(ra, 0, sa, ca, ga);
+            decode(rb, 1, sb, cb, gb);
+            wave_sync();
+            const int2 *epa = &sh.stage[wave][0][sa + grp];
+            const int2 *epb = &sh.stage[wave][1][sb + grp];
+            const int ka = ca >> 4, kb = cb >> 4;
+            const int kk = ka < kb ? ka : kb;
+            for (int k = kk; k > 0; --k, epa += 16, epb += 16) {
+                const int2 a0 = epa[0], a1 = epa[8], b0 = epb[0], b1 = epb[8];
+                const uint4 wa0 = *reinterpret_cast<const uint4 *>(wbase + a0.x);
+                const uint4 wa1 = *reinterpret_cast<const uint4 *>(wbase + a1.x);
+                const uint4 wb0 = *reinterpret_cast<const uint4 *>(wbase + b0.x);
+                const uint4 wb1 = *reinterpret_cast<const uint4 *>(wbase + b1.x);
+                fma8(acc[ra], __int_as_float(a0.y), wa0);
+                fma8(acc[rb], __int_as_float(b0.y), wb0);
+                fma8(acc[ra], __int_as_float(a1.y), wa1);
+                fma8(acc[rb], __int_as_float(b1.y), wb1);
             }
+            steps(ra, epa, ka - kk, ca);
+            steps(rb, epb, kb - kk, cb);
+            wave_sync();
+            const bool more_a = ca > 0 && advance(ra, sa + ca, ca);
+            const bool more_b = cb > 0 && advance(rb, sb + cb, cb);
+            if (more_a) visit_rest(ra, lo, span);
+            if (more_b) visit_rest(rb, lo, span);
         }
         // Refill the windows that are running low for the next part (from the cursor rounded
         // down to a code byte). Issued after all visits, the loads write the window registers
