@@ -21,8 +21,8 @@
 //     the run from the LDS metadata, stages (LDS offset of the weight row, value), and lets
 //     lane group g = lane / 8 take entry s + g while lane j = lane % 8 reads 16 B of that
 //     weight row and issues 8 v_fma_mix_f32 into the row's 8 partial sums;
-//   * after the visits of a part, every row window with fewer than kRefill entries left is
-//     refilled; those loads complete behind the next part's copy into LDS.
+//   * right after a pair's visits, each row window with fewer than kRefill entries left is
+//     refilled; those loads complete behind the rest of the part.
 // After the last part the 8 lane groups' partials of each row are reduce-scattered
 // (permlane32 swap, permlane16 swap, DPP row rotate), leaving one column per lane.
 // Rows whose cursor cannot advance (a column out of order across parts, or outside
@@ -321,6 +321,18 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_parts(QcsrArgs a) {
         }
     };
 
+    // Refills row rw's window for the next part when fewer than kRefill entries are left
+    // (from the cursor rounded down to a code byte). Issued right after the row's visit, the
+    // loads write the window registers directly and complete behind the rest of the part.
+    auto refill = [&](int rw) {
+        if (base[rw] + kWave < end[rw] && base[rw] + kWave - cur[rw] < kRefill) {
+            const int step = (cur[rw] - base[rw]) / kCpb;
+            base[rw] += step * kCpb;
+            pb[rw] += step;
+            load_window<kBits>(win[rw], a, base[rw], pb[rw], lane, nnz, nbytes);
+        }
+    };
+
     const int cols = static_cast<int>(a.cols);
     const int parts = (cols + kPartGenes - 1) / kPartGenes;
     for (int part = 0; part < parts; ++part) {
@@ -363,18 +375,8 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_parts(QcsrArgs a) {
             const bool more_b = cb > 0 && advance(rb, sb + cb, cb);
             if (more_a) visit_rest(ra, lo, span);
             if (more_b) visit_rest(rb, lo, span);
-        }
-        // Refill the windows that are running low for the next part (from the cursor rounded
-        // down to a code byte). Issued after all visits, the loads write the window registers
-        // directly and complete behind the next part's copy into LDS.
-#pragma unroll
-        for (int rw = 0; rw < kRw; ++rw) {
-            if (base[rw] + kWave < end[rw] && base[rw] + kWave - cur[rw] < kRefill) {
-                const int step = (cur[rw] - base[rw]) / kCpb;
-                base[rw] += step * kCpb;
-                pb[rw] += step;
-                load_window<kBits>(win[rw], a, base[rw], pb[rw], lane, nnz, nbytes);
-            }
+            refill(ra);
+            refill(rb);
         }
     }
 
