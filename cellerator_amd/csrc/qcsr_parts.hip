@@ -1,5 +1,5 @@
 // qcsr_parts.hip -- quantized CSR SpMM with the weight panel streamed through LDS by gene
-// part (fp16 weights, N = 64, column-sorted rows).
+// part (fp16 weights, N a multiple of 64 in blocks of 64 columns, column-sorted rows).
 //
 // Same value semantics as qcsr_spmm.hip (decode fma(float(code), scale, offset), exact fp16
 // widening, fp32 products and sums); only the summation order differs, and it is fixed.
@@ -419,17 +419,31 @@ int launch_policy_parts(const QcsrArgs &a, std::uint32_t bits, hipStream_t strea
 
 bool qcsr_parts_applicable(const QcsrArgs &a, std::uint32_t bits, std::uint32_t rhs_dtype,
                            std::int64_t out_cols, bool aligned) {
-    return bits != 0u && rhs_dtype == CELLERATOR_DTYPE_F16 && out_cols == 64 && aligned
-        && a.cols < kGeneMask && a.rows > 0u && a.cols > 0u
+    return bits != 0u && rhs_dtype == CELLERATOR_DTYPE_F16 && out_cols > 0 && out_cols % 64 == 0
+        && out_cols <= 256 && aligned && a.cols < kGeneMask && a.rows > 0u && a.cols > 0u
         && a.rhs_ld <= (INT32_MAX / 2) / kPartGenes;
 }
 
-int launch_qcsr_parts(const QcsrArgs &a, std::uint32_t bits, std::uint32_t policy, hipStream_t stream) {
-    if (policy == CX_DECODE_PER_GENE_AFFINE_PAIRS)
-        return launch_policy_parts<CX_DECODE_PER_GENE_AFFINE_PAIRS>(a, bits, stream);
-    if (policy == CX_DECODE_PER_GENE_AFFINE)
-        return launch_policy_parts<CX_DECODE_PER_GENE_AFFINE>(a, bits, stream);
-    return launch_policy_parts<CX_DECODE_COLUMN_SCALE_ROW_OFFSET>(a, bits, stream);
+// N = 64 c columns: one launch per 64-column block of the weights and the output (and of
+// the epilogue's bias and initial values).
+int launch_qcsr_parts(const QcsrArgs &a, std::uint32_t bits, std::uint32_t policy, std::int64_t out_cols,
+                      hipStream_t stream) {
+    for (std::int64_t c0 = 0; c0 < out_cols; c0 += 64) {
+        QcsrArgs b = a;
+        b.rhs = static_cast<const std::uint16_t *>(a.rhs) + c0;
+        b.out = a.out + c0;
+        if (b.ep.bias != nullptr) b.ep.bias += c0;
+        if (b.ep.initial != nullptr) b.ep.initial += c0;
+        int rc;
+        if (policy == CX_DECODE_PER_GENE_AFFINE_PAIRS)
+            rc = launch_policy_parts<CX_DECODE_PER_GENE_AFFINE_PAIRS>(b, bits, stream);
+        else if (policy == CX_DECODE_PER_GENE_AFFINE)
+            rc = launch_policy_parts<CX_DECODE_PER_GENE_AFFINE>(b, bits, stream);
+        else
+            rc = launch_policy_parts<CX_DECODE_COLUMN_SCALE_ROW_OFFSET>(b, bits, stream);
+        if (rc != CX_STATUS_SUCCESS) return rc;
+    }
+    return CX_STATUS_SUCCESS;
 }
 
 } // namespace cx

@@ -471,7 +471,7 @@ int qcsr_forward(const cx_qcsr_matrix *m, const void *rhs, std::uint32_t rhs_dty
         bal = &balance;
     }
     if (bal == nullptr && qcsr_parts_applicable(a, m->bits, rhs_dtype, out_cols, aligned))
-        return launch_qcsr_parts(a, m->bits, m->decode_policy, s);
+        return launch_qcsr_parts(a, m->bits, m->decode_policy, out_cols, s);
     if (m->bits == 0u) {
         if (m->value_dtype == CELLERATOR_DTYPE_F16)
             return launch_mode<0, CX_DECODE_PER_GENE_AFFINE, ValueMode::f16>(a, rhs_dtype,

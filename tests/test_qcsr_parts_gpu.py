@@ -166,3 +166,30 @@ def test_generated_c3_rows_with_epilogue(oracle):
     got = out.cpu().numpy().astype(np.float64)
     tol = 1e-4 * np.abs(expect) + 1e-4 * mag.reshape(m.rows, 64)  # the suite's bound
     assert np.all(np.abs(got - expect) <= tol)
+
+
+@pytest.mark.parametrize("n", [128, 192])
+def test_wide_outputs_in_64_column_blocks_with_epilogue(oracle, n):
+    """N = 128 and 192 run one launch per 64 output columns; the bias and the beta * C
+    operand are shifted with each block (in-place affine update plus bias + GELU)."""
+    import torch
+
+    from cellerator_amd import Epilogue, qcsr_spmm
+    from cellerator_amd._native import EPILOGUE_BIAS_GELU_ERF
+    from math import erf, sqrt
+    rng = np.random.default_rng(961 + n)
+    fx = _skewed_fixture(oracle, rng, 330, 2500, 4, 1)
+    rhs = (rng.standard_normal((2500, n)) * 0.02).astype(np.float16)
+    c0 = (rng.standard_normal((330, n)) * 0.1).astype(np.float32)
+    bias = (rng.standard_normal(n) * 0.05).astype(np.float32)
+    out = torch.from_numpy(c0.copy()).cuda()
+    ep = Epilogue(kind=EPILOGUE_BIAS_GELU_ERF, alpha=0.5, beta=2.0,
+                  bias=torch.from_numpy(bias).cuda(), initial=out)
+    qcsr_spmm(to_device_qcsr(fx), torch.from_numpy(rhs).cuda(), out=out, epilogue=ep)
+    torch.cuda.synchronize()
+    ref, mag = _referee(oracle, fx, rhs)
+    pre = 0.5 * ref.reshape(330, n) + 2.0 * c0.astype(np.float64) + bias.astype(np.float64)
+    expect = np.vectorize(lambda v: 0.5 * v * (1.0 + erf(v / sqrt(2.0))))(pre)
+    got = out.cpu().numpy().astype(np.float64)
+    tol = 1e-4 * np.abs(expect) + 1e-4 * (0.5 * mag.reshape(330, n) + 2.0 * np.abs(c0)) + 1e-6
+    assert np.all(np.abs(got - expect) <= tol)
