@@ -15,9 +15,9 @@
 // parts of kPartGenes:
 //   * the part's fp16 weight rows (128 B each) and (scale, offset) pairs are copied into
 //     LDS by buffer loads that write LDS directly;
-//   * each wave then visits its rows in turn. Columns within a row are sorted, so the row's
-//     entries in the part are the run starting at the row's cursor. The wave keeps the next
-//     64 (gene, code) pairs of every row in one register (gene in the low 24 bits), decodes
+//   * each wave then visits its rows, two at a time. Columns within a row are sorted, so
+//     the row's entries in the part are the run starting at the row's cursor. The wave keeps
+//     the next 64 entries of every row in two registers (column index, code byte), decodes
 //     the run from the LDS metadata, stages (LDS offset of the weight row, value), and lets
 //     lane group g = lane / 8 take entry s + g while lane j = lane % 8 reads 16 B of that
 //     weight row and issues 8 v_fma_mix_f32 into the row's 8 partial sums;
@@ -34,8 +34,7 @@ namespace cx {
 namespace {
 
 constexpr int kPartGenes = 1024;                 // 128 KB of fp16 weight rows per part
-constexpr std::uint32_t kGeneMask = 0xffffffu;   // window register: gene | code << 24
-constexpr std::uint32_t kNoGene = kGeneMask;     // never inside a part
+constexpr std::uint32_t kNoGene = 0xffffffffu;   // never inside a part
 constexpr std::uint32_t kNoRow = 0xffffffffu;
 constexpr int kRefill = 48;                      // refill a row's window below this many
 
@@ -420,7 +419,7 @@ int launch_policy_parts(const QcsrArgs &a, std::uint32_t bits, hipStream_t strea
 bool qcsr_parts_applicable(const QcsrArgs &a, std::uint32_t bits, std::uint32_t rhs_dtype,
                            std::int64_t out_cols, bool aligned) {
     return bits != 0u && rhs_dtype == CELLERATOR_DTYPE_F16 && out_cols > 0 && out_cols % 64 == 0
-        && out_cols <= 256 && aligned && a.cols < kGeneMask && a.rows > 0u && a.cols > 0u
+        && out_cols <= 256 && aligned && a.cols <= static_cast<std::uint32_t>(INT32_MAX) && a.rows > 0u && a.cols > 0u
         && a.rhs_ld <= (INT32_MAX / 2) / kPartGenes;
 }
 
