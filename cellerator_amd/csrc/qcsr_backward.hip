@@ -408,6 +408,9 @@ extern "C" int cx_qcsr_spmm_bwd_values(const cx_qcsr_matrix *m, const float *gra
     const bool aligned = aligned16(grad_out) && aligned16(rhs) && (grad_out_ld * 4) % 16 == 0
         && (rhs_ld * static_cast<std::int64_t>(esize)) % 16 == 0;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (bwd_values_parts_applicable(m->rows, m->cols, rhs_dtype, out_cols, aligned, rhs_ld))
+        return launch_bwd_values_parts(m->row_ptr, m->col_idx, grad_out, grad_out_ld, rhs, rhs_ld, grad_values,
+                                       m->rows, m->cols, s);
     if (rhs_dtype == CELLERATOR_DTYPE_F16) return launch_bwd_values<std::uint16_t>(a, out_cols, aligned, s);
     return launch_bwd_values<float>(a, out_cols, aligned, s);
 }

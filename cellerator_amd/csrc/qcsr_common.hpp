@@ -64,6 +64,12 @@ bool qcsr_parts_applicable(const QcsrArgs &a, std::uint32_t bits, std::uint32_t 
                            std::int64_t out_cols, bool aligned);
 int launch_qcsr_parts(const QcsrArgs &a, std::uint32_t bits, std::uint32_t policy, std::int64_t out_cols,
                       hipStream_t stream);
+// grad_values of the backward pass by gene part (fp16 weights, N = 64).
+bool bwd_values_parts_applicable(std::uint32_t rows, std::uint32_t cols, std::uint32_t rhs_dtype,
+                                 std::int64_t out_cols, bool aligned, std::int64_t rhs_ld);
+int launch_bwd_values_parts(const std::int32_t *row_ptr, const std::int32_t *col_idx, const float *grad_out,
+                            std::int64_t grad_out_ld, const void *rhs, std::int64_t rhs_ld,
+                            float *grad_values, std::uint32_t rows, std::uint32_t cols, hipStream_t stream);
 
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");

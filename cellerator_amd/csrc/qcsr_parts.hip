@@ -120,23 +120,34 @@ using lds_ptr = __attribute__((address_space(3))) void *;
 // 8 rows, at no register cost); loads past the part's last row return zeros. Interleaved
 // (scale, offset) pairs go the same way; the other decode policies build their pairs in
 // registers.
-template<int kPolicy, int kWaves, typename Shared>
-__device__ __forceinline__ void load_part(Shared &sh, const QcsrArgs &a, int lo, int hi, int wave, int lane,
-                                          int tid) {
+// The fp16 weight rows of genes [lo, hi) straight from memory into LDS (buffer loads with
+// the lds flag: wave instruction k of wave w fills 1 KB, 8 rows, at no register cost);
+// loads past the part's last row return zeros.
+template<int kWaves>
+__device__ __forceinline__ void load_part_weights(uint4 *w, const std::uint16_t *rhs, std::int64_t rhs_ld,
+                                                  int lo, int hi, int wave, int lane) {
     constexpr int kChunks = kPartGenes * 8 / kWave;  // 1 KB wave loads per part
     static_assert(kChunks % kWaves == 0, "part chunks must divide among the waves");
-    const int span = hi - lo;
-    const std::uint32_t row_bytes = static_cast<std::uint32_t>(a.rhs_ld) * 2u;
-    const rsrc_t rw = make_rsrc(static_cast<const std::uint16_t *>(a.rhs) + static_cast<std::int64_t>(lo) * a.rhs_ld,
-                                static_cast<std::uint32_t>(span - 1) * row_bytes + 128u);
+    const std::uint32_t row_bytes = static_cast<std::uint32_t>(rhs_ld) * 2u;
+    const rsrc_t rw = make_rsrc(rhs + static_cast<std::int64_t>(lo) * rhs_ld,
+                                static_cast<std::uint32_t>(hi - lo - 1) * row_bytes + 128u);
 #pragma unroll
     for (int k = 0; k < kChunks / kWaves; ++k) {
         const int chunk = k * kWaves + wave;
         const int idx = chunk * kWave + lane;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rw, (lds_ptr)(&sh.w[chunk * kWave]), 16,
+            rw, (lds_ptr)(&w[chunk * kWave]), 16,
             static_cast<std::uint32_t>(idx / 8) * row_bytes + static_cast<std::uint32_t>(idx % 8) * 16u, 0, 0, 0);
     }
+}
+
+// The weight rows and (scale, offset) pairs of genes [lo, hi) into LDS. Interleaved pairs
+// go straight to LDS like the weights; the other decode policies build them in registers.
+template<int kPolicy, int kWaves, typename Shared>
+__device__ __forceinline__ void load_part(Shared &sh, const QcsrArgs &a, int lo, int hi, int wave, int lane,
+                                          int tid) {
+    const int span = hi - lo;
+    load_part_weights<kWaves>(sh.w, static_cast<const std::uint16_t *>(a.rhs), a.rhs_ld, lo, hi, wave, lane);
     if constexpr (kPolicy == CX_DECODE_PER_GENE_AFFINE_PAIRS) {
         constexpr int kMetaChunks = kPartGenes * 8 / (kWave * 16);  // 2 pairs per lane
         if (wave < kMetaChunks) {
@@ -154,6 +165,34 @@ __device__ __forceinline__ void load_part(Shared &sh, const QcsrArgs &a, int lo,
         }
     }
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the LDS writes of the loads above
+}
+
+// Snake assignment of a block's rows to waves: rank the rows by length (descending, ties
+// by index) and deal rank r to slot r / kWaves of wave (r / kWaves even ? r % kWaves
+// : kWaves - 1 - r % kWaves), so every wave carries about the same number of nonzeros.
+template<int kWaves, int kRw>
+__device__ __forceinline__ void assign_rows(int *len, std::uint32_t *rows_out, const std::int32_t *row_ptr,
+                                            std::uint32_t rows, std::uint32_t first, int tid) {
+    constexpr int kBlockRows = kWaves * kRw;
+    if (tid < kBlockRows) {
+        const std::uint32_t row = first + static_cast<std::uint32_t>(tid);
+        len[tid] = row < rows ? row_ptr[row + 1] - row_ptr[row] : -1;
+    }
+    __syncthreads();
+    if (tid < kBlockRows) {
+        const int my = len[tid];
+        int rank = 0;
+#pragma unroll 4
+        for (int u = 0; u < kBlockRows; ++u) {
+            const int lu = len[u];
+            rank += lu > my || (lu == my && u < tid) ? 1 : 0;
+        }
+        const int round = rank / kWaves, pos = rank % kWaves;
+        const int w = (round & 1) != 0 ? kWaves - 1 - pos : pos;
+        const std::uint32_t row = first + static_cast<std::uint32_t>(tid);
+        rows_out[w * kRw + round] = row < rows ? row : kNoRow;
+    }
+    __syncthreads();
 }
 
 __device__ __forceinline__ void fma8(float (&p)[8], float x, uint4 w) {
@@ -199,28 +238,7 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_parts(QcsrArgs a) {
     const std::uint32_t first = blockIdx.x * static_cast<std::uint32_t>(kBlockRows);
     const std::uint32_t code_shift = static_cast<std::uint32_t>((lane % kCpb) * kBits);
 
-    // Balanced assignment: rank the block's rows by length (descending, ties by index) and
-    // deal rank r to slot r / kWaves of wave (r / kWaves even ? r % kWaves
-    // : kWaves - 1 - r % kWaves).
-    if (tid < kBlockRows) {
-        const std::uint32_t row = first + static_cast<std::uint32_t>(tid);
-        sh.len[tid] = row < a.rows ? a.row_ptr[row + 1] - a.row_ptr[row] : -1;
-    }
-    __syncthreads();
-    if (tid < kBlockRows) {
-        const int len = sh.len[tid];
-        int rank = 0;
-#pragma unroll 4
-        for (int u = 0; u < kBlockRows; ++u) {
-            const int lu = sh.len[u];
-            rank += lu > len || (lu == len && u < tid) ? 1 : 0;
-        }
-        const int round = rank / kWaves, pos = rank % kWaves;
-        const int w = (round & 1) != 0 ? kWaves - 1 - pos : pos;
-        const std::uint32_t row = first + static_cast<std::uint32_t>(tid);
-        sh.rows[w * kRw + round] = row < a.rows ? row : kNoRow;
-    }
-    __syncthreads();
+    assign_rows<kWaves, kRw>(sh.len, sh.rows, a.row_ptr, a.rows, first, tid);
 
     // Matrix totals (window loads stop at them).
     const int nnz = __builtin_amdgcn_readfirstlane(a.row_ptr[a.rows]);
@@ -395,6 +413,206 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_parts(QcsrArgs a) {
     }
 }
 
+// ---- backward values: grad_values[i] = <G[row_i, :], W[col_i, :]> over 64 columns --------
+//
+// The same part walk without decode (the gradient does not depend on the stored values):
+// each wave keeps its rows' G (lane j: columns 8j..8j+7, fp32) in registers; lane group g
+// takes staged entry s + g, lane j multiplies its 8 columns with 16 B of the LDS weight
+// row, the group sums its 8 lanes (DPP), and the dots are staged and stored coalesced per
+// visit.
+
+struct BwdPartsArgs {
+    const std::int32_t *row_ptr;
+    const std::int32_t *col_idx;
+    const float *grad_out;
+    std::int64_t grad_out_ld;
+    const std::uint16_t *rhs;  // fp16 [cols x 64]
+    std::int64_t rhs_ld;
+    float *grad_values;
+    std::uint32_t rows;
+    std::uint32_t cols;
+};
+
+template<int kWaves, int kRw>
+struct BwdPartsShared {
+    uint4 w[kPartGenes * 8];          // [gene][16-byte quarter-rows]: fp16 weights
+    int stage[kWaves][2][kWave];      // per wave, two rows: LDS byte offset of the weight row
+    float dots[kWaves][2][kWave];     // per wave, two rows: the staged entries' results
+    int len[kWaves * kRw];
+    std::uint32_t rows[kWaves * kRw];
+};
+
+__device__ __forceinline__ float dot8(const float (&g)[8], uint4 w) {
+    const std::uint32_t words[4] = {w.x, w.y, w.z, w.w};
+    float d = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        d = __builtin_fmaf(g[2 * k], h2f(static_cast<std::uint16_t>(words[k] & 0xffffu)), d);
+        d = __builtin_fmaf(g[2 * k + 1], h2f(static_cast<std::uint16_t>(words[k] >> 16)), d);
+    }
+    return d;
+}
+
+// Sum over the 8 lanes of each lane group (quad xor 1, xor 2, then the half-row mirror).
+__device__ __forceinline__ float group_sum8(float d) {
+    d += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d), 0xB1, 0xf, 0xf, false));
+    d += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d), 0x4E, 0xf, 0xf, false));
+    d += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d), 0x141, 0xf, 0xf, false));
+    return d;
+}
+
+template<int kWaves, int kRw>
+__global__ __launch_bounds__(kWaves * kWave) void qcsr_bwd_values_parts(BwdPartsArgs a) {
+    constexpr int kBlockRows = kWaves * kRw;
+    static_assert(kBlockRows <= kWaves * kWave && kRw <= kWave && kRw % 2 == 0, "bad part-kernel shape");
+    __shared__ BwdPartsShared<kWaves, kRw> sh;
+    const int tid = static_cast<int>(threadIdx.x);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int lane = tid % kWave;
+    const int grp = lane >> 3;
+    const int j = lane & 7;
+    const std::uint32_t first = blockIdx.x * static_cast<std::uint32_t>(kBlockRows);
+    assign_rows<kWaves, kRw>(sh.len, sh.rows, a.row_ptr, a.rows, first, tid);
+    const int nnz = __builtin_amdgcn_readfirstlane(a.row_ptr[a.rows]);
+
+    int cur[kRw], end[kRw], base[kRw];
+    float g[kRw][8];
+    std::uint32_t win[kRw];
+    auto load_cols = [&](int rw) {  // window: column indices of entries [base, base + 64)
+        const std::uint32_t ub = static_cast<std::uint32_t>(base[rw]);
+        const std::uint32_t n = static_cast<std::uint32_t>(nnz) - ub < kWave ? static_cast<std::uint32_t>(nnz) - ub : kWave;
+        win[rw] = static_cast<std::uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+            make_rsrc(a.col_idx + ub, n * 4u), lane * 4, 0, 0));
+    };
+#pragma unroll
+    for (int rw = 0; rw < kRw; ++rw) {
+        const std::uint32_t row = __builtin_amdgcn_readfirstlane(sh.rows[wave * kRw + rw]);
+        cur[rw] = end[rw] = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) g[rw][k] = 0.0f;
+        if (row != kNoRow) {
+            cur[rw] = __builtin_amdgcn_readfirstlane(a.row_ptr[row]);
+            end[rw] = __builtin_amdgcn_readfirstlane(a.row_ptr[row + 1]);
+            const float4 *gp = reinterpret_cast<const float4 *>(a.grad_out + static_cast<std::int64_t>(row) * a.grad_out_ld + j * 8);
+            const float4 g0 = gp[0], g1 = gp[1];
+            g[rw][0] = g0.x; g[rw][1] = g0.y; g[rw][2] = g0.z; g[rw][3] = g0.w;
+            g[rw][4] = g1.x; g[rw][5] = g1.y; g[rw][6] = g1.z; g[rw][7] = g1.w;
+        }
+        base[rw] = cur[rw];
+        win[rw] = kNoGene;
+        if (cur[rw] < end[rw]) load_cols(rw);
+    }
+    const char *wbase = reinterpret_cast<const char *>(sh.w) + j * 16;
+
+    auto segment = [&](int rw, int lo, std::uint32_t span, int &start, int &cnt, std::uint32_t &gl) {
+        start = cur[rw] - base[rw];
+        gl = win[rw] - static_cast<std::uint32_t>(lo);
+        const std::uint64_t run = ~(__builtin_amdgcn_ballot_w64(gl < span) >> start);
+        const int in_run = run == 0u ? kWave - start : __builtin_ctzll(run);
+        cnt = in_run < end[rw] - cur[rw] ? in_run : end[rw] - cur[rw];
+    };
+    auto stage = [&](int slot, int start, int cnt, std::uint32_t gl) {
+        if (static_cast<std::uint32_t>(lane - start) < static_cast<std::uint32_t>(cnt))
+            sh.stage[wave][slot][lane] = static_cast<int>(gl) * 128;
+    };
+    // dots of staged entries [start, start + cnt) of slot `slot` into sh.dots
+    auto step1 = [&](int rw, int slot, int s) {
+        const int e = sh.stage[wave][slot][s + grp];
+        const float d = group_sum8(dot8(g[rw], *reinterpret_cast<const uint4 *>(wbase + e)));
+        if (j == 0) sh.dots[wave][slot][s + grp] = d;
+    };
+    auto dots = [&](int rw, int slot, int s, int stop) {
+        for (; s + 8 <= stop; s += 8) step1(rw, slot, s);
+        if (s + grp < stop) step1(rw, slot, s);
+    };
+    auto store = [&](int rw, int slot, int start, int cnt) {
+        if (static_cast<std::uint32_t>(lane - start) < static_cast<std::uint32_t>(cnt))
+            a.grad_values[static_cast<std::uint32_t>(base[rw] + lane)] = sh.dots[wave][slot][lane];
+    };
+    auto advance = [&](int rw, int stop, int cnt) -> bool {
+        cur[rw] += cnt;
+        if (stop < kWave || cur[rw] >= end[rw]) return false;
+        base[rw] = cur[rw];
+        load_cols(rw);
+        return true;
+    };
+    auto visit_rest = [&](int rw, int lo, std::uint32_t span) {
+        for (;;) {
+            int start, cnt;
+            std::uint32_t gl;
+            segment(rw, lo, span, start, cnt, gl);
+            if (cnt == 0) return;
+            stage(0, start, cnt, gl);
+            wave_sync();
+            dots(rw, 0, start, start + cnt);
+            wave_sync();
+            store(rw, 0, start, cnt);
+            if (!advance(rw, start + cnt, cnt)) return;
+        }
+    };
+    auto refill = [&](int rw) {
+        if (base[rw] + kWave < end[rw] && base[rw] + kWave - cur[rw] < kRefill) {
+            base[rw] = cur[rw];
+            load_cols(rw);
+        }
+    };
+
+    const int cols = static_cast<int>(a.cols);
+    const int parts = (cols + kPartGenes - 1) / kPartGenes;
+    for (int part = 0; part < parts; ++part) {
+        const int lo = part * kPartGenes;
+        const int hi = lo + kPartGenes < cols ? lo + kPartGenes : cols;
+        const std::uint32_t span = static_cast<std::uint32_t>(hi - lo);
+        __syncthreads();  // every wave is done reading part - 1
+        load_part_weights<kWaves>(sh.w, a.rhs, a.rhs_ld, lo, hi, wave, lane);
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the copy (and the window refills)
+        __syncthreads();
+#pragma unroll
+        for (int ra = 0; ra < kRw; ra += 2) {
+            const int rb = ra + 1;
+            int sa = 0, ca = 0, sb = 0, cb = 0;
+            std::uint32_t ga = 0u, gb = 0u;
+            if (cur[ra] < end[ra]) segment(ra, lo, span, sa, ca, ga);
+            if (cur[rb] < end[rb]) segment(rb, lo, span, sb, cb, gb);
+            stage(0, sa, ca, ga);
+            stage(1, sb, cb, gb);
+            wave_sync();
+            int s_a = sa, s_b = sb;
+            const int stop_a = sa + ca, stop_b = sb + cb;
+            for (; s_a + 8 <= stop_a && s_b + 8 <= stop_b; s_a += 8, s_b += 8) {
+                step1(ra, 0, s_a);
+                step1(rb, 1, s_b);
+            }
+            dots(ra, 0, s_a, stop_a);
+            dots(rb, 1, s_b, stop_b);
+            wave_sync();
+            store(ra, 0, sa, ca);
+            store(rb, 1, sb, cb);
+            const bool more_a = ca > 0 && advance(ra, stop_a, ca);
+            const bool more_b = cb > 0 && advance(rb, stop_b, cb);
+            if (more_a) visit_rest(ra, lo, span);
+            if (more_b) visit_rest(rb, lo, span);
+            refill(ra);
+            refill(rb);
+        }
+    }
+
+    // rows the walk could not finish: the remaining entries on a plain path (lane = column;
+    // columns outside [0, cols) give 0)
+#pragma unroll
+    for (int rw = 0; rw < kRw; ++rw) {
+        if (cur[rw] >= end[rw]) continue;
+        const std::uint32_t row = __builtin_amdgcn_readfirstlane(sh.rows[wave * kRw + rw]);
+        const float gl = a.grad_out[static_cast<std::int64_t>(row) * a.grad_out_ld + lane];
+        for (int i = cur[rw]; i < end[rw]; ++i) {
+            const std::uint32_t col = static_cast<std::uint32_t>(a.col_idx[i]);
+            float d = col < a.cols ? gl * h2f(a.rhs[static_cast<std::int64_t>(col) * a.rhs_ld + lane]) : 0.0f;
+            d = xor_reduce<0, 5>(d);
+            if (lane == 0) a.grad_values[i] = d;
+        }
+    }
+}
+
 template<int kBits, int kPolicy>
 int launch_bits_parts(const QcsrArgs &a, hipStream_t stream) {
     constexpr int kWaves = 16, kRw = 8;
@@ -425,6 +643,24 @@ bool qcsr_parts_applicable(const QcsrArgs &a, std::uint32_t bits, std::uint32_t 
 
 // N = 64 c columns: one launch per 64-column block of the weights and the output (and of
 // the epilogue's bias and initial values).
+bool bwd_values_parts_applicable(std::uint32_t rows, std::uint32_t cols, std::uint32_t rhs_dtype,
+                                 std::int64_t out_cols, bool aligned, std::int64_t rhs_ld) {
+    return rhs_dtype == CELLERATOR_DTYPE_F16 && out_cols == 64 && aligned && rows > 0u && cols > 0u
+        && cols <= static_cast<std::uint32_t>(INT32_MAX) && rhs_ld <= (INT32_MAX / 2) / kPartGenes;
+}
+
+int launch_bwd_values_parts(const std::int32_t *row_ptr, const std::int32_t *col_idx, const float *grad_out,
+                            std::int64_t grad_out_ld, const void *rhs, std::int64_t rhs_ld,
+                            float *grad_values, std::uint32_t rows, std::uint32_t cols, hipStream_t stream) {
+    constexpr int kWaves = 16, kRw = 8;
+    const BwdPartsArgs a{row_ptr, col_idx, grad_out, grad_out_ld, static_cast<const std::uint16_t *>(rhs), rhs_ld,
+                         grad_values, rows, cols};
+    const unsigned rows_per_block = kWaves * kRw;
+    const dim3 grid((rows + rows_per_block - 1) / rows_per_block), block(kWaves * kWave);
+    hipLaunchKernelGGL((qcsr_bwd_values_parts<kWaves, kRw>), grid, block, 0, stream, a);
+    return check_launch("qcsr_bwd_values_parts");
+}
+
 int launch_qcsr_parts(const QcsrArgs &a, std::uint32_t bits, std::uint32_t policy, std::int64_t out_cols,
                       hipStream_t stream) {
     for (std::int64_t c0 = 0; c0 < out_cols; c0 += 64) {

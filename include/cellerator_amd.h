@@ -227,7 +227,9 @@ int cx_qcsr_spmm_bwd_rhs_panelled(const cx_qcsr_matrix *panelled, uint32_t panel
  * csr_spmm_bwd_values_f16_f32 (src/compute/sparse/ops/ops.hh:111-120,
  * kernels/base_sparse/csr_spmm_bwd_values_kernel_.cuh), whose kernel reads grad_out with the
  * rhs leading dimension; here each operand has its own. Reads only A's structure. fp32
- * products and sums in a fixed order; rhs F16 or F32, grad_out F32. */
+ * products and sums in a fixed order; rhs F16 or F32, grad_out F32. With F16 rhs at
+ * out_cols = 64 the rhs streams through LDS by gene part (fastest with each row's columns
+ * ascending); there an entry whose column lies outside [0, cols) gets 0. */
 int cx_qcsr_spmm_bwd_values(const cx_qcsr_matrix *a, const float *grad_out,
                             int64_t grad_out_ld, const void *rhs, uint32_t rhs_dtype,
                             int64_t rhs_ld, int64_t out_cols, float *grad_values, void *stream);

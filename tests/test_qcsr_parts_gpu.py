@@ -193,3 +193,60 @@ def test_wide_outputs_in_64_column_blocks_with_epilogue(oracle, n):
     got = out.cpu().numpy().astype(np.float64)
     tol = 1e-4 * np.abs(expect) + 1e-4 * (0.5 * mag.reshape(330, n) + 2.0 * np.abs(c0)) + 1e-6
     assert np.all(np.abs(got - expect) <= tol)
+
+
+def _bwd_values_check(oracle, fx, g, w, got):
+    ref = oracle.spmm_bwd_values(fx["row_ptr"], fx["col_idx"], g, w)
+    rows_of = np.repeat(np.arange(fx["rows"]), np.diff(fx["row_ptr"]))
+    mag = np.einsum("ij,ij->i", np.abs(g.astype(np.float64))[rows_of],
+                    np.abs(w.astype(np.float64))[fx["col_idx"]])
+    check_against_referee(oracle, ref, mag, got)
+
+
+def test_bwd_values_parts_skewed_rows(oracle):
+    """grad_values by gene part (fp16 W, N = 64): 5 parts, rows from empty to every gene,
+    several workgroups; against the float64 restatement of csr_spmm_bwd_values."""
+    import torch
+
+    from cellerator_amd import qcsr_spmm_bwd_values
+    rng = np.random.default_rng(971)
+    fx = _skewed_fixture(oracle, rng, 420, 4700, 8, 1)
+    g = rng.standard_normal((420, 64)).astype(np.float32)
+    w = (rng.standard_normal((4700, 64)) * 0.1).astype(np.float16)
+    gv = qcsr_spmm_bwd_values(to_device_qcsr(fx), torch.from_numpy(g).cuda(), torch.from_numpy(w).cuda())
+    torch.cuda.synchronize()
+    _bwd_values_check(oracle, fx, g, w, gv.cpu().numpy())
+
+
+def test_bwd_values_parts_unsorted_and_out_of_range(oracle):
+    """Rows out of order across parts finish on the per-row path from their cursor; entries
+    with columns outside [0, cols) get 0."""
+    import torch
+
+    from cellerator_amd import qcsr_spmm_bwd_values
+    rng = np.random.default_rng(977)
+    cols = 3000
+    fx = _skewed_fixture(oracle, rng, 260, cols, 4, 1)
+    row_ptr, col_idx = fx["row_ptr"], fx["col_idx"].copy()
+    for r in range(0, 260, 3):
+        s, e = row_ptr[r], row_ptr[r + 1]
+        col_idx[s:e] = col_idx[s:e][::-1]
+    bad = rng.choice(len(col_idx), 30, replace=False)
+    col_idx[bad[:15]] = cols + 7
+    col_idx[bad[15:]] = -1
+    dev = dict(fx, col_idx=col_idx)
+    g = rng.standard_normal((260, 64)).astype(np.float32)
+    w = (rng.standard_normal((cols, 64)) * 0.1).astype(np.float16)
+    gv = qcsr_spmm_bwd_values(to_device_qcsr(dev), torch.from_numpy(g).cuda(), torch.from_numpy(w).cuda())
+    torch.cuda.synchronize()
+    got = gv.cpu().numpy()
+    assert np.all(got[bad] == 0.0)
+    good = np.ones(len(col_idx), bool)
+    good[bad] = False
+    ref_cols = col_idx.copy()
+    ref_cols[bad] = 0
+    ref = oracle.spmm_bwd_values(row_ptr, ref_cols, g, w)
+    rows_of = np.repeat(np.arange(260), np.diff(row_ptr))
+    mag = np.einsum("ij,ij->i", np.abs(g.astype(np.float64))[rows_of],
+                    np.abs(w.astype(np.float64))[ref_cols])
+    check_against_referee(oracle, ref[good], mag[good], got[good])
