@@ -9,10 +9,13 @@
 //      size to its wave's LDS counter -- no atomics, no per-lane LDS traffic.
 //      Counts go to hist[digit * tiles + tile] (digit-major).
 //   2. exclusive scan of hist: offset of (digit, tile) in the output.
-//   3. scatter: same ballots; wave bases per digit = tile offset + counts of the earlier
-//      waves; inside a wave the rounds run in order, each lane's slot = base + running count
-//      of its digit + its rank among the lower lanes of its group. The output order is the
-//      input order within equal digits, so the sort is stable and deterministic.
+//   3. scatter: same ballots; the tile is first reordered in LDS by digit (wave bases per
+//      digit = the digit's tile-local start + counts of the earlier waves; inside a wave the
+//      rounds run in order, each lane's slot = base + running count of its digit + its rank
+//      among the lower lanes of its group), then written out with consecutive threads on
+//      consecutive slots of each digit's run (global slot = tile offset of the digit +
+//      position in the run). The output order is the input order within equal digits, so
+//      the sort is stable and deterministic.
 // Keys are sorted on their low key_bits bits (passes = ceil(key_bits / 8)).
 #include "cx_common.hpp"
 
@@ -88,7 +91,10 @@ __global__ __launch_bounds__(kSortThreads) void radix_histogram(PassArgs a) {
 
 __global__ __launch_bounds__(kSortThreads) void radix_scatter(PassArgs a) {
     __shared__ std::uint32_t counts[kSortWaves][256];
-    __shared__ std::uint32_t base[kSortWaves][256];
+    __shared__ std::uint32_t base[kSortWaves][256];   // tile-local start of (wave, digit)
+    __shared__ std::uint32_t delta[256];              // global minus tile-local position
+    __shared__ std::uint32_t wave_sums[kSortWaves];
+    __shared__ std::uint32_t sk[kTileItems], sv[kTileItems];
     const int wave = static_cast<int>(threadIdx.x) / kWave;
     const int lane = static_cast<int>(threadIdx.x) % kWave;
     const std::uint32_t tile = blockIdx.x;
@@ -114,16 +120,31 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter(PassArgs a) {
     }
     __syncthreads();
     {
-        // per digit: global offset of this tile, then the earlier waves' counts
+        // per digit: the tile's count, its tile-local start (exclusive scan over digits, one
+        // digit per thread), the waves' local starts, and the shift to the global output
         const int d = static_cast<int>(threadIdx.x);
-        std::uint32_t running = a.hist[static_cast<std::uint64_t>(d) * a.tiles + tile];
+        std::uint32_t total = 0u;
+#pragma unroll
+        for (int w = 0; w < kSortWaves; ++w) total += counts[w][d];
+        std::uint32_t incl = total;  // inclusive scan inside the wave
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+            const std::uint32_t o = static_cast<std::uint32_t>(__shfl_up(static_cast<int>(incl), off, kWave));
+            if (lane >= off) incl += o;
+        }
+        if (lane == kWave - 1) wave_sums[wave] = incl;
+        __syncthreads();
+        std::uint32_t start = incl - total;
+        for (int w = 0; w < wave; ++w) start += wave_sums[w];
+        delta[d] = a.hist[static_cast<std::uint64_t>(d) * a.tiles + tile] - start;
 #pragma unroll
         for (int w = 0; w < kSortWaves; ++w) {
-            base[w][d] = running;
-            running += counts[w][d];
+            base[w][d] = start;
+            start += counts[w][d];
         }
     }
     __syncthreads();
+    // tile-local stable order in LDS: wave, then round, then rank among equal digits
 #pragma unroll
     for (int r = 0; r < kRounds; ++r) {
         const std::uint32_t i = item_index(tile, wave, r, lane);
@@ -131,8 +152,8 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter(PassArgs a) {
         const std::uint64_t below = peers[r] & lanemask_lt();
         const std::uint32_t slot = base[wave][digit[r]] + static_cast<std::uint32_t>(__popcll(below));
         if (valid) {
-            a.keys_out[slot] = key[r];
-            a.vals_out[slot] = val[r];
+            sk[slot] = key[r];
+            sv[slot] = val[r];
         }
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -140,6 +161,18 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter(PassArgs a) {
         if (valid && higher == 0u) base[wave][digit[r]] += static_cast<std::uint32_t>(__popcll(peers[r]));
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+    // equal digits are now contiguous: consecutive threads write consecutive output slots
+    const std::uint32_t first = tile * static_cast<std::uint32_t>(kTileItems);
+    const std::uint32_t n = a.count - first < static_cast<std::uint32_t>(kTileItems)
+        ? a.count - first : static_cast<std::uint32_t>(kTileItems);
+#pragma unroll 4
+    for (std::uint32_t i = threadIdx.x; i < n; i += kSortThreads) {
+        const std::uint32_t k = sk[i];
+        const std::uint32_t slot = delta[(k >> a.shift) & 255u] + i;
+        a.keys_out[slot] = k;
+        a.vals_out[slot] = sv[i];
     }
 }
 
