@@ -70,12 +70,22 @@ __device__ __forceinline__ std::uint32_t uniform(std::uint32_t v) {
     return static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
 }
 
-__device__ __forceinline__ int wave_inclusive_max(int v, int lane) {
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        const int o = __shfl_up(v, off, kWave);
-        if (lane >= off) v = v > o ? v : o;
-    }
+// Inclusive max-scan over the wave of non-negative values, in DPP (no LDS crossbar traffic):
+// row shifts by 1, 2, 4, 8 scan each 16-lane row, then the row broadcasts of lanes 15 and
+// 31 carry the running maximum into the later rows. Lanes without a source see 0.
+template<int kCtrl, int kRowMask>
+__device__ __forceinline__ int dpp_max_step(int v) {
+    const int o = __builtin_amdgcn_update_dpp(0, v, kCtrl, kRowMask, 0xf, false);
+    return v > o ? v : o;
+}
+
+__device__ __forceinline__ int wave_inclusive_max(int v, int /*lane*/) {
+    v = dpp_max_step<0x111, 0xf>(v);  // row_shr:1
+    v = dpp_max_step<0x112, 0xf>(v);  // row_shr:2
+    v = dpp_max_step<0x114, 0xf>(v);  // row_shr:4
+    v = dpp_max_step<0x118, 0xf>(v);  // row_shr:8
+    v = dpp_max_step<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    v = dpp_max_step<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
     return v;
 }
 
