@@ -200,7 +200,8 @@ __device__ __forceinline__ BatchExtent batch_extent(const BatchInput<MaskT> &b) 
     x.s0 = uniform(b.s_j);
     const unsigned long long fit = __ballot(b.has_entry && b.s_next - x.s0 <= kBatchValues);
     x.n = max(1u, static_cast<std::uint32_t>(__popcll(fit)));
-    const std::uint32_t v_end = uniform(__shfl(b.s_next, static_cast<int>(x.n) - 1, kWave));
+    const std::uint32_t v_end = static_cast<std::uint32_t>(
+        __builtin_amdgcn_readlane(static_cast<int>(b.s_next), static_cast<int>(x.n) - 1));
     x.nv = min(v_end - x.s0, kBatchValues);
     return x;
 }
