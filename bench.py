@@ -127,7 +127,7 @@ def bench_qcsr(args, torch, cfg, n_out: int) -> dict:
                    "nnz_per_row_mean": m.nnz / m.rows, "seed": hex(cfg.seed)},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(cfg.name),
-                     "kernel": ("qcsr_spmm_parts" if m.bits and n_out % 64 == 0 and n_out <= 256
+                     "kernel": ("qcsr_spmm_groups" if m.bits and n_out % 64 == 0 and n_out <= 256
                                 else "qcsr_spmm_rowwave")
                                + ("<gene-affine pairs>" if pairs else ""),
                      "kernel_ms_mean": kern_ms,

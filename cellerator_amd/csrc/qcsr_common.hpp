@@ -58,8 +58,8 @@ __device__ __forceinline__ float load_entry(const QcsrArgs &a, std::int64_t i,
     }
 }
 
-// Gene-part kernel (qcsr_parts.hip): quantized codes, fp16 weights, N a multiple of 64 (one
-// launch per 64 columns), 16-byte aligned operands.
+// Row-group kernel over LDS gene parts (qcsr_parts.hip): quantized codes, fp16 weights, N a
+// multiple of 64 up to 256 (one launch per 64 columns), 16-byte aligned operands.
 bool qcsr_parts_applicable(const QcsrArgs &a, std::uint32_t bits, std::uint32_t rhs_dtype,
                            std::int64_t out_cols, bool aligned);
 int launch_qcsr_parts(const QcsrArgs &a, std::uint32_t bits, std::uint32_t policy, std::int64_t out_cols,

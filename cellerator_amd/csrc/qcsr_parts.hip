@@ -1,5 +1,6 @@
 // qcsr_parts.hip -- quantized CSR SpMM with the weight panel streamed through LDS by gene
-// part (fp16 weights, N a multiple of 64 in blocks of 64 columns, column-sorted rows).
+// part (fp16 weights, N a multiple of 64 in blocks of 64 columns), and the gradient of the
+// stored values by the same part walk.
 //
 // Same value semantics as qcsr_spmm.hip (decode fma(float(code), scale, offset), exact fp16
 // widening, fp32 products and sums); only the summation order differs, and it is fixed.
@@ -9,25 +10,17 @@
 // serves the same 16-byte-per-lane gathers at about twice the rate, and the per-gene
 // metadata of a part sits beside its weight rows.
 //
-// Layout: one workgroup of kWaves waves per CU (LDS-bound) owns kWaves x kRw rows. A
-// prologue ranks the block's rows by length and deals them to the waves in snake order,
-// so every wave carries about the same number of nonzeros. The workgroup walks the genes in
-// parts of kPartGenes:
-//   * the part's fp16 weight rows (128 B each) and (scale, offset) pairs are copied into
-//     LDS by buffer loads that write LDS directly;
-//   * each wave then visits its rows, two at a time. Columns within a row are sorted, so
-//     the row's entries in the part are the run starting at the row's cursor. The wave keeps
-//     the next 64 entries of every row in two registers (column index, code byte), decodes
-//     the run from the LDS metadata, stages (LDS offset of the weight row, value), and lets
-//     lane group g = lane / 8 take entry s + g while lane j = lane % 8 reads 16 B of that
-//     weight row and issues 8 v_fma_mix_f32 into the row's 8 partial sums;
-//   * right after a pair's visits, each row window with fewer than kRefill entries left is
-//     refilled; those loads complete behind the rest of the part.
-// After the last part the 8 lane groups' partials of each row are reduce-scattered
-// (permlane32 swap, permlane16 swap, DPP row rotate), leaving one column per lane.
-// Rows whose cursor cannot advance (a column out of order across parts, or outside
-// [0, cols)) are recomputed at the end on a plain per-row path that skips columns outside
-// [0, cols); valid sorted input never takes it.
+// One workgroup of 16 waves per CU (LDS-bound) walks the genes in parts of kPartGenes. Each
+// part's fp16 weight rows (128 B each) and (scale, offset) pairs are copied into LDS by
+// buffer loads that write LDS directly; then every wave works through its rows' entries in
+// that part, and the next part replaces it. A prologue ranks the block's rows by length so
+// every wave carries about the same number of nonzeros into each part barrier.
+//
+// Forward (qcsr_spmm_groups): lane group g (8 lanes) of a wave owns one row of each of the
+// wave's layers, and lane j of the group holds that row's output columns 8j..8j+7 in
+// registers, so a row costs 8 registers and a workgroup owns 512 rows (details at the
+// kernel). Backward values (qcsr_bwd_values_parts): all 8 lane groups of a wave work on one
+// row at a time, each group on a different entry, with the row's gradient in registers.
 #include "qcsr_common.hpp"
 
 namespace cx {
@@ -43,74 +36,6 @@ using rsrc_t = __amdgpu_buffer_rsrc_t;
 __device__ __forceinline__ rsrc_t make_rsrc(const void *base, std::uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
                                              static_cast<int>(bytes), 0x00020000);
-}
-
-template<int kWaves, int kRw>
-struct PartsShared {
-    uint4 w[kPartGenes * 8];          // [gene][16-byte quarter-rows]: fp16 weights
-    float2 meta[kPartGenes];          // (scale, offset) per gene of the part
-    int2 stage[kWaves][2][kWave];     // per wave, two rows: (LDS byte offset of the row, value)
-    int len[kWaves * kRw];            // prologue: row lengths
-    std::uint32_t rows[kWaves * kRw]; // prologue: row of (wave, slot)
-};
-
-// Output column held by `lane` after reduce_scatter: 8 (lane % 8) + 4 bit3 + 2 bit4 + bit5.
-__device__ __forceinline__ int scatter_column(int lane) {
-    return 8 * (lane & 7) + 4 * ((lane >> 3) & 1) + 2 * ((lane >> 4) & 1) + ((lane >> 5) & 1);
-}
-
-// Sums the 8 lane groups' partials of columns 8 j + k (k < 8, j = lane % 8) and leaves
-// each lane with the total of scatter_column(lane).
-__device__ __forceinline__ float reduce_scatter(const float (&p)[8], int lane) {
-    float q[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        // lanes 32..63 of p[2m] trade places with lanes 0..31 of p[2m+1]
-        const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(p[2 * m]),
-                                                        __float_as_uint(p[2 * m + 1]), false, false);
-        q[m] = __uint_as_float(s[0]) + __uint_as_float(s[1]);  // bit5 = 0: slot 2m, 1: 2m+1
-    }
-    float r[2];
-#pragma unroll
-    for (int n = 0; n < 2; ++n) {
-        const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(q[2 * n]),
-                                                        __float_as_uint(q[2 * n + 1]), false, false);
-        r[n] = __uint_as_float(s[0]) + __uint_as_float(s[1]);  // bit4 selects q[2n + bit4]
-    }
-    const bool hi = (lane & 8) != 0;
-    const float keep = hi ? r[1] : r[0];
-    const float send = hi ? r[0] : r[1];
-    // row_ror:8 inside each 16-lane row pairs lane l with l ^ 8
-    const float got = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), 0x128, 0xf, 0xf, false));
-    return keep + got;
-}
-
-// A row's register window: entries [base, base + 64) as the raw column index and the byte
-// holding the entry's code (`base` - `begin` is a multiple of the codes per byte, so lane
-// i's code sits at byte i / cpb, shift (i % cpb) * bits). Lanes past the row end are not
-// loaded; every reader bounds the lanes by the row end.
-struct Window {
-    std::uint32_t col;
-    std::uint32_t byte;
-};
-
-// `pb` is the packed byte of entry `base`; `entries` / `bytes` are the matrix totals. The
-// loads are buffer loads from descriptors built in scalar registers with a constant lane
-// offset, so they write the window registers directly (no address registers that would
-// have to wait for earlier loads), and the descriptor bounds stop them at the end of the
-// matrix arrays (those lanes read zeros; readers bound lanes by the row end anyway).
-template<int kBits>
-__device__ __forceinline__ void load_window(Window &w, const QcsrArgs &a, int base, int pb, int lane,
-                                            int entries, int bytes) {
-    constexpr int kCpb = 8 / kBits;
-    const std::uint32_t ub = static_cast<std::uint32_t>(base), upb = static_cast<std::uint32_t>(pb);
-    const std::uint32_t n = static_cast<std::uint32_t>(entries) - ub < kWave ? static_cast<std::uint32_t>(entries) - ub : kWave;
-    const std::uint32_t nb = static_cast<std::uint32_t>(bytes) - upb < kWave / kCpb
-        ? static_cast<std::uint32_t>(bytes) - upb : kWave / kCpb;
-    const rsrc_t rc = make_rsrc(a.col_idx + ub, n * 4u);
-    const rsrc_t rp = make_rsrc(a.packed + upb, nb);
-    w.col = static_cast<std::uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rc, lane * 4, 0, 0));
-    w.byte = __builtin_amdgcn_raw_buffer_load_b8(rp, lane / kCpb, 0, 0);
 }
 
 using lds_ptr = __attribute__((address_space(3))) void *;
@@ -129,15 +54,17 @@ __device__ __forceinline__ void load_part_weights(uint4 *w, const std::uint16_t 
     constexpr int kChunks = kPartGenes * 8 / kWave;  // 1 KB wave loads per part
     static_assert(kChunks % kWaves == 0, "part chunks must divide among the waves");
     const std::uint32_t row_bytes = static_cast<std::uint32_t>(rhs_ld) * 2u;
-    const rsrc_t rw = make_rsrc(rhs + static_cast<std::int64_t>(lo) * rhs_ld,
-                                static_cast<std::uint32_t>(hi - lo - 1) * row_bytes + 128u);
+    // One descriptor per chunk (built in scalar registers) and one lane offset for all of
+    // them, so the copy keeps a single address register live across the part loop.
+    const std::uint32_t lane_off = static_cast<std::uint32_t>(lane >> 3) * row_bytes + static_cast<std::uint32_t>(lane & 7) * 16u;
 #pragma unroll
     for (int k = 0; k < kChunks / kWaves; ++k) {
         const int chunk = k * kWaves + wave;
-        const int idx = chunk * kWave + lane;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rw, (lds_ptr)(&w[chunk * kWave]), 16,
-            static_cast<std::uint32_t>(idx / 8) * row_bytes + static_cast<std::uint32_t>(idx % 8) * 16u, 0, 0, 0);
+        const int row0 = chunk * 8;  // first of the chunk's 8 rows within the part
+        const int left = hi - lo - row0;
+        const rsrc_t rw = make_rsrc(rhs + static_cast<std::int64_t>(lo + row0) * rhs_ld,
+                                    left > 0 ? static_cast<std::uint32_t>(left - 1) * row_bytes + 128u : 0u);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(&w[chunk * kWave]), 16, lane_off, 0, 0, 0);
     }
 }
 
@@ -151,10 +78,11 @@ __device__ __forceinline__ void load_part(Shared &sh, const QcsrArgs &a, int lo,
     if constexpr (kPolicy == CX_DECODE_PER_GENE_AFFINE_PAIRS) {
         constexpr int kMetaChunks = kPartGenes * 8 / (kWave * 16);  // 2 pairs per lane
         if (wave < kMetaChunks) {
-            const rsrc_t rm = make_rsrc(reinterpret_cast<const float2 *>(a.scales) + lo,
-                                        static_cast<std::uint32_t>(span) * 8u);
+            const int left = span - wave * 2 * kWave;  // pairs of this wave's chunk
+            const rsrc_t rm = make_rsrc(reinterpret_cast<const float2 *>(a.scales) + lo + wave * 2 * kWave,
+                                        left > 0 ? static_cast<std::uint32_t>(left) * 8u : 0u);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_ptr)(&sh.meta[wave * 2 * kWave]), 16,
-                                                     static_cast<std::uint32_t>(wave * kWave + lane) * 16u, 0, 0, 0);
+                                                     static_cast<std::uint32_t>(lane) * 16u, 0, 0, 0);
         }
     } else {
         for (int g = tid; g < span; g += kWaves * kWave) {
@@ -224,131 +152,214 @@ __device__ float row_fallback(const QcsrArgs &a, std::uint32_t row, int lane) {
     return acc;
 }
 
-template<int kBits, int kPolicy, int kWaves, int kRw>
-__global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_parts(QcsrArgs a) {
-    constexpr int kBlockRows = kWaves * kRw;
-    constexpr int kCpb = 8 / kBits;
-    static_assert(kBlockRows <= kWaves * kWave && kRw <= kWave && kRw % 2 == 0, "bad part-kernel shape");
-    __shared__ PartsShared<kWaves, kRw> sh;
+// ---- row-group form: lane group g of a wave owns one row of every layer ----------------------
+//
+// Each wave owns kLayers layers of 8 rows. Lane group g (8 lanes) owns row g of every layer,
+// and lane j of the group holds columns 8j..8j+7 of that row's output in registers for the
+// whole launch (8 fp32 per row and lane; no cross-lane reduction at the end). So the row
+// control of a part is vector work over 8 rows at once, and a row costs 8 registers instead
+// of 64, which lets one workgroup own 512 rows and copy each part for 4x as many rows.
+//
+// Every layer keeps a 64-entry window of each of its rows in registers: lane j holds the
+// column indices of entries cur + 8j .. cur + 8j + 7 and the two (three for 8-bit codes)
+// aligned dwords that hold their codes. A pass over a layer:
+//   * counts the window entries with column < hi (entries past the row end excluded): with
+//     sorted columns this is the row's run in the part (`run`, at most 64);
+//   * decodes the run in four fills of two window slots per lane: slots 2f, 2f + 1 of lane j
+//     (entries 8j + 2f, 8j + 2f + 1) go to stage slots 2j, 2j + 1 of the group, so each
+//     fill's valid entries are a prefix of the group's 16 stage slots; the rest are pads
+//     (the all-zero weight row, value 0);
+//   * steps through the fill: lane j of group g reads 16 B of the weight row of the group's
+//     staged entry and issues 8 v_fma_mix_f32 into its 8 partial sums, two entries per step;
+//   * advances the cursors by the runs and reloads the windows at the new cursors (buffer
+//     loads that complete behind the rest of the part); a row whose run filled the whole
+//     window continues in another pass.
+// An entry inside a run whose column is outside the part (columns out of order across
+// parts) marks the row broken; broken rows and rows whose cursor stops before the row end
+// (a column outside [0, cols)) are recomputed at the end on the plain per-row path.
+
+constexpr int kPadGene = kPartGenes;  // all-zero weight row, (0, 0) metadata
+
+template<int kWaves, int kLayers>
+struct GroupsShared {
+    static constexpr int kRows = kWaves * kLayers * 8;
+    union {
+        uint4 stage[kWaves][8][9];  // per wave and lane group: 16 (metadata byte offset, value) pairs (+16 B pad)
+        int len[kRows];             // prologue: row lengths
+    } u;
+    float2 meta[kPartGenes + 2];    // (scale, offset) per gene of the part; [kPadGene] = (0, 0)
+    uint4 w[(kPartGenes + 1) * 8];  // fp16 weight rows of the part; row kPadGene is zeros
+    std::uint32_t rows[kRows];      // row of (wave, layer, group)
+};
+
+// Rank the block's rows by length (descending, ties by index); ranks 8s .. 8s + 7 form row
+// set s (similar lengths, so the 8 groups of a layer finish their runs together), and the
+// sets are dealt to the waves in snake order (set s -> layer s / kWaves), so every wave
+// carries about the same number of nonzeros.
+template<int kWaves, int kLayers>
+__device__ __forceinline__ void assign_groups(int *len, std::uint32_t *rows_out, const std::int32_t *row_ptr,
+                                              std::uint32_t rows, std::uint32_t first, int tid) {
+    constexpr int kRows = kWaves * kLayers * 8;
+    const std::uint32_t row = first + static_cast<std::uint32_t>(tid);
+    if (tid < kRows) len[tid] = row < rows ? row_ptr[row + 1] - row_ptr[row] : -1;
+    __syncthreads();
+    if (tid < kRows) {
+        const int my = len[tid];
+        int rank = 0;
+        const int4 *l4 = reinterpret_cast<const int4 *>(len);
+#pragma unroll 4
+        for (int u = 0; u < kRows / 4; ++u) {
+            const int4 v = l4[u];
+            const int b = 4 * u;
+            rank += v.x > my || (v.x == my && b < tid) ? 1 : 0;
+            rank += v.y > my || (v.y == my && b + 1 < tid) ? 1 : 0;
+            rank += v.z > my || (v.z == my && b + 2 < tid) ? 1 : 0;
+            rank += v.w > my || (v.w == my && b + 3 < tid) ? 1 : 0;
+        }
+        const int set = rank / 8, g = rank % 8;
+        const int round = set / kWaves, pos = set % kWaves;
+        const int w = (round & 1) != 0 ? kWaves - 1 - pos : pos;
+        rows_out[(w * kLayers + round) * 8 + g] = row < rows ? row : kNoRow;
+    }
+    __syncthreads();
+}
+
+// Sum over the 8 lanes of each lane group (integer form of the DPP butterfly).
+__device__ __forceinline__ int group_sum8i(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false);
+    return v;
+}
+
+// Maximum over the wave of a value that is uniform within each lane group.
+__device__ __forceinline__ int wave_max_groups(int v) {
+    const int r = __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false);  // row_ror:8
+    v = v > r ? v : r;
+    const auto s = __builtin_amdgcn_permlane16_swap(static_cast<std::uint32_t>(v), static_cast<std::uint32_t>(v),
+                                                    false, false);
+    v = static_cast<int>(s[0] > s[1] ? s[0] : s[1]);
+    const auto t = __builtin_amdgcn_permlane32_swap(static_cast<std::uint32_t>(v), static_cast<std::uint32_t>(v),
+                                                    false, false);
+    v = static_cast<int>(t[0] > t[1] ? t[0] : t[1]);
+    return __builtin_amdgcn_readfirstlane(v);
+}
+
+// Entries of fill f (window entries 8j + 2f + r, j < 8, r < 2) below `run`.
+__device__ __forceinline__ int fill_count(int run, int f) {
+    const int t = run - 2 * f;
+    if (t <= 0) return 0;
+    const int blocks = t >> 3;
+    if (blocks >= 8) return 16;
+    const int rem = t & 7;
+    return 2 * blocks + (rem < 2 ? rem : 2);
+}
+
+template<int kBits, int kPolicy, int kWaves, int kLayers>
+__global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
+    using Shared = GroupsShared<kWaves, kLayers>;
+    constexpr int kRows = Shared::kRows;
+    constexpr int kCodeDw = kBits == 8 ? 3 : 2;
+    constexpr std::uint32_t kMask = (1u << kBits) - 1u;
+    __shared__ Shared sh;
     const int tid = static_cast<int>(threadIdx.x);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int lane = tid % kWave;
     const int grp = lane >> 3;
     const int j = lane & 7;
-    const std::uint32_t first = blockIdx.x * static_cast<std::uint32_t>(kBlockRows);
-    const std::uint32_t code_shift = static_cast<std::uint32_t>((lane % kCpb) * kBits);
+    const std::uint32_t first = blockIdx.x * static_cast<std::uint32_t>(kRows);
+    const std::uint32_t last = first + kRows < a.rows ? first + kRows : a.rows;
 
-    assign_rows<kWaves, kRw>(sh.len, sh.rows, a.row_ptr, a.rows, first, tid);
+    if (tid < 8) sh.w[kPadGene * 8 + tid] = make_uint4(0u, 0u, 0u, 0u);
+    if (tid == 8) sh.meta[kPadGene] = make_float2(0.0f, 0.0f);
+    assign_groups<kWaves, kLayers>(sh.u.len, sh.rows, a.row_ptr, a.rows, first, tid);
 
-    // Matrix totals (window loads stop at them).
-    const int nnz = __builtin_amdgcn_readfirstlane(a.row_ptr[a.rows]);
-    const int nbytes = __builtin_amdgcn_readfirstlane(a.packed_row_ptr[a.rows]);
+    // The block's entries and packed bytes, addressed by 32-bit buffer offsets.
+    const int wg_begin = __builtin_amdgcn_readfirstlane(a.row_ptr[first]);
+    const int wg_end = __builtin_amdgcn_readfirstlane(a.row_ptr[last]);
+    const int pk_al = __builtin_amdgcn_readfirstlane(a.packed_row_ptr[first]) & ~3;
+    const int pk_end = __builtin_amdgcn_readfirstlane(a.packed_row_ptr[last]);
+    const bool fits = wg_end - wg_begin < (1 << 27);  // bit offsets of the codes stay below 2^31
+    // A window reads up to 63 entries (and their code bytes) past the block's last entry:
+    // the ranges extend that far where the arrays do. In the block whose ranges stop at an
+    // array's end (`tail`), windows that reach past it are reloaded dword by dword and byte
+    // by byte, so no valid entry shares a multi-dword load with bytes outside the range.
+    const int nnz_all = __builtin_amdgcn_readfirstlane(a.row_ptr[a.rows]);
+    const int pk_all = __builtin_amdgcn_readfirstlane(a.packed_row_ptr[a.rows]);
+    const int col_n = nnz_all - wg_end < 72 ? nnz_all - wg_begin : wg_end - wg_begin + 72;
+    const int pk_n = pk_all - pk_end < 128 ? pk_all - pk_al : pk_end - pk_al + 128;
+    const bool tail = nnz_all - wg_end < 72 || pk_all - pk_end < 128;
+    const std::uint32_t col_lim = fits ? static_cast<std::uint32_t>(col_n) * 4u : 0u;
+    const std::uint32_t pk_lim = fits ? static_cast<std::uint32_t>(pk_n) : 0u;
+    const rsrc_t rc = make_rsrc(a.col_idx + wg_begin, col_lim);
+    const rsrc_t rp = make_rsrc(a.packed + pk_al, pk_lim);
 
-    // Per-row state (wave-uniform, kept in scalar registers): cursor, end, window base,
-    // packed byte of the window base, row offset (column-scale/row-offset decode).
-    int cur[kRw], end[kRw], base[kRw], pb[kRw];
-    float roff[kRw];
-    float acc[kRw][8];
-    Window win[kRw];
-#pragma unroll
-    for (int rw = 0; rw < kRw; ++rw) {
-        const std::uint32_t row = __builtin_amdgcn_readfirstlane(sh.rows[wave * kRw + rw]);
-        cur[rw] = end[rw] = pb[rw] = 0;
-        roff[rw] = 0.0f;
-        if (row != kNoRow) {
-            cur[rw] = __builtin_amdgcn_readfirstlane(a.row_ptr[row]);
-            end[rw] = __builtin_amdgcn_readfirstlane(a.row_ptr[row + 1]);
-            pb[rw] = __builtin_amdgcn_readfirstlane(a.packed_row_ptr[row]);
-            if constexpr (kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET)
-                roff[rw] = a.row_offsets != nullptr
-                    ? __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(a.row_offsets[row])))
-                    : 0.0f;
+    // Per layer (values uniform within the lane group): cursor and end relative to the
+    // block's first entry, bit offset q of the codes (entry e's code starts at bit
+    // q + e * kBits of the block's aligned packed bytes), row offset.
+    float acc[kLayers][8];
+    std::uint32_t colw[kLayers][8];
+    std::uint32_t cw[kLayers][kCodeDw];
+    int cur[kLayers], end[kLayers], q[kLayers];
+    float roff[kLayers];
+    std::uint32_t broken = 0u;  // bit l: layer l's row placed a run entry outside its part
+
+    auto load_window = [&](int l) {
+        const std::uint32_t e0 = static_cast<std::uint32_t>(cur[l] + 8 * j);
+        const auto c0 = __builtin_amdgcn_raw_buffer_load_b128(rc, e0 * 4u, 0, 0);
+        const auto c1 = __builtin_amdgcn_raw_buffer_load_b128(rc, e0 * 4u + 16u, 0, 0);
+        colw[l][0] = c0[0]; colw[l][1] = c0[1]; colw[l][2] = c0[2]; colw[l][3] = c0[3];
+        colw[l][4] = c1[0]; colw[l][5] = c1[1]; colw[l][6] = c1[2]; colw[l][7] = c1[3];
+        const std::uint32_t al = ((static_cast<std::uint32_t>(q[l]) + e0 * kBits) >> 3) & ~3u;
+        if constexpr (kCodeDw == 2) {
+            const auto c = __builtin_amdgcn_raw_buffer_load_b64(rp, al, 0, 0);
+            cw[l][0] = c[0]; cw[l][1] = c[1];
+        } else {
+            const auto c = __builtin_amdgcn_raw_buffer_load_b96(rp, al, 0, 0);
+            cw[l][0] = c[0]; cw[l][1] = c[1]; cw[l][2] = c[2];
         }
-        base[rw] = cur[rw];
+    };
+
+    // Tail block only: reload layer l's window with single-dword / single-byte loads when
+    // some lane's multi-dword loads reach past the array ends.
+    auto fix_tail = [&](int l) {
+        const std::uint32_t e0 = static_cast<std::uint32_t>(cur[l] + 8 * j);
+        const std::uint32_t al = ((static_cast<std::uint32_t>(q[l]) + e0 * kBits) >> 3) & ~3u;
+        if (__builtin_amdgcn_ballot_w64(e0 * 4u + 32u > col_lim || al + 4u * kCodeDw > pk_lim) == 0u) return;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) acc[rw][k] = 0.0f;
-        win[rw].col = kNoGene;
-        win[rw].byte = 0u;
-        if (cur[rw] < end[rw]) load_window<kBits>(win[rw], a, base[rw], pb[rw], lane, nnz, nbytes);
+        for (int k = 0; k < 8; ++k)
+            colw[l][k] = static_cast<std::uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rc, (e0 + k) * 4u, 0, 0));
+#pragma unroll
+        for (int d = 0; d < kCodeDw; ++d) {
+            std::uint32_t v = 0u;
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                v |= static_cast<std::uint32_t>(__builtin_amdgcn_raw_buffer_load_b8(rp, al + 4u * d + b, 0, 0)) << (8 * b);
+            cw[l][d] = v;
+        }
+    };
+
+#pragma unroll
+    for (int l = 0; l < kLayers; ++l) {
+        const std::uint32_t row = sh.rows[(wave * kLayers + l) * 8 + grp];
+        cur[l] = end[l] = q[l] = 0;
+        roff[l] = 0.0f;
+        if (row != kNoRow && fits) {
+            const int b = a.row_ptr[row];
+            cur[l] = b - wg_begin;
+            end[l] = a.row_ptr[row + 1] - wg_begin;
+            q[l] = (a.packed_row_ptr[row] - pk_al) * 8 - cur[l] * kBits;
+            if constexpr (kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET)
+                roff[l] = a.row_offsets != nullptr ? a.row_offsets[row] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[l][k] = 0.0f;
+        load_window(l);
     }
 
     const char *wbase = reinterpret_cast<const char *>(sh.w) + j * 16;
-
-    // Run of row rw's window lanes from the cursor whose genes lie in [lo, lo + span), cut
-    // at the row end: window lanes [start, start + cnt); g = gene - lo per lane.
-    auto segment = [&](int rw, int lo, std::uint32_t span, int &start, int &cnt, std::uint32_t &g) {
-        start = cur[rw] - base[rw];  // 0 <= start < 64
-        g = win[rw].col - static_cast<std::uint32_t>(lo);
-        const std::uint64_t run = ~(__builtin_amdgcn_ballot_w64(g < span) >> start);
-        const int in_run = run == 0u ? kWave - start : __builtin_ctzll(run);
-        cnt = in_run < end[rw] - cur[rw] ? in_run : end[rw] - cur[rw];
-    };
-    // Decodes the run into stage slot `slot`: (LDS byte offset of the weight row, value).
-    auto decode = [&](int rw, int slot, int start, int cnt, std::uint32_t g) {
-        if (static_cast<std::uint32_t>(lane - start) < static_cast<std::uint32_t>(cnt)) {
-            const float2 md = sh.meta[g];
-            const float code = static_cast<float>((win[rw].byte >> code_shift) & ((1u << kBits) - 1u));
-            const float off = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET ? roff[rw] : md.y;
-            sh.stage[wave][slot][lane] = make_int2(static_cast<int>(g) * 128,
-                                                   __float_as_int(__builtin_fmaf(code, md.x, off)));
-        }
-    };
-    // `pairs` two-entry steps from ep, then the run's last cnt % 16 entries: lane group grp
-    // takes staged entry s + grp, lane j reads 16 B of its weight row.
-    auto steps = [&](int rw, const int2 *ep, int pairs, int cnt) {
-        for (int k = pairs; k > 0; --k, ep += 16) {
-            const int2 e0 = ep[0], e1 = ep[8];
-            const uint4 w0 = *reinterpret_cast<const uint4 *>(wbase + e0.x);
-            const uint4 w1 = *reinterpret_cast<const uint4 *>(wbase + e1.x);
-            fma8(acc[rw], __int_as_float(e0.y), w0);
-            fma8(acc[rw], __int_as_float(e1.y), w1);
-        }
-        if ((cnt & 8) != 0) {
-            const int2 e = ep[0];
-            fma8(acc[rw], __int_as_float(e.y), *reinterpret_cast<const uint4 *>(wbase + e.x));
-            ep += 8;
-        }
-        if (grp < (cnt & 7)) {
-            const int2 e = ep[0];
-            fma8(acc[rw], __int_as_float(e.y), *reinterpret_cast<const uint4 *>(wbase + e.x));
-        }
-    };
-    // Moves row rw's cursor past a run ending at window lane `stop`; when the run used the
-    // window up inside the part, loads the next 64 entries and returns true.
-    auto advance = [&](int rw, int stop, int cnt) -> bool {
-        cur[rw] += cnt;
-        if (stop < kWave || cur[rw] >= end[rw]) return false;
-        base[rw] = cur[rw];
-        pb[rw] += kWave / kCpb;
-        load_window<kBits>(win[rw], a, base[rw], pb[rw], lane, nnz, nbytes);
-        return true;
-    };
-    // The rest of row rw's part after a window reload, one row at a time.
-    auto visit_rest = [&](int rw, int lo, std::uint32_t span) {
-        for (;;) {
-            int start, cnt;
-            std::uint32_t g;
-            segment(rw, lo, span, start, cnt, g);
-            if (cnt == 0) return;
-            decode(rw, 0, start, cnt, g);
-            wave_sync();
-            steps(rw, &sh.stage[wave][0][start + grp], cnt >> 4, cnt);
-            wave_sync();
-            if (!advance(rw, start + cnt, cnt)) return;
-        }
-    };
-
-    // Refills row rw's window for the next part when fewer than kRefill entries are left
-    // (from the cursor rounded down to a code byte). Issued right after the row's visit, the
-    // loads write the window registers directly and complete behind the rest of the part.
-    auto refill = [&](int rw) {
-        if (base[rw] + kWave < end[rw] && base[rw] + kWave - cur[rw] < kRefill) {
-            const int step = (cur[rw] - base[rw]) / kCpb;
-            base[rw] += step * kCpb;
-            pb[rw] += step;
-            load_window<kBits>(win[rw], a, base[rw], pb[rw], lane, nnz, nbytes);
-        }
-    };
+    const char *mbase = reinterpret_cast<const char *>(sh.meta);
+    uint4 *sp = &sh.u.stage[wave][grp][0];
 
     const int cols = static_cast<int>(a.cols);
     const int parts = (cols + kPartGenes - 1) / kPartGenes;
@@ -356,60 +367,105 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_parts(QcsrArgs a) {
         const int lo = part * kPartGenes;
         const int hi = lo + kPartGenes < cols ? lo + kPartGenes : cols;
         const std::uint32_t span = static_cast<std::uint32_t>(hi - lo);
+        const std::uint32_t uhi = static_cast<std::uint32_t>(hi);
         __syncthreads();  // every wave is done reading part - 1
-        load_part<kPolicy, kWaves>(sh, a, lo, hi, wave, lane, tid);  // also completes the refills
+        load_part<kPolicy, kWaves>(sh, a, lo, hi, wave, lane, tid);  // also completes the window loads
         __syncthreads();
-        // Rows are visited in pairs so two independent decode / step chains are in flight.
 #pragma unroll
-        for (int ra = 0; ra < kRw; ra += 2) {
-            const int rb = ra + 1;
-            int sa = 0, ca = 0, sb = 0, cb = 0;
-            std::uint32_t ga = 0u, gb = 0u;
-            if (cur[ra] < end[ra]) segment(ra, lo, span, sa, ca, ga);
-            if (cur[rb] < end[rb]) segment(rb, lo, span, sb, cb, gb);
-            decode(ra, 0, sa, ca, ga);
-            decode(rb, 1, sb, cb, gb);
-            wave_sync();
-            const int2 *epa = &sh.stage[wave][0][sa + grp];
-            const int2 *epb = &sh.stage[wave][1][sb + grp];
-            const int ka = ca >> 4, kb = cb >> 4;
-            const int kk = ka < kb ? ka : kb;
-            for (int k = kk; k > 0; --k, epa += 16, epb += 16) {
-                const int2 a0 = epa[0], a1 = epa[8], b0 = epb[0], b1 = epb[8];
-                const uint4 wa0 = *reinterpret_cast<const uint4 *>(wbase + a0.x);
-                const uint4 wa1 = *reinterpret_cast<const uint4 *>(wbase + a1.x);
-                const uint4 wb0 = *reinterpret_cast<const uint4 *>(wbase + b0.x);
-                const uint4 wb1 = *reinterpret_cast<const uint4 *>(wbase + b1.x);
-                fma8(acc[ra], __int_as_float(a0.y), wa0);
-                fma8(acc[rb], __int_as_float(b0.y), wb0);
-                fma8(acc[ra], __int_as_float(a1.y), wa1);
-                fma8(acc[rb], __int_as_float(b1.y), wb1);
+        for (int l = 0; l < kLayers; ++l) {
+            for (;;) {
+                if (tail) fix_tail(l);
+                // the run: window entries with column < hi, entries past the row end excluded
+                const int nv = end[l] - cur[l] - 8 * j;
+                int n = 0;
+                if (__builtin_amdgcn_ballot_w64(nv < 8) == 0u) {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) n += colw[l][k] < uhi ? 1 : 0;
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) n += k < nv && colw[l][k] < uhi ? 1 : 0;
+                }
+                const int run = group_sum8i(n);
+                const int rmax = wave_max_groups(run);
+                const std::uint32_t bp = static_cast<std::uint32_t>(q[l]) + static_cast<std::uint32_t>(cur[l] + 8 * j) * kBits;
+                const std::uint32_t c0 = __builtin_amdgcn_alignbit(cw[l][1], cw[l][0], bp & 31u);
+                std::uint32_t c1 = 0u;
+                if constexpr (kCodeDw == 3) c1 = __builtin_amdgcn_alignbit(cw[l][2], cw[l][1], bp & 31u);
+                int okc = 0;
+#pragma unroll
+                for (int f = 0; f < 4; ++f) {
+                    if (2 * f >= rmax) break;
+                    std::uint32_t st[4];
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) {
+                        const int k = 2 * f + r;
+                        const std::uint32_t gk = colw[l][k] - static_cast<std::uint32_t>(lo);
+                        const bool ok = 8 * j + k < run && gk < span;
+                        okc += ok ? 1 : 0;
+                        const std::uint32_t gg = ok ? gk : static_cast<std::uint32_t>(kPadGene);
+                        const float2 md = *reinterpret_cast<const float2 *>(mbase + gg * 8u);
+                        std::uint32_t code;
+                        if constexpr (kBits == 8) code = ((k < 4 ? c0 : c1) >> (8 * (k & 3))) & 0xffu;
+                        else code = (c0 >> (k * kBits)) & kMask;
+                        const float off = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET ? roff[l] : md.y;
+                        const float x = ok ? __builtin_fmaf(static_cast<float>(code), md.x, off) : 0.0f;
+                        st[2 * r] = gg * 8u;
+                        st[2 * r + 1] = __float_as_uint(x);
+                    }
+                    sp[j] = make_uint4(st[0], st[1], st[2], st[3]);
+                    const int n2 = (fill_count(rmax, f) + 1) >> 1;
+                    int it = 0;
+                    for (; it + 2 <= n2; it += 2) {
+                        const uint4 ea = sp[it], eb = sp[it + 1];
+                        const uint4 wa0 = *reinterpret_cast<const uint4 *>(wbase + (ea.x << 4));
+                        const uint4 wa1 = *reinterpret_cast<const uint4 *>(wbase + (ea.z << 4));
+                        const uint4 wb0 = *reinterpret_cast<const uint4 *>(wbase + (eb.x << 4));
+                        const uint4 wb1 = *reinterpret_cast<const uint4 *>(wbase + (eb.z << 4));
+                        fma8(acc[l], __uint_as_float(ea.y), wa0);
+                        fma8(acc[l], __uint_as_float(ea.w), wa1);
+                        fma8(acc[l], __uint_as_float(eb.y), wb0);
+                        fma8(acc[l], __uint_as_float(eb.w), wb1);
+                    }
+                    if (it < n2) {
+                        const uint4 e = sp[it];
+                        const uint4 w0 = *reinterpret_cast<const uint4 *>(wbase + (e.x << 4));
+                        const uint4 w1 = *reinterpret_cast<const uint4 *>(wbase + (e.z << 4));
+                        fma8(acc[l], __uint_as_float(e.y), w0);
+                        fma8(acc[l], __uint_as_float(e.w), w1);
+                    }
+                }
+                const int in_run = run - 8 * j < 0 ? 0 : (run - 8 * j > 8 ? 8 : run - 8 * j);
+                if (okc != in_run) broken |= 1u << l;
+                cur[l] += run;
+                const bool more = __builtin_amdgcn_ballot_w64(run == 64 && cur[l] < end[l]) != 0u;
+                load_window(l);
+                if (!more) break;
             }
-            steps(ra, epa, ka - kk, ca);
-            steps(rb, epb, kb - kk, cb);
-            wave_sync();
-            const bool more_a = ca > 0 && advance(ra, sa + ca, ca);
-            const bool more_b = cb > 0 && advance(rb, sb + cb, cb);
-            if (more_a) visit_rest(ra, lo, span);
-            if (more_b) visit_rest(rb, lo, span);
-            refill(ra);
-            refill(rb);
         }
     }
 
-    const int col = scatter_column(lane);
 #pragma unroll
-    for (int rw = 0; rw < kRw; ++rw) {
-        const std::uint32_t row = __builtin_amdgcn_readfirstlane(sh.rows[wave * kRw + rw]);
-        if (row == kNoRow) continue;
-        if (cur[rw] < end[rw]) {
-            // unfinished: recompute the row on the plain path (lane = column)
-            const float v = row_fallback<kBits, kPolicy>(a, row, lane);
-            a.out[static_cast<std::int64_t>(row) * a.out_ld + lane] = a.ep.active ? epilogue_value(a.ep, v, row, lane) : v;
-            continue;
+    for (int l = 0; l < kLayers; ++l) {
+        const std::uint32_t row = sh.rows[(wave * kLayers + l) * 8 + grp];
+        const int bad = group_sum8i(((broken >> l) & 1u) != 0u || cur[l] != end[l] || !fits ? 1 : 0);
+        if (row != kNoRow && bad == 0) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                v[k] = a.ep.active ? epilogue_value(a.ep, acc[l][k], row, 8 * j + k) : acc[l][k];
+            float4 *o = reinterpret_cast<float4 *>(a.out + static_cast<std::int64_t>(row) * a.out_ld + 8 * j);
+            o[0] = make_float4(v[0], v[1], v[2], v[3]);
+            o[1] = make_float4(v[4], v[5], v[6], v[7]);
         }
-        const float v = reduce_scatter(acc[rw], lane);
-        a.out[static_cast<std::int64_t>(row) * a.out_ld + col] = a.ep.active ? epilogue_value(a.ep, v, row, col) : v;
+        // unfinished rows: recompute on the plain path (lane = column), one row at a time
+        std::uint64_t todo = __builtin_amdgcn_ballot_w64(j == 0 && row != kNoRow && bad != 0);
+        while (todo != 0u) {
+            const int g = __builtin_ctzll(todo) >> 3;
+            todo &= todo - 1u;
+            const std::uint32_t r = sh.rows[(wave * kLayers + l) * 8 + g];
+            const float v = row_fallback<kBits, kPolicy>(a, r, lane);
+            a.out[static_cast<std::int64_t>(r) * a.out_ld + lane] = a.ep.active ? epilogue_value(a.ep, v, r, lane) : v;
+        }
     }
 }
 
@@ -614,21 +670,21 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_bwd_values_parts(BwdParts
 }
 
 template<int kBits, int kPolicy>
-int launch_bits_parts(const QcsrArgs &a, hipStream_t stream) {
-    constexpr int kWaves = 16, kRw = 8;
-    const unsigned rows_per_block = kWaves * kRw;
+int launch_bits_groups(const QcsrArgs &a, hipStream_t stream) {
+    constexpr int kWaves = 16, kLayers = 4;
+    const unsigned rows_per_block = kWaves * kLayers * 8;
     const dim3 grid((a.rows + rows_per_block - 1) / rows_per_block), block(kWaves * kWave);
-    hipLaunchKernelGGL((qcsr_spmm_parts<kBits, kPolicy, kWaves, kRw>), grid, block, 0, stream, a);
-    return check_launch("qcsr_spmm_parts");
+    hipLaunchKernelGGL((qcsr_spmm_groups<kBits, kPolicy, kWaves, kLayers>), grid, block, 0, stream, a);
+    return check_launch("qcsr_spmm_groups");
 }
 
 template<int kPolicy>
 int launch_policy_parts(const QcsrArgs &a, std::uint32_t bits, hipStream_t stream) {
     switch (bits) {
-    case 1: return launch_bits_parts<1, kPolicy>(a, stream);
-    case 2: return launch_bits_parts<2, kPolicy>(a, stream);
-    case 4: return launch_bits_parts<4, kPolicy>(a, stream);
-    default: return launch_bits_parts<8, kPolicy>(a, stream);
+    case 1: return launch_bits_groups<1, kPolicy>(a, stream);
+    case 2: return launch_bits_groups<2, kPolicy>(a, stream);
+    case 4: return launch_bits_groups<4, kPolicy>(a, stream);
+    default: return launch_bits_groups<8, kPolicy>(a, stream);
     }
 }
 

@@ -149,7 +149,7 @@ typedef struct cx_qcsr_matrix {
  * (row stride rhs_ld, dtype F16 or F32; F16 widens exactly). fp32 multiply and
  * fp32 accumulation, deterministic (fixed per-row summation order). Quantized codes with
  * F16 RHS at out_cols = 64, 128, 192 or 256 stream RHS through LDS by gene part, 64 output
- * columns per launch: fastest with each row's columns ascending; rows out of order are
+ * columns per launch: fastest with each row's columns ascending; rows out of order across parts are
  * recomputed per row, and columns outside [0, cols) contribute nothing on that path.
  * Replaces csr_spmm_fwd_f16_f32 (src/compute/sparse/project/project.hh:12-23). */
 int cx_qcsr_spmm_fwd(const cx_qcsr_matrix *a, const void *rhs, uint32_t rhs_dtype,

@@ -1,13 +1,14 @@
-"""GPU parity of the gene-part quantized CSR kernel (qcsr_parts.hip).
+"""GPU parity of the gene-part quantized CSR kernels (qcsr_parts.hip).
 
-cx_qcsr_spmm_fwd takes this kernel for quantized codes with fp16 weights and N = 64: the
-weight panel is streamed through LDS in parts of 1,024 genes, each row keeps a cursor, and
-rows the part walk cannot finish (columns out of order across parts, or outside
-[0, cols)) are recomputed on a plain per-row path. These cases pin each of those paths
-against the float64 referee on the same inputs: many parts, rows longer than a 64-entry
-window inside one part, skewed row lengths across workgroups (the balanced row
-assignment), unsorted and duplicated columns, and out-of-range columns (which contribute
-nothing on this path).
+cx_qcsr_spmm_fwd takes the row-group kernel for quantized codes with fp16 weights and
+N = 64 (N = 128..256 in 64-column launches): the weight panel is streamed through LDS in
+parts of 1,024 genes, each 8-lane group owns a row with a 64-entry register window and a
+cursor, and rows the part walk cannot finish (columns out of order across parts, or
+outside [0, cols)) are recomputed on a plain per-row path. These cases pin each of those
+paths against the float64 referee on the same inputs: many parts, runs that fill whole
+windows inside one part, skewed row lengths within and across workgroups of 512 rows (the
+balanced row assignment), windows at the ends of the column and code arrays, unsorted and
+duplicated columns, and out-of-range columns (which contribute nothing on this path).
 """
 from __future__ import annotations
 
@@ -67,11 +68,36 @@ def _rebuild(oracle, rng, fx, row_ptr, col_idx):
 
 @pytest.mark.parametrize("bits,policy", [(4, 1), (8, 1), (2, 2), (1, 1)])
 def test_many_parts_skewed_rows(oracle, bits, policy):
-    """5 parts (the last one partial), 3 workgroups of 128 rows plus a ragged one, rows from
-    empty to all 4,700 genes (windows refilled inside a part)."""
+    """5 parts (the last one partial), one ragged workgroup, rows from empty to all 4,700
+    genes (windows reloaded inside a part)."""
     rng = np.random.default_rng(900 + bits * 10 + policy)
     fx = _skewed_fixture(oracle, rng, 400, 4700, bits, policy)
     rhs = (rng.standard_normal((4700, 64)) * 0.02).astype(np.float16)
+    ref, mag = _referee(oracle, fx, rhs)
+    check_against_referee(oracle, ref, mag, _run(to_device_qcsr(fx), rhs))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_many_workgroups_long_last_rows(oracle, bits):
+    """1,300 rows: workgroups of 512, 512 and 276 rows. The last rows of the matrix are long
+    (whole-window runs inside a part, windows reaching the ends of the column and code
+    arrays, code tails ending inside a byte), so block-end and array-end window loads
+    are both exercised."""
+    rng = np.random.default_rng(971 + bits)
+    rows, cols = 1300, 2600
+    fx = quantized_fixture(oracle, rng, rows, cols, 10.0, bits, 1)
+    lengths = np.minimum(rng.lognormal(np.log(300.0), 0.9, rows).astype(np.int64), cols)
+    lengths[rng.choice(rows - 5, 40, replace=False)] = 0
+    lengths[510:514] = [cols, 0, 2049, 1]  # across the first block boundary
+    lengths[-5:] = [cols, 1777, 3, cols - 1, 1501]
+    row_ptr = np.zeros(rows + 1, np.int64)
+    row_ptr[1:] = np.cumsum(lengths)
+    col_idx = np.empty(int(row_ptr[-1]), np.int32)
+    for r in range(rows):
+        if lengths[r]:
+            col_idx[row_ptr[r]:row_ptr[r + 1]] = np.sort(rng.choice(cols, lengths[r], replace=False))
+    fx = _rebuild(oracle, rng, fx, row_ptr.astype(np.int32), col_idx)
+    rhs = (rng.standard_normal((cols, 64)) * 0.02).astype(np.float16)
     ref, mag = _referee(oracle, fx, rhs)
     check_against_referee(oracle, ref, mag, _run(to_device_qcsr(fx), rhs))
 
