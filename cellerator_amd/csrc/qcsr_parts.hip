@@ -304,12 +304,13 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
     float roff[kLayers];
     std::uint32_t broken = 0u;  // bit l: layer l's row placed a run entry outside its part
 
-    auto load_window = [&](int l) {
-        const std::uint32_t e0 = static_cast<std::uint32_t>(cur[l] + 8 * j);
-        const auto c0 = __builtin_amdgcn_raw_buffer_load_b128(rc, e0 * 4u, 0, 0);
-        const auto c1 = __builtin_amdgcn_raw_buffer_load_b128(rc, e0 * 4u + 16u, 0, 0);
-        colw[l][0] = c0[0]; colw[l][1] = c0[1]; colw[l][2] = c0[2]; colw[l][3] = c0[3];
-        colw[l][4] = c1[0]; colw[l][5] = c1[1]; colw[l][6] = c1[2]; colw[l][7] = c1[3];
+    // Window of layer l at entry offset e0 = cursor + 8j: column slots 4h..4h+3 (h = 0, 1)
+    // and the dwords holding the 8 entries' codes.
+    auto load_cols = [&](int l, int h, std::uint32_t e0) {
+        const auto c = __builtin_amdgcn_raw_buffer_load_b128(rc, e0 * 4u + 16u * h, 0, 0);
+        colw[l][4 * h] = c[0]; colw[l][4 * h + 1] = c[1]; colw[l][4 * h + 2] = c[2]; colw[l][4 * h + 3] = c[3];
+    };
+    auto load_codes = [&](int l, std::uint32_t e0) {
         const std::uint32_t al = ((static_cast<std::uint32_t>(q[l]) + e0 * kBits) >> 3) & ~3u;
         if constexpr (kCodeDw == 2) {
             const auto c = __builtin_amdgcn_raw_buffer_load_b64(rp, al, 0, 0);
@@ -318,6 +319,12 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
             const auto c = __builtin_amdgcn_raw_buffer_load_b96(rp, al, 0, 0);
             cw[l][0] = c[0]; cw[l][1] = c[1]; cw[l][2] = c[2];
         }
+    };
+    auto load_window = [&](int l) {
+        const std::uint32_t e0 = static_cast<std::uint32_t>(cur[l] + 8 * j);
+        load_cols(l, 0, e0);
+        load_cols(l, 1, e0);
+        load_codes(l, e0);
     };
 
     // Tail block only: reload layer l's window with single-dword / single-byte loads when
@@ -391,54 +398,72 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
                 const std::uint32_t c0 = __builtin_amdgcn_alignbit(cw[l][1], cw[l][0], bp & 31u);
                 std::uint32_t c1 = 0u;
                 if constexpr (kCodeDw == 3) c1 = __builtin_amdgcn_alignbit(cw[l][2], cw[l][1], bp & 31u);
+                // The next window starts at the new cursor, known now. Its code dwords are
+                // reloaded at once (this pass's codes are extracted above), its column slots
+                // 0-3 once fill 1 has decoded them and slots 4-7 once fill 3 has: in a pass
+                // that continues, the loads complete behind the remaining fills.
+                const int next = cur[l] + run;
+                const std::uint32_t e1 = static_cast<std::uint32_t>(next + 8 * j);
+                load_codes(l, e1);
                 int okc = 0;
 #pragma unroll
                 for (int f = 0; f < 4; ++f) {
-                    if (2 * f >= rmax) break;
-                    std::uint32_t st[4];
+                    const bool live = 2 * f < rmax;
+                    if (live) {
+                        std::uint32_t st[4];
 #pragma unroll
-                    for (int r = 0; r < 2; ++r) {
-                        const int k = 2 * f + r;
-                        const std::uint32_t gk = colw[l][k] - static_cast<std::uint32_t>(lo);
-                        const bool ok = 8 * j + k < run && gk < span;
-                        okc += ok ? 1 : 0;
-                        const std::uint32_t gg = ok ? gk : static_cast<std::uint32_t>(kPadGene);
-                        const float2 md = *reinterpret_cast<const float2 *>(mbase + gg * 8u);
-                        std::uint32_t code;
-                        if constexpr (kBits == 8) code = ((k < 4 ? c0 : c1) >> (8 * (k & 3))) & 0xffu;
-                        else code = (c0 >> (k * kBits)) & kMask;
-                        const float off = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET ? roff[l] : md.y;
-                        const float x = ok ? __builtin_fmaf(static_cast<float>(code), md.x, off) : 0.0f;
-                        st[2 * r] = gg * 8u;
-                        st[2 * r + 1] = __float_as_uint(x);
+                        for (int r = 0; r < 2; ++r) {
+                            const int k = 2 * f + r;
+                            const std::uint32_t gk = colw[l][k] - static_cast<std::uint32_t>(lo);
+                            const bool ok = 8 * j + k < run && gk < span;
+                            okc += ok ? 1 : 0;
+                            const std::uint32_t gg = ok ? gk : static_cast<std::uint32_t>(kPadGene);
+                            const float2 md = *reinterpret_cast<const float2 *>(mbase + gg * 8u);
+                            std::uint32_t code;
+                            if constexpr (kBits == 8) code = ((k < 4 ? c0 : c1) >> (8 * (k & 3))) & 0xffu;
+                            else code = (c0 >> (k * kBits)) & kMask;
+                            const float off = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET ? roff[l] : md.y;
+                            const float x = ok ? __builtin_fmaf(static_cast<float>(code), md.x, off) : 0.0f;
+                            st[2 * r] = gg * 8u;
+                            st[2 * r + 1] = __float_as_uint(x);
+                        }
+                        sp[j] = make_uint4(st[0], st[1], st[2], st[3]);
                     }
-                    sp[j] = make_uint4(st[0], st[1], st[2], st[3]);
-                    const int n2 = (fill_count(rmax, f) + 1) >> 1;
-                    int it = 0;
-                    for (; it + 2 <= n2; it += 2) {
-                        const uint4 ea = sp[it], eb = sp[it + 1];
-                        const uint4 wa0 = *reinterpret_cast<const uint4 *>(wbase + (ea.x << 4));
-                        const uint4 wa1 = *reinterpret_cast<const uint4 *>(wbase + (ea.z << 4));
-                        const uint4 wb0 = *reinterpret_cast<const uint4 *>(wbase + (eb.x << 4));
-                        const uint4 wb1 = *reinterpret_cast<const uint4 *>(wbase + (eb.z << 4));
-                        fma8(acc[l], __uint_as_float(ea.y), wa0);
-                        fma8(acc[l], __uint_as_float(ea.w), wa1);
-                        fma8(acc[l], __uint_as_float(eb.y), wb0);
-                        fma8(acc[l], __uint_as_float(eb.w), wb1);
-                    }
-                    if (it < n2) {
-                        const uint4 e = sp[it];
-                        const uint4 w0 = *reinterpret_cast<const uint4 *>(wbase + (e.x << 4));
-                        const uint4 w1 = *reinterpret_cast<const uint4 *>(wbase + (e.z << 4));
-                        fma8(acc[l], __uint_as_float(e.y), w0);
-                        fma8(acc[l], __uint_as_float(e.w), w1);
+                    if (f == 1) load_cols(l, 0, e1);
+                    if (f == 3) load_cols(l, 1, e1);
+                    if (live) {
+                        // pairs of stage slots, two pairs per iteration; an odd last slot alone
+                        const int cnt = fill_count(rmax, f);
+                        const int n2 = cnt >> 1;
+                        int it = 0;
+                        for (; it + 2 <= n2; it += 2) {
+                            const uint4 ea = sp[it], eb = sp[it + 1];
+                            const uint4 wa0 = *reinterpret_cast<const uint4 *>(wbase + (ea.x << 4));
+                            const uint4 wa1 = *reinterpret_cast<const uint4 *>(wbase + (ea.z << 4));
+                            const uint4 wb0 = *reinterpret_cast<const uint4 *>(wbase + (eb.x << 4));
+                            const uint4 wb1 = *reinterpret_cast<const uint4 *>(wbase + (eb.z << 4));
+                            fma8(acc[l], __uint_as_float(ea.y), wa0);
+                            fma8(acc[l], __uint_as_float(ea.w), wa1);
+                            fma8(acc[l], __uint_as_float(eb.y), wb0);
+                            fma8(acc[l], __uint_as_float(eb.w), wb1);
+                        }
+                        if (it < n2) {
+                            const uint4 e = sp[it];
+                            const uint4 w0 = *reinterpret_cast<const uint4 *>(wbase + (e.x << 4));
+                            const uint4 w1 = *reinterpret_cast<const uint4 *>(wbase + (e.z << 4));
+                            fma8(acc[l], __uint_as_float(e.y), w0);
+                            fma8(acc[l], __uint_as_float(e.w), w1);
+                        }
+                        if ((cnt & 1) != 0) {
+                            const uint2 e = reinterpret_cast<const uint2 *>(sp)[cnt - 1];
+                            fma8(acc[l], __uint_as_float(e.y), *reinterpret_cast<const uint4 *>(wbase + (e.x << 4)));
+                        }
                     }
                 }
                 const int in_run = run - 8 * j < 0 ? 0 : (run - 8 * j > 8 ? 8 : run - 8 * j);
                 if (okc != in_run) broken |= 1u << l;
-                cur[l] += run;
+                cur[l] = next;
                 const bool more = __builtin_amdgcn_ballot_w64(run == 64 && cur[l] < end[l]) != 0u;
-                load_window(l);
                 if (!more) break;
             }
         }
