@@ -190,6 +190,7 @@ struct GroupsShared {
     float2 meta[kPartGenes + 2];    // (scale, offset) per gene of the part; [kPadGene] = (0, 0)
     uint4 w[(kPartGenes + 1) * 8];  // fp16 weight rows of the part; row kPadGene is zeros
     std::uint32_t rows[kRows];      // row of (wave, layer, group)
+    int qbits[kWaves][kLayers][8];  // code bit offset q of (wave, layer, group): kept here, not in registers
 };
 
 // Rank the block's rows by length (descending, ties by index); ranks 8s .. 8s + 7 form row
@@ -300,9 +301,8 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
     float acc[kLayers][8];
     std::uint32_t colw[kLayers][8];
     std::uint32_t cw[kLayers][kCodeDw];
-    int cur[kLayers], end[kLayers], q[kLayers];
+    int cur[kLayers], end[kLayers];
     float roff[kLayers];
-    std::uint32_t broken = 0u;  // bit l: layer l's row placed a run entry outside its part
 
     // Window of layer l at entry offset e0 = cursor + 8j: column slots 4h..4h+3 (h = 0, 1)
     // and the dwords holding the 8 entries' codes.
@@ -310,8 +310,8 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
         const auto c = __builtin_amdgcn_raw_buffer_load_b128(rc, e0 * 4u + 16u * h, 0, 0);
         colw[l][4 * h] = c[0]; colw[l][4 * h + 1] = c[1]; colw[l][4 * h + 2] = c[2]; colw[l][4 * h + 3] = c[3];
     };
-    auto load_codes = [&](int l, std::uint32_t e0) {
-        const std::uint32_t al = ((static_cast<std::uint32_t>(q[l]) + e0 * kBits) >> 3) & ~3u;
+    auto load_codes = [&](int l, std::uint32_t e0, int q) {
+        const std::uint32_t al = ((static_cast<std::uint32_t>(q) + e0 * kBits) >> 3) & ~3u;
         if constexpr (kCodeDw == 2) {
             const auto c = __builtin_amdgcn_raw_buffer_load_b64(rp, al, 0, 0);
             cw[l][0] = c[0]; cw[l][1] = c[1];
@@ -320,18 +320,18 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
             cw[l][0] = c[0]; cw[l][1] = c[1]; cw[l][2] = c[2];
         }
     };
-    auto load_window = [&](int l) {
+    auto load_window = [&](int l, int q) {
         const std::uint32_t e0 = static_cast<std::uint32_t>(cur[l] + 8 * j);
         load_cols(l, 0, e0);
         load_cols(l, 1, e0);
-        load_codes(l, e0);
+        load_codes(l, e0, q);
     };
 
     // Tail block only: reload layer l's window with single-dword / single-byte loads when
     // some lane's multi-dword loads reach past the array ends.
     auto fix_tail = [&](int l) {
         const std::uint32_t e0 = static_cast<std::uint32_t>(cur[l] + 8 * j);
-        const std::uint32_t al = ((static_cast<std::uint32_t>(q[l]) + e0 * kBits) >> 3) & ~3u;
+        const std::uint32_t al = ((static_cast<std::uint32_t>(sh.qbits[wave][l][grp]) + e0 * kBits) >> 3) & ~3u;
         if (__builtin_amdgcn_ballot_w64(e0 * 4u + 32u > col_lim || al + 4u * kCodeDw > pk_lim) == 0u) return;
 #pragma unroll
         for (int k = 0; k < 8; ++k)
@@ -349,19 +349,21 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
 #pragma unroll
     for (int l = 0; l < kLayers; ++l) {
         const std::uint32_t row = sh.rows[(wave * kLayers + l) * 8 + grp];
-        cur[l] = end[l] = q[l] = 0;
+        cur[l] = end[l] = 0;
+        int q = 0;
         roff[l] = 0.0f;
         if (row != kNoRow && fits) {
             const int b = a.row_ptr[row];
             cur[l] = b - wg_begin;
             end[l] = a.row_ptr[row + 1] - wg_begin;
-            q[l] = (a.packed_row_ptr[row] - pk_al) * 8 - cur[l] * kBits;
+            q = (a.packed_row_ptr[row] - pk_al) * 8 - cur[l] * kBits;
             if constexpr (kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET)
                 roff[l] = a.row_offsets != nullptr ? a.row_offsets[row] : 0.0f;
         }
 #pragma unroll
         for (int k = 0; k < 8; ++k) acc[l][k] = 0.0f;
-        load_window(l);
+        if (j == 0) sh.qbits[wave][l][grp] = q;
+        load_window(l, q);
     }
 
     const char *wbase = reinterpret_cast<const char *>(sh.w) + j * 16;
@@ -394,7 +396,8 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
                 }
                 const int run = group_sum8i(n);
                 const int rmax = wave_max_groups(run);
-                const std::uint32_t bp = static_cast<std::uint32_t>(q[l]) + static_cast<std::uint32_t>(cur[l] + 8 * j) * kBits;
+                const int ql = sh.qbits[wave][l][grp];
+                const std::uint32_t bp = static_cast<std::uint32_t>(ql) + static_cast<std::uint32_t>(cur[l] + 8 * j) * kBits;
                 const std::uint32_t c0 = __builtin_amdgcn_alignbit(cw[l][1], cw[l][0], bp & 31u);
                 std::uint32_t c1 = 0u;
                 if constexpr (kCodeDw == 3) c1 = __builtin_amdgcn_alignbit(cw[l][2], cw[l][1], bp & 31u);
@@ -404,7 +407,7 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
                 // that continues, the loads complete behind the remaining fills.
                 const int next = cur[l] + run;
                 const std::uint32_t e1 = static_cast<std::uint32_t>(next + 8 * j);
-                load_codes(l, e1);
+                load_codes(l, e1, ql);
                 int okc = 0;
 #pragma unroll
                 for (int f = 0; f < 4; ++f) {
@@ -461,7 +464,7 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
                     }
                 }
                 const int in_run = run - 8 * j < 0 ? 0 : (run - 8 * j > 8 ? 8 : run - 8 * j);
-                if (okc != in_run) broken |= 1u << l;
+                if (okc != in_run) end[l] = -1;  // broken: no further runs; recomputed at the end
                 cur[l] = next;
                 const bool more = __builtin_amdgcn_ballot_w64(run == 64 && cur[l] < end[l]) != 0u;
                 if (!more) break;
@@ -472,7 +475,7 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
 #pragma unroll
     for (int l = 0; l < kLayers; ++l) {
         const std::uint32_t row = sh.rows[(wave * kLayers + l) * 8 + grp];
-        const int bad = group_sum8i(((broken >> l) & 1u) != 0u || cur[l] != end[l] || !fits ? 1 : 0);
+        const int bad = group_sum8i(cur[l] != end[l] || !fits ? 1 : 0);
         if (row != kNoRow && bad == 0) {
             float v[8];
 #pragma unroll
