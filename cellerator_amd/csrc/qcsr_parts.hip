@@ -19,17 +19,15 @@
 // Forward (qcsr_spmm_groups): lane group g (8 lanes) of a wave owns one row of each of the
 // wave's layers, and lane j of the group holds that row's output columns 8j..8j+7 in
 // registers, so a row costs 8 registers and a workgroup owns 512 rows (details at the
-// kernel). Backward values (qcsr_bwd_values_parts): all 8 lane groups of a wave work on one
-// row at a time, each group on a different entry, with the row's gradient in registers.
+// kernel). Backward values (qcsr_bwd_values_groups) use the same walk with the row's
+// gradient in place of the output sums.
 #include "qcsr_common.hpp"
 
 namespace cx {
 namespace {
 
 constexpr int kPartGenes = 1024;                 // 128 KB of fp16 weight rows per part
-constexpr std::uint32_t kNoGene = 0xffffffffu;   // never inside a part
 constexpr std::uint32_t kNoRow = 0xffffffffu;
-constexpr int kRefill = 48;                      // refill a row's window below this many
 
 using rsrc_t = __amdgpu_buffer_rsrc_t;
 
@@ -93,34 +91,6 @@ __device__ __forceinline__ void load_part(Shared &sh, const QcsrArgs &a, int lo,
         }
     }
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the LDS writes of the loads above
-}
-
-// Snake assignment of a block's rows to waves: rank the rows by length (descending, ties
-// by index) and deal rank r to slot r / kWaves of wave (r / kWaves even ? r % kWaves
-// : kWaves - 1 - r % kWaves), so every wave carries about the same number of nonzeros.
-template<int kWaves, int kRw>
-__device__ __forceinline__ void assign_rows(int *len, std::uint32_t *rows_out, const std::int32_t *row_ptr,
-                                            std::uint32_t rows, std::uint32_t first, int tid) {
-    constexpr int kBlockRows = kWaves * kRw;
-    if (tid < kBlockRows) {
-        const std::uint32_t row = first + static_cast<std::uint32_t>(tid);
-        len[tid] = row < rows ? row_ptr[row + 1] - row_ptr[row] : -1;
-    }
-    __syncthreads();
-    if (tid < kBlockRows) {
-        const int my = len[tid];
-        int rank = 0;
-#pragma unroll 4
-        for (int u = 0; u < kBlockRows; ++u) {
-            const int lu = len[u];
-            rank += lu > my || (lu == my && u < tid) ? 1 : 0;
-        }
-        const int round = rank / kWaves, pos = rank % kWaves;
-        const int w = (round & 1) != 0 ? kWaves - 1 - pos : pos;
-        const std::uint32_t row = first + static_cast<std::uint32_t>(tid);
-        rows_out[w * kRw + round] = row < rows ? row : kNoRow;
-    }
-    __syncthreads();
 }
 
 __device__ __forceinline__ void fma8(float (&p)[8], float x, uint4 w) {
@@ -497,13 +467,15 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
     }
 }
 
-// ---- backward values: grad_values[i] = <G[row_i, :], W[col_i, :]> over 64 columns --------
+// ---- backward values in the row-group form -------------------------------------------------
 //
-// The same part walk without decode (the gradient does not depend on the stored values):
-// each wave keeps its rows' G (lane j: columns 8j..8j+7, fp32) in registers; lane group g
-// takes staged entry s + g, lane j multiplies its 8 columns with 16 B of the LDS weight
-// row, the group sums its 8 lanes (DPP), and the dots are staged and stored coalesced per
-// visit.
+// grad_values[i] = <G[row_i, :], W[col_i, :]> (64 columns) with the forward's row-group walk:
+// lane group g owns one row of each layer and lane j holds G[row, 8j..8j+7] in registers;
+// each pass counts the run, stages the run's weight-row offsets (pads: the zero row) in the
+// forward's four fills, and per stage slot every lane multiplies its 8 columns with 16 B of
+// the weight row; the 8 lanes' partial dots are summed (DPP) and lane j keeps the result
+// of window entry 8j + k in register k, so each lane stores the 8 consecutive results of
+// its own window slots (two 16-byte stores when the whole slot range is in the run).
 
 struct BwdPartsArgs {
     const std::int32_t *row_ptr;
@@ -517,26 +489,6 @@ struct BwdPartsArgs {
     std::uint32_t cols;
 };
 
-template<int kWaves, int kRw>
-struct BwdPartsShared {
-    uint4 w[kPartGenes * 8];          // [gene][16-byte quarter-rows]: fp16 weights
-    int stage[kWaves][2][kWave];      // per wave, two rows: LDS byte offset of the weight row
-    float dots[kWaves][2][kWave];     // per wave, two rows: the staged entries' results
-    int len[kWaves * kRw];
-    std::uint32_t rows[kWaves * kRw];
-};
-
-__device__ __forceinline__ float dot8(const float (&g)[8], uint4 w) {
-    const std::uint32_t words[4] = {w.x, w.y, w.z, w.w};
-    float d = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        d = __builtin_fmaf(g[2 * k], h2f(static_cast<std::uint16_t>(words[k] & 0xffffu)), d);
-        d = __builtin_fmaf(g[2 * k + 1], h2f(static_cast<std::uint16_t>(words[k] >> 16)), d);
-    }
-    return d;
-}
-
 // Sum over the 8 lanes of each lane group (quad xor 1, xor 2, then the half-row mirror).
 __device__ __forceinline__ float group_sum8(float d) {
     d += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(d), 0xB1, 0xf, 0xf, false));
@@ -545,101 +497,95 @@ __device__ __forceinline__ float group_sum8(float d) {
     return d;
 }
 
-template<int kWaves, int kRw>
-__global__ __launch_bounds__(kWaves * kWave) void qcsr_bwd_values_parts(BwdPartsArgs a) {
-    constexpr int kBlockRows = kWaves * kRw;
-    static_assert(kBlockRows <= kWaves * kWave && kRw <= kWave && kRw % 2 == 0, "bad part-kernel shape");
-    __shared__ BwdPartsShared<kWaves, kRw> sh;
+template<int kWaves, int kLayers>
+struct BwdGroupsShared {
+    static constexpr int kRows = kWaves * kLayers * 8;
+    union {
+        std::uint32_t stage[kWaves][8][20];  // per wave and lane group: 16 weight-row offsets (+16 B pad)
+        int len[kRows];                      // prologue: row lengths
+    } u;
+    uint4 w[(kPartGenes + 1) * 8];           // fp16 weight rows of the part; row kPadGene is zeros
+    std::uint32_t rows[kRows];
+};
+
+__device__ __forceinline__ float dot8x2(const float (&g)[8], uint4 w) {
+    float d0 = 0.0f, d1 = 0.0f;
+    d0 = __builtin_fmaf(g[0], h2f(static_cast<std::uint16_t>(w.x & 0xffffu)), d0);
+    d1 = __builtin_fmaf(g[1], h2f(static_cast<std::uint16_t>(w.x >> 16)), d1);
+    d0 = __builtin_fmaf(g[2], h2f(static_cast<std::uint16_t>(w.y & 0xffffu)), d0);
+    d1 = __builtin_fmaf(g[3], h2f(static_cast<std::uint16_t>(w.y >> 16)), d1);
+    d0 = __builtin_fmaf(g[4], h2f(static_cast<std::uint16_t>(w.z & 0xffffu)), d0);
+    d1 = __builtin_fmaf(g[5], h2f(static_cast<std::uint16_t>(w.z >> 16)), d1);
+    d0 = __builtin_fmaf(g[6], h2f(static_cast<std::uint16_t>(w.w & 0xffffu)), d0);
+    d1 = __builtin_fmaf(g[7], h2f(static_cast<std::uint16_t>(w.w >> 16)), d1);
+    return d0 + d1;
+}
+
+template<int kWaves, int kLayers>
+__global__ __launch_bounds__(kWaves * kWave) void qcsr_bwd_values_groups(BwdPartsArgs a) {
+    using Shared = BwdGroupsShared<kWaves, kLayers>;
+    constexpr int kRows = Shared::kRows;
+    __shared__ Shared sh;
     const int tid = static_cast<int>(threadIdx.x);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int lane = tid % kWave;
     const int grp = lane >> 3;
     const int j = lane & 7;
-    const std::uint32_t first = blockIdx.x * static_cast<std::uint32_t>(kBlockRows);
-    assign_rows<kWaves, kRw>(sh.len, sh.rows, a.row_ptr, a.rows, first, tid);
-    const int nnz = __builtin_amdgcn_readfirstlane(a.row_ptr[a.rows]);
+    const std::uint32_t first = blockIdx.x * static_cast<std::uint32_t>(kRows);
+    const std::uint32_t last = first + kRows < a.rows ? first + kRows : a.rows;
 
-    int cur[kRw], end[kRw], base[kRw];
-    float g[kRw][8];
-    std::uint32_t win[kRw];
-    auto load_cols = [&](int rw) {  // window: column indices of entries [base, base + 64)
-        const std::uint32_t ub = static_cast<std::uint32_t>(base[rw]);
-        const std::uint32_t n = static_cast<std::uint32_t>(nnz) - ub < kWave ? static_cast<std::uint32_t>(nnz) - ub : kWave;
-        win[rw] = static_cast<std::uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(
-            make_rsrc(a.col_idx + ub, n * 4u), lane * 4, 0, 0));
+    if (tid < 8) sh.w[kPadGene * 8 + tid] = make_uint4(0u, 0u, 0u, 0u);
+    assign_groups<kWaves, kLayers>(sh.u.len, sh.rows, a.row_ptr, a.rows, first, tid);
+
+    const int wg_begin = __builtin_amdgcn_readfirstlane(a.row_ptr[first]);
+    const int wg_end = __builtin_amdgcn_readfirstlane(a.row_ptr[last]);
+    const bool fits = wg_end - wg_begin < (1 << 27);
+    // Windows read up to 63 entries past the block (where the array goes on); the tail
+    // block reloads windows that reach past the array end a dword at a time.
+    const int nnz_all = __builtin_amdgcn_readfirstlane(a.row_ptr[a.rows]);
+    const int col_n = nnz_all - wg_end < 72 ? nnz_all - wg_begin : wg_end - wg_begin + 72;
+    const bool tail = nnz_all - wg_end < 72;
+    const std::uint32_t col_lim = fits ? static_cast<std::uint32_t>(col_n) * 4u : 0u;
+    const rsrc_t rc = make_rsrc(a.col_idx + wg_begin, col_lim);
+    const rsrc_t ro = make_rsrc(a.grad_values + wg_begin, fits ? static_cast<std::uint32_t>(wg_end - wg_begin) * 4u : 0u);
+
+    float g[kLayers][8];
+    std::uint32_t colw[kLayers][8];
+    int cur[kLayers], end[kLayers];
+
+    auto load_cols = [&](int l, int h, std::uint32_t e0) {
+        const auto c = __builtin_amdgcn_raw_buffer_load_b128(rc, e0 * 4u + 16u * h, 0, 0);
+        colw[l][4 * h] = c[0]; colw[l][4 * h + 1] = c[1]; colw[l][4 * h + 2] = c[2]; colw[l][4 * h + 3] = c[3];
     };
+    auto fix_tail = [&](int l) {
+        const std::uint32_t e0 = static_cast<std::uint32_t>(cur[l] + 8 * j);
+        if (__builtin_amdgcn_ballot_w64(e0 * 4u + 32u > col_lim) == 0u) return;
 #pragma unroll
-    for (int rw = 0; rw < kRw; ++rw) {
-        const std::uint32_t row = __builtin_amdgcn_readfirstlane(sh.rows[wave * kRw + rw]);
-        cur[rw] = end[rw] = 0;
+        for (int k = 0; k < 8; ++k)
+            colw[l][k] = static_cast<std::uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rc, (e0 + k) * 4u, 0, 0));
+    };
+
 #pragma unroll
-        for (int k = 0; k < 8; ++k) g[rw][k] = 0.0f;
-        if (row != kNoRow) {
-            cur[rw] = __builtin_amdgcn_readfirstlane(a.row_ptr[row]);
-            end[rw] = __builtin_amdgcn_readfirstlane(a.row_ptr[row + 1]);
+    for (int l = 0; l < kLayers; ++l) {
+        const std::uint32_t row = sh.rows[(wave * kLayers + l) * 8 + grp];
+        cur[l] = end[l] = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) g[l][k] = 0.0f;
+        if (row != kNoRow && fits) {
+            cur[l] = a.row_ptr[row] - wg_begin;
+            end[l] = a.row_ptr[row + 1] - wg_begin;
             const float4 *gp = reinterpret_cast<const float4 *>(a.grad_out + static_cast<std::int64_t>(row) * a.grad_out_ld + j * 8);
             const float4 g0 = gp[0], g1 = gp[1];
-            g[rw][0] = g0.x; g[rw][1] = g0.y; g[rw][2] = g0.z; g[rw][3] = g0.w;
-            g[rw][4] = g1.x; g[rw][5] = g1.y; g[rw][6] = g1.z; g[rw][7] = g1.w;
+            g[l][0] = g0.x; g[l][1] = g0.y; g[l][2] = g0.z; g[l][3] = g0.w;
+            g[l][4] = g1.x; g[l][5] = g1.y; g[l][6] = g1.z; g[l][7] = g1.w;
         }
-        base[rw] = cur[rw];
-        win[rw] = kNoGene;
-        if (cur[rw] < end[rw]) load_cols(rw);
+        const std::uint32_t e0 = static_cast<std::uint32_t>(cur[l] + 8 * j);
+        load_cols(l, 0, e0);
+        load_cols(l, 1, e0);
     }
-    const char *wbase = reinterpret_cast<const char *>(sh.w) + j * 16;
 
-    auto segment = [&](int rw, int lo, std::uint32_t span, int &start, int &cnt, std::uint32_t &gl) {
-        start = cur[rw] - base[rw];
-        gl = win[rw] - static_cast<std::uint32_t>(lo);
-        const std::uint64_t run = ~(__builtin_amdgcn_ballot_w64(gl < span) >> start);
-        const int in_run = run == 0u ? kWave - start : __builtin_ctzll(run);
-        cnt = in_run < end[rw] - cur[rw] ? in_run : end[rw] - cur[rw];
-    };
-    auto stage = [&](int slot, int start, int cnt, std::uint32_t gl) {
-        if (static_cast<std::uint32_t>(lane - start) < static_cast<std::uint32_t>(cnt))
-            sh.stage[wave][slot][lane] = static_cast<int>(gl) * 128;
-    };
-    // dots of staged entries [start, start + cnt) of slot `slot` into sh.dots
-    auto step1 = [&](int rw, int slot, int s) {
-        const int e = sh.stage[wave][slot][s + grp];
-        const float d = group_sum8(dot8(g[rw], *reinterpret_cast<const uint4 *>(wbase + e)));
-        if (j == 0) sh.dots[wave][slot][s + grp] = d;
-    };
-    auto dots = [&](int rw, int slot, int s, int stop) {
-        for (; s + 8 <= stop; s += 8) step1(rw, slot, s);
-        if (s + grp < stop) step1(rw, slot, s);
-    };
-    auto store = [&](int rw, int slot, int start, int cnt) {
-        if (static_cast<std::uint32_t>(lane - start) < static_cast<std::uint32_t>(cnt))
-            a.grad_values[static_cast<std::uint32_t>(base[rw] + lane)] = sh.dots[wave][slot][lane];
-    };
-    auto advance = [&](int rw, int stop, int cnt) -> bool {
-        cur[rw] += cnt;
-        if (stop < kWave || cur[rw] >= end[rw]) return false;
-        base[rw] = cur[rw];
-        load_cols(rw);
-        return true;
-    };
-    auto visit_rest = [&](int rw, int lo, std::uint32_t span) {
-        for (;;) {
-            int start, cnt;
-            std::uint32_t gl;
-            segment(rw, lo, span, start, cnt, gl);
-            if (cnt == 0) return;
-            stage(0, start, cnt, gl);
-            wave_sync();
-            dots(rw, 0, start, start + cnt);
-            wave_sync();
-            store(rw, 0, start, cnt);
-            if (!advance(rw, start + cnt, cnt)) return;
-        }
-    };
-    auto refill = [&](int rw) {
-        if (base[rw] + kWave < end[rw] && base[rw] + kWave - cur[rw] < kRefill) {
-            base[rw] = cur[rw];
-            load_cols(rw);
-        }
-    };
+    const char *wbase = reinterpret_cast<const char *>(sh.w) + j * 16;
+    std::uint32_t *sp = &sh.u.stage[wave][grp][0];
 
     const int cols = static_cast<int>(a.cols);
     const int parts = (cols + kPartGenes - 1) / kPartGenes;
@@ -647,52 +593,107 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_bwd_values_parts(BwdParts
         const int lo = part * kPartGenes;
         const int hi = lo + kPartGenes < cols ? lo + kPartGenes : cols;
         const std::uint32_t span = static_cast<std::uint32_t>(hi - lo);
+        const std::uint32_t uhi = static_cast<std::uint32_t>(hi);
         __syncthreads();  // every wave is done reading part - 1
         load_part_weights<kWaves>(sh.w, a.rhs, a.rhs_ld, lo, hi, wave, lane);
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the copy (and the window refills)
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the copy (and the window loads)
         __syncthreads();
 #pragma unroll
-        for (int ra = 0; ra < kRw; ra += 2) {
-            const int rb = ra + 1;
-            int sa = 0, ca = 0, sb = 0, cb = 0;
-            std::uint32_t ga = 0u, gb = 0u;
-            if (cur[ra] < end[ra]) segment(ra, lo, span, sa, ca, ga);
-            if (cur[rb] < end[rb]) segment(rb, lo, span, sb, cb, gb);
-            stage(0, sa, ca, ga);
-            stage(1, sb, cb, gb);
-            wave_sync();
-            int s_a = sa, s_b = sb;
-            const int stop_a = sa + ca, stop_b = sb + cb;
-            for (; s_a + 8 <= stop_a && s_b + 8 <= stop_b; s_a += 8, s_b += 8) {
-                step1(ra, 0, s_a);
-                step1(rb, 1, s_b);
+        for (int l = 0; l < kLayers; ++l) {
+            for (;;) {
+                if (tail) fix_tail(l);
+                const int nv = end[l] - cur[l] - 8 * j;
+                int n = 0;
+                if (__builtin_amdgcn_ballot_w64(nv < 8) == 0u) {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) n += colw[l][k] < uhi ? 1 : 0;
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) n += k < nv && colw[l][k] < uhi ? 1 : 0;
+                }
+                const int run = group_sum8i(n);
+                const int rmax = wave_max_groups(run);
+                const int next = cur[l] + run;
+                const std::uint32_t e1 = static_cast<std::uint32_t>(next + 8 * j);
+                float res[8];
+                int okc = 0;
+#pragma unroll
+                for (int f = 0; f < 4; ++f) {
+                    const bool live = 2 * f < rmax;
+                    if (live) {
+                        std::uint32_t st[2];
+#pragma unroll
+                        for (int r = 0; r < 2; ++r) {
+                            const int k = 2 * f + r;
+                            const std::uint32_t gk = colw[l][k] - static_cast<std::uint32_t>(lo);
+                            const bool ok = 8 * j + k < run && gk < span;
+                            okc += ok ? 1 : 0;
+                            st[r] = (ok ? gk : static_cast<std::uint32_t>(kPadGene)) * 128u;
+                        }
+                        *reinterpret_cast<uint2 *>(sp + 2 * j) = make_uint2(st[0], st[1]);
+                    }
+                    if (f == 1) load_cols(l, 0, e1);
+                    if (f == 3) load_cols(l, 1, e1);
+                    if (live) {
+                        // stage slot pair `it` holds window entries 8 it + 2f and 8 it + 2f + 1:
+                        // lane it of the group keeps their results in res[2f], res[2f + 1]
+                        const int n2 = (fill_count(rmax, f) + 1) >> 1;
+                        res[2 * f] = res[2 * f + 1] = 0.0f;
+                        for (int it = 0; it < n2; ++it) {
+                            const uint2 e = reinterpret_cast<const uint2 *>(sp)[it];
+                            const uint4 w0 = *reinterpret_cast<const uint4 *>(wbase + e.x);
+                            const uint4 w1 = *reinterpret_cast<const uint4 *>(wbase + e.y);
+                            const float d0 = group_sum8(dot8x2(g[l], w0));
+                            const float d1 = group_sum8(dot8x2(g[l], w1));
+                            if (j == it) {
+                                res[2 * f] = d0;
+                                res[2 * f + 1] = d1;
+                            }
+                        }
+                    }
+                }
+                // this lane's window slots in the run: entries cur + 8j .. cur + 8j + in_run - 1
+                const int in_run = run - 8 * j < 0 ? 0 : (run - 8 * j > 8 ? 8 : run - 8 * j);
+                const std::uint32_t o0 = static_cast<std::uint32_t>(cur[l] + 8 * j) * 4u;
+                if (in_run == 8) {
+                    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+                    const u32x4 lo4 = {__float_as_uint(res[0]), __float_as_uint(res[1]), __float_as_uint(res[2]),
+                                       __float_as_uint(res[3])};
+                    const u32x4 hi4 = {__float_as_uint(res[4]), __float_as_uint(res[5]), __float_as_uint(res[6]),
+                                       __float_as_uint(res[7])};
+                    __builtin_amdgcn_raw_buffer_store_b128(lo4, ro, o0, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b128(hi4, ro, o0 + 16u, 0, 0);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k)
+                        if (k < in_run) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(res[k]), ro, o0 + 4u * k, 0, 0);
+                }
+                if (okc != in_run) end[l] = -1;  // broken: no further runs; recomputed at the end
+                cur[l] = next;
+                if (__builtin_amdgcn_ballot_w64(run == 64 && cur[l] < end[l]) == 0u) break;
             }
-            dots(ra, 0, s_a, stop_a);
-            dots(rb, 1, s_b, stop_b);
-            wave_sync();
-            store(ra, 0, sa, ca);
-            store(rb, 1, sb, cb);
-            const bool more_a = ca > 0 && advance(ra, stop_a, ca);
-            const bool more_b = cb > 0 && advance(rb, stop_b, cb);
-            if (more_a) visit_rest(ra, lo, span);
-            if (more_b) visit_rest(rb, lo, span);
-            refill(ra);
-            refill(rb);
         }
     }
 
-    // rows the walk could not finish: the remaining entries on a plain path (lane = column;
-    // columns outside [0, cols) give 0)
+    // rows the walk could not finish: the whole row again on a plain path (lane = column;
+    // columns outside [0, cols) give 0), after this wave's stores above have completed
+    __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
-    for (int rw = 0; rw < kRw; ++rw) {
-        if (cur[rw] >= end[rw]) continue;
-        const std::uint32_t row = __builtin_amdgcn_readfirstlane(sh.rows[wave * kRw + rw]);
-        const float gl = a.grad_out[static_cast<std::int64_t>(row) * a.grad_out_ld + lane];
-        for (int i = cur[rw]; i < end[rw]; ++i) {
-            const std::uint32_t col = static_cast<std::uint32_t>(a.col_idx[i]);
-            float d = col < a.cols ? gl * h2f(a.rhs[static_cast<std::int64_t>(col) * a.rhs_ld + lane]) : 0.0f;
-            d = xor_reduce<0, 5>(d);
-            if (lane == 0) a.grad_values[i] = d;
+    for (int l = 0; l < kLayers; ++l) {
+        const std::uint32_t row = sh.rows[(wave * kLayers + l) * 8 + grp];
+        const int bad = group_sum8i(cur[l] != end[l] || !fits ? 1 : 0);
+        std::uint64_t todo = __builtin_amdgcn_ballot_w64(j == 0 && row != kNoRow && bad != 0);
+        while (todo != 0u) {
+            const int gsel = __builtin_ctzll(todo) >> 3;
+            todo &= todo - 1u;
+            const std::uint32_t r = sh.rows[(wave * kLayers + l) * 8 + gsel];
+            const float gl = a.grad_out[static_cast<std::int64_t>(r) * a.grad_out_ld + lane];
+            for (int i = a.row_ptr[r]; i < a.row_ptr[r + 1]; ++i) {
+                const std::uint32_t col = static_cast<std::uint32_t>(a.col_idx[i]);
+                float d = col < a.cols ? gl * h2f(a.rhs[static_cast<std::int64_t>(col) * a.rhs_ld + lane]) : 0.0f;
+                d = xor_reduce<0, 5>(d);
+                if (lane == 0) a.grad_values[i] = d;
+            }
         }
     }
 }
@@ -736,13 +737,13 @@ bool bwd_values_parts_applicable(std::uint32_t rows, std::uint32_t cols, std::ui
 int launch_bwd_values_parts(const std::int32_t *row_ptr, const std::int32_t *col_idx, const float *grad_out,
                             std::int64_t grad_out_ld, const void *rhs, std::int64_t rhs_ld,
                             float *grad_values, std::uint32_t rows, std::uint32_t cols, hipStream_t stream) {
-    constexpr int kWaves = 16, kRw = 8;
+    constexpr int kWaves = 16, kLayers = 4;
     const BwdPartsArgs a{row_ptr, col_idx, grad_out, grad_out_ld, static_cast<const std::uint16_t *>(rhs), rhs_ld,
                          grad_values, rows, cols};
-    const unsigned rows_per_block = kWaves * kRw;
+    const unsigned rows_per_block = kWaves * kLayers * 8;
     const dim3 grid((rows + rows_per_block - 1) / rows_per_block), block(kWaves * kWave);
-    hipLaunchKernelGGL((qcsr_bwd_values_parts<kWaves, kRw>), grid, block, 0, stream, a);
-    return check_launch("qcsr_bwd_values_parts");
+    hipLaunchKernelGGL((qcsr_bwd_values_groups<kWaves, kLayers>), grid, block, 0, stream, a);
+    return check_launch("qcsr_bwd_values_groups");
 }
 
 int launch_qcsr_parts(const QcsrArgs &a, std::uint32_t bits, std::uint32_t policy, std::int64_t out_cols,

@@ -77,18 +77,14 @@ def test_many_parts_skewed_rows(oracle, bits, policy):
     check_against_referee(oracle, ref, mag, _run(to_device_qcsr(fx), rhs))
 
 
-@pytest.mark.parametrize("bits", [4, 8])
-def test_many_workgroups_long_last_rows(oracle, bits):
-    """1,300 rows: workgroups of 512, 512 and 276 rows. The last rows of the matrix are long
-    (whole-window runs inside a part, windows reaching the ends of the column and code
-    arrays, code tails ending inside a byte), so block-end and array-end window loads
-    are both exercised."""
-    rng = np.random.default_rng(971 + bits)
-    rows, cols = 1300, 2600
+def _long_tail_fixture(oracle, rng, bits, rows=1300, cols=2600):
+    """Workgroups of 512, 512 and 276 rows; long rows across the first block boundary and at
+    the end of the matrix (whole-window runs inside a part, windows reaching the ends of the
+    column and code arrays, code tails ending inside a byte)."""
     fx = quantized_fixture(oracle, rng, rows, cols, 10.0, bits, 1)
     lengths = np.minimum(rng.lognormal(np.log(300.0), 0.9, rows).astype(np.int64), cols)
     lengths[rng.choice(rows - 5, 40, replace=False)] = 0
-    lengths[510:514] = [cols, 0, 2049, 1]  # across the first block boundary
+    lengths[510:514] = [cols, 0, 2049, 1]
     lengths[-5:] = [cols, 1777, 3, cols - 1, 1501]
     row_ptr = np.zeros(rows + 1, np.int64)
     row_ptr[1:] = np.cumsum(lengths)
@@ -96,8 +92,16 @@ def test_many_workgroups_long_last_rows(oracle, bits):
     for r in range(rows):
         if lengths[r]:
             col_idx[row_ptr[r]:row_ptr[r + 1]] = np.sort(rng.choice(cols, lengths[r], replace=False))
-    fx = _rebuild(oracle, rng, fx, row_ptr.astype(np.int32), col_idx)
-    rhs = (rng.standard_normal((cols, 64)) * 0.02).astype(np.float16)
+    return _rebuild(oracle, rng, fx, row_ptr.astype(np.int32), col_idx)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_many_workgroups_long_last_rows(oracle, bits):
+    """Three workgroups, long rows at a block boundary and at the array ends: block-end and
+    array-end window loads are both exercised."""
+    rng = np.random.default_rng(971 + bits)
+    fx = _long_tail_fixture(oracle, rng, bits)
+    rhs = (rng.standard_normal((fx["cols"], 64)) * 0.02).astype(np.float16)
     ref, mag = _referee(oracle, fx, rhs)
     check_against_referee(oracle, ref, mag, _run(to_device_qcsr(fx), rhs))
 
@@ -230,8 +234,8 @@ def _bwd_values_check(oracle, fx, g, w, got):
 
 
 def test_bwd_values_parts_skewed_rows(oracle):
-    """grad_values by gene part (fp16 W, N = 64): 5 parts, rows from empty to every gene,
-    several workgroups; against the float64 restatement of csr_spmm_bwd_values."""
+    """grad_values by the row-group walk (fp16 W, N = 64): 5 parts, rows from empty to every
+    gene; against the float64 restatement of csr_spmm_bwd_values."""
     import torch
 
     from cellerator_amd import qcsr_spmm_bwd_values
@@ -245,8 +249,8 @@ def test_bwd_values_parts_skewed_rows(oracle):
 
 
 def test_bwd_values_parts_unsorted_and_out_of_range(oracle):
-    """Rows out of order across parts finish on the per-row path from their cursor; entries
-    with columns outside [0, cols) get 0."""
+    """Rows out of order across parts, and rows stopped by a column outside [0, cols), are
+    recomputed whole on the per-row path; entries with such columns get 0."""
     import torch
 
     from cellerator_amd import qcsr_spmm_bwd_values
@@ -276,3 +280,18 @@ def test_bwd_values_parts_unsorted_and_out_of_range(oracle):
     mag = np.einsum("ij,ij->i", np.abs(g.astype(np.float64))[rows_of],
                     np.abs(w.astype(np.float64))[ref_cols])
     check_against_referee(oracle, ref[good], mag[good], got[good])
+
+
+def test_bwd_values_many_workgroups_long_last_rows(oracle):
+    """grad_values over three workgroups with long rows at a block boundary and at the end
+    of the column array (whole-window runs, array-end windows, partial last stores)."""
+    import torch
+
+    from cellerator_amd import qcsr_spmm_bwd_values
+    rng = np.random.default_rng(983)
+    fx = _long_tail_fixture(oracle, rng, 4)
+    g = rng.standard_normal((fx["rows"], 64)).astype(np.float32)
+    w = (rng.standard_normal((fx["cols"], 64)) * 0.1).astype(np.float16)
+    gv = qcsr_spmm_bwd_values(to_device_qcsr(fx), torch.from_numpy(g).cuda(), torch.from_numpy(w).cuda())
+    torch.cuda.synchronize()
+    _bwd_values_check(oracle, fx, g, w, gv.cpu().numpy())
