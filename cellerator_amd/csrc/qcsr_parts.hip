@@ -395,8 +395,9 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
                             std::uint32_t code;
                             if constexpr (kBits == 8) code = ((k < 4 ? c0 : c1) >> (8 * (k & 3))) & 0xffu;
                             else code = (c0 >> (k * kBits)) & kMask;
-                            const float off = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET ? roff[l] : md.y;
-                            const float x = ok ? __builtin_fmaf(static_cast<float>(code), md.x, off) : 0.0f;
+                            // pads read the (0, 0) metadata of the zero row: x = 0 without a branch
+                            const float off = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET ? (ok ? roff[l] : 0.0f) : md.y;
+                            const float x = __builtin_fmaf(static_cast<float>(code), md.x, off);
                             st[2 * r] = gg * 8u;
                             st[2 * r + 1] = __float_as_uint(x);
                         }
