@@ -640,7 +640,27 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_bwd_values_groups(BwdPart
                         // lane it of the group keeps their results in res[2f], res[2f + 1]
                         const int n2 = (fill_count(rmax, f) + 1) >> 1;
                         res[2 * f] = res[2 * f + 1] = 0.0f;
-                        for (int it = 0; it < n2; ++it) {
+                        int it = 0;
+                        for (; it + 2 <= n2; it += 2) {
+                            const uint4 e = reinterpret_cast<const uint4 *>(sp)[it >> 1];
+                            const uint4 w0 = *reinterpret_cast<const uint4 *>(wbase + e.x);
+                            const uint4 w1 = *reinterpret_cast<const uint4 *>(wbase + e.y);
+                            const uint4 w2 = *reinterpret_cast<const uint4 *>(wbase + e.z);
+                            const uint4 w3 = *reinterpret_cast<const uint4 *>(wbase + e.w);
+                            const float d0 = group_sum8(dot8x2(g[l], w0));
+                            const float d1 = group_sum8(dot8x2(g[l], w1));
+                            const float d2 = group_sum8(dot8x2(g[l], w2));
+                            const float d3 = group_sum8(dot8x2(g[l], w3));
+                            if (j == it) {
+                                res[2 * f] = d0;
+                                res[2 * f + 1] = d1;
+                            }
+                            if (j == it + 1) {
+                                res[2 * f] = d2;
+                                res[2 * f + 1] = d3;
+                            }
+                        }
+                        if (it < n2) {
                             const uint2 e = reinterpret_cast<const uint2 *>(sp)[it];
                             const uint4 w0 = *reinterpret_cast<const uint4 *>(wbase + e.x);
                             const uint4 w1 = *reinterpret_cast<const uint4 *>(wbase + e.y);
