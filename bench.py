@@ -93,7 +93,7 @@ def cpu_baseline_qcsr(m, w, sample_rows: int, threads: int) -> dict:
 
 def bench_qcsr(args, torch, cfg, n_out: int) -> dict:
     from cellerator_amd import _native as N
-    from cellerator_amd import qcsr_pack_gene_affine, qcsr_spmm
+    from cellerator_amd import qcsr_check_columns, qcsr_pack_gene_affine, qcsr_spmm
     from cellerator_amd.synth import dense_normal, generate_qcsr
 
     t0 = time.perf_counter()
@@ -104,6 +104,10 @@ def bench_qcsr(args, torch, cfg, n_out: int) -> dict:
     # packed weight panel); decodes bit-identically to the separate arrays
     pairs = bool(m.bits) and m.decode_policy == N.DECODE_PER_GENE_AFFINE and not args.separate_meta
     mt = qcsr_pack_gene_affine(m) if pairs else m
+    # the structure's column order checked once on the device (untimed prepare step): sorted
+    # rows let the gene-part kernel skip its per-entry out-of-order check
+    if not args.unchecked_columns:
+        mt = qcsr_check_columns(mt)
     torch.cuda.synchronize()
     log(f"generated {cfg.name}: nnz={m.nnz} in {time.perf_counter() - t0:.1f}s")
     stream = torch.cuda.current_stream()
@@ -124,7 +128,8 @@ def bench_qcsr(args, torch, cfg, n_out: int) -> dict:
         "dtype": f"u{m.bits}-codes/f16-W/f32-accumulate" if m.bits else "f32",
         "config": {"workload": cfg.name, "rows": m.rows, "genes": m.cols, "nnz": m.nnz,
                    "bits": m.bits, "n_out": n_out, "rhs": "fp16",
-                   "nnz_per_row_mean": m.nnz / m.rows, "seed": hex(cfg.seed)},
+                   "nnz_per_row_mean": m.nnz / m.rows, "seed": hex(cfg.seed),
+                   "columns_sorted": bool(mt.flags & N.QCSR_COLUMNS_SORTED)},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(cfg.name),
                      "kernel": ("qcsr_spmm_groups" if m.bits and n_out % 64 == 0 and n_out <= 256
@@ -358,6 +363,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--ungrouped", action="store_true",
                     help="C4: time the per-row-block MFMA kernel without the row-block grouping")
+    ap.add_argument("--unchecked-columns", action="store_true",
+                    help="qCSR: skip the column-order check (kernel keeps its per-entry check)")
     ap.add_argument("--separate-meta", action="store_true",
                     help="C2/C3: time the separate scale/offset arrays instead of interleaved pairs")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",

@@ -17,6 +17,7 @@ SYNTH_PATH = PKG / "libcx_synth.so"
 # cellerator_dtype (include/cellerator_amd.h)
 DTYPE_F16, DTYPE_F32, DTYPE_U8, DTYPE_U32, DTYPE_BF16 = 1, 2, 3, 4, 5
 DECODE_PER_GENE_AFFINE, DECODE_COLUMN_SCALE_ROW_OFFSET, DECODE_PER_GENE_AFFINE_PAIRS = 1, 2, 3
+QCSR_COLUMNS_SORTED = 1  # cx_qcsr_matrix.flags
 # CX_EPILOGUE_* = the reference's epilogue_kind values
 (EPILOGUE_NONE, EPILOGUE_BIAS, EPILOGUE_RELU, EPILOGUE_GELU_ERF, EPILOGUE_GELU_TANH,
  EPILOGUE_BIAS_RELU, EPILOGUE_BIAS_GELU_ERF, EPILOGUE_BIAS_GELU_TANH) = range(8)
@@ -32,7 +33,7 @@ class CxQcsrMatrix(C.Structure):
         ("rows", u32), ("cols", u32), ("nnz", u64), ("bits", u32), ("decode_policy", u32),
         ("row_ptr", p_void), ("packed_row_ptr", p_void), ("col_idx", p_void),
         ("packed_values", p_void), ("column_scales", p_void), ("column_offsets", p_void),
-        ("row_offsets", p_void), ("values", p_void), ("value_dtype", u32), ("reserved", u32),
+        ("row_offsets", p_void), ("values", p_void), ("value_dtype", u32), ("flags", u32),
     ]
 
 
@@ -173,6 +174,7 @@ ENGINE_SIGNATURES = {
     "cx_qcsr_spmm_fwd_epilogue": (C.c_int, [C.POINTER(CxQcsrMatrix), p_void, u32, i64, i64, p_void,
                                             i64, C.POINTER(CxSpmmEpilogue), p_void]),
     "cx_qcsr_pack_gene_affine": (C.c_int, [p_void, p_void, u32, p_void, p_void]),
+    "cx_qcsr_check_columns": (C.c_int, [p_void, p_void, p_void]),
     "cx_qcsr_transpose_workspace": (C.c_int, [C.POINTER(CxQcsrMatrix), C.POINTER(u64)]),
     "cx_qcsr_transpose": (C.c_int, [C.POINTER(CxQcsrMatrix), p_void, p_void, p_void, p_void, u64,
                                     p_void]),

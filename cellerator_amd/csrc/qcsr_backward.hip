@@ -410,7 +410,7 @@ extern "C" int cx_qcsr_spmm_bwd_values(const cx_qcsr_matrix *m, const float *gra
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (bwd_values_parts_applicable(m->rows, m->cols, rhs_dtype, out_cols, aligned, rhs_ld))
         return launch_bwd_values_parts(m->row_ptr, m->col_idx, grad_out, grad_out_ld, rhs, rhs_ld, grad_values,
-                                       m->rows, m->cols, s);
+                                       m->rows, m->cols, (m->flags & CX_QCSR_COLUMNS_SORTED) != 0u, s);
     if (rhs_dtype == CELLERATOR_DTYPE_F16) return launch_bwd_values<std::uint16_t>(a, out_cols, aligned, s);
     return launch_bwd_values<float>(a, out_cols, aligned, s);
 }

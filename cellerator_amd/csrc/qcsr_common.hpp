@@ -22,6 +22,7 @@ struct QcsrArgs {
     std::int64_t out_ld;
     std::uint32_t rows;
     std::uint32_t cols;
+    std::uint32_t flags;  // cx_qcsr_matrix.flags (CX_QCSR_COLUMNS_SORTED)
     Epilogue ep;
 };
 
@@ -69,7 +70,8 @@ bool bwd_values_parts_applicable(std::uint32_t rows, std::uint32_t cols, std::ui
                                  std::int64_t out_cols, bool aligned, std::int64_t rhs_ld);
 int launch_bwd_values_parts(const std::int32_t *row_ptr, const std::int32_t *col_idx, const float *grad_out,
                             std::int64_t grad_out_ld, const void *rhs, std::int64_t rhs_ld,
-                            float *grad_values, std::uint32_t rows, std::uint32_t cols, hipStream_t stream);
+                            float *grad_values, std::uint32_t rows, std::uint32_t cols, bool sorted,
+                            hipStream_t stream);
 
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");

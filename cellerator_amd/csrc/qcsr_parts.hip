@@ -226,7 +226,7 @@ __device__ __forceinline__ int fill_count(int run, int f) {
     return 2 * blocks + (rem < 2 ? rem : 2);
 }
 
-template<int kBits, int kPolicy, int kWaves, int kLayers>
+template<int kBits, int kPolicy, int kWaves, int kLayers, bool kSorted>
 __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
     using Shared = GroupsShared<kWaves, kLayers>;
     constexpr int kRows = Shared::kRows;
@@ -388,9 +388,12 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
                         for (int r = 0; r < 2; ++r) {
                             const int k = 2 * f + r;
                             const std::uint32_t gk = colw[l][k] - static_cast<std::uint32_t>(lo);
-                            const bool ok = 8 * j + k < run && gk < span;
-                            okc += ok ? 1 : 0;
-                            const std::uint32_t gg = ok ? gk : static_cast<std::uint32_t>(kPadGene);
+                            // sorted columns (vouched for): a run entry lies in the part; the
+                            // clamp only keeps a broken promise inside LDS
+                            const bool ok = 8 * j + k < run && (kSorted || gk < span);
+                            if constexpr (!kSorted) okc += ok ? 1 : 0;
+                            const std::uint32_t gg = ok ? (kSorted ? min(gk, static_cast<std::uint32_t>(kPadGene)) : gk)
+                                                        : static_cast<std::uint32_t>(kPadGene);
                             const float2 md = *reinterpret_cast<const float2 *>(mbase + gg * 8u);
                             std::uint32_t code;
                             if constexpr (kBits == 8) code = ((k < 4 ? c0 : c1) >> (8 * (k & 3))) & 0xffu;
@@ -434,8 +437,10 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
                         }
                     }
                 }
-                const int in_run = run - 8 * j < 0 ? 0 : (run - 8 * j > 8 ? 8 : run - 8 * j);
-                if (okc != in_run) end[l] = -1;  // broken: no further runs; recomputed at the end
+                if constexpr (!kSorted) {
+                    const int in_run = run - 8 * j < 0 ? 0 : (run - 8 * j > 8 ? 8 : run - 8 * j);
+                    if (okc != in_run) end[l] = -1;  // broken: no further runs; recomputed at the end
+                }
                 cur[l] = next;
                 const bool more = __builtin_amdgcn_ballot_w64(run == 64 && cur[l] < end[l]) != 0u;
                 if (!more) break;
@@ -522,7 +527,7 @@ __device__ __forceinline__ float dot8x2(const float (&g)[8], uint4 w) {
     return d0 + d1;
 }
 
-template<int kWaves, int kLayers>
+template<int kWaves, int kLayers, bool kSorted>
 __global__ __launch_bounds__(kWaves * kWave) void qcsr_bwd_values_groups(BwdPartsArgs a) {
     using Shared = BwdGroupsShared<kWaves, kLayers>;
     constexpr int kRows = Shared::kRows;
@@ -627,9 +632,10 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_bwd_values_groups(BwdPart
                         for (int r = 0; r < 2; ++r) {
                             const int k = 2 * f + r;
                             const std::uint32_t gk = colw[l][k] - static_cast<std::uint32_t>(lo);
-                            const bool ok = 8 * j + k < run && gk < span;
-                            okc += ok ? 1 : 0;
-                            st[r] = (ok ? gk : static_cast<std::uint32_t>(kPadGene)) * 128u;
+                            const bool ok = 8 * j + k < run && (kSorted || gk < span);
+                            if constexpr (!kSorted) okc += ok ? 1 : 0;
+                            st[r] = (ok ? (kSorted ? min(gk, static_cast<std::uint32_t>(kPadGene)) : gk)
+                                        : static_cast<std::uint32_t>(kPadGene)) * 128u;
                         }
                         *reinterpret_cast<uint2 *>(sp + 2 * j) = make_uint2(st[0], st[1]);
                     }
@@ -689,7 +695,8 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_bwd_values_groups(BwdPart
                     for (int k = 0; k < 8; ++k)
                         if (k < in_run) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(res[k]), ro, o0 + 4u * k, 0, 0);
                 }
-                if (okc != in_run) end[l] = -1;  // broken: no further runs; recomputed at the end
+                if constexpr (!kSorted)
+                    if (okc != in_run) end[l] = -1;  // broken: no further runs; recomputed at the end
                 cur[l] = next;
                 if (__builtin_amdgcn_ballot_w64(run == 64 && cur[l] < end[l]) == 0u) break;
             }
@@ -724,7 +731,10 @@ int launch_bits_groups(const QcsrArgs &a, hipStream_t stream) {
     constexpr int kWaves = 16, kLayers = 4;
     const unsigned rows_per_block = kWaves * kLayers * 8;
     const dim3 grid((a.rows + rows_per_block - 1) / rows_per_block), block(kWaves * kWave);
-    hipLaunchKernelGGL((qcsr_spmm_groups<kBits, kPolicy, kWaves, kLayers>), grid, block, 0, stream, a);
+    if ((a.flags & CX_QCSR_COLUMNS_SORTED) != 0u)
+        hipLaunchKernelGGL((qcsr_spmm_groups<kBits, kPolicy, kWaves, kLayers, true>), grid, block, 0, stream, a);
+    else
+        hipLaunchKernelGGL((qcsr_spmm_groups<kBits, kPolicy, kWaves, kLayers, false>), grid, block, 0, stream, a);
     return check_launch("qcsr_spmm_groups");
 }
 
@@ -757,13 +767,17 @@ bool bwd_values_parts_applicable(std::uint32_t rows, std::uint32_t cols, std::ui
 
 int launch_bwd_values_parts(const std::int32_t *row_ptr, const std::int32_t *col_idx, const float *grad_out,
                             std::int64_t grad_out_ld, const void *rhs, std::int64_t rhs_ld,
-                            float *grad_values, std::uint32_t rows, std::uint32_t cols, hipStream_t stream) {
+                            float *grad_values, std::uint32_t rows, std::uint32_t cols, bool sorted,
+                            hipStream_t stream) {
     constexpr int kWaves = 16, kLayers = 4;
     const BwdPartsArgs a{row_ptr, col_idx, grad_out, grad_out_ld, static_cast<const std::uint16_t *>(rhs), rhs_ld,
                          grad_values, rows, cols};
     const unsigned rows_per_block = kWaves * kLayers * 8;
     const dim3 grid((rows + rows_per_block - 1) / rows_per_block), block(kWaves * kWave);
-    hipLaunchKernelGGL((qcsr_bwd_values_groups<kWaves, kLayers>), grid, block, 0, stream, a);
+    if (sorted)
+        hipLaunchKernelGGL((qcsr_bwd_values_groups<kWaves, kLayers, true>), grid, block, 0, stream, a);
+    else
+        hipLaunchKernelGGL((qcsr_bwd_values_groups<kWaves, kLayers, false>), grid, block, 0, stream, a);
     return check_launch("qcsr_bwd_values_groups");
 }
 

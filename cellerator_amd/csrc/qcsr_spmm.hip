@@ -452,6 +452,7 @@ int qcsr_forward(const cx_qcsr_matrix *m, const void *rhs, std::uint32_t rhs_dty
     a.out_ld = out_ld;
     a.rows = m->rows;
     a.cols = m->cols;
+    a.flags = m->flags;
     const std::size_t esize = rhs_dtype == CELLERATOR_DTYPE_F16 ? 2u : 4u;
     const bool aligned = aligned16(rhs) && aligned16(out) && (rhs_ld * esize) % 16 == 0
         && (out_ld * 4) % 16 == 0;
@@ -489,6 +490,48 @@ int qcsr_forward(const cx_qcsr_matrix *m, const void *rhs, std::uint32_t rhs_dty
 
 } // namespace
 } // namespace cx
+
+namespace cx {
+namespace {
+
+__global__ void check_columns_init(std::uint32_t *flag) { *flag = CX_QCSR_COLUMNS_SORTED; }
+
+// One wave per row (grid-stride): any column outside [0, cols) or above its successor in the
+// row clears the flag.
+__global__ __launch_bounds__(256) void check_columns_kernel(const std::int32_t *row_ptr, const std::int32_t *col_idx,
+                                                            std::uint32_t rows, std::int32_t cols, std::uint32_t *flag) {
+    const std::uint32_t lane = threadIdx.x % kWave;
+    const std::uint32_t waves = gridDim.x * (blockDim.x / kWave);
+    bool bad = false;
+    for (std::uint32_t r = (blockIdx.x * blockDim.x + threadIdx.x) / kWave; r < rows; r += waves) {
+        const std::int32_t b = row_ptr[r], e = row_ptr[r + 1];
+        for (std::int32_t i = b + static_cast<std::int32_t>(lane); i < e; i += kWave) {
+            const std::int32_t c = col_idx[i];
+            bad = bad || c < 0 || c >= cols || (i + 1 < e && c > col_idx[i + 1]);
+        }
+    }
+    if (__ballot(bad) != 0ull && lane == 0u) atomicAnd(flag, 0u);
+}
+
+} // namespace
+} // namespace cx
+
+extern "C" int cx_qcsr_check_columns(const cx_qcsr_matrix *m, uint32_t *device_flag, void *stream) {
+    using namespace cx;
+    clear_error();
+    if (m == nullptr || device_flag == nullptr)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_check_columns: null matrix or flag");
+    if (m->rows != 0u && (m->row_ptr == nullptr || (m->nnz != 0u && m->col_idx == nullptr)))
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_check_columns: missing row_ptr or col_idx");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(check_columns_init, dim3(1), dim3(1), 0, s, device_flag);
+    if (m->rows != 0u) {
+        const std::uint32_t blocks = std::min<std::uint32_t>((m->rows + 3u) / 4u, 8192u);
+        hipLaunchKernelGGL(check_columns_kernel, dim3(blocks), dim3(256), 0, s, m->row_ptr, m->col_idx, m->rows,
+                           static_cast<std::int32_t>(std::min<std::uint32_t>(m->cols, INT32_MAX)), device_flag);
+    }
+    return check_launch("cx_qcsr_check_columns");
+}
 
 extern "C" int cx_qcsr_pack_gene_affine(const float *scales, const float *offsets, uint32_t cols,
                                         float *pairs, void *stream) {

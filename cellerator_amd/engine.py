@@ -13,6 +13,7 @@ Containers mirror the reference's types:
 from __future__ import annotations
 
 import ctypes as C
+import dataclasses
 from dataclasses import dataclass, field
 from typing import Optional
 
@@ -55,6 +56,7 @@ class QcsrMatrix:
     values: Optional[torch.Tensor] = None  # f16/f32 [nnz] when bits == 0
     decode_policy: int = N.DECODE_PER_GENE_AFFINE
     meta: dict = field(default_factory=dict)
+    flags: int = 0  # cx_qcsr_matrix.flags: N.QCSR_COLUMNS_SORTED once qcsr_check_columns confirms it
 
     @property
     def nnz(self) -> int:
@@ -69,6 +71,7 @@ class QcsrMatrix:
         d.column_scales, d.column_offsets = _ptr(self.column_scales), _ptr(self.column_offsets)
         d.row_offsets, d.values = _ptr(self.row_offsets), _ptr(self.values)
         d.value_dtype = _DTYPE_CODE[self.values.dtype] if self.values is not None else 0
+        d.flags = self.flags
         return d
 
     def nbytes_algorithmic(self, rhs_cols: int, rhs_bytes: int = 2) -> int:
@@ -144,7 +147,19 @@ def qcsr_pack_gene_affine(m: QcsrMatrix, stream=None) -> QcsrMatrix:
         _ptr(m.column_scales), _ptr(m.column_offsets), m.cols, pairs.data_ptr(), _stream(stream)))
     return QcsrMatrix(m.rows, m.cols, m.bits, m.row_ptr, m.col_idx, packed_row_ptr=m.packed_row_ptr,
                       packed_values=m.packed_values, column_scales=pairs, column_offsets=None,
-                      decode_policy=N.DECODE_PER_GENE_AFFINE_PAIRS, meta=dict(m.meta))
+                      decode_policy=N.DECODE_PER_GENE_AFFINE_PAIRS, meta=dict(m.meta), flags=m.flags)
+
+
+def qcsr_check_columns(m: QcsrMatrix, stream=None) -> QcsrMatrix:
+    """The same matrix with flags = QCSR_COLUMNS_SORTED when every row's columns are
+    non-decreasing and in [0, cols) (checked on the device, one pass over the structure),
+    else flags = 0. Run once per structure: the gene-part kernels then skip their per-entry
+    out-of-order check."""
+    _require_cuda(m.row_ptr)
+    flag = torch.empty(1, dtype=torch.int32, device=m.row_ptr.device)
+    d = m.descriptor()
+    N.check("cx_qcsr_check_columns", N.engine().cx_qcsr_check_columns(C.byref(d), flag.data_ptr(), _stream(stream)))
+    return dataclasses.replace(m, flags=int(flag.item()) & N.QCSR_COLUMNS_SORTED)
 
 
 def qcsr_transpose(m: QcsrMatrix, stream=None) -> QcsrMatrix:

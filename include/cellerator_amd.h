@@ -142,8 +142,15 @@ typedef struct cx_qcsr_matrix {
     const float *row_offsets;      /* rows or NULL (-> 0); column_scale_row_offset */
     const void *values;            /* nnz of value_dtype when bits == 0 */
     uint32_t value_dtype;          /* cellerator_dtype, bits == 0 only */
-    uint32_t reserved;
+    uint32_t flags;                /* CX_QCSR_* properties the caller vouches for; 0 = none */
 } cx_qcsr_matrix;
+
+/* cx_qcsr_matrix.flags: every row's columns are non-decreasing and lie in [0, cols), as the
+ * reference's containers store them (cx_qcsr_check_columns establishes it). The gene-part
+ * kernels then skip the per-entry check that sends rows out of order to a per-row path; a
+ * row that breaks the promise gets wrong sums, never an out-of-bounds read. Engine addition,
+ * no counterpart in the reference. */
+#define CX_QCSR_COLUMNS_SORTED 1u
 
 /* Y[rows x out_cols] (fp32, row stride out_ld) = decode(A) . RHS[cols x out_cols]
  * (row stride rhs_ld, dtype F16 or F32; F16 widens exactly). fp32 multiply and
@@ -183,6 +190,12 @@ int cx_qcsr_spmm_fwd_balanced(const cx_qcsr_matrix *a, const void *rhs, uint32_t
  * the reference: it prepares the layout the decode reads in one gather. */
 int cx_qcsr_pack_gene_affine(const float *scales, const float *offsets, uint32_t cols,
                              float *pairs, void *stream);
+
+/* Writes CX_QCSR_COLUMNS_SORTED to *device_flag (one uint32 in device memory) when every row
+ * of a has non-decreasing columns in [0, cols), else 0; stream-ordered, reads row_ptr and
+ * col_idx once. The prepare step behind cx_qcsr_matrix.flags; engine addition, no
+ * counterpart in the reference. */
+int cx_qcsr_check_columns(const cx_qcsr_matrix *a, uint32_t *device_flag, void *stream);
 
 /* ---- transpose and backward of the CSR SpMM ------------------------------------ */
 

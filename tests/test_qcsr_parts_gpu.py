@@ -295,3 +295,38 @@ def test_bwd_values_many_workgroups_long_last_rows(oracle):
     gv = qcsr_spmm_bwd_values(to_device_qcsr(fx), torch.from_numpy(g).cuda(), torch.from_numpy(w).cuda())
     torch.cuda.synchronize()
     _bwd_values_check(oracle, fx, g, w, gv.cpu().numpy())
+
+
+def test_check_columns_and_sorted_flag(oracle):
+    """qcsr_check_columns sets QCSR_COLUMNS_SORTED exactly for non-decreasing in-range rows
+    (repeats allowed); with the flag the row-group kernels skip their out-of-order check and
+    give bit-identical forward outputs and gradients on sorted input."""
+    import torch
+
+    from cellerator_amd import _native as N
+    from cellerator_amd import qcsr_check_columns, qcsr_spmm, qcsr_spmm_bwd_values
+    rng = np.random.default_rng(991)
+    fx = _long_tail_fixture(oracle, rng, 4, rows=700, cols=2300)
+    m = to_device_qcsr(fx)
+    ms = qcsr_check_columns(m)
+    assert ms.flags == N.QCSR_COLUMNS_SORTED
+    rhs = torch.from_numpy((rng.standard_normal((2300, 64)) * 0.02).astype(np.float16)).cuda()
+    a, b = qcsr_spmm(m, rhs), qcsr_spmm(ms, rhs)
+    g = torch.from_numpy(rng.standard_normal((700, 64)).astype(np.float32)).cuda()
+    ga, gb = qcsr_spmm_bwd_values(m, g, rhs), qcsr_spmm_bwd_values(ms, g, rhs)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    assert torch.equal(ga.view(torch.int32), gb.view(torch.int32))
+    ref, mag = _referee(oracle, fx, rhs.cpu().numpy())
+    check_against_referee(oracle, ref, mag, b.cpu().numpy())
+    # a repeated column keeps the flag; a descent, a column >= cols or < 0 clears it
+    row_ptr = fx["row_ptr"]
+    r = int(np.argmax(np.diff(row_ptr) > 10))
+    s = int(row_ptr[r])
+    for change, expect in ((lambda c: c.__setitem__(s + 1, c[s]), N.QCSR_COLUMNS_SORTED),
+                           (lambda c: c.__setitem__(s, c[s + 1] + 1), 0),
+                           (lambda c: c.__setitem__(int(row_ptr[-1]) - 1, 2300), 0),
+                           (lambda c: c.__setitem__(0 if row_ptr[1] > 0 else s, -1), 0)):
+        col_idx = fx["col_idx"].copy()
+        change(col_idx)
+        assert qcsr_check_columns(to_device_qcsr(dict(fx, col_idx=col_idx))).flags == expect
