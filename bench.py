@@ -35,11 +35,42 @@ def log(msg: str) -> None:
 
 
 def host_cores() -> int:
+    """Threads for the CPU baselines: every core this process may run on, within the host's
+    CPU share for one GPU when the environment states it (OMP_NUM_THREADS)."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
         n = os.cpu_count() or 1
-    return max(1, min(n, 16))
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    if share.isdigit() and int(share) > 0:
+        n = min(n, int(share))
+    return max(1, n)
+
+
+def host_description() -> dict:
+    """What the CPU baseline ran on: nproc, the affinity mask (as CPU ranges) and the model."""
+    try:
+        cpus = sorted(os.sched_getaffinity(0))
+    except AttributeError:
+        cpus = list(range(os.cpu_count() or 1))
+    ranges, start = [], None
+    for i, c in enumerate(cpus):
+        if start is None:
+            start = c
+        if i + 1 == len(cpus) or cpus[i + 1] != c + 1:
+            ranges.append(f"{start}-{c}" if c != start else str(start))
+            start = None
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "affinity": ",".join(ranges), "affinity_cpus": len(cpus),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"), "threads_used": host_cores(),
+            "cpu_model": model}
 
 
 def time_launches(torch, launch, steps: int, warmup: int, stream):
@@ -61,7 +92,11 @@ def time_launches(torch, launch, steps: int, warmup: int, stream):
     return wall_ms, ev
 
 
-def cpu_baseline_qcsr(m, w, sample_rows: int, threads: int) -> dict:
+def cpu_baseline_qcsr(m, w, out, sample_rows: int, threads: int) -> tuple[dict, dict]:
+    """Times the oracle's row-parallel fp32 restatement on the first `sample_rows` rows, then
+    (untimed) checks the GPU's timed output on those rows against it: the CPU product and
+    its magnitude Sigma |x||w| give |gpu - cpu| <= 1e-4 + 1e-4 |cpu| + 2^-20 Sigma |x||w|
+    per element (both fp32, only the summation order differs)."""
     import numpy as np
 
     from oracle import pyoracle
@@ -78,17 +113,25 @@ def cpu_baseline_qcsr(m, w, sample_rows: int, threads: int) -> dict:
     offsets = m.column_offsets.cpu().numpy()
     wn = w.cpu().numpy()
     args = (m.bits, m.decode_policy, rows, m.cols, rp, prp, cols, packed, scales, offsets, None, wn)
-    pyoracle.qcsr_spmm_f32_mt(*args, threads=threads)  # warm caches / page-in
+    cpu_out = pyoracle.qcsr_spmm_f32_mt(*args, threads=threads)  # warm caches / page-in
     times = []
     for _ in range(3):
         t0 = time.perf_counter()
-        pyoracle.qcsr_spmm_f32_mt(*args, threads=threads)
+        cpu_out = pyoracle.qcsr_spmm_f32_mt(*args, threads=threads)
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
-    return {"value": nnz / t, "unit": "nnz/s", "cores": threads, "kind": "port",
+    base = {"value": nnz / t, "unit": "nnz/s", "cores": threads, "kind": "port",
             "sample": f"first {rows} of {m.rows} rows ({nnz} nnz), median of 3 after 1 warmup; "
                       f"oracle or_qcsr_spmm_f32_mt (decode + fp32 FMA, AVX2, row-parallel)",
-            "seconds": t}
+            "seconds": t, "host": host_description()}
+    mag = pyoracle.qcsr_spmm_f32_mt(*args, threads=threads, magnitude=True)
+    got = out[:rows].cpu().numpy()
+    err = np.abs(got.astype(np.float64) - cpu_out)
+    bound = 1e-4 + 1e-4 * np.abs(cpu_out) + 2.0 ** -20 * mag
+    check = {"rows": rows, "elements": int(got.size), "mismatches": int((err > bound).sum()),
+             "max_abs_err": float(err.max()) if got.size else 0.0,
+             "rule": "|gpu - cpu_fp32| <= 1e-4 + 1e-4 |cpu| + 2^-20 sum |x||w|"}
+    return base, check
 
 
 def bench_qcsr(args, torch, cfg, n_out: int) -> dict:
@@ -142,25 +185,47 @@ def bench_qcsr(args, torch, cfg, n_out: int) -> dict:
                      "valu_fp32_peak_tflops_nonpacked": 78.6},
     }
     if not args.no_cpu:
-        res["cpu_baseline"] = cpu_baseline_qcsr(m, w, args.cpu_rows, host_cores())
-        res["parity_sample"] = parity_sample_qcsr(m, w, out, min(args.cpu_rows, 2000))
+        res["cpu_baseline"], res["full_output_check"] = cpu_baseline_qcsr(
+            m, w, out, args.cpu_rows, host_cores())
+    res["parity_sample"] = parity_sample_qcsr(m, w, out, 2000, seed=cfg.seed)
     return res
 
 
-def parity_sample_qcsr(m, w, out, rows: int) -> dict:
-    """The timed output's first rows against the oracle's float64 referee, at the tests'
-    tolerance (1e-4 abs-scaled + 1e-4 relative)."""
+def parity_sample_qcsr(m, w, out, count: int, seed: int) -> dict:
+    """The timed output against the oracle's float64 referee on a seeded sample of rows
+    spread over the whole matrix, plus the first 64 rows and the last 600 (the last
+    workgroup of 512 rows, whose windows reach the array ends), at the tests' tolerance
+    (1e-4 + 1e-4 relative + 1e-4 sum |x||w|)."""
+    import numpy as np
+
     from oracle import pyoracle
 
-    rp = m.row_ptr[: rows + 1].cpu().numpy()
-    prp = m.packed_row_ptr[: rows + 1].cpu().numpy()
-    nnz = int(rp[-1])
+    rng = np.random.default_rng(seed & 0xFFFFFFFF)
+    tail = np.arange(max(0, m.rows - 600), m.rows)
+    picks = np.unique(np.concatenate([np.arange(min(64, m.rows)), tail,
+                                      rng.choice(m.rows, size=min(count, m.rows), replace=False)]))
+    rp = m.row_ptr.cpu().numpy().astype(np.int64)
+    prp = m.packed_row_ptr.cpu().numpy().astype(np.int64)
+    lens, blens = rp[picks + 1] - rp[picks], prp[picks + 1] - prp[picks]
+    # gather the sampled rows' entries and code bytes on the device into a compact matrix
+    idx = np.concatenate([np.arange(a, b) for a, b in zip(rp[picks], rp[picks + 1])]) if lens.sum() else np.zeros(0, np.int64)
+    bidx = np.concatenate([np.arange(a, b) for a, b in zip(prp[picks], prp[picks + 1])]) if blens.sum() else np.zeros(0, np.int64)
+    import torch
+    dev = m.col_idx.device
+    cols = m.col_idx[torch.from_numpy(idx).to(dev)].cpu().numpy()
+    packed = m.packed_values[torch.from_numpy(bidx).to(dev)].cpu().numpy()
+    sub_rp = np.zeros(len(picks) + 1, np.int32)
+    sub_rp[1:] = np.cumsum(lens)
+    sub_prp = np.zeros(len(picks) + 1, np.int32)
+    sub_prp[1:] = np.cumsum(blens)
     ref, mag = pyoracle.qcsr_spmm_referee(
-        m.bits, m.decode_policy, rows, m.cols, rp, prp, m.col_idx[:nnz].cpu().numpy(),
-        m.packed_values[: int(prp[-1]) + 16].cpu().numpy(), m.column_scales.cpu().numpy(),
+        m.bits, m.decode_policy, len(picks), m.cols, sub_rp, sub_prp, cols,
+        np.concatenate([packed, np.zeros(16, np.uint8)]), m.column_scales.cpu().numpy(),
         m.column_offsets.cpu().numpy(), None, w.cpu().numpy())
-    cmp = pyoracle.compare(ref, out[:rows].cpu().numpy(), 1e-4, 1e-4, mag)
-    return {"rows": rows, "within_tolerance": bool(cmp["within_tolerance"]),
+    got = out[torch.from_numpy(picks).to(dev)].cpu().numpy()
+    cmp = pyoracle.compare(ref, got, 1e-4, 1e-4, mag)
+    return {"rows": int(len(picks)), "sample": "seeded uniform over all rows + first 64 + last 600",
+            "within_tolerance": bool(cmp["within_tolerance"]),
             "max_relative_error": float(cmp["max_relative_error"])}
 
 
@@ -225,12 +290,24 @@ def bench_bell(args, torch, cfg) -> dict:
         idx = m.block_col_idx[:rb].cpu().numpy()
         vals = m.values[:rows].view(torch.int16).cpu().numpy().view(np.uint16)
         wn = w.view(torch.int16).cpu().numpy().view(np.uint16)
-        t1 = time.perf_counter()
-        pyoracle.bell_spmm_referee(rows, m.cols, bs, m.ell_cols, idx, vals, wn,
-                                   value_type=pyoracle.BF16, rhs_type=pyoracle.BF16,
-                                   want_magnitude=False)
-        t = time.perf_counter() - t1
+        threads = host_cores()
+        cpu_out = pyoracle.bell_spmm_bf16_mt(rows, m.cols, bs, m.ell_cols, idx, vals, wn,
+                                             threads=threads)  # warm caches / page-in
+        times = []
+        for _ in range(3):
+            t1 = time.perf_counter()
+            cpu_out = pyoracle.bell_spmm_bf16_mt(rows, m.cols, bs, m.ell_cols, idx, vals, wn,
+                                                 threads=threads)
+            times.append(time.perf_counter() - t1)
+        t = statistics.median(times)
         nvalid = int((idx != np.uint32(0xFFFFFFFF).astype(idx.dtype)).sum())
+        got = out[:rows].cpu().numpy()
+        err = np.abs(got.astype(np.float64) - cpu_out)
+        res["full_output_check"] = {
+            "rows": rows, "elements": int(got.size),
+            "mismatches": int((err > 1e-4 + 1e-4 * np.abs(cpu_out)).sum()),
+            "max_abs_err": float(err.max()) if got.size else 0.0,
+            "rule": "|gpu - cpu_fp32| <= 1e-4 + 1e-4 |cpu|"}
         prb = min(rb, 4096 // bs)
         ref, mag = pyoracle.bell_spmm_referee(prb * bs, m.cols, bs, m.ell_cols, idx[:prb],
                                               vals[:prb * bs], wn, value_type=pyoracle.BF16,
@@ -239,10 +316,11 @@ def bench_bell(args, torch, cfg) -> dict:
         res["parity_sample"] = {"rows": prb * bs, "within_tolerance": bool(cmp["within_tolerance"]),
                                 "max_relative_error": float(cmp["max_relative_error"])}
         res["cpu_baseline"] = {"value": nvalid * bs * bs / t, "unit": "stored block elements/s",
-                               "cores": 1, "kind": "port",
-                               "sample": f"first {rows} of {m.rows} rows ({nvalid} blocks), one pass of "
-                                         f"the oracle's float64 Blocked-ELL referee (single thread)",
-                               "seconds": t}
+                               "cores": threads, "kind": "port",
+                               "sample": f"first {rows} of {m.rows} rows ({nvalid} blocks), median of 3 "
+                                         f"after 1 warmup; oracle or_bell_spmm_bf16_mt (fp32 FMA in slot "
+                                         f"order, AVX2, row-block-parallel, zero values skipped)",
+                               "seconds": t, "host": host_description()}
     return res
 
 
@@ -266,7 +344,6 @@ def bench_cpbp(args, torch, cfg) -> dict:
                                        window_size=cfg.window_size)
     torch.cuda.synchronize()
     build_ms = (time.perf_counter() - tb) * 1e3
-    del d_offs, d_feats, d_vals
     weights = dense_normal((cfg.genes,), 1.0, torch.float32, seed=cfg.seed + 1)
     out = torch.empty(cfg.rows, dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
@@ -283,6 +360,17 @@ def bench_cpbp(args, torch, cfg) -> dict:
     kern_ms = statistics.mean(ev)
     alg_bytes = tiles.nbytes_algorithmic()
     achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
+    # the N = 1 CSR comparator on the same canonical matrix, as the reference's reduction
+    # bench times it (components/CellPack/bench/feature_weighted_row_reduction_bench.cu:339-344)
+    from cellerator_amd import csr_spmv
+    spmv_out = torch.empty(cfg.rows, dtype=torch.float32, device="cuda")
+    _, spmv_ev = time_launches(torch, lambda: csr_spmv(d_offs, d_feats, d_vals, weights, out=spmv_out,
+                                                         stream=stream),
+                               args.steps, args.warmup, stream)
+    spmv_ms = statistics.mean(spmv_ev)
+    spmv_bytes = (cfg.rows + 1) * 4 + nnz * 8 + cfg.genes * 4 + cfg.rows * 4
+    spmv_vs_tiles = float(torch.max(torch.abs(spmv_out - out)).item())
+    del d_offs, d_feats, d_vals
     res = {
         "metric": "CP-BP feature-weighted row reduction: nnz/s + effective HBM GB/s (% roofline), 2M cells, 64-row tiles",
         "value": nnz / (wall_ms * 1e-3), "unit": "nnz/s", "ms_per_step": wall_ms,
@@ -296,6 +384,10 @@ def bench_cpbp(args, torch, cfg) -> dict:
                      "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(cfg.name),
                      "kernel": "cpbp_reduce_kernel<u64,f32,lds-weights>", "kernel_ms_mean": kern_ms,
                      "kernel_ms_median": statistics.median(ev), "algorithmic_bytes": alg_bytes},
+        "csr_spmv_comparator": {"kernel": "csr_spmv_kernel<f32>", "kernel_ms_mean": spmv_ms,
+                                "algorithmic_bytes": spmv_bytes,
+                                "achieved_gbs": spmv_bytes / (spmv_ms * 1e-3) / 1e9,
+                                "max_abs_diff_vs_tiles": spmv_vs_tiles},
     }
     if not args.no_cpu:
         from oracle import pyoracle
@@ -304,14 +396,20 @@ def bench_cpbp(args, torch, cfg) -> dict:
         sub_offs = offs[:rows + 1]
         n = int(sub_offs[-1])
         wn = weights.cpu().numpy()
-        t1 = time.perf_counter()
-        ref = pyoracle.cpbp_canonical(sub_offs, feats[:n], vals[:n], wn)
-        t = time.perf_counter() - t1
-        res["cpu_baseline"] = {"value": n / t, "unit": "nnz/s", "cores": 1, "kind": "port",
-                               "sample": f"first {rows} of {cfg.rows} rows ({n} nnz), one pass of the "
-                                         f"oracle's canonical referee (fp32 accumulate, single thread)",
-                               "seconds": t}
-        # the timed output, checked on the same rows against the referee (reference
+        threads = host_cores()
+        ref = pyoracle.cpbp_canonical_mt(sub_offs, feats[:n], vals[:n], wn, threads=threads)
+        times = []
+        for _ in range(3):
+            t1 = time.perf_counter()
+            ref = pyoracle.cpbp_canonical_mt(sub_offs, feats[:n], vals[:n], wn, threads=threads)
+            times.append(time.perf_counter() - t1)
+        t = statistics.median(times)
+        res["cpu_baseline"] = {"value": n / t, "unit": "nnz/s", "cores": threads, "kind": "port",
+                               "sample": f"first {rows} of {cfg.rows} rows ({n} nnz), median of 3 after "
+                                         f"1 warmup; oracle or_cpbp_canonical_mt (the canonical referee, "
+                                         f"fp32 accumulate, row-parallel)",
+                               "seconds": t, "host": host_description()}
+        # the timed output, checked on the same rows against the float64 referee (reference
         # tolerance 1e-5 abs + 1e-5 rel, widened for fp32 reordering)
         got = out[:rows].cpu().numpy()
         ref64, mag = pyoracle.cpbp_canonical_f64(sub_offs, feats[:n], vals[:n], wn)
@@ -358,8 +456,7 @@ def main() -> int:
     ap.add_argument("--config", default="c3", choices=["c3", "c3n128", "c2", "c4", "c5"])
     ap.add_argument("--rows", type=int, default=0, help="override the row count (smaller runs)")
     ap.add_argument("--cpu-rows", type=int, default=0,
-                    help="rows of the CPU-baseline sample (0: the whole matrix for C2/C3/C5, "
-                         "16,384 rows for C4's float64 Blocked-ELL referee)")
+                    help="rows of the CPU-baseline sample (0: the whole matrix)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--ungrouped", action="store_true",
                     help="C4: time the per-row-block MFMA kernel without the row-block grouping")
@@ -383,7 +480,7 @@ def main() -> int:
     if args.calibrate_copy:
         return calibrate_copy(args.calibrate_copy, max(args.steps, 1))
     if args.cpu_rows <= 0:
-        args.cpu_rows = 16_384 if args.config == "c4" else 1 << 31
+        args.cpu_rows = 1 << 31  # the whole matrix
     from cellerator_amd.synth import C2, C3
 
     if args.config in ("c4", "c5"):

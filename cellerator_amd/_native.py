@@ -175,6 +175,8 @@ ENGINE_SIGNATURES = {
                                             i64, C.POINTER(CxSpmmEpilogue), p_void]),
     "cx_qcsr_pack_gene_affine": (C.c_int, [p_void, p_void, u32, p_void, p_void]),
     "cx_qcsr_check_columns": (C.c_int, [p_void, p_void, p_void]),
+    "cx_qcsr_check_columns_sync": (C.c_int, [p_void, C.POINTER(u32), p_void]),
+    "cx_stream_synchronize": (C.c_int, [p_void]),
     "cx_qcsr_transpose_workspace": (C.c_int, [C.POINTER(CxQcsrMatrix), C.POINTER(u64)]),
     "cx_qcsr_transpose": (C.c_int, [C.POINTER(CxQcsrMatrix), p_void, p_void, p_void, p_void, u64,
                                     p_void]),
@@ -244,6 +246,10 @@ ENGINE_SIGNATURES = {
     "cellerator_sparse_projection_forward": (
         C.c_int, [p_void, C.POINTER(CelleratorSparseLayoutDesc), C.POINTER(CelleratorTensorDesc),
                   C.POINTER(CelleratorTensorDesc), C.POINTER(p_void)]),
+    "cellerator_sparse_projection_backward": (
+        C.c_int, [p_void, C.POINTER(CelleratorSparseLayoutDesc), C.POINTER(CelleratorTensorDesc),
+                  C.POINTER(CelleratorTensorDesc), C.POINTER(CelleratorTensorDesc),
+                  C.POINTER(CelleratorTensorDesc)]),
 }
 
 SYNTH_SIGNATURES = {

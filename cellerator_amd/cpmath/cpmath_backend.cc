@@ -21,9 +21,31 @@ constexpr u32 projection_capacity = 64u;
 // bytes, at most this many (65,536 genes x 256 columns of bf16).
 constexpr u64 mfma_panel_limit = 65536ull * 256ull * 2ull;
 
+// Physical preparations of a quantized CSR projection (prepare_quantized_csr_state).
+struct qcsr_prepared {
+    bool sorted = false;                  // the structure below passed the column-order check
+    const int32_t *row_ptr = nullptr;     // structure the check ran on
+    const int32_t *col_idx = nullptr;
+    float *pairs = nullptr;               // interleaved (scale, offset) of the plane below
+    const void *scales = nullptr;
+    const void *offsets = nullptr;
+    u64 generation = 0u;
+};
+
+// Physical preparations of a Blocked-ELL projection (prepare_blocked_ell_state).
+struct bell_prepared {
+    const void *weights = nullptr;        // W the panel was packed from
+    uint16_t *panel = nullptr;
+    bool grouped = false;
+    const uint32_t *block_col_idx = nullptr;  // structure the groups were planned on
+    cx_bell_groups groups{};
+};
+
 struct projection_state {
     bool live = false;
     projection_declaration declaration{};
+    qcsr_prepared qcsr{};
+    bell_prepared bell{};
     execution::operand_axis_contract inputs[3]{};  // sparse, dense, bias (epilogue only)
     execution::operand_axis_contract outputs[1]{};
     execution::output_axis_contract orders[2]{};
@@ -34,6 +56,7 @@ struct projection_state {
 projection_state projections[projection_capacity];
 std::mutex projections_mutex;
 thread_local char engine_error[512] = "";
+thread_local const char *dispatched = "";
 
 constexpr core::operation_status fail(code c, const char *message) noexcept {
     return {c, execution::binding_validation_code::ok, message};
@@ -247,6 +270,8 @@ core::operation_status run_quantized_csr(const core::prepared_operation &p,
     if (a.packed_values != nullptr || a.values != nullptr || a.column_scales != nullptr
         || a.column_offsets != nullptr || a.row_offsets != nullptr)
         return bad_launch("values and quantization metadata travel in the value plane");
+    if (a.flags != 0u)
+        return bad_launch("view flags are established by prepare_quantized_csr_state, not the caller");
     const execution::value_plane *plane = value_plane_of(*s, p, l);
     if (plane == nullptr || plane->element_count != a.nnz)
         return bad_launch("one value plane of the structure with nnz elements is required");
@@ -260,6 +285,13 @@ core::operation_status run_quantized_csr(const core::prepared_operation &p,
         a.packed_values = static_cast<const uint8_t *>(plane->values);
         a.column_scales = static_cast<const float *>(q.scales);
         a.column_offsets = static_cast<const float *>(q.offsets);
+        const qcsr_prepared &pre = s->qcsr;
+        if (pre.pairs != nullptr && pre.generation == plane->generation.value
+            && pre.scales == q.scales && pre.offsets == q.offsets) {
+            a.decode_policy = CX_DECODE_PER_GENE_AFFINE_PAIRS;
+            a.column_scales = pre.pairs;
+            a.column_offsets = nullptr;
+        }
     } else {
         if (q.kind != execution::quantization_kind::none)
             return bad_launch("plain CSR values must not be quantized");
@@ -275,10 +307,17 @@ core::operation_status run_quantized_csr(const core::prepared_operation &p,
         return bad_launch("Y must be a row-major f32 [cells x N] tensor");
     cx_spmm_epilogue ep;
     if (const char *why = bind_epilogue(p, d, l, y, &ep)) return bad_launch(why);
+    const bool sorted = s->qcsr.sorted && s->qcsr.row_ptr == a.row_ptr && s->qcsr.col_idx == a.col_idx;
+    if (sorted) a.flags = CX_QCSR_COLUMNS_SORTED;
     const int rc = cx_qcsr_spmm_fwd_epilogue(&a, w.data, engine_dtype(w.value_type), w.stride[0],
                                              d.output_columns, static_cast<float *>(y.data),
                                              y.stride[0], &ep, l.stream.stream);
-    return rc == CX_STATUS_SUCCESS ? core::operation_status{} : engine_failed(rc);
+    if (rc != CX_STATUS_SUCCESS) return engine_failed(rc);
+    const bool pairs = a.decode_policy == CX_DECODE_PER_GENE_AFFINE_PAIRS;
+    dispatched = a.bits == 0u ? "qcsr:plain"
+        : pairs ? (sorted ? "qcsr:pairs+sorted" : "qcsr:pairs")
+                : (sorted ? "qcsr:gene-affine+sorted" : "qcsr:gene-affine");
+    return {};
 }
 
 core::operation_status run_blocked_ell(const core::prepared_operation &p,
@@ -313,17 +352,32 @@ core::operation_status run_blocked_ell(const core::prepared_operation &p,
     if (const char *why = bind_epilogue(p, d, l, y, &ep)) return bad_launch(why);
     int rc;
     if (core::same_stable_id(p.kernel, blocked_ell_mfma_kernel_id)) {
-        auto *panel = static_cast<uint16_t *>(l.workspace.data);
-        rc = cx_bell_pack_rhs(static_cast<const uint16_t *>(w.data), w.stride[0], d.cols,
-                              d.output_columns, panel, l.stream.stream);
+        const bell_prepared &pre = s->bell;
+        const bool prepacked = pre.panel != nullptr && pre.weights == w.data;
+        const uint16_t *panel = pre.panel;
+        rc = CX_STATUS_SUCCESS;
+        if (!prepacked) {
+            auto *scratch = static_cast<uint16_t *>(l.workspace.data);
+            rc = cx_bell_pack_rhs(static_cast<const uint16_t *>(w.data), w.stride[0], d.cols,
+                                  d.output_columns, scratch, l.stream.stream);
+            panel = scratch;
+        }
+        const bool grouped = pre.grouped && pre.block_col_idx == a.block_col_idx;
         if (rc == CX_STATUS_SUCCESS)
-            rc = cx_bell_spmm_fwd_packed_epilogue(&a, panel, d.output_columns,
-                                                  static_cast<float *>(y.data), y.stride[0], &ep,
-                                                  l.stream.stream);
+            rc = grouped
+                ? cx_bell_spmm_fwd_grouped_epilogue(&a, panel, &pre.groups, d.output_columns,
+                                                    static_cast<float *>(y.data), y.stride[0], &ep,
+                                                    l.stream.stream)
+                : cx_bell_spmm_fwd_packed_epilogue(&a, panel, d.output_columns,
+                                                   static_cast<float *>(y.data), y.stride[0], &ep,
+                                                   l.stream.stream);
+        dispatched = grouped ? (prepacked ? "bell:grouped+panel" : "bell:grouped+repack")
+                             : (prepacked ? "bell:mfma+panel" : "bell:mfma+repack");
     } else {
         rc = cx_bell_spmm_fwd_epilogue(&a, w.data, engine_dtype(w.value_type), w.stride[0],
                                        d.output_columns, static_cast<float *>(y.data),
                                        y.stride[0], &ep, l.stream.stream);
+        dispatched = "bell:generic";
     }
     return rc == CX_STATUS_SUCCESS ? core::operation_status{} : engine_failed(rc);
 }
@@ -357,7 +411,9 @@ core::operation_status run_cpbp(const core::prepared_operation &p,
         return bad_launch("row values must be a contiguous f32 [cells] tensor");
     const int rc = cx_cpbp_reduce(&t, static_cast<const float *>(w.data), d.cols,
                                   static_cast<float *>(y.data), d.rows, l.stream.stream);
-    return rc == CX_STATUS_SUCCESS ? core::operation_status{} : engine_failed(rc);
+    if (rc != CX_STATUS_SUCCESS) return engine_failed(rc);
+    dispatched = "cpbp";
+    return {};
 }
 
 // ---- prepare --------------------------------------------------------------------------
@@ -583,6 +639,83 @@ core::operation_candidate cpbp_candidate() noexcept {
         core::operation_kind::weighted_relation_reduce, core::projection_kind::native_row_masked,
         supports_cpbp, 0u);
 }
+
+core::operation_status prepare_quantized_csr_state(execution::projection_handle projection,
+                                                   const cx_qcsr_matrix &structure,
+                                                   const execution::value_plane *plane,
+                                                   float *pairs, void *stream) noexcept {
+    std::lock_guard<std::mutex> lock(projections_mutex);
+    projection_state *s = find_live(projection);
+    if (s == nullptr) return fail(code::invalid_argument, "projection is not declared");
+    const projection_declaration &d = s->declaration;
+    if (d.key.kind != core::projection_kind::csr)
+        return fail(code::unsupported_projection, "not a quantized CSR projection");
+    if (structure.rows != d.rows || structure.cols != d.cols
+        || structure.nnz != d.structure.logical_edge_count || structure.row_ptr == nullptr
+        || (structure.nnz != 0u && structure.col_idx == nullptr))
+        return fail(code::invalid_argument, "structure differs from the declared projection");
+    qcsr_prepared pre{};
+    if (pairs != nullptr) {
+        if (plane == nullptr || d.key.variant == 0u
+            || plane->quantization.kind != execution::quantization_kind::per_module
+            || plane->quantization.scale_type != numeric_type::f32
+            || plane->quantization.group_count != d.cols
+            || (plane->quantization.offsets != nullptr
+                && plane->quantization.offset_type != numeric_type::f32)
+            || !execution::same_handle(plane->structure, d.structure.identity))
+            return fail(code::invalid_argument, "pairs need the projection's per-gene f32 quantization plane");
+        int rc = cx_qcsr_pack_gene_affine(static_cast<const float *>(plane->quantization.scales),
+                                          static_cast<const float *>(plane->quantization.offsets),
+                                          d.cols, pairs, stream);
+        if (rc != CX_STATUS_SUCCESS) return engine_failed(rc);
+        pre.pairs = pairs;
+        pre.scales = plane->quantization.scales;
+        pre.offsets = plane->quantization.offsets;
+        pre.generation = plane->generation.value;
+    }
+    uint32_t host_flag = 0u;
+    const int rc = cx_qcsr_check_columns_sync(&structure, &host_flag, stream);
+    if (rc != CX_STATUS_SUCCESS) return engine_failed(rc);
+    pre.sorted = (host_flag & CX_QCSR_COLUMNS_SORTED) != 0u;
+    pre.row_ptr = structure.row_ptr;
+    pre.col_idx = structure.col_idx;
+    s->qcsr = pre;
+    return {};
+}
+
+core::operation_status prepare_blocked_ell_state(execution::projection_handle projection,
+                                                 const cx_bell_matrix &structure,
+                                                 const uint16_t *weights, int64_t weights_ld,
+                                                 uint16_t *panel, const cx_bell_groups *groups,
+                                                 void *stream) noexcept {
+    std::lock_guard<std::mutex> lock(projections_mutex);
+    projection_state *s = find_live(projection);
+    if (s == nullptr) return fail(code::invalid_argument, "projection is not declared");
+    const projection_declaration &d = s->declaration;
+    if (d.key.kind != core::projection_kind::blocked_ell)
+        return fail(code::unsupported_projection, "not a Blocked-ELL projection");
+    if (structure.rows != d.rows || structure.cols != d.cols || structure.block_size != d.block_size
+        || structure.block_col_idx == nullptr)
+        return fail(code::invalid_argument, "structure differs from the declared projection");
+    bell_prepared pre{};
+    if (panel != nullptr) {
+        if (weights == nullptr) return fail(code::invalid_argument, "the panel is packed from weights");
+        int rc = cx_bell_pack_rhs(weights, weights_ld, d.cols, d.output_columns, panel, stream);
+        if (rc == CX_STATUS_SUCCESS) rc = cx_stream_synchronize(stream);
+        if (rc != CX_STATUS_SUCCESS) return engine_failed(rc);
+        pre.weights = weights;
+        pre.panel = panel;
+    }
+    if (groups != nullptr) {
+        pre.grouped = true;
+        pre.groups = *groups;
+        pre.block_col_idx = structure.block_col_idx;
+    }
+    s->bell = pre;
+    return {};
+}
+
+const char *last_dispatch() noexcept { return dispatched; }
 
 const char *last_engine_error() noexcept { return engine_error; }
 

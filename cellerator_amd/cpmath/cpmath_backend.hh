@@ -92,6 +92,43 @@ struct projection_declaration {
 core::operation_status declare_projection(const projection_declaration &declaration) noexcept;
 core::operation_status retire_projection(execution::projection_handle projection) noexcept;
 
+// Persistent physical state of a declared quantized CSR projection. A one-time preparation,
+// not a launch: it enqueues work on `stream` and synchronizes it.
+//  * The structure's column order is checked once on the device (cx_qcsr_check_columns).
+//    Launches whose sparse view carries that structure (the same row_ptr and col_idx; the
+//    core already pins the structure handle and epoch) then run with
+//    CX_QCSR_COLUMNS_SORTED, the kernels that skip the per-entry order check.
+//  * With `pairs` (device, 2 x genes floats, caller-owned, outliving the projection), the
+//    per-gene scales and offsets of `plane` are interleaved into it. Launches whose value
+//    plane has the same generation and metadata pointers then decode from the pairs
+//    (CX_DECODE_PER_GENE_AFFINE_PAIRS, bit-identical to the separate arrays); any other
+//    plane decodes from its own arrays.
+// A sparse view's own flags must be 0: only this preparation establishes them.
+core::operation_status prepare_quantized_csr_state(execution::projection_handle projection,
+                                                   const cx_qcsr_matrix &structure,
+                                                   const execution::value_plane *plane,
+                                                   float *pairs, void *stream) noexcept;
+
+// Persistent state of a declared Blocked-ELL projection for the MFMA kernels (bf16 values
+// and weights, 32 x 32 blocks). A one-time preparation that synchronizes `stream`.
+//  * `panel` (device, ceil(genes/32) * 32 * N bf16, caller-owned) is packed now from
+//    `weights` (device bf16 [genes x N], row stride weights_ld). Launches whose W is that
+//    same pointer read the panel instead of repacking W into the workspace. Call again
+//    after W is written in place: the panel is the weight generation packed last.
+//  * `groups` (cx_bell_plan_groups of this structure, device arrays, caller-owned): launches
+//    whose view carries the same block_col_idx run the grouped kernel. NULL keeps the
+//    per-row-block kernel.
+core::operation_status prepare_blocked_ell_state(execution::projection_handle projection,
+                                                 const cx_bell_matrix &structure,
+                                                 const uint16_t *weights, int64_t weights_ld,
+                                                 uint16_t *panel, const cx_bell_groups *groups,
+                                                 void *stream) noexcept;
+
+// Kernel form the last successful run on this thread dispatched, e.g.
+// "qcsr:pairs+sorted", "qcsr:gene-affine", "bell:grouped+panel", "bell:mfma+repack",
+// "bell:generic", "cpbp".
+const char *last_dispatch() noexcept;
+
 core::operation_candidate quantized_csr_candidate() noexcept;
 core::operation_candidate blocked_ell_candidate() noexcept;
 core::operation_candidate cpbp_candidate() noexcept;

@@ -533,6 +533,31 @@ extern "C" int cx_qcsr_check_columns(const cx_qcsr_matrix *m, uint32_t *device_f
     return check_launch("cx_qcsr_check_columns");
 }
 
+extern "C" int cx_qcsr_check_columns_sync(const cx_qcsr_matrix *m, uint32_t *host_flag, void *stream) {
+    using namespace cx;
+    clear_error();
+    if (host_flag == nullptr) return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_check_columns_sync: null flag");
+    *host_flag = 0u;
+    std::uint32_t *flag = nullptr;
+    hipError_t e = hipMalloc(reinterpret_cast<void **>(&flag), sizeof(std::uint32_t));
+    if (e != hipSuccess) return hip_fail(e, "cx_qcsr_check_columns_sync: hipMalloc");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int rc = cx_qcsr_check_columns(m, flag, stream);
+    if (rc == CX_STATUS_SUCCESS) {
+        e = hipMemcpyAsync(host_flag, flag, sizeof(std::uint32_t), hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) rc = hip_fail(e, "cx_qcsr_check_columns_sync");
+    }
+    (void)hipFree(flag);
+    return rc;
+}
+
+extern "C" int cx_stream_synchronize(void *stream) {
+    cx::clear_error();
+    const hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? CX_STATUS_SUCCESS : cx::hip_fail(e, "cx_stream_synchronize");
+}
+
 extern "C" int cx_qcsr_pack_gene_affine(const float *scales, const float *offsets, uint32_t cols,
                                         float *pairs, void *stream) {
     using namespace cx;

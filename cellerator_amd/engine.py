@@ -32,6 +32,16 @@ def _stream(stream) -> int:
     return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
 
 
+def _torch_stream(stream, device) -> torch.cuda.Stream:
+    """`stream` (None = the current stream, a torch stream, or a raw hipStream_t handle) as
+    a torch stream object that can be made current."""
+    if stream is None:
+        return torch.cuda.current_stream(device)
+    if isinstance(stream, torch.cuda.Stream):
+        return stream
+    return torch.cuda.ExternalStream(int(stream), device=device)
+
+
 def _require_cuda(*tensors: Optional[torch.Tensor]) -> None:
     for t in tensors:
         if t is not None and not t.is_cuda:
@@ -156,10 +166,16 @@ def qcsr_check_columns(m: QcsrMatrix, stream=None) -> QcsrMatrix:
     else flags = 0. Run once per structure: the gene-part kernels then skip their per-entry
     out-of-order check."""
     _require_cuda(m.row_ptr)
-    flag = torch.empty(1, dtype=torch.int32, device=m.row_ptr.device)
-    d = m.descriptor()
-    N.check("cx_qcsr_check_columns", N.engine().cx_qcsr_check_columns(C.byref(d), flag.data_ptr(), _stream(stream)))
-    return dataclasses.replace(m, flags=int(flag.item()) & N.QCSR_COLUMNS_SORTED)
+    dev = m.row_ptr.device
+    # Allocation, launch and read all run on the check's stream: the flag's read-back then
+    # waits for the check, and the buffer is released on the stream that wrote it.
+    with torch.cuda.stream(_torch_stream(stream, dev)) as s:
+        flag = torch.zeros(1, dtype=torch.int32, device=dev)
+        d = m.descriptor()
+        N.check("cx_qcsr_check_columns", N.engine().cx_qcsr_check_columns(
+            C.byref(d), flag.data_ptr(), s.cuda_stream))
+        value = int(flag.item())
+    return dataclasses.replace(m, flags=value & N.QCSR_COLUMNS_SORTED)
 
 
 def qcsr_transpose(m: QcsrMatrix, stream=None) -> QcsrMatrix:

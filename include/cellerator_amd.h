@@ -197,6 +197,15 @@ int cx_qcsr_pack_gene_affine(const float *scales, const float *offsets, uint32_t
  * counterpart in the reference. */
 int cx_qcsr_check_columns(const cx_qcsr_matrix *a, uint32_t *device_flag, void *stream);
 
+/* Synchronous form for preparation steps: runs cx_qcsr_check_columns on `stream`, waits for
+ * it and stores CX_QCSR_COLUMNS_SORTED or 0 in *host_flag. Allocates (and frees) one word of
+ * device memory, so it is not for launch paths. Engine addition, no reference counterpart. */
+int cx_qcsr_check_columns_sync(const cx_qcsr_matrix *a, uint32_t *host_flag, void *stream);
+
+/* Waits for the work enqueued on `stream` (a hipStream_t; NULL = the null stream). For host
+ * code that reaches the engine only through this C-ABI. Engine addition. */
+int cx_stream_synchronize(void *stream);
+
 /* ---- transpose and backward of the CSR SpMM ------------------------------------ */
 
 /* Device bytes of workspace cx_qcsr_transpose needs for `a`. */
@@ -700,6 +709,22 @@ cellerator_status cellerator_sparse_projection_forward(cellerator_context *conte
                                                        const cellerator_tensor_desc *rhs,
                                                        cellerator_tensor_desc *out,
                                                        cellerator_saved_state **saved_state);
+
+/* include/Cellerator/abi.h:120-126, src/abi/abi.cu:337-400: gradients of
+ * out = A . rhs. grad_values (F32 rank-1 [nnz], optional) = <grad_out[row_i,:], rhs[col_i,:]>;
+ * grad_rhs (F32 rank-2 [cols x N], optional) = A^T . grad_out; at least one is required.
+ * Layouts: CSR (F16, or additively F32, values) and QUANTIZED_CSR (additive); others return
+ * UNSUPPORTED as the reference does. rhs F32 (reference contract) or F16; grad_out F32.
+ * Deterministic: grad_rhs builds A^T (stable device sort) in the context scratch and sums
+ * each gene row in a fixed order, where the reference adds with float atomics. The scratch
+ * is the config's (too small -> INVALID_ARGUMENT) or, without one, the context's own block,
+ * grown on demand and released by cellerator_context_destroy. */
+cellerator_status cellerator_sparse_projection_backward(cellerator_context *context,
+                                                        const cellerator_sparse_layout_desc *layout,
+                                                        const cellerator_tensor_desc *rhs,
+                                                        const cellerator_tensor_desc *grad_out,
+                                                        cellerator_tensor_desc *grad_values,
+                                                        cellerator_tensor_desc *grad_rhs);
 
 #ifdef __cplusplus
 }

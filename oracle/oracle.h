@@ -134,6 +134,25 @@ int or_qcsr_spmm_f32_mt(uint32_t bits, uint32_t policy, int32_t rows, int32_t co
                         const float *row_offsets, const void *rhs, int rhs_type, uint32_t n,
                         uint64_t ldb, int32_t row_begin, int32_t row_end, float *out,
                         int threads);
+/* The same walk with |decoded x| and |w|: out = Sigma |x||w| per element (fp32), the
+ * magnitude term of the reordered-summation tolerance for a full-output comparison. */
+int or_qcsr_spmm_f32_mt_magnitude(uint32_t bits, uint32_t policy, int32_t rows, int32_t cols,
+                                  const int32_t *row_ptr, const int32_t *packed_row_ptr,
+                                  const int32_t *col_idx, const uint8_t *packed,
+                                  const float *col_scales, const float *col_offsets,
+                                  const float *row_offsets, const void *rhs, int rhs_type,
+                                  uint32_t n, uint64_t ldb, int32_t row_begin, int32_t row_end,
+                                  float *out, int threads);
+/* Row-parallel or_cpbp_canonical (bitwise equal to it: rows are independent). */
+int or_cpbp_canonical_mt(uint32_t rows, const uint32_t *row_offsets,
+                         const uint32_t *canonical_features, const void *values, int value_type,
+                         const float *weights, float *out, int threads);
+/* Row-block-parallel bf16 Blocked-ELL SpMM, fp32 accumulation in slot order per output
+ * element (blocked_ell_spmm_fwd_kernel_.cuh:1-33); rhs bf16 [cols x n] row-major, out fp32
+ * [rows x n]. Zero values are skipped (their products add nothing). CPU baseline. */
+int or_bell_spmm_bf16_mt(int32_t rows, int32_t cols, int32_t block_size, int32_t ell_cols,
+                         const uint32_t *block_col_idx, const uint16_t *values,
+                         const uint16_t *rhs, uint32_t n, float *out, int threads);
 
 /* ---- Blocked-ELL: quantized/blocked_ell.cuh:120-150 (column_for_slot, get_value);
  * kernels/blocked_ell_spmm_fwd_kernel_.cuh:1-33. value_type OR_BF16/OR_F16/OR_F32 for

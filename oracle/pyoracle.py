@@ -87,6 +87,11 @@ def lib() -> C.CDLL:
         _lib.or_qcsr_spmm_f32_mt.argtypes = [
             C.c_uint32, C.c_uint32, C.c_int32, C.c_int32] + [C.c_void_p] * 8 + [
             C.c_int, C.c_uint32, C.c_uint64, C.c_int32, C.c_int32, C.c_void_p, C.c_int]
+        _lib.or_qcsr_spmm_f32_mt_magnitude.argtypes = _lib.or_qcsr_spmm_f32_mt.argtypes
+        _lib.or_cpbp_canonical_mt.argtypes = [C.c_uint32] + [C.c_void_p] * 3 + [C.c_int] + [
+            C.c_void_p] * 2 + [C.c_int]
+        _lib.or_bell_spmm_bf16_mt.argtypes = [C.c_int32] * 4 + [C.c_void_p] * 3 + [
+            C.c_uint32, C.c_void_p, C.c_int]
         _lib.or_bell_spmm_referee.argtypes = [
             C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_void_p, C.c_void_p, C.c_int,
             C.c_uint32, C.c_uint32, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
@@ -234,7 +239,9 @@ def qcsr_spmm_referee(bits, policy, rows, cols, row_ptr, packed_row_ptr, col_idx
 
 
 def qcsr_spmm_f32_mt(bits, policy, rows, cols, row_ptr, packed_row_ptr, col_idx, packed,
-                     scales, offsets, row_offsets, rhs, row_begin=0, row_end=None, threads=1):
+                     scales, offsets, row_offsets, rhs, row_begin=0, row_end=None, threads=1,
+                     magnitude=False):
+    """Row-parallel fp32 product (or, with magnitude=True, Sigma |x||w| per element)."""
     row_end = rows if row_end is None else row_end
     row_ptr, packed_row_ptr = _c(row_ptr, np.int32), _c(packed_row_ptr, np.int32)
     col_idx, packed = _c(col_idx, np.int32), _c(packed, np.uint8)
@@ -242,10 +249,10 @@ def qcsr_spmm_f32_mt(bits, policy, rows, cols, row_ptr, packed_row_ptr, col_idx,
     rhs = np.ascontiguousarray(rhs)
     n = rhs.shape[1]
     out = np.zeros((row_end - row_begin, n), dtype=np.float32)
-    rc = lib().or_qcsr_spmm_f32_mt(bits, policy, rows, cols, _p(row_ptr), _p(packed_row_ptr),
-                                   _p(col_idx), _p(packed), _p(scales), _p(offsets),
-                                   _p(row_offsets), _p(rhs), _rhs_type(rhs), n, rhs.shape[1],
-                                   row_begin, row_end, _p(out), threads)
+    fn = lib().or_qcsr_spmm_f32_mt_magnitude if magnitude else lib().or_qcsr_spmm_f32_mt
+    rc = fn(bits, policy, rows, cols, _p(row_ptr), _p(packed_row_ptr), _p(col_idx), _p(packed),
+            _p(scales), _p(offsets), _p(row_offsets), _p(rhs), _rhs_type(rhs), n, rhs.shape[1],
+            row_begin, row_end, _p(out), threads)
     if rc != 0:
         raise ValueError(f"qcsr_spmm_f32_mt failed ({rc})")
     return out
@@ -298,6 +305,34 @@ def cpbp_canonical(row_offsets, features, values, weights, value_type=F32) -> np
                                  value_type, _p(weights), _p(out))
     if rc != 0:
         raise ValueError("cpbp_canonical failed")
+    return out
+
+
+def cpbp_canonical_mt(row_offsets, features, values, weights, value_type=F32, threads=1):
+    """Row-parallel cpbp_canonical (bitwise equal to it)."""
+    row_offsets, features = _c(row_offsets, np.uint32), _c(features, np.uint32)
+    values = np.ascontiguousarray(values)
+    weights = _c(weights, np.float32)
+    out = np.zeros(len(row_offsets) - 1, dtype=np.float32)
+    rc = lib().or_cpbp_canonical_mt(len(out), _p(row_offsets), _p(features), _p(values),
+                                    value_type, _p(weights), _p(out), threads)
+    if rc != 0:
+        raise ValueError("cpbp_canonical_mt failed")
+    return out
+
+
+def bell_spmm_bf16_mt(rows, cols, block_size, ell_cols, block_col_idx, values_bf16, rhs_bf16,
+                      threads=1):
+    """Row-block-parallel bf16 Blocked-ELL SpMM (fp32 [rows, n]); values and rhs as uint16
+    bf16 bit patterns."""
+    block_col_idx = _c(block_col_idx, np.uint32)
+    values_bf16, rhs_bf16 = _c(values_bf16, np.uint16), _c(rhs_bf16, np.uint16)
+    n = rhs_bf16.shape[1]
+    out = np.zeros((rows, n), dtype=np.float32)
+    rc = lib().or_bell_spmm_bf16_mt(rows, cols, block_size, ell_cols, _p(block_col_idx),
+                                    _p(values_bf16), _p(rhs_bf16), n, _p(out), threads)
+    if rc != 0:
+        raise ValueError("bell_spmm_bf16_mt failed")
     return out
 
 

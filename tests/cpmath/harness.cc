@@ -44,14 +44,24 @@ typedef struct h_case {
     uint32_t fused, epilogue_kind, affine, reserved3;
     const void *bias;
     float alpha, beta;
+    // Physical preparations before the launch (cpmath_backend.hh): quantized CSR -- check the
+    // column order (check_columns != 0) and interleave the plane's metadata into `pairs`
+    // (non-NULL); Blocked-ELL -- pack W into `panel` (non-NULL) and use `groups` (non-NULL,
+    // a cx_bell_groups). `repeats` runs the prepared operation that many times (0 -> 1).
+    float *pairs;
+    uint32_t check_columns, repeats;
+    uint16_t *panel;
+    const void *groups;
 } h_case;
 
 typedef struct h_result {
     int32_t prepare_status, status, binding, second_status;
     uint64_t kernel_low, kernel_high, workspace_bytes;
     uint32_t capability_flags, registered;
+    int32_t state_status, reserved;
     char message[160];
     char engine[256];
+    char dispatch[64];
 } h_result;
 
 int h_case_size(void) { return (int)sizeof(h_case); }
@@ -292,14 +302,36 @@ extern "C" int h_run(const h_case *c, h_result *r) {
         rel.projection_data = view_copy;
     }
 
-    s = core::run_prepared_operation(prepared, launch);
+    r->state_status = 0;
+    if (c->kind == 1 && (c->check_columns != 0u || c->pairs != nullptr)) {
+        const core::operation_status st = cp::prepare_quantized_csr_state(
+            d.key.runtime, *static_cast<const cx_qcsr_matrix *>(c->view), &plane, c->pairs, c->stream);
+        r->state_status = static_cast<int32_t>(st.code);
+        if (!st) { note(r, st, false); cp::retire_projection(d.key.runtime); return 0; }
+    }
+    if (c->kind == 2 && (c->panel != nullptr || c->groups != nullptr)) {
+        const core::operation_status st = cp::prepare_blocked_ell_state(
+            d.key.runtime, *static_cast<const cx_bell_matrix *>(c->view),
+            static_cast<const uint16_t *>(c->w), c->w_ld, c->panel,
+            static_cast<const cx_bell_groups *>(c->groups), c->stream);
+        r->state_status = static_cast<int32_t>(st.code);
+        if (!st) { note(r, st, false); cp::retire_projection(d.key.runtime); return 0; }
+    }
+
+    const uint32_t repeats = c->repeats == 0u ? 1u : c->repeats;
+    for (uint32_t i = 0; i < repeats; ++i) {
+        s = core::run_prepared_operation(prepared, launch);
+        if (!s) break;
+    }
     note(r, s, false);
+    std::strncpy(r->dispatch, cp::last_dispatch(), sizeof(r->dispatch) - 1u);
     if (s && c->y2 != nullptr) {
         // Rebinding without re-preparation: new W and Y pointers, same prepared record.
         w.data = const_cast<void *>(c->w2 != nullptr ? c->w2 : c->w);
         y.data = c->y2;
         const core::operation_status again = core::run_prepared_operation(prepared, launch);
         r->second_status = static_cast<int32_t>(again.code);
+        std::strncpy(r->dispatch, cp::last_dispatch(), sizeof(r->dispatch) - 1u);
     }
     if (c->mutation != retired_projection) cp::retire_projection(d.key.runtime);
     return 0;

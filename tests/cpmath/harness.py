@@ -49,7 +49,8 @@ class HCase(C.Structure):
                 ("stream", p), ("device", C.c_int32), ("reserved2", C.c_int32),
                 ("fused", C.c_uint32), ("epilogue_kind", C.c_uint32), ("affine", C.c_uint32),
                 ("reserved3", C.c_uint32), ("bias", p), ("alpha", C.c_float),
-                ("beta", C.c_float)]
+                ("beta", C.c_float), ("pairs", p), ("check_columns", C.c_uint32),
+                ("repeats", C.c_uint32), ("panel", p), ("groups", p)]
 
 
 class HResult(C.Structure):
@@ -57,7 +58,9 @@ class HResult(C.Structure):
                 ("second_status", C.c_int32), ("kernel_low", C.c_uint64),
                 ("kernel_high", C.c_uint64), ("workspace_bytes", C.c_uint64),
                 ("capability_flags", C.c_uint32), ("registered", C.c_uint32),
-                ("message", C.c_char * 160), ("engine", C.c_char * 256)]
+                ("state_status", C.c_int32), ("reserved", C.c_int32),
+                ("message", C.c_char * 160), ("engine", C.c_char * 256),
+                ("dispatch", C.c_char * 64)]
 
 
 _lib = None

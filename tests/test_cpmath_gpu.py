@@ -294,3 +294,136 @@ def test_blocked_ell_epilogue_through_reference_core():
                      epilogue=Epilogue(6, 2.0, 0.25, bias, direct))
     torch.cuda.synchronize()
     assert torch.equal(y.view(torch.int32), direct.view(torch.int32))
+
+
+# ---------------------------------------------------------------- prepared physical state
+
+def _time_ms(fn, reps: int) -> float:
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / reps
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantized_csr_prepared_state_runs_the_fast_form(oracle, bits):
+    """prepare_quantized_csr_state: the column-order check and interleaved pairs make the
+    core's launch run the sorted + pairs kernel, bitwise equal to the direct C-ABI call on the
+    same prepared matrix; a new value generation falls back to the plane's own arrays."""
+    import torch
+
+    from cellerator_amd import qcsr_check_columns, qcsr_pack_gene_affine, qcsr_spmm
+    rng = np.random.default_rng(90 + bits)
+    fx = quantized_fixture(oracle, rng, 3000, 2500, 80.0, bits, oracle.PER_GENE_AFFINE, empty_every=11)
+    m = to_device_qcsr(fx)
+    w = torch.from_numpy((rng.standard_normal((fx["cols"], 64)) * 0.02).astype(np.float16)).cuda()
+    y = torch.full((fx["rows"], 64), float("nan"), device="cuda")
+    pairs = torch.empty(2 * fx["cols"], dtype=torch.float32, device="cuda")
+    c = qcsr_case(m, w, y)
+    c.pairs, c.check_columns = pairs.data_ptr(), 1
+    r = H.run(c)
+    assert (r.prepare_status, r.state_status, r.status) == (H.OK, H.OK, H.OK), (r.message, r.engine)
+    assert r.dispatch == b"qcsr:pairs+sorted"
+    torch.cuda.synchronize()
+    fast = qcsr_check_columns(qcsr_pack_gene_affine(m))
+    assert fast.flags == 1
+    direct = qcsr_spmm(fast, w)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), direct.view(torch.int32))
+    ref, mag = oracle.qcsr_spmm_referee(bits, 1, fx["rows"], fx["cols"], fx["row_ptr"],
+                                        fx["packed_row_ptr"], fx["col_idx"], fx["packed"],
+                                        fx["scales"], fx["offsets"], None, w.cpu().numpy())
+    check_against_referee(oracle, ref, mag, y.cpu().numpy())
+
+
+def test_quantized_csr_view_flags_are_not_the_callers():
+    """A view that arrives with flags set is rejected: only the backend's own check sets
+    CX_QCSR_COLUMNS_SORTED."""
+    import torch
+
+    from cellerator_amd import QcsrMatrix
+    row_ptr = torch.tensor([0, 2, 4, 5], dtype=torch.int32).cuda()
+    col_idx = torch.tensor([2, 0, 1, 2, 0], dtype=torch.int32).cuda()  # row 0 out of order
+    vals = torch.tensor([1, 2, 3, 4, 5], dtype=torch.float32).cuda()
+    m = QcsrMatrix(3, 3, 0, row_ptr, col_idx, values=vals, flags=1)
+    w = torch.ones(3, 64, dtype=torch.float32, device="cuda")
+    y = torch.zeros(3, 64, device="cuda")
+    r = H.run(qcsr_case(m, w, y))
+    assert r.status == H.INVALID_LAUNCH and b"flags" in r.message
+    # the backend's own check finds the disorder and keeps the checked path
+    m.flags = 0
+    c = qcsr_case(m, w, y)
+    c.check_columns = 1
+    r = H.run(c)
+    assert (r.state_status, r.status) == (H.OK, H.OK), r.message
+    assert r.dispatch == b"qcsr:plain"
+    torch.cuda.synchronize()
+    assert y[:, 0].cpu().tolist() == [3.0, 7.0, 5.0]
+
+
+def test_prepared_quantized_csr_launch_costs_no_more_than_direct(oracle):
+    """The core's prepared launch runs the same kernel as the direct call: over 20 launches
+    of a C2-sized slice the time per launch stays within 5% (plus 20 us of host dispatch)."""
+    import torch
+
+    from cellerator_amd import qcsr_check_columns, qcsr_pack_gene_affine, qcsr_spmm
+    from cellerator_amd.synth import C3, dense_normal, generate_qcsr
+    m = generate_qcsr(C3.scaled(30000))
+    w = dense_normal((m.cols, 64), 0.02, torch.float16, seed=5)
+    y = torch.empty((m.rows, 64), device="cuda")
+    pairs = torch.empty(2 * m.cols, dtype=torch.float32, device="cuda")
+    c = qcsr_case(m, w, y)
+    c.pairs, c.check_columns, c.repeats = pairs.data_ptr(), 1, 20
+    r = H.run(c)  # prepares the state once; also the warm-up
+    assert r.status == H.OK and r.dispatch == b"qcsr:pairs+sorted", (r.message, r.engine)
+    fast = qcsr_check_columns(qcsr_pack_gene_affine(m))
+    out = torch.empty_like(y)
+    direct_ms = _time_ms(lambda: qcsr_spmm(fast, w, out=out), 20)
+    core_ms = _time_ms(lambda: H.run(c), 1) / 20.0
+    print(f"direct {direct_ms:.4f} ms, through the core {core_ms:.4f} ms per launch")
+    assert core_ms <= direct_ms * 1.05 + 0.02
+
+
+def test_blocked_ell_prepared_panel_and_groups(monkeypatch):
+    """prepare_blocked_ell_state: a prepacked panel and the grouping plan make the core's
+    launch run the grouped kernel without repacking, bitwise equal to the direct grouped call;
+    a launch with another W pointer repacks into the workspace."""
+    import torch
+
+    from cellerator_amd import bell_pack_rhs, bell_plan_groups, bell_spmm_grouped
+    from cellerator_amd import _native as N
+    m, rng = _bell(n_rows_blocks=64, seed=13)
+    n = 128
+    w = (torch.randn(m.cols, n, device="cuda") * 0.02).bfloat16()
+    y = torch.empty(m.rows, n, device="cuda")
+    ws = torch.empty(((m.cols + 31) // 32) * 32 * n * 2, dtype=torch.uint8, device="cuda")
+    panel = torch.empty(((m.cols + 31) // 32) * 32 * n, dtype=torch.bfloat16, device="cuda")
+    groups = bell_plan_groups(m)
+    gd = groups.descriptor()
+    c = bell_case(m, w, y, ws)
+    c.panel, c.groups = panel.data_ptr(), C.addressof(gd)
+    c._keep2 = (panel, groups, gd)
+    r = H.run(c)
+    assert (r.state_status, r.status) == (H.OK, H.OK), (r.message, r.engine)
+    assert r.dispatch == b"bell:grouped+panel"
+    torch.cuda.synchronize()
+    direct = bell_spmm_grouped(m, bell_pack_rhs(w), groups, n)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), direct.view(torch.int32))
+    assert torch.equal(panel, bell_pack_rhs(w))
+    # second launch with a different W (not the packed one): repacked into the workspace
+    w2 = (torch.randn(m.cols, n, device="cuda") * 0.02).bfloat16()
+    y2 = torch.empty_like(y)
+    c.w2, c.y2 = w2.data_ptr(), y2.data_ptr()
+    r = H.run(c)
+    assert (r.status, r.second_status) == (H.OK, H.OK), r.message
+    assert r.dispatch == b"bell:grouped+repack"
+    torch.cuda.synchronize()
+    assert torch.equal(y2.view(torch.int32), bell_spmm_grouped(m, bell_pack_rhs(w2), groups, n).view(torch.int32))
+    del N

@@ -330,3 +330,77 @@ def test_check_columns_and_sorted_flag(oracle):
         col_idx = fx["col_idx"].copy()
         change(col_idx)
         assert qcsr_check_columns(to_device_qcsr(dict(fx, col_idx=col_idx))).flags == expect
+
+
+@pytest.mark.parametrize("n", [64, 128])
+@pytest.mark.parametrize("policy", [1, 2, 3])
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+def test_sorted_flag_forms_bitwise_and_referee(oracle, bits, policy, n):
+    """Every instantiation the column-order flag selects (bits x metadata policy, where 3 is
+    the interleaved pairs, N = 64 and two 64-column blocks at N = 128) gives bitwise the
+    same output as the checked kernel, and is within tolerance of the referee, over three
+    workgroups of rows with a ragged last one."""
+    import torch
+
+    from cellerator_amd import qcsr_check_columns, qcsr_pack_gene_affine, qcsr_spmm
+    rng = np.random.default_rng(1200 + 10 * bits + policy + n)
+    fx = _long_tail_fixture(oracle, rng, bits, rows=1300, cols=2300)
+    if policy == 2:
+        fx = _rebuild(oracle, rng, dict(fx, policy=2, offsets=None,
+                                        row_offsets=rng.uniform(-1, 1, fx["rows"]).astype(np.float32)),
+                      fx["row_ptr"], fx["col_idx"])
+    m = to_device_qcsr(fx)
+    if policy == 3:
+        m = qcsr_pack_gene_affine(m)
+    ms = qcsr_check_columns(m)
+    assert ms.flags == 1
+    rhs = torch.from_numpy((rng.standard_normal((fx["cols"], n)) * 0.02).astype(np.float16)).cuda()
+    a, b = qcsr_spmm(m, rhs), qcsr_spmm(ms, rhs)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    ref, mag = _referee(oracle, fx, rhs.cpu().numpy())
+    check_against_referee(oracle, ref, mag, b.cpu().numpy())
+
+
+def test_sorted_flag_with_epilogue(oracle):
+    """Sorted + pairs with a fused bias-GELU epilogue and beta * C: bitwise the checked
+    kernel's output."""
+    import torch
+
+    from cellerator_amd import Epilogue, qcsr_check_columns, qcsr_pack_gene_affine, qcsr_spmm
+    rng = np.random.default_rng(1333)
+    fx = _long_tail_fixture(oracle, rng, 4, rows=1100, cols=2100)
+    m = qcsr_pack_gene_affine(to_device_qcsr(fx))
+    ms = qcsr_check_columns(m)
+    rhs = torch.from_numpy((rng.standard_normal((fx["cols"], 64)) * 0.02).astype(np.float16)).cuda()
+    bias = torch.randn(64, device="cuda")
+    c0 = torch.randn(fx["rows"], 64, device="cuda")
+    a = c0.clone()
+    b = c0.clone()
+    qcsr_spmm(m, rhs, out=a, epilogue=Epilogue(6, 0.75, -0.5, bias, a))
+    qcsr_spmm(ms, rhs, out=b, epilogue=Epilogue(6, 0.75, -0.5, bias, b))
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+
+
+def test_benched_instantiation_on_c3_rows(oracle):
+    """The exact form bench.py times at C3 -- 4-bit codes, interleaved pairs, the checked
+    column-order flag, N = 64 -- on C3-generated rows spanning three full workgroups of 512
+    rows and a ragged fourth (the tail block whose windows reach the array ends), against the
+    float64 referee on every row."""
+    import torch
+
+    from cellerator_amd import qcsr_check_columns, qcsr_pack_gene_affine, qcsr_spmm
+    from cellerator_amd.synth import C3, dense_normal, generate_qcsr
+    from tests.helpers import qcsr_to_host
+    m = generate_qcsr(C3.scaled(3 * 512 + 77))
+    fast = qcsr_check_columns(qcsr_pack_gene_affine(m))
+    assert fast.flags == 1 and fast.decode_policy == 3
+    w = dense_normal((m.cols, 64), 0.02, torch.float16, seed=77)
+    y = qcsr_spmm(fast, w)
+    torch.cuda.synchronize()
+    h = qcsr_to_host(m)
+    ref, mag = oracle.qcsr_spmm_referee(4, 1, m.rows, m.cols, h["row_ptr"], h["packed_row_ptr"],
+                                        h["col_idx"], h["packed"], h["scales"], h["offsets"], None,
+                                        w.cpu().numpy())
+    check_against_referee(oracle, ref, mag, y.cpu().numpy())
