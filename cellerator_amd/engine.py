@@ -169,7 +169,8 @@ def qcsr_check_columns(m: QcsrMatrix, stream=None) -> QcsrMatrix:
     dev = m.row_ptr.device
     # Allocation, launch and read all run on the check's stream: the flag's read-back then
     # waits for the check, and the buffer is released on the stream that wrote it.
-    with torch.cuda.stream(_torch_stream(stream, dev)) as s:
+    s = _torch_stream(stream, dev)
+    with torch.cuda.stream(s):
         flag = torch.zeros(1, dtype=torch.int32, device=dev)
         d = m.descriptor()
         N.check("cx_qcsr_check_columns", N.engine().cx_qcsr_check_columns(
