@@ -194,6 +194,8 @@ ENGINE_SIGNATURES = {
     "cx_qcsr_spmm_balanced_workspace": (C.c_int, [C.POINTER(CxQcsrMatrix), i64, C.POINTER(u64)]),
     "cx_qcsr_spmm_fwd_balanced": (C.c_int, [C.POINTER(CxQcsrMatrix), p_void, u32, i64, i64, p_void,
                                             i64, C.POINTER(CxSpmmEpilogue), p_void, u64, p_void]),
+    "cx_qcsr_spmm_fwd_balanced_noalloc": (C.c_int, [C.POINTER(CxQcsrMatrix), p_void, u32, i64, i64,
+                                                    p_void, i64, C.POINTER(CxSpmmEpilogue), p_void]),
     "cx_sort_pairs_workspace": (C.c_int, [u64, u32, C.POINTER(u64)]),
     "cx_sort_pairs": (C.c_int, [p_void, p_void, p_void, p_void, u64, u32, p_void, u64, p_void]),
     "cx_exclusive_scan_u32_workspace": (C.c_int, [u64, C.POINTER(u64)]),

@@ -22,6 +22,8 @@
 // wave per row, lanes over output columns, entries in nnz order.
 #include "qcsr_common.hpp"
 
+#include <mutex>
+
 namespace cx {
 namespace {
 
@@ -571,4 +573,75 @@ extern "C" int cx_qcsr_pack_gene_affine(const float *scales, const float *offset
                        static_cast<hipStream_t>(stream), scales, offsets, cols,
                        reinterpret_cast<float2 *>(pairs));
     return check_launch("cx_qcsr_pack_gene_affine");
+}
+
+// ---- allocation-free balanced forward -------------------------------------------------------
+//
+// The balanced form's only scratch is the partial rows of the rows that cross a chunk edge:
+// at most 65,536 chunks x 2 slots x N fp32. This entry keeps them in a device array of this
+// library (one per GPU, held until the process ends) instead of a caller workspace, so
+// callers that cannot allocate (graph capture, tight serving loops) can still run it. Every
+// slot the fixup reads is written by the same launch first, so the array is never cleared.
+// Calls that overlap on one GPU share the array and race.
+
+namespace {
+constexpr std::uint64_t kNoAllocScratchBytes = 32ull << 20;  // 65,536 chunks x 2 x 64 fp32
+constexpr int kNoAllocMaxDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+std::mutex g_noalloc_lock;
+void *g_noalloc_ptr[kNoAllocMaxDevices] = {};
+
+// Device address of `scratch` on the stream's device, resolved once per device with that
+// device current (the host-side name is only a stand-in for the symbol).
+int noalloc_scratch(hipStream_t stream, void **out) {
+    int current = 0;
+    hipError_t e = hipGetDevice(&current);
+    if (e != hipSuccess) return cx::hip_fail(e, "cx_qcsr_spmm_fwd_balanced_noalloc: hipGetDevice");
+    int device = current;
+    if (stream != nullptr) {
+        e = hipStreamGetDevice(stream, &device);
+        if (e != hipSuccess) return cx::hip_fail(e, "cx_qcsr_spmm_fwd_balanced_noalloc: hipStreamGetDevice");
+    }
+    if (device != current)
+        return cx::fail(CX_STATUS_INVALID_ARGUMENT,
+                        "cx_qcsr_spmm_fwd_balanced_noalloc: the stream's device must be the current device");
+    if (device < 0 || device >= kNoAllocMaxDevices)
+        return cx::fail(CX_STATUS_UNSUPPORTED, "cx_qcsr_spmm_fwd_balanced_noalloc: device ordinal above 63");
+    std::lock_guard<std::mutex> lock(g_noalloc_lock);
+    if (g_noalloc_ptr[device] == nullptr) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return cx::hip_fail(e, "cx_qcsr_spmm_fwd_balanced_noalloc: hipGetSymbolAddress");
+        g_noalloc_ptr[device] = p;
+    }
+    *out = g_noalloc_ptr[device];
+    return CX_STATUS_SUCCESS;
+}
+}  // namespace
+
+extern "C" int cx_qcsr_spmm_fwd_balanced_noalloc(const cx_qcsr_matrix *m, const void *rhs,
+                                                 uint32_t rhs_dtype, int64_t rhs_ld, int64_t out_cols,
+                                                 float *out, int64_t out_ld,
+                                                 const cx_spmm_epilogue *epilogue, void *stream) {
+    cx::clear_error();
+    if (m == nullptr)
+        return cx::fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd_balanced_noalloc: null matrix");
+    // only the 64- and 128-column balanced kernels use partial rows
+    const std::uint64_t need = out_cols == 64 || out_cols == 128 ? cx::balance_bytes(m->nnz, out_cols) : 0u;
+    if (need > kNoAllocScratchBytes) {
+        cx::set_error("cx_qcsr_spmm_fwd_balanced_noalloc: %llu bytes of partial rows exceed the %llu-byte "
+                      "scratch (use cx_qcsr_spmm_fwd_balanced with a workspace)",
+                      static_cast<unsigned long long>(need),
+                      static_cast<unsigned long long>(kNoAllocScratchBytes));
+        return CX_STATUS_INVALID_SHAPE;
+    }
+    void *ws = nullptr;
+    const int rc = noalloc_scratch(static_cast<hipStream_t>(stream), &ws);
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    return cx::qcsr_forward(m, rhs, rhs_dtype, rhs_ld, out_cols, out, out_ld, epilogue, ws,
+                            kNoAllocScratchBytes, stream);
 }

@@ -184,6 +184,19 @@ int cx_qcsr_spmm_fwd_balanced(const cx_qcsr_matrix *a, const void *rhs, uint32_t
                               const cx_spmm_epilogue *epilogue, void *workspace,
                               uint64_t workspace_bytes, void *stream);
 
+/* cx_qcsr_spmm_fwd_balanced without a workspace argument: the partial rows of rows that
+ * cross a chunk edge live in a 32 MiB device array of the library (one per GPU, held until
+ * the process ends; resolved on the first call on a device), so the call allocates nothing.
+ * Same kernels, chunking and results (bitwise) as cx_qcsr_spmm_fwd_balanced. Returns
+ * INVALID_SHAPE when the partial rows need more than 32 MiB (N = 128 with more than 32,768
+ * chunks, i.e. above about 33.5M entries). The array keeps the last call's contents and is
+ * shared by every call on its GPU: calls that overlap on one GPU race. The stream's device
+ * must be the current device. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (HIP graph capture, tight serving loops, allocation-free harnesses). */
+int cx_qcsr_spmm_fwd_balanced_noalloc(const cx_qcsr_matrix *a, const void *rhs, uint32_t rhs_dtype,
+                                      int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
+                                      const cx_spmm_epilogue *epilogue, void *stream);
+
 /* Interleaves per-gene metadata for CX_DECODE_PER_GENE_AFFINE_PAIRS:
  * pairs[2c] = scales[c] (1 if scales is NULL), pairs[2c+1] = offsets[c] (0 if NULL),
  * for c < cols; pairs (device, 8-byte aligned) holds 2 * cols floats. No counterpart in
