@@ -146,6 +146,48 @@ class CxsCpbpParams(C.Structure):
     ]
 
 
+class CxFeatureOrder(C.Structure):
+    _fields_ = [("schema_version", u32), ("kind", u32), ("feature_count", u32),
+                ("feature_axis_identity_version", u32), ("feature_axis_identity", u64),
+                ("packing_geometry_identity", u64)]
+
+
+class CxDenseOperand(C.Structure):
+    _fields_ = [("values", p_void), ("feature_count", u32), ("value_size_bytes", u32),
+                ("column_count", u64), ("leading_dimension", u64), ("column_major", u32),
+                ("reserved", u32), ("feature_order", CxFeatureOrder), ("operand_identity", u64)]
+
+
+class CxOrderedPartition(C.Structure):
+    _fields_ = [("global_row_begin", u64), ("full_row_count", u32), ("row_count", u32),
+                ("feature_count", u32), ("nnz_count", u32), ("value_size_bytes", u32),
+                ("feature_axis_fingerprint_version", u32), ("feature_axis_fingerprint", u64),
+                ("row_domain_identity", u64), ("row_offsets", p_void), ("block_ids", p_void),
+                ("local_feature_ids", p_void), ("canonical_feature_ids", p_void), ("values", p_void)]
+
+
+class CxExecutionCsr(C.Structure):
+    _fields_ = [("global_row_begin", u64), ("full_row_count", u32), ("row_count", u32),
+                ("feature_count", u32), ("nnz_count", u32), ("value_size_bytes", u32),
+                ("reserved", u32), ("row_domain_identity", u64), ("structure_identity", u64),
+                ("feature_order", CxFeatureOrder), ("row_offsets", p_void),
+                ("execution_feature_ids", p_void), ("values", p_void)]
+
+
+class CxLazyCsrRequirements(C.Structure):
+    _fields_ = [("row_offset_count", u64), ("execution_feature_count", u64), ("value_bytes", u64),
+                ("row_cursor_count", u64), ("total_bytes", u64)]
+
+
+class CxLazyCsrBuffers(C.Structure):
+    _fields_ = [("row_offset_capacity", u64), ("execution_feature_capacity", u64),
+                ("value_capacity_bytes", u64), ("row_cursor_capacity", u64), ("row_offsets", p_void),
+                ("execution_feature_ids", p_void), ("values", p_void), ("row_cursors", p_void)]
+
+
+FEATURE_ORDER_CANONICAL, FEATURE_ORDER_PACKED = 1, 2
+
+
 # ---- public context ABI structs (include/Cellerator/abi.h layout) ----
 class CelleratorExecutionConfig(C.Structure):
     _fields_ = [("version", u32), ("size", C.c_size_t), ("device", i32), ("stream", p_void),
@@ -224,6 +266,24 @@ ENGINE_SIGNATURES = {
     "cx_cpk1_rebind": (C.c_int, [C.POINTER(CxCpk1View), p_void, u64, C.POINTER(CxCpk1View)]),
     "cx_cpk1_last_error": (C.c_char_p, []),
     "cx_csr_spmv_fwd": (C.c_int, [u32, p_void, p_void, p_void, u32, p_void, p_void, p_void]),
+    "cx_packed_dense_operand_describe": (C.c_int, [C.POINTER(CxCpbpPlan), u64, C.POINTER(CxDenseOperand),
+                                                   C.POINTER(CxDenseOperand), C.POINTER(u64)]),
+    "cx_pack_dense_operand_host": (C.c_int, [C.POINTER(CxCpbpPlan), u64, C.POINTER(CxDenseOperand), p_void,
+                                             u64, C.POINTER(CxDenseOperand)]),
+    "cx_pack_dense_operand_device": (C.c_int, [C.POINTER(CxCpbpPlan), u64, C.POINTER(CxDenseOperand),
+                                               p_void, u64, p_void, C.POINTER(CxDenseOperand)]),
+    "cx_pack_dense_operand": (C.c_int, [p_void, u32, p_void, u64, u64, u32, u32, p_void, u64, p_void]),
+    "cx_build_execution_csr_host": (C.c_int, [C.POINTER(CxCpbpPlan), u64, C.POINTER(CxOrderedPartition),
+                                              p_void, u64, C.POINTER(CxExecutionCsr)]),
+    "cx_lazy_execution_csr_requirements": (C.c_int, [C.POINTER(CxCpk1View), C.POINTER(CxLazyCsrRequirements)]),
+    "cx_materialize_execution_csr_from_cpk1_host": (C.c_int, [C.POINTER(CxCpk1View), C.POINTER(CxLazyCsrBuffers),
+                                                              C.POINTER(CxExecutionCsr)]),
+    "cx_qcsr_column_counts": (C.c_int, [C.POINTER(CxQcsrMatrix), p_void, p_void]),
+    "cx_popularity_order": (C.c_int, [p_void, u32, p_void, p_void]),
+    "cx_qcsr_to_execution_order": (C.c_int, [C.POINTER(CxQcsrMatrix), p_void, p_void, p_void, p_void, p_void,
+                                             p_void]),
+    "cx_qcsr_execution_order_lds_bytes": (C.c_int, [C.POINTER(CxQcsrMatrix), C.POINTER(u64)]),
+    "cx_exec_last_error": (C.c_char_p, []),
     "cx_cpbp_builder_create": (C.c_int, [C.POINTER(CxCpbpPlan), C.POINTER(CxCpbpCsr),
                                          C.POINTER(CxCpbpOrderConfig), u32, C.POINTER(p_void)]),
     "cx_cpbp_builder_requirements": (C.c_int, [p_void, C.POINTER(CxCpbpTileRequirements)]),

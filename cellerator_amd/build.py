@@ -43,6 +43,8 @@ ENGINE_SOURCES = [
     "cpbp_build_device.hip",
     "cpk1.cpp",
     "bell_plan.cpp",
+    "exec_order.hip",
+    "exec_csr.cpp",
 ]
 SYNTH_SOURCES = ["synth.hip"]
 

@@ -1,0 +1,113 @@
+"""Execution feature order on the host side of the engine: the popularity order of a
+quantized CSR's genes, the packed dense operand (W rows in execution order), and the
+quantized CSR relabelled into execution order -- thin ctypes mirrors of the C-ABI entries
+(include/cellerator_amd.h, exec_order.hip / exec_csr.cpp). The reference's counterparts are
+pack_dense_operand_{host,cuda} (include/Cellerator/compute/math/packed_dense_operand.hh:16-70)
+and execution_csr_view (include/Cellerator/compute/math/physical_csr.hh:40-215).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import dataclasses
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import _native as N
+from .engine import QcsrMatrix, _require_cuda, _stream
+
+
+@dataclasses.dataclass
+class ExecutionOrder:
+    """feature_permutation[e] = canonical gene at execution position e; inverse the other
+    way round. Both int32-stored u32 device tensors of length genes."""
+    feature_permutation: torch.Tensor
+    inverse_permutation: torch.Tensor
+
+    @property
+    def genes(self) -> int:
+        return int(self.feature_permutation.numel())
+
+
+def column_counts(m: QcsrMatrix, stream=None) -> torch.Tensor:
+    """Stored entries per gene (device u32 as int32)."""
+    _require_cuda(m.col_idx)
+    counts = torch.empty(max(m.cols, 1), dtype=torch.int32, device=m.col_idx.device)
+    d = m.descriptor()
+    N.check("cx_qcsr_column_counts", N.engine().cx_qcsr_column_counts(C.byref(d), counts.data_ptr(),
+                                                                      _stream(stream)))
+    return counts[: m.cols]
+
+
+def popularity_order(m: QcsrMatrix, stream=None) -> ExecutionOrder:
+    """Genes by descending stored-entry count (ties by gene index): the order whose leading
+    genes are dense enough for matrix-core tiles."""
+    counts = column_counts(m, stream).cpu().numpy().view(np.uint32)
+    perm = np.empty(m.cols, np.uint32)
+    inv = np.empty(m.cols, np.uint32)
+    lib = N.engine()
+    st = lib.cx_popularity_order(counts.ctypes.data, m.cols, perm.ctypes.data, inv.ctypes.data)
+    if st != 0:
+        raise N.EngineError("cx_popularity_order", st, lib.cx_exec_last_error().decode())
+    dev = m.col_idx.device
+    return ExecutionOrder(torch.from_numpy(perm.view(np.int32)).to(dev),
+                          torch.from_numpy(inv.view(np.int32)).to(dev))
+
+
+def pack_rows(order: ExecutionOrder, canonical: torch.Tensor, stream=None) -> torch.Tensor:
+    """Rows of a feature-major device tensor [genes, ...] gathered into execution order
+    (cx_pack_dense_operand): the packed dense operand for a row-major W, or the per-gene
+    metadata for a 1-D tensor (8-byte rows for interleaved pairs given as [genes, 2])."""
+    _require_cuda(canonical)
+    if canonical.shape[0] != order.genes or not canonical.is_contiguous():
+        raise ValueError("canonical must be a contiguous [genes, ...] tensor")
+    flat = canonical.reshape(order.genes, -1)
+    row_bytes = flat.shape[1] * flat.element_size()
+    if row_bytes in (1, 2, 4, 8):
+        cols, ld, vsize = 1, 1, row_bytes
+    else:
+        cols, ld, vsize = flat.shape[1], flat.shape[1], flat.element_size()
+    out = torch.empty_like(canonical)
+    N.check("cx_pack_dense_operand", N.engine().cx_pack_dense_operand(
+        order.feature_permutation.data_ptr(), order.genes, canonical.data_ptr(), cols, ld, 0, vsize,
+        out.data_ptr(), out.numel() * out.element_size(), _stream(stream)))
+    return out
+
+
+def to_execution_order(m: QcsrMatrix, order: ExecutionOrder, stream=None) -> QcsrMatrix:
+    """The matrix with genes relabelled by `order` and every row re-sorted (codes carried),
+    per-gene metadata permuted alongside; row offsets are shared with `m`. Raises if a row
+    repeats a gene or holds a column outside [0, cols)."""
+    _require_cuda(m.row_ptr, m.col_idx)
+    if order.genes != m.cols:
+        raise ValueError("order must cover every gene of the matrix")
+    dev = m.col_idx.device
+    col_out = torch.empty_like(m.col_idx)
+    packed_out = torch.zeros_like(m.packed_values) if m.packed_values is not None else None
+    values_out = torch.empty_like(m.values) if m.values is not None else None
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    d = m.descriptor()
+    s = _stream(stream)
+    N.check("cx_qcsr_to_execution_order", N.engine().cx_qcsr_to_execution_order(
+        C.byref(d), order.inverse_permutation.data_ptr(), col_out.data_ptr(),
+        packed_out.data_ptr() if packed_out is not None else None,
+        values_out.data_ptr() if values_out is not None else None, err.data_ptr(), s))
+    ts = torch.cuda.ExternalStream(s, device=dev) if stream is not None else torch.cuda.current_stream(dev)
+    with torch.cuda.stream(ts):
+        bad = int(err.item())
+    if bad:
+        raise ValueError("to_execution_order: a row repeats a gene or holds a column outside [0, cols)")
+
+    def meta(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+        if t is None:
+            return None
+        if m.decode_policy == N.DECODE_PER_GENE_AFFINE_PAIRS and t is m.column_scales:
+            return pack_rows(order, t.view(m.cols, 2), stream).view(-1)
+        return pack_rows(order, t, stream)
+
+    return QcsrMatrix(m.rows, m.cols, m.bits, m.row_ptr, col_out, packed_row_ptr=m.packed_row_ptr,
+                      packed_values=packed_out, column_scales=meta(m.column_scales),
+                      column_offsets=meta(m.column_offsets), row_offsets=m.row_offsets,
+                      values=values_out, decode_policy=m.decode_policy,
+                      meta={**m.meta, "execution_order": order}, flags=N.QCSR_COLUMNS_SORTED)

@@ -625,6 +625,160 @@ int cx_cpk1_rebind(const cx_cpk1_view *validated, const void *new_base, uint64_t
                    cx_cpk1_view *out);
 const char *cx_cpk1_last_error(void);
 
+/* ---- execution feature order: packed dense operand and execution-order CSR ---------------
+ * feature_permutation[e] = the canonical gene at execution position e (cx_cpbp_plan's
+ * convention). X . W does not change when the genes of X and the rows of W are relabelled
+ * together, so a projection can run on (X_exec, W_exec). Identities follow the reference's
+ * FNV-1a rules, including its offset basis. */
+
+/* feature_order_identity (include/Cellerator/compute/math/operation.hh:63-96) */
+#define CX_FEATURE_ORDER_CANONICAL 1u
+#define CX_FEATURE_ORDER_PACKED 2u
+typedef struct cx_feature_order {
+    uint32_t schema_version; /* 1 */
+    uint32_t kind;           /* CX_FEATURE_ORDER_* */
+    uint32_t feature_count;
+    uint32_t feature_axis_identity_version;
+    uint64_t feature_axis_identity;
+    uint64_t packing_geometry_identity; /* 0 for the canonical order */
+} cx_feature_order;
+
+/* canonical_dense_operand_view / packed_dense_operand_view
+ * (include/Cellerator/compute/math/packed_dense_operand.hh:16-38): a feature-major dense
+ * operand; column_major 0 = row-major [features x columns] with leading_dimension >= columns,
+ * 1 = column-major with leading_dimension >= features. */
+typedef struct cx_dense_operand {
+    const void *values;
+    uint32_t feature_count;
+    uint32_t value_size_bytes; /* 2, 4 or 8 */
+    uint64_t column_count;
+    uint64_t leading_dimension;
+    uint32_t column_major;
+    uint32_t reserved;
+    cx_feature_order feature_order;
+    uint64_t operand_identity;
+} cx_dense_operand;
+
+/* query_packed_dense_operand_requirements (packed_dense_operand.cu:163-175): validates the
+ * canonical operand against the plan (whose geometry identity is geometry_identity) and
+ * describes the packed result (row-major [features x columns], packed feature order, its
+ * identity) without values; *value_bytes = the packed size. */
+int cx_packed_dense_operand_describe(const cx_cpbp_plan *plan, uint64_t geometry_identity,
+                                     const cx_dense_operand *canonical, cx_dense_operand *packed,
+                                     uint64_t *value_bytes);
+/* pack_dense_operand_host (packed_dense_operand.cu:177-215): packed row e = canonical feature
+ * plan->feature_permutation[e]. Host plan and buffers. */
+int cx_pack_dense_operand_host(const cx_cpbp_plan *plan, uint64_t geometry_identity,
+                               const cx_dense_operand *canonical, void *packed, uint64_t capacity_bytes,
+                               cx_dense_operand *out);
+/* pack_dense_operand_cuda (packed_dense_operand.cu:217-260): the same on the device (device
+ * permutation and values; the block offsets are not read). Enqueues on `stream`, one pass. */
+int cx_pack_dense_operand_device(const cx_cpbp_plan *device_plan, uint64_t geometry_identity,
+                                 const cx_dense_operand *canonical, void *packed, uint64_t capacity_bytes,
+                                 void *stream, cx_dense_operand *out);
+/* The raw device gather behind it: packed[e][c] = canonical[perm[e]][c] (row-major source) or
+ * canonical[c][perm[e]] (column-major), value_size_bytes 1, 2, 4 or 8. Also permutes per-gene
+ * metadata (columns = 1; 8-byte values for interleaved scale/offset pairs). */
+int cx_pack_dense_operand(const uint32_t *feature_permutation, uint32_t feature_count,
+                          const void *canonical, uint64_t column_count, uint64_t leading_dimension,
+                          uint32_t column_major, uint32_t value_size_bytes, void *packed,
+                          uint64_t packed_capacity_bytes, void *stream);
+
+/* ordered_plan_partition_view subset (components/CellPack/include/CellPack/apply_plan.hh):
+ * rows in canonical order, entries per row in execution order as (block, local) plus the
+ * canonical feature id they stand for. */
+typedef struct cx_ordered_partition {
+    uint64_t global_row_begin;
+    uint32_t full_row_count;
+    uint32_t row_count;
+    uint32_t feature_count;
+    uint32_t nnz_count;
+    uint32_t value_size_bytes;
+    uint32_t feature_axis_fingerprint_version;
+    uint64_t feature_axis_fingerprint;
+    uint64_t row_domain_identity;
+    const uint32_t *row_offsets;        /* row_count + 1 */
+    const uint32_t *block_ids;          /* nnz_count */
+    const uint32_t *local_feature_ids;  /* nnz_count */
+    const uint32_t *canonical_feature_ids; /* nnz_count */
+    const void *values;                 /* nnz_count x value_size_bytes */
+} cx_ordered_partition;
+
+/* execution_csr_view (include/Cellerator/compute/math/physical_csr.hh:40-56): a row-compressed
+ * view in frozen execution-feature order with its FNV structure identity (:92-110). */
+typedef struct cx_execution_csr {
+    uint64_t global_row_begin;
+    uint32_t full_row_count;
+    uint32_t row_count;
+    uint32_t feature_count;
+    uint32_t nnz_count;
+    uint32_t value_size_bytes;
+    uint32_t reserved;
+    uint64_t row_domain_identity;
+    uint64_t structure_identity; /* sparse_structure_identity.value, identity version 1 */
+    cx_feature_order feature_order;
+    const uint32_t *row_offsets;
+    const uint32_t *execution_feature_ids;
+    const void *values;
+} cx_execution_csr;
+
+/* build_execution_csr_view_host (src/compute/math/physical_csr.cc:16-97): maps every entry to
+ * its execution feature (block offset + local id), checks it stands for the recorded canonical
+ * feature and that each row is strictly increasing in execution order; aliases the partition's
+ * row offsets and values, writes execution_feature_ids (capacity >= nnz). */
+int cx_build_execution_csr_host(const cx_cpbp_plan *plan, uint64_t geometry_identity,
+                                const cx_ordered_partition *ordered, uint32_t *execution_feature_ids,
+                                uint64_t capacity, cx_execution_csr *out);
+
+/* lazy_execution_csr_requirements / _buffers (physical_csr.hh:58-77, :180-207), in elements
+ * and bytes. */
+typedef struct cx_lazy_csr_requirements {
+    uint64_t row_offset_count;
+    uint64_t execution_feature_count;
+    uint64_t value_bytes;
+    uint64_t row_cursor_count;
+    uint64_t total_bytes;
+} cx_lazy_csr_requirements;
+typedef struct cx_lazy_csr_buffers {
+    uint64_t row_offset_capacity;
+    uint64_t execution_feature_capacity;
+    uint64_t value_capacity_bytes;
+    uint64_t row_cursor_capacity;
+    uint32_t *row_offsets;
+    uint32_t *execution_feature_ids;
+    void *values;
+    uint32_t *row_cursors;
+} cx_lazy_csr_buffers;
+int cx_lazy_execution_csr_requirements(const cx_cpk1_view *payload, cx_lazy_csr_requirements *out);
+/* materialize_execution_csr_from_cpk1_host (physical_csr.cc:99-240): rebuilds the CSR of a
+ * validated HOST CPK1 view (tiles of any width up to 64) into caller-owned buffers, rows in
+ * tile order, entries in execution order; the image is not modified. */
+int cx_materialize_execution_csr_from_cpk1_host(const cx_cpk1_view *payload, const cx_lazy_csr_buffers *buffers,
+                                                cx_execution_csr *out);
+
+/* Per-gene stored-entry counts of `a` (device, cols u32; columns outside [0, cols) are not
+ * counted), and the popularity order of such counts (host): genes by descending count, ties by
+ * gene index -- an execution order that puts the most frequently stored genes first. Engine
+ * additions: the reference takes its orders from a frozen packing plan. */
+int cx_qcsr_column_counts(const cx_qcsr_matrix *a, uint32_t *counts, void *stream);
+int cx_popularity_order(const uint32_t *counts, uint32_t genes, uint32_t *feature_permutation,
+                        uint32_t *inverse_permutation);
+
+/* The quantized (or plain) CSR `a` relabelled into execution order on the device: entry
+ * (row, g) becomes (row, inverse_permutation[g]) and every row is re-sorted by the new label
+ * with its code (or value) carried along. row_ptr and packed_row_ptr are unchanged (the
+ * outputs reuse them); col_idx_out [nnz] and packed_out [packed bytes] (or values_out [nnz]
+ * for bits == 0) must not alias the inputs. Rows need not be sorted on input, but a gene may
+ * occur once per row: a repeated gene or a column outside [0, cols) sets *device_error to
+ * nonzero (outputs undefined). Per-gene metadata is permuted with cx_pack_dense_operand.
+ * The execution-order CSR of build_execution_csr_view_host, produced on the device for a
+ * quantized matrix. */
+int cx_qcsr_to_execution_order(const cx_qcsr_matrix *a, const uint32_t *inverse_permutation,
+                               int32_t *col_idx_out, uint8_t *packed_out, void *values_out,
+                               uint32_t *device_error, void *stream);
+int cx_qcsr_execution_order_lds_bytes(const cx_qcsr_matrix *a, uint64_t *bytes);
+const char *cx_exec_last_error(void);
+
 /* N = 1 CSR comparator: csr_spmv_fwd_f16_f32 (src/compute/sparse/ops/ops.hh:83-90);
  * y[r] = sum fp32(values) * x[col]. values F16 or F32. */
 int cx_csr_spmv_fwd(uint32_t rows, const uint32_t *row_ptr, const uint32_t *col_idx,
