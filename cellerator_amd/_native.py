@@ -284,6 +284,10 @@ ENGINE_SIGNATURES = {
                                              p_void]),
     "cx_qcsr_execution_order_lds_bytes": (C.c_int, [C.POINTER(CxQcsrMatrix), C.POINTER(u64)]),
     "cx_exec_last_error": (C.c_char_p, []),
+    "cx_qcsr_hybrid_prepare": (C.c_int, [C.POINTER(CxQcsrMatrix), u32, p_void, i64, u32, p_void, p_void]),
+    "cx_qcsr_hybrid_workspace": (C.c_int, [C.POINTER(CxQcsrMatrix), C.POINTER(u64)]),
+    "cx_qcsr_spmm_fwd_hybrid": (C.c_int, [C.POINTER(CxQcsrMatrix), u32, p_void, p_void, i64, i64, p_void, i64,
+                                          C.POINTER(CxSpmmEpilogue), p_void, u64, p_void]),
     "cx_cpbp_builder_create": (C.c_int, [C.POINTER(CxCpbpPlan), C.POINTER(CxCpbpCsr),
                                          C.POINTER(CxCpbpOrderConfig), u32, C.POINTER(p_void)]),
     "cx_cpbp_builder_requirements": (C.c_int, [p_void, C.POINTER(CxCpbpTileRequirements)]),

@@ -24,7 +24,18 @@ struct QcsrArgs {
     std::uint32_t cols;
     std::uint32_t flags;  // cx_qcsr_matrix.flags (CX_QCSR_COLUMNS_SORTED)
     Epilogue ep;
+    // Tail of the execution-order hybrid (row-group kernel only; NULL / 0 otherwise): each
+    // row starts at entry row_start[row] instead of row_ptr[row], its sums start from
+    // acc_init[row][0..64) (the head's partial), and the gene parts start at first_part.
+    const std::int32_t *row_start;
+    const float *acc_init;
+    std::uint32_t first_part;
 };
+
+// Launchers shared across translation units (qcsr_hybrid.hip, qcsr_parts.hip).
+int launch_qcsr_head(const QcsrArgs &a, std::uint32_t bits, std::uint32_t policy, std::uint32_t head,
+                     const std::uint16_t *panel, std::uint32_t panel_n, float *partial, std::int32_t *head_end,
+                     hipStream_t stream);
 
 constexpr int kWavesPerBlock = 4;
 

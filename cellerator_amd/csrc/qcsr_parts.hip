@@ -104,6 +104,7 @@ __device__ __forceinline__ void fma8(float (&p)[8], float x, uint4 w) {
 
 // Plain per-row path for rows the part walk could not finish: lane c accumulates column
 // c over the row's entries in storage order; columns outside [0, cols) contribute nothing.
+// In the hybrid tail the walk starts at row_start[row] from the head's partial sum.
 template<int kBits, int kPolicy>
 __device__ float row_fallback(const QcsrArgs &a, std::uint32_t row, int lane) {
     const std::int64_t begin = a.row_ptr[row], end = a.row_ptr[row + 1];
@@ -111,8 +112,9 @@ __device__ float row_fallback(const QcsrArgs &a, std::uint32_t row, int lane) {
     const float row_offset = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET && a.row_offsets != nullptr
         ? a.row_offsets[row] : 0.0f;
     const std::uint16_t *rhs = static_cast<const std::uint16_t *>(a.rhs);
-    float acc = 0.0f;
-    for (std::int64_t i = begin; i < end; ++i) {
+    float acc = a.acc_init != nullptr ? a.acc_init[static_cast<std::int64_t>(row) * 64 + lane] : 0.0f;
+    const std::int64_t start = a.row_start != nullptr ? a.row_start[row] : begin;
+    for (std::int64_t i = start; i < end; ++i) {
         const std::uint32_t col = static_cast<std::uint32_t>(a.col_idx[i]);
         if (col >= a.cols) continue;
         int c = 0;
@@ -324,14 +326,22 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
         roff[l] = 0.0f;
         if (row != kNoRow && fits) {
             const int b = a.row_ptr[row];
-            cur[l] = b - wg_begin;
+            // the code of entry e (relative to the block) starts at bit q + e * kBits
+            q = (a.packed_row_ptr[row] - pk_al) * 8 - (b - wg_begin) * kBits;
+            cur[l] = (a.row_start != nullptr ? a.row_start[row] : b) - wg_begin;
             end[l] = a.row_ptr[row + 1] - wg_begin;
-            q = (a.packed_row_ptr[row] - pk_al) * 8 - cur[l] * kBits;
             if constexpr (kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET)
                 roff[l] = a.row_offsets != nullptr ? a.row_offsets[row] : 0.0f;
         }
+        if (a.acc_init != nullptr && row != kNoRow) {
+            const float4 *init = reinterpret_cast<const float4 *>(a.acc_init + static_cast<std::int64_t>(row) * 64 + 8 * j);
+            const float4 i0 = init[0], i1 = init[1];
+            acc[l][0] = i0.x; acc[l][1] = i0.y; acc[l][2] = i0.z; acc[l][3] = i0.w;
+            acc[l][4] = i1.x; acc[l][5] = i1.y; acc[l][6] = i1.z; acc[l][7] = i1.w;
+        } else {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) acc[l][k] = 0.0f;
+            for (int k = 0; k < 8; ++k) acc[l][k] = 0.0f;
+        }
         if (j == 0) sh.qbits[wave][l][grp] = q;
         load_window(l, q);
     }
@@ -342,7 +352,7 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
 
     const int cols = static_cast<int>(a.cols);
     const int parts = (cols + kPartGenes - 1) / kPartGenes;
-    for (int part = 0; part < parts; ++part) {
+    for (int part = static_cast<int>(a.first_part); part < parts; ++part) {
         const int lo = part * kPartGenes;
         const int hi = lo + kPartGenes < cols ? lo + kPartGenes : cols;
         const std::uint32_t span = static_cast<std::uint32_t>(hi - lo);

@@ -111,3 +111,55 @@ def to_execution_order(m: QcsrMatrix, order: ExecutionOrder, stream=None) -> Qcs
                       column_offsets=meta(m.column_offsets), row_offsets=m.row_offsets,
                       values=values_out, decode_policy=m.decode_policy,
                       meta={**m.meta, "execution_order": order}, flags=N.QCSR_COLUMNS_SORTED)
+
+
+@dataclasses.dataclass
+class HybridProjection:
+    """A quantized CSR in execution order prepared for cx_qcsr_spmm_fwd_hybrid: the packed
+    weights of its first head_cols genes (a multiple of 1,024) and the workspace of the head's
+    partial sums. Built once per matrix and weight generation by hybrid_prepare."""
+    matrix: QcsrMatrix
+    head_cols: int
+    panel: Optional[torch.Tensor]
+    workspace: Optional[torch.Tensor]
+    out_cols: int
+
+
+def hybrid_prepare(m: QcsrMatrix, w: torch.Tensor, head_cols: int, stream=None) -> HybridProjection:
+    """m in execution order (sorted rows), w = the execution-order weights (F16 [genes, N],
+    N a multiple of 64). Raises if the head genes decode outside the exact fp16 split."""
+    _require_cuda(m.row_ptr, w)
+    if w.dtype != torch.float16 or w.dim() != 2 or w.stride(1) != 1 or w.shape[0] != m.cols:
+        raise ValueError("w must be a row-major F16 [genes, N] tensor")
+    n = int(w.shape[1])
+    lib = N.engine()
+    d = m.descriptor()
+    panel = None
+    if head_cols:
+        panel = torch.empty((head_cols // 32) * n * 32, dtype=torch.float16, device=w.device)
+        N.check("cx_qcsr_hybrid_prepare", lib.cx_qcsr_hybrid_prepare(
+            C.byref(d), head_cols, w.data_ptr(), w.stride(0), n, panel.data_ptr(), _stream(stream)))
+    nbytes = C.c_uint64()
+    N.check("cx_qcsr_hybrid_workspace", lib.cx_qcsr_hybrid_workspace(C.byref(d), C.byref(nbytes)))
+    ws = torch.empty(max(nbytes.value, 256), dtype=torch.uint8, device=w.device) if head_cols else None
+    return HybridProjection(m, head_cols, panel, ws, n)
+
+
+def hybrid_spmm(p: HybridProjection, w: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None,
+                epilogue=None) -> torch.Tensor:
+    """Y = X . W (+ epilogue) on the prepared execution-order projection; Y rows are the
+    matrix's rows (cells keep their order), columns the weights' columns."""
+    m = p.matrix
+    _require_cuda(w)
+    if w.shape != (m.cols, p.out_cols) or w.dtype != torch.float16 or w.stride(1) != 1:
+        raise ValueError("w must be the F16 [genes, N] weights the projection was prepared with")
+    if out is None:
+        out = torch.empty((m.rows, p.out_cols), dtype=torch.float32, device=w.device)
+    d = m.descriptor()
+    e = epilogue.descriptor(out) if epilogue is not None else None
+    ws = p.workspace
+    N.check("cx_qcsr_spmm_fwd_hybrid", N.engine().cx_qcsr_spmm_fwd_hybrid(
+        C.byref(d), p.head_cols, p.panel.data_ptr() if p.panel is not None else None, w.data_ptr(),
+        w.stride(0), p.out_cols, out.data_ptr(), out.stride(0), C.byref(e) if e is not None else None,
+        ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, _stream(stream)))
+    return out

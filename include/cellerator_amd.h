@@ -779,6 +779,38 @@ int cx_qcsr_to_execution_order(const cx_qcsr_matrix *a, const uint32_t *inverse_
 int cx_qcsr_execution_order_lds_bytes(const cx_qcsr_matrix *a, uint64_t *bytes);
 const char *cx_exec_last_error(void);
 
+/* ---- execution-order quantized CSR SpMM with a dense head on the matrix cores -----------
+ * For a matrix in an execution order whose first head_cols genes are the most frequently
+ * stored ones (cx_popularity_order + cx_qcsr_to_execution_order), the product splits into
+ * Y = X[:, 0:H) . W[0:H, :] + X[:, H:) . W[H:, :]. The head runs on v_mfma_f32_16x16x32_f16
+ * over dense 16-row tiles: every code is decoded exactly as the reference codec does
+ * (fma(code, scale, offset), include/Cellerator/quantized/access.cuh:81-91) and split into
+ * three fp16 parts whose sum is the decoded value (exact for |x| in [2^-2, 2^15); below,
+ * an absolute error under 2^-25 |w|), so each product is exact in fp32 and only the fp32
+ * summation order differs from the plain kernel. The tail runs on the row-group VALU kernel
+ * from each row's first entry >= H, adds the head's partial sums and applies the epilogue.
+ * W is F16 (the execution-order packed dense operand). Engine addition; the reference's
+ * projection has no matrix-core path for CSR. */
+
+/* Checks that every code of the first head_cols genes decodes to |x| < 2^15 (UNSUPPORTED
+ * otherwise) and packs those genes' weights (F16 [cols x out_cols], row stride rhs_ld) into
+ * head_panel ([head_cols/32][out_cols][32] F16). head_cols a multiple of 1,024 (0: nothing to
+ * do). Once per weight generation; allocates one 8-byte word and synchronizes `stream`. */
+int cx_qcsr_hybrid_prepare(const cx_qcsr_matrix *a, uint32_t head_cols, const uint16_t *rhs_f16,
+                           int64_t rhs_ld, uint32_t out_cols, uint16_t *head_panel, void *stream);
+/* Workspace bytes of cx_qcsr_spmm_fwd_hybrid: the head's partial sums (rows x 64 fp32, 256-byte
+ * aligned) and each row's first tail entry (rows int32). */
+int cx_qcsr_hybrid_workspace(const cx_qcsr_matrix *a, uint64_t *bytes);
+/* Y = act(alpha * (A . W) + beta * C + bias) for A in execution order with a.flags including
+ * CX_QCSR_COLUMNS_SORTED, codes of 1/2/4/8 bits (any decode policy), F16 W, out_cols 64..256
+ * in steps of 64 (one head and one tail launch per 64 columns), 16-byte aligned operands.
+ * head_cols == 0 runs the plain row-group kernel. workspace: 256-byte aligned,
+ * cx_qcsr_hybrid_workspace bytes. Deterministic. */
+int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *a, uint32_t head_cols, const uint16_t *head_panel,
+                            const void *rhs, int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
+                            const cx_spmm_epilogue *epilogue, void *workspace, uint64_t workspace_bytes,
+                            void *stream);
+
 /* N = 1 CSR comparator: csr_spmv_fwd_f16_f32 (src/compute/sparse/ops/ops.hh:83-90);
  * y[r] = sum fp32(values) * x[col]. values F16 or F32. */
 int cx_csr_spmv_fwd(uint32_t rows, const uint32_t *row_ptr, const uint32_t *col_idx,
