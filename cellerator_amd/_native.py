@@ -188,6 +188,12 @@ class CxLazyCsrBuffers(C.Structure):
 FEATURE_ORDER_CANONICAL, FEATURE_ORDER_PACKED = 1, 2
 
 
+class CxQcsrHybridLayout(C.Structure):
+    _fields_ = [("head_cols", u32), ("rows", u32), ("rows_ld", u32), ("bits", u32), ("decode_policy", u32),
+                ("scale_exp", i32), ("nnz", u64), ("codes", p_void), ("masks", p_void), ("head_end", p_void),
+                ("meta", p_void), ("row_offsets", p_void)]
+
+
 # ---- public context ABI structs (include/Cellerator/abi.h layout) ----
 class CelleratorExecutionConfig(C.Structure):
     _fields_ = [("version", u32), ("size", C.c_size_t), ("device", i32), ("stream", p_void),
@@ -284,10 +290,12 @@ ENGINE_SIGNATURES = {
                                              p_void]),
     "cx_qcsr_execution_order_lds_bytes": (C.c_int, [C.POINTER(CxQcsrMatrix), C.POINTER(u64)]),
     "cx_exec_last_error": (C.c_char_p, []),
-    "cx_qcsr_hybrid_prepare": (C.c_int, [C.POINTER(CxQcsrMatrix), u32, p_void, i64, u32, p_void, p_void]),
-    "cx_qcsr_hybrid_workspace": (C.c_int, [C.POINTER(CxQcsrMatrix), C.POINTER(u64)]),
-    "cx_qcsr_spmm_fwd_hybrid": (C.c_int, [C.POINTER(CxQcsrMatrix), u32, p_void, p_void, i64, i64, p_void, i64,
-                                          C.POINTER(CxSpmmEpilogue), p_void, u64, p_void]),
+    "cx_qcsr_hybrid_layout_bytes": (C.c_int, [C.POINTER(CxQcsrMatrix), u32, C.POINTER(u64)]),
+    "cx_qcsr_hybrid_prepare": (C.c_int, [C.POINTER(CxQcsrMatrix), u32, p_void, u64,
+                                         C.POINTER(CxQcsrHybridLayout), p_void]),
+    "cx_qcsr_hybrid_workspace": (C.c_int, [C.POINTER(CxQcsrMatrix), u32, i64, C.POINTER(u64)]),
+    "cx_qcsr_spmm_fwd_hybrid": (C.c_int, [C.POINTER(CxQcsrMatrix), C.POINTER(CxQcsrHybridLayout), p_void, i64,
+                                          i64, p_void, i64, C.POINTER(CxSpmmEpilogue), p_void, u64, p_void]),
     "cx_cpbp_builder_create": (C.c_int, [C.POINTER(CxCpbpPlan), C.POINTER(CxCpbpCsr),
                                          C.POINTER(CxCpbpOrderConfig), u32, C.POINTER(p_void)]),
     "cx_cpbp_builder_requirements": (C.c_int, [p_void, C.POINTER(CxCpbpTileRequirements)]),

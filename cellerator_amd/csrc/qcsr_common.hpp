@@ -32,11 +32,6 @@ struct QcsrArgs {
     std::uint32_t first_part;
 };
 
-// Launchers shared across translation units (qcsr_hybrid.hip, qcsr_parts.hip).
-int launch_qcsr_head(const QcsrArgs &a, std::uint32_t bits, std::uint32_t policy, std::uint32_t head,
-                     const std::uint16_t *panel, std::uint32_t panel_n, float *partial, std::int32_t *head_end,
-                     hipStream_t stream);
-
 constexpr int kWavesPerBlock = 4;
 
 // Decoded value of entry `i` (global nnz index) of row `row` whose packed codes start

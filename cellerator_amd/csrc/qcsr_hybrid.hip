@@ -4,316 +4,315 @@
 // In an execution order that puts the most frequently stored genes first (the popularity
 // order of exec_order.hip, or any frozen plan order), the first H genes of a single-cell
 // matrix are stored in a large share of the cells: at C3, the first 4,096 of 33,538 genes
-// hold 2/3 of the nonzeros at 24% mean density (93% for the first 256). Those columns are
-// dense enough for the matrix cores. The head kernel here computes Y_head = X[:, 0:H) .
-// W[0:H, :] with v_mfma_f32_16x16x32_f16; the tail X[:, H:) . W[H:, :] runs on the row-group
-// VALU kernel of qcsr_parts.hip, which starts every row at its first entry >= H (recorded
-// here) and adds Y_head before its epilogue.
+// hold 2/3 of the nonzeros at 24% mean density (59% for the first 1,024). Those columns are
+// dense enough for the matrix cores. Y = X[:, 0:H) . W[0:H, :] + X[:, H:) . W[H:, :]: the
+// head runs here on v_mfma_f32_16x16x32_f16 over a dense copy of X[:, 0:H); the tail runs on
+// the row-group VALU kernel of qcsr_parts.hip, which starts every row at its first entry
+// >= H and adds the head's sums before its epilogue.
 //
-// Exactness. Each stored code is decoded exactly as the reference codec does,
-// x = fma(float(code), scale, offset) in fp32 (include/Cellerator/quantized/access.cuh:81-91),
-// and then split into three fp16 parts x = hi + mid + lo (each the round-to-nearest fp16 of
-// the remaining residual; the residuals are exact in fp32). For |x| in [2^-2, 2^15) the
-// three parts hold all 24 bits of x, so hi + mid + lo == x exactly; below 2^-2 the lowest
-// part may lose bits under 2^-24 (an absolute error below 2^-25 |w|). Each part times an
-// fp16 weight (11 x 11 bits) is exact in fp32, and the matrix cores accumulate in fp32: the
-// result differs from an fp32 FMA chain only in summation order. The host rejects head
-// genes whose decoded values can reach 2^15.
+// Head layout (built once per matrix by cx_qcsr_hybrid_prepare; the CSR itself is unchanged
+// and still serves the tail). Word-major, row-minor arrays of rows_ld rows (rows rounded up
+// to a workgroup; padding rows are zero), so the 16 rows of a matrix tile read 64
+// consecutive bytes of a word:
+//   codes [H * bits / 32][rows_ld] u32: word w of a row holds the codes of genes
+//         [w * 32 / bits, (w + 1) * 32 / bits), gene g at bit (g % (32 / bits)) * bits;
+//         zero where the row stores no such gene;
+//   masks [H / 32][rows_ld] u32: bit g % 32 of word g / 32 is set where the row stores g;
+//   head_end [rows]: each row's first entry whose gene is >= H (the tail's start);
+//   meta [H] (scale, offset) per head gene and, for the column-scale / row-offset policy,
+//         row offsets, all multiplied by 2^k (k = scale_exp).
 //
-// Layout per workgroup (8 waves, 256 rows): the genes of the head are walked in slabs of 64
-// (two 32-gene MFMA chunks). Per slab:
-//   * the slab's packed weights ([chunk][column][32 genes], 8 KB) and per-gene metadata are
-//     double-buffered in LDS, loaded one slab ahead into registers by all waves;
-//   * each wave owns 32 rows (two 16-row MFMA blocks) and an LDS tile of 3 planes (hi, mid,
-//     lo) x 32 rows x 64 genes of fp16, zeroed, then filled with the decoded entries of its
-//     rows that fall in the slab (2 lanes per row, 4 consecutive entries per lane per step,
-//     the row's cursor advanced by the run it found);
-//   * per chunk: 4 weight fragments (one per 16-column tile of the 64 outputs) and per row
-//     block 3 value fragments, 24 MFMAs into 2 x 4 fp32 accumulator tiles.
-// Operands: A = W^T (output column x gene), B = X^T (gene x cell row), so each lane ends with
-// 4 consecutive output columns of one row (a 16-byte store).
+// Exactness. x' = fma(code, 2^k s, 2^k o) = 2^k fma(code, s, o) exactly: the reference
+// decode (include/Cellerator/quantized/access.cuh:81-91) rounds once, and scaling by a power
+// of two commutes with that rounding. x' is split into three fp16 parts with
+// round-toward-zero conversions, hi = rtz(x'), mid = rtz(x' - hi), lo = rtz(x' - hi - mid):
+// each residual is exact in fp32 (it has at most 13, then 2, significant bits), so
+// hi + mid + lo == x' whenever lo is an fp16 normal number or zero -- always for
+// |x'| >= 2^9 -- and below that only bits under 2^-14 (in x' units) can be lost: the matrix
+// cores are not relied on to keep fp16 subnormal inputs. k = 14 - floor(log2 B) for B the
+// largest |decoded value| any head code can take, so |x'| < 2^15 and hi cannot overflow.
+// Each part times an fp16 weight is exact in fp32 and the matrix cores accumulate in fp32;
+// the sums are multiplied by 2^-k (exact). The result differs from an fp32 FMA chain over the
+// decoded values only in summation order.
+//
+// Kernel: a workgroup of 4 waves, 64 rows per wave (four 16-row tiles), no LDS. Per 32-gene
+// chunk, lane (row r = lane % 16 of a tile, gene octet q = lane / 16) decodes its 8 genes
+// from one code word and one mask byte straight into the three B fragments (the operand
+// layout of the 16x16x32 instruction: 8 consecutive K values of one column per lane), and the
+// wave issues 4 tiles x 4 column blocks x 3 parts = 48 MFMAs against A = W^T fragments read
+// from the packed panel ([H/32][N][32] fp16: one coalesced kilobyte per fragment, shared by
+// every wave through L2). The loads of chunk c + 1 are issued before chunk c is decoded.
+// Lane l ends with output columns 4(l / 16) .. +3 of row l % 16 of each tile and column block.
 #include "qcsr_common.hpp"
 
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 
 typedef _Float16 cx_half8 __attribute__((ext_vector_type(8)));
 typedef float cx_float4 __attribute__((ext_vector_type(4)));
+typedef __fp16 cx_fp16x2 __attribute__((ext_vector_type(2)));
 
 namespace cx {
 namespace {
 
-constexpr int kHeadWaves = 8;
-constexpr int kRowsPerWave = 32;
-constexpr int kHeadRows = kHeadWaves * kRowsPerWave;  // rows per workgroup
-constexpr int kSlab = 64;                              // genes per slab
-constexpr int kXStride = kSlab + 8;                    // fp16 per tile row (16 B pad: the 16 rows of a fragment read fall in distinct banks)
-constexpr int kWStride = 40;                           // fp16 per panel column in LDS (32 genes + 16 B pad)
-
-struct HeadShared {
-    _Float16 x[kHeadWaves][3][kRowsPerWave][kXStride];
-    _Float16 w[2][2][64][kWStride];
-    float2 meta[2][kSlab];
-};
+constexpr int kHeadWaves = 4;
+constexpr int kTiles = 4;                             // 16-row tiles per wave
+constexpr int kRowsPerWave = 16 * kTiles;
+constexpr std::uint32_t kHeadRows = kHeadWaves * kRowsPerWave;  // rows per workgroup
+constexpr std::uint32_t kHeadAlign = 1024;            // head_cols granularity (the tail's gene part)
 
 struct HeadArgs {
-    const std::int32_t *row_ptr;
-    const std::int32_t *packed_row_ptr;
-    const std::int32_t *col_idx;
-    const std::uint8_t *packed;
-    const float *scales;   // per gene, or (scale, offset) pairs for the pairs policy
-    const float *offsets;
-    const float *row_offsets;
+    const std::uint32_t *codes;
+    const std::uint32_t *masks;
+    const float2 *meta;          // [head] pre-scaled (scale, offset)
+    const float *row_offsets;    // [rows] pre-scaled (column-scale / row-offset policy), else null
     const std::uint16_t *panel;  // fp16 [head/32][panel_n][32] at this launch's first column
     float *partial;              // [rows][64] fp32: Y_head
-    std::int32_t *head_end;      // [rows]: first entry of each row with gene >= head
     std::uint32_t rows;
-    std::uint32_t head;          // head genes, a multiple of kSlab
-    std::uint32_t panel_n;       // output columns of the packed panel
+    std::uint32_t rows_ld;
+    std::uint32_t chunks;        // head / 32
+    std::uint32_t panel_n;
+    float inv_scale;             // 2^-k
 };
 
-__device__ __forceinline__ uint4 ldg4(const void *p) { return *static_cast<const uint4 *>(p); }
+template<int kBits>
+struct CodeWords {
+    std::uint32_t w[kBits == 8 ? 2 : 1];
+};
 
-template<int kPolicy>
-__device__ __forceinline__ float2 gene_meta(const HeadArgs &h, std::uint32_t g) {
-    if constexpr (kPolicy == CX_DECODE_PER_GENE_AFFINE_PAIRS) {
-        return reinterpret_cast<const float2 *>(h.scales)[g];
+template<int kBits>
+__device__ __forceinline__ CodeWords<kBits> load_code_words(const HeadArgs &h, std::uint32_t c, int q,
+                                                            std::uint32_t row) {
+    CodeWords<kBits> cw;
+    if constexpr (kBits == 8) {
+        const std::uint32_t *p = h.codes + static_cast<std::uint64_t>(c * 8u + 2u * q) * h.rows_ld + row;
+        cw.w[0] = p[0];
+        cw.w[1] = p[h.rows_ld];
     } else {
-        const float s = h.scales != nullptr ? h.scales[g] : 1.0f;
-        const float o = kPolicy == CX_DECODE_PER_GENE_AFFINE && h.offsets != nullptr ? h.offsets[g] : 0.0f;
-        return make_float2(s, o);
+        // octet q covers bits [8 q bits, 8 q bits + 8 bits) of the chunk's `bits` words
+        cw.w[0] = h.codes[static_cast<std::uint64_t>(c * kBits + (q * kBits) / 4) * h.rows_ld + row];
+    }
+    return cw;
+}
+
+// Sign-extended bit j of v (0 or all ones), kept as one v_bfe_i32: the AND-mask form of a
+// presence bit, which the optimizer would otherwise rewrite into a compare and a select.
+template<int kBit>
+__device__ __forceinline__ std::uint32_t bit_mask(std::uint32_t v) {
+    std::uint32_t r;
+    asm("v_bfe_i32 %0, %1, %2, 1" : "=v"(r) : "v"(v), "n"(kBit));
+    return r;
+}
+
+// Code of gene j of an octet as a float: 4- and 8-bit codes through byte conversions.
+template<int kBits, int kJ>
+__device__ __forceinline__ float octet_code(const std::uint32_t (&w)[2], std::uint32_t lo4, std::uint32_t hi4) {
+    if constexpr (kBits == 8) return static_cast<float>((w[kJ >> 2] >> (8 * (kJ & 3))) & 0xffu);
+    else if constexpr (kBits == 4) return static_cast<float>((((kJ & 1) != 0 ? hi4 : lo4) >> (8 * (kJ >> 1))) & 0xffu);
+    else return static_cast<float>((w[0] >> (kJ * kBits)) & ((1u << kBits) - 1u));
+}
+
+// fp16 parts of a pair of values: rtz conversions, residuals through v_fma_mix_f32 (the fp16
+// part is widened inside the instruction).
+__device__ __forceinline__ void split_pair(float x0, float x1, std::uint32_t &hw, std::uint32_t &mw, std::uint32_t &lw) {
+    const cx_fp16x2 h2 = __builtin_amdgcn_cvt_pkrtz(x0, x1);
+    const float r0 = __builtin_fmaf(static_cast<float>(h2[0]), -1.0f, x0);
+    const float r1 = __builtin_fmaf(static_cast<float>(h2[1]), -1.0f, x1);
+    const cx_fp16x2 m2 = __builtin_amdgcn_cvt_pkrtz(r0, r1);
+    const cx_fp16x2 l2 = __builtin_amdgcn_cvt_pkrtz(__builtin_fmaf(static_cast<float>(m2[0]), -1.0f, r0),
+                                                     __builtin_fmaf(static_cast<float>(m2[1]), -1.0f, r1));
+    hw = __builtin_bit_cast(std::uint32_t, h2);
+    mw = __builtin_bit_cast(std::uint32_t, m2);
+    lw = __builtin_bit_cast(std::uint32_t, l2);
+}
+
+template<int kBits, int kPolicy, int kJ>
+__device__ __forceinline__ float octet_value(const std::uint32_t (&w)[2], std::uint32_t lo4, std::uint32_t hi4,
+                                             std::uint32_t mb, const float2 (&md)[8], float roff) {
+    const float off = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET ? roff : md[kJ].y;
+    const float v = __builtin_fmaf(octet_code<kBits, kJ>(w, lo4, hi4), md[kJ].x, off);
+    return __uint_as_float(__float_as_uint(v) & bit_mask<kJ>(mb));  // absent genes: +0
+}
+
+// The 8 genes of one octet, decoded, masked and split into three fp16 fragments.
+template<int kBits, int kPolicy>
+__device__ __forceinline__ void decode_octet(const CodeWords<kBits> &cw, int q, std::uint32_t mask_word,
+                                             const float2 (&md)[8], float roff, cx_half8 &bh, cx_half8 &bm,
+                                             cx_half8 &bl) {
+    const std::uint32_t mb = mask_word >> (8 * q);
+    std::uint32_t w[2] = {cw.w[0], kBits == 8 ? cw.w[kBits == 8 ? 1 : 0] : 0u};
+    if constexpr (kBits < 8) w[0] = cw.w[0] >> ((8 * q * kBits) & 31);
+    const std::uint32_t lo4 = w[0] & 0x0f0f0f0fu;
+    const std::uint32_t hi4 = (w[0] >> 4) & 0x0f0f0f0fu;
+    std::uint32_t hw[4], mw[4], lw[4];
+    split_pair(octet_value<kBits, kPolicy, 0>(w, lo4, hi4, mb, md, roff),
+               octet_value<kBits, kPolicy, 1>(w, lo4, hi4, mb, md, roff), hw[0], mw[0], lw[0]);
+    split_pair(octet_value<kBits, kPolicy, 2>(w, lo4, hi4, mb, md, roff),
+               octet_value<kBits, kPolicy, 3>(w, lo4, hi4, mb, md, roff), hw[1], mw[1], lw[1]);
+    split_pair(octet_value<kBits, kPolicy, 4>(w, lo4, hi4, mb, md, roff),
+               octet_value<kBits, kPolicy, 5>(w, lo4, hi4, mb, md, roff), hw[2], mw[2], lw[2]);
+    split_pair(octet_value<kBits, kPolicy, 6>(w, lo4, hi4, mb, md, roff),
+               octet_value<kBits, kPolicy, 7>(w, lo4, hi4, mb, md, roff), hw[3], mw[3], lw[3]);
+    bh = __builtin_bit_cast(cx_half8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+    bm = __builtin_bit_cast(cx_half8, make_uint4(mw[0], mw[1], mw[2], mw[3]));
+    bl = __builtin_bit_cast(cx_half8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
+}
+
+template<int kBits>
+struct ChunkLoads {
+    cx_half8 aw[4];             // A = W^T fragments of the 4 column blocks
+    float2 md[8];               // pre-scaled (scale, offset) of the octet's genes
+    CodeWords<kBits> cw[kTiles];
+    std::uint32_t mw[kTiles];
+};
+
+template<int kBits>
+__device__ __forceinline__ void load_chunk(ChunkLoads<kBits> &L, const HeadArgs &h, std::uint32_t c, int q, int r16,
+                                           std::uint32_t row0) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+        L.aw[t] = *reinterpret_cast<const cx_half8 *>(
+            h.panel + (static_cast<std::uint64_t>(c) * h.panel_n + t * 16 + r16) * 32u + 8u * q);
+    const float4 *mp = reinterpret_cast<const float4 *>(h.meta + c * 32u + 8u * q);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float4 v = mp[k];
+        L.md[2 * k] = make_float2(v.x, v.y);
+        L.md[2 * k + 1] = make_float2(v.z, v.w);
+    }
+    const std::uint32_t *mrow = h.masks + static_cast<std::uint64_t>(c) * h.rows_ld;
+#pragma unroll
+    for (int b = 0; b < kTiles; ++b) {
+        const std::uint32_t row = row0 + 16u * b;
+        L.mw[b] = mrow[row];
+        L.cw[b] = load_code_words<kBits>(h, c, q, row);
     }
 }
 
 template<int kBits, int kPolicy>
-__global__ __launch_bounds__(kHeadWaves * kWave) void qcsr_head_mfma(HeadArgs h) {
-    __shared__ HeadShared sh;
-    const int tid = static_cast<int>(threadIdx.x);
-    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const int lane = tid % kWave;
-    const std::uint32_t wave_first = blockIdx.x * static_cast<std::uint32_t>(kHeadRows) + wave * kRowsPerWave;
+__global__ __launch_bounds__(kHeadWaves * kWave) void qcsr_head_dense(HeadArgs h) {
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    const int r16 = lane & 15;
+    const int q = lane >> 4;
+    // row of tile 0 (tile b: + 16 b); rows up to rows_ld exist in the dense arrays
+    const std::uint32_t row0 = blockIdx.x * kHeadRows + static_cast<std::uint32_t>(wave * kRowsPerWave + r16);
 
-    // ---- scatter role: lanes 2r, 2r + 1 walk row r of the wave -------------------------
-    const int rr = lane >> 1;
-    const int sub = lane & 1;
-    const std::uint32_t row = wave_first + static_cast<std::uint32_t>(rr);
-    const bool has_row = row < h.rows;
-    std::int32_t cur = 0, end = 0, rbeg = 0;
-    std::int64_t pbyte = 0;
-    float roff = 0.0f;
-    if (has_row) {
-        rbeg = cur = h.row_ptr[row];
-        end = h.row_ptr[row + 1];
-        pbyte = h.packed_row_ptr[row];
-        if constexpr (kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET)
-            roff = h.row_offsets != nullptr ? h.row_offsets[row] : 0.0f;
+    float roff[kTiles];
+#pragma unroll
+    for (int b = 0; b < kTiles; ++b) {
+        const std::uint32_t row = row0 + 16u * b;
+        roff[b] = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET && h.row_offsets != nullptr && row < h.rows
+            ? h.row_offsets[row] : 0.0f;
     }
 
-    // ---- weight slab staging: thread tid moves one 16-byte piece of the slab's panel -----
-    const int wc = tid >> 8;            // chunk of the slab
-    const int wcol = (tid >> 2) & 63;   // output column
-    const int wpiece = tid & 3;         // 8 genes
-    // bounds of the entry and code arrays: the matrix's own extent
-    const std::int64_t nnz_all = h.row_ptr[h.rows];
-    const std::int64_t packed_bytes = h.packed_row_ptr[h.rows];
-    auto load_slab = [&](std::uint32_t s, uint4 &wv, float2 &mv) {
-        const std::uint64_t chunk = 2u * s + static_cast<std::uint32_t>(wc);
-        wv = ldg4(h.panel + ((chunk * h.panel_n + static_cast<std::uint32_t>(wcol)) * 32u + wpiece * 8u));
-        if (tid < kSlab) mv = gene_meta<kPolicy>(h, s * kSlab + static_cast<std::uint32_t>(tid));
-    };
-    auto store_slab = [&](int buf, const uint4 &wv, const float2 &mv) {
-        *reinterpret_cast<uint4 *>(&sh.w[buf][wc][wcol][wpiece * 8]) = wv;
-        if (tid < kSlab) sh.meta[buf][tid] = mv;
-    };
-
-    // acc sums the hi and mid parts; acc_lo the lo parts, which are stored scaled by 2^12
-    // (an exact power-of-two scale) so they stay normal fp16 numbers: the matrix cores are
-    // not relied on to keep fp16 subnormal inputs
-    cx_float4 acc[2][4], acc_lo[2][4];
+    cx_float4 acc[kTiles][4];
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < kTiles; ++b)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[b][t] = acc_lo[b][t] = cx_float4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int t = 0; t < 4; ++t) acc[b][t] = cx_float4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const std::uint32_t slabs = h.head / kSlab;
-    uint4 wnext = make_uint4(0u, 0u, 0u, 0u);
-    float2 mnext = make_float2(0.0f, 0.0f);
-    if (slabs != 0u) {
-        load_slab(0u, wnext, mnext);
-        store_slab(0, wnext, mnext);
-    }
-    __syncthreads();
-
-    _Float16 *xw = &sh.x[wave][0][0][0];
-    constexpr std::uint32_t kMask = (1u << kBits) - 1u;
-    for (std::uint32_t s = 0; s < slabs; ++s) {
-        const int buf = static_cast<int>(s & 1u);
-        if (s + 1u < slabs) load_slab(s + 1u, wnext, mnext);
-
-        // zero this wave's tiles: 3 planes x 32 rows x 64 genes (768 pieces of 16 bytes)
+    ChunkLoads<kBits> cur, nxt;
+    if (h.chunks != 0u) load_chunk<kBits>(cur, h, 0u, q, r16, row0);
+    for (std::uint32_t c = 0; c < h.chunks; ++c) {
+        if (c + 1u < h.chunks) load_chunk<kBits>(nxt, h, c + 1u, q, r16, row0);
 #pragma unroll
-        for (int k = 0; k < 12; ++k) {
-            const int piece = k * kWave + lane;             // 0 .. 767
-            const int plane = piece >> 8, r = (piece >> 3) & 31, c8 = piece & 7;
-            *reinterpret_cast<uint4 *>(&sh.x[wave][plane][r][c8 * 8]) = make_uint4(0u, 0u, 0u, 0u);
+        for (int b = 0; b < kTiles; ++b) {
+            cx_half8 bh, bm, bl;
+            decode_octet<kBits, kPolicy>(cur.cw[b], q, cur.mw[b], cur.md, roff[b], bh, bm, bl);
+            // each accumulator's three products are 4 instructions apart
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.aw[t], bh, acc[b][t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.aw[t], bm, acc[b][t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.aw[t], bl, acc[b][t], 0, 0, 0);
         }
-
-        // scatter the decoded entries of the slab: step by 8 entries per row
-        const std::int32_t lo = static_cast<std::int32_t>(s * kSlab);
-        const std::int32_t hi = lo + kSlab;
-        const float2 *meta = sh.meta[buf];
-        bool active = has_row && cur < end;
-        while (__builtin_amdgcn_ballot_w64(active) != 0u) {
-            int n_in = 0;
-            if (active) {
-                const std::int32_t e0 = cur + 4 * sub;
-                std::int32_t c[4];
-                if (static_cast<std::int64_t>(e0) + 4 <= nnz_all) {
-                    const uint4 v = ldg4(h.col_idx + e0);
-                    c[0] = static_cast<std::int32_t>(v.x); c[1] = static_cast<std::int32_t>(v.y);
-                    c[2] = static_cast<std::int32_t>(v.z); c[3] = static_cast<std::int32_t>(v.w);
-                } else {
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) c[k] = e0 + k < nnz_all ? h.col_idx[e0 + k] : 0x7fffffff;
-                }
-                // codes of entries e0 .. e0 + 3: an aligned dword pair around their first bit
-                const std::int64_t bit = (pbyte << 3) + static_cast<std::int64_t>(e0 - rbeg) * kBits;
-                const std::int64_t al = (bit >> 3) & ~static_cast<std::int64_t>(3);
-                std::uint32_t d0, d1;
-                if (al + 8 <= packed_bytes) {
-                    const uint2 d = *reinterpret_cast<const uint2 *>(h.packed + al);
-                    d0 = d.x; d1 = d.y;
-                } else {
-                    d0 = d1 = 0u;
-#pragma unroll
-                    for (int b = 0; b < 8; ++b) {
-                        const std::uint32_t v = al + b < packed_bytes ? h.packed[al + b] : 0u;
-                        if (b < 4) d0 |= v << (8 * b);
-                        else d1 |= v << (8 * (b - 4));
-                    }
-                }
-                const std::uint32_t cw = __builtin_amdgcn_alignbit(d1, d0, static_cast<std::uint32_t>(bit - (al << 3)));
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    // sorted rows (the launch requires it): a run entry is in [lo, hi); the
-                    // lower bound only keeps a broken promise inside the tile
-                    const bool in = e0 + k < end && c[k] < hi && c[k] >= lo;
-                    if (in) {
-                        const int g = c[k] - lo;
-                        const float2 md = meta[g];
-                        const float off = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET ? roff : md.y;
-                        const float x = __builtin_fmaf(static_cast<float>((cw >> (k * kBits)) & kMask), md.x, off);
-                        const _Float16 p0 = static_cast<_Float16>(x);
-                        const float r1 = x - static_cast<float>(p0);
-                        const _Float16 p1 = static_cast<_Float16>(r1);
-                        const _Float16 p2 = static_cast<_Float16>((r1 - static_cast<float>(p1)) * 4096.0f);
-                        _Float16 *px = xw + rr * kXStride + g;
-                        px[0] = p0;
-                        px[kRowsPerWave * kXStride] = p1;
-                        px[2 * kRowsPerWave * kXStride] = p2;
-                        ++n_in;
-                    }
-                }
-            }
-            // both lanes of a row advance by the entries the pair found in the slab
-            const int total = n_in + __shfl_xor(n_in, 1, kWave);
-            cur += total;
-            active = active && total == 8 && cur < end;
-        }
-
-        // matrix cores: two 32-gene chunks
-        const int fr = lane & 15;        // A row / B column / D column of this lane
-        const int fk = (lane >> 4) * 8;  // first gene of this lane's fragment
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            cx_half8 aw[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-                aw[t] = *reinterpret_cast<const cx_half8 *>(&sh.w[buf][c][t * 16 + fr][fk]);
-#pragma unroll
-            for (int b = 0; b < 2; ++b) {
-                cx_half8 bx[3];
-#pragma unroll
-                for (int p = 0; p < 3; ++p)
-                    bx[p] = *reinterpret_cast<const cx_half8 *>(&sh.x[wave][p][b * 16 + fr][c * 32 + fk]);
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[t], bx[0], acc[b][t], 0, 0, 0);
-                    acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[t], bx[1], acc[b][t], 0, 0, 0);
-                    acc_lo[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[t], bx[2], acc_lo[b][t], 0, 0, 0);
-                }
-            }
-        }
-
-        if (s + 1u < slabs) store_slab(buf ^ 1, wnext, mnext);
-        __syncthreads();
+        cur = nxt;
     }
 
-    // Y_head: lane holds columns t*16 + 4*(lane/16) .. +3 of row (lane % 16) of each block
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-        const std::uint32_t r = wave_first + static_cast<std::uint32_t>(b * 16 + (lane & 15));
-        if (r < h.rows) {
+    for (int b = 0; b < kTiles; ++b) {
+        const std::uint32_t row = row0 + 16u * b;
+        if (row < h.rows) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                float v[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(acc_lo[b][t][i], 1.0f / 4096.0f, acc[b][t][i]);
-                float *o = h.partial + static_cast<std::int64_t>(r) * 64 + t * 16 + 4 * (lane >> 4);
-                *reinterpret_cast<float4 *>(o) = make_float4(v[0], v[1], v[2], v[3]);
+                float *o = h.partial + static_cast<std::uint64_t>(row) * 64u + t * 16 + 4 * q;
+                *reinterpret_cast<float4 *>(o) = make_float4(acc[b][t][0] * h.inv_scale, acc[b][t][1] * h.inv_scale,
+                                                             acc[b][t][2] * h.inv_scale, acc[b][t][3] * h.inv_scale);
             }
         }
     }
-    if (has_row && sub == 0) h.head_end[row] = cur;
 }
 
-} // namespace
+// ---- building the dense head -----------------------------------------------------------
 
-// Launches the head kernel for codes of `bits` under `policy` (validated by the caller).
-int launch_qcsr_head(const QcsrArgs &a, std::uint32_t bits, std::uint32_t policy, std::uint32_t head,
-                     const std::uint16_t *panel, std::uint32_t panel_n, float *partial, std::int32_t *head_end,
-                     hipStream_t stream) {
-    HeadArgs h{};
-    h.row_ptr = a.row_ptr;
-    h.packed_row_ptr = a.packed_row_ptr;
-    h.col_idx = a.col_idx;
-    h.packed = a.packed;
-    h.scales = a.scales;
-    h.offsets = a.offsets;
-    h.row_offsets = a.row_offsets;
-    h.panel = panel;
-    h.partial = partial;
-    h.head_end = head_end;
-    h.rows = a.rows;
-    h.head = head;
-    h.panel_n = panel_n;
-    const dim3 grid((a.rows + kHeadRows - 1) / kHeadRows), block(kHeadWaves * kWave);
-#define CX_HEAD(B, P) hipLaunchKernelGGL((qcsr_head_mfma<B, P>), grid, block, 0, stream, h)
-#define CX_HEAD_POLICY(B)                                                                   \
-    do {                                                                                    \
-        if (policy == CX_DECODE_PER_GENE_AFFINE) CX_HEAD(B, CX_DECODE_PER_GENE_AFFINE);     \
-        else if (policy == CX_DECODE_PER_GENE_AFFINE_PAIRS) CX_HEAD(B, CX_DECODE_PER_GENE_AFFINE_PAIRS); \
-        else CX_HEAD(B, CX_DECODE_COLUMN_SCALE_ROW_OFFSET);                                 \
-    } while (0)
-    switch (bits) {
-    case 1: CX_HEAD_POLICY(1); break;
-    case 2: CX_HEAD_POLICY(2); break;
-    case 4: CX_HEAD_POLICY(4); break;
-    default: CX_HEAD_POLICY(8); break;
+struct BuildArgs {
+    const std::int32_t *row_ptr;
+    const std::int32_t *packed_row_ptr;
+    const std::int32_t *col_idx;
+    const std::uint8_t *packed;
+    std::uint32_t rows;
+    std::uint32_t rows_ld;
+    std::uint32_t head;
+    std::uint32_t *codes;
+    std::uint32_t *masks;
+    std::int32_t *head_end;
+    std::uint32_t *error;  // set to 1 where a row's genes are not strictly increasing
+};
+
+// One thread per row (consecutive rows in consecutive lanes, so every word store of a
+// wave is 256 contiguous bytes): walks the row's head entries in order and writes every
+// code word and mask word of the row, zeros included.
+template<int kBits>
+__global__ __launch_bounds__(256) void dense_head_build(BuildArgs a) {
+    const std::uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= a.rows_ld) return;
+    constexpr std::uint32_t kGenesPerWord = 32u / kBits;
+    constexpr std::uint32_t kMask = (1u << kBits) - 1u;
+    const std::uint32_t words = a.head / kGenesPerWord;
+    std::int64_t e = 0, end = 0, rb = 0, pbit = 0;
+    if (row < a.rows) {
+        rb = e = a.row_ptr[row];
+        end = a.row_ptr[row + 1];
+        pbit = static_cast<std::int64_t>(a.packed_row_ptr[row]) * 8;
     }
-#undef CX_HEAD_POLICY
-#undef CX_HEAD
-    return check_launch("qcsr_head_mfma");
+    std::int64_t prev = -1;
+    bool bad = false;
+    std::uint32_t mword = 0u;
+    for (std::uint32_t w = 0; w < words; ++w) {
+        const std::int64_t g_lo = static_cast<std::int64_t>(w) * kGenesPerWord;
+        const std::int64_t g_hi = g_lo + kGenesPerWord;
+        std::uint32_t word = 0u;
+        while (e < end) {
+            const std::int64_t c = a.col_idx[e];
+            if (c >= g_hi) break;
+            if (c <= prev) {  // repeated, decreasing or negative gene: not a sorted row
+                bad = true;
+                break;
+            }
+            const std::int64_t bit = pbit + (e - rb) * kBits;
+            const std::uint32_t code = (static_cast<std::uint32_t>(a.packed[bit >> 3]) >> (bit & 7)) & kMask;
+            word |= code << (static_cast<std::uint32_t>(c - g_lo) * kBits);
+            mword |= 1u << (static_cast<std::uint32_t>(c) & 31u);
+            prev = c;
+            ++e;
+        }
+        a.codes[static_cast<std::uint64_t>(w) * a.rows_ld + row] = word;
+        if (((w + 1u) * kGenesPerWord) % 32u == 0u) {
+            a.masks[static_cast<std::uint64_t>((w + 1u) * kGenesPerWord / 32u - 1u) * a.rows_ld + row] = mword;
+            mword = 0u;
+        }
+        if (bad) e = end;  // the remaining words of the row stay zero
+    }
+    if (row < a.rows) a.head_end[row] = static_cast<std::int32_t>(e);
+    if (bad) atomicOr(a.error, 1u);
 }
-
-} // namespace cx
-
-namespace cx {
-namespace {
 
 // Largest |decoded value| any code of a head gene can take, as float bits (non-negative
 // floats order like their bit patterns): per-gene affine max(|o|, |o + qmax s|); column
-// scale with row offsets |s| qmax (the row offsets' largest magnitude is added by the host).
+// scale with row offsets |s| qmax (the row offsets' largest magnitude is found separately).
 __global__ __launch_bounds__(256) void head_range_kernel(const float *scales, const float *offsets, std::uint32_t policy,
                                                          std::uint32_t head, float qmax, std::uint32_t *max_bits) {
     const std::uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
@@ -329,7 +328,7 @@ __global__ __launch_bounds__(256) void head_range_kernel(const float *scales, co
         }
         b = fmaxf(fabsf(o), fabsf(__builtin_fmaf(qmax, s, o)));
         if (policy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET) b = fabsf(s) * qmax;
-        if (!(b == b)) b = __builtin_huge_valf();  // NaN metadata: reject
+        if (!(s == s) || !(o == o) || !(b == b)) b = __builtin_huge_valf();  // NaN metadata: reject
     }
     for (int d = 32; d >= 1; d >>= 1) b = fmaxf(b, __shfl_xor(b, d, kWave));
     if ((threadIdx.x & (kWave - 1)) == 0) atomicMax(max_bits, __float_as_uint(b));
@@ -345,9 +344,31 @@ __global__ __launch_bounds__(256) void abs_max_kernel(const float *v, std::uint3
     if ((threadIdx.x & (kWave - 1)) == 0) atomicMax(max_bits, __float_as_uint(b));
 }
 
-__global__ void zero_two_words(std::uint32_t *p) { p[0] = 0u; p[1] = 0u; }
+__global__ void zero_words(std::uint32_t *p, int n) {
+    if (static_cast<int>(threadIdx.x) < n) p[threadIdx.x] = 0u;
+}
 
-constexpr float kHeadValueLimit = 32768.0f;  // fp16 parts of |x| < 2^15 cannot overflow
+// meta[g] = 2^k (scale, offset) of head gene g (offset 0 under the row-offset policy);
+// row_offsets_out[r] = 2^k row offset.
+__global__ __launch_bounds__(256) void scale_meta_kernel(const float *scales, const float *offsets,
+                                                         const float *row_offsets, std::uint32_t policy,
+                                                         std::uint32_t head, std::uint32_t rows, float factor,
+                                                         float2 *meta, float *row_offsets_out) {
+    const std::uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < head) {
+        float s, o;
+        if (policy == CX_DECODE_PER_GENE_AFFINE_PAIRS) {
+            s = scales[2 * i];
+            o = scales[2 * i + 1];
+        } else {
+            s = scales != nullptr ? scales[i] : 1.0f;
+            o = policy == CX_DECODE_PER_GENE_AFFINE && offsets != nullptr ? offsets[i] : 0.0f;
+        }
+        meta[i] = make_float2(s * factor, o * factor);
+    }
+    if (row_offsets_out != nullptr && i < rows)
+        row_offsets_out[i] = row_offsets != nullptr ? row_offsets[i] * factor : 0.0f;
+}
 
 bool valid_bits(std::uint32_t b) { return b == 1u || b == 2u || b == 4u || b == 8u; }
 
@@ -358,87 +379,221 @@ int validate_hybrid(const cx_qcsr_matrix *m, std::uint32_t head, const char *who
     if (m->decode_policy != CX_DECODE_PER_GENE_AFFINE && m->decode_policy != CX_DECODE_PER_GENE_AFFINE_PAIRS
         && m->decode_policy != CX_DECODE_COLUMN_SCALE_ROW_OFFSET)
         return fail(CX_STATUS_UNSUPPORTED, "hybrid quantized CSR: unknown decode policy");
-    if (head % 1024u != 0u || head > m->cols)
+    if (head % kHeadAlign != 0u || head > m->cols)
         return fail(CX_STATUS_INVALID_SHAPE, "hybrid quantized CSR: head_cols must be a multiple of 1,024 within cols");
     if (m->rows != 0u && (m->row_ptr == nullptr || m->packed_row_ptr == nullptr
                           || (m->nnz != 0u && (m->col_idx == nullptr || m->packed_values == nullptr))))
         return fail(CX_STATUS_INVALID_ARGUMENT, "hybrid quantized CSR: null structure or codes");
     if (m->decode_policy == CX_DECODE_PER_GENE_AFFINE_PAIRS && m->column_scales == nullptr)
         return fail(CX_STATUS_INVALID_ARGUMENT, "hybrid quantized CSR: the pairs policy needs column_scales");
+    if ((m->flags & CX_QCSR_COLUMNS_SORTED) == 0u)
+        return fail(CX_STATUS_INVALID_ARGUMENT,
+                    "hybrid quantized CSR: rows must be sorted (CX_QCSR_COLUMNS_SORTED, e.g. from cx_qcsr_to_execution_order)");
+    if (m->nnz > static_cast<std::uint64_t>(INT32_MAX) || m->cols > static_cast<std::uint32_t>(INT32_MAX))
+        return fail(CX_STATUS_INVALID_SHAPE, "hybrid quantized CSR: nnz exceeds int32 row offsets");
     return CX_STATUS_SUCCESS;
+}
+
+constexpr std::uint64_t align256(std::uint64_t b) { return (b + 255u) & ~std::uint64_t{255u}; }
+
+struct LayoutSizes {
+    std::uint64_t header, codes, masks, head_end, meta, row_offsets, total;
+    std::uint32_t rows_ld;
+};
+
+LayoutSizes layout_sizes(const cx_qcsr_matrix *m, std::uint32_t head) {
+    LayoutSizes s{};
+    s.rows_ld = static_cast<std::uint32_t>((static_cast<std::uint64_t>(m->rows) + kHeadRows - 1) / kHeadRows * kHeadRows);
+    s.header = 256;
+    s.codes = align256(static_cast<std::uint64_t>(head) * m->bits / 32u * s.rows_ld * 4u);
+    s.masks = align256(static_cast<std::uint64_t>(head) / 32u * s.rows_ld * 4u);
+    s.head_end = align256(static_cast<std::uint64_t>(m->rows) * 4u);
+    s.meta = align256(static_cast<std::uint64_t>(head) * 8u);
+    s.row_offsets = m->decode_policy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET ? align256(static_cast<std::uint64_t>(m->rows) * 4u) : 0u;
+    s.total = s.header + s.codes + s.masks + s.head_end + s.meta + s.row_offsets;
+    return s;
+}
+
+// Launches the dense head kernel for one 64-column block.
+int launch_head(const cx_qcsr_hybrid_layout &L, const std::uint16_t *panel, std::uint32_t panel_n, float *partial,
+                hipStream_t stream) {
+    HeadArgs h{};
+    h.codes = L.codes;
+    h.masks = L.masks;
+    h.meta = reinterpret_cast<const float2 *>(L.meta);
+    h.row_offsets = L.row_offsets;
+    h.panel = panel;
+    h.partial = partial;
+    h.rows = L.rows;
+    h.rows_ld = L.rows_ld;
+    h.chunks = L.head_cols / 32u;
+    h.panel_n = panel_n;
+    h.inv_scale = std::ldexp(1.0f, -L.scale_exp);
+    const dim3 grid(L.rows_ld / kHeadRows), block(kHeadWaves * kWave);
+#define CX_HEAD(B, P) hipLaunchKernelGGL((qcsr_head_dense<B, P>), grid, block, 0, stream, h)
+#define CX_HEAD_POLICY(B)                                                                        \
+    do {                                                                                         \
+        if (L.decode_policy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET) CX_HEAD(B, CX_DECODE_COLUMN_SCALE_ROW_OFFSET); \
+        else CX_HEAD(B, CX_DECODE_PER_GENE_AFFINE);                                              \
+    } while (0)
+    switch (L.bits) {
+    case 1: CX_HEAD_POLICY(1); break;
+    case 2: CX_HEAD_POLICY(2); break;
+    case 4: CX_HEAD_POLICY(4); break;
+    default: CX_HEAD_POLICY(8); break;
+    }
+#undef CX_HEAD_POLICY
+#undef CX_HEAD
+    return check_launch("qcsr_head_dense");
 }
 
 } // namespace
 } // namespace cx
 
-extern "C" int cx_qcsr_hybrid_prepare(const cx_qcsr_matrix *m, uint32_t head_cols, const uint16_t *rhs_f16,
-                                      int64_t rhs_ld, uint32_t out_cols, uint16_t *head_panel, void *stream) {
+extern "C" int cx_qcsr_hybrid_layout_bytes(const cx_qcsr_matrix *m, uint32_t head_cols, uint64_t *bytes) {
+    using namespace cx;
+    clear_error();
+    if (bytes == nullptr) return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_hybrid_layout_bytes: null bytes");
+    const int rc = validate_hybrid(m, head_cols, "cx_qcsr_hybrid_layout_bytes: null matrix");
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    *bytes = layout_sizes(m, head_cols).total;
+    return CX_STATUS_SUCCESS;
+}
+
+extern "C" int cx_qcsr_hybrid_prepare(const cx_qcsr_matrix *m, uint32_t head_cols, void *storage,
+                                      uint64_t storage_bytes, cx_qcsr_hybrid_layout *layout, void *stream) {
     using namespace cx;
     clear_error();
     int rc = validate_hybrid(m, head_cols, "cx_qcsr_hybrid_prepare: null matrix");
     if (rc != CX_STATUS_SUCCESS) return rc;
-    if (head_cols == 0u) return CX_STATUS_SUCCESS;
-    if (rhs_f16 == nullptr || head_panel == nullptr || out_cols == 0u || out_cols % 64u != 0u || rhs_ld < out_cols)
-        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_hybrid_prepare: null weights or panel, or out_cols not a multiple of 64");
+    if (layout == nullptr) return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_hybrid_prepare: null layout");
+    const LayoutSizes sz = layout_sizes(m, head_cols);
+    if (storage == nullptr || storage_bytes < sz.total || (reinterpret_cast<std::uintptr_t>(storage) & 255u) != 0u)
+        return fail(CX_STATUS_INVALID_ARGUMENT,
+                    "cx_qcsr_hybrid_prepare: storage must be 256-byte aligned and hold cx_qcsr_hybrid_layout_bytes");
+    cx_qcsr_hybrid_layout L{};
+    L.head_cols = head_cols;
+    L.rows = m->rows;
+    L.rows_ld = sz.rows_ld;
+    L.bits = m->bits;
+    L.decode_policy = m->decode_policy;
+    L.nnz = m->nnz;
+    auto *base = static_cast<unsigned char *>(storage);
+    std::uint64_t off = sz.header;
+    L.codes = reinterpret_cast<uint32_t *>(base + off);
+    off += sz.codes;
+    L.masks = reinterpret_cast<uint32_t *>(base + off);
+    off += sz.masks;
+    L.head_end = reinterpret_cast<int32_t *>(base + off);
+    off += sz.head_end;
+    L.meta = reinterpret_cast<float *>(base + off);
+    off += sz.meta;
+    L.row_offsets = sz.row_offsets != 0u ? reinterpret_cast<float *>(base + off) : nullptr;
+
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    std::uint32_t *words = nullptr;
-    hipError_t e = hipMalloc(reinterpret_cast<void **>(&words), 2 * sizeof(std::uint32_t));
-    if (e != hipSuccess) return hip_fail(e, "cx_qcsr_hybrid_prepare: hipMalloc");
-    hipLaunchKernelGGL(zero_two_words, dim3(1), dim3(1), 0, s, words);
-    const float qmax = static_cast<float>((1u << m->bits) - 1u);
-    hipLaunchKernelGGL(head_range_kernel, dim3((head_cols + 255u) / 256u), dim3(256), 0, s, m->column_scales,
-                       m->column_offsets, m->decode_policy, head_cols, qmax, words);
-    if (m->decode_policy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET && m->row_offsets != nullptr && m->rows != 0u)
-        hipLaunchKernelGGL(abs_max_kernel, dim3(std::min<std::uint32_t>((m->rows + 255u) / 256u, 4096u)), dim3(256), 0,
-                           s, m->row_offsets, m->rows, words + 1);
-    std::uint32_t host[2] = {0u, 0u};
-    e = hipMemcpyAsync(host, words, sizeof(host), hipMemcpyDeviceToHost, s);
+    auto *words = reinterpret_cast<std::uint32_t *>(base);  // header: range bits, row-offset bits, error
+    hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, s, words, 4);
+    if (head_cols != 0u) {
+        const float qmax = static_cast<float>((1u << m->bits) - 1u);
+        hipLaunchKernelGGL(head_range_kernel, dim3((head_cols + 255u) / 256u), dim3(256), 0, s, m->column_scales,
+                           m->column_offsets, m->decode_policy, head_cols, qmax, words);
+        if (m->decode_policy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET && m->row_offsets != nullptr && m->rows != 0u)
+            hipLaunchKernelGGL(abs_max_kernel, dim3(std::min<std::uint32_t>((m->rows + 255u) / 256u, 4096u)), dim3(256),
+                               0, s, m->row_offsets, m->rows, words + 1);
+    }
+    if (L.rows_ld != 0u) {
+        BuildArgs b{};
+        b.row_ptr = m->row_ptr;
+        b.packed_row_ptr = m->packed_row_ptr;
+        b.col_idx = m->col_idx;
+        b.packed = m->packed_values;
+        b.rows = m->rows;
+        b.rows_ld = L.rows_ld;
+        b.head = head_cols;
+        b.codes = L.codes;
+        b.masks = L.masks;
+        b.head_end = L.head_end;
+        b.error = words + 2;
+        const dim3 grid(L.rows_ld / 256u), block(256);
+        switch (m->bits) {
+        case 1: hipLaunchKernelGGL(dense_head_build<1>, grid, block, 0, s, b); break;
+        case 2: hipLaunchKernelGGL(dense_head_build<2>, grid, block, 0, s, b); break;
+        case 4: hipLaunchKernelGGL(dense_head_build<4>, grid, block, 0, s, b); break;
+        default: hipLaunchKernelGGL(dense_head_build<8>, grid, block, 0, s, b); break;
+        }
+    }
+    rc = check_launch("cx_qcsr_hybrid_prepare");
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    std::uint32_t host[4] = {0u, 0u, 0u, 0u};
+    hipError_t e = hipMemcpyAsync(host, words, sizeof(host), hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
-    (void)hipFree(words);
     if (e != hipSuccess) return hip_fail(e, "cx_qcsr_hybrid_prepare");
+    if (host[2] != 0u)
+        return fail(CX_STATUS_INVALID_ARGUMENT,
+                    "cx_qcsr_hybrid_prepare: a row's genes are not strictly increasing despite CX_QCSR_COLUMNS_SORTED");
     float bound, roff;
     std::memcpy(&bound, &host[0], 4);
     std::memcpy(&roff, &host[1], 4);
-    if (!(bound + roff < kHeadValueLimit))
-        return fail(CX_STATUS_UNSUPPORTED,
-                    "cx_qcsr_hybrid_prepare: head genes decode to |x| >= 2^15, outside the exact fp16 split");
-    // the panel is a 16-bit word permutation ([head/32][out_cols][32]); the Blocked-ELL packer
-    // moves fp16 words as well as bf16
-    rc = cx_bell_pack_rhs(rhs_f16, rhs_ld, head_cols, out_cols, head_panel, stream);
-    return rc;
+    const float total = bound + roff;
+    if (!(total < 3.0e38f))
+        return fail(CX_STATUS_UNSUPPORTED, "cx_qcsr_hybrid_prepare: head metadata is not finite");
+    // k = 14 - floor(log2 B): every |x'| = 2^k |x| stays below 2^15
+    int k = 0;
+    if (total > 0.0f) {
+        int ex = 0;
+        (void)std::frexp(total, &ex);  // total = f 2^ex, f in [0.5, 1): floor(log2) = ex - 1
+        k = 14 - (ex - 1);
+    }
+    k = std::max(-100, std::min(100, k));
+    L.scale_exp = k;
+    const std::uint32_t n = std::max(head_cols, L.row_offsets != nullptr ? m->rows : 0u);
+    if (n != 0u) {
+        hipLaunchKernelGGL(scale_meta_kernel, dim3((n + 255u) / 256u), dim3(256), 0, s, m->column_scales,
+                           m->column_offsets, m->row_offsets, m->decode_policy, head_cols, m->rows,
+                           std::ldexp(1.0f, k), reinterpret_cast<float2 *>(L.meta), L.row_offsets);
+        rc = check_launch("cx_qcsr_hybrid_prepare");
+        if (rc != CX_STATUS_SUCCESS) return rc;
+    }
+    *layout = L;
+    return CX_STATUS_SUCCESS;
 }
 
-extern "C" int cx_qcsr_hybrid_workspace(const cx_qcsr_matrix *m, uint64_t *bytes) {
+extern "C" int cx_qcsr_hybrid_workspace(const cx_qcsr_matrix *m, uint32_t head_cols, int64_t out_cols,
+                                        uint64_t *bytes) {
     using namespace cx;
     clear_error();
     if (m == nullptr || bytes == nullptr)
         return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_hybrid_workspace: null argument");
-    const std::uint64_t partial = (static_cast<std::uint64_t>(m->rows) * 64u * 4u + 255u) & ~std::uint64_t{255u};
-    *bytes = partial + static_cast<std::uint64_t>(m->rows) * 4u;
+    if (out_cols <= 0 || out_cols % 64 != 0 || out_cols > 256)
+        return fail(CX_STATUS_INVALID_SHAPE, "cx_qcsr_hybrid_workspace: out_cols must be 64, 128, 192 or 256");
+    const std::uint64_t partial = align256(static_cast<std::uint64_t>(m->rows) * 64u * 4u);
+    const std::uint64_t panel = align256(static_cast<std::uint64_t>(head_cols) * static_cast<std::uint64_t>(out_cols) * 2u);
+    *bytes = partial + panel;
     return CX_STATUS_SUCCESS;
 }
 
-extern "C" int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *m, uint32_t head_cols, const uint16_t *head_panel,
+extern "C" int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *m, const cx_qcsr_hybrid_layout *layout,
                                        const void *rhs, int64_t rhs_ld, int64_t out_cols, float *out,
                                        int64_t out_ld, const cx_spmm_epilogue *epilogue, void *workspace,
                                        uint64_t workspace_bytes, void *stream) {
     using namespace cx;
     clear_error();
-    int rc = validate_hybrid(m, head_cols, "cx_qcsr_spmm_fwd_hybrid: null matrix");
+    if (layout == nullptr) return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd_hybrid: null layout");
+    const cx_qcsr_hybrid_layout &L = *layout;
+    int rc = validate_hybrid(m, L.head_cols, "cx_qcsr_spmm_fwd_hybrid: null matrix");
     if (rc != CX_STATUS_SUCCESS) return rc;
+    if (L.rows != m->rows || L.bits != m->bits || L.decode_policy != m->decode_policy || L.nnz != m->nnz
+        || L.rows_ld != layout_sizes(m, L.head_cols).rows_ld
+        || (L.head_cols != 0u && (L.codes == nullptr || L.masks == nullptr || L.head_end == nullptr || L.meta == nullptr)))
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd_hybrid: the layout was not prepared for this matrix");
     if (rhs == nullptr || out == nullptr)
         return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd_hybrid: null rhs or output");
     if (out_cols <= 0 || out_cols % 64 != 0 || out_cols > 256 || rhs_ld < out_cols || out_ld < out_cols)
         return fail(CX_STATUS_INVALID_SHAPE, "cx_qcsr_spmm_fwd_hybrid: out_cols must be 64, 128, 192 or 256");
-    if ((m->flags & CX_QCSR_COLUMNS_SORTED) == 0u)
-        return fail(CX_STATUS_INVALID_ARGUMENT,
-                    "cx_qcsr_spmm_fwd_hybrid: rows must be sorted (CX_QCSR_COLUMNS_SORTED, e.g. from cx_qcsr_to_execution_order)");
     const bool aligned = (reinterpret_cast<std::uintptr_t>(rhs) & 15u) == 0u
         && (reinterpret_cast<std::uintptr_t>(out) & 15u) == 0u && (rhs_ld * 2) % 16 == 0 && (out_ld * 4) % 16 == 0;
-    if (!aligned || m->cols > static_cast<std::uint32_t>(INT32_MAX) || rhs_ld > (INT32_MAX / 2) / 1024)
+    if (!aligned || rhs_ld > (INT32_MAX / 2) / 1024)
         return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd_hybrid: rhs and output must be 16-byte aligned");
-    if (m->nnz > static_cast<std::uint64_t>(INT32_MAX))
-        return fail(CX_STATUS_INVALID_SHAPE, "cx_qcsr_spmm_fwd_hybrid: nnz exceeds int32 row offsets");
     if (static_cast<const void *>(out) == rhs)
         return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd_hybrid: output aliases the rhs");
     if (m->rows == 0u) return CX_STATUS_SUCCESS;
@@ -446,11 +601,11 @@ extern "C" int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *m, uint32_t head_co
     rc = make_epilogue(epilogue, m->rows, out_cols, out, out_ld, &ep, "cx_qcsr_spmm_fwd_hybrid");
     if (rc != CX_STATUS_SUCCESS) return rc;
     std::uint64_t need = 0u;
-    (void)cx_qcsr_hybrid_workspace(m, &need);
-    if (head_cols != 0u && (workspace == nullptr || workspace_bytes < need || head_panel == nullptr
-                            || (reinterpret_cast<std::uintptr_t>(workspace) & 255u) != 0u))
+    (void)cx_qcsr_hybrid_workspace(m, L.head_cols, out_cols, &need);
+    if (L.head_cols != 0u && (workspace == nullptr || workspace_bytes < need
+                              || (reinterpret_cast<std::uintptr_t>(workspace) & 255u) != 0u))
         return fail(CX_STATUS_INVALID_ARGUMENT,
-                    "cx_qcsr_spmm_fwd_hybrid: needs the head panel and a 256-byte aligned workspace of cx_qcsr_hybrid_workspace bytes");
+                    "cx_qcsr_spmm_fwd_hybrid: needs a 256-byte aligned workspace of cx_qcsr_hybrid_workspace bytes");
     QcsrArgs a{};
     a.ep = ep;
     a.row_ptr = m->row_ptr;
@@ -468,22 +623,25 @@ extern "C" int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *m, uint32_t head_co
     a.cols = m->cols;
     a.flags = m->flags;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (head_cols == 0u) return launch_qcsr_parts(a, m->bits, m->decode_policy, out_cols, s);
+    if (L.head_cols == 0u) return launch_qcsr_parts(a, m->bits, m->decode_policy, out_cols, s);
     auto *partial = static_cast<float *>(workspace);
-    const std::uint64_t partial_bytes = (static_cast<std::uint64_t>(m->rows) * 64u * 4u + 255u) & ~std::uint64_t{255u};
-    auto *head_end = reinterpret_cast<std::int32_t *>(static_cast<unsigned char *>(workspace) + partial_bytes);
+    auto *panel = reinterpret_cast<std::uint16_t *>(static_cast<unsigned char *>(workspace)
+                                                    + align256(static_cast<std::uint64_t>(m->rows) * 256u));
+    // the head genes' weights as the matrix-core operand panel [H/32][out_cols][32]
+    rc = cx_bell_pack_rhs(static_cast<const std::uint16_t *>(rhs), rhs_ld, L.head_cols,
+                          static_cast<std::uint32_t>(out_cols), panel, stream);
+    if (rc != CX_STATUS_SUCCESS) return rc;
     for (std::int64_t c0 = 0; c0 < out_cols; c0 += 64) {
-        QcsrArgs b = a;
-        rc = launch_qcsr_head(b, m->bits, m->decode_policy, head_cols, head_panel + c0 * 32,
-                              static_cast<std::uint32_t>(out_cols), partial, head_end, s);
+        rc = launch_head(L, panel + c0 * 32, static_cast<std::uint32_t>(out_cols), partial, s);
         if (rc != CX_STATUS_SUCCESS) return rc;
+        QcsrArgs b = a;
         b.rhs = static_cast<const std::uint16_t *>(rhs) + c0;
         b.out = out + c0;
         if (b.ep.bias != nullptr) b.ep.bias += c0;
         if (b.ep.initial != nullptr) b.ep.initial += c0;
-        b.row_start = head_end;
+        b.row_start = L.head_end;
         b.acc_init = partial;
-        b.first_part = head_cols / 1024u;
+        b.first_part = L.head_cols / kHeadAlign;
         rc = launch_qcsr_parts(b, m->bits, m->decode_policy, 64, s);
         if (rc != CX_STATUS_SUCCESS) return rc;
     }

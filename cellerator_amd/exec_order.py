@@ -115,51 +115,83 @@ def to_execution_order(m: QcsrMatrix, order: ExecutionOrder, stream=None) -> Qcs
 
 @dataclasses.dataclass
 class HybridProjection:
-    """A quantized CSR in execution order prepared for cx_qcsr_spmm_fwd_hybrid: the packed
-    weights of its first head_cols genes (a multiple of 1,024) and the workspace of the head's
-    partial sums. Built once per matrix and weight generation by hybrid_prepare."""
+    """A quantized CSR in execution order prepared for cx_qcsr_spmm_fwd_hybrid: the dense
+    copy of its first head_cols genes (codes and presence bits; head_cols a multiple of
+    1,024), each row's first tail entry, and the pre-scaled head metadata. Built once per
+    matrix by hybrid_prepare; independent of the weights."""
     matrix: QcsrMatrix
     head_cols: int
-    panel: Optional[torch.Tensor]
-    workspace: Optional[torch.Tensor]
-    out_cols: int
+    layout: N.CxQcsrHybridLayout
+    storage: Optional[torch.Tensor]
+    workspaces: dict = dataclasses.field(default_factory=dict)
+
+    @property
+    def scale_exp(self) -> int:
+        return int(self.layout.scale_exp)
+
+    def workspace(self, out_cols: int, device) -> torch.Tensor:
+        ws = self.workspaces.get(out_cols)
+        if ws is None:
+            nbytes = C.c_uint64()
+            d = self.matrix.descriptor()
+            N.check("cx_qcsr_hybrid_workspace", N.engine().cx_qcsr_hybrid_workspace(
+                C.byref(d), self.head_cols, out_cols, C.byref(nbytes)))
+            ws = torch.empty(max(nbytes.value, 256), dtype=torch.uint8, device=device)
+            self.workspaces[out_cols] = ws
+        return ws
 
 
-def hybrid_prepare(m: QcsrMatrix, w: torch.Tensor, head_cols: int, stream=None) -> HybridProjection:
-    """m in execution order (sorted rows), w = the execution-order weights (F16 [genes, N],
-    N a multiple of 64). Raises if the head genes decode outside the exact fp16 split."""
-    _require_cuda(m.row_ptr, w)
-    if w.dtype != torch.float16 or w.dim() != 2 or w.stride(1) != 1 or w.shape[0] != m.cols:
-        raise ValueError("w must be a row-major F16 [genes, N] tensor")
-    n = int(w.shape[1])
+def hybrid_prepare(m: QcsrMatrix, head_cols: int, stream=None) -> HybridProjection:
+    """m in execution order (sorted rows, flags QCSR_COLUMNS_SORTED). Raises if a row's genes
+    are not strictly increasing or the head metadata is not finite."""
+    _require_cuda(m.row_ptr)
     lib = N.engine()
     d = m.descriptor()
-    panel = None
-    if head_cols:
-        panel = torch.empty((head_cols // 32) * n * 32, dtype=torch.float16, device=w.device)
-        N.check("cx_qcsr_hybrid_prepare", lib.cx_qcsr_hybrid_prepare(
-            C.byref(d), head_cols, w.data_ptr(), w.stride(0), n, panel.data_ptr(), _stream(stream)))
     nbytes = C.c_uint64()
-    N.check("cx_qcsr_hybrid_workspace", lib.cx_qcsr_hybrid_workspace(C.byref(d), C.byref(nbytes)))
-    ws = torch.empty(max(nbytes.value, 256), dtype=torch.uint8, device=w.device) if head_cols else None
-    return HybridProjection(m, head_cols, panel, ws, n)
+    N.check("cx_qcsr_hybrid_layout_bytes", lib.cx_qcsr_hybrid_layout_bytes(C.byref(d), head_cols, C.byref(nbytes)))
+    storage = torch.empty(max(nbytes.value, 256), dtype=torch.uint8, device=m.row_ptr.device)
+    layout = N.CxQcsrHybridLayout()
+    N.check("cx_qcsr_hybrid_prepare", lib.cx_qcsr_hybrid_prepare(
+        C.byref(d), head_cols, storage.data_ptr(), storage.numel(), C.byref(layout), _stream(stream)))
+    return HybridProjection(m, head_cols, layout, storage)
+
+
+def hybrid_head_arrays(p: HybridProjection):
+    """(codes, masks, head_end, meta) of the prepared layout as device tensor views:
+    codes [H * bits / 32, rows_ld] and masks [H / 32, rows_ld] int32 (u32 bits),
+    head_end [rows] int32, meta [H, 2] float32 (times 2^scale_exp)."""
+    L, base = p.layout, p.storage.data_ptr()
+
+    def view(ptr, count, dtype, shape):
+        off = ptr - base
+        size = torch.tensor([], dtype=dtype).element_size()
+        return p.storage[off:off + count * size].view(dtype).view(shape)
+
+    h, ld = p.head_cols, int(L.rows_ld)
+    codes = view(L.codes, h * L.bits // 32 * ld, torch.int32, (h * L.bits // 32, ld))
+    masks = view(L.masks, h // 32 * ld, torch.int32, (h // 32, ld))
+    head_end = view(L.head_end, int(L.rows), torch.int32, (int(L.rows),))
+    meta = view(L.meta, 2 * h, torch.float32, (h, 2))
+    return codes, masks, head_end, meta
 
 
 def hybrid_spmm(p: HybridProjection, w: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None,
                 epilogue=None) -> torch.Tensor:
-    """Y = X . W (+ epilogue) on the prepared execution-order projection; Y rows are the
-    matrix's rows (cells keep their order), columns the weights' columns."""
+    """Y = X . W (+ epilogue) on the prepared execution-order projection; w = the
+    execution-order weights (F16 [genes, N], N in 64..256 by 64). Y rows are the matrix's
+    rows (cells keep their order), columns the weights' columns."""
     m = p.matrix
     _require_cuda(w)
-    if w.shape != (m.cols, p.out_cols) or w.dtype != torch.float16 or w.stride(1) != 1:
-        raise ValueError("w must be the F16 [genes, N] weights the projection was prepared with")
+    if w.dim() != 2 or w.shape[0] != m.cols or w.dtype != torch.float16 or w.stride(1) != 1:
+        raise ValueError("w must be a row-major F16 [genes, N] tensor")
+    n = int(w.shape[1])
     if out is None:
-        out = torch.empty((m.rows, p.out_cols), dtype=torch.float32, device=w.device)
+        out = torch.empty((m.rows, n), dtype=torch.float32, device=w.device)
     d = m.descriptor()
     e = epilogue.descriptor(out) if epilogue is not None else None
-    ws = p.workspace
+    ws = p.workspace(n, w.device) if p.head_cols else None
     N.check("cx_qcsr_spmm_fwd_hybrid", N.engine().cx_qcsr_spmm_fwd_hybrid(
-        C.byref(d), p.head_cols, p.panel.data_ptr() if p.panel is not None else None, w.data_ptr(),
-        w.stride(0), p.out_cols, out.data_ptr(), out.stride(0), C.byref(e) if e is not None else None,
-        ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, _stream(stream)))
+        C.byref(d), C.byref(p.layout), w.data_ptr(), w.stride(0), n, out.data_ptr(), out.stride(0),
+        C.byref(e) if e is not None else None, ws.data_ptr() if ws is not None else None,
+        ws.numel() if ws is not None else 0, _stream(stream)))
     return out

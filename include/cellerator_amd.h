@@ -783,31 +783,50 @@ const char *cx_exec_last_error(void);
  * For a matrix in an execution order whose first head_cols genes are the most frequently
  * stored ones (cx_popularity_order + cx_qcsr_to_execution_order), the product splits into
  * Y = X[:, 0:H) . W[0:H, :] + X[:, H:) . W[H:, :]. The head runs on v_mfma_f32_16x16x32_f16
- * over dense 16-row tiles: every code is decoded exactly as the reference codec does
- * (fma(code, scale, offset), include/Cellerator/quantized/access.cuh:81-91) and split into
- * three fp16 parts whose sum is the decoded value (exact for |x| in [2^-2, 2^15); below,
- * an absolute error under 2^-25 |w|), so each product is exact in fp32 and only the fp32
- * summation order differs from the plain kernel. The tail runs on the row-group VALU kernel
- * from each row's first entry >= H, adds the head's partial sums and applies the epilogue.
+ * over a dense copy of X[:, 0:H) (codes and presence bits, built once per matrix): every
+ * code is decoded exactly as the reference codec does (fma(code, scale, offset),
+ * include/Cellerator/quantized/access.cuh:81-91), scaled by a power of two 2^k and split
+ * into three fp16 parts whose sum is the scaled value (exact for |x| >= 2^(9-k); below,
+ * only bits under 2^(-14-k) can be lost), so each product is exact in fp32 and only the
+ * fp32 summation order differs from the plain kernel. The tail runs on the row-group VALU
+ * kernel from each row's first entry >= H, adds the head's sums and applies the epilogue.
  * W is F16 (the execution-order packed dense operand). Engine addition; the reference's
  * projection has no matrix-core path for CSR. */
+typedef struct cx_qcsr_hybrid_layout {
+    uint32_t head_cols;     /* H, a multiple of 1,024 (0: no head) */
+    uint32_t rows;
+    uint32_t rows_ld;       /* rows rounded up to 256: the row stride of codes and masks */
+    uint32_t bits;
+    uint32_t decode_policy;
+    int32_t scale_exp;      /* k: meta and row_offsets hold values times 2^k */
+    uint64_t nnz;           /* of the matrix it was built from */
+    uint32_t *codes;        /* [H * bits / 32][rows_ld]: word w of a row = codes of genes
+                               [w * 32 / bits, (w + 1) * 32 / bits), 0 where not stored */
+    uint32_t *masks;        /* [H / 32][rows_ld]: presence bit of gene g at bit g % 32 */
+    int32_t *head_end;      /* [rows]: first entry of each row with gene >= H */
+    float *meta;            /* [H] (scale, offset) pairs times 2^k */
+    float *row_offsets;     /* [rows] times 2^k (column-scale / row-offset policy), else NULL */
+} cx_qcsr_hybrid_layout;
 
-/* Checks that every code of the first head_cols genes decodes to |x| < 2^15 (UNSUPPORTED
- * otherwise) and packs those genes' weights (F16 [cols x out_cols], row stride rhs_ld) into
- * head_panel ([head_cols/32][out_cols][32] F16). head_cols a multiple of 1,024 (0: nothing to
- * do). Once per weight generation; allocates one 8-byte word and synchronizes `stream`. */
-int cx_qcsr_hybrid_prepare(const cx_qcsr_matrix *a, uint32_t head_cols, const uint16_t *rhs_f16,
-                           int64_t rhs_ld, uint32_t out_cols, uint16_t *head_panel, void *stream);
-/* Workspace bytes of cx_qcsr_spmm_fwd_hybrid: the head's partial sums (rows x 64 fp32, 256-byte
- * aligned) and each row's first tail entry (rows int32). */
-int cx_qcsr_hybrid_workspace(const cx_qcsr_matrix *a, uint64_t *bytes);
+/* Device bytes of the head layout of `a` (a.flags must include CX_QCSR_COLUMNS_SORTED). */
+int cx_qcsr_hybrid_layout_bytes(const cx_qcsr_matrix *a, uint32_t head_cols, uint64_t *bytes);
+/* Builds the head layout into `storage` (256-byte aligned, cx_qcsr_hybrid_layout_bytes) and
+ * fills *layout with its pointers and k. Once per matrix; synchronizes `stream`. Rejects
+ * rows whose genes are not strictly increasing (INVALID_ARGUMENT) and non-finite metadata
+ * (UNSUPPORTED). */
+int cx_qcsr_hybrid_prepare(const cx_qcsr_matrix *a, uint32_t head_cols, void *storage, uint64_t storage_bytes,
+                           cx_qcsr_hybrid_layout *layout, void *stream);
+/* Workspace bytes of cx_qcsr_spmm_fwd_hybrid: the head's sums (rows x 64 fp32) and the head
+ * genes' weight panel ([H/32][out_cols][32] F16), each 256-byte aligned. */
+int cx_qcsr_hybrid_workspace(const cx_qcsr_matrix *a, uint32_t head_cols, int64_t out_cols, uint64_t *bytes);
 /* Y = act(alpha * (A . W) + beta * C + bias) for A in execution order with a.flags including
- * CX_QCSR_COLUMNS_SORTED, codes of 1/2/4/8 bits (any decode policy), F16 W, out_cols 64..256
- * in steps of 64 (one head and one tail launch per 64 columns), 16-byte aligned operands.
+ * CX_QCSR_COLUMNS_SORTED, codes of 1/2/4/8 bits (any decode policy), F16 W [cols x out_cols]
+ * (row stride rhs_ld), out_cols 64..256 in steps of 64 (one head and one tail launch per 64
+ * columns), 16-byte aligned operands, `layout` from cx_qcsr_hybrid_prepare on this matrix.
  * head_cols == 0 runs the plain row-group kernel. workspace: 256-byte aligned,
  * cx_qcsr_hybrid_workspace bytes. Deterministic. */
-int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *a, uint32_t head_cols, const uint16_t *head_panel,
-                            const void *rhs, int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
+int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *a, const cx_qcsr_hybrid_layout *layout, const void *rhs,
+                            int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
                             const cx_spmm_epilogue *epilogue, void *workspace, uint64_t workspace_bytes,
                             void *stream);
 

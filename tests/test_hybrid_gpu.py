@@ -1,9 +1,11 @@
 """GPU parity of the execution-order quantized CSR SpMM with a matrix-core head
-(cx_qcsr_spmm_fwd_hybrid, qcsr_hybrid.hip): the head's three-part fp16 split reproduces
-every decoded value exactly (an identity weight panel), and the product over random and
-C3-generated matrices -- every code width and decode policy, N = 64 and 128, fused
-epilogues, ragged workgroups, empty rows and rows wholly inside or outside the head --
-matches the float64 referee of the canonical matrix. Repeats are bitwise equal."""
+(cx_qcsr_spmm_fwd_hybrid, qcsr_hybrid.hip): the dense head layout is bit-exact against a
+numpy restatement of its definition (codes, presence bits, tail starts, 2^k-scaled
+metadata), the head's three-part fp16 split reproduces every decoded value exactly (an
+identity weight panel), and the product over random and C3-generated matrices -- every
+code width and decode policy, N = 64 and 128, fused epilogues, ragged workgroups, empty
+rows and rows wholly inside or outside the head -- matches the float64 referee of the
+canonical matrix. Repeats are bitwise equal."""
 from __future__ import annotations
 
 import numpy as np
@@ -60,7 +62,7 @@ def test_hybrid_matches_referee(oracle, bits, policy):
     mx, order = _exec(m)
     w = (rng.standard_normal((3100, 64)) * 0.02).astype(np.float16)
     wx = pack_rows(order, torch.from_numpy(w).cuda())
-    p = hybrid_prepare(mx, wx, 2048)
+    p = hybrid_prepare(mx, 2048)
     y = hybrid_spmm(p, wx)
     y2 = hybrid_spmm(p, wx)
     torch.cuda.synchronize()
@@ -72,7 +74,7 @@ def test_hybrid_matches_referee(oracle, bits, policy):
 def test_identity_panel_gives_exact_decoded_values(oracle):
     """W = the identity on the first 64 execution genes: Y[r, c] is the decoded value of
     (r, gene c), through the head's split and the tail's (zero) sum -- bitwise for
-    |x| >= 2^-2 and within 2^-24 below."""
+    |x| >= 2^(9-k) and within 2^(-13-k) below (k = the layout's scale exponent)."""
     import torch
 
     from cellerator_amd.exec_order import hybrid_prepare, hybrid_spmm
@@ -81,7 +83,8 @@ def test_identity_panel_gives_exact_decoded_values(oracle):
     mx, order = _exec(to_device_qcsr(fx))
     w = torch.zeros((2100, 64), dtype=torch.float16, device="cuda")
     w[torch.arange(64), torch.arange(64)] = 1.0
-    y = hybrid_spmm(hybrid_prepare(mx, w, 1024), w)
+    p = hybrid_prepare(mx, 1024)
+    y = hybrid_spmm(p, w)
     torch.cuda.synchronize()
     h = qcsr_to_host(mx)
     decoded = oracle.decode_csr(4, 1, h["row_ptr"], h["packed_row_ptr"], h["col_idx"], h["packed"],
@@ -91,9 +94,74 @@ def test_identity_panel_gives_exact_decoded_values(oracle):
     sel = h["col_idx"] < 64
     want[rows[sel], h["col_idx"][sel]] = decoded[sel]
     got = y.cpu().numpy()
-    big = np.abs(want) >= 0.25
+    k = p.scale_exp
+    big = np.abs(want) >= 2.0 ** (9 - k)
+    assert big.sum() > 1000
     assert np.array_equal(got[big].view(np.uint32), want[big].view(np.uint32))
-    assert np.all(np.abs(got[~big] - want[~big]) <= 2.0 ** -24)
+    assert np.all(np.abs(got[~big] - want[~big]) <= 2.0 ** (-13 - k))
+
+
+def _layout_reference(h, head, rows_ld):
+    """The dense head layout by its definition, from the host CSR (sorted rows)."""
+    bits, rows = h["bits"], len(h["row_ptr"]) - 1
+    per_word = 32 // bits
+    codes = np.zeros((head * bits // 32, rows_ld), np.uint32)
+    masks = np.zeros((head // 32, rows_ld), np.uint32)
+    head_end = np.zeros(rows, np.int32)
+    packed = h["packed"]
+    for r in range(rows):
+        b, e = int(h["row_ptr"][r]), int(h["row_ptr"][r + 1])
+        pbit = int(h["packed_row_ptr"][r]) * 8
+        i = b
+        while i < e and h["col_idx"][i] < head:
+            g = int(h["col_idx"][i])
+            bit = pbit + (i - b) * bits
+            code = (int(packed[bit >> 3]) >> (bit & 7)) & ((1 << bits) - 1)
+            codes[g // per_word, r] |= np.uint32(code << ((g % per_word) * bits))
+            masks[g // 32, r] |= np.uint32(1 << (g % 32))
+            i += 1
+        head_end[r] = i
+    return codes, masks, head_end
+
+
+@pytest.mark.parametrize("bits,policy", [(4, 1), (8, 3), (2, 2), (1, 1)])
+def test_dense_head_layout_is_bit_exact(oracle, bits, policy):
+    import torch
+
+    from cellerator_amd import qcsr_pack_gene_affine
+    from cellerator_amd.exec_order import hybrid_head_arrays, hybrid_prepare
+    rng = np.random.default_rng(700 + bits)
+    fx = _skewed(oracle, rng, 300, 2500, bits, policy)
+    m = to_device_qcsr(fx)
+    if policy == 3:
+        m = qcsr_pack_gene_affine(m)
+    mx, _ = _exec(m)
+    p = hybrid_prepare(mx, 2048)
+    codes, masks, head_end, meta = hybrid_head_arrays(p)
+    torch.cuda.synchronize()
+    h = qcsr_to_host(mx)
+    want_codes, want_masks, want_end = _layout_reference(h, 2048, int(p.layout.rows_ld))
+    assert np.array_equal(codes.cpu().numpy().view(np.uint32), want_codes)
+    assert np.array_equal(masks.cpu().numpy().view(np.uint32), want_masks)
+    assert np.array_equal(head_end.cpu().numpy(), want_end)
+    # scale exponent and metadata: k = 14 - floor(log2 B), B = largest |decoded value| of a head code
+    if policy == 3:
+        pairs = h["scales"].reshape(-1, 2)
+        s, o = pairs[:2048, 0].astype(np.float64), pairs[:2048, 1].astype(np.float64)
+    else:
+        s = h["scales"][:2048].astype(np.float64)
+        o = h["offsets"][:2048].astype(np.float64) if policy == 1 else np.zeros(2048)
+    qmax = (1 << bits) - 1
+    if policy == 2:
+        bound = np.float32(np.max(np.abs(s) * qmax)) + np.float32(np.max(np.abs(h["row_offsets"])))
+    else:
+        bound = np.max(np.maximum(np.abs(o), np.abs(o + qmax * s)))
+    k = 14 - int(np.floor(np.log2(bound)))
+    assert p.scale_exp == k
+    got_meta = meta.cpu().numpy()
+    assert np.array_equal(got_meta[:, 0], (s * 2.0 ** k).astype(np.float32))
+    if policy != 2:
+        assert np.array_equal(got_meta[:, 1], (o * 2.0 ** k).astype(np.float32))
 
 
 @pytest.mark.parametrize("n,kind,beta", [(128, 0, 0.0), (64, 6, 0.5), (128, 2, -1.0)])
@@ -112,7 +180,7 @@ def test_hybrid_epilogue_and_wide_outputs(oracle, n, kind, beta):
     y = torch.from_numpy(c0.copy()).cuda()
     ep = Epilogue(kind, 1.5, beta, torch.from_numpy(bias).cuda() if kind in (1, 5, 6, 7) else None,
                   y if beta != 0.0 else None)
-    hybrid_spmm(hybrid_prepare(mx, wx, 2048), wx, out=y, epilogue=ep)
+    hybrid_spmm(hybrid_prepare(mx, 2048), wx, out=y, epilogue=ep)
     torch.cuda.synchronize()
     decoded = oracle.decode_csr(4, 1, fx["row_ptr"], fx["packed_row_ptr"], fx["col_idx"], fx["packed"],
                                 fx["scales"], fx["offsets"], None)
@@ -136,7 +204,7 @@ def test_hybrid_on_c3_rows(oracle):
     w = dense_normal((m.cols, 64), 0.02, torch.float16, seed=3)
     mx, order = _exec(qcsr_pack_gene_affine(m))
     wx = pack_rows(order, w)
-    y = hybrid_spmm(hybrid_prepare(mx, wx, 4096), wx)
+    y = hybrid_spmm(hybrid_prepare(mx, 4096), wx)
     torch.cuda.synchronize()
     h = qcsr_to_host(m)
     ref, mag = oracle.qcsr_spmm_referee(4, 1, m.rows, m.cols, h["row_ptr"], h["packed_row_ptr"], h["col_idx"],
@@ -144,7 +212,7 @@ def test_hybrid_on_c3_rows(oracle):
     check_against_referee(oracle, ref, mag, y.cpu().numpy())
 
 
-def test_hybrid_rejects_unsorted_and_out_of_range_heads(oracle):
+def test_hybrid_rejects_unsorted_rows_and_bad_metadata(oracle):
     import torch
 
     from cellerator_amd import _native as N
@@ -152,12 +220,36 @@ def test_hybrid_rejects_unsorted_and_out_of_range_heads(oracle):
     rng = np.random.default_rng(9)
     fx = _skewed(oracle, rng, 300, 2100, 4, 1)
     m = to_device_qcsr(fx)  # canonical order, flags 0
-    w = torch.zeros((2100, 64), dtype=torch.float16, device="cuda")
-    p = hybrid_prepare(m, w, 1024)
     with pytest.raises(N.EngineError, match="sorted"):
-        hybrid_spmm(p, w)
+        hybrid_prepare(m, 1024)
+    m.flags = N.QCSR_COLUMNS_SORTED
     with pytest.raises(N.EngineError, match="1,024"):
-        hybrid_prepare(m, w, 1000)
-    big = to_device_qcsr(dict(fx, offsets=(fx["offsets"] + 40000.0).astype(np.float32)))
-    with pytest.raises(N.EngineError, match="2\\^15"):
-        hybrid_prepare(big, w, 1024)
+        hybrid_prepare(m, 1000)
+    # a promise the rows break: two entries of row 7 swapped
+    bad = dict(fx)
+    col = fx["col_idx"].copy()
+    b = int(fx["row_ptr"][7])
+    assert fx["row_ptr"][8] - b >= 2
+    col[b], col[b + 1] = col[b + 1], col[b]
+    mb = to_device_qcsr(dict(bad, col_idx=col))
+    mb.flags = N.QCSR_COLUMNS_SORTED
+    with pytest.raises(N.EngineError, match="strictly increasing"):
+        hybrid_prepare(mb, 1024)
+    nan_meta = fx["scales"].copy()
+    nan_meta[3] = np.nan
+    mn = to_device_qcsr(dict(fx, scales=nan_meta))
+    mn.flags = N.QCSR_COLUMNS_SORTED
+    with pytest.raises(N.EngineError, match="finite"):
+        hybrid_prepare(mn, 1024)
+    # a layout used with another matrix
+    p = hybrid_prepare(m, 1024)
+    other = to_device_qcsr(_skewed(oracle, np.random.default_rng(10), 301, 2100, 4, 1))
+    other.flags = N.QCSR_COLUMNS_SORTED
+    w = torch.zeros((2100, 64), dtype=torch.float16, device="cuda")
+    with pytest.raises(N.EngineError, match="not prepared for this matrix"):
+        hybrid_spmm(dataclasses_replace(p, matrix=other), w)
+
+
+def dataclasses_replace(obj, **kw):
+    import dataclasses
+    return dataclasses.replace(obj, **kw)
