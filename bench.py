@@ -125,13 +125,21 @@ def cpu_baseline_qcsr(m, w, out, sample_rows: int, threads: int) -> tuple[dict, 
                       f"oracle or_qcsr_spmm_f32_mt (decode + fp32 FMA, AVX2, row-parallel)",
             "seconds": t, "host": host_description()}
     mag = pyoracle.qcsr_spmm_f32_mt(*args, threads=threads, magnitude=True)
+    return base, (rows, cpu_out, mag)
+
+
+def full_output_check(out, cpu) -> dict:
+    """The GPU's timed output against the CPU product on the CPU leg's rows: both fp32, only
+    the summation order differs, so |gpu - cpu| <= 1e-4 + 1e-4 |cpu| + 2^-20 Sigma |x||w|."""
+    import numpy as np
+
+    rows, cpu_out, mag = cpu
     got = out[:rows].cpu().numpy()
     err = np.abs(got.astype(np.float64) - cpu_out)
     bound = 1e-4 + 1e-4 * np.abs(cpu_out) + 2.0 ** -20 * mag
-    check = {"rows": rows, "elements": int(got.size), "mismatches": int((err > bound).sum()),
-             "max_abs_err": float(err.max()) if got.size else 0.0,
-             "rule": "|gpu - cpu_fp32| <= 1e-4 + 1e-4 |cpu| + 2^-20 sum |x||w|"}
-    return base, check
+    return {"rows": rows, "elements": int(got.size), "mismatches": int((err > bound).sum()),
+            "max_abs_err": float(err.max()) if got.size else 0.0,
+            "rule": "|gpu - cpu_fp32| <= 1e-4 + 1e-4 |cpu| + 2^-20 sum |x||w|"}
 
 
 def bench_qcsr(args, torch, cfg, n_out: int) -> dict:
@@ -184,11 +192,50 @@ def bench_qcsr(args, torch, cfg, n_out: int) -> dict:
                      "fp32_fma_tflops": flops / (kern_ms * 1e-3) / 1e12,
                      "valu_fp32_peak_tflops_nonpacked": 78.6},
     }
+    hybrid = None
+    if args.head and m.bits and n_out % 64 == 0 and n_out <= 256:
+        hybrid, hyb_out = bench_qcsr_hybrid(args, torch, mt, w, n_out, stream)
     if not args.no_cpu:
-        res["cpu_baseline"], res["full_output_check"] = cpu_baseline_qcsr(
-            m, w, out, args.cpu_rows, host_cores())
+        res["cpu_baseline"], cpu = cpu_baseline_qcsr(m, w, out, args.cpu_rows, host_cores())
+        res["full_output_check"] = full_output_check(out, cpu)
+        if hybrid is not None:
+            hybrid["full_output_check"] = full_output_check(hyb_out, cpu)
     res["parity_sample"] = parity_sample_qcsr(m, w, out, 2000, seed=cfg.seed)
+    if hybrid is not None:
+        hybrid["parity_sample"] = parity_sample_qcsr(m, w, hyb_out, 2000, seed=cfg.seed)
+        res["execution_order_hybrid"] = hybrid
     return res
+
+
+def bench_qcsr_hybrid(args, torch, mt, w, n_out: int, stream):
+    """The same product on the execution-order layout (cx_qcsr_spmm_fwd_hybrid): genes
+    relabelled by popularity, the first --head genes as a dense code plane on the matrix
+    cores, the rest on the row-group kernel. The layout and the reordered weights are built
+    once (untimed, reported as prepare_ms); output rows are the same cells."""
+    from cellerator_amd.exec_order import (hybrid_prepare, hybrid_spmm, pack_rows, popularity_order,
+                                           to_execution_order)
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    order = popularity_order(mt)
+    mx = to_execution_order(mt, order)
+    wx = pack_rows(order, w)
+    layout = hybrid_prepare(mx, args.head)
+    torch.cuda.synchronize()
+    prep_ms = (time.perf_counter() - t0) * 1e3
+    out = torch.empty((mt.rows, n_out), dtype=torch.float32, device="cuda")
+
+    def launch():
+        hybrid_spmm(layout, wx, out=out, stream=stream)
+
+    wall_ms, ev = time_launches(torch, launch, args.steps, args.warmup, stream)
+    log(f"hybrid head={args.head}: {wall_ms:.3f} ms/step (prepare {prep_ms:.0f} ms)")
+    return {"ms_per_step": wall_ms, "value": mt.nnz / (wall_ms * 1e-3), "unit": "nnz/s",
+            "head_genes": args.head, "kernel_ms_mean": statistics.mean(ev),
+            "kernels": "qcsr_head_dense (matrix cores, genes < head) + qcsr_spmm_groups (tail) per 64 columns",
+            "prepare_ms": prep_ms,
+            "prepare": "popularity order, execution-order relabel, weight rows reordered, dense head layout",
+            "layout_bytes": int(layout.storage.numel())}, out
 
 
 def parity_sample_qcsr(m, w, out, count: int, seed: int) -> dict:
@@ -464,6 +511,9 @@ def main() -> int:
                     help="qCSR: skip the column-order check (kernel keeps its per-entry check)")
     ap.add_argument("--separate-meta", action="store_true",
                     help="C2/C3: time the separate scale/offset arrays instead of interleaved pairs")
+    ap.add_argument("--head", type=int, default=2048,
+                    help="qCSR: also time the execution-order hybrid with this many matrix-core head "
+                         "genes (a multiple of 1,024; 0 skips it)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="run only a plain copy of BYTES (rocprofv3 counter calibration)")
     args = ap.parse_args()
