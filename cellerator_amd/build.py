@@ -45,6 +45,7 @@ ENGINE_SOURCES = [
     "bell_plan.cpp",
     "exec_order.hip",
     "exec_csr.cpp",
+    "bell_lowering.cpp",
     "qcsr_hybrid.hip",
 ]
 SYNTH_SOURCES = ["synth.hip"]

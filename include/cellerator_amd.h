@@ -389,6 +389,187 @@ int cx_bell_spmm_fwd_grouped_epilogue(const cx_bell_matrix *a, const uint16_t *p
                                       float *out, int64_t out_ld,
                                       const cx_spmm_epilogue *epilogue, void *stream);
 
+/* ---- CSR -> Blocked-ELL lowering (include/Cellerator/compute/math/physical_bell.hh) -----
+ * A canonical partition-local CSR, a frozen plan's feature blocks and permutation, and a
+ * local row order lower to a Blocked-ELL candidate of block size 8, 16 or 32: rows in
+ * execution order padded to a block multiple, features in execution order with every
+ * semantic feature block padded on its own to a block multiple (membership and order are
+ * never changed), one ELL slot list per block row as wide as the fullest block row. The
+ * query reports all three candidates with their metrics and the safety rule's verdict
+ * (value-slot expansion, storage expansion, persistent bytes); materialization re-checks
+ * the candidate against the inputs and fills caller buffers. Status values are the
+ * reference's bell_lowering_status_code; cx_bell_lowering_last_error() has the message. */
+#define CX_BELL_LOWERING_SCHEMA_VERSION 1u
+#define CX_BELL_CANDIDATE_COUNT 3u
+/* bell_candidate_state */
+#define CX_BELL_CANDIDATE_LEGAL 0u
+#define CX_BELL_CANDIDATE_EMPTY_SOURCE 1u
+#define CX_BELL_CANDIDATE_VALUE_EXPANSION_EXCEEDED 2u
+#define CX_BELL_CANDIDATE_STORAGE_EXPANSION_EXCEEDED 3u
+#define CX_BELL_CANDIDATE_PERSISTENT_BYTES_EXCEEDED 4u
+#define CX_BELL_CANDIDATE_OVERFLOW 5u
+/* bell_lowering_status_code */
+#define CX_BELL_LOWERING_OK 0
+#define CX_BELL_LOWERING_INVALID_ARGUMENT 1
+#define CX_BELL_LOWERING_INVALID_SOURCE 2
+#define CX_BELL_LOWERING_INCOMPATIBLE_PLAN 3
+#define CX_BELL_LOWERING_INCOMPATIBLE_ORDER 4
+#define CX_BELL_LOWERING_INSUFFICIENT_CAPACITY 5
+#define CX_BELL_LOWERING_CANDIDATE_REJECTED 6
+#define CX_BELL_LOWERING_CANDIDATE_MISMATCH 7
+#define CX_BELL_LOWERING_OVERFLOW 8
+/* value layouts of a materialized candidate */
+#define CX_BELL_VALUES_BLOCK_MAJOR 0u /* the reference's: [block row][slot][row in block][column in block] */
+#define CX_BELL_VALUES_ROW_MAJOR 1u   /* the engine's cx_bell_matrix: [padded row][ell column] */
+
+/* bell_csr_source_view (physical_bell.hh:47-57): feature ids canonical and strictly
+ * increasing per row; values copied byte for byte (1..16 bytes each). */
+typedef struct cx_bell_csr_source {
+    uint32_t row_count;
+    uint32_t feature_count;
+    uint32_t nnz_count;
+    uint32_t value_size_bytes;
+    const uint32_t *row_offsets;
+    const uint32_t *feature_ids;
+    const void *values;
+} cx_bell_csr_source;
+
+/* bell_semantic_plan_view (physical_bell.hh:62-72). */
+typedef struct cx_bell_semantic_plan {
+    uint32_t semantic_schema_version; /* 1 */
+    uint32_t full_row_count;
+    uint32_t feature_count;
+    uint32_t feature_block_count;
+    uint64_t feature_block_geometry_identity;
+    uint64_t row_domain_identity;
+    const uint32_t *feature_block_offsets;       /* execution order, feature_block_count + 1 */
+    const uint32_t *feature_permutation;         /* execution -> canonical */
+    const uint32_t *inverse_feature_permutation; /* canonical -> execution */
+} cx_bell_semantic_plan;
+
+/* The fields of local_cell_order_view (components/CellPack/include/CellPack/
+ * local_cell_ordering.hh:47-67) the lowering reads. */
+typedef struct cx_bell_row_order {
+    uint32_t order_schema_version;        /* 1 */
+    uint32_t signature_algorithm_version; /* 1 */
+    uint32_t kind;
+    uint32_t window_size;
+    uint32_t group_width;
+    uint32_t full_row_count;
+    uint32_t row_count;
+    uint32_t feature_block_count;
+    uint64_t ordering_identity;
+    uint64_t global_row_begin;
+    uint64_t feature_block_geometry_identity;
+    uint64_t row_domain_identity;
+    const uint32_t *row_permutation;         /* execution row -> canonical row */
+    const uint32_t *inverse_row_permutation; /* canonical row -> execution row */
+} cx_bell_row_order;
+
+/* bell_lowering_policy (physical_bell.hh:91-95); the reference's defaults are 64, 64 and
+ * the largest size_t. */
+typedef struct cx_bell_lowering_policy {
+    double maximum_value_slot_expansion;
+    double maximum_storage_expansion;
+    uint64_t maximum_persistent_bytes;
+} cx_bell_lowering_policy;
+
+typedef struct cx_bell_candidate_metrics {
+    uint64_t occupied_blocks;
+    uint64_t stored_blocks;
+    uint64_t dense_value_slots;
+    uint64_t persistent_bytes;
+    uint64_t source_bytes;
+    double scalar_occupancy;
+    double ell_slot_utilization;
+    double value_slot_expansion;
+    double storage_expansion;
+} cx_bell_candidate_metrics;
+
+/* bell_candidate_requirements (physical_bell.hh:109-124). */
+typedef struct cx_bell_candidate {
+    uint32_t state;
+    uint32_t block_size;
+    uint32_t row_count;
+    uint32_t feature_count;
+    uint32_t padded_row_count;
+    uint32_t padded_feature_count;
+    uint32_t block_row_count;
+    uint32_t ell_blocks_per_row;
+    uint32_t ell_columns;
+    uint32_t reserved;
+    uint64_t feature_block_offset_count;
+    uint64_t column_index_count;
+    uint64_t value_bytes;
+    uint64_t candidate_identity;
+    cx_bell_candidate_metrics metrics;
+} cx_bell_candidate;
+
+typedef struct cx_bell_lowering_workspace {
+    uint64_t marker_capacity;
+    uint32_t *markers;
+    uint64_t feature_block_offset_capacity;
+    uint32_t *feature_block_block_offsets;
+} cx_bell_lowering_workspace;
+
+typedef struct cx_bell_candidate_buffers {
+    uint64_t feature_block_offset_capacity;
+    uint32_t *padded_feature_block_offsets;
+    uint64_t column_index_capacity;
+    int32_t *column_indices; /* -1 = empty slot (the engine reads it as 0xffffffff) */
+    uint64_t value_capacity_bytes;
+    void *values;
+    uint32_t value_layout;   /* CX_BELL_VALUES_* */
+} cx_bell_candidate_buffers;
+
+/* physical_bell_view (physical_bell.hh:150-168) plus the value layout. */
+typedef struct cx_physical_bell_view {
+    uint32_t schema_version;
+    uint32_t block_size;
+    uint32_t row_count;
+    uint32_t feature_count;
+    uint32_t padded_row_count;
+    uint32_t padded_feature_count;
+    uint32_t ell_columns;
+    uint32_t value_size_bytes;
+    uint64_t feature_block_geometry_identity;
+    uint64_t ordering_identity;
+    uint64_t row_domain_identity;
+    uint64_t candidate_identity;
+    const uint32_t *padded_feature_block_offsets;
+    const int32_t *column_indices;
+    const void *values;
+    cx_bell_candidate_metrics metrics;
+    uint32_t value_layout;
+} cx_physical_bell_view;
+
+/* query_bell_lowering_workspace_requirements (physical_bell.cc:84-96): marker_count =
+ * max(rows, features), feature_block_offset_count = feature blocks + 1. Host. */
+int cx_bell_lowering_workspace_requirements(const cx_bell_csr_source *source, const cx_bell_semantic_plan *plan,
+                                            const cx_bell_row_order *order, uint64_t *marker_count,
+                                            uint64_t *feature_block_offset_count);
+/* query_bell_candidates_host (physical_bell_candidates.cc:216-238): validates every input
+ * (permutations are inverses, CSR sorted and unique) and evaluates block sizes 8, 16, 32
+ * into out[0..2]. NULL policy = the reference's defaults. Host. */
+int cx_bell_query_candidates_host(const cx_bell_csr_source *source, const cx_bell_semantic_plan *plan,
+                                  const cx_bell_row_order *order, const cx_bell_lowering_policy *policy,
+                                  const cx_bell_lowering_workspace *workspace, cx_bell_candidate *out);
+/* materialize_bell_candidate_host (physical_bell.cc:98-200): re-queries, rejects a
+ * non-legal or stale candidate (CANDIDATE_REJECTED / CANDIDATE_MISMATCH), then writes the
+ * padded block offsets, slot columns (-1 = empty) and values (zeros where not stored) in
+ * buffers->value_layout. Host. */
+int cx_bell_materialize_candidate_host(const cx_bell_csr_source *source, const cx_bell_semantic_plan *plan,
+                                       const cx_bell_row_order *order, const cx_bell_lowering_policy *policy,
+                                       const cx_bell_candidate *candidate,
+                                       const cx_bell_lowering_workspace *workspace,
+                                       const cx_bell_candidate_buffers *buffers, cx_physical_bell_view *out);
+/* Canonical feature of every physical (padded) feature column of `view`, -1 for padding:
+ * the gather map that lays a canonical weight matrix out for the engine's Blocked-ELL
+ * SpMM (W_phys[p] = W[map[p]] or 0). map holds view->padded_feature_count entries. Host. */
+int cx_bell_physical_feature_map(const cx_physical_bell_view *view, const cx_bell_semantic_plan *plan,
+                                 int32_t *map, uint64_t capacity);
+const char *cx_bell_lowering_last_error(void);
+
 /* CP-BP warp-tile projection (components/CellPack/include/CellPack/warp_tiles.hh:41-79)
  * plus the plan subset of feature_weighted_row_reduction_plan_view
  * (components/CellPack/include/CellPack/feature_weighted_row_reduction.hh:16-26).
