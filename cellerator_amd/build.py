@@ -46,6 +46,7 @@ ENGINE_SOURCES = [
     "exec_order.hip",
     "exec_csr.cpp",
     "bell_lowering.cpp",
+    "spmm_request.cpp",
     "qcsr_hybrid.hip",
 ]
 SYNTH_SOURCES = ["synth.hip"]

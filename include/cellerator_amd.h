@@ -219,6 +219,166 @@ int cx_qcsr_check_columns_sync(const cx_qcsr_matrix *a, uint32_t *host_flag, voi
  * code that reaches the engine only through this C-ABI. Engine addition. */
 int cx_stream_synchronize(void *stream);
 
+/* ---- backend-neutral SpMM request (include/Cellerator/compute/math/operation.hh) -------
+ * The reference's math contract as plain C structs with the same member order, sizes and
+ * values (so the bytes of a reference spmm_request are a valid cx_spmm_request), its
+ * validation, its 128-bit operation signature, the trivial-work classification, and a
+ * request-driven entry onto the quantized CSR kernels. Type codes are the reference's
+ * real::value_* codes (f16 3, f32 4, f64 5, bf16 6, fp8 e4m3 7, fp8 e5m2 8). */
+#define CX_OPERATION_CONTRACT_SCHEMA_VERSION 1u
+#define CX_OPERATION_SPMM 1u
+#define CX_TRANSPOSE_NONE 0u
+#define CX_TRANSPOSE 1u
+#define CX_LAYOUT_ROW_MAJOR 1u
+#define CX_LAYOUT_COLUMN_MAJOR 2u
+#define CX_ALLOW_NONDETERMINISTIC 0u
+#define CX_DETERMINISTIC 1u
+#define CX_WORKSPACE_REUSABLE_POOL 1u
+#define CX_WORKSPACE_CALLER_LIMIT 2u
+#define CX_WORKSPACE_NONE 3u
+#define CX_REUSE_SINGLE_RUN 1u
+#define CX_REUSE_BOUNDED 2u
+#define CX_REUSE_PERSISTENT 3u
+#define CX_FEATURE_ORDER_KIND_CANONICAL 1u
+#define CX_FEATURE_ORDER_KIND_PACKED 2u
+#define CX_REAL_F16 3u
+#define CX_REAL_F32 4u
+#define CX_REAL_F64 5u
+#define CX_REAL_BF16 6u
+#define CX_REAL_FP8_E4M3 7u
+#define CX_REAL_FP8_E5M2 8u
+/* request_validation_code (operation.hh:68-85) */
+#define CX_REQUEST_OK 0u
+#define CX_REQUEST_UNSUPPORTED_VERSION 1u
+#define CX_REQUEST_INVALID_SHAPE 2u
+#define CX_REQUEST_INVALID_TYPE 3u
+#define CX_REQUEST_INVALID_SCALAR 4u
+#define CX_REQUEST_INVALID_WORKSPACE_POLICY 5u
+#define CX_REQUEST_INVALID_REUSE 6u
+#define CX_REQUEST_INVALID_FEATURE_ORDER 7u
+#define CX_REQUEST_FEATURE_ORDER_MISMATCH 8u
+#define CX_REQUEST_MISSING_BIAS 9u
+#define CX_REQUEST_UNEXPECTED_BIAS 10u
+#define CX_REQUEST_INVALID_LAYOUT 11u
+#define CX_REQUEST_INVALID_IDENTITY 12u
+#define CX_REQUEST_MISSING_BINDING 13u
+#define CX_REQUEST_INVALID_DETERMINISM 14u
+#define CX_REQUEST_INVALID_EPILOGUE 15u
+/* trivial_operation_kind (operation.hh:197-201) */
+#define CX_TRIVIAL_NONE 0u
+#define CX_TRIVIAL_NO_OUTPUT 1u
+#define CX_TRIVIAL_EPILOGUE_ONLY 2u
+
+typedef struct cx_feature_order_identity {  /* operation.hh:89-96 */
+    uint32_t schema_version;                /* 1 */
+    uint32_t kind;                          /* CX_FEATURE_ORDER_KIND_* */
+    uint32_t feature_count;
+    uint32_t feature_axis_identity_version;
+    uint64_t feature_axis_identity;
+    uint64_t packing_geometry_identity;     /* nonzero exactly for packed orders */
+} cx_feature_order_identity;
+
+typedef struct cx_sparse_structure_identity {  /* operation.hh:100-104 */
+    uint32_t schema_version;                   /* 1 */
+    uint32_t identity_version;
+    uint64_t value;
+} cx_sparse_structure_identity;
+
+typedef struct cx_scalar_value {  /* operation.hh:106-110: f32 bits in the low word, or f64 */
+    uint32_t type_code;
+    uint32_t reserved;
+    uint64_t bits;
+} cx_scalar_value;
+
+typedef struct cx_workspace_policy {  /* operation.hh:112-117 */
+    uint32_t kind;
+    uint32_t reserved;
+    uint64_t byte_limit;
+} cx_workspace_policy;
+
+typedef struct cx_expected_reuse {  /* operation.hh:119-124 */
+    uint32_t kind;
+    uint32_t reserved;
+    uint64_t expected_run_count;
+} cx_expected_reuse;
+
+typedef struct cx_epilogue_descriptor {  /* operation.hh:126-130 */
+    uint32_t kind;                       /* CX_EPILOGUE_* */
+    uint32_t bias_type_code;
+    uint64_t bias_element_count;
+} cx_epilogue_descriptor;
+
+typedef struct cx_spmm_request {  /* spmm_request, operation.hh:136-164 */
+    uint32_t schema_version;
+    uint32_t operation;
+    uint64_t m, k, n;
+    uint64_t sparse_nnz;
+    cx_sparse_structure_identity sparse_structure;
+    uint32_t transpose_sparse;
+    uint32_t transpose_dense;
+    uint32_t dense_rhs_layout;
+    uint32_t output_layout;
+    uint64_t dense_rhs_leading_dimension;
+    uint64_t output_leading_dimension;
+    uint32_t sparse_storage_type_code;
+    uint32_t dense_storage_type_code;
+    uint32_t output_storage_type_code;
+    uint32_t compute_type_code;
+    uint32_t accumulation_type_code;
+    cx_scalar_value alpha;
+    cx_scalar_value beta;
+    uint32_t determinism;
+    cx_workspace_policy workspace;
+    cx_expected_reuse reuse;
+    cx_epilogue_descriptor epilogue;
+    cx_feature_order_identity sparse_feature_order;
+    cx_feature_order_identity dense_feature_order;
+} cx_spmm_request;
+
+typedef struct cx_spmm_bindings {  /* operation.hh:166-174 */
+    const void *sparse_matrix;
+    const void *dense_rhs;
+    void *output;
+    const void *bias;
+    uint64_t sparse_matrix_identity;
+    uint64_t dense_rhs_identity;
+    uint64_t output_identity;
+} cx_spmm_bindings;
+
+typedef struct cx_operation_signature {  /* operation.hh:181-186 */
+    uint32_t schema_version;
+    uint32_t operation;
+    uint64_t low;
+    uint64_t high;
+} cx_operation_signature;
+
+/* A cx_spmm_request with the reference's defaults (request_fixture-neutral: schema 1,
+ * SpMM, row-major layouts, reusable pool, single run, canonical feature orders). */
+void cx_spmm_request_init(cx_spmm_request *request);
+cx_scalar_value cx_scalar_f32(float value);
+cx_scalar_value cx_scalar_f64(double value);
+/* validate_spmm_request (src/compute/math/operation.cc:119-249): CX_REQUEST_* code;
+ * *message (may be NULL) gets the reference's text. */
+uint32_t cx_validate_spmm_request(const cx_spmm_request *request, const char **message);
+/* validate_math_request (operation.cc:251-280): the request, then the bindings. */
+uint32_t cx_validate_math_request(const cx_spmm_request *request, const cx_spmm_bindings *bindings,
+                                  const char **message);
+/* make_operation_signature (src/compute/math/operation_signature.cc:30-68). */
+cx_operation_signature cx_make_operation_signature(const cx_spmm_request *request);
+/* classify_trivial_operation (operation.cc:282-293). */
+uint32_t cx_classify_trivial_operation(const cx_spmm_request *request);
+/* Runs a validated math request on a quantized CSR: bindings.sparse_matrix is a
+ * cx_qcsr_matrix, dense_rhs the weights, output the fp32 output, bias the fp32 bias. The
+ * request must describe this matrix (m = rows, k = cols, sparse_nnz = nnz), untransposed
+ * row-major operands, F16 or F32 dense storage, F32 output / compute / accumulation,
+ * feature orders that agree (checked by validation; a packed order means the matrix and W
+ * are both in that execution order). alpha and beta f32, or f64 exactly representable in
+ * f32. No-output requests return at once; epilogue-only requests (alpha 0, K 0 or no
+ * stored entries) write act(beta C + bias) without reading the matrix's values.
+ * INVALID_ARGUMENT with the validation text for a rejected request, UNSUPPORTED for a valid
+ * form this entry does not run. */
+int cx_qcsr_spmm_fwd_request(const cx_spmm_request *request, const cx_spmm_bindings *bindings, void *stream);
+
 /* ---- transpose and backward of the CSR SpMM ------------------------------------ */
 
 /* Device bytes of workspace cx_qcsr_transpose needs for `a`. */
