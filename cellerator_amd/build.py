@@ -47,6 +47,7 @@ ENGINE_SOURCES = [
     "exec_csr.cpp",
     "bell_lowering.cpp",
     "spmm_request.cpp",
+    "qcsr_codec.hip",
     "qcsr_hybrid.hip",
 ]
 SYNTH_SOURCES = ["synth.hip"]

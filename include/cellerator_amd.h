@@ -219,6 +219,39 @@ int cx_qcsr_check_columns_sync(const cx_qcsr_matrix *a, uint32_t *host_flag, voi
  * code that reaches the engine only through this C-ABI. Engine addition. */
 int cx_stream_synchronize(void *stream);
 
+/* ---- the quantized codec as device passes over a row block -----------------------------
+ * csr_block (include/Cellerator/quantized/layout.cuh:41-49): a row range of the matrix and
+ * its entry and packed-byte ranges. */
+typedef struct cx_qcsr_block {
+    int32_t block_index;
+    int32_t row_begin;
+    int32_t row_end;
+    int32_t nnz_begin;
+    int32_t nnz_end;
+    int32_t packed_begin;
+    int32_t packed_end;
+    int32_t reserved;  /* the reference's alignas(32) */
+} cx_qcsr_block;
+
+/* get_block (include/Cellerator/quantized/access.cuh:7-45) over host arrays: block
+ * block_index of block_row_ptr (block_count + 1 row starts), or the whole matrix when
+ * block_row_ptr is NULL or block_count <= 0. */
+int cx_qcsr_get_block(const int32_t *block_row_ptr, int32_t block_count, const int32_t *row_ptr,
+                      const int32_t *packed_row_ptr, int32_t rows, int32_t block_index, cx_qcsr_block *out);
+/* launch_quantize_block (include/Cellerator/quantized/dispatch.cuh:35-47) with
+ * pack_row_values (packing.cuh:13-146): the F32 values of the block's entries
+ * (values_by_nnz_block[i - block->nnz_begin]) encoded by the portable rule
+ * (access.cuh:104-131) with a's metadata and packed into packed_out (a's packed layout; the
+ * high bits of a row's last byte are zero). block NULL = every row (values from entry 0).
+ * Writes only the block's packed bytes. */
+int cx_qcsr_quantize_block(const cx_qcsr_matrix *a, const cx_qcsr_block *block,
+                           const float *values_by_nnz_block, uint8_t *packed_out, void *stream);
+/* launch_dequantize_block (dispatch.cuh:49-61) with unpack_row_values (packing.cuh:148-260):
+ * values_by_nnz_block[i - block->nnz_begin] = fma(code, scale, offset) for the block's
+ * entries. */
+int cx_qcsr_dequantize_block(const cx_qcsr_matrix *a, const cx_qcsr_block *block, float *values_by_nnz_block,
+                             void *stream);
+
 /* ---- backend-neutral SpMM request (include/Cellerator/compute/math/operation.hh) -------
  * The reference's math contract as plain C structs with the same member order, sizes and
  * values (so the bytes of a reference spmm_request are a valid cx_spmm_request), its
