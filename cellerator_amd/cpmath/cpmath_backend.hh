@@ -44,6 +44,7 @@
 #pragma once
 
 #include <Cellerator/compute/math/operation_core/operation_core.hh>
+#include <Cellerator/planner/end_to_end_planner.hh>
 
 #include <cstdint>
 
@@ -135,5 +136,34 @@ core::operation_candidate cpbp_candidate() noexcept;
 
 // Engine error text behind the last execution_failed status of this thread.
 const char *last_engine_error() noexcept;
+
+// ---- planner side (include/Cellerator/planner/end_to_end_planner.hh:118-291) ----------
+// What an end-to-end planner needs to rank the engine's candidates without running them:
+// the shape of the work and an analytical cost per phase from MI355X peaks (HBM 8 TB/s,
+// non-packed fp32 VALU 78.6 TFLOP/s, bf16 matrix cores 2.5 PFLOP/s) scaled by the fraction
+// of peak each kernel family reaches, and the physical bytes each projection keeps. The
+// planner's measurement hook then replaces the kernel estimate with timings of the real
+// kernels.
+struct workload_shape {
+    std::uint64_t rows = 0u;          // cells
+    std::uint64_t cols = 0u;          // genes
+    std::uint64_t nnz = 0u;           // stored entries of the logical matrix
+    std::uint32_t out_cols = 0u;      // N (multiply); 0 for the reduction
+    std::uint32_t bits = 0u;          // quantized code width; 0 = plain values
+    std::uint32_t value_bytes = 4u;   // bytes per plain value (Blocked-ELL, CP-BP)
+    std::uint32_t block_size = 0u;    // Blocked-ELL block edge
+    std::uint64_t ell_columns = 0u;   // Blocked-ELL padded columns per row
+    std::uint64_t tile_blocks = 0u;   // CP-BP (tile, block) entries
+};
+
+// Analytical phases of `candidate` (one of the three above) on `shape`; false for an
+// unknown candidate or an incomplete shape.
+bool analytical_costs(core::stable_id candidate, const workload_shape &shape,
+                      cellerator::planner::phase_costs *out) noexcept;
+// A planner candidate for an engine operation candidate and its declared projection:
+// identity and name of the operation candidate, flags from its capabilities (correct by
+// construction, deterministic and graph capture as advertised), analytical phases.
+bool planner_candidate_for(const core::operation_candidate &operation, const core::projection_key &projection,
+                           const workload_shape &shape, cellerator::planner::planner_candidate *out) noexcept;
 
 } // namespace cellerator_amd::cpmath
