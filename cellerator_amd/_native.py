@@ -119,6 +119,21 @@ class CxCpk1View(C.Structure):
                 ("inverse_row_permutation", p_void), ("tiles", CxCpbpTiles)]
 
 
+class CxCpbpReductionView(C.Structure):
+    _fields_ = [("schema_version", u32), ("storage_type_code", u32), ("weight_type_code", u32),
+                ("accumulation_type_code", u32), ("feature_weight_identity", u64), ("reduction_identity", u64),
+                ("plan_schema_version", u32), ("plan_geometry_identity_version", u32), ("plan_feature_count", u32),
+                ("plan_feature_block_count", u32), ("plan_geometry_identity", u64), ("tile_schema_version", u32),
+                ("tiles_plan_schema_version", u32), ("tiles_geometry_identity_version", u32),
+                ("feature_axis_fingerprint_version", u32), ("tile_identity", u64), ("tiles_geometry_identity", u64),
+                ("tiles_ordering_identity", u64), ("tiles_global_row_begin", u64), ("feature_axis_fingerprint", u64),
+                ("tiles_row_domain_identity", u64), ("tiles_full_row_count", u32), ("order_schema_version", u32),
+                ("order_signature_version", u32), ("order_full_row_count", u32), ("order_row_count", u32),
+                ("order_feature_block_count", u32), ("order_group_width", u32), ("reserved", u32),
+                ("order_ordering_identity", u64), ("order_global_row_begin", u64), ("order_geometry_identity", u64),
+                ("order_row_domain_identity", u64), ("tiles", CxCpbpTiles)]
+
+
 class CxCpk1Metadata(C.Structure):
     _fields_ = [("feature_axis_fingerprint", u64), ("feature_axis_fingerprint_version", u32),
                 ("row_domain_kind", u32), ("row_domain_identity", u64),
@@ -264,6 +279,9 @@ ENGINE_SIGNATURES = {
                                                     C.POINTER(CxBellGroups), i64, p_void, i64,
                                                     C.POINTER(CxSpmmEpilogue), p_void]),
     "cx_cpbp_reduce": (C.c_int, [C.POINTER(CxCpbpTiles), p_void, u64, p_void, u64, p_void]),
+    "cx_cpbp_reduction_identity": (u64, [C.POINTER(CxCpbpReductionView)]),
+    "cx_cpbp_reduction_view_from_cpk1": (C.c_int, [C.POINTER(CxCpk1View), u64, C.POINTER(CxCpbpReductionView)]),
+    "cx_cpbp_reduce_checked": (C.c_int, [C.POINTER(CxCpbpReductionView), p_void, u64, p_void, u64, p_void]),
     "cx_cpk1_image_bytes": (C.c_int, [C.POINTER(CxCpbpTileRequirements), u32, C.POINTER(u64)]),
     "cx_cpk1_write": (C.c_int, [C.POINTER(CxCpbpPlan), C.POINTER(CxCpk1Metadata),
                                 C.POINTER(CxCpbpTileRequirements), C.POINTER(CxCpbpTileBuffers),

@@ -439,3 +439,118 @@ extern "C" int cx_cpbp_reduce(const cx_cpbp_tiles *t, const float *feature_weigh
 #undef CX_CPBP_LAUNCH
     return check_launch("cpbp_reduce");
 }
+
+// ---- the reference's full direct-consumer contract --------------------------------------
+// validate_metadata (components/CellPack/src/feature_weighted_row_reduction_cuda.cu:57-136):
+// schema versions, the numeric contract, every identity (the reduction identity recomputed),
+// then agreement of the plan, the local order and the tiles on their shared domain, before
+// the dimension, pointer and aliasing checks of cx_cpbp_reduce.
+
+namespace cx {
+namespace {
+
+constexpr std::uint32_t kReductionSchema = 1u, kTileSchema = 1u, kPlanSchema = 1u, kGeometryVersion = 1u;
+constexpr std::uint32_t kOrderSchema = 1u, kSignatureVersion = 1u;
+constexpr std::uint32_t kRealF16 = 3u, kRealF32 = 4u;  // cellerator::real codes
+
+std::uint64_t splitmix64(std::uint64_t x) {
+    x += 0x9e3779b97f4a7c15ull;
+    x = (x ^ (x >> 30u)) * 0xbf58476d1ce4e5b9ull;
+    x = (x ^ (x >> 27u)) * 0x94d049bb133111ebull;
+    return x ^ (x >> 31u);
+}
+
+std::uint32_t storage_code(const cx_cpbp_tiles &t) {
+    return t.value_dtype == CELLERATOR_DTYPE_F16 ? kRealF16 : t.value_dtype == CELLERATOR_DTYPE_F32 ? kRealF32 : 0u;
+}
+
+} // namespace
+} // namespace cx
+
+// reduction_identity (feature_weighted_row_reduction_cuda.cu:44-55): a splitmix64 chain over
+// the tile identity, the plan geometry, the weight identity, the schema version and the
+// storage / weight / accumulation type codes.
+extern "C" uint64_t cx_cpbp_reduction_identity(const cx_cpbp_reduction_view *v) {
+    using namespace cx;
+    if (v == nullptr) return 0u;
+    std::uint64_t h = splitmix64(v->tile_identity);
+    h = splitmix64(h ^ v->plan_geometry_identity);
+    h = splitmix64(h ^ v->feature_weight_identity);
+    h = splitmix64(h ^ (static_cast<std::uint64_t>(v->schema_version) << 32u) ^ v->storage_type_code);
+    h = splitmix64(h ^ (static_cast<std::uint64_t>(v->weight_type_code) << 32u) ^ v->accumulation_type_code);
+    return h == 0u ? 1u : h;
+}
+
+extern "C" int cx_cpbp_reduction_view_from_cpk1(const cx_cpk1_view *image, uint64_t feature_weight_identity,
+                                                cx_cpbp_reduction_view *out) {
+    using namespace cx;
+    clear_error();
+    if (image == nullptr || out == nullptr)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_cpbp_reduction_view_from_cpk1: null argument");
+    cx_cpbp_reduction_view v{};
+    v.schema_version = kReductionSchema;
+    v.storage_type_code = storage_code(image->tiles);
+    v.weight_type_code = v.accumulation_type_code = kRealF32;
+    v.feature_weight_identity = feature_weight_identity;
+    v.plan_schema_version = v.tiles_plan_schema_version = kPlanSchema;
+    v.plan_geometry_identity_version = v.tiles_geometry_identity_version = kGeometryVersion;
+    v.plan_feature_count = image->tiles.feature_count;
+    v.plan_feature_block_count = image->tiles.feature_block_count;
+    v.plan_geometry_identity = image->feature_block_geometry_identity;
+    v.tile_schema_version = kTileSchema;
+    v.tile_identity = image->tile_identity;
+    v.tiles_geometry_identity = image->feature_block_geometry_identity;
+    v.tiles_ordering_identity = image->ordering_identity;
+    v.tiles_global_row_begin = image->global_row_begin;
+    v.tiles_full_row_count = image->full_row_count;
+    v.feature_axis_fingerprint = image->feature_axis_fingerprint;
+    v.feature_axis_fingerprint_version = image->feature_axis_fingerprint_version;
+    v.tiles_row_domain_identity = image->row_domain_identity;
+    v.order_schema_version = kOrderSchema;
+    v.order_signature_version = kSignatureVersion;
+    v.order_ordering_identity = image->ordering_identity;
+    v.order_global_row_begin = image->global_row_begin;
+    v.order_full_row_count = image->full_row_count;
+    v.order_row_count = image->tiles.row_count;
+    v.order_feature_block_count = image->tiles.feature_block_count;
+    v.order_group_width = image->order.group_width;
+    v.order_geometry_identity = image->feature_block_geometry_identity;
+    v.order_row_domain_identity = image->row_domain_identity;
+    v.tiles = image->tiles;
+    v.reduction_identity = cx_cpbp_reduction_identity(&v);
+    *out = v;
+    return CX_STATUS_SUCCESS;
+}
+
+extern "C" int cx_cpbp_reduce_checked(const cx_cpbp_reduction_view *v, const float *feature_weights,
+                                      uint64_t feature_weight_capacity, float *row_values, uint64_t row_capacity,
+                                      void *stream) {
+    using namespace cx;
+    clear_error();
+    if (v == nullptr) return fail(CX_STATUS_INVALID_ARGUMENT, "cx_cpbp_reduce_checked: null view");
+    const cx_cpbp_tiles &t = v->tiles;
+    if (v->schema_version != kReductionSchema || v->tile_schema_version != kTileSchema
+        || v->plan_schema_version != kPlanSchema || v->tiles_plan_schema_version != kPlanSchema
+        || v->plan_geometry_identity_version != kGeometryVersion
+        || v->tiles_geometry_identity_version != kGeometryVersion || v->order_schema_version != kOrderSchema
+        || v->order_signature_version != kSignatureVersion)
+        return fail(CX_STATUS_UNSUPPORTED, "weighted-row-reduction version is unsupported");
+    if (v->storage_type_code == 0u || v->storage_type_code != storage_code(t) || v->weight_type_code != kRealF32
+        || v->accumulation_type_code != kRealF32)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "weighted-row-reduction numeric contract is incompatible");
+    if (v->feature_weight_identity == 0u || v->reduction_identity == 0u || v->tile_identity == 0u
+        || v->tiles_ordering_identity == 0u || v->feature_axis_fingerprint == 0u
+        || v->feature_axis_fingerprint_version == 0u || v->tiles_row_domain_identity == 0u
+        || v->reduction_identity != cx_cpbp_reduction_identity(v))
+        return fail(CX_STATUS_INVALID_ARGUMENT, "weighted-row-reduction identity is invalid");
+    if (v->plan_feature_count != t.feature_count || v->plan_feature_block_count != t.feature_block_count
+        || v->plan_geometry_identity != v->tiles_geometry_identity
+        || v->order_geometry_identity != v->tiles_geometry_identity
+        || v->order_ordering_identity != v->tiles_ordering_identity
+        || v->order_global_row_begin != v->tiles_global_row_begin
+        || v->order_full_row_count != v->tiles_full_row_count || v->order_row_count != t.row_count
+        || v->order_feature_block_count != t.feature_block_count
+        || v->order_row_domain_identity != v->tiles_row_domain_identity || v->order_group_width != t.tile_row_width)
+        return fail(CX_STATUS_INVALID_SHAPE, "weighted-row-reduction plan, order, and tile domains disagree");
+    return cx_cpbp_reduce(&t, feature_weights, feature_weight_capacity, row_values, row_capacity, stream);
+}

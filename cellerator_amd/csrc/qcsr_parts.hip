@@ -38,11 +38,6 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void *base, std::uint32_t byte
 
 using lds_ptr = __attribute__((address_space(3))) void *;
 
-// The weight rows and metadata of genes [lo, hi) into LDS. The weight rows go straight from
-// memory to LDS (buffer loads with the lds flag: wave instruction k of wave w fills 1 KB,
-// 8 rows, at no register cost); loads past the part's last row return zeros. Interleaved
-// (scale, offset) pairs go the same way; the other decode policies build their pairs in
-// registers.
 // The fp16 weight rows of genes [lo, hi) straight from memory into LDS (buffer loads with
 // the lds flag: wave instruction k of wave w fills 1 KB, 8 rows, at no register cost);
 // loads past the part's last row return zeros.

@@ -999,6 +999,65 @@ int cx_cpk1_rebind(const cx_cpk1_view *validated, const void *new_base, uint64_t
                    cx_cpk1_view *out);
 const char *cx_cpk1_last_error(void);
 
+/* ---- CP-BP reduction under the reference's full direct-consumer contract ----------------
+ * feature_weighted_row_reduction_view (components/CellPack/include/CellPack/
+ * feature_weighted_row_reduction.hh:20-44) with the warp_tile_view identity fields
+ * (warp_tiles.hh:49-79) and the local_cell_order_view fields the reduction checks
+ * (local_cell_ordering.hh:47-67), around the engine's cx_cpbp_tiles. */
+typedef struct cx_cpbp_reduction_view {
+    uint32_t schema_version;               /* 1 */
+    uint32_t storage_type_code;            /* cellerator real code of the values: f16 3, f32 4 */
+    uint32_t weight_type_code;             /* f32 4 */
+    uint32_t accumulation_type_code;       /* f32 4 */
+    uint64_t feature_weight_identity;      /* the caller's weight generation, nonzero */
+    uint64_t reduction_identity;           /* cx_cpbp_reduction_identity of this view */
+    /* plan (feature_weighted_row_reduction_plan_view) */
+    uint32_t plan_schema_version;          /* 1 */
+    uint32_t plan_geometry_identity_version; /* 1 */
+    uint32_t plan_feature_count;
+    uint32_t plan_feature_block_count;
+    uint64_t plan_geometry_identity;
+    /* tiles (warp_tile_view identities) */
+    uint32_t tile_schema_version;          /* 1 */
+    uint32_t tiles_plan_schema_version;    /* 1 */
+    uint32_t tiles_geometry_identity_version; /* 1 */
+    uint32_t feature_axis_fingerprint_version;
+    uint64_t tile_identity;
+    uint64_t tiles_geometry_identity;
+    uint64_t tiles_ordering_identity;
+    uint64_t tiles_global_row_begin;
+    uint64_t feature_axis_fingerprint;
+    uint64_t tiles_row_domain_identity;
+    uint32_t tiles_full_row_count;
+    /* local order */
+    uint32_t order_schema_version;         /* 1 */
+    uint32_t order_signature_version;      /* 1 */
+    uint32_t order_full_row_count;
+    uint32_t order_row_count;
+    uint32_t order_feature_block_count;
+    uint32_t order_group_width;
+    uint32_t reserved;
+    uint64_t order_ordering_identity;
+    uint64_t order_global_row_begin;
+    uint64_t order_geometry_identity;
+    uint64_t order_row_domain_identity;
+    cx_cpbp_tiles tiles;
+} cx_cpbp_reduction_view;
+
+/* reduction_identity (components/CellPack/src/feature_weighted_row_reduction_cuda.cu:44-55). */
+uint64_t cx_cpbp_reduction_identity(const cx_cpbp_reduction_view *view);
+/* The view of a validated (or rebound) CPK1 image and a weight generation: every identity
+ * and domain field from the image, reduction_identity computed. */
+int cx_cpbp_reduction_view_from_cpk1(const cx_cpk1_view *image, uint64_t feature_weight_identity,
+                                     cx_cpbp_reduction_view *out);
+/* validate_metadata (feature_weighted_row_reduction_cuda.cu:57-136) then cx_cpbp_reduce:
+ * UNSUPPORTED for a version, INVALID_ARGUMENT for the numeric contract or an identity
+ * (including a reduction identity that is not the recomputed one), INVALID_SHAPE when plan,
+ * order and tiles disagree on their domain. */
+int cx_cpbp_reduce_checked(const cx_cpbp_reduction_view *view, const float *feature_weights,
+                           uint64_t feature_weight_capacity, float *row_values, uint64_t row_capacity,
+                           void *stream);
+
 /* ---- execution feature order: packed dense operand and execution-order CSR ---------------
  * feature_permutation[e] = the canonical gene at execution position e (cx_cpbp_plan's
  * convention). X . W does not change when the genes of X and the rows of W are relabelled

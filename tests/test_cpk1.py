@@ -229,3 +229,72 @@ def test_larger_image_on_the_device(oracle):
     ref, mag = oracle.cpbp_canonical_f64(offs, feats, vals, w, oracle.F16)
     tol = 1e-5 + 1e-5 * np.abs(ref) + 2.0 ** -22 * mag
     assert np.all(np.abs(got.cpu().numpy().astype(np.float64) - ref) <= tol)
+
+
+def _reduction_view(view, weight_identity=0x5EED):
+    out = N.CxCpbpReductionView()
+    assert N.engine().cx_cpbp_reduction_view_from_cpk1(C.byref(view), weight_identity, C.byref(out)) == 0
+    return out
+
+
+def test_reduction_identity_chain():
+    """reduction_identity (feature_weighted_row_reduction_cuda.cu:44-55) restated here from the
+    splitmix64 chain; the C-ABI's value and the view built from an image agree with it."""
+    _, _, image, view = build_reference_image()
+    v = _reduction_view(cpk1.validate(image, cpk1.expected_of(view)))
+    M = (1 << 64) - 1
+
+    def splitmix(x):
+        x = (x + 0x9E3779B97F4A7C15) & M
+        x = ((x ^ (x >> 30)) * 0xBF58476D1CE4E5B9) & M
+        x = ((x ^ (x >> 27)) * 0x94D049BB133111EB) & M
+        return x ^ (x >> 31)
+
+    h = splitmix(v.tile_identity)
+    h = splitmix(h ^ v.plan_geometry_identity)
+    h = splitmix(h ^ 0x5EED)
+    h = splitmix(h ^ (1 << 32) ^ 3)  # schema 1, storage f16 (code 3)
+    h = splitmix(h ^ (4 << 32) ^ 4)  # weights and accumulation f32
+    assert v.reduction_identity == h == N.engine().cx_cpbp_reduction_identity(C.byref(v))
+    assert (v.storage_type_code, v.weight_type_code, v.accumulation_type_code) == (3, 4, 4)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("field,value,status", [
+    (None, None, 0),
+    ("schema_version", 2, "UNSUPPORTED"),
+    ("order_signature_version", 2, "UNSUPPORTED"),
+    ("storage_type_code", 4, "INVALID_ARGUMENT"),
+    ("feature_weight_identity", 0, "INVALID_ARGUMENT"),
+    ("reduction_identity", 12345, "INVALID_ARGUMENT"),
+    ("tile_identity", 99, "INVALID_ARGUMENT"),  # the recomputed reduction identity no longer matches
+    ("order_ordering_identity", 7, "INVALID_SHAPE"),
+    ("order_group_width", 16, "INVALID_SHAPE"),
+    ("order_row_count", 1, "INVALID_SHAPE"),
+    ("plan_geometry_identity", 5, "INVALID_ARGUMENT"),  # part of the reduction identity too
+    ("order_geometry_identity", 5, "INVALID_SHAPE"),
+    ("order_row_domain_identity", 5, "INVALID_SHAPE"),
+])
+def test_checked_reduction_rejects_mismatched_contracts(oracle, field, value, status):
+    """validate_metadata (feature_weighted_row_reduction_cuda.cu:57-136): the checked entry runs
+    the reduction (bitwise equal to the plain one) only when versions, numeric contract,
+    identities and the plan / order / tile domains agree; every mismatch is rejected before
+    any launch."""
+    import torch
+
+    from cellerator_amd import cpbp_reduce
+    _, _, image, view = build_reference_image()
+    dev = cpk1.upload(cpk1.validate(image, cpk1.expected_of(view)), image)
+    v = _reduction_view(dev.view)
+    if field is not None:
+        setattr(v, field, value)
+    w = torch.from_numpy((0.5 + 0.125 * np.arange(6)).astype(np.float32)).cuda()
+    out = torch.full((dev.row_count,), -7.0, device="cuda")
+    rc = N.engine().cx_cpbp_reduce_checked(C.byref(v), w.data_ptr(), w.numel(), out.data_ptr(), out.numel(), None)
+    torch.cuda.synchronize()
+    if status == 0:
+        assert rc == 0
+        assert torch.equal(out.view(torch.int32), cpbp_reduce(dev, w).view(torch.int32))
+    else:
+        assert N.STATUS_NAMES.get(rc) == status, rc
+        assert torch.all(out == -7.0)
