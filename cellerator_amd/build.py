@@ -48,6 +48,7 @@ ENGINE_SOURCES = [
     "bell_lowering.cpp",
     "spmm_request.cpp",
     "qcsr_codec.hip",
+    "cpe2.cpp",
     "qcsr_hybrid.hip",
 ]
 SYNTH_SOURCES = ["synth.hip"]

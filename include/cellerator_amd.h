@@ -999,6 +999,167 @@ int cx_cpk1_rebind(const cx_cpk1_view *validated, const void *new_base, uint64_t
                    cx_cpk1_view *out);
 const char *cx_cpk1_last_error(void);
 
+/* ---- CPE2 execution image (components/CellPack/include/CellPack/persistence/
+ * execution_image_v2.hh, EXECUTION_IMAGE_V2.md) ---------------------------------------------
+ * Pointer-free container of one relation / semantic geometry and a directory of projections
+ * of it; the byte format, checks and messages are the reference's. Host build and validate;
+ * rebind and prebind only form addresses (a device destination is never touched). */
+#define CX_CPE2_SCHEMA_VERSION 2u
+#define CX_CPE2_PAYLOAD_KIND 0x43504532u /* "CPE2" */
+#define CX_CPE2_ALIGNMENT 64u
+#define CX_CPE2_ENDIAN_MARKER 0x01020304u
+#define CX_CPE2_INVALID_INDEX 0xffffffffu
+/* execution_section_kind */
+#define CX_CPE2_SECTION_DOMAIN_TABLE 1u
+#define CX_CPE2_SECTION_ORDER_PARTITION_TABLE 2u
+#define CX_CPE2_SECTION_RELATION_STRUCTURE 3u
+#define CX_CPE2_SECTION_SEMANTIC_GEOMETRY 4u
+#define CX_CPE2_SECTION_INITIAL_VALUES 5u
+#define CX_CPE2_SECTION_PROJECTION_PAYLOAD 6u
+#define CX_CPE2_SECTION_FORWARD_VALUE_MAP 7u
+#define CX_CPE2_SECTION_TRANSPOSE_VALUE_MAP 8u
+#define CX_CPE2_SECTION_HIERARCHY_PARTITION_INDEX 9u
+#define CX_CPE2_SECTION_SCHEDULING_SUMMARY 10u
+#define CX_CPE2_SECTION_CPK1_V1_COMPATIBILITY 11u
+/* execution_projection_kind */
+#define CX_CPE2_PROJECTION_NATIVE_ROW_MASKED 1u
+#define CX_CPE2_PROJECTION_CSR 5u
+#define CX_CPE2_PROJECTION_BLOCKED_ELL 8u
+#define CX_CPE2_PROJECTION_ARCHITECTURE_SPECIFIC 11u
+/* execution_directory_flags */
+#define CX_CPE2_DIRECTORY_OPTIONAL 1u
+#define CX_CPE2_DIRECTORY_DEVICE_READABLE 2u
+#define CX_CPE2_PROJECTION_LAZY_CONSTRUCTIBLE 4u
+#define CX_CPE2_PROJECTION_FORWARD_CAPABLE 8u
+#define CX_CPE2_PROJECTION_TRANSPOSE_CAPABLE 16u
+
+typedef struct cx_cpe2_id {
+    uint64_t low, high;
+} cx_cpe2_id;
+
+typedef struct cx_cpe2_axis_record {  /* execution_axis_record_v1 */
+    uint64_t domain_low, domain_high, order_low, order_high;
+    uint64_t geometry_low, geometry_high, partition_low, partition_high;
+} cx_cpe2_axis_record;
+
+typedef struct cx_cpe2_axis_identity {  /* persistent_axis_identity (execution/identity.hh:94-100) */
+    uint16_t schema_version;            /* 1 */
+    uint16_t record_kind;               /* 1 */
+    uint32_t byte_count;                /* 72 */
+    cx_cpe2_id domain, order, geometry, partition;
+} cx_cpe2_axis_identity;
+
+typedef struct cx_cpe2_header {  /* execution_image_v2_header, 256 bytes */
+    unsigned char magic[8];      /* "CELLEX02" */
+    uint32_t schema_version;
+    uint32_t header_bytes;
+    uint32_t endian;
+    uint32_t alignment;
+    uint64_t image_bytes;
+    uint64_t image_identity;
+    uint64_t structure_identity_low, structure_identity_high;
+    uint64_t structure_epoch;
+    uint64_t semantic_geometry_identity_low, semantic_geometry_identity_high;
+    uint64_t projection_catalog_identity_low, projection_catalog_identity_high;
+    uint64_t initial_value_generation;
+    cx_cpe2_axis_record source_axis;
+    cx_cpe2_axis_record destination_axis;
+    uint32_t section_count;
+    uint32_t projection_count;
+    uint64_t section_directory_offset;
+    uint64_t projection_directory_offset;
+} cx_cpe2_header;
+
+typedef struct cx_cpe2_section_entry {  /* execution_section_entry_v1, 64 bytes */
+    uint32_t kind, schema_version, flags, alignment;
+    uint64_t identity_low, identity_high;
+    uint64_t offset, bytes, checksum;
+    uint32_t element_count, element_bytes;
+} cx_cpe2_section_entry;
+
+typedef struct cx_cpe2_projection_entry {  /* execution_projection_entry_v1, 64 bytes */
+    uint64_t identity_low, identity_high;
+    uint32_t kind, schema_version, flags, operation_family;
+    uint16_t storage_type, compute_type, accumulation_type, orientation;
+    uint32_t architecture_class;
+    uint32_t payload_section, forward_map_section, transpose_map_section;
+    uint32_t scheduling_summary_section, capability_section;
+} cx_cpe2_projection_entry;
+
+typedef struct cx_cpe2_section_source {
+    uint32_t kind, schema_version, flags, alignment;
+    uint64_t identity_low, identity_high;
+    const void *data;
+    uint64_t bytes;
+    uint32_t element_count, element_bytes;
+} cx_cpe2_section_source;
+
+typedef struct cx_cpe2_build_request {
+    cx_cpe2_id structure_identity;
+    uint64_t structure_epoch;
+    cx_cpe2_id semantic_geometry_identity;
+    cx_cpe2_id projection_catalog_identity;
+    uint64_t initial_value_generation;
+    cx_cpe2_axis_identity source_axis;
+    cx_cpe2_axis_identity destination_axis;
+    const cx_cpe2_section_source *sections;
+    uint32_t section_count, reserved;
+    const cx_cpe2_projection_entry *projections;
+    uint32_t projection_count, reserved2;
+} cx_cpe2_build_request;
+
+typedef struct cx_cpe2_requirements {
+    uint64_t image_bytes, directory_bytes, section_bytes, alignment_padding_bytes;
+} cx_cpe2_requirements;
+
+typedef struct cx_cpe2_expected {
+    cx_cpe2_id structure_identity;
+    uint64_t structure_epoch;
+    cx_cpe2_id semantic_geometry_identity;
+    cx_cpe2_id projection_catalog_identity;
+    uint64_t image_identity;  /* 0 = any */
+} cx_cpe2_expected;
+
+typedef struct cx_cpe2_view {
+    cx_cpe2_header header;
+    const void *image_base;
+    uint64_t image_bytes;
+    const cx_cpe2_section_entry *sections;
+    const cx_cpe2_projection_entry *projections;
+} cx_cpe2_view;
+
+typedef struct cx_cpe2_prebound_projection {  /* prebound_projection_view_v1 */
+    cx_cpe2_projection_entry descriptor;
+    const void *payload;
+    uint64_t payload_bytes;
+    const void *forward_map;
+    uint64_t forward_map_bytes;
+    const void *transpose_map;
+    uint64_t transpose_map_bytes;
+    const void *scheduling_summary;
+    uint64_t scheduling_summary_bytes;
+} cx_cpe2_prebound_projection;
+
+/* query_execution_image_v2_requirements_host (execution_image_v2.cc:288-300) */
+int cx_cpe2_query_requirements(const cx_cpe2_build_request *request, cx_cpe2_requirements *out);
+/* build_execution_image_v2_host (:302-377): writes and then validates the image. */
+int cx_cpe2_build(const cx_cpe2_build_request *request, void *image, uint64_t capacity, cx_cpe2_view *out);
+/* validate_execution_image_v2_host (:379-518). */
+int cx_cpe2_validate(const void *image, uint64_t image_bytes, const cx_cpe2_expected *expected, cx_cpe2_view *out);
+/* rebind_execution_image_v2 (:520-541): directory pointers of an equal-sized copy. */
+int cx_cpe2_rebind(const cx_cpe2_view *validated, const void *new_base, uint64_t new_bytes, cx_cpe2_view *out);
+/* prebind_execution_projection_host / _for_base_host (:543-591): hot pointers = base +
+ * validated section offset; no dereference of destination_base. */
+int cx_cpe2_prebind(const cx_cpe2_view *validated_host, uint32_t projection_index, cx_cpe2_prebound_projection *out);
+int cx_cpe2_prebind_for_base(const cx_cpe2_view *validated_host, uint32_t projection_index,
+                             const void *destination_base, uint64_t destination_bytes,
+                             cx_cpe2_prebound_projection *out);
+/* load_cpk1_v1_compatibility_host (execution_image_v2_cpk1.cc:5-31): the CPK1 section of a
+ * native row-masked projection through the CPK1 validator, unconverted. */
+int cx_cpe2_load_cpk1(const cx_cpe2_view *validated_host, uint32_t projection_index,
+                      const cx_cpk1_expected *expected, cx_cpk1_view *out);
+const char *cx_cpe2_last_error(void);
+
 /* ---- CP-BP reduction under the reference's full direct-consumer contract ----------------
  * feature_weighted_row_reduction_view (components/CellPack/include/CellPack/
  * feature_weighted_row_reduction.hh:20-44) with the warp_tile_view identity fields
