@@ -206,7 +206,13 @@ FEATURE_ORDER_CANONICAL, FEATURE_ORDER_PACKED = 1, 2
 class CxQcsrHybridLayout(C.Structure):
     _fields_ = [("head_cols", u32), ("rows", u32), ("rows_ld", u32), ("bits", u32), ("decode_policy", u32),
                 ("scale_exp", i32), ("nnz", u64), ("codes", p_void), ("masks", p_void), ("head_end", p_void),
-                ("meta", p_void), ("row_offsets", p_void)]
+                ("meta", p_void), ("row_offsets", p_void), ("tail", p_void)]
+
+
+class CxQcsrTailStream(C.Structure):
+    _fields_ = [("rows", u32), ("first_part", u32), ("parts", u32), ("blocks", u32), ("bits", u32),
+                ("entry_bytes", u32), ("fills", u64), ("nnz", u64), ("slot_rows", p_void), ("fill_index", p_void),
+                ("entries", p_void)]
 
 
 # ---- public context ABI structs (include/Cellerator/abi.h layout) ----
@@ -312,6 +318,11 @@ ENGINE_SIGNATURES = {
     "cx_qcsr_hybrid_prepare": (C.c_int, [C.POINTER(CxQcsrMatrix), u32, p_void, u64,
                                          C.POINTER(CxQcsrHybridLayout), p_void]),
     "cx_qcsr_hybrid_workspace": (C.c_int, [C.POINTER(CxQcsrMatrix), u32, i64, C.POINTER(u64)]),
+    "cx_qcsr_tail_plan_bytes": (C.c_int, [C.POINTER(CxQcsrMatrix), C.POINTER(CxQcsrHybridLayout), C.POINTER(u64)]),
+    "cx_qcsr_tail_plan": (C.c_int, [C.POINTER(CxQcsrMatrix), C.POINTER(CxQcsrHybridLayout), p_void, u64,
+                                    C.POINTER(CxQcsrTailStream), C.POINTER(u64), p_void]),
+    "cx_qcsr_tail_fill": (C.c_int, [C.POINTER(CxQcsrMatrix), C.POINTER(CxQcsrHybridLayout),
+                                    C.POINTER(CxQcsrTailStream), p_void, u64, p_void]),
     "cx_qcsr_spmm_fwd_hybrid": (C.c_int, [C.POINTER(CxQcsrMatrix), C.POINTER(CxQcsrHybridLayout), p_void, i64,
                                           i64, p_void, i64, C.POINTER(CxSpmmEpilogue), p_void, u64, p_void]),
     "cx_cpbp_builder_create": (C.c_int, [C.POINTER(CxCpbpPlan), C.POINTER(CxCpbpCsr),

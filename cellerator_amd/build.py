@@ -50,6 +50,7 @@ ENGINE_SOURCES = [
     "qcsr_codec.hip",
     "cpe2.cpp",
     "qcsr_hybrid.hip",
+    "qcsr_stream.hip",
 ]
 SYNTH_SOURCES = ["synth.hip"]
 

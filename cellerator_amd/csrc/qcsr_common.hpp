@@ -30,7 +30,32 @@ struct QcsrArgs {
     const std::int32_t *row_start;
     const float *acc_init;
     std::uint32_t first_part;
+    // Prepared tail stream (qcsr_spmm_stream only; built by qcsr_stream.hip): the row of
+    // every (block, wave, layer, group) slot, the fill index, the entries in fill order, and
+    // the number of gene parts the stream covers (from first_part on).
+    const std::uint32_t *slot_rows;
+    const std::uint32_t *fill_index;
+    const void *stream_entries;
+    std::uint32_t stream_parts;
 };
+
+// Geometry of the prepared tail stream, shared by its builder and its kernel: 16 waves of
+// 4 layers of 8 rows per 512-row block; a fill is 16 steps of the 8 lane groups of a
+// layer, 128 entries stored group-major ([group][step]); entries are u16
+// (gene in part | code << 11) for codes of up to 4 bits and u32 (gene | code << 16) for
+// 8-bit codes. fill_index[(block * parts + part) * 64 + wave * 4 + layer] holds the
+// layer's first fill (low 28 bits) and the step count of its last fill minus one (high 4
+// bits); the entry after the last is the total.
+constexpr int kStreamWaves = 16;
+constexpr int kStreamLayers = 4;
+constexpr int kStreamSlots = kStreamWaves * kStreamLayers;        // (wave, layer) per block and part
+constexpr int kStreamRows = kStreamSlots * 8;
+constexpr std::uint32_t kFillMask = 0x0fffffffu;
+constexpr int kStreamPartGenes = 1024;
+constexpr std::uint32_t kStreamPad = 1024u;                       // gene of a pad entry: the zero row
+
+// One 64-column block of the tail through the prepared stream (fp16 weights).
+int launch_qcsr_stream(const QcsrArgs &a, std::uint32_t bits, std::uint32_t policy, hipStream_t stream);
 
 constexpr int kWavesPerBlock = 4;
 

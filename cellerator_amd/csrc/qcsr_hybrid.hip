@@ -622,8 +622,38 @@ extern "C" int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *m, const cx_qcsr_hy
     a.rows = m->rows;
     a.cols = m->cols;
     a.flags = m->flags;
+    const cx_qcsr_tail_stream *ts = L.tail;
+    if (ts != nullptr) {
+        const std::uint32_t all_parts = (m->cols + kHeadAlign - 1u) / kHeadAlign;
+        if (ts->rows != m->rows || ts->bits != m->bits || ts->nnz != m->nnz || ts->first_part != L.head_cols / kHeadAlign
+            || ts->parts != all_parts - ts->first_part || ts->blocks != (m->rows + kStreamRows - 1u) / kStreamRows
+            || ts->slot_rows == nullptr || ts->fill_index == nullptr || ts->entries == nullptr)
+            return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd_hybrid: the tail stream was not built for this layout");
+        a.slot_rows = ts->slot_rows;
+        a.fill_index = ts->fill_index;
+        a.stream_entries = ts->entries;
+        a.stream_parts = ts->parts;
+        a.first_part = ts->first_part;
+    }
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (L.head_cols == 0u) return launch_qcsr_parts(a, m->bits, m->decode_policy, out_cols, s);
+    // one 64-column block of the tail: the prepared stream, else the row-group kernel
+    auto tail = [&](const QcsrArgs &b) {
+        return ts != nullptr ? launch_qcsr_stream(b, m->bits, m->decode_policy, s)
+                             : launch_qcsr_parts(b, m->bits, m->decode_policy, 64, s);
+    };
+    if (L.head_cols == 0u) {
+        if (ts == nullptr) return launch_qcsr_parts(a, m->bits, m->decode_policy, out_cols, s);
+        for (std::int64_t c0 = 0; c0 < out_cols; c0 += 64) {
+            QcsrArgs b = a;
+            b.rhs = static_cast<const std::uint16_t *>(rhs) + c0;
+            b.out = out + c0;
+            if (b.ep.bias != nullptr) b.ep.bias += c0;
+            if (b.ep.initial != nullptr) b.ep.initial += c0;
+            rc = tail(b);
+            if (rc != CX_STATUS_SUCCESS) return rc;
+        }
+        return CX_STATUS_SUCCESS;
+    }
     auto *partial = static_cast<float *>(workspace);
     auto *panel = reinterpret_cast<std::uint16_t *>(static_cast<unsigned char *>(workspace)
                                                     + align256(static_cast<std::uint64_t>(m->rows) * 256u));
@@ -642,7 +672,7 @@ extern "C" int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *m, const cx_qcsr_hy
         b.row_start = L.head_end;
         b.acc_init = partial;
         b.first_part = L.head_cols / kHeadAlign;
-        rc = launch_qcsr_parts(b, m->bits, m->decode_policy, 64, s);
+        rc = tail(b);
         if (rc != CX_STATUS_SUCCESS) return rc;
     }
     return CX_STATUS_SUCCESS;

@@ -478,6 +478,186 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
     }
 }
 
+// ---- the row-group walk over a prepared tail stream ------------------------------------------
+//
+// Same rows per lane group, registers, part copies and step loop as qcsr_spmm_groups, but the
+// entries come prepared (qcsr_stream.hip): for each (block, part, wave, layer) the layer's
+// runs are stored as fills of 16 steps x 8 lane groups in the order the stage holds them,
+// and the fill index gives their position and the last fill's step count. So a pass loads
+// one dword (two entries) per lane per fill, decodes it into the stage and steps; there is
+// no window, run count or reload, and no per-row fallback (the builder rejects what the
+// walk could not finish). The builder orders each group's run by gene parity, even-first in
+// even groups and odd-first in odd groups: a weight row of gene g covers the LDS bank half
+// g & 1, and groups 2i and 2i+1 read in the same LDS cycle, so their reads fall in
+// different halves until one of them runs out of its preferred parity.
+
+struct StreamShared {
+    uint4 stage[kStreamWaves][8][9];  // per wave and lane group: 16 (gene * 8, value) pairs (+16 B pad)
+    float2 meta[kPartGenes + 2];      // (scale, offset) per gene of the part; [kPadGene] = (0, 0)
+    uint4 w[(kPartGenes + 1) * 8];    // fp16 weight rows of the part; row kPadGene is zeros
+};
+
+static_assert(kPadGene == static_cast<int>(kStreamPad) && kPartGenes == kStreamPartGenes,
+              "the stream builder and the part walk must agree on parts and pads");
+
+// Entries of one lane for one fill: group g's stage slots 2j, 2j + 1.
+template<bool kWide>
+struct FillWord {
+    std::uint32_t w[kWide ? 2 : 1];
+};
+
+template<bool kWide>
+__device__ __forceinline__ FillWord<kWide> load_fill(rsrc_t r, std::uint32_t offset) {
+    FillWord<kWide> q;
+    if constexpr (kWide) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, offset, 0, 0);
+        q.w[0] = v[0];
+        q.w[1] = v[1];
+    } else {
+        q.w[0] = static_cast<std::uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, 0));
+    }
+    return q;
+}
+
+template<int kBits, int kPolicy>
+__global__ __launch_bounds__(kStreamWaves * kWave) void qcsr_spmm_stream(QcsrArgs a) {
+    constexpr int kWaves = kStreamWaves, kLayers = kStreamLayers;
+    constexpr bool kWide = kBits == 8;
+    constexpr std::uint32_t kFillBytes = kWide ? 512u : 256u;
+    __shared__ StreamShared sh;
+    const int tid = static_cast<int>(threadIdx.x);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int lane = tid % kWave;
+    const int grp = lane >> 3;
+    const int j = lane & 7;
+    const std::uint32_t block = blockIdx.x;
+
+    if (tid < 8) sh.w[kPadGene * 8 + tid] = make_uint4(0u, 0u, 0u, 0u);
+    if (tid == 8) sh.meta[kPadGene] = make_float2(0.0f, 0.0f);
+
+    const int parts = static_cast<int>(a.stream_parts);
+    const std::uint32_t *ix = a.fill_index + static_cast<std::uint64_t>(block) * parts * kStreamSlots;
+    const std::uint32_t blk_first = __builtin_amdgcn_readfirstlane(ix[0]) & kFillMask;
+    const std::uint32_t blk_end =
+        __builtin_amdgcn_readfirstlane(ix[static_cast<std::uint64_t>(parts) * kStreamSlots]) & kFillMask;
+    // the block's fills, addressed by 32-bit offsets (the builder bounds a block's bytes)
+    const rsrc_t re = make_rsrc(static_cast<const char *>(a.stream_entries) + static_cast<std::uint64_t>(blk_first) * kFillBytes,
+                                (blk_end - blk_first) * kFillBytes);
+    const std::uint32_t lane_off = static_cast<std::uint32_t>(grp * 16 + 2 * j) * (kWide ? 4u : 2u);
+
+    float acc[kLayers][8];
+    float roff[kLayers];
+    std::uint32_t rows[kLayers];
+#pragma unroll
+    for (int l = 0; l < kLayers; ++l) {
+        const std::uint32_t row = a.slot_rows[static_cast<std::uint64_t>(block) * kStreamRows + (wave * kLayers + l) * 8 + grp];
+        rows[l] = row;
+        roff[l] = 0.0f;
+        if constexpr (kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET)
+            roff[l] = row != kNoRow && a.row_offsets != nullptr ? a.row_offsets[row] : 0.0f;
+        if (a.acc_init != nullptr && row != kNoRow) {
+            const float4 *init = reinterpret_cast<const float4 *>(a.acc_init + static_cast<std::int64_t>(row) * 64 + 8 * j);
+            const float4 i0 = init[0], i1 = init[1];
+            acc[l][0] = i0.x; acc[l][1] = i0.y; acc[l][2] = i0.z; acc[l][3] = i0.w;
+            acc[l][4] = i1.x; acc[l][5] = i1.y; acc[l][6] = i1.z; acc[l][7] = i1.w;
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc[l][k] = 0.0f;
+        }
+    }
+
+    const char *wbase = reinterpret_cast<const char *>(sh.w) + j * 16;
+    const char *mbase = reinterpret_cast<const char *>(sh.meta);
+    uint4 *sp = &sh.stage[wave][grp][0];
+    const int cols = static_cast<int>(a.cols);
+
+    for (int p = 0; p < parts; ++p) {
+        const int lo = (static_cast<int>(a.first_part) + p) * kPartGenes;
+        const int hi = lo + kPartGenes < cols ? lo + kPartGenes : cols;
+        const std::uint32_t *wx = ix + static_cast<std::uint64_t>(p) * kStreamSlots + wave * kLayers;
+        std::uint32_t b[kLayers + 1];
+#pragma unroll
+        for (int k = 0; k <= kLayers; ++k) b[k] = __builtin_amdgcn_readfirstlane(wx[k]);
+        const std::uint32_t s_all = b[0] & kFillMask;
+        // the wave's first three fills of the part load behind the part copy
+        FillWord<kWide> q0 = load_fill<kWide>(re, (s_all - blk_first) * kFillBytes + lane_off);
+        FillWord<kWide> q1 = load_fill<kWide>(re, (s_all + 1u - blk_first) * kFillBytes + lane_off);
+        FillWord<kWide> q2 = load_fill<kWide>(re, (s_all + 2u - blk_first) * kFillBytes + lane_off);
+        __syncthreads();  // every wave is done reading part p - 1
+        load_part<kPolicy, kWaves>(sh, a, lo, hi, wave, lane, tid);
+        __syncthreads();
+        std::uint32_t f = s_all;
+#pragma unroll
+        for (int l = 0; l < kLayers; ++l) {
+            const std::uint32_t e_l = b[l + 1] & kFillMask;
+            const int last = static_cast<int>(b[l] >> 28) + 1;
+            for (; f < e_l; ++f) {
+                const FillWord<kWide> cur = q0;
+                q0 = q1;
+                q1 = q2;
+                q2 = load_fill<kWide>(re, (f + 3u - blk_first) * kFillBytes + lane_off);  // past the block: zeros, never used
+                std::uint32_t st[4];
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    std::uint32_t g, code;
+                    if constexpr (kWide) {
+                        g = cur.w[r] & 0xffffu;
+                        code = cur.w[r] >> 16;
+                    } else {
+                        const std::uint32_t e = r == 0 ? (cur.w[0] & 0xffffu) : (cur.w[0] >> 16);
+                        g = e & 0x7ffu;
+                        code = e >> 11;
+                    }
+                    g = min(g, static_cast<std::uint32_t>(kPadGene));  // keeps a damaged stream inside LDS
+                    const float2 md = *reinterpret_cast<const float2 *>(mbase + g * 8u);
+                    const float off = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET
+                        ? (g != static_cast<std::uint32_t>(kPadGene) ? roff[l] : 0.0f) : md.y;
+                    st[2 * r] = g * 8u;
+                    st[2 * r + 1] = __float_as_uint(__builtin_fmaf(static_cast<float>(code), md.x, off));
+                }
+                sp[j] = make_uint4(st[0], st[1], st[2], st[3]);
+                const int cnt = f + 1u < e_l ? 16 : last;
+                const int n2 = cnt >> 1;
+                int it = 0;
+                for (; it + 2 <= n2; it += 2) {
+                    const uint4 ea = sp[it], eb = sp[it + 1];
+                    const uint4 wa0 = *reinterpret_cast<const uint4 *>(wbase + (ea.x << 4));
+                    const uint4 wa1 = *reinterpret_cast<const uint4 *>(wbase + (ea.z << 4));
+                    const uint4 wb0 = *reinterpret_cast<const uint4 *>(wbase + (eb.x << 4));
+                    const uint4 wb1 = *reinterpret_cast<const uint4 *>(wbase + (eb.z << 4));
+                    fma8(acc[l], __uint_as_float(ea.y), wa0);
+                    fma8(acc[l], __uint_as_float(ea.w), wa1);
+                    fma8(acc[l], __uint_as_float(eb.y), wb0);
+                    fma8(acc[l], __uint_as_float(eb.w), wb1);
+                }
+                if (it < n2) {
+                    const uint4 e = sp[it];
+                    const uint4 w0 = *reinterpret_cast<const uint4 *>(wbase + (e.x << 4));
+                    const uint4 w1 = *reinterpret_cast<const uint4 *>(wbase + (e.z << 4));
+                    fma8(acc[l], __uint_as_float(e.y), w0);
+                    fma8(acc[l], __uint_as_float(e.w), w1);
+                }
+                if ((cnt & 1) != 0) {
+                    const uint2 e = reinterpret_cast<const uint2 *>(sp)[cnt - 1];
+                    fma8(acc[l], __uint_as_float(e.y), *reinterpret_cast<const uint4 *>(wbase + (e.x << 4)));
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int l = 0; l < kLayers; ++l) {
+        const std::uint32_t row = rows[l];
+        if (row == kNoRow) continue;
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = a.ep.active ? epilogue_value(a.ep, acc[l][k], row, 8 * j + k) : acc[l][k];
+        float4 *o = reinterpret_cast<float4 *>(a.out + static_cast<std::int64_t>(row) * a.out_ld + 8 * j);
+        o[0] = make_float4(v[0], v[1], v[2], v[3]);
+        o[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+}
+
 // ---- backward values in the row-group form -------------------------------------------------
 //
 // grad_values[i] = <G[row_i, :], W[col_i, :]> (64 columns) with the forward's row-group walk:
@@ -784,6 +964,27 @@ int launch_bwd_values_parts(const std::int32_t *row_ptr, const std::int32_t *col
     else
         hipLaunchKernelGGL((qcsr_bwd_values_groups<kWaves, kLayers, false>), grid, block, 0, stream, a);
     return check_launch("qcsr_bwd_values_groups");
+}
+
+int launch_qcsr_stream(const QcsrArgs &a, std::uint32_t bits, std::uint32_t policy, hipStream_t stream) {
+    const unsigned blocks = (a.rows + kStreamRows - 1) / kStreamRows;
+    const dim3 grid(blocks), block(kStreamWaves * kWave);
+#define CX_STREAM(B, P) hipLaunchKernelGGL((qcsr_spmm_stream<B, P>), grid, block, 0, stream, a)
+#define CX_STREAM_POLICY(B)                                                                         \
+    do {                                                                                            \
+        if (policy == CX_DECODE_PER_GENE_AFFINE_PAIRS) CX_STREAM(B, CX_DECODE_PER_GENE_AFFINE_PAIRS);   \
+        else if (policy == CX_DECODE_PER_GENE_AFFINE) CX_STREAM(B, CX_DECODE_PER_GENE_AFFINE);          \
+        else CX_STREAM(B, CX_DECODE_COLUMN_SCALE_ROW_OFFSET);                                           \
+    } while (0)
+    switch (bits) {
+    case 1: CX_STREAM_POLICY(1); break;
+    case 2: CX_STREAM_POLICY(2); break;
+    case 4: CX_STREAM_POLICY(4); break;
+    default: CX_STREAM_POLICY(8); break;
+    }
+#undef CX_STREAM_POLICY
+#undef CX_STREAM
+    return check_launch("qcsr_spmm_stream");
 }
 
 int launch_qcsr_parts(const QcsrArgs &a, std::uint32_t bits, std::uint32_t policy, std::int64_t out_cols,

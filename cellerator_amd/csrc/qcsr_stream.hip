@@ -1,0 +1,381 @@
+// qcsr_stream.hip -- the prepared tail stream of an execution-order quantized CSR: the
+// entries of every row from its first tail entry (head_end of the hybrid layout) on,
+// rearranged once per structure into the order the row-group walk consumes them
+// (qcsr_spmm_stream in qcsr_parts.hip), so the walk loads them instead of finding them.
+//
+// Geometry (qcsr_common.hpp): blocks of 512 rows; in each block the rows are ranked by tail
+// length (descending, ties by row) and ranks 8s .. 8s + 7 form row set s, dealt to the 16
+// waves in snake order (set s -> layer s / 16), which is how the part walk balances its
+// waves. For gene part p and layer (wave w, layer l) the 8 rows' runs in the part are
+// r_0 .. r_7; the layer gets ceil(max r_g / 16) fills of 128 entries, entry k of group g's
+// run at fill k / 16, slot g * 16 + k % 16; unused slots hold the pad gene (the zero
+// weight row, value 0). Each group's run is stored even genes first in even groups and odd
+// genes first in odd groups (the LDS bank half of a weight row is its gene's parity).
+//
+// Building: plan (slot rows and each layer's fill count and last step count), an exclusive
+// scan of the counts into the fill index, then the fill. The plan and the fill walk each
+// row the same way (a run is the entries from the cursor while the gene is below the
+// part's end), so a fill never exceeds its plan; a row whose genes are not non-decreasing
+// within [head, cols) -- which the columns-sorted flag promised -- is reported instead.
+#include "qcsr_common.hpp"
+
+#include <algorithm>
+
+namespace cx {
+namespace {
+
+constexpr int kPlanChunk = 32;  // parts counted per pass of the plan kernel (LDS: 32 KB of runs)
+constexpr std::uint32_t kNoSlotRow = 0xffffffffu;
+
+struct PlanArgs {
+    const std::int32_t *row_ptr;
+    const std::int32_t *col_idx;
+    const std::int32_t *head_end;
+    std::uint32_t rows;
+    std::uint32_t cols;
+    std::uint32_t first_part;
+    std::uint32_t parts;          // parts in the stream
+    std::uint32_t *slot_rows;     // [blocks][512]
+    std::uint32_t *counts;        // [blocks * parts * 64 + 1]: fills per layer and part (last: 0)
+    std::uint8_t *lasts;          // [blocks * parts * 64]: step count of the last fill (0: none)
+    std::uint32_t *error;         // [0]: a row not sorted within [head, cols); [1]: a block's fills reach 4 GiB
+};
+
+// Ranks the block's rows by tail length and records the row of every slot.
+__device__ __forceinline__ std::uint32_t rank_slot(int *len, std::uint32_t *slot_row, const PlanArgs &a,
+                                                   std::uint32_t first, int tid) {
+    const std::uint32_t row = first + static_cast<std::uint32_t>(tid);
+    len[tid] = row < a.rows ? a.row_ptr[row + 1] - a.head_end[row] : -1;
+    __syncthreads();
+    const int my = len[tid];
+    int rank = 0;
+    for (int u = 0; u < kStreamRows; ++u) {
+        const int v = len[u];
+        rank += v > my || (v == my && u < tid) ? 1 : 0;
+    }
+    const int set = rank / 8, g = rank % 8;
+    const int round = set / kStreamWaves, pos = set % kStreamWaves;
+    const int w = (round & 1) != 0 ? kStreamWaves - 1 - pos : pos;
+    const int slot = (w * kStreamLayers + round) * 8 + g;
+    slot_row[slot] = row < a.rows ? row : kNoSlotRow;
+    __syncthreads();
+    return slot_row[tid];  // thread tid now works for slot tid
+}
+
+__global__ __launch_bounds__(kStreamRows) void stream_plan_kernel(PlanArgs a) {
+    __shared__ int len[kStreamRows];
+    __shared__ std::uint32_t slot_row[kStreamRows];
+    __shared__ std::uint16_t runs[kPlanChunk][kStreamRows];
+    const int tid = static_cast<int>(threadIdx.x);
+    const std::uint32_t block = blockIdx.x;
+    const std::uint32_t first = block * kStreamRows;
+    const std::uint32_t row = rank_slot(len, slot_row, a, first, tid);
+    a.slot_rows[static_cast<std::uint64_t>(block) * kStreamRows + tid] = row;
+
+    std::int64_t cur = 0, end = 0;
+    if (row != kNoSlotRow) {
+        cur = a.head_end[row];
+        end = a.row_ptr[row + 1];
+    }
+    bool bad = false;
+    for (std::uint32_t c0 = 0; c0 < a.parts; c0 += kPlanChunk) {
+        const std::uint32_t cn = min(static_cast<std::uint32_t>(kPlanChunk), a.parts - c0);
+        for (std::uint32_t c = 0; c < cn; ++c) {
+            const std::int64_t lo = static_cast<std::int64_t>(a.first_part + c0 + c) * kStreamPartGenes;
+            const std::int64_t hi = std::min<std::int64_t>(lo + kStreamPartGenes, a.cols);
+            int n = 0;
+            while (cur < end) {
+                const std::int64_t g = a.col_idx[cur];
+                if (g >= hi) break;
+                if (g < lo) bad = true;  // below the part (or the head): not sorted
+                ++cur;
+                ++n;
+            }
+            runs[c][tid] = static_cast<std::uint16_t>(min(n, 0xffff));
+            if (n > 0xffff) bad = true;
+        }
+        __syncthreads();
+        // one (part, wave, layer) per thread-iteration: the largest run of its 8 groups
+        for (int t = tid; t < static_cast<int>(cn) * kStreamSlots; t += kStreamRows) {
+            const int c = t / kStreamSlots, s = t % kStreamSlots;
+            int m = 0;
+#pragma unroll
+            for (int g = 0; g < 8; ++g) m = max(m, static_cast<int>(runs[c][s * 8 + g]));
+            const std::uint64_t k = (static_cast<std::uint64_t>(block) * a.parts + c0 + c) * kStreamSlots + s;
+            const int fills = (m + 15) / 16;
+            a.counts[k] = static_cast<std::uint32_t>(fills);
+            a.lasts[k] = static_cast<std::uint8_t>(fills == 0 ? 0 : m - 16 * (fills - 1));
+        }
+        __syncthreads();
+    }
+    if (cur != end) bad = true;  // genes at or past cols, or negative: the walk could not finish
+    if (bad) atomicOr(&a.error[0], 1u);
+}
+
+// index[k] = first fill | (last steps - 1) << 28; the scan left the first fills in index.
+// The walk addresses a block's fills by 32-bit byte offsets: a block needing 2^32 bytes or
+// more of fills is reported (error word 1).
+__global__ __launch_bounds__(256) void stream_pack_kernel(std::uint32_t *index, const std::uint8_t *lasts,
+                                                          std::uint64_t n, std::uint64_t per_block,
+                                                          std::uint32_t max_block_fills, std::uint32_t *error) {
+    const std::uint64_t k = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (k >= n) return;
+    const std::uint32_t first = index[k] & kFillMask;
+    if (k % per_block == 0u && (index[k + per_block] & kFillMask) - first >= max_block_fills) atomicOr(&error[1], 1u);
+    if (lasts[k] != 0u) index[k] = first | static_cast<std::uint32_t>(lasts[k] - 1u) << 28;
+}
+
+__global__ __launch_bounds__(256) void fill_pattern_kernel(std::uint32_t *p, std::uint64_t words, std::uint32_t v) {
+    for (std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < words;
+         i += static_cast<std::uint64_t>(gridDim.x) * blockDim.x)
+        p[i] = v;
+}
+
+struct FillArgs {
+    const std::int32_t *row_ptr;
+    const std::int32_t *packed_row_ptr;
+    const std::int32_t *col_idx;
+    const std::uint8_t *packed;
+    const std::int32_t *head_end;
+    const std::uint32_t *slot_rows;
+    const std::uint32_t *index;
+    void *entries;
+    std::uint32_t cols;
+    std::uint32_t first_part;
+    std::uint32_t parts;
+};
+
+// One thread per slot: walks its row's tail part by part (the plan's walk) and writes each
+// run in parity order at its fills.
+template<int kBits>
+__global__ __launch_bounds__(kStreamRows) void stream_fill_kernel(FillArgs a) {
+    constexpr bool kWide = kBits == 8;
+    constexpr std::uint32_t kMask = (1u << kBits) - 1u;
+    const int slot = static_cast<int>(threadIdx.x);
+    const std::uint32_t block = blockIdx.x;
+    const std::uint32_t row = a.slot_rows[static_cast<std::uint64_t>(block) * kStreamRows + slot];
+    if (row == kNoSlotRow) return;
+    const int layer_slot = slot / 8, g = slot % 8;
+    const std::uint32_t pref = static_cast<std::uint32_t>(g & 1);  // parity stored first
+    const std::int64_t rb = a.row_ptr[row], end = a.row_ptr[row + 1];
+    const std::int64_t pbit = static_cast<std::int64_t>(a.packed_row_ptr[row]) * 8;
+    std::int64_t cur = a.head_end[row];
+    for (std::uint32_t p = 0; p < a.parts && cur < end; ++p) {
+        const std::int64_t lo = static_cast<std::int64_t>(a.first_part + p) * kStreamPartGenes;
+        const std::int64_t hi = std::min<std::int64_t>(lo + kStreamPartGenes, a.cols);
+        std::int64_t stop = cur;
+        while (stop < end && a.col_idx[stop] < hi) ++stop;
+        if (stop == cur) continue;
+        const std::uint32_t fill0 =
+            a.index[(static_cast<std::uint64_t>(block) * a.parts + p) * kStreamSlots + layer_slot] & kFillMask;
+        std::uint32_t k = 0;
+        for (int pass = 0; pass < 2; ++pass) {
+            for (std::int64_t e = cur; e < stop; ++e) {
+                const std::int64_t gene = a.col_idx[e];
+                const std::uint32_t local = gene >= lo ? static_cast<std::uint32_t>(gene - lo) : kStreamPad;
+                if (((local & 1u) == pref) != (pass == 0)) continue;
+                const std::int64_t bit = pbit + (e - rb) * kBits;
+                const std::uint32_t code = (static_cast<std::uint32_t>(a.packed[bit >> 3]) >> (bit & 7)) & kMask;
+                const std::uint64_t pos = static_cast<std::uint64_t>(fill0 + k / 16u) * 128u + g * 16u + k % 16u;
+                if constexpr (kWide) static_cast<std::uint32_t *>(a.entries)[pos] = local | code << 16;
+                else static_cast<std::uint16_t *>(a.entries)[pos] = static_cast<std::uint16_t>(local | code << 11);
+                ++k;
+            }
+        }
+        cur = stop;
+    }
+}
+
+constexpr std::uint64_t align256(std::uint64_t b) { return (b + 255u) & ~std::uint64_t{255u}; }
+
+struct PlanSizes {
+    std::uint64_t n;  // fill-index entries before the sentinel
+    std::uint64_t error, slot_rows, index, counts, lasts, scan, total;
+    std::uint32_t blocks, parts;
+};
+
+PlanSizes plan_sizes(const cx_qcsr_matrix *m, const cx_qcsr_hybrid_layout *L) {
+    PlanSizes s{};
+    s.blocks = (m->rows + kStreamRows - 1) / kStreamRows;
+    const std::uint32_t all_parts = (m->cols + kStreamPartGenes - 1) / kStreamPartGenes;
+    const std::uint32_t first = L->head_cols / kStreamPartGenes;
+    s.parts = all_parts > first ? all_parts - first : 0u;
+    s.n = static_cast<std::uint64_t>(s.blocks) * s.parts * kStreamSlots;
+    s.error = 256;
+    s.slot_rows = align256(static_cast<std::uint64_t>(s.blocks) * kStreamRows * 4u);
+    s.index = align256((s.n + 1u) * 4u);
+    s.counts = align256((s.n + 1u) * 4u);
+    s.lasts = align256(s.n + 1u);
+    s.scan = align256(scan_workspace_bytes(s.n + 1u));
+    s.total = s.error + s.slot_rows + s.index + s.counts + s.lasts + s.scan;
+    return s;
+}
+
+int validate_stream(const cx_qcsr_matrix *m, const cx_qcsr_hybrid_layout *L, const char *who) {
+    if (m == nullptr || L == nullptr) return fail(CX_STATUS_INVALID_ARGUMENT, who);
+    if (m->bits != 1u && m->bits != 2u && m->bits != 4u && m->bits != 8u)
+        return fail(CX_STATUS_UNSUPPORTED, "quantized CSR tail stream: codes of 1, 2, 4 or 8 bits only");
+    if ((m->flags & CX_QCSR_COLUMNS_SORTED) == 0u)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "quantized CSR tail stream: rows must be sorted (CX_QCSR_COLUMNS_SORTED)");
+    if (L->rows != m->rows || L->bits != m->bits || L->nnz != m->nnz || L->head_end == nullptr
+        || L->head_cols % kStreamPartGenes != 0u || L->head_cols > m->cols)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "quantized CSR tail stream: the hybrid layout was not prepared for this matrix");
+    if (m->rows == 0u || m->cols == 0u)
+        return fail(CX_STATUS_INVALID_SHAPE, "quantized CSR tail stream: empty matrix");
+    if (m->row_ptr == nullptr || m->packed_row_ptr == nullptr
+        || (m->nnz != 0u && (m->col_idx == nullptr || m->packed_values == nullptr)))
+        return fail(CX_STATUS_INVALID_ARGUMENT, "quantized CSR tail stream: null structure or codes");
+    const PlanSizes s = plan_sizes(m, L);
+    if (s.n + 1u > 0x7fffffffull)
+        return fail(CX_STATUS_INVALID_SHAPE, "quantized CSR tail stream: too many (block, part, layer) entries");
+    return CX_STATUS_SUCCESS;
+}
+
+} // namespace
+} // namespace cx
+
+extern "C" int cx_qcsr_tail_plan_bytes(const cx_qcsr_matrix *m, const cx_qcsr_hybrid_layout *layout, uint64_t *bytes) {
+    using namespace cx;
+    clear_error();
+    if (bytes == nullptr) return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_tail_plan_bytes: null bytes");
+    const int rc = validate_stream(m, layout, "cx_qcsr_tail_plan_bytes: null argument");
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    *bytes = plan_sizes(m, layout).total;
+    return CX_STATUS_SUCCESS;
+}
+
+extern "C" int cx_qcsr_tail_plan(const cx_qcsr_matrix *m, const cx_qcsr_hybrid_layout *layout, void *storage,
+                                 uint64_t storage_bytes, cx_qcsr_tail_stream *out, uint64_t *entry_bytes,
+                                 void *stream) {
+    using namespace cx;
+    clear_error();
+    int rc = validate_stream(m, layout, "cx_qcsr_tail_plan: null argument");
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    if (out == nullptr || entry_bytes == nullptr)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_tail_plan: null output");
+    const PlanSizes sz = plan_sizes(m, layout);
+    if (storage == nullptr || storage_bytes < sz.total || (reinterpret_cast<std::uintptr_t>(storage) & 255u) != 0u)
+        return fail(CX_STATUS_INVALID_ARGUMENT,
+                    "cx_qcsr_tail_plan: storage must be 256-byte aligned and hold cx_qcsr_tail_plan_bytes");
+    auto *base = static_cast<unsigned char *>(storage);
+    auto *error = reinterpret_cast<std::uint32_t *>(base);
+    std::uint64_t off = sz.error;
+    auto *slot_rows = reinterpret_cast<std::uint32_t *>(base + off);
+    off += sz.slot_rows;
+    auto *index = reinterpret_cast<std::uint32_t *>(base + off);
+    off += sz.index;
+    auto *counts = reinterpret_cast<std::uint32_t *>(base + off);
+    off += sz.counts;
+    auto *lasts = reinterpret_cast<std::uint8_t *>(base + off);
+    off += sz.lasts;
+    void *scan_ws = base + off;
+
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    // error words, and the sentinel count that the scan turns into the total
+    hipLaunchKernelGGL(fill_pattern_kernel, dim3(1), dim3(64), 0, s, error, std::uint64_t{4}, 0u);
+    hipLaunchKernelGGL(fill_pattern_kernel, dim3(1), dim3(64), 0, s, counts + sz.n, std::uint64_t{1}, 0u);
+    PlanArgs pa{};
+    pa.row_ptr = m->row_ptr;
+    pa.col_idx = m->col_idx;
+    pa.head_end = layout->head_end;
+    pa.rows = m->rows;
+    pa.cols = m->cols;
+    pa.first_part = layout->head_cols / kStreamPartGenes;
+    pa.parts = sz.parts;
+    pa.slot_rows = slot_rows;
+    pa.counts = counts;
+    pa.lasts = lasts;
+    pa.error = error;
+    hipLaunchKernelGGL(stream_plan_kernel, dim3(sz.blocks), dim3(kStreamRows), 0, s, pa);
+    rc = check_launch("cx_qcsr_tail_plan");
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    rc = exclusive_scan_u32(counts, index, sz.n + 1u, scan_ws, s);
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    if (sz.n != 0u) {
+        const std::uint32_t max_block_fills = m->bits == 8u ? (1u << 23) - 4u : (1u << 24) - 4u;
+        hipLaunchKernelGGL(stream_pack_kernel, dim3(static_cast<unsigned>((sz.n + 255u) / 256u)), dim3(256), 0, s,
+                           index, lasts, sz.n, static_cast<std::uint64_t>(sz.parts) * kStreamSlots, max_block_fills,
+                           error);
+        rc = check_launch("cx_qcsr_tail_plan");
+        if (rc != CX_STATUS_SUCCESS) return rc;
+    }
+    std::uint32_t host[2] = {0u, 0u};
+    std::uint32_t total = 0u;
+    hipError_t e = hipMemcpyAsync(host, error, sizeof(host), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(&total, index + sz.n, 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "cx_qcsr_tail_plan");
+    if (host[0] != 0u)
+        return fail(CX_STATUS_INVALID_ARGUMENT,
+                    "cx_qcsr_tail_plan: a row's genes are not sorted within [head_cols, cols) despite CX_QCSR_COLUMNS_SORTED");
+    // The u32 scan is exact: a layer's fills are at most its largest run / 16 + 1, so the
+    // total is below nnz / 16 + n < 2^32 (nnz and n are below 2^31).
+    if (host[1] != 0u)
+        return fail(CX_STATUS_INVALID_SHAPE, "cx_qcsr_tail_plan: a 512-row block needs 4 GiB of stream or more");
+    if (total >= kFillMask)
+        return fail(CX_STATUS_INVALID_SHAPE, "cx_qcsr_tail_plan: the stream needs 2^28 fills or more");
+    const std::uint64_t fill_bytes = m->bits == 8u ? 512u : 256u;
+    cx_qcsr_tail_stream t{};
+    t.rows = m->rows;
+    t.first_part = layout->head_cols / kStreamPartGenes;
+    t.parts = sz.parts;
+    t.blocks = sz.blocks;
+    t.bits = m->bits;
+    t.entry_bytes = m->bits == 8u ? 4u : 2u;
+    t.fills = total;
+    t.nnz = m->nnz;
+    t.slot_rows = slot_rows;
+    t.fill_index = index;
+    t.entries = nullptr;
+    *out = t;
+    // three fills of slack: the walk's prefetch reads up to three fills past a block's last
+    *entry_bytes = (static_cast<std::uint64_t>(total) + 3u) * fill_bytes;
+    return CX_STATUS_SUCCESS;
+}
+
+extern "C" int cx_qcsr_tail_fill(const cx_qcsr_matrix *m, const cx_qcsr_hybrid_layout *layout,
+                                 cx_qcsr_tail_stream *ts, void *entries, uint64_t entry_bytes, void *stream) {
+    using namespace cx;
+    clear_error();
+    int rc = validate_stream(m, layout, "cx_qcsr_tail_fill: null argument");
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    if (ts == nullptr) return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_tail_fill: null stream");
+    const PlanSizes sz = plan_sizes(m, layout);
+    const std::uint64_t fill_bytes = m->bits == 8u ? 512u : 256u;
+    if (ts->rows != m->rows || ts->bits != m->bits || ts->nnz != m->nnz || ts->parts != sz.parts
+        || ts->blocks != sz.blocks || ts->first_part != layout->head_cols / kStreamPartGenes
+        || ts->slot_rows == nullptr || ts->fill_index == nullptr)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_tail_fill: the stream was not planned for this matrix");
+    const std::uint64_t need = (ts->fills + 3u) * fill_bytes;
+    if (entries == nullptr || entry_bytes < need || (reinterpret_cast<std::uintptr_t>(entries) & 255u) != 0u)
+        return fail(CX_STATUS_INVALID_ARGUMENT,
+                    "cx_qcsr_tail_fill: entries must be 256-byte aligned and hold the bytes cx_qcsr_tail_plan returned");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const std::uint32_t pad = m->bits == 8u ? kStreamPad : (kStreamPad | kStreamPad << 16);
+    const std::uint64_t words = need / 4u;
+    hipLaunchKernelGGL(fill_pattern_kernel, dim3(static_cast<unsigned>(std::min<std::uint64_t>((words + 255u) / 256u, 65536u))),
+                       dim3(256), 0, s, static_cast<std::uint32_t *>(entries), words, pad);
+    FillArgs fa{};
+    fa.row_ptr = m->row_ptr;
+    fa.packed_row_ptr = m->packed_row_ptr;
+    fa.col_idx = m->col_idx;
+    fa.packed = m->packed_values;
+    fa.head_end = layout->head_end;
+    fa.slot_rows = ts->slot_rows;
+    fa.index = ts->fill_index;
+    fa.entries = entries;
+    fa.cols = m->cols;
+    fa.first_part = ts->first_part;
+    fa.parts = ts->parts;
+    const dim3 grid(sz.blocks), block(kStreamRows);
+    switch (m->bits) {
+    case 1: hipLaunchKernelGGL(stream_fill_kernel<1>, grid, block, 0, s, fa); break;
+    case 2: hipLaunchKernelGGL(stream_fill_kernel<2>, grid, block, 0, s, fa); break;
+    case 4: hipLaunchKernelGGL(stream_fill_kernel<4>, grid, block, 0, s, fa); break;
+    default: hipLaunchKernelGGL(stream_fill_kernel<8>, grid, block, 0, s, fa); break;
+    }
+    rc = check_launch("cx_qcsr_tail_fill");
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    ts->entries = entries;
+    return CX_STATUS_SUCCESS;
+}

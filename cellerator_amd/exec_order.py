@@ -124,6 +124,8 @@ class HybridProjection:
     layout: N.CxQcsrHybridLayout
     storage: Optional[torch.Tensor]
     workspaces: dict = dataclasses.field(default_factory=dict)
+    tail: Optional[N.CxQcsrTailStream] = None        # prepared tail stream (hybrid_prepare(..., stream_tail=True))
+    tail_storage: tuple = ()                         # (plan storage, entries) tensors behind `tail`
 
     @property
     def scale_exp(self) -> int:
@@ -141,9 +143,11 @@ class HybridProjection:
         return ws
 
 
-def hybrid_prepare(m: QcsrMatrix, head_cols: int, stream=None) -> HybridProjection:
+def hybrid_prepare(m: QcsrMatrix, head_cols: int, stream=None, stream_tail: bool = False) -> HybridProjection:
     """m in execution order (sorted rows, flags QCSR_COLUMNS_SORTED). Raises if a row's genes
-    are not strictly increasing or the head metadata is not finite."""
+    are not strictly increasing or the head metadata is not finite. With stream_tail the
+    tail's entries are also rearranged into the prepared tail stream (cx_qcsr_tail_plan /
+    cx_qcsr_tail_fill), which the tail kernel then reads instead of the CSR."""
     _require_cuda(m.row_ptr)
     lib = N.engine()
     d = m.descriptor()
@@ -153,7 +157,51 @@ def hybrid_prepare(m: QcsrMatrix, head_cols: int, stream=None) -> HybridProjecti
     layout = N.CxQcsrHybridLayout()
     N.check("cx_qcsr_hybrid_prepare", lib.cx_qcsr_hybrid_prepare(
         C.byref(d), head_cols, storage.data_ptr(), storage.numel(), C.byref(layout), _stream(stream)))
-    return HybridProjection(m, head_cols, layout, storage)
+    p = HybridProjection(m, head_cols, layout, storage)
+    if stream_tail:
+        tail_prepare(p, stream)
+    return p
+
+
+def tail_prepare(p: HybridProjection, stream=None) -> N.CxQcsrTailStream:
+    """Plans and fills the prepared tail stream of p and attaches it (p.layout.tail)."""
+    lib = N.engine()
+    d = p.matrix.descriptor()
+    dev = p.matrix.row_ptr.device
+    nbytes = C.c_uint64()
+    N.check("cx_qcsr_tail_plan_bytes", lib.cx_qcsr_tail_plan_bytes(C.byref(d), C.byref(p.layout), C.byref(nbytes)))
+    plan = torch.empty(max(nbytes.value, 256), dtype=torch.uint8, device=dev)
+    ts = N.CxQcsrTailStream()
+    entry_bytes = C.c_uint64()
+    N.check("cx_qcsr_tail_plan", lib.cx_qcsr_tail_plan(C.byref(d), C.byref(p.layout), plan.data_ptr(), plan.numel(),
+                                                        C.byref(ts), C.byref(entry_bytes), _stream(stream)))
+    entries = torch.empty(max(entry_bytes.value, 256), dtype=torch.uint8, device=dev)
+    N.check("cx_qcsr_tail_fill", lib.cx_qcsr_tail_fill(C.byref(d), C.byref(p.layout), C.byref(ts),
+                                                        entries.data_ptr(), entries.numel(), _stream(stream)))
+    p.tail, p.tail_storage = ts, (plan, entries)
+    p.layout.tail = C.addressof(ts)
+    return ts
+
+
+def tail_arrays(p: HybridProjection):
+    """(slot_rows [blocks, 512] int32 (u32 bits), fill_index [blocks * parts * 64 + 1] int32,
+    entries [fills, 128] int16 or int32) of the prepared tail stream, as device views."""
+    ts = p.tail
+    plan, entries = p.tail_storage
+    base = plan.data_ptr()
+
+    def view(t, ptr, count, dtype):
+        off = ptr - t.data_ptr()
+        size = torch.tensor([], dtype=dtype).element_size()
+        return t[off:off + count * size].view(dtype)
+
+    n = int(ts.blocks) * int(ts.parts) * 64 + 1
+    slot_rows = view(plan, ts.slot_rows, int(ts.blocks) * 512, torch.int32).view(int(ts.blocks), 512)
+    index = view(plan, ts.fill_index, n, torch.int32)
+    et = torch.int32 if ts.entry_bytes == 4 else torch.int16
+    ents = view(entries, ts.entries, int(ts.fills) * 128, et).view(int(ts.fills), 128)
+    del base
+    return slot_rows, index, ents
 
 
 def hybrid_head_arrays(p: HybridProjection):

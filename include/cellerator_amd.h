@@ -1400,6 +1400,8 @@ typedef struct cx_qcsr_hybrid_layout {
     int32_t *head_end;      /* [rows]: first entry of each row with gene >= H */
     float *meta;            /* [H] (scale, offset) pairs times 2^k */
     float *row_offsets;     /* [rows] times 2^k (column-scale / row-offset policy), else NULL */
+    const struct cx_qcsr_tail_stream *tail;  /* prepared tail stream (cx_qcsr_tail_fill), or NULL:
+                                                the tail then runs on the row-group kernel */
 } cx_qcsr_hybrid_layout;
 
 /* Device bytes of the head layout of `a` (a.flags must include CX_QCSR_COLUMNS_SORTED). */
@@ -1417,12 +1419,52 @@ int cx_qcsr_hybrid_workspace(const cx_qcsr_matrix *a, uint32_t head_cols, int64_
  * CX_QCSR_COLUMNS_SORTED, codes of 1/2/4/8 bits (any decode policy), F16 W [cols x out_cols]
  * (row stride rhs_ld), out_cols 64..256 in steps of 64 (one head and one tail launch per 64
  * columns), 16-byte aligned operands, `layout` from cx_qcsr_hybrid_prepare on this matrix.
- * head_cols == 0 runs the plain row-group kernel. workspace: 256-byte aligned,
- * cx_qcsr_hybrid_workspace bytes. Deterministic. */
+ * head_cols == 0 runs the plain row-group kernel (or the tail stream over the whole matrix
+ * when layout.tail is set). workspace: 256-byte aligned, cx_qcsr_hybrid_workspace bytes.
+ * Deterministic. */
 int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *a, const cx_qcsr_hybrid_layout *layout, const void *rhs,
                             int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
                             const cx_spmm_epilogue *epilogue, void *workspace, uint64_t workspace_bytes,
                             void *stream);
+
+/* ---- prepared tail stream ----------------------------------------------------------------
+ * The entries of every row from its first tail entry (layout.head_end) on, rearranged once
+ * per structure into the order the row-group walk consumes them: blocks of 512 rows ranked
+ * by tail length into 16 waves x 4 layers x 8 rows; per gene part of 1,024 and layer, the 8
+ * rows' runs as fills of 16 steps x 8 rows (group-major), padded with the zero row, each
+ * row's run even genes first in even groups and odd genes first in odd groups. With the
+ * stream the tail kernel loads its entries instead of finding them (no per-pass run count,
+ * window or reload). Built in two steps because the stream's size depends on the data:
+ * cx_qcsr_tail_plan (slot rows and fill index; returns the entry bytes) and
+ * cx_qcsr_tail_fill. Then set layout.tail to the stream. head_cols may be 0: the whole
+ * matrix is then the tail. Engine addition; no counterpart in the reference. */
+typedef struct cx_qcsr_tail_stream {
+    uint32_t rows;
+    uint32_t first_part;    /* head_cols / 1024 */
+    uint32_t parts;         /* gene parts of 1,024 in the stream: ceil(cols / 1024) - first_part */
+    uint32_t blocks;        /* ceil(rows / 512) */
+    uint32_t bits;
+    uint32_t entry_bytes;   /* 2 (codes of up to 4 bits: gene in part | code << 11) or 4 (8-bit: gene | code << 16) */
+    uint64_t fills;         /* fills of 128 entries */
+    uint64_t nnz;           /* of the matrix it was built from */
+    uint32_t *slot_rows;    /* [blocks][512]: row of slot (wave * 4 + layer) * 8 + group, 0xffffffff none */
+    uint32_t *fill_index;   /* [blocks * parts * 64 + 1]: first fill of (block, part, wave, layer) in the low
+                               28 bits, steps of its last fill - 1 in the high 4; last entry: the total */
+    void *entries;          /* [fills + 3][128] entries (set by cx_qcsr_tail_fill) */
+} cx_qcsr_tail_stream;
+
+/* Device bytes of the plan storage (slot rows, fill index, counts, scan workspace). */
+int cx_qcsr_tail_plan_bytes(const cx_qcsr_matrix *a, const cx_qcsr_hybrid_layout *layout, uint64_t *bytes);
+/* Plans the stream of `a` (rows sorted: CX_QCSR_COLUMNS_SORTED) after `layout`'s head into
+ * `storage` (256-byte aligned, cx_qcsr_tail_plan_bytes); *entry_bytes receives the bytes the
+ * entries need. Synchronizes `stream`. Rejects rows not sorted within [head_cols, cols)
+ * (INVALID_ARGUMENT) and streams of 2^28 fills or more (INVALID_SHAPE). */
+int cx_qcsr_tail_plan(const cx_qcsr_matrix *a, const cx_qcsr_hybrid_layout *layout, void *storage,
+                      uint64_t storage_bytes, cx_qcsr_tail_stream *out, uint64_t *entry_bytes, void *stream);
+/* Writes the entries into `entries` (256-byte aligned, the bytes cx_qcsr_tail_plan returned)
+ * and sets out->entries. Stream-ordered, no synchronization. */
+int cx_qcsr_tail_fill(const cx_qcsr_matrix *a, const cx_qcsr_hybrid_layout *layout, cx_qcsr_tail_stream *stream_out,
+                      void *entries, uint64_t entry_bytes, void *stream);
 
 /* N = 1 CSR comparator: csr_spmv_fwd_f16_f32 (src/compute/sparse/ops/ops.hh:83-90);
  * y[r] = sum fp32(values) * x[col]. values F16 or F32. */

@@ -1,0 +1,194 @@
+"""GPU parity of the prepared tail stream (qcsr_stream.hip) and the walk that reads it
+(qcsr_spmm_stream in qcsr_parts.hip): the slot rows, fill index and entries are bit-exact
+against a numpy restatement of the stream's definition (rank by tail length, snake-order
+layers, per-part fills of 16 steps x 8 groups, parity order within each run, pads), and the
+product through the stream -- every code width and decode policy, with and without a dense
+head, N = 64 and 128, fused epilogues, empty rows, rows longer than a part, ragged last
+block -- matches the float64 referee of the canonical matrix; repeats are bitwise equal.
+Rows that break the sorted-columns promise are rejected when the stream is planned."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests.helpers import check_against_referee, qcsr_to_host, to_device_qcsr
+from tests.test_hybrid_gpu import _exec, _referee, _skewed
+
+pytestmark = pytest.mark.gpu
+
+ROWS_PER_BLOCK, WAVES, LAYERS, PART = 512, 16, 4, 1024
+
+
+def _stream_reference(h, head_end, head, bits):
+    """slot_rows, fill_index and entries of the stream by its definition."""
+    rows = len(h["row_ptr"]) - 1
+    cols = int(h["cols"])
+    blocks = (rows + ROWS_PER_BLOCK - 1) // ROWS_PER_BLOCK
+    first = head // PART
+    parts = (cols + PART - 1) // PART - first
+    wide = bits == 8
+    slot_rows = np.full((blocks, ROWS_PER_BLOCK), 0xFFFFFFFF, np.uint32)
+    runs = {}  # (block, part, slot) -> list of (local gene, code) in stored order
+    counts = np.zeros(blocks * parts * 64 + 1, np.int64)
+    lasts = np.zeros(blocks * parts * 64, np.int64)
+    for b in range(blocks):
+        lens = np.full(ROWS_PER_BLOCK, -1, np.int64)
+        for t in range(ROWS_PER_BLOCK):
+            r = b * ROWS_PER_BLOCK + t
+            if r < rows:
+                lens[t] = int(h["row_ptr"][r + 1]) - int(head_end[r])
+        order = sorted(range(ROWS_PER_BLOCK), key=lambda t: (-lens[t], t))
+        for rank, t in enumerate(order):
+            s, g = divmod(rank, 8)
+            rnd, pos = divmod(s, WAVES)
+            w = WAVES - 1 - pos if rnd & 1 else pos
+            r = b * ROWS_PER_BLOCK + t
+            slot_rows[b, (w * LAYERS + rnd) * 8 + g] = r if r < rows else 0xFFFFFFFF
+        for slot in range(ROWS_PER_BLOCK):
+            r = int(slot_rows[b, slot])
+            if r == 0xFFFFFFFF:
+                continue
+            rb, re = int(h["row_ptr"][r]), int(h["row_ptr"][r + 1])
+            pbit = int(h["packed_row_ptr"][r]) * 8
+            for e in range(int(head_end[r]), re):
+                gene = int(h["col_idx"][e])
+                bit = pbit + (e - rb) * bits
+                code = (int(h["packed"][bit >> 3]) >> (bit & 7)) & ((1 << bits) - 1)
+                runs.setdefault((b, gene // PART - first, slot), []).append((gene % PART, code))
+        for p in range(parts):
+            for ls in range(64):
+                m = 0
+                for g in range(8):
+                    run = runs.get((b, p, ls * 8 + g), [])
+                    pref = g & 1
+                    run.sort(key=lambda x: 0 if (x[0] & 1) == pref else 1)  # stable: gene order within a parity
+                    m = max(m, len(run))
+                k = (b * parts + p) * 64 + ls
+                counts[k] = (m + 15) // 16
+                lasts[k] = 0 if m == 0 else m - 16 * (counts[k] - 1)
+    starts = np.zeros_like(counts)
+    starts[1:] = np.cumsum(counts)[:-1]
+    index = starts.astype(np.uint64)
+    index[:-1] |= np.where(lasts > 0, (lasts - 1) << 28, 0).astype(np.uint64)
+    total = int(starts[-1])
+    pad = 1024
+    entries = np.full((total, 128), pad, np.uint32 if wide else np.uint16)
+    for (b, p, slot), run in runs.items():
+        ls, g = divmod(slot, 8)
+        f0 = int(starts[(b * parts + p) * 64 + ls])
+        for k, (gene, code) in enumerate(run):
+            entries[f0 + k // 16, g * 16 + k % 16] = gene | (code << (16 if wide else 11))
+    return slot_rows, index.astype(np.uint32), entries
+
+
+@pytest.mark.parametrize("bits,head", [(4, 1024), (8, 0), (2, 2048)])
+def test_stream_layout_is_bit_exact(oracle, bits, head):
+    import torch
+
+    from cellerator_amd.exec_order import hybrid_prepare, tail_arrays
+    rng = np.random.default_rng(40 + bits + head)
+    fx = _skewed(oracle, rng, 1100, 3100, bits, 1)
+    mx, _ = _exec(to_device_qcsr(fx))
+    p = hybrid_prepare(mx, head, stream_tail=True)
+    torch.cuda.synchronize()
+    slot_rows, index, entries = tail_arrays(p)
+    h = qcsr_to_host(mx)
+    from cellerator_amd.exec_order import hybrid_head_arrays
+    he = hybrid_head_arrays(p)[2].cpu().numpy()
+    want_rows, want_index, want_entries = _stream_reference(h, he, head, bits)
+    assert np.array_equal(slot_rows.cpu().numpy().view(np.uint32), want_rows)
+    assert np.array_equal(index.cpu().numpy().view(np.uint32), want_index)
+    got = entries.cpu().numpy().view(np.uint32 if bits == 8 else np.uint16)
+    assert got.shape == want_entries.shape
+    assert np.array_equal(got, want_entries)
+    assert int(p.tail.fills) == want_entries.shape[0]
+
+
+@pytest.mark.parametrize("bits,policy,head", [(4, 1, 2048), (4, 1, 0), (8, 1, 1024), (2, 2, 2048), (1, 1, 1024),
+                                              (4, 3, 2048), (8, 3, 0)])
+def test_stream_product_matches_referee(oracle, bits, policy, head):
+    import torch
+
+    from cellerator_amd import qcsr_pack_gene_affine
+    from cellerator_amd.exec_order import hybrid_prepare, hybrid_spmm, pack_rows
+    rng = np.random.default_rng(3000 + 10 * bits + policy + head)
+    fx = _skewed(oracle, rng, 1300, 3100, bits, policy)
+    m = to_device_qcsr(fx)
+    if policy == 3:
+        m = qcsr_pack_gene_affine(m)
+    mx, order = _exec(m)
+    w = (rng.standard_normal((3100, 64)) * 0.02).astype(np.float16)
+    wx = pack_rows(order, torch.from_numpy(w).cuda())
+    p = hybrid_prepare(mx, head, stream_tail=True)
+    y = hybrid_spmm(p, wx)
+    y2 = hybrid_spmm(p, wx)
+    torch.cuda.synchronize()
+    ref, mag = _referee(oracle, dict(fx, policy=1 if policy == 3 else policy), w)
+    check_against_referee(oracle, ref, mag, y.cpu().numpy())
+    assert torch.equal(y.view(torch.int32), y2.view(torch.int32))
+
+
+def test_stream_epilogue_and_wide_outputs(oracle):
+    import torch
+
+    from cellerator_amd import Epilogue
+    from cellerator_amd.exec_order import hybrid_prepare, hybrid_spmm, pack_rows
+    rng = np.random.default_rng(77)
+    fx = _skewed(oracle, rng, 900, 2500, 4, 1)
+    mx, order = _exec(to_device_qcsr(fx))
+    w = (rng.standard_normal((2500, 128)) * 0.02).astype(np.float16)
+    wx = pack_rows(order, torch.from_numpy(w).cuda())
+    bias = torch.from_numpy(rng.standard_normal(128).astype(np.float32)).cuda()
+    c0 = torch.from_numpy(rng.standard_normal((900, 128)).astype(np.float32)).cuda()
+    p = hybrid_prepare(mx, 1024, stream_tail=True)
+    plain = hybrid_prepare(mx, 1024)
+    y = c0.clone()
+    hybrid_spmm(p, wx, out=y, epilogue=Epilogue(kind=5, alpha=0.5, beta=2.0, bias=bias, initial=y))
+    base = hybrid_spmm(plain, wx)
+    torch.cuda.synchronize()
+    ref, mag = _referee(oracle, fx, w)
+    check_against_referee(oracle, ref, mag, base.cpu().numpy())
+    want = np.maximum(0.5 * ref + 2.0 * c0.cpu().numpy() + bias.cpu().numpy(), 0.0)
+    got = y.cpu().numpy()
+    assert np.all(np.abs(got - want) <= 1e-4 + 1e-4 * np.abs(want) + 1e-4 * mag)
+
+
+def test_long_rows_and_unsorted_rows(oracle):
+    """Rows longer than a part (several fills per layer) and a ragged last block; then a row
+    that breaks the sorted promise in the tail is rejected by the planner."""
+    import dataclasses
+
+    import torch
+
+    from cellerator_amd import _native as N
+    from cellerator_amd.exec_order import hybrid_prepare, hybrid_spmm
+    from tests.test_qcsr_parts_gpu import _rebuild
+    from tests.helpers import quantized_fixture
+    rng = np.random.default_rng(91)
+    rows, cols = 530, 2048 + 700
+    fx = quantized_fixture(oracle, rng, rows, cols, 5.0, 4, 1)
+    lengths = rng.integers(0, 40, rows)
+    lengths[:20] = rng.integers(900, 1500, 20)  # dense rows: up to 1,500 entries, ~1,000 in one part
+    row_ptr = np.zeros(rows + 1, np.int64)
+    row_ptr[1:] = np.cumsum(lengths)
+    col_idx = np.concatenate([np.sort(rng.choice(cols, n, replace=False)) for n in lengths]).astype(np.int32)
+    fx = _rebuild(oracle, rng, fx, row_ptr.astype(np.int32), col_idx)
+    m = dataclasses.replace(to_device_qcsr(fx), flags=N.QCSR_COLUMNS_SORTED)
+    w = (rng.standard_normal((cols, 64)) * 0.02).astype(np.float16)
+    p = hybrid_prepare(m, 1024, stream_tail=True)
+    y = hybrid_spmm(p, torch.from_numpy(w).cuda())
+    torch.cuda.synchronize()
+    ref, mag = _referee(oracle, fx, w)
+    check_against_referee(oracle, ref, mag, y.cpu().numpy())
+    # swap two tail genes of a long row across a part boundary: still inside [head, cols),
+    # but a gene of part 1 now follows one of part 2 (disorder inside a part leaves the
+    # product unchanged and is not an error)
+    bad = fx["col_idx"].copy()
+    r = 3
+    b, e = int(fx["row_ptr"][r]), int(fx["row_ptr"][r + 1])
+    part1 = np.nonzero((bad[b:e] >= 1024) & (bad[b:e] < 2048))[0] + b
+    part2 = np.nonzero(bad[b:e] >= 2048)[0] + b
+    bad[part1[0]], bad[part2[0]] = bad[part2[0]], bad[part1[0]]
+    mb = dataclasses.replace(m, col_idx=torch.from_numpy(bad).cuda())
+    with pytest.raises(N.EngineError, match="not sorted"):
+        hybrid_prepare(mb, 1024, stream_tail=True)
