@@ -210,9 +210,9 @@ class CxQcsrHybridLayout(C.Structure):
 
 
 class CxQcsrTailStream(C.Structure):
-    _fields_ = [("rows", u32), ("first_part", u32), ("parts", u32), ("blocks", u32), ("bits", u32),
-                ("entry_bytes", u32), ("fills", u64), ("nnz", u64), ("slot_rows", p_void), ("fill_index", p_void),
-                ("entries", p_void)]
+    _fields_ = [("rows", u32), ("first_part", u32), ("parts", u32), ("blocks", u32), ("block_rows", u32),
+                ("layers", u32), ("bits", u32), ("entry_bytes", u32), ("fills", u64), ("nnz", u64),
+                ("slot_rows", p_void), ("fill_index", p_void), ("entries", p_void)]
 
 
 # ---- public context ABI structs (include/Cellerator/abi.h layout) ----

@@ -40,14 +40,14 @@ struct QcsrArgs {
 };
 
 // Geometry of the prepared tail stream, shared by its builder and its kernel: 16 waves of
-// 4 layers of 8 rows per 512-row block; a fill is 16 steps of the 8 lane groups of a
+// 8 layers of 8 rows per 1,024-row block; a fill is 16 steps of the 8 lane groups of a
 // layer, 128 entries stored group-major ([group][step]); entries are u16
 // (gene in part | code << 11) for codes of up to 4 bits and u32 (gene | code << 16) for
-// 8-bit codes. fill_index[(block * parts + part) * 64 + wave * 4 + layer] holds the
-// layer's first fill (low 28 bits) and the step count of its last fill minus one (high 4
-// bits); the entry after the last is the total.
+// 8-bit codes. fill_index[(block * parts + part) * kStreamSlots + wave * kStreamLayers +
+// layer] holds the layer's first fill (low 28 bits) and the step count of its last fill
+// minus one (high 4 bits); the entry after the last is the total.
 constexpr int kStreamWaves = 16;
-constexpr int kStreamLayers = 4;
+constexpr int kStreamLayers = 8;
 constexpr int kStreamSlots = kStreamWaves * kStreamLayers;        // (wave, layer) per block and part
 constexpr int kStreamRows = kStreamSlots * 8;
 constexpr std::uint32_t kFillMask = 0x0fffffffu;

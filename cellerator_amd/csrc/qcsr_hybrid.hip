@@ -627,6 +627,7 @@ extern "C" int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *m, const cx_qcsr_hy
         const std::uint32_t all_parts = (m->cols + kHeadAlign - 1u) / kHeadAlign;
         if (ts->rows != m->rows || ts->bits != m->bits || ts->nnz != m->nnz || ts->first_part != L.head_cols / kHeadAlign
             || ts->parts != all_parts - ts->first_part || ts->blocks != (m->rows + kStreamRows - 1u) / kStreamRows
+            || ts->block_rows != kStreamRows || ts->layers != kStreamLayers
             || ts->slot_rows == nullptr || ts->fill_index == nullptr || ts->entries == nullptr)
             return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd_hybrid: the tail stream was not built for this layout");
         a.slot_rows = ts->slot_rows;

@@ -616,11 +616,11 @@ __global__ __launch_bounds__(kStreamWaves * kWave) void qcsr_spmm_stream(QcsrArg
                     st[2 * r + 1] = __float_as_uint(__builtin_fmaf(static_cast<float>(code), md.x, off));
                 }
                 sp[j] = make_uint4(st[0], st[1], st[2], st[3]);
-                const int cnt = f + 1u < e_l ? 16 : last;
-                const int n2 = cnt >> 1;
-                int it = 0;
-                for (; it + 2 <= n2; it += 2) {
-                    const uint4 ea = sp[it], eb = sp[it + 1];
+                // Steps in blocks of 4 stage slots; slots past a group's run hold pads (zero
+                // row, value 0), so a block may run past `cnt`. A full fill is straight-line
+                // code, which lets the weight reads of later blocks issue under earlier FMAs.
+                auto step4 = [&](int q) {
+                    const uint4 ea = sp[2 * q], eb = sp[2 * q + 1];
                     const uint4 wa0 = *reinterpret_cast<const uint4 *>(wbase + (ea.x << 4));
                     const uint4 wa1 = *reinterpret_cast<const uint4 *>(wbase + (ea.z << 4));
                     const uint4 wb0 = *reinterpret_cast<const uint4 *>(wbase + (eb.x << 4));
@@ -629,18 +629,11 @@ __global__ __launch_bounds__(kStreamWaves * kWave) void qcsr_spmm_stream(QcsrArg
                     fma8(acc[l], __uint_as_float(ea.w), wa1);
                     fma8(acc[l], __uint_as_float(eb.y), wb0);
                     fma8(acc[l], __uint_as_float(eb.w), wb1);
-                }
-                if (it < n2) {
-                    const uint4 e = sp[it];
-                    const uint4 w0 = *reinterpret_cast<const uint4 *>(wbase + (e.x << 4));
-                    const uint4 w1 = *reinterpret_cast<const uint4 *>(wbase + (e.z << 4));
-                    fma8(acc[l], __uint_as_float(e.y), w0);
-                    fma8(acc[l], __uint_as_float(e.w), w1);
-                }
-                if ((cnt & 1) != 0) {
-                    const uint2 e = reinterpret_cast<const uint2 *>(sp)[cnt - 1];
-                    fma8(acc[l], __uint_as_float(e.y), *reinterpret_cast<const uint4 *>(wbase + (e.x << 4)));
-                }
+                };
+                const int cnt = f + 1u < e_l ? 16 : last;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (4 * q < cnt) step4(q);
             }
         }
     }

@@ -3,9 +3,9 @@
 // rearranged once per structure into the order the row-group walk consumes them
 // (qcsr_spmm_stream in qcsr_parts.hip), so the walk loads them instead of finding them.
 //
-// Geometry (qcsr_common.hpp): blocks of 512 rows; in each block the rows are ranked by tail
-// length (descending, ties by row) and ranks 8s .. 8s + 7 form row set s, dealt to the 16
-// waves in snake order (set s -> layer s / 16), which is how the part walk balances its
+// Geometry (qcsr_common.hpp): blocks of 1,024 rows; in each block the rows are ranked by
+// tail length (descending, ties by row) and ranks 8s .. 8s + 7 form row set s, dealt to the
+// 16 waves in snake order (set s -> layer s / 16), which is how the part walk balances its
 // waves. For gene part p and layer (wave w, layer l) the 8 rows' runs in the part are
 // r_0 .. r_7; the layer gets ceil(max r_g / 16) fills of 128 entries, entry k of group g's
 // run at fill k / 16, slot g * 16 + k % 16; unused slots hold the pad gene (the zero
@@ -35,9 +35,9 @@ struct PlanArgs {
     std::uint32_t cols;
     std::uint32_t first_part;
     std::uint32_t parts;          // parts in the stream
-    std::uint32_t *slot_rows;     // [blocks][512]
-    std::uint32_t *counts;        // [blocks * parts * 64 + 1]: fills per layer and part (last: 0)
-    std::uint8_t *lasts;          // [blocks * parts * 64]: step count of the last fill (0: none)
+    std::uint32_t *slot_rows;     // [blocks][kStreamRows]
+    std::uint32_t *counts;        // [blocks * parts * kStreamSlots + 1]: fills per layer and part (last: 0)
+    std::uint8_t *lasts;          // [blocks * parts * kStreamSlots]: step count of the last fill (0: none)
     std::uint32_t *error;         // [0]: a row not sorted within [head, cols); [1]: a block's fills reach 4 GiB
 };
 
@@ -311,7 +311,7 @@ extern "C" int cx_qcsr_tail_plan(const cx_qcsr_matrix *m, const cx_qcsr_hybrid_l
     // The u32 scan is exact: a layer's fills are at most its largest run / 16 + 1, so the
     // total is below nnz / 16 + n < 2^32 (nnz and n are below 2^31).
     if (host[1] != 0u)
-        return fail(CX_STATUS_INVALID_SHAPE, "cx_qcsr_tail_plan: a 512-row block needs 4 GiB of stream or more");
+        return fail(CX_STATUS_INVALID_SHAPE, "cx_qcsr_tail_plan: a block needs 4 GiB of stream or more");
     if (total >= kFillMask)
         return fail(CX_STATUS_INVALID_SHAPE, "cx_qcsr_tail_plan: the stream needs 2^28 fills or more");
     const std::uint64_t fill_bytes = m->bits == 8u ? 512u : 256u;
@@ -320,6 +320,8 @@ extern "C" int cx_qcsr_tail_plan(const cx_qcsr_matrix *m, const cx_qcsr_hybrid_l
     t.first_part = layout->head_cols / kStreamPartGenes;
     t.parts = sz.parts;
     t.blocks = sz.blocks;
+    t.block_rows = kStreamRows;
+    t.layers = kStreamLayers;
     t.bits = m->bits;
     t.entry_bytes = m->bits == 8u ? 4u : 2u;
     t.fills = total;
@@ -343,7 +345,8 @@ extern "C" int cx_qcsr_tail_fill(const cx_qcsr_matrix *m, const cx_qcsr_hybrid_l
     const PlanSizes sz = plan_sizes(m, layout);
     const std::uint64_t fill_bytes = m->bits == 8u ? 512u : 256u;
     if (ts->rows != m->rows || ts->bits != m->bits || ts->nnz != m->nnz || ts->parts != sz.parts
-        || ts->blocks != sz.blocks || ts->first_part != layout->head_cols / kStreamPartGenes
+        || ts->blocks != sz.blocks || ts->block_rows != kStreamRows || ts->layers != kStreamLayers
+        || ts->first_part != layout->head_cols / kStreamPartGenes
         || ts->slot_rows == nullptr || ts->fill_index == nullptr)
         return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_tail_fill: the stream was not planned for this matrix");
     const std::uint64_t need = (ts->fills + 3u) * fill_bytes;

@@ -184,23 +184,23 @@ def tail_prepare(p: HybridProjection, stream=None) -> N.CxQcsrTailStream:
 
 
 def tail_arrays(p: HybridProjection):
-    """(slot_rows [blocks, 512] int32 (u32 bits), fill_index [blocks * parts * 64 + 1] int32,
-    entries [fills, 128] int16 or int32) of the prepared tail stream, as device views."""
+    """(slot_rows [blocks, block_rows] int32 (u32 bits), fill_index [blocks * parts *
+    block_rows / 8 + 1] int32, entries [fills, 128] int16 or int32) of the prepared tail
+    stream, as device views."""
     ts = p.tail
     plan, entries = p.tail_storage
-    base = plan.data_ptr()
 
     def view(t, ptr, count, dtype):
         off = ptr - t.data_ptr()
         size = torch.tensor([], dtype=dtype).element_size()
         return t[off:off + count * size].view(dtype)
 
-    n = int(ts.blocks) * int(ts.parts) * 64 + 1
-    slot_rows = view(plan, ts.slot_rows, int(ts.blocks) * 512, torch.int32).view(int(ts.blocks), 512)
+    br = int(ts.block_rows)
+    n = int(ts.blocks) * int(ts.parts) * (br // 8) + 1
+    slot_rows = view(plan, ts.slot_rows, int(ts.blocks) * br, torch.int32).view(int(ts.blocks), br)
     index = view(plan, ts.fill_index, n, torch.int32)
     et = torch.int32 if ts.entry_bytes == 4 else torch.int16
     ents = view(entries, ts.entries, int(ts.fills) * 128, et).view(int(ts.fills), 128)
-    del base
     return slot_rows, index, ents
 
 

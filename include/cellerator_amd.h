@@ -1429,8 +1429,8 @@ int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *a, const cx_qcsr_hybrid_layout
 
 /* ---- prepared tail stream ----------------------------------------------------------------
  * The entries of every row from its first tail entry (layout.head_end) on, rearranged once
- * per structure into the order the row-group walk consumes them: blocks of 512 rows ranked
- * by tail length into 16 waves x 4 layers x 8 rows; per gene part of 1,024 and layer, the 8
+ * per structure into the order the row-group walk consumes them: blocks of 1,024 rows ranked
+ * by tail length into 16 waves x 8 layers x 8 rows; per gene part of 1,024 and layer, the 8
  * rows' runs as fills of 16 steps x 8 rows (group-major), padded with the zero row, each
  * row's run even genes first in even groups and odd genes first in odd groups. With the
  * stream the tail kernel loads its entries instead of finding them (no per-pass run count,
@@ -1442,14 +1442,16 @@ typedef struct cx_qcsr_tail_stream {
     uint32_t rows;
     uint32_t first_part;    /* head_cols / 1024 */
     uint32_t parts;         /* gene parts of 1,024 in the stream: ceil(cols / 1024) - first_part */
-    uint32_t blocks;        /* ceil(rows / 512) */
+    uint32_t blocks;        /* ceil(rows / block_rows) */
+    uint32_t block_rows;    /* rows per block: 16 waves x layers x 8 (1,024) */
+    uint32_t layers;        /* layers of 8 rows per wave (8) */
     uint32_t bits;
     uint32_t entry_bytes;   /* 2 (codes of up to 4 bits: gene in part | code << 11) or 4 (8-bit: gene | code << 16) */
     uint64_t fills;         /* fills of 128 entries */
     uint64_t nnz;           /* of the matrix it was built from */
-    uint32_t *slot_rows;    /* [blocks][512]: row of slot (wave * 4 + layer) * 8 + group, 0xffffffff none */
-    uint32_t *fill_index;   /* [blocks * parts * 64 + 1]: first fill of (block, part, wave, layer) in the low
-                               28 bits, steps of its last fill - 1 in the high 4; last entry: the total */
+    uint32_t *slot_rows;    /* [blocks][block_rows]: row of slot (wave * layers + layer) * 8 + group, 0xffffffff none */
+    uint32_t *fill_index;   /* [blocks * parts * (block_rows / 8) + 1]: first fill of (block, part, wave, layer)
+                               in the low 28 bits, steps of its last fill - 1 in the high 4; last entry: the total */
     void *entries;          /* [fills + 3][128] entries (set by cx_qcsr_tail_fill) */
 } cx_qcsr_tail_stream;
 

@@ -16,11 +16,14 @@ from tests.test_hybrid_gpu import _exec, _referee, _skewed
 
 pytestmark = pytest.mark.gpu
 
-ROWS_PER_BLOCK, WAVES, LAYERS, PART = 512, 16, 4, 1024
+WAVES, PART = 16, 1024
 
 
-def _stream_reference(h, head_end, head, bits):
-    """slot_rows, fill_index and entries of the stream by its definition."""
+def _stream_reference(h, head_end, head, bits, LAYERS):
+    """slot_rows, fill_index and entries of the stream by its definition (16 waves of LAYERS
+    layers of 8 rows per block)."""
+    ROWS_PER_BLOCK = WAVES * LAYERS * 8
+    SLOTS = WAVES * LAYERS
     rows = len(h["row_ptr"]) - 1
     cols = int(h["cols"])
     blocks = (rows + ROWS_PER_BLOCK - 1) // ROWS_PER_BLOCK
@@ -29,8 +32,8 @@ def _stream_reference(h, head_end, head, bits):
     wide = bits == 8
     slot_rows = np.full((blocks, ROWS_PER_BLOCK), 0xFFFFFFFF, np.uint32)
     runs = {}  # (block, part, slot) -> list of (local gene, code) in stored order
-    counts = np.zeros(blocks * parts * 64 + 1, np.int64)
-    lasts = np.zeros(blocks * parts * 64, np.int64)
+    counts = np.zeros(blocks * parts * SLOTS + 1, np.int64)
+    lasts = np.zeros(blocks * parts * SLOTS, np.int64)
     for b in range(blocks):
         lens = np.full(ROWS_PER_BLOCK, -1, np.int64)
         for t in range(ROWS_PER_BLOCK):
@@ -56,14 +59,14 @@ def _stream_reference(h, head_end, head, bits):
                 code = (int(h["packed"][bit >> 3]) >> (bit & 7)) & ((1 << bits) - 1)
                 runs.setdefault((b, gene // PART - first, slot), []).append((gene % PART, code))
         for p in range(parts):
-            for ls in range(64):
+            for ls in range(SLOTS):
                 m = 0
                 for g in range(8):
                     run = runs.get((b, p, ls * 8 + g), [])
                     pref = g & 1
                     run.sort(key=lambda x: 0 if (x[0] & 1) == pref else 1)  # stable: gene order within a parity
                     m = max(m, len(run))
-                k = (b * parts + p) * 64 + ls
+                k = (b * parts + p) * SLOTS + ls
                 counts[k] = (m + 15) // 16
                 lasts[k] = 0 if m == 0 else m - 16 * (counts[k] - 1)
     starts = np.zeros_like(counts)
@@ -75,7 +78,7 @@ def _stream_reference(h, head_end, head, bits):
     entries = np.full((total, 128), pad, np.uint32 if wide else np.uint16)
     for (b, p, slot), run in runs.items():
         ls, g = divmod(slot, 8)
-        f0 = int(starts[(b * parts + p) * 64 + ls])
+        f0 = int(starts[(b * parts + p) * SLOTS + ls])
         for k, (gene, code) in enumerate(run):
             entries[f0 + k // 16, g * 16 + k % 16] = gene | (code << (16 if wide else 11))
     return slot_rows, index.astype(np.uint32), entries
@@ -87,7 +90,7 @@ def test_stream_layout_is_bit_exact(oracle, bits, head):
 
     from cellerator_amd.exec_order import hybrid_prepare, tail_arrays
     rng = np.random.default_rng(40 + bits + head)
-    fx = _skewed(oracle, rng, 1100, 3100, bits, 1)
+    fx = _skewed(oracle, rng, 2100, 3100, bits, 1)
     mx, _ = _exec(to_device_qcsr(fx))
     p = hybrid_prepare(mx, head, stream_tail=True)
     torch.cuda.synchronize()
@@ -95,7 +98,8 @@ def test_stream_layout_is_bit_exact(oracle, bits, head):
     h = qcsr_to_host(mx)
     from cellerator_amd.exec_order import hybrid_head_arrays
     he = hybrid_head_arrays(p)[2].cpu().numpy()
-    want_rows, want_index, want_entries = _stream_reference(h, he, head, bits)
+    want_rows, want_index, want_entries = _stream_reference(h, he, head, bits, int(p.tail.layers))
+    assert int(p.tail.block_rows) == WAVES * int(p.tail.layers) * 8
     assert np.array_equal(slot_rows.cpu().numpy().view(np.uint32), want_rows)
     assert np.array_equal(index.cpu().numpy().view(np.uint32), want_index)
     got = entries.cpu().numpy().view(np.uint32 if bits == 8 else np.uint16)
