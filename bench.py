@@ -143,6 +143,10 @@ def full_output_check(out, cpu) -> dict:
 
 
 def bench_qcsr(args, torch, cfg, n_out: int) -> dict:
+    """C2 / C3. The headline is the prepared execution-order path (cx_qcsr_spmm_fwd_hybrid
+    with a dense head and the prepared tail stream), built once per structure (untimed,
+    reported as prepare_ms); the canonical row-group kernel on the unprepared CSR is timed
+    beside it (`canonical_kernel`), and --canonical makes it the headline."""
     from cellerator_amd import _native as N
     from cellerator_amd import qcsr_check_columns, qcsr_pack_gene_affine, qcsr_spmm
     from cellerator_amd.synth import dense_normal, generate_qcsr
@@ -162,56 +166,66 @@ def bench_qcsr(args, torch, cfg, n_out: int) -> dict:
     torch.cuda.synchronize()
     log(f"generated {cfg.name}: nnz={m.nnz} in {time.perf_counter() - t0:.1f}s")
     stream = torch.cuda.current_stream()
+    alg_bytes = m.nbytes_algorithmic(n_out, 2)
+    flops = 2.0 * m.nnz * n_out
+
+    def roofline(kern_ms: float, kernel: str, traffic_key: str) -> dict:
+        achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
+        return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(traffic_key), "kernel": kernel,
+                "kernel_ms_mean": kern_ms, "algorithmic_bytes": alg_bytes,
+                "fp32_fma_tflops": flops / (kern_ms * 1e-3) / 1e12, "valu_fp32_peak_tflops_nonpacked": 78.6}
 
     def launch():
         qcsr_spmm(mt, w, out=out, stream=stream)
 
     wall_ms, ev = time_launches(torch, launch, args.steps, args.warmup, stream)
-    kern_ms = statistics.mean(ev)
-    alg_bytes = m.nbytes_algorithmic(n_out, 2)
-    achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
-    flops = 2.0 * m.nnz * n_out
+    kernel = (("qcsr_spmm_groups" if m.bits and n_out % 64 == 0 and n_out <= 256 else "qcsr_spmm_rowwave")
+              + ("<gene-affine pairs>" if pairs else ""))
+    canonical = {"ms_per_step": wall_ms, "value": m.nnz / (wall_ms * 1e-3), "unit": "nnz/s",
+                 "kernel_ms_median": statistics.median(ev),
+                 "roofline": roofline(statistics.mean(ev), kernel, cfg.name)}
+    log(f"canonical {kernel}: {wall_ms:.3f} ms/step")
+    prepared = None
+    if not args.canonical and args.head >= 0 and m.bits and n_out % 64 == 0 and n_out <= 256:
+        prepared, prep_out = bench_qcsr_prepared(args, torch, mt, w, n_out, stream)
+        prepared["roofline"] = roofline(prepared.pop("kernel_ms_mean"), prepared["kernels"],
+                                        cfg.name + " prepared")
+    head = prepared if prepared is not None else canonical
     res = {
         "metric": "quantized CSR SpMM nnz/s + effective HBM GB/s (% roofline), 1M cells, N=64",
-        "value": m.nnz / (wall_ms * 1e-3),
+        "value": head["value"],
         "unit": "nnz/s",
-        "ms_per_step": wall_ms,
+        "ms_per_step": head["ms_per_step"],
         "dtype": f"u{m.bits}-codes/f16-W/f32-accumulate" if m.bits else "f32",
         "config": {"workload": cfg.name, "rows": m.rows, "genes": m.cols, "nnz": m.nnz,
                    "bits": m.bits, "n_out": n_out, "rhs": "fp16",
                    "nnz_per_row_mean": m.nnz / m.rows, "seed": hex(cfg.seed),
-                   "columns_sorted": bool(mt.flags & N.QCSR_COLUMNS_SORTED)},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(cfg.name),
-                     "kernel": ("qcsr_spmm_groups" if m.bits and n_out % 64 == 0 and n_out <= 256
-                                else "qcsr_spmm_rowwave")
-                               + ("<gene-affine pairs>" if pairs else ""),
-                     "kernel_ms_mean": kern_ms,
-                     "kernel_ms_median": statistics.median(ev),
-                     "algorithmic_bytes": alg_bytes,
-                     "fp32_fma_tflops": flops / (kern_ms * 1e-3) / 1e12,
-                     "valu_fp32_peak_tflops_nonpacked": 78.6},
+                   "columns_sorted": bool(mt.flags & N.QCSR_COLUMNS_SORTED),
+                   "path": ("prepared execution order: dense head + tail stream" if prepared is not None
+                            else "canonical row-group kernel")},
+        "roofline": head["roofline"],
     }
-    hybrid = None
-    if args.head and m.bits and n_out % 64 == 0 and n_out <= 256:
-        hybrid, hyb_out = bench_qcsr_hybrid(args, torch, mt, w, n_out, stream)
+    if prepared is not None:
+        res["prepared_path"] = {k: v for k, v in prepared.items() if k not in ("value", "ms_per_step", "roofline")}
+    res["canonical_kernel"] = canonical
     if not args.no_cpu:
         res["cpu_baseline"], cpu = cpu_baseline_qcsr(m, w, out, args.cpu_rows, host_cores())
-        res["full_output_check"] = full_output_check(out, cpu)
-        if hybrid is not None:
-            hybrid["full_output_check"] = full_output_check(hyb_out, cpu)
-    res["parity_sample"] = parity_sample_qcsr(m, w, out, 2000, seed=cfg.seed)
-    if hybrid is not None:
-        hybrid["parity_sample"] = parity_sample_qcsr(m, w, hyb_out, 2000, seed=cfg.seed)
-        res["execution_order_hybrid"] = hybrid
+        canonical["full_output_check"] = full_output_check(out, cpu)
+        res["full_output_check"] = (full_output_check(prep_out, cpu) if prepared is not None
+                                    else canonical["full_output_check"])
+    canonical["parity_sample"] = parity_sample_qcsr(m, w, out, 2000, seed=cfg.seed)
+    res["parity_sample"] = (parity_sample_qcsr(m, w, prep_out, 2000, seed=cfg.seed) if prepared is not None
+                            else canonical["parity_sample"])
     return res
 
 
-def bench_qcsr_hybrid(args, torch, mt, w, n_out: int, stream):
-    """The same product on the execution-order layout (cx_qcsr_spmm_fwd_hybrid): genes
-    relabelled by popularity, the first --head genes as a dense code plane on the matrix
-    cores, the rest on the row-group kernel. The layout and the reordered weights are built
-    once (untimed, reported as prepare_ms); output rows are the same cells."""
+def bench_qcsr_prepared(args, torch, mt, w, n_out: int, stream):
+    """The same product on the prepared execution-order projection (cx_qcsr_spmm_fwd_hybrid):
+    genes relabelled by popularity (W rows gathered to match, the reference's packed dense
+    operand), the first --head genes as a dense code plane on the matrix cores, the rest
+    from the prepared tail stream on the row-group walk. Built once per structure (untimed,
+    reported as prepare_ms); output rows are the same cells in the same order."""
     from cellerator_amd.exec_order import (hybrid_prepare, hybrid_spmm, pack_rows, popularity_order,
                                            to_execution_order)
 
@@ -220,7 +234,7 @@ def bench_qcsr_hybrid(args, torch, mt, w, n_out: int, stream):
     order = popularity_order(mt)
     mx = to_execution_order(mt, order)
     wx = pack_rows(order, w)
-    layout = hybrid_prepare(mx, args.head)
+    layout = hybrid_prepare(mx, args.head, stream_tail=True)
     torch.cuda.synchronize()
     prep_ms = (time.perf_counter() - t0) * 1e3
     out = torch.empty((mt.rows, n_out), dtype=torch.float32, device="cuda")
@@ -229,13 +243,17 @@ def bench_qcsr_hybrid(args, torch, mt, w, n_out: int, stream):
         hybrid_spmm(layout, wx, out=out, stream=stream)
 
     wall_ms, ev = time_launches(torch, launch, args.steps, args.warmup, stream)
-    log(f"hybrid head={args.head}: {wall_ms:.3f} ms/step (prepare {prep_ms:.0f} ms)")
+    log(f"prepared head={args.head} + tail stream: {wall_ms:.3f} ms/step (prepare {prep_ms:.0f} ms)")
+    plan, entries = layout.tail_storage
     return {"ms_per_step": wall_ms, "value": mt.nnz / (wall_ms * 1e-3), "unit": "nnz/s",
             "head_genes": args.head, "kernel_ms_mean": statistics.mean(ev),
-            "kernels": "qcsr_head_dense (matrix cores, genes < head) + qcsr_spmm_groups (tail) per 64 columns",
+            "kernel_ms_median": statistics.median(ev),
+            "kernels": "qcsr_head_dense (matrix cores, genes < head) + qcsr_spmm_stream (tail) per 64 columns",
             "prepare_ms": prep_ms,
-            "prepare": "popularity order, execution-order relabel, weight rows reordered, dense head layout",
-            "layout_bytes": int(layout.storage.numel())}, out
+            "prepare": "popularity order, execution-order relabel, weight rows reordered, dense head layout, "
+                       "tail stream (plan + fill)",
+            "layout_bytes": int(layout.storage.numel()), "tail_stream_bytes": int(entries.numel() + plan.numel()),
+            "tail_fills": int(layout.tail.fills)}, out
 
 
 def parity_sample_qcsr(m, w, out, count: int, seed: int) -> dict:
@@ -512,8 +530,10 @@ def main() -> int:
     ap.add_argument("--separate-meta", action="store_true",
                     help="C2/C3: time the separate scale/offset arrays instead of interleaved pairs")
     ap.add_argument("--head", type=int, default=2048,
-                    help="qCSR: also time the execution-order hybrid with this many matrix-core head "
-                         "genes (a multiple of 1,024; 0 skips it)")
+                    help="qCSR: matrix-core head genes of the prepared execution-order path (a multiple "
+                         "of 1,024; 0: the whole matrix through the tail stream; -1 skips the path)")
+    ap.add_argument("--canonical", action="store_true",
+                    help="qCSR: headline the canonical row-group kernel on the unprepared CSR")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="run only a plain copy of BYTES (rocprofv3 counter calibration)")
     args = ap.parse_args()
