@@ -206,7 +206,11 @@ FEATURE_ORDER_CANONICAL, FEATURE_ORDER_PACKED = 1, 2
 class CxQcsrHybridLayout(C.Structure):
     _fields_ = [("head_cols", u32), ("rows", u32), ("rows_ld", u32), ("bits", u32), ("decode_policy", u32),
                 ("scale_exp", i32), ("nnz", u64), ("codes", p_void), ("masks", p_void), ("head_end", p_void),
-                ("meta", p_void), ("row_offsets", p_void), ("tail", p_void)]
+                ("meta", p_void), ("row_offsets", p_void), ("tail", p_void), ("head_form", u32),
+                ("reserved", u32), ("code_bytes", p_void), ("lut", p_void)]
+
+
+HEAD_FORM_WORDS, HEAD_FORM_TABLE = 1, 2
 
 
 class CxQcsrTailStream(C.Structure):

@@ -105,26 +105,44 @@ __device__ __forceinline__ std::uint32_t bit_mask(std::uint32_t v) {
     return r;
 }
 
+// Byte k of v as a float, one v_cvt_f32_ubyte<k> (the optimizer would otherwise extract
+// the byte with a shift or a bitfield extract first).
+template<int kByte>
+__device__ __forceinline__ float ubyte_f32(std::uint32_t v) {
+    float r;
+    if constexpr (kByte == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+    else if constexpr (kByte == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+    else if constexpr (kByte == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+
+// x - float(half kHalf of h2), exact (x - rtz(x) fits in fp32), as one v_fma_mix_f32 that
+// widens the fp16 operand itself (the optimizer would split it into a conversion and a
+// subtraction).
+template<int kHalf>
+__device__ __forceinline__ float sub_half(float x, std::uint32_t h2) {
+    float r;
+    if constexpr (kHalf == 0) asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(x));
+    else asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(x));
+    return r;
+}
+
 // Code of gene j of an octet as a float: 4- and 8-bit codes through byte conversions.
 template<int kBits, int kJ>
 __device__ __forceinline__ float octet_code(const std::uint32_t (&w)[2], std::uint32_t lo4, std::uint32_t hi4) {
-    if constexpr (kBits == 8) return static_cast<float>((w[kJ >> 2] >> (8 * (kJ & 3))) & 0xffu);
-    else if constexpr (kBits == 4) return static_cast<float>((((kJ & 1) != 0 ? hi4 : lo4) >> (8 * (kJ >> 1))) & 0xffu);
+    if constexpr (kBits == 8) return ubyte_f32<kJ & 3>(w[kJ >> 2]);
+    else if constexpr (kBits == 4) return ubyte_f32<(kJ >> 1)>((kJ & 1) != 0 ? hi4 : lo4);
     else return static_cast<float>((w[0] >> (kJ * kBits)) & ((1u << kBits) - 1u));
 }
 
-// fp16 parts of a pair of values: rtz conversions, residuals through v_fma_mix_f32 (the fp16
-// part is widened inside the instruction).
+// fp16 parts of a pair of values: rtz conversions, each residual one v_fma_mix_f32.
 __device__ __forceinline__ void split_pair(float x0, float x1, std::uint32_t &hw, std::uint32_t &mw, std::uint32_t &lw) {
-    const cx_fp16x2 h2 = __builtin_amdgcn_cvt_pkrtz(x0, x1);
-    const float r0 = __builtin_fmaf(static_cast<float>(h2[0]), -1.0f, x0);
-    const float r1 = __builtin_fmaf(static_cast<float>(h2[1]), -1.0f, x1);
-    const cx_fp16x2 m2 = __builtin_amdgcn_cvt_pkrtz(r0, r1);
-    const cx_fp16x2 l2 = __builtin_amdgcn_cvt_pkrtz(__builtin_fmaf(static_cast<float>(m2[0]), -1.0f, r0),
-                                                     __builtin_fmaf(static_cast<float>(m2[1]), -1.0f, r1));
-    hw = __builtin_bit_cast(std::uint32_t, h2);
-    mw = __builtin_bit_cast(std::uint32_t, m2);
-    lw = __builtin_bit_cast(std::uint32_t, l2);
+    hw = __builtin_bit_cast(std::uint32_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+    const float r0 = sub_half<0>(x0, hw);
+    const float r1 = sub_half<1>(x1, hw);
+    mw = __builtin_bit_cast(std::uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1));
+    lw = __builtin_bit_cast(std::uint32_t, __builtin_amdgcn_cvt_pkrtz(sub_half<0>(r0, mw), sub_half<1>(r1, mw)));
 }
 
 template<int kBits, int kPolicy, int kJ>
@@ -213,23 +231,207 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void qcsr_head_dense(HeadArgs h
 #pragma unroll
         for (int t = 0; t < 4; ++t) acc[b][t] = cx_float4{0.0f, 0.0f, 0.0f, 0.0f};
 
+    auto chunk = [&](const ChunkLoads<kBits> &L) {
+#pragma unroll
+        for (int b = 0; b < kTiles; ++b) {
+            cx_half8 bh, bm, bl;
+            decode_octet<kBits, kPolicy>(L.cw[b], q, L.mw[b], L.md, roff[b], bh, bm, bl);
+            // each accumulator's three products are 4 instructions apart
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(L.aw[t], bh, acc[b][t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(L.aw[t], bm, acc[b][t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(L.aw[t], bl, acc[b][t], 0, 0, 0);
+        }
+    };
     ChunkLoads<kBits> cur, nxt;
     if (h.chunks != 0u) load_chunk<kBits>(cur, h, 0u, q, r16, row0);
     for (std::uint32_t c = 0; c < h.chunks; ++c) {
         if (c + 1u < h.chunks) load_chunk<kBits>(nxt, h, c + 1u, q, r16, row0);
+        chunk(cur);
+        cur = nxt;
+    }
+
+#pragma unroll
+    for (int b = 0; b < kTiles; ++b) {
+        const std::uint32_t row = row0 + 16u * b;
+        if (row < h.rows) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                float *o = h.partial + static_cast<std::uint64_t>(row) * 64u + t * 16 + 4 * q;
+                *reinterpret_cast<float4 *>(o) = make_float4(acc[b][t][0] * h.inv_scale, acc[b][t][1] * h.inv_scale,
+                                                             acc[b][t][2] * h.inv_scale, acc[b][t][3] * h.inv_scale);
+            }
+        }
+    }
+}
+
+// ---- the table form: code bytes and a per-gene table of pre-split values -------------------
+//
+// For codes of up to 4 bits under a per-gene decode policy, the 17 values a head gene can take
+// (codes 0..15, and "not stored") are split once, at prepare, into their three fp16 parts:
+// lut[chunk][gene][code] = (hi, mid, lo, 0), entry 16 all zero. The head plane then holds one
+// byte per (row, gene), code * 8 or 128 when the gene is not stored (the table entry's byte
+// offset), chunk-major: bytes[chunk][rows_ld][32]. Decoding a value is one table read; the
+// parts of two genes are packed into the fragments with byte permutes. The values and their
+// order of accumulation are those of the per-value decode above, so the results are the same.
+//
+// Workgroup: 4 waves of 64 rows. Per 32-gene chunk the W^T fragments (4 KB, in fragment order),
+// the chunk's table (4,352 B) and the workgroup's code bytes (8 KB) go through an LDS double
+// buffer: each lane loads up to five 16-byte pieces of chunk c + 2 from memory while chunk c
+// is computed and stores them into the free buffer at the start of chunk c + 1; one barrier
+// per chunk. Every memory load is thus consumed a whole chunk after it was issued.
+
+constexpr int kLutWaves = 4;
+constexpr std::uint32_t kLutRows = kLutWaves * kRowsPerWave;  // 256 rows per workgroup
+constexpr std::uint32_t kLayoutRows = 512;                    // row granularity of the head planes
+constexpr std::uint32_t kLutEntries = 17;                     // codes 0..15 and "not stored"
+constexpr std::uint32_t kLutGeneBytes = kLutEntries * 8u;     // 136
+constexpr std::uint32_t kLutChunkBytes = 32u * kLutGeneBytes; // 4,352
+constexpr std::uint32_t kCodeChunkBytes = kLutRows * 32u;     // the workgroup's code bytes of one chunk
+static_assert(kLayoutRows % kLutRows == 0u && kLayoutRows % kHeadRows == 0u, "head plane rows");
+constexpr std::uint32_t kAbsentWord = 0x80808080u;            // four genes not stored: entry 16 (byte 128)
+
+struct LutArgs {
+    const std::uint8_t *bytes;   // [head/32][rows_ld][32]
+    const uint4 *lut;            // [head/32][kLutChunkBytes / 16]
+    const std::uint16_t *panel;  // fp16 [head/32][panel_n][32] at this launch's first column
+    float *partial;              // [rows][64] fp32: Y_head
+    std::uint32_t rows;
+    std::uint32_t rows_ld;
+    std::uint32_t chunks;
+    std::uint32_t panel_n;
+    float inv_scale;
+};
+
+struct LutShared {
+    uint4 a[2][4][kWave];                  // W^T fragments: [buffer][column block][lane]
+    uint4 lut[2][kLutChunkBytes / 16];     // the chunk's table
+    uint4 codes[2][kCodeChunkBytes / 16];  // the workgroup's code bytes: [row][32]
+};
+
+// The share of chunk c is loaded in five 16-byte pieces per thread (256 threads), each kind
+// of piece in its own step so no step branches per lane: (0) the A fragments, column block
+// tid / 64, lane tid % 64 (row tid % 16 of the block, genes 8 (tid % 64 / 16) .. +7);
+// (1) table pieces 0..255; (2), (3) the workgroup's code bytes, pieces tid and 256 + tid;
+// (4) table pieces 256..271 (threads 0..15).
+constexpr int kSharePieces5 = 5;
+constexpr int kLutPieces = static_cast<int>(kLutChunkBytes / 16u);  // 272
+static_assert(kLutWaves * kWave == 256 && kCodeChunkBytes / 16u == 512u && kLutPieces == 272, "share pieces");
+
+template<int kK>
+__device__ __forceinline__ bool has_piece(int tid) {
+    return kK != 4 || tid < kLutPieces - 256;
+}
+
+template<int kK>
+__device__ __forceinline__ uint4 load_piece(const LutArgs &h, std::uint32_t c, int tid, std::uint32_t wg_row) {
+    if constexpr (kK == 0) {
+        const std::uint32_t t = static_cast<std::uint32_t>(tid) / 64u, l = static_cast<std::uint32_t>(tid) % 64u;
+        return *static_cast<const uint4 *>(__builtin_assume_aligned(
+            h.panel + (static_cast<std::uint64_t>(c) * h.panel_n + t * 16u + l % 16u) * 32u + 8u * (l / 16u), 16));
+    } else if constexpr (kK == 1 || kK == 4) {
+        return h.lut[static_cast<std::uint64_t>(c) * kLutPieces + (kK == 4 ? 256 : 0) + tid];
+    } else {
+        return *reinterpret_cast<const uint4 *>(h.bytes + (static_cast<std::uint64_t>(c) * h.rows_ld + wg_row) * 32u
+                                                + static_cast<std::uint32_t>((kK == 3 ? 256 : 0) + tid) * 16u);
+    }
+}
+
+template<int kK>
+__device__ __forceinline__ void store_piece(LutShared &sh, int buf, int tid, uint4 v) {
+    if constexpr (kK == 0) sh.a[buf][tid / 64][tid % 64] = v;
+    else if constexpr (kK == 1 || kK == 4) sh.lut[buf][(kK == 4 ? 256 : 0) + tid] = v;
+    else sh.codes[buf][(kK == 3 ? 256 : 0) + tid] = v;
+}
+
+// Byte k of v as a 32-bit offset.
+template<int kK>
+__device__ __forceinline__ std::uint32_t byte_of(std::uint32_t v) {
+    return kK == 3 ? v >> 24 : (v >> (8 * kK)) & 0xffu;
+}
+
+__global__ __launch_bounds__(kLutWaves * kWave) void qcsr_head_lut(LutArgs h) {
+    __shared__ LutShared sh;
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int r16 = lane & 15;
+    const int q = lane >> 4;
+    const std::uint32_t wg_row = blockIdx.x * kLutRows;
+    const std::uint32_t row0 = wg_row + static_cast<std::uint32_t>(wave * kRowsPerWave + r16);
+    cx_float4 acc[kTiles][4];
+#pragma unroll
+    for (int b = 0; b < kTiles; ++b)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[b][t] = cx_float4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    uint4 sv[kSharePieces5];
+#pragma unroll
+    for (int k = 0; k < kSharePieces5; ++k) sv[k] = make_uint4(0u, 0u, 0u, 0u);
+    auto load_share = [&](std::uint32_t c) {
+        sv[0] = load_piece<0>(h, c, tid, wg_row);
+        sv[1] = load_piece<1>(h, c, tid, wg_row);
+        sv[2] = load_piece<2>(h, c, tid, wg_row);
+        sv[3] = load_piece<3>(h, c, tid, wg_row);
+        if (has_piece<4>(tid)) sv[4] = load_piece<4>(h, c, tid, wg_row);
+    };
+    auto store_share = [&](int buf) {
+        store_piece<0>(sh, buf, tid, sv[0]);
+        store_piece<1>(sh, buf, tid, sv[1]);
+        store_piece<2>(sh, buf, tid, sv[2]);
+        store_piece<3>(sh, buf, tid, sv[3]);
+        if (has_piece<4>(tid)) store_piece<4>(sh, buf, tid, sv[4]);
+    };
+    if (h.chunks != 0u) {
+        load_share(0u);
+        store_share(0);
+    }
+    if (h.chunks > 1u) load_share(1u);
+    __syncthreads();
+    for (std::uint32_t c = 0; c < h.chunks; ++c) {
+        const int buf = static_cast<int>(c & 1u);
+        if (c + 1u < h.chunks) store_share(buf ^ 1);  // into the buffer chunk c - 1 used (all waves passed the barrier)
+        if (c + 2u < h.chunks) load_share(c + 2u);
+        cx_half8 aw[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) aw[t] = __builtin_bit_cast(cx_half8, sh.a[buf][t][lane]);
+        const char *lb = reinterpret_cast<const char *>(&sh.lut[buf][0]) + 8u * q * kLutGeneBytes;
+        const char *cbase = reinterpret_cast<const char *>(&sh.codes[buf][0])
+            + (wave * kRowsPerWave + r16) * 32 + 8 * q;
 #pragma unroll
         for (int b = 0; b < kTiles; ++b) {
-            cx_half8 bh, bm, bl;
-            decode_octet<kBits, kPolicy>(cur.cw[b], q, cur.mw[b], cur.md, roff[b], bh, bm, bl);
-            // each accumulator's three products are 4 instructions apart
+            uint2 e[8];
+            const uint2 cw = *reinterpret_cast<const uint2 *>(cbase + 16 * 32 * b);
+            const std::uint32_t w0 = cw.x, w1 = cw.y;
+            e[0] = *reinterpret_cast<const uint2 *>(lb + 0 * kLutGeneBytes + byte_of<0>(w0));
+            e[1] = *reinterpret_cast<const uint2 *>(lb + 1 * kLutGeneBytes + byte_of<1>(w0));
+            e[2] = *reinterpret_cast<const uint2 *>(lb + 2 * kLutGeneBytes + byte_of<2>(w0));
+            e[3] = *reinterpret_cast<const uint2 *>(lb + 3 * kLutGeneBytes + byte_of<3>(w0));
+            e[4] = *reinterpret_cast<const uint2 *>(lb + 4 * kLutGeneBytes + byte_of<0>(w1));
+            e[5] = *reinterpret_cast<const uint2 *>(lb + 5 * kLutGeneBytes + byte_of<1>(w1));
+            e[6] = *reinterpret_cast<const uint2 *>(lb + 6 * kLutGeneBytes + byte_of<2>(w1));
+            e[7] = *reinterpret_cast<const uint2 *>(lb + 7 * kLutGeneBytes + byte_of<3>(w1));
+            std::uint32_t hw[4], mw[4], lw[4];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.aw[t], bh, acc[b][t], 0, 0, 0);
+            for (int k = 0; k < 4; ++k) {
+                // (hi | mid << 16, lo) of genes 2k and 2k + 1 -> hi pair, mid pair, lo pair
+                hw[k] = __builtin_amdgcn_perm(e[2 * k + 1].x, e[2 * k].x, 0x05040100u);
+                mw[k] = __builtin_amdgcn_perm(e[2 * k + 1].x, e[2 * k].x, 0x07060302u);
+                lw[k] = __builtin_amdgcn_perm(e[2 * k + 1].y, e[2 * k].y, 0x05040100u);
+            }
+            const cx_half8 bh = __builtin_bit_cast(cx_half8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+            const cx_half8 bm = __builtin_bit_cast(cx_half8, make_uint4(mw[0], mw[1], mw[2], mw[3]));
+            const cx_half8 bl = __builtin_bit_cast(cx_half8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
 #pragma unroll
-            for (int t = 0; t < 4; ++t) acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.aw[t], bm, acc[b][t], 0, 0, 0);
+            for (int t = 0; t < 4; ++t) acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[t], bh, acc[b][t], 0, 0, 0);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.aw[t], bl, acc[b][t], 0, 0, 0);
+            for (int t = 0; t < 4; ++t) acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[t], bm, acc[b][t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[t], bl, acc[b][t], 0, 0, 0);
         }
-        cur = nxt;
+        __syncthreads();  // buffer `buf` is free again; chunk c + 1 is in place
     }
 
 #pragma unroll
@@ -308,6 +510,67 @@ __global__ __launch_bounds__(256) void dense_head_build(BuildArgs a) {
     }
     if (row < a.rows) a.head_end[row] = static_cast<std::int32_t>(e);
     if (bad) atomicOr(a.error, 1u);
+}
+
+// Table form: one thread per row writes every chunk's 32 bytes (128: not stored), then the
+// code byte (code * 8) of each stored head gene; also the row's first tail entry.
+template<int kBits>
+__global__ __launch_bounds__(256) void dense_head_bytes(BuildArgs a, std::uint8_t *bytes) {
+    const std::uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= a.rows_ld) return;
+    constexpr std::uint32_t kMask = (1u << kBits) - 1u;
+    std::int64_t e = 0, end = 0, rb = 0, pbit = 0;
+    if (row < a.rows) {
+        rb = e = a.row_ptr[row];
+        end = a.row_ptr[row + 1];
+        pbit = static_cast<std::int64_t>(a.packed_row_ptr[row]) * 8;
+    }
+    std::int64_t prev = -1;
+    bool bad = false;
+    const std::uint32_t chunks = a.head / 32u;
+    const uint4 absent = make_uint4(kAbsentWord, kAbsentWord, kAbsentWord, kAbsentWord);
+    for (std::uint32_t c = 0; c < chunks; ++c) {
+        std::uint8_t *dst = bytes + (static_cast<std::uint64_t>(c) * a.rows_ld + row) * 32u;
+        reinterpret_cast<uint4 *>(dst)[0] = absent;
+        reinterpret_cast<uint4 *>(dst)[1] = absent;
+        const std::int64_t g_hi = static_cast<std::int64_t>(c + 1u) * 32;
+        while (e < end) {
+            const std::int64_t g = a.col_idx[e];
+            if (g >= g_hi) break;
+            if (g <= prev) {  // repeated, decreasing or negative gene: not a sorted row
+                bad = true;
+                break;
+            }
+            const std::int64_t bit = pbit + (e - rb) * kBits;
+            const std::uint32_t code = (static_cast<std::uint32_t>(a.packed[bit >> 3]) >> (bit & 7)) & kMask;
+            dst[g - static_cast<std::int64_t>(c) * 32] = static_cast<std::uint8_t>(code * 8u);
+            prev = g;
+            ++e;
+        }
+        if (bad) e = end;  // the remaining chunks of the row stay "not stored"
+    }
+    if (row < a.rows) a.head_end[row] = static_cast<std::int32_t>(e);
+    if (bad) atomicOr(a.error, 1u);
+}
+
+// lut[chunk][gene][code] = the three round-toward-zero fp16 parts of fma(code, 2^k s, 2^k o)
+// (the per-value decode's split, computed once) for codes up to qmax; other entries (codes
+// the width cannot hold, and entry 16) zero.
+__global__ __launch_bounds__(256) void head_lut_kernel(const float2 *meta, std::uint32_t head, std::uint32_t qmax,
+                                                       std::uint16_t *lut) {
+    const std::uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= head * kLutEntries) return;
+    const std::uint32_t g = i / kLutEntries, code = i % kLutEntries;
+    std::uint32_t hw = 0u, mw = 0u, lw = 0u;
+    if (code <= qmax) {
+        const float2 md = meta[g];
+        split_pair(__builtin_fmaf(static_cast<float>(code), md.x, md.y), 0.0f, hw, mw, lw);
+    }
+    std::uint16_t *dst = lut + ((g / 32u) * kLutChunkBytes + (g % 32u) * kLutGeneBytes + code * 8u) / 2u;
+    dst[0] = static_cast<std::uint16_t>(hw & 0xffffu);
+    dst[1] = static_cast<std::uint16_t>(mw & 0xffffu);
+    dst[2] = static_cast<std::uint16_t>(lw & 0xffffu);
+    dst[3] = 0u;
 }
 
 // Largest |decoded value| any code of a head gene can take, as float bits (non-negative
@@ -396,27 +659,55 @@ int validate_hybrid(const cx_qcsr_matrix *m, std::uint32_t head, const char *who
 
 constexpr std::uint64_t align256(std::uint64_t b) { return (b + 255u) & ~std::uint64_t{255u}; }
 
+// Table form for codes of up to 4 bits under a per-gene policy; code words and presence bits
+// otherwise (8-bit codes have 257 table entries per gene; row offsets make a value depend on
+// the row).
+std::uint32_t head_form(const cx_qcsr_matrix *m) {
+    return m->bits <= 4u && m->decode_policy != CX_DECODE_COLUMN_SCALE_ROW_OFFSET ? CX_HEAD_FORM_TABLE
+                                                                                  : CX_HEAD_FORM_WORDS;
+}
+
 struct LayoutSizes {
-    std::uint64_t header, codes, masks, head_end, meta, row_offsets, total;
-    std::uint32_t rows_ld;
+    std::uint64_t header, codes, masks, bytes, lut, head_end, meta, row_offsets, total;
+    std::uint32_t rows_ld, form;
 };
 
 LayoutSizes layout_sizes(const cx_qcsr_matrix *m, std::uint32_t head) {
     LayoutSizes s{};
-    s.rows_ld = static_cast<std::uint32_t>((static_cast<std::uint64_t>(m->rows) + kHeadRows - 1) / kHeadRows * kHeadRows);
+    s.form = head_form(m);
+    s.rows_ld = static_cast<std::uint32_t>((static_cast<std::uint64_t>(m->rows) + kLayoutRows - 1) / kLayoutRows * kLayoutRows);
     s.header = 256;
-    s.codes = align256(static_cast<std::uint64_t>(head) * m->bits / 32u * s.rows_ld * 4u);
-    s.masks = align256(static_cast<std::uint64_t>(head) / 32u * s.rows_ld * 4u);
+    if (s.form == CX_HEAD_FORM_WORDS) {
+        s.codes = align256(static_cast<std::uint64_t>(head) * m->bits / 32u * s.rows_ld * 4u);
+        s.masks = align256(static_cast<std::uint64_t>(head) / 32u * s.rows_ld * 4u);
+    } else {
+        s.bytes = align256(static_cast<std::uint64_t>(head) * s.rows_ld);
+        s.lut = align256(static_cast<std::uint64_t>(head) / 32u * kLutChunkBytes);
+    }
     s.head_end = align256(static_cast<std::uint64_t>(m->rows) * 4u);
     s.meta = align256(static_cast<std::uint64_t>(head) * 8u);
     s.row_offsets = m->decode_policy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET ? align256(static_cast<std::uint64_t>(m->rows) * 4u) : 0u;
-    s.total = s.header + s.codes + s.masks + s.head_end + s.meta + s.row_offsets;
+    s.total = s.header + s.codes + s.masks + s.bytes + s.lut + s.head_end + s.meta + s.row_offsets;
     return s;
 }
 
 // Launches the dense head kernel for one 64-column block.
 int launch_head(const cx_qcsr_hybrid_layout &L, const std::uint16_t *panel, std::uint32_t panel_n, float *partial,
                 hipStream_t stream) {
+    if (L.head_form == CX_HEAD_FORM_TABLE) {
+        LutArgs t{};
+        t.bytes = L.code_bytes;
+        t.lut = reinterpret_cast<const uint4 *>(L.lut);
+        t.panel = panel;
+        t.partial = partial;
+        t.rows = L.rows;
+        t.rows_ld = L.rows_ld;
+        t.chunks = L.head_cols / 32u;
+        t.panel_n = panel_n;
+        t.inv_scale = std::ldexp(1.0f, -L.scale_exp);
+        hipLaunchKernelGGL(qcsr_head_lut, dim3(L.rows_ld / kLutRows), dim3(kLutWaves * kWave), 0, stream, t);
+        return check_launch("qcsr_head_lut");
+    }
     HeadArgs h{};
     h.codes = L.codes;
     h.masks = L.masks;
@@ -478,12 +769,20 @@ extern "C" int cx_qcsr_hybrid_prepare(const cx_qcsr_matrix *m, uint32_t head_col
     L.bits = m->bits;
     L.decode_policy = m->decode_policy;
     L.nnz = m->nnz;
+    L.head_form = sz.form;
     auto *base = static_cast<unsigned char *>(storage);
     std::uint64_t off = sz.header;
-    L.codes = reinterpret_cast<uint32_t *>(base + off);
-    off += sz.codes;
-    L.masks = reinterpret_cast<uint32_t *>(base + off);
-    off += sz.masks;
+    if (sz.form == CX_HEAD_FORM_WORDS) {
+        L.codes = reinterpret_cast<uint32_t *>(base + off);
+        off += sz.codes;
+        L.masks = reinterpret_cast<uint32_t *>(base + off);
+        off += sz.masks;
+    } else {
+        L.code_bytes = reinterpret_cast<uint8_t *>(base + off);
+        off += sz.bytes;
+        L.lut = reinterpret_cast<uint16_t *>(base + off);
+        off += sz.lut;
+    }
     L.head_end = reinterpret_cast<int32_t *>(base + off);
     off += sz.head_end;
     L.meta = reinterpret_cast<float *>(base + off);
@@ -515,11 +814,19 @@ extern "C" int cx_qcsr_hybrid_prepare(const cx_qcsr_matrix *m, uint32_t head_col
         b.head_end = L.head_end;
         b.error = words + 2;
         const dim3 grid(L.rows_ld / 256u), block(256);
-        switch (m->bits) {
-        case 1: hipLaunchKernelGGL(dense_head_build<1>, grid, block, 0, s, b); break;
-        case 2: hipLaunchKernelGGL(dense_head_build<2>, grid, block, 0, s, b); break;
-        case 4: hipLaunchKernelGGL(dense_head_build<4>, grid, block, 0, s, b); break;
-        default: hipLaunchKernelGGL(dense_head_build<8>, grid, block, 0, s, b); break;
+        if (sz.form == CX_HEAD_FORM_TABLE) {
+            switch (m->bits) {
+            case 1: hipLaunchKernelGGL(dense_head_bytes<1>, grid, block, 0, s, b, L.code_bytes); break;
+            case 2: hipLaunchKernelGGL(dense_head_bytes<2>, grid, block, 0, s, b, L.code_bytes); break;
+            default: hipLaunchKernelGGL(dense_head_bytes<4>, grid, block, 0, s, b, L.code_bytes); break;
+            }
+        } else {
+            switch (m->bits) {
+            case 1: hipLaunchKernelGGL(dense_head_build<1>, grid, block, 0, s, b); break;
+            case 2: hipLaunchKernelGGL(dense_head_build<2>, grid, block, 0, s, b); break;
+            case 4: hipLaunchKernelGGL(dense_head_build<4>, grid, block, 0, s, b); break;
+            default: hipLaunchKernelGGL(dense_head_build<8>, grid, block, 0, s, b); break;
+            }
         }
     }
     rc = check_launch("cx_qcsr_hybrid_prepare");
@@ -554,6 +861,12 @@ extern "C" int cx_qcsr_hybrid_prepare(const cx_qcsr_matrix *m, uint32_t head_col
         rc = check_launch("cx_qcsr_hybrid_prepare");
         if (rc != CX_STATUS_SUCCESS) return rc;
     }
+    if (sz.form == CX_HEAD_FORM_TABLE && head_cols != 0u) {
+        hipLaunchKernelGGL(head_lut_kernel, dim3((head_cols * kLutEntries + 255u) / 256u), dim3(256), 0, s,
+                           reinterpret_cast<const float2 *>(L.meta), head_cols, (1u << m->bits) - 1u, L.lut);
+        rc = check_launch("cx_qcsr_hybrid_prepare");
+        if (rc != CX_STATUS_SUCCESS) return rc;
+    }
     *layout = L;
     return CX_STATUS_SUCCESS;
 }
@@ -583,8 +896,10 @@ extern "C" int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *m, const cx_qcsr_hy
     int rc = validate_hybrid(m, L.head_cols, "cx_qcsr_spmm_fwd_hybrid: null matrix");
     if (rc != CX_STATUS_SUCCESS) return rc;
     if (L.rows != m->rows || L.bits != m->bits || L.decode_policy != m->decode_policy || L.nnz != m->nnz
-        || L.rows_ld != layout_sizes(m, L.head_cols).rows_ld
-        || (L.head_cols != 0u && (L.codes == nullptr || L.masks == nullptr || L.head_end == nullptr || L.meta == nullptr)))
+        || L.rows_ld != layout_sizes(m, L.head_cols).rows_ld || L.head_form != head_form(m) || L.head_end == nullptr
+        || (L.head_cols != 0u && (L.meta == nullptr
+                                  || (L.head_form == CX_HEAD_FORM_WORDS ? L.codes == nullptr || L.masks == nullptr
+                                                                        : L.code_bytes == nullptr || L.lut == nullptr))))
         return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd_hybrid: the layout was not prepared for this matrix");
     if (rhs == nullptr || out == nullptr)
         return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd_hybrid: null rhs or output");

@@ -205,9 +205,11 @@ def tail_arrays(p: HybridProjection):
 
 
 def hybrid_head_arrays(p: HybridProjection):
-    """(codes, masks, head_end, meta) of the prepared layout as device tensor views:
-    codes [H * bits / 32, rows_ld] and masks [H / 32, rows_ld] int32 (u32 bits),
-    head_end [rows] int32, meta [H, 2] float32 (times 2^scale_exp)."""
+    """The prepared head as device tensor views: (codes, masks, head_end, meta) in the words
+    form -- codes [H * bits / 32, rows_ld] and masks [H / 32, rows_ld] int32 (u32 bits) --
+    or (code_bytes, lut, head_end, meta) in the table form -- code_bytes [H / 32, rows_ld, 32]
+    uint8 and lut [H, 17, 4] int16 (fp16 bits); head_end [rows] int32, meta [H, 2] float32
+    (times 2^scale_exp)."""
     L, base = p.layout, p.storage.data_ptr()
 
     def view(ptr, count, dtype, shape):
@@ -216,10 +218,14 @@ def hybrid_head_arrays(p: HybridProjection):
         return p.storage[off:off + count * size].view(dtype).view(shape)
 
     h, ld = p.head_cols, int(L.rows_ld)
-    codes = view(L.codes, h * L.bits // 32 * ld, torch.int32, (h * L.bits // 32, ld))
-    masks = view(L.masks, h // 32 * ld, torch.int32, (h // 32, ld))
     head_end = view(L.head_end, int(L.rows), torch.int32, (int(L.rows),))
     meta = view(L.meta, 2 * h, torch.float32, (h, 2))
+    if L.head_form == N.HEAD_FORM_TABLE:
+        code_bytes = view(L.code_bytes, h * ld, torch.uint8, (h // 32, ld, 32))
+        lut = view(L.lut, h * 17 * 4, torch.int16, (h, 17, 4))
+        return code_bytes, lut, head_end, meta
+    codes = view(L.codes, h * L.bits // 32 * ld, torch.int32, (h * L.bits // 32, ld))
+    masks = view(L.masks, h // 32 * ld, torch.int32, (h // 32, ld))
     return codes, masks, head_end, meta
 
 

@@ -1389,20 +1389,31 @@ const char *cx_exec_last_error(void);
 typedef struct cx_qcsr_hybrid_layout {
     uint32_t head_cols;     /* H, a multiple of 1,024 (0: no head) */
     uint32_t rows;
-    uint32_t rows_ld;       /* rows rounded up to 256: the row stride of codes and masks */
+    uint32_t rows_ld;       /* rows rounded up to 512: the row stride of the head planes */
     uint32_t bits;
     uint32_t decode_policy;
     int32_t scale_exp;      /* k: meta and row_offsets hold values times 2^k */
     uint64_t nnz;           /* of the matrix it was built from */
-    uint32_t *codes;        /* [H * bits / 32][rows_ld]: word w of a row = codes of genes
-                               [w * 32 / bits, (w + 1) * 32 / bits), 0 where not stored */
-    uint32_t *masks;        /* [H / 32][rows_ld]: presence bit of gene g at bit g % 32 */
+    uint32_t *codes;        /* words form: [H * bits / 32][rows_ld]: word w of a row = codes of genes
+                               [w * 32 / bits, (w + 1) * 32 / bits), 0 where not stored; else NULL */
+    uint32_t *masks;        /* words form: [H / 32][rows_ld]: presence bit of gene g at bit g % 32; else NULL */
     int32_t *head_end;      /* [rows]: first entry of each row with gene >= H */
     float *meta;            /* [H] (scale, offset) pairs times 2^k */
     float *row_offsets;     /* [rows] times 2^k (column-scale / row-offset policy), else NULL */
     const struct cx_qcsr_tail_stream *tail;  /* prepared tail stream (cx_qcsr_tail_fill), or NULL:
                                                 the tail then runs on the row-group kernel */
+    uint32_t head_form;     /* CX_HEAD_FORM_WORDS (codes, masks) or CX_HEAD_FORM_TABLE (code_bytes, lut) */
+    uint32_t reserved;
+    uint8_t *code_bytes;    /* table form: [H/32][rows_ld][32]: code * 8 of each (row, gene), 128 where not stored */
+    uint16_t *lut;          /* table form: [H/32][32][17][4] fp16: (hi, mid, lo, 0) of each code's value times
+                               2^k (the three-part split above), entry 16 zero */
 } cx_qcsr_hybrid_layout;
+
+/* Head forms: code words and presence bits, decoded per value (8-bit codes or the
+ * column-scale / row-offset policy); or code bytes and a per-gene table of the pre-split
+ * values (codes of up to 4 bits under a per-gene policy). Same values and sums either way. */
+#define CX_HEAD_FORM_WORDS 1u
+#define CX_HEAD_FORM_TABLE 2u
 
 /* Device bytes of the head layout of `a` (a.flags must include CX_QCSR_COLUMNS_SORTED). */
 int cx_qcsr_hybrid_layout_bytes(const cx_qcsr_matrix *a, uint32_t head_cols, uint64_t *bytes);

@@ -137,12 +137,24 @@ def test_dense_head_layout_is_bit_exact(oracle, bits, policy):
         m = qcsr_pack_gene_affine(m)
     mx, _ = _exec(m)
     p = hybrid_prepare(mx, 2048)
-    codes, masks, head_end, meta = hybrid_head_arrays(p)
+    first, second, head_end, meta = hybrid_head_arrays(p)
     torch.cuda.synchronize()
     h = qcsr_to_host(mx)
     want_codes, want_masks, want_end = _layout_reference(h, 2048, int(p.layout.rows_ld))
-    assert np.array_equal(codes.cpu().numpy().view(np.uint32), want_codes)
-    assert np.array_equal(masks.cpu().numpy().view(np.uint32), want_masks)
+    table = bits <= 4 and policy != 2
+    assert p.layout.head_form == (2 if table else 1)
+    if table:
+        # code bytes: code * 8 where stored, 128 elsewhere (the same codes and presence as the words)
+        per_word = 32 // bits
+        g = np.arange(2048)
+        codes = (want_codes[g // per_word, :] >> ((g % per_word) * bits)[:, None]) & ((1 << bits) - 1)
+        present = (want_masks[g // 32, :] >> (g % 32)[:, None]) & 1
+        want_bytes = np.where(present == 1, codes * 8, 128).astype(np.uint8)  # [gene, rows_ld]
+        got_bytes = first.cpu().numpy()  # [chunk, rows_ld, 32]
+        assert np.array_equal(got_bytes.transpose(0, 2, 1).reshape(2048, -1), want_bytes)
+    else:
+        assert np.array_equal(first.cpu().numpy().view(np.uint32), want_codes)
+        assert np.array_equal(second.cpu().numpy().view(np.uint32), want_masks)
     assert np.array_equal(head_end.cpu().numpy(), want_end)
     # scale exponent and metadata: k = 14 - floor(log2 B), B = largest |decoded value| of a head code
     if policy == 3:
@@ -162,6 +174,32 @@ def test_dense_head_layout_is_bit_exact(oracle, bits, policy):
     assert np.array_equal(got_meta[:, 0], (s * 2.0 ** k).astype(np.float32))
     if policy != 2:
         assert np.array_equal(got_meta[:, 1], (o * 2.0 ** k).astype(np.float32))
+    if table:
+        # the value table: three round-toward-zero fp16 parts of fma(code, 2^k s, 2^k o) in
+        # float32, summing back to it exactly wherever the last part is normal; entry 16 zero
+        lut = second.cpu().numpy().view(np.float16).astype(np.float32)  # [gene, 17, 4]
+        sk, ok = got_meta[:, 0], got_meta[:, 1]
+        x = np.arange(16, dtype=np.float64)[None, :] * sk[:, None].astype(np.float64) + ok[:, None].astype(np.float64)
+        x32 = x.astype(np.float32)  # one rounding: the fp32 fma (the product is exact in fp64)
+        # rtz to fp16 by truncating the float32 to 11 significant bits (values < 2^15 here)
+
+        def rtz16(v):
+            v = v.astype(np.float32)
+            bits_ = v.view(np.uint32)
+            e = ((bits_ >> 23) & 0xFF).astype(np.int64) - 127
+            drop = np.clip(13 + np.maximum(0, -14 - e), 0, 23)  # fp16 subnormals keep fewer bits
+            keep = np.where(e < -24, 0, ~((np.uint32(1) << drop.astype(np.uint32)) - np.uint32(1)))
+            return (bits_ & keep.astype(np.uint32)).view(np.float32)
+
+        hi = rtz16(x32)
+        mid = rtz16(x32 - hi)
+        lo = rtz16((x32 - hi) - mid)
+        n = qmax + 1  # codes the width can hold; the other entries are zero
+        assert np.array_equal(lut[:, :n, 0], hi[:, :n]) and np.array_equal(lut[:, :n, 1], mid[:, :n])
+        assert np.array_equal(lut[:, :n, 2], lo[:, :n])
+        assert np.all(lut[:, n:, :] == 0) and np.all(lut[:, :, 3] == 0)
+        big = np.abs(x32[:, :n]) >= 2.0 ** 9
+        assert np.array_equal((hi + mid + lo)[:, :n][big], x32[:, :n][big])
 
 
 @pytest.mark.parametrize("n,kind,beta", [(128, 0, 0.0), (64, 6, 0.5), (128, 2, -1.0)])
