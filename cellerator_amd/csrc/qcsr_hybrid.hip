@@ -279,9 +279,8 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void qcsr_head_dense(HeadArgs h
 //
 // Workgroup: 4 waves of 64 rows. Per 32-gene chunk the W^T fragments (4 KB, in fragment order),
 // the chunk's table (4,352 B) and the workgroup's code bytes (8 KB) go through an LDS double
-// buffer: each lane loads up to five 16-byte pieces of chunk c + 2 from memory while chunk c
-// is computed and stores them into the free buffer at the start of chunk c + 1; one barrier
-// per chunk. Every memory load is thus consumed a whole chunk after it was issued.
+// buffer, loaded straight into LDS while the previous chunk is computed; one barrier per
+// chunk. No registers hold the share, so the kernel fits four waves per SIMD.
 
 constexpr int kLutWaves = 4;
 constexpr std::uint32_t kLutRows = kLutWaves * kRowsPerWave;  // 256 rows per workgroup
@@ -311,40 +310,38 @@ struct LutShared {
     uint4 codes[2][kCodeChunkBytes / 16];  // the workgroup's code bytes: [row][32]
 };
 
-// The share of chunk c is loaded in five 16-byte pieces per thread (256 threads), each kind
-// of piece in its own step so no step branches per lane: (0) the A fragments, column block
-// tid / 64, lane tid % 64 (row tid % 16 of the block, genes 8 (tid % 64 / 16) .. +7);
-// (1) table pieces 0..255; (2), (3) the workgroup's code bytes, pieces tid and 256 + tid;
-// (4) table pieces 256..271 (threads 0..15).
-constexpr int kSharePieces5 = 5;
-constexpr int kLutPieces = static_cast<int>(kLutChunkBytes / 16u);  // 272
-static_assert(kLutWaves * kWave == 256 && kCodeChunkBytes / 16u == 512u && kLutPieces == 272, "share pieces");
+using head_rsrc_t = __amdgpu_buffer_rsrc_t;
+using lds_void = __attribute__((address_space(3))) void *;
 
-template<int kK>
-__device__ __forceinline__ bool has_piece(int tid) {
-    return kK != 4 || tid < kLutPieces - 256;
+__device__ __forceinline__ head_rsrc_t head_rsrc(const void *base, std::uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), 0x00020000);
 }
 
-template<int kK>
-__device__ __forceinline__ uint4 load_piece(const LutArgs &h, std::uint32_t c, int tid, std::uint32_t wg_row) {
-    if constexpr (kK == 0) {
-        const std::uint32_t t = static_cast<std::uint32_t>(tid) / 64u, l = static_cast<std::uint32_t>(tid) % 64u;
-        return *static_cast<const uint4 *>(__builtin_assume_aligned(
-            h.panel + (static_cast<std::uint64_t>(c) * h.panel_n + t * 16u + l % 16u) * 32u + 8u * (l / 16u), 16));
-    } else if constexpr (kK == 1 || kK == 4) {
-        return h.lut[static_cast<std::uint64_t>(c) * kLutPieces + (kK == 4 ? 256 : 0) + tid];
-    } else {
-        return *reinterpret_cast<const uint4 *>(h.bytes + (static_cast<std::uint64_t>(c) * h.rows_ld + wg_row) * 32u
-                                                + static_cast<std::uint32_t>((kK == 3 ? 256 : 0) + tid) * 16u);
-    }
+// The share of chunk c goes straight from memory into LDS buffer `buf` (buffer loads with the
+// lds flag: each wave instruction fills 1 KB, no registers): the A fragments (wave w loads
+// column block w: lane l reads row w * 16 + l % 16 of the panel, genes 8 (l / 16) .. +7),
+// table pieces w * 64 + lane (pieces 256..271 by lanes 0..15 of wave 0), and the
+// workgroup's code bytes, pieces w * 64 + lane and 256 + w * 64 + lane.
+__device__ __forceinline__ void issue_share(LutShared &sh, const LutArgs &h, std::uint32_t c, int buf, int wave,
+                                            int lane, std::uint32_t wg_row) {
+    const head_rsrc_t pa = head_rsrc(h.panel + static_cast<std::uint64_t>(c) * h.panel_n * 32u, 64u * 64u);
+    const std::uint32_t pa_off = ((static_cast<std::uint32_t>(wave) * 16u + static_cast<std::uint32_t>(lane) % 16u) * 32u
+                                  + 8u * (static_cast<std::uint32_t>(lane) / 16u)) * 2u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(pa, (lds_void)&sh.a[buf][wave][0], 16, pa_off, 0, 0, 0);
+    const head_rsrc_t lu = head_rsrc(h.lut + static_cast<std::uint64_t>(c) * (kLutChunkBytes / 16u), kLutChunkBytes);
+    const std::uint32_t piece = static_cast<std::uint32_t>(wave * kWave + lane);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(lu, (lds_void)&sh.lut[buf][wave * kWave], 16, piece * 16u, 0, 0, 0);
+    const head_rsrc_t cb = head_rsrc(h.bytes + (static_cast<std::uint64_t>(c) * h.rows_ld + wg_row) * 32u, kCodeChunkBytes);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(cb, (lds_void)&sh.codes[buf][wave * kWave], 16, piece * 16u, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(cb, (lds_void)&sh.codes[buf][256 + wave * kWave], 16,
+                                             (256u + piece) * 16u, 0, 0, 0);
+    if (wave == 0 && lane < static_cast<int>(kLutChunkBytes / 16u) - 256)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(lu, (lds_void)&sh.lut[buf][256], 16, (256u + static_cast<std::uint32_t>(lane)) * 16u,
+                                                 0, 0, 0);
 }
 
-template<int kK>
-__device__ __forceinline__ void store_piece(LutShared &sh, int buf, int tid, uint4 v) {
-    if constexpr (kK == 0) sh.a[buf][tid / 64][tid % 64] = v;
-    else if constexpr (kK == 1 || kK == 4) sh.lut[buf][(kK == 4 ? 256 : 0) + tid] = v;
-    else sh.codes[buf][(kK == 3 ? 256 : 0) + tid] = v;
-}
+static_assert(kLutWaves * kWave == 256 && kCodeChunkBytes / 16u == 512u && kLutChunkBytes / 16u == 272u, "share pieces");
 
 // Byte k of v as a 32-bit offset.
 template<int kK>
@@ -352,7 +349,7 @@ __device__ __forceinline__ std::uint32_t byte_of(std::uint32_t v) {
     return kK == 3 ? v >> 24 : (v >> (8 * kK)) & 0xffu;
 }
 
-__global__ __launch_bounds__(kLutWaves * kWave) void qcsr_head_lut(LutArgs h) {
+__global__ __launch_bounds__(kLutWaves * kWave) __attribute__((amdgpu_waves_per_eu(4, 4))) void qcsr_head_lut(LutArgs h) {
     __shared__ LutShared sh;
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid % kWave;
@@ -367,33 +364,13 @@ __global__ __launch_bounds__(kLutWaves * kWave) void qcsr_head_lut(LutArgs h) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) acc[b][t] = cx_float4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    uint4 sv[kSharePieces5];
-#pragma unroll
-    for (int k = 0; k < kSharePieces5; ++k) sv[k] = make_uint4(0u, 0u, 0u, 0u);
-    auto load_share = [&](std::uint32_t c) {
-        sv[0] = load_piece<0>(h, c, tid, wg_row);
-        sv[1] = load_piece<1>(h, c, tid, wg_row);
-        sv[2] = load_piece<2>(h, c, tid, wg_row);
-        sv[3] = load_piece<3>(h, c, tid, wg_row);
-        if (has_piece<4>(tid)) sv[4] = load_piece<4>(h, c, tid, wg_row);
-    };
-    auto store_share = [&](int buf) {
-        store_piece<0>(sh, buf, tid, sv[0]);
-        store_piece<1>(sh, buf, tid, sv[1]);
-        store_piece<2>(sh, buf, tid, sv[2]);
-        store_piece<3>(sh, buf, tid, sv[3]);
-        if (has_piece<4>(tid)) store_piece<4>(sh, buf, tid, sv[4]);
-    };
-    if (h.chunks != 0u) {
-        load_share(0u);
-        store_share(0);
-    }
-    if (h.chunks > 1u) load_share(1u);
+    if (h.chunks != 0u) issue_share(sh, h, 0u, 0, wave, lane, wg_row);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's share loads are in LDS
     __syncthreads();
     for (std::uint32_t c = 0; c < h.chunks; ++c) {
         const int buf = static_cast<int>(c & 1u);
-        if (c + 1u < h.chunks) store_share(buf ^ 1);  // into the buffer chunk c - 1 used (all waves passed the barrier)
-        if (c + 2u < h.chunks) load_share(c + 2u);
+        // chunk c + 1 into the buffer chunk c - 1 used (every wave passed the barrier after it)
+        if (c + 1u < h.chunks) issue_share(sh, h, c + 1u, buf ^ 1, wave, lane, wg_row);
         cx_half8 aw[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) aw[t] = __builtin_bit_cast(cx_half8, sh.a[buf][t][lane]);
@@ -431,6 +408,7 @@ __global__ __launch_bounds__(kLutWaves * kWave) void qcsr_head_lut(LutArgs h) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[t], bl, acc[b][t], 0, 0, 0);
         }
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of chunk c + 1 are in LDS
         __syncthreads();  // buffer `buf` is free again; chunk c + 1 is in place
     }
 
