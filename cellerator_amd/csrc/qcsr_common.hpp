@@ -52,7 +52,10 @@ constexpr int kStreamSlots = kStreamWaves * kStreamLayers;        // (wave, laye
 constexpr int kStreamRows = kStreamSlots * 8;
 constexpr std::uint32_t kFillMask = 0x0fffffffu;
 constexpr int kStreamPartGenes = 1024;
-constexpr std::uint32_t kStreamPad = 1024u;                       // gene of a pad entry: the zero row
+constexpr std::uint32_t kStreamPad = 1024u;                       // gene of a pad entry: a zero row
+// Pads of odd parity (a second zero row): a pad takes the parity opposite to the entry of
+// the paired lane group at the same step, so the two reads stay in different LDS bank halves.
+constexpr std::uint32_t kStreamPadOdd = 1025u;
 
 // One 64-column block of the tail through the prepared stream (fp16 weights).
 int launch_qcsr_stream(const QcsrArgs &a, std::uint32_t bits, std::uint32_t policy, hipStream_t stream);

@@ -493,12 +493,12 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
 
 struct StreamShared {
     uint4 stage[kStreamWaves][8][9];  // per wave and lane group: 16 (gene * 8, value) pairs (+16 B pad)
-    float2 meta[kPartGenes + 2];      // (scale, offset) per gene of the part; [kPadGene] = (0, 0)
-    uint4 w[(kPartGenes + 1) * 8];    // fp16 weight rows of the part; row kPadGene is zeros
+    float2 meta[kPartGenes + 2];      // (scale, offset) per gene of the part; the two pads (0, 0)
+    uint4 w[(kPartGenes + 2) * 8];    // fp16 weight rows of the part; the two pad rows are zeros
 };
 
-static_assert(kPadGene == static_cast<int>(kStreamPad) && kPartGenes == kStreamPartGenes,
-              "the stream builder and the part walk must agree on parts and pads");
+static_assert(kPadGene == static_cast<int>(kStreamPad) && kPadGene + 1 == static_cast<int>(kStreamPadOdd)
+              && kPartGenes == kStreamPartGenes, "the stream builder and the part walk must agree on parts and pads");
 
 // Entries of one lane for one fill: group g's stage slots 2j, 2j + 1.
 template<bool kWide>
@@ -532,8 +532,8 @@ __global__ __launch_bounds__(kStreamWaves * kWave) void qcsr_spmm_stream(QcsrArg
     const int j = lane & 7;
     const std::uint32_t block = blockIdx.x;
 
-    if (tid < 8) sh.w[kPadGene * 8 + tid] = make_uint4(0u, 0u, 0u, 0u);
-    if (tid == 8) sh.meta[kPadGene] = make_float2(0.0f, 0.0f);
+    if (tid < 16) sh.w[kPadGene * 8 + tid] = make_uint4(0u, 0u, 0u, 0u);
+    if (tid == 16 || tid == 17) sh.meta[kPadGene + tid - 16] = make_float2(0.0f, 0.0f);
 
     const int parts = static_cast<int>(a.stream_parts);
     const std::uint32_t *ix = a.fill_index + static_cast<std::uint64_t>(block) * parts * kStreamSlots;
@@ -608,10 +608,10 @@ __global__ __launch_bounds__(kStreamWaves * kWave) void qcsr_spmm_stream(QcsrArg
                         g = e & 0x7ffu;
                         code = e >> 11;
                     }
-                    g = min(g, static_cast<std::uint32_t>(kPadGene));  // keeps a damaged stream inside LDS
+                    g = min(g, static_cast<std::uint32_t>(kPadGene + 1));  // keeps a damaged stream inside LDS
                     const float2 md = *reinterpret_cast<const float2 *>(mbase + g * 8u);
                     const float off = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET
-                        ? (g != static_cast<std::uint32_t>(kPadGene) ? roff[l] : 0.0f) : md.y;
+                        ? (g < static_cast<std::uint32_t>(kPadGene) ? roff[l] : 0.0f) : md.y;
                     st[2 * r] = g * 8u;
                     st[2 * r + 1] = __float_as_uint(__builtin_fmaf(static_cast<float>(code), md.x, off));
                 }

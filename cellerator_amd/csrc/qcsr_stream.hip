@@ -9,8 +9,9 @@
 // waves. For gene part p and layer (wave w, layer l) the 8 rows' runs in the part are
 // r_0 .. r_7; the layer gets ceil(max r_g / 16) fills of 128 entries, entry k of group g's
 // run at fill k / 16, slot g * 16 + k % 16; unused slots hold the pad gene (the zero
-// weight row, value 0). Each group's run is stored even genes first in even groups and odd
-// genes first in odd groups (the LDS bank half of a weight row is its gene's parity).
+// weight row, value 0; of the parity opposite to the paired group's entry at that step).
+// Each group's run is stored even genes first in even groups and odd genes first in odd
+// groups (the LDS bank half of a weight row is its gene's parity).
 //
 // Building: plan (slot rows and each layer's fill count and last step count), an exclusive
 // scan of the counts into the fill index, then the fill. The plan and the fill walk each
@@ -184,6 +185,30 @@ __global__ __launch_bounds__(kStreamRows) void stream_fill_kernel(FillArgs a) {
         }
         cur = stop;
     }
+}
+
+// Pads of a fill take the parity opposite to the paired group's entry at the same step
+// (groups 2i and 2i + 1 read in the same LDS cycle; a weight row of gene g occupies bank
+// half g & 1): one thread per (fill, group pair, step).
+template<bool kWide>
+__global__ __launch_bounds__(256) void stream_pad_parity_kernel(void *entries, std::uint64_t fills) {
+    const std::uint64_t i = static_cast<std::uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= fills * 64u) return;
+    const std::uint64_t fill = i / 64u;
+    const std::uint32_t pair = static_cast<std::uint32_t>(i % 64u) / 16u, step = static_cast<std::uint32_t>(i % 16u);
+    const std::uint64_t e0 = fill * 128u + (2u * pair) * 16u + step, e1 = e0 + 16u;
+    constexpr std::uint32_t kGeneMask = kWide ? 0xffffu : 0x7ffu;
+    auto get = [&](std::uint64_t e) -> std::uint32_t {
+        return kWide ? static_cast<std::uint32_t *>(entries)[e] : static_cast<std::uint16_t *>(entries)[e];
+    };
+    auto put = [&](std::uint64_t e, std::uint32_t v) {
+        if constexpr (kWide) static_cast<std::uint32_t *>(entries)[e] = v;
+        else static_cast<std::uint16_t *>(entries)[e] = static_cast<std::uint16_t>(v);
+    };
+    const std::uint32_t a = get(e0), b = get(e1);
+    const bool pa = (a & kGeneMask) >= kStreamPad, pb = (b & kGeneMask) >= kStreamPad;
+    if (pa && !pb) put(e0, (b & 1u) != 0u ? kStreamPad : kStreamPadOdd);
+    if (pb && !pa) put(e1, (a & 1u) != 0u ? kStreamPad : kStreamPadOdd);
 }
 
 constexpr std::uint64_t align256(std::uint64_t b) { return (b + 255u) & ~std::uint64_t{255u}; }
@@ -379,6 +404,14 @@ extern "C" int cx_qcsr_tail_fill(const cx_qcsr_matrix *m, const cx_qcsr_hybrid_l
     }
     rc = check_launch("cx_qcsr_tail_fill");
     if (rc != CX_STATUS_SUCCESS) return rc;
+    if (ts->fills != 0u) {
+        const std::uint64_t threads = ts->fills * 64u;
+        const dim3 pgrid(static_cast<unsigned>((threads + 255u) / 256u));
+        if (m->bits == 8u) hipLaunchKernelGGL(stream_pad_parity_kernel<true>, pgrid, dim3(256), 0, s, entries, ts->fills);
+        else hipLaunchKernelGGL(stream_pad_parity_kernel<false>, pgrid, dim3(256), 0, s, entries, ts->fills);
+        rc = check_launch("cx_qcsr_tail_fill");
+        if (rc != CX_STATUS_SUCCESS) return rc;
+    }
     ts->entries = entries;
     return CX_STATUS_SUCCESS;
 }

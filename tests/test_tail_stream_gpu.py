@@ -1,7 +1,8 @@
 """GPU parity of the prepared tail stream (qcsr_stream.hip) and the walk that reads it
 (qcsr_spmm_stream in qcsr_parts.hip): the slot rows, fill index and entries are bit-exact
 against a numpy restatement of the stream's definition (rank by tail length, snake-order
-layers, per-part fills of 16 steps x 8 groups, parity order within each run, pads), and the
+layers, per-part fills of 16 steps x 8 groups, parity order within each run, pads of the
+parity opposite to the paired group's entry), and the
 product through the stream -- every code width and decode policy, with and without a dense
 head, N = 64 and 128, fused epilogues, empty rows, rows longer than a part, ragged last
 block -- matches the float64 referee of the canonical matrix; repeats are bitwise equal.
@@ -81,6 +82,16 @@ def _stream_reference(h, head_end, head, bits, LAYERS):
         f0 = int(starts[(b * parts + p) * SLOTS + ls])
         for k, (gene, code) in enumerate(run):
             entries[f0 + k // 16, g * 16 + k % 16] = gene | (code << (16 if wide else 11))
+    # a pad beside a stored entry of the paired group (2i, 2i + 1) at the same step takes the
+    # opposite parity: gene 1024 (even) or 1025 (odd)
+    gene_mask = 0xFFFF if wide else 0x7FF
+    e = entries.reshape(total, 4, 2, 16).astype(np.int64)  # [fill, pair, group of pair, step]
+    pad = (e & gene_mask) >= 1024
+    for side in (0, 1):
+        other = e[:, :, 1 - side, :]
+        fix = pad[:, :, side, :] & ~pad[:, :, 1 - side, :]
+        e[:, :, side, :] = np.where(fix, np.where((other & 1) == 1, 1024, 1025), e[:, :, side, :])
+    entries = e.reshape(total, 128).astype(entries.dtype)
     return slot_rows, index.astype(np.uint32), entries
 
 
