@@ -195,6 +195,8 @@ constexpr int kGroupWaves = 4;
 constexpr int kPanelColStride = 80;
 constexpr int kRing = 3;
 
+using lds_void = __attribute__((address_space(3))) void *;
+
 template<int kN>
 __global__ __launch_bounds__(kWave *kGroupWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void bell_spmm_mfma_grouped(BellArgs a, const std::uint16_t *packed_rhs, std::uint32_t panel_bytes,
@@ -342,6 +344,221 @@ void bell_spmm_mfma_grouped(BellArgs a, const std::uint16_t *packed_rhs, std::ui
                     a.ep.active ? epilogue_value(a.ep, acc[t][i], r, col) : acc[t][i];
         }
     }
+}
+
+// Grouped MFMA path by column slab (N = 128, 256). Same groups, steps and sums as above, but
+// wave w computes output columns [w N/4, (w + 1) N/4) of every member. The members' A
+// fragments (2 KB each per step) are shared through an LDS ring, loaded straight into LDS
+// (buffer loads with the lds flag), and each wave's B fragments (its slab of the step's
+// panel slice) come from the packed panel into registers; both run three steps ahead. Per
+// group and step the LDS carries 8 KB of A, written once and read by every wave with
+// conflict-free 16-byte reads, instead of a 16 KB slice read four times. A member without a
+// step k skips its products. Per output element the products are accumulated in the same
+// slot order as the other MFMA kernels, so the results are bitwise equal.
+// s_waitcnt operand: vector memory count n (6 bits, split over two fields), lgkmcnt(0),
+// expcnt unchecked
+constexpr unsigned vmcnt_wait(int n) {
+    return 0x0070u | (static_cast<unsigned>(n) & 15u) | ((static_cast<unsigned>(n) >> 4) << 14);
+}
+
+// 16 bytes per lane from a buffer straight into LDS at dst + lane * 16 (dst wave-uniform)
+__device__ __forceinline__ void load_lds16(rsrc_t r, uint4 *dst, std::uint32_t voffset, std::uint32_t soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void)dst, 16, voffset, soffset, 0, 0);
+}
+
+template<int kN>
+__global__ __launch_bounds__(kWave *kGroupWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void bell_spmm_mfma_slab(BellArgs a, const std::uint16_t *packed_rhs, std::uint32_t panel_bytes,
+                         const std::uint32_t *order, const std::uint32_t *group_offsets,
+                         std::uint32_t group_count, std::uint32_t grouped_row_blocks) {
+    constexpr int kSlabTiles = kN / (32 * kGroupWaves);
+    static_assert(kSlabTiles >= 1, "a slab is at least one 32-column tile");
+    constexpr int kStepLoads = 2 * kSlabTiles + 2;  // vector loads one step issues: B, then A
+    // Loads run three steps ahead; at the end of step k only the loads of steps k + 2 and k + 3
+    // may still be in flight.
+    constexpr unsigned kStepWait = vmcnt_wait(2 * kStepLoads);
+    // The A ring: four separately declared slots ([member][K half][lane]), addressed with
+    // compile-time slot numbers, so that the compiler can tell a read of one slot from the
+    // LDS loads in flight into the others and adds no wait for those.
+    __shared__ uint4 a_lds0[kGroupWaves][2][kWave];
+    __shared__ uint4 a_lds1[kGroupWaves][2][kWave];
+    __shared__ uint4 a_lds2[kGroupWaves][2][kWave];
+    __shared__ uint4 a_lds3[kGroupWaves][2][kWave];
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const std::uint32_t wave = static_cast<std::uint32_t>(
+        __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave)));
+    const std::uint32_t wg = xcd_major(blockIdx.x, gridDim.x);
+    const bool single = wg >= group_count;
+    const std::uint32_t g0 = single ? grouped_row_blocks + (wg - group_count) : group_offsets[wg];
+    const std::uint32_t g1 = single ? g0 + 1u : group_offsets[wg + 1];
+    const std::uint32_t members = g1 - g0;
+    const std::uint32_t leader = order[g1 - 1u];
+    const std::uint32_t width = a.ell_cols / 32u;
+
+    // slot lists: the leader's (the B sequence) and the two members whose A this wave loads
+    // (member wave / 2 and 2 + wave / 2, K half wave % 2)
+    const std::uint32_t lead_sid = static_cast<std::uint32_t>(lane) < width
+        ? a.block_col_idx[static_cast<std::uint64_t>(leader) * width + lane] : kInvalidBlock;
+    unsigned long long lead_valid = __ballot(lead_sid != kInvalidBlock);
+    const std::uint32_t steps = static_cast<std::uint32_t>(__popcll(lead_valid));
+    std::uint32_t own_steps[kGroupWaves];
+    std::uint32_t rbs[kGroupWaves];
+#pragma unroll
+    for (int mm = 0; mm < kGroupWaves; ++mm) {
+        const std::uint32_t rb = static_cast<std::uint32_t>(mm) < members ? order[g0 + mm] : leader;
+        rbs[mm] = rb;
+        const std::uint32_t sid = static_cast<std::uint32_t>(lane) < width
+            ? a.block_col_idx[static_cast<std::uint64_t>(rb) * width + lane] : kInvalidBlock;
+        own_steps[mm] = static_cast<std::uint32_t>(mm) < members ? static_cast<std::uint32_t>(__popcll(__ballot(sid != kInvalidBlock))) : 0u;
+    }
+    // this wave's A loads: members la and lb, K half kh (all wave-uniform)
+    const std::uint32_t la = wave / 2u, lb = 2u + wave / 2u, kh = wave % 2u;
+    struct ALoads {
+        rsrc_t r;
+        unsigned long long valid;
+        std::uint32_t steps;
+    };
+    auto a_loads = [&](std::uint32_t mm) {
+        const std::uint32_t rb = static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(
+            static_cast<int>(mm < members ? order[g0 + mm] : leader)));
+        const std::uint32_t sid = static_cast<std::uint32_t>(lane) < width
+            ? a.block_col_idx[static_cast<std::uint64_t>(rb) * width + lane] : kInvalidBlock;
+        ALoads l;
+        l.valid = mm < members ? __ballot(sid != kInvalidBlock) : 0ull;
+        l.steps = static_cast<std::uint32_t>(__popcll(l.valid));
+        const std::uint32_t rows_here = min(32u, a.rows - rb * 32u);
+        l.r = make_rsrc(static_cast<const std::uint16_t *>(a.values) + static_cast<std::uint64_t>(rb) * 32u * a.ell_cols,
+                        rows_here * a.ell_cols * 2u);
+        return l;
+    };
+    ALoads ld_a = a_loads(la), ld_b = a_loads(lb);
+    const rsrc_t rbp = make_rsrc(packed_rhs, panel_bytes);
+    const int m = lane % 32;
+    const int kq = (lane / 32) * 8;
+    const std::uint32_t a_lane = (static_cast<std::uint32_t>(m) * a.ell_cols + static_cast<std::uint32_t>(kq)
+                                  + kh * 16u) * 2u;
+
+    cx_floatx16 acc[kGroupWaves][kSlabTiles];
+#pragma unroll
+    for (int mm = 0; mm < kGroupWaves; ++mm)
+#pragma unroll
+        for (int t = 0; t < kSlabTiles; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[mm][t][i] = 0.0f;
+
+    std::uint32_t last_bc = 0u;
+    auto next_lead = [&]() {
+        if (lead_valid != 0ull) {
+            const std::uint32_t sl = static_cast<std::uint32_t>(__builtin_ctzll(lead_valid));
+            lead_valid &= lead_valid - 1ull;
+            last_bc = static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lead_sid), static_cast<int>(sl)));
+        }
+        return last_bc;
+    };
+    struct BFrags { cx_bf16x8 f[kSlabTiles][2]; };
+    auto load_b = [&](BFrags &b, std::uint32_t bc) {
+#pragma unroll
+        for (int t = 0; t < kSlabTiles; ++t)
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc)
+                b.f[t][kc] = load_frag(rbp, ((static_cast<std::uint32_t>(wave) * kSlabTiles + t) * 32u + m) * 64u
+                                            + static_cast<std::uint32_t>(kq + kc * 16) * 2u,
+                                       bc * static_cast<std::uint32_t>(kN) * 64u);
+    };
+    using Slot = uint4[kGroupWaves][2][kWave];
+    // A of the next step for members la, lb (K half kh) into a ring slot. Both loads are
+    // always issued (a member without that step reloads its first slot into a part of the
+    // ring nobody reads), so every step has the same count of loads in flight and the waits
+    // below are exact.
+    auto issue_one = [&](ALoads &l, std::uint32_t mm, Slot &slot) {
+        const std::uint32_t sl = l.valid != 0ull ? static_cast<std::uint32_t>(__builtin_ctzll(l.valid)) : 0u;
+        l.valid &= l.valid - 1ull;
+        load_lds16(l.r, &slot[mm][kh][0], a_lane, sl * 64u);
+    };
+    auto issue_a = [&](Slot &slot) {
+        issue_one(ld_a, la, slot);
+        issue_one(ld_b, lb, slot);
+    };
+    // Barrier without a memory fence (a fence would wait for every LDS load in flight): the
+    // waits before it are explicit, and the asm's memory clobber keeps LDS accesses on their
+    // side of it.
+    auto barrier = []() { asm volatile("s_barrier" ::: "memory"); };
+
+    if (steps != 0u) {
+        BFrags b0, b1, b2, b3;
+        load_b(b0, next_lead());
+        issue_a(a_lds0);
+        load_b(b1, next_lead());
+        issue_a(a_lds1);
+        load_b(b2, next_lead());
+        issue_a(a_lds2);
+        __builtin_amdgcn_s_waitcnt(kStepWait);  // step 0's loads are in
+        barrier();
+        std::uint32_t k = 0;
+        // step k reads set and slot k % 4 and loads B(k + 3), A(k + 3) into set and slot
+        // (k + 3) % 4, the ones step k - 1 read (every wave has passed the barrier after it)
+        auto step = [&](BFrags &b_cur, BFrags &b_new, Slot &slot, Slot &fill_slot) {
+            __builtin_amdgcn_sched_barrier(0);
+            load_b(b_new, next_lead());  // B(k + 3)
+            __builtin_amdgcn_sched_barrier(0);
+            issue_a(fill_slot);  // A(k + 3)
+            __builtin_amdgcn_sched_barrier(0);
+            // all members' A fragments first (one LDS round trip), then their products
+            cx_bf16x8 af[kGroupWaves][2];
+#pragma unroll
+            for (int mm = 0; mm < kGroupWaves; ++mm)
+#pragma unroll
+                for (int kc = 0; kc < 2; ++kc) af[mm][kc] = __builtin_bit_cast(cx_bf16x8, slot[mm][kc][lane]);
+#pragma unroll
+            for (int mm = 0; mm < kGroupWaves; ++mm) {
+                if (k < own_steps[mm]) {
+#pragma unroll
+                    for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+                        for (int t = 0; t < kSlabTiles; ++t)
+                            acc[mm][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mm][kc], b_cur.f[t][kc], acc[mm][t], 0, 0, 0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // B(k + 1) and A(k + 1) (issued at step k - 2) must be in for the next step, and this
+            // step's LDS reads done before the slot is refilled
+            __builtin_amdgcn_s_waitcnt(kStepWait);
+            barrier();
+            ++k;
+        };
+        for (;;) {
+            step(b0, b3, a_lds0, a_lds3);
+            if (k >= steps) break;
+            step(b1, b0, a_lds1, a_lds0);
+            if (k >= steps) break;
+            step(b2, b1, a_lds2, a_lds1);
+            if (k >= steps) break;
+            step(b3, b2, a_lds3, a_lds2);
+            if (k >= steps) break;
+        }
+        // the last steps' A loads are still landing in LDS: nothing may leave before them
+        __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+    }
+
+    // one call per member (a loop over members with the accumulators indexed by it is not
+    // unrolled at this size, which would put them in scratch)
+    auto store_member = [&](const cx_floatx16 (&acc_m)[kSlabTiles], std::uint32_t rb) {
+#pragma unroll
+        for (int t = 0; t < kSlabTiles; ++t) {
+            const int col = (static_cast<int>(wave) * kSlabTiles + t) * 32 + m;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const std::uint32_t r = rb * 32u + 8u * (i / 4) + 4u * (lane / 32) + (i % 4);
+                if (r < a.rows)
+                    a.out[static_cast<std::int64_t>(r) * a.out_ld + col] =
+                        a.ep.active ? epilogue_value(a.ep, acc_m[t][i], r, col) : acc_m[t][i];
+            }
+        }
+    };
+    store_member(acc[0], rbs[0]);
+    if (members > 1u) store_member(acc[1], rbs[1]);
+    if (members > 2u) store_member(acc[2], rbs[2]);
+    if (members > 3u) store_member(acc[3], rbs[3]);
 }
 
 __global__ void pack_rhs_kernel(const std::uint16_t *rhs, std::int64_t rhs_ld, std::uint32_t k,
@@ -606,8 +823,8 @@ extern "C" int cx_bell_spmm_fwd_grouped_epilogue(const cx_bell_matrix *m,
     const std::uint32_t gc = groups->group_count, grb = groups->grouped_row_blocks;
     switch (out_cols) {
     case 64: hipLaunchKernelGGL(bell_spmm_mfma_grouped<64>, ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb); break;
-    case 128: hipLaunchKernelGGL(bell_spmm_mfma_grouped<128>, ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb); break;
-    default: hipLaunchKernelGGL(bell_spmm_mfma_grouped<256>, ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb); break;
+    case 128: hipLaunchKernelGGL(bell_spmm_mfma_slab<128>, ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb); break;
+    default: hipLaunchKernelGGL(bell_spmm_mfma_slab<256>, ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb); break;
     }
     rc = check_launch("bell_spmm_mfma_grouped");
     return rc;
