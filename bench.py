@@ -341,7 +341,7 @@ def bench_bell(args, torch, cfg) -> dict:
                        "single_row_blocks": groups.single_count}},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(cfg.name),
-                     "kernel": "bell_spmm_mfma<256>" if groups is None else "bell_spmm_mfma_grouped<256> (+ singles)",
+                     "kernel": "bell_spmm_mfma<256>" if groups is None else "bell_spmm_mfma_slab<256> (grouped, + singles)",
                      "kernel_ms_mean": kern_ms,
                      "kernel_ms_median": statistics.median(ev), "algorithmic_bytes": alg_bytes,
                      "mfma_tflops": flops / (kern_ms * 1e-3) / 1e12,

@@ -569,9 +569,11 @@ int cx_bell_plan_groups(const uint32_t *block_col_idx, uint32_t row_blocks, uint
 const char *cx_bell_plan_last_error(void);
 
 /* Same result contract as cx_bell_spmm_fwd_packed: per group, each N x 32 panel slice is
- * loaded once (into LDS) for all members; per output element the MFMA accumulation runs in
- * the same slot order as the ungrouped kernel. One launch: single row blocks run as
- * one-member groups. At most 64 slots per row block. */
+ * loaded once for all members (staged in LDS at N = 64; at N = 128 and 256 each wave loads
+ * its column slab and the members' value blocks are shared through LDS); per output element
+ * the MFMA accumulation runs in the same slot order as the ungrouped kernel, so the results
+ * are bitwise equal. One launch: single row blocks run as one-member groups. At most 64
+ * slots per row block. */
 int cx_bell_spmm_fwd_grouped(const cx_bell_matrix *a, const uint16_t *packed_rhs,
                              const cx_bell_groups *groups, int64_t out_cols, float *out,
                              int64_t out_ld, void *stream);
