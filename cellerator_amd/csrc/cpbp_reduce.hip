@@ -315,10 +315,15 @@ __global__ __launch_bounds__(kWave *kCpbpWaves) void cpbp_reduce_kernel(CpbpArgs
                         const bool h3 = m != 0u;
                         const std::uint32_t b3 = h3 ? static_cast<std::uint32_t>(__builtin_ctz(m)) : 0u;
                         m &= m - 1u;
-                        sum = __builtin_fmaf(v[0], w[b0], sum);
-                        sum = __builtin_fmaf(h1 ? v[1] : 0.0f, h1 ? w[b1] : 0.0f, sum);
-                        sum = __builtin_fmaf(h2 ? v[2] : 0.0f, h2 ? w[b2] : 0.0f, sum);
-                        sum = __builtin_fmaf(h3 ? v[3] : 0.0f, h3 ? w[b3] : 0.0f, sum);
+                        // loads first, selects after: every read is in bounds (the stage has
+                        // a 4-value tail, an absent bit reads the block's first weight), so
+                        // no read needs its own exec mask
+                        const float v0 = v[0], v1 = v[1], v2 = v[2], v3 = v[3];
+                        const float w0 = w[b0], w1 = w[b1], w2 = w[b2], w3 = w[b3];
+                        sum = __builtin_fmaf(v0, w0, sum);
+                        sum = __builtin_fmaf(h1 ? v1 : 0.0f, h1 ? w1 : 0.0f, sum);
+                        sum = __builtin_fmaf(h2 ? v2 : 0.0f, h2 ? w2 : 0.0f, sum);
+                        sum = __builtin_fmaf(h3 ? v3 : 0.0f, h3 ? w3 : 0.0f, sum);
                         v += 4;
                     }
                 } else {
