@@ -298,7 +298,8 @@ def bench_bell(args, torch, cfg) -> dict:
     """Config 4: Blocked-ELL bf16 SpMM on MFMA (cx_bell_spmm_fwd_packed), N = 256."""
     import numpy as np
 
-    from cellerator_amd import bell_pack_rhs, bell_plan_groups, bell_spmm_grouped, bell_spmm_packed
+    from cellerator_amd import (bell_block_major, bell_pack_rhs, bell_plan_groups, bell_spmm_grouped,
+                                bell_spmm_packed)
     from cellerator_amd.synth import dense_normal, generate_bell
 
     t0 = time.perf_counter()
@@ -315,14 +316,27 @@ def bench_bell(args, torch, cfg) -> dict:
         + ("" if groups is None else f"; {groups.group_count} groups cover {groups.grouped_row_blocks} "
                                      f"row blocks, {groups.single_count} single"))
     stream = torch.cuda.current_stream()
+    # Headline: the values in block-major order (every 32x32 block's 2 KB contiguous, the
+    # layout the CSR -> Blocked-ELL lowering emits), copied once like the packed panel; the
+    # generator's row-major values are timed beside it.
+    mb = None if args.row_major else bell_block_major(m)
+    torch.cuda.synchronize()
 
-    def launch():
-        if groups is None:
-            bell_spmm_packed(m, packed, n_out, out=out, stream=stream)
-        else:
-            bell_spmm_grouped(m, packed, groups, n_out, out=out, stream=stream)
+    def launch_with(mat):
+        def launch():
+            if groups is None:
+                bell_spmm_packed(mat, packed, n_out, out=out, stream=stream)
+            else:
+                bell_spmm_grouped(mat, packed, groups, n_out, out=out, stream=stream)
+        return launch
 
-    wall_ms, ev = time_launches(torch, launch, args.steps, args.warmup, stream)
+    row_major = None
+    if mb is not None:
+        rm_wall, rm_ev = time_launches(torch, launch_with(m), args.steps, args.warmup, stream)
+        row_major = {"ms_per_step": rm_wall, "kernel_ms_mean": statistics.mean(rm_ev),
+                     "kernel_ms_median": statistics.median(rm_ev)}
+    wall_ms, ev = time_launches(torch, launch_with(mb if mb is not None else m), args.steps, args.warmup,
+                                stream)
     kern_ms = statistics.mean(ev)
     bs = m.block_size
     alg_bytes = (valid_blocks * bs * bs * 2 + m.block_col_idx.numel() * 4 + m.cols * n_out * 2
@@ -336,6 +350,7 @@ def bench_bell(args, torch, cfg) -> dict:
         "config": {"workload": cfg.name, "rows": m.rows, "genes": m.cols, "block_size": bs,
                    "valid_blocks": valid_blocks, "ell_width": cfg.ell_width, "n_out": n_out,
                    "seed": hex(cfg.seed),
+                   "value_layout": "row-major" if mb is None else "block-major (copied once, untimed)",
                    "row_block_groups": None if groups is None else {
                        "groups": groups.group_count, "grouped_row_blocks": groups.grouped_row_blocks,
                        "single_row_blocks": groups.single_count}},
@@ -347,6 +362,8 @@ def bench_bell(args, torch, cfg) -> dict:
                      "mfma_tflops": flops / (kern_ms * 1e-3) / 1e12,
                      "mfma_frac_of_bf16_dense_peak": flops / (kern_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS},
     }
+    if row_major is not None:
+        res["row_major_path"] = row_major
     if not args.no_cpu:
         from oracle import pyoracle
         pyoracle.build()
@@ -523,6 +540,8 @@ def main() -> int:
     ap.add_argument("--cpu-rows", type=int, default=0,
                     help="rows of the CPU-baseline sample (0: the whole matrix)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--row-major", action="store_true",
+                    help="c4: time the generator's row-major values only (no block-major copy)")
     ap.add_argument("--ungrouped", action="store_true",
                     help="C4: time the per-row-block MFMA kernel without the row-block grouping")
     ap.add_argument("--unchecked-columns", action="store_true",

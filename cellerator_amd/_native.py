@@ -43,7 +43,11 @@ class CxBellMatrix(C.Structure):
         ("block_col_idx", p_void), ("values", p_void), ("value_dtype", u32), ("bits", u32),
         ("decode_policy", u32), ("row_stride_bytes", u32), ("packed_values", p_void),
         ("column_scales", p_void), ("column_offsets", p_void), ("row_offsets", p_void),
+        ("value_layout_flags", u32), ("reserved", u32),
     ]
+
+
+BELL_BLOCK_MAJOR_VALUES = 1
 
 
 class CxSpmmEpilogue(C.Structure):
@@ -277,6 +281,7 @@ ENGINE_SIGNATURES = {
     "cx_bell_spmm_fwd_epilogue": (C.c_int, [C.POINTER(CxBellMatrix), p_void, u32, i64, i64, p_void,
                                             i64, C.POINTER(CxSpmmEpilogue), p_void]),
     "cx_bell_pack_rhs": (C.c_int, [p_void, i64, u32, u32, p_void, p_void]),
+    "cx_bell_block_major_values": (C.c_int, [C.POINTER(CxBellMatrix), p_void, u64, p_void]),
     "cx_bell_spmm_fwd_packed": (C.c_int, [C.POINTER(CxBellMatrix), p_void, i64, p_void, i64, p_void]),
     "cx_bell_spmm_fwd_packed_epilogue": (C.c_int, [C.POINTER(CxBellMatrix), p_void, i64, p_void, i64,
                                                    C.POINTER(CxSpmmEpilogue), p_void]),

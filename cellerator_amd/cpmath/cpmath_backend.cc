@@ -335,6 +335,8 @@ core::operation_status run_blocked_ell(const core::prepared_operation &p,
     if (a.values != nullptr || a.packed_values != nullptr || a.column_scales != nullptr
         || a.column_offsets != nullptr || a.row_offsets != nullptr)
         return bad_launch("Blocked-ELL values travel in the value plane");
+    if (a.value_layout_flags != 0u || a.reserved != 0u)
+        return bad_launch("the projection-order value plane is row-major [rows x ell_cols]");
     const execution::value_plane *plane = value_plane_of(*s, p, l);
     if (plane == nullptr || plane->layout != execution::value_layout_kind::projection_local_order
         || plane->quantization.kind != execution::quantization_kind::none

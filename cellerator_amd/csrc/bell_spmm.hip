@@ -2,10 +2,12 @@
 //
 // MFMA path (bf16 values, bf16 weights, 32x32 blocks, N a multiple of 64):
 //   * the weight panel is packed once per weight generation (cx_bell_pack_rhs) from
-//     row-major K x N into [K/32][N][32]: for every 32-gene block column and output
-//     column the 32 gene weights are contiguous, which is the K-contiguous operand form
-//     the matrix cores read (the role of the reference's packed dense operand,
+//     row-major K x N into fragment order: per 32-gene block column, 32-column tile and
+//     K half, the 64 lanes' 16-byte B operands one after another, so a wave reads each
+//     1 KB piece contiguously (the role of the reference's packed dense operand,
 //     src/compute/math/packed_dense_operand.cu:131-260);
+//   * values are row-major [rows][ell_cols] or block-major (CX_BELL_BLOCK_MAJOR_VALUES:
+//     every 32x32 block's 2 KB contiguous); the kernels take the row and slot pitches;
 //   * one workgroup owns one 32-row block; wave w owns output columns [64w, 64w+64)
 //     as two 32x32 fp32 accumulator tiles;
 //   * per valid ELL slot each lane loads its 16-byte A fragment (8 bf16 of one row of
@@ -44,8 +46,22 @@ struct BellArgs {
     std::uint32_t block_size;
     std::uint32_t ell_cols;
     std::uint32_t row_stride_bytes;
+    // unquantized values: bytes between two rows of one row block's values, bytes between
+    // two slots of one row, and the layout (row-major: ell_cols * size and block_size * size;
+    // block-major: block_size * size and block_size^2 * size)
+    std::uint32_t a_row_bytes;
+    std::uint32_t a_slot_bytes;
+    std::uint32_t block_major;
     Epilogue ep;
 };
+
+// Byte offset of panel fragment (tile t, K half h) of block column bc for lane `lane`, in a
+// panel of n output columns (cx_bell_pack_rhs's fragment order).
+__device__ __forceinline__ std::uint32_t panel_frag(std::uint32_t n, std::uint32_t tile, std::uint32_t half,
+                                                    int lane) {
+    (void)n;
+    return ((tile * 2u + half) * 64u + static_cast<std::uint32_t>(lane)) * 16u;
+}
 
 // Row block handled by workgroup `wg` of `count`: XCD-major so that the row blocks a
 // single XCD processes are contiguous in the matrix (dispatch places wg on XCD wg % 8).
@@ -62,6 +78,12 @@ using rsrc_t = __amdgpu_buffer_rsrc_t;
 __device__ __forceinline__ rsrc_t make_rsrc(const void *base, std::uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
                                              static_cast<int>(bytes), 0x00020000);
+}
+
+// Bytes of row block rb's bf16 values (both layouts start it at rb * 32 * ell_cols
+// elements): row-major, the rows the matrix has; block-major, whole blocks.
+__device__ __forceinline__ std::uint32_t a_block_row_bytes(const BellArgs &a, std::uint32_t rb) {
+    return a.block_major != 0u ? a.ell_cols * 64u : min(32u, a.rows - rb * 32u) * a.ell_cols * 2u;
 }
 
 // 16 bytes at voffset (per lane) + soffset (wave-uniform, kept in an SGPR so the per-step
@@ -100,25 +122,23 @@ __global__ __launch_bounds__(kN) void bell_spmm_mfma(BellArgs a, const std::uint
     const int kq = (lane / 32) * 8;  // first K element of this lane's fragment
     const int n0 = wave * 64;
     // A: this row block's value rows (rows past the matrix read as 0 from the buffer)
-    const std::uint32_t rows_here = min(32u, a.rows - rb * 32u);
     const rsrc_t ra = make_rsrc(static_cast<const std::uint16_t *>(a.values)
                                     + static_cast<std::uint64_t>(rb) * 32u * a.ell_cols,
-                                rows_here * a.ell_cols * 2u);
+                                a_block_row_bytes(a, rb));
     const rsrc_t rbp = make_rsrc(packed_rhs, panel_bytes);
-    const std::uint32_t a_lane = (static_cast<std::uint32_t>(m) * a.ell_cols + static_cast<std::uint32_t>(kq)) * 2u;
-    const std::uint32_t b_lane = (static_cast<std::uint32_t>(n0 + m) * 32u + static_cast<std::uint32_t>(kq)) * 2u;
+    const std::uint32_t a_lane = static_cast<std::uint32_t>(m) * a.a_row_bytes + static_cast<std::uint32_t>(kq) * 2u;
 
     auto load_slot = [&](SlotFrags &f, std::uint32_t s, std::uint32_t bc) {
-        const std::uint32_t ao = a_lane + s * 64u;
+        const std::uint32_t ao = a_lane + s * a.a_slot_bytes;
 #pragma unroll
         for (int kc = 0; kc < 2; ++kc) f.a[kc] = load_frag(ra, ao + static_cast<std::uint32_t>(kc) * 32u);
-        const std::uint32_t bo = bc * static_cast<std::uint32_t>(kN) * 64u + b_lane;
+        const std::uint32_t bo = bc * static_cast<std::uint32_t>(kN) * 64u;
 #pragma unroll
         for (int t = 0; t < kTilesPerWave; ++t)
 #pragma unroll
             for (int kc = 0; kc < 2; ++kc)
-                f.b[t][kc] = load_frag(rbp, bo + static_cast<std::uint32_t>(t) * 32u * 64u
-                                                + static_cast<std::uint32_t>(kc) * 32u);
+                f.b[t][kc] = load_frag(rbp, bo + panel_frag(kN, static_cast<std::uint32_t>(wave * kTilesPerWave + t),
+                                                            static_cast<std::uint32_t>(kc), lane));
     };
 
     cx_floatx16 acc[kTilesPerWave];
@@ -234,12 +254,11 @@ void bell_spmm_mfma_grouped(BellArgs a, const std::uint16_t *packed_rhs, std::ui
 
     const int m = lane % 32;
     const int kq = (lane / 32) * 8;
-    const std::uint32_t rows_here = min(32u, a.rows - rb * 32u);
     const rsrc_t ra = make_rsrc(static_cast<const std::uint16_t *>(a.values)
                                     + static_cast<std::uint64_t>(rb) * 32u * a.ell_cols,
-                                rows_here * a.ell_cols * 2u);
+                                a_block_row_bytes(a, rb));
     const rsrc_t rbp = make_rsrc(packed_rhs, panel_bytes);
-    const std::uint32_t a_lane = (static_cast<std::uint32_t>(m) * a.ell_cols + static_cast<std::uint32_t>(kq)) * 2u;
+    const std::uint32_t a_lane = static_cast<std::uint32_t>(m) * a.a_row_bytes + static_cast<std::uint32_t>(kq) * 2u;
 
     cx_floatx16 acc[kTiles];
 #pragma unroll
@@ -273,18 +292,22 @@ void bell_spmm_mfma_grouped(BellArgs a, const std::uint16_t *packed_rhs, std::ui
             __builtin_memcpy(&b.c[i], &v, 16);
         }
     };
+    // chunk c of the slice is fragment (tile c / 128, K half (c / 64) % 2) of lane c % 64:
+    // column 32 tile + (c % 32), genes 16 half + 8 ((c % 64) / 32) .. + 7
     auto store_b = [&](const BRegs &b, std::uint32_t slot) {
 #pragma unroll
         for (int i = 0; i < kLoadIters; ++i) {
             const std::uint32_t c = threadIdx.x + static_cast<std::uint32_t>(i) * kThreads;
+            const std::uint32_t col = (c / 128u) * 32u + c % 32u;
+            const std::uint32_t kchunk = ((c / 64u) % 2u) * 2u + (c % 64u) / 32u;
             if (c < static_cast<std::uint32_t>(kChunks))
-                *reinterpret_cast<uint4 *>(&bslice[slot][(c / 4u) * kPanelColStride + (c % 4u) * 16u]) = b.c[i];
+                *reinterpret_cast<uint4 *>(&bslice[slot][col * kPanelColStride + kchunk * 16u]) = b.c[i];
         }
     };
     auto load_a = [&](cx_bf16x8 (&af)[2], std::uint32_t s) {
 #pragma unroll
         for (int kc = 0; kc < 2; ++kc)
-            af[kc] = load_frag(ra, a_lane + static_cast<std::uint32_t>(kc) * 32u, s * 64u);
+            af[kc] = load_frag(ra, a_lane + static_cast<std::uint32_t>(kc) * 32u, s * a.a_slot_bytes);
     };
     auto mfma_step = [&](const cx_bf16x8 (&af)[2], std::uint32_t slot) {
 #pragma unroll
@@ -366,7 +389,7 @@ __device__ __forceinline__ void load_lds16(rsrc_t r, uint4 *dst, std::uint32_t v
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void)dst, 16, voffset, soffset, 0, 0);
 }
 
-template<int kN>
+template<int kN, bool kBlockMajor>
 __global__ __launch_bounds__(kWave *kGroupWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void bell_spmm_mfma_slab(BellArgs a, const std::uint16_t *packed_rhs, std::uint32_t panel_bytes,
                          const std::uint32_t *order, const std::uint32_t *group_offsets,
@@ -426,17 +449,31 @@ void bell_spmm_mfma_slab(BellArgs a, const std::uint16_t *packed_rhs, std::uint3
         ALoads l;
         l.valid = mm < members ? __ballot(sid != kInvalidBlock) : 0ull;
         l.steps = static_cast<std::uint32_t>(__popcll(l.valid));
-        const std::uint32_t rows_here = min(32u, a.rows - rb * 32u);
         l.r = make_rsrc(static_cast<const std::uint16_t *>(a.values) + static_cast<std::uint64_t>(rb) * 32u * a.ell_cols,
-                        rows_here * a.ell_cols * 2u);
+                        a_block_row_bytes(a, rb));
         return l;
     };
     ALoads ld_a = a_loads(la), ld_b = a_loads(lb);
     const rsrc_t rbp = make_rsrc(packed_rhs, panel_bytes);
     const int m = lane % 32;
     const int kq = (lane / 32) * 8;
-    const std::uint32_t a_lane = (static_cast<std::uint32_t>(m) * a.ell_cols + static_cast<std::uint32_t>(kq)
-                                  + kh * 16u) * 2u;
+    // Row-major values: wave w loads K half kh (16 columns) of all 32 rows, lane by lane in
+    // fragment order. Block-major values: wave w loads rows [16 kh, 16 kh + 16) whole, a
+    // contiguous 1 KB, and lane l puts row 16 kh + l / 4's 16-byte chunk
+    // (l % 4) ^ ((row / 4) % 4) at position l: each row's four chunks rotate by its quad, so
+    // the fragment reads below (16 rows, one chunk) meet every bank once.
+    std::uint32_t a_lane, a_read[2] = {0u, 0u};
+    if constexpr (kBlockMajor) {
+        const std::uint32_t r = kh * 16u + static_cast<std::uint32_t>(lane) / 4u;
+        a_lane = r * 64u + ((static_cast<std::uint32_t>(lane) % 4u) ^ ((r / 4u) % 4u)) * 16u;
+        const std::uint32_t mm_ = static_cast<std::uint32_t>(m), h = static_cast<std::uint32_t>(lane) / 32u;
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc)
+            a_read[kc] = mm_ * 4u + ((static_cast<std::uint32_t>(kc) * 2u + h) ^ ((mm_ / 4u) % 4u));
+    } else {
+        a_lane = (static_cast<std::uint32_t>(m) * a.ell_cols + static_cast<std::uint32_t>(kq) + kh * 16u) * 2u;
+    }
+    constexpr std::uint32_t kSlotBytes = kBlockMajor ? 2048u : 64u;
 
     cx_floatx16 acc[kGroupWaves][kSlabTiles];
 #pragma unroll
@@ -461,8 +498,8 @@ void bell_spmm_mfma_slab(BellArgs a, const std::uint16_t *packed_rhs, std::uint3
         for (int t = 0; t < kSlabTiles; ++t)
 #pragma unroll
             for (int kc = 0; kc < 2; ++kc)
-                b.f[t][kc] = load_frag(rbp, ((static_cast<std::uint32_t>(wave) * kSlabTiles + t) * 32u + m) * 64u
-                                            + static_cast<std::uint32_t>(kq + kc * 16) * 2u,
+                b.f[t][kc] = load_frag(rbp, panel_frag(kN, wave * kSlabTiles + static_cast<std::uint32_t>(t),
+                                                       static_cast<std::uint32_t>(kc), lane),
                                        bc * static_cast<std::uint32_t>(kN) * 64u);
     };
     using Slot = uint4[kGroupWaves][2][kWave];
@@ -473,7 +510,7 @@ void bell_spmm_mfma_slab(BellArgs a, const std::uint16_t *packed_rhs, std::uint3
     auto issue_one = [&](ALoads &l, std::uint32_t mm, Slot &slot) {
         const std::uint32_t sl = l.valid != 0ull ? static_cast<std::uint32_t>(__builtin_ctzll(l.valid)) : 0u;
         l.valid &= l.valid - 1ull;
-        load_lds16(l.r, &slot[mm][kh][0], a_lane, sl * 64u);
+        load_lds16(l.r, &slot[mm][kh][0], a_lane, sl * kSlotBytes);
     };
     auto issue_a = [&](Slot &slot) {
         issue_one(ld_a, la, slot);
@@ -508,7 +545,12 @@ void bell_spmm_mfma_slab(BellArgs a, const std::uint16_t *packed_rhs, std::uint3
 #pragma unroll
             for (int mm = 0; mm < kGroupWaves; ++mm)
 #pragma unroll
-                for (int kc = 0; kc < 2; ++kc) af[mm][kc] = __builtin_bit_cast(cx_bf16x8, slot[mm][kc][lane]);
+                for (int kc = 0; kc < 2; ++kc) {
+                    if constexpr (kBlockMajor)
+                        af[mm][kc] = __builtin_bit_cast(cx_bf16x8, (&slot[mm][0][0])[a_read[kc]]);
+                    else
+                        af[mm][kc] = __builtin_bit_cast(cx_bf16x8, slot[mm][kc][lane]);
+                }
 #pragma unroll
             for (int mm = 0; mm < kGroupWaves; ++mm) {
                 if (k < own_steps[mm]) {
@@ -561,9 +603,10 @@ void bell_spmm_mfma_slab(BellArgs a, const std::uint16_t *packed_rhs, std::uint3
     if (members > 3u) store_member(acc[3], rbs[3]);
 }
 
+// Column-contiguous panel [ceil(k/32)][n][32] (the dense head of the quantized CSR path
+// reads this form): one thread per packed element (kb, col, kk).
 __global__ void pack_rhs_kernel(const std::uint16_t *rhs, std::int64_t rhs_ld, std::uint32_t k,
                                 std::uint32_t n, std::uint16_t *packed) {
-    // one thread per packed element: (kb, col, kk)
     const std::uint64_t idx = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x;
     const std::uint32_t kblocks = (k + 31u) / 32u;
     const std::uint64_t total = static_cast<std::uint64_t>(kblocks) * n * 32u;
@@ -573,6 +616,39 @@ __global__ void pack_rhs_kernel(const std::uint16_t *rhs, std::int64_t rhs_ld, s
     const std::uint32_t kb = static_cast<std::uint32_t>(idx / (32ull * n));
     const std::uint32_t gene = kb * 32u + kk;
     packed[idx] = gene < k ? rhs[static_cast<std::int64_t>(gene) * rhs_ld + col] : 0;
+}
+
+// Fragment-order panel (cx_bell_pack_rhs): element idx of block column kb is
+// ((tile * 2 + half) * 64 + lane) * 8 + i, holding column 32 tile + lane % 32 and gene
+// 32 kb + 16 half + 8 (lane / 32) + i. One thread per element.
+__global__ void pack_rhs_frag_kernel(const std::uint16_t *rhs, std::int64_t rhs_ld, std::uint32_t k,
+                                     std::uint32_t n, std::uint16_t *packed) {
+    const std::uint64_t idx = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x;
+    const std::uint32_t kblocks = (k + 31u) / 32u;
+    const std::uint64_t total = static_cast<std::uint64_t>(kblocks) * n * 32u;
+    if (idx >= total) return;
+    const std::uint32_t kb = static_cast<std::uint32_t>(idx / (32ull * n));
+    const std::uint32_t e = static_cast<std::uint32_t>(idx % (32ull * n));
+    const std::uint32_t i = e % 8u, lane = (e / 8u) % 64u, half = (e / 512u) % 2u, tile = e / 1024u;
+    const std::uint32_t col = tile * 32u + lane % 32u;
+    const std::uint32_t gene = kb * 32u + half * 16u + (lane / 32u) * 8u + i;
+    packed[idx] = gene < k ? rhs[static_cast<std::int64_t>(gene) * rhs_ld + col] : 0;
+}
+
+// Row-major -> block-major values (CX_BELL_BLOCK_MAJOR_VALUES), one thread per element of
+// the output; rows past the matrix are zero.
+template<typename T>
+__global__ void block_major_kernel(const T *values, std::uint32_t rows, std::uint32_t bs,
+                                   std::uint32_t ell_cols, std::uint64_t total, T *out) {
+    const std::uint64_t idx = blockIdx.x * static_cast<std::uint64_t>(blockDim.x) + threadIdx.x;
+    if (idx >= total) return;
+    const std::uint64_t block = idx / (static_cast<std::uint64_t>(bs) * bs);  // rb * width + slot
+    const std::uint32_t within = static_cast<std::uint32_t>(idx % (static_cast<std::uint64_t>(bs) * bs));
+    const std::uint32_t width = ell_cols / bs;
+    const std::uint64_t rb = block / width;
+    const std::uint32_t slot = static_cast<std::uint32_t>(block % width);
+    const std::uint64_t row = rb * bs + within / bs;
+    out[idx] = row < rows ? values[row * ell_cols + static_cast<std::uint64_t>(slot) * bs + within % bs] : T{};
 }
 
 template<typename T>
@@ -616,8 +692,10 @@ __global__ __launch_bounds__(256) void bell_spmm_generic(BellArgs a, std::uint32
                         : row_offset;
                     x = __builtin_fmaf(static_cast<float>(code), scale, offset);
                 } else {
-                    x = load_as_float<float>(a.values, static_cast<std::uint64_t>(row) * a.ell_cols + slot,
-                                             value_dtype);
+                    const std::uint64_t vi = a.block_major != 0u
+                        ? ((static_cast<std::uint64_t>(rb) * width + s) * bs + row % bs) * bs + kk
+                        : static_cast<std::uint64_t>(row) * a.ell_cols + slot;
+                    x = load_as_float<float>(a.values, vi, value_dtype);
                 }
                 if (c < n) {
                     const float w = load_as_float<float>(a.rhs, col * a.rhs_ld + c, rhs_dtype);
@@ -641,6 +719,10 @@ int validate_bell(const cx_bell_matrix *m, const void *rhs, std::int64_t rhs_ld,
         return fail(CX_STATUS_INVALID_SHAPE, "Blocked-ELL: ell_cols must be a positive multiple of block_size");
     if (m->rows != 0u && m->block_col_idx == nullptr)
         return fail(CX_STATUS_INVALID_ARGUMENT, "Blocked-ELL: null block_col_idx");
+    if ((m->value_layout_flags & ~CX_BELL_BLOCK_MAJOR_VALUES) != 0u || m->reserved != 0u)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "Blocked-ELL: unknown value layout flags");
+    if (m->bits != 0u && m->value_layout_flags != 0u)
+        return fail(CX_STATUS_UNSUPPORTED, "Blocked-ELL: quantized values are row-major only");
     if (m->bits != 0u) {
         if (!(m->bits == 1u || m->bits == 2u || m->bits == 4u || m->bits == 8u))
             return fail(CX_STATUS_UNSUPPORTED, "quantized Blocked-ELL bits must be 1, 2, 4 or 8");
@@ -681,6 +763,10 @@ BellArgs make_args(const cx_bell_matrix *m, const void *rhs, std::int64_t rhs_ld
     a.block_size = m->block_size;
     a.ell_cols = m->ell_cols;
     a.row_stride_bytes = m->row_stride_bytes;
+    a.block_major = m->value_layout_flags & CX_BELL_BLOCK_MAJOR_VALUES;
+    const std::uint32_t size = m->value_dtype == CELLERATOR_DTYPE_F32 ? 4u : 2u;
+    a.a_row_bytes = (a.block_major ? m->block_size : m->ell_cols) * size;
+    a.a_slot_bytes = m->block_size * (a.block_major ? m->block_size : 1u) * size;
     return a;
 }
 
@@ -723,12 +809,53 @@ extern "C" int cx_bell_pack_rhs(const uint16_t *rhs_bf16, int64_t rhs_ld, uint32
     clear_error();
     if (rhs_bf16 == nullptr || packed == nullptr)
         return fail(CX_STATUS_INVALID_ARGUMENT, "cx_bell_pack_rhs: null rhs or packed output");
-    if (k == 0u || n == 0u || rhs_ld < static_cast<int64_t>(n))
-        return fail(CX_STATUS_INVALID_SHAPE, "cx_bell_pack_rhs: bad shape");
+    if (k == 0u || n == 0u || n % 32u != 0u || rhs_ld < static_cast<int64_t>(n))
+        return fail(CX_STATUS_INVALID_SHAPE, "cx_bell_pack_rhs: bad shape (n must be a multiple of 32)");
     const std::uint64_t total = static_cast<std::uint64_t>((k + 31u) / 32u) * n * 32u;
-    hipLaunchKernelGGL(pack_rhs_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256),
+    hipLaunchKernelGGL(pack_rhs_frag_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256),
                        0, static_cast<hipStream_t>(stream), rhs_bf16, rhs_ld, k, n, packed);
     return check_launch("cx_bell_pack_rhs");
+}
+
+namespace cx {
+int pack_panel_columns(const std::uint16_t *rhs, std::int64_t rhs_ld, std::uint32_t k, std::uint32_t n,
+                       std::uint16_t *packed, hipStream_t stream) {
+    const std::uint64_t total = static_cast<std::uint64_t>((k + 31u) / 32u) * n * 32u;
+    hipLaunchKernelGGL(pack_rhs_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256),
+                       0, stream, rhs, rhs_ld, k, n, packed);
+    return check_launch("pack_rhs_kernel");
+}
+} // namespace cx
+
+extern "C" int cx_bell_block_major_values(const cx_bell_matrix *m, void *out, uint64_t capacity,
+                                          void *stream) {
+    using namespace cx;
+    clear_error();
+    if (m == nullptr || out == nullptr || (m->rows != 0u && m->values == nullptr))
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_bell_block_major_values: null matrix, values or output");
+    if (m->bits != 0u || m->value_layout_flags != 0u)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_bell_block_major_values: needs row-major unquantized values");
+    if (m->block_size == 0u || m->ell_cols == 0u || m->ell_cols % m->block_size != 0u)
+        return fail(CX_STATUS_INVALID_SHAPE, "cx_bell_block_major_values: ell_cols must be a positive multiple of block_size");
+    const std::uint32_t size = m->value_dtype == CELLERATOR_DTYPE_F32 ? 4u
+        : (m->value_dtype == CELLERATOR_DTYPE_BF16 || m->value_dtype == CELLERATOR_DTYPE_F16) ? 2u : 0u;
+    if (size == 0u) return fail(CX_STATUS_UNSUPPORTED, "cx_bell_block_major_values: values must be BF16, F16 or F32");
+    const std::uint64_t total = static_cast<std::uint64_t>((m->rows + m->block_size - 1u) / m->block_size)
+        * m->ell_cols * m->block_size;
+    if (capacity < total * size)
+        return fail(CX_STATUS_INVALID_SHAPE, "cx_bell_block_major_values: output capacity is too small");
+    if (total == 0u) return CX_STATUS_SUCCESS;
+    const dim3 grid(static_cast<unsigned>((total + 255) / 256));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (size == 4u)
+        hipLaunchKernelGGL(block_major_kernel<std::uint32_t>, grid, dim3(256), 0, s,
+                           static_cast<const std::uint32_t *>(m->values), m->rows, m->block_size, m->ell_cols,
+                           total, static_cast<std::uint32_t *>(out));
+    else
+        hipLaunchKernelGGL(block_major_kernel<std::uint16_t>, grid, dim3(256), 0, s,
+                           static_cast<const std::uint16_t *>(m->values), m->rows, m->block_size, m->ell_cols,
+                           total, static_cast<std::uint16_t *>(out));
+    return check_launch("cx_bell_block_major_values");
 }
 
 extern "C" int cx_bell_spmm_fwd_packed(const cx_bell_matrix *m, const uint16_t *packed_rhs,
@@ -823,8 +950,14 @@ extern "C" int cx_bell_spmm_fwd_grouped_epilogue(const cx_bell_matrix *m,
     const std::uint32_t gc = groups->group_count, grb = groups->grouped_row_blocks;
     switch (out_cols) {
     case 64: hipLaunchKernelGGL(bell_spmm_mfma_grouped<64>, ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb); break;
-    case 128: hipLaunchKernelGGL(bell_spmm_mfma_slab<128>, ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb); break;
-    default: hipLaunchKernelGGL(bell_spmm_mfma_slab<256>, ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb); break;
+    case 128:
+        if (a.block_major) hipLaunchKernelGGL((bell_spmm_mfma_slab<128, true>), ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb);
+        else hipLaunchKernelGGL((bell_spmm_mfma_slab<128, false>), ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb);
+        break;
+    default:
+        if (a.block_major) hipLaunchKernelGGL((bell_spmm_mfma_slab<256, true>), ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb);
+        else hipLaunchKernelGGL((bell_spmm_mfma_slab<256, false>), ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb);
+        break;
     }
     rc = check_launch("bell_spmm_mfma_grouped");
     return rc;

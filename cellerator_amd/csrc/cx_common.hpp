@@ -28,6 +28,11 @@ inline int fail(int status, const char *message) {
 // Returns CX_STATUS_HIP_ERROR if the last launch on this thread failed.
 int check_launch(const char *kernel);
 
+// Column-contiguous 16-bit weight panel [ceil(k/32)][n][32] (genes past k zero), the matrix-
+// core operand of the quantized CSR path's dense head (bell_spmm.hip).
+int pack_panel_columns(const std::uint16_t *rhs, std::int64_t rhs_ld, std::uint32_t k, std::uint32_t n,
+                       std::uint16_t *packed, hipStream_t stream);
+
 // Exact fp16 -> fp32 widening on the device.
 __device__ __forceinline__ float h2f(std::uint16_t bits) {
     _Float16 h;

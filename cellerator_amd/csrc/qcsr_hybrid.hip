@@ -952,8 +952,8 @@ extern "C" int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *m, const cx_qcsr_hy
     auto *panel = reinterpret_cast<std::uint16_t *>(static_cast<unsigned char *>(workspace)
                                                     + align256(static_cast<std::uint64_t>(m->rows) * 256u));
     // the head genes' weights as the matrix-core operand panel [H/32][out_cols][32]
-    rc = cx_bell_pack_rhs(static_cast<const std::uint16_t *>(rhs), rhs_ld, L.head_cols,
-                          static_cast<std::uint32_t>(out_cols), panel, stream);
+    rc = pack_panel_columns(static_cast<const std::uint16_t *>(rhs), rhs_ld, L.head_cols,
+                            static_cast<std::uint32_t>(out_cols), panel, s);
     if (rc != CX_STATUS_SUCCESS) return rc;
     for (std::int64_t c0 = 0; c0 < out_cols; c0 += 64) {
         rc = launch_head(L, panel + c0 * 32, static_cast<std::uint32_t>(out_cols), partial, s);

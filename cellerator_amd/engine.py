@@ -343,7 +343,9 @@ class BellMatrix:
     block_size: int
     ell_cols: int
     block_col_idx: torch.Tensor  # uint32 as int32 storage [rows/bs, ell_cols/bs]
-    values: Optional[torch.Tensor] = None  # [rows, ell_cols] bf16/f16/f32
+    # [rows, ell_cols] bf16/f16/f32, or block-major [rows/bs, ell_cols/bs, bs, bs] when
+    # block_major is set (cx_bell_block_major_values)
+    values: Optional[torch.Tensor] = None
     bits: int = 0
     decode_policy: int = N.DECODE_PER_GENE_AFFINE
     row_stride_bytes: int = 0
@@ -352,6 +354,7 @@ class BellMatrix:
     column_offsets: Optional[torch.Tensor] = None
     row_offsets: Optional[torch.Tensor] = None
     meta: dict = field(default_factory=dict)
+    block_major: bool = False
 
     def descriptor(self) -> N.CxBellMatrix:
         d = N.CxBellMatrix()
@@ -363,7 +366,23 @@ class BellMatrix:
         d.packed_values = _ptr(self.packed_values)
         d.column_scales, d.column_offsets = _ptr(self.column_scales), _ptr(self.column_offsets)
         d.row_offsets = _ptr(self.row_offsets)
+        d.value_layout_flags = N.BELL_BLOCK_MAJOR_VALUES if self.block_major else 0
         return d
+
+
+def bell_block_major(m: BellMatrix, stream=None) -> BellMatrix:
+    """The same matrix with its values copied into block-major order
+    (cx_bell_block_major_values): every block_size x block_size value block contiguous."""
+    _require_cuda(m.block_col_idx)
+    if m.values is None or m.bits != 0 or m.block_major:
+        raise ValueError("bell_block_major takes a matrix with row-major unquantized values")
+    bs, rb = m.block_size, (m.rows + m.block_size - 1) // m.block_size
+    out = torch.empty((rb, m.ell_cols // bs, bs, bs), dtype=m.values.dtype, device=m.values.device)
+    d = m.descriptor()
+    N.check("cx_bell_block_major_values", N.engine().cx_bell_block_major_values(
+        C.byref(d), out.data_ptr(), out.numel() * out.element_size(), _stream(stream)))
+    return BellMatrix(m.rows, m.cols, bs, m.ell_cols, m.block_col_idx, values=out,
+                      meta=dict(m.meta), block_major=True)
 
 
 def bell_spmm(m: BellMatrix, rhs: torch.Tensor, out: Optional[torch.Tensor] = None,

@@ -506,7 +506,25 @@ typedef struct cx_bell_matrix {
     const float *column_scales;
     const float *column_offsets;
     const float *row_offsets;
+    uint32_t value_layout_flags; /* 0 or CX_BELL_BLOCK_MAJOR_VALUES */
+    uint32_t reserved;           /* 0 */
 } cx_bell_matrix;
+
+/* cx_bell_matrix.value_layout_flags: the unquantized values are block-major,
+ * [ceil(rows / block_size)][slot][row in block][column in block] with every block whole
+ * (rows past the matrix are padding) -- the layout the CSR -> Blocked-ELL lowering emits as
+ * CX_BELL_VALUES_BLOCK_MAJOR (physical_bell.hh) -- instead of row-major [rows][ell_cols].
+ * Every Blocked-ELL entry point takes either layout with the same results; quantized
+ * (packed) values are row-major only. Engine addition (the reference's projection kernels
+ * read row-major values). */
+#define CX_BELL_BLOCK_MAJOR_VALUES 1u
+
+/* Copies the row-major unquantized values of `a` into block-major order
+ * (CX_BELL_BLOCK_MAJOR_VALUES), zero rows for the padding of the last row block:
+ * ceil(rows / block_size) * ell_cols * block_size elements of a->value_dtype; `capacity`
+ * is the size of `out` in bytes. Engine addition, done once per matrix. */
+int cx_bell_block_major_values(const cx_bell_matrix *a, void *out, uint64_t capacity,
+                               void *stream);
 
 /* Y = X_bell . RHS with a row-major RHS (F32, F16 or BF16), any block size and N, plain
  * (BF16/F16/F32) or quantized values: fp32 accumulation in slot order per output
@@ -525,9 +543,12 @@ int cx_bell_spmm_fwd_epilogue(const cx_bell_matrix *a, const void *rhs, uint32_t
                               int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
                               const cx_spmm_epilogue *epilogue, void *stream);
 
-/* Packs a row-major bf16 RHS [k x n] into the matrix-core operand panel
- * [ceil(k/32)][n][32] (genes of one 32-gene block column contiguous per output column,
- * zero-padded past k): the Blocked-ELL counterpart of pack_dense_operand_cuda
+/* Packs a row-major bf16 RHS [k x n] (n a multiple of 32) into the matrix-core operand
+ * panel, in fragment order: for every 32-gene block column kb, output-column tile t
+ * (32 columns) and K half h (16 genes), 64 groups of 8 bf16, group l holding column
+ * 32 t + l % 32, genes 32 kb + 16 h + 8 (l / 32) .. + 7 -- exactly the 16 bytes lane l of a
+ * v_mfma_f32_32x32x16_bf16 B operand takes, so one wave reads each 1 KB piece contiguously
+ * (genes past k are zero). The Blocked-ELL counterpart of pack_dense_operand_cuda
  * (include/Cellerator/compute/math/packed_dense_operand.hh:16-70). `packed` holds
  * ceil(k/32) * n * 32 bf16. Done once per weight generation. */
 int cx_bell_pack_rhs(const uint16_t *rhs_bf16, int64_t rhs_ld, uint32_t k, uint32_t n,
