@@ -355,8 +355,10 @@ def bench_bell(args, torch, cfg) -> dict:
                        "groups": groups.group_count, "grouped_row_blocks": groups.grouped_row_blocks,
                        "single_row_blocks": groups.single_count}},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(cfg.name),
-                     "kernel": "bell_spmm_mfma<256>" if groups is None else "bell_spmm_mfma_slab<256> (grouped, + singles)",
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": load_traffic(cfg.name + ("" if mb is not None else " row-major")),
+                     "kernel": ("bell_spmm_mfma<256>" if groups is None else "bell_spmm_mfma_slab<256> (grouped, + singles)")
+                               + (", row-major values" if mb is None else ", block-major values"),
                      "kernel_ms_mean": kern_ms,
                      "kernel_ms_median": statistics.median(ev), "algorithmic_bytes": alg_bytes,
                      "mfma_tflops": flops / (kern_ms * 1e-3) / 1e12,
