@@ -389,14 +389,16 @@ __device__ __forceinline__ void load_lds16(rsrc_t r, uint4 *dst, std::uint32_t v
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void)dst, 16, voffset, soffset, 0, 0);
 }
 
-template<int kN, bool kBlockMajor>
-__global__ __launch_bounds__(kWave *kGroupWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template<int kN, bool kBlockMajor, int kWaves>
+__global__ __launch_bounds__(kWave *kWaves) __attribute__((amdgpu_waves_per_eu(kWaves / 2, kWaves / 2)))
 void bell_spmm_mfma_slab(BellArgs a, const std::uint16_t *packed_rhs, std::uint32_t panel_bytes,
                          const std::uint32_t *order, const std::uint32_t *group_offsets,
                          std::uint32_t group_count, std::uint32_t grouped_row_blocks) {
-    constexpr int kSlabTiles = kN / (32 * kGroupWaves);
+    constexpr int kSlabTiles = kN / (32 * kWaves);
     static_assert(kSlabTiles >= 1, "a slab is at least one 32-column tile");
-    constexpr int kStepLoads = 2 * kSlabTiles + 2;  // vector loads one step issues: B, then A
+    constexpr int kPieces = 2 * kGroupWaves / kWaves;  // A pieces (member, half) per wave per step
+    static_assert(kPieces == 1 || kPieces == 2, "4 or 8 waves");
+    constexpr int kStepLoads = 2 * kSlabTiles + kPieces;  // vector loads one step issues: B, then A
     // Loads run three steps ahead; at the end of step k only the loads of steps k + 2 and k + 3
     // may still be in flight.
     constexpr unsigned kStepWait = vmcnt_wait(2 * kStepLoads);
@@ -434,8 +436,9 @@ void bell_spmm_mfma_slab(BellArgs a, const std::uint16_t *packed_rhs, std::uint3
             ? a.block_col_idx[static_cast<std::uint64_t>(rb) * width + lane] : kInvalidBlock;
         own_steps[mm] = static_cast<std::uint32_t>(mm) < members ? static_cast<std::uint32_t>(__popcll(__ballot(sid != kInvalidBlock))) : 0u;
     }
-    // this wave's A loads: members la and lb, K half kh (all wave-uniform)
-    const std::uint32_t la = wave / 2u, lb = 2u + wave / 2u, kh = wave % 2u;
+    // this wave's A loads: pieces wave and wave + kWaves of the 8 (member, half) pieces, i.e.
+    // members la and lb (4 waves) or la alone (8 waves), half kh (all wave-uniform)
+    const std::uint32_t la = wave / 2u, lb = (wave + static_cast<std::uint32_t>(kWaves)) / 2u, kh = wave % 2u;
     struct ALoads {
         rsrc_t r;
         unsigned long long valid;
@@ -453,7 +456,8 @@ void bell_spmm_mfma_slab(BellArgs a, const std::uint16_t *packed_rhs, std::uint3
                         a_block_row_bytes(a, rb));
         return l;
     };
-    ALoads ld_a = a_loads(la), ld_b = a_loads(lb);
+    ALoads ld_a = a_loads(la), ld_b;
+    if constexpr (kPieces == 2) ld_b = a_loads(lb);
     const rsrc_t rbp = make_rsrc(packed_rhs, panel_bytes);
     const int m = lane % 32;
     const int kq = (lane / 32) * 8;
@@ -514,7 +518,7 @@ void bell_spmm_mfma_slab(BellArgs a, const std::uint16_t *packed_rhs, std::uint3
     };
     auto issue_a = [&](Slot &slot) {
         issue_one(ld_a, la, slot);
-        issue_one(ld_b, lb, slot);
+        if constexpr (kPieces == 2) issue_one(ld_b, lb, slot);
     };
     // Barrier without a memory fence (a fence would wait for every LDS load in flight): the
     // waits before it are explicit, and the asm's memory clobber keeps LDS accesses on their
@@ -540,25 +544,33 @@ void bell_spmm_mfma_slab(BellArgs a, const std::uint16_t *packed_rhs, std::uint3
             __builtin_amdgcn_sched_barrier(0);
             issue_a(fill_slot);  // A(k + 3)
             __builtin_amdgcn_sched_barrier(0);
-            // all members' A fragments first (one LDS round trip), then their products
-            cx_bf16x8 af[kGroupWaves][2];
-#pragma unroll
-            for (int mm = 0; mm < kGroupWaves; ++mm)
+            // 4 waves: all members' A fragments first (one LDS round trip), then their
+            // products; 8 waves (128 registers): each member's fragments just before its own
+            auto read_a = [&](cx_bf16x8 (&f)[2], int mm) {
 #pragma unroll
                 for (int kc = 0; kc < 2; ++kc) {
                     if constexpr (kBlockMajor)
-                        af[mm][kc] = __builtin_bit_cast(cx_bf16x8, (&slot[mm][0][0])[a_read[kc]]);
+                        f[kc] = __builtin_bit_cast(cx_bf16x8, (&slot[mm][0][0])[a_read[kc]]);
                     else
-                        af[mm][kc] = __builtin_bit_cast(cx_bf16x8, slot[mm][kc][lane]);
+                        f[kc] = __builtin_bit_cast(cx_bf16x8, slot[mm][kc][lane]);
                 }
+            };
+            constexpr bool kHoist = kWaves == 4;
+            cx_bf16x8 af[kHoist ? kGroupWaves : 1][2];
+            if constexpr (kHoist) {
+#pragma unroll
+                for (int mm = 0; mm < kGroupWaves; ++mm) read_a(af[mm], mm);
+            }
 #pragma unroll
             for (int mm = 0; mm < kGroupWaves; ++mm) {
                 if (k < own_steps[mm]) {
+                    if constexpr (!kHoist) read_a(af[0], mm);
 #pragma unroll
                     for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
                         for (int t = 0; t < kSlabTiles; ++t)
-                            acc[mm][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mm][kc], b_cur.f[t][kc], acc[mm][t], 0, 0, 0);
+                            acc[mm][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kHoist ? mm : 0][kc], b_cur.f[t][kc],
+                                                                                 acc[mm][t], 0, 0, 0);
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -951,13 +963,15 @@ extern "C" int cx_bell_spmm_fwd_grouped_epilogue(const cx_bell_matrix *m,
     switch (out_cols) {
     case 64: hipLaunchKernelGGL(bell_spmm_mfma_grouped<64>, ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb); break;
     case 128:
-        if (a.block_major) hipLaunchKernelGGL((bell_spmm_mfma_slab<128, true>), ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb);
-        else hipLaunchKernelGGL((bell_spmm_mfma_slab<128, false>), ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb);
+        if (a.block_major) hipLaunchKernelGGL((bell_spmm_mfma_slab<128, true, 4>), ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb);
+        else hipLaunchKernelGGL((bell_spmm_mfma_slab<128, false, 4>), ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb);
         break;
-    default:
-        if (a.block_major) hipLaunchKernelGGL((bell_spmm_mfma_slab<256, true>), ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb);
-        else hipLaunchKernelGGL((bell_spmm_mfma_slab<256, false>), ggrid, gblock, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb);
+    default: {
+        const dim3 gblock8(kWave * 8);
+        if (a.block_major) hipLaunchKernelGGL((bell_spmm_mfma_slab<256, true, 8>), ggrid, gblock8, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb);
+        else hipLaunchKernelGGL((bell_spmm_mfma_slab<256, false, 8>), ggrid, gblock8, 0, s, a, packed_rhs, pb, groups->order, groups->group_offsets, gc, grb);
         break;
+    }
     }
     rc = check_launch("bell_spmm_mfma_grouped");
     return rc;
