@@ -6,10 +6,17 @@ quantized CSR, 1,000,000 cells x 33,538 genes, row nnz ~ LogNormal(mean 1,500, s
 Zipf(1.1) gene popularity, per-gene scale/offset, fp16 W 33,538 x 64 ~ N(0, 0.02), fp32 Y.
 Inputs are generated seeded on the GPU and are resident in HBM before timing starts.
 
-One step = one cx_qcsr_spmm_fwd launch over the whole matrix. Prints ONE JSON line:
-metric/value (nnz/s), ms_per_step, roofline of the kernel (achieved algorithmic GB/s from
-HIP events on the launch stream vs 8 TB/s), and the CPU baseline (the oracle's row-parallel
-fp32 restatement timed on this host on a bounded row sample).
+One step = one launch of the prepared execution-order path over the whole matrix
+(cx_qcsr_spmm_fwd_hybrid: the 2,048 most stored genes on the matrix cores, the rest
+through the prepared tail stream; the structure is prepared once, untimed), with the
+canonical cx_qcsr_spmm_fwd kernel timed beside it (--canonical makes it the headline).
+Prints ONE JSON line: metric/value (nnz/s), ms_per_step, roofline of the kernels
+(achieved algorithmic GB/s from HIP events on the launch stream vs 8 TB/s), and the CPU
+baseline (the oracle's row-parallel fp32 restatement timed on this host).
+
+Other configs: c2, c3n128 (the same path), c4 (Blocked-ELL on the matrix cores; block-major
+values copied once before timing, the row-major values timed beside them; --row-major for
+those alone), c5 (CP-BP warp-tile reduction).
 
   python bench.py [--steps K] [--warmup W] [--config c3|c3n128|c2|c4|c5] [--no-cpu]
 """
