@@ -55,11 +55,10 @@ struct BellArgs {
     Epilogue ep;
 };
 
-// Byte offset of panel fragment (tile t, K half h) of block column bc for lane `lane`, in a
-// panel of n output columns (cx_bell_pack_rhs's fragment order).
-__device__ __forceinline__ std::uint32_t panel_frag(std::uint32_t n, std::uint32_t tile, std::uint32_t half,
-                                                    int lane) {
-    (void)n;
+// Byte offset, within one block column's slice of the fragment-order panel
+// (cx_bell_pack_rhs), of lane `lane`'s 16-byte B operand for 32-column tile `tile`, K half
+// `half`.
+__device__ __forceinline__ std::uint32_t panel_frag(std::uint32_t tile, std::uint32_t half, int lane) {
     return ((tile * 2u + half) * 64u + static_cast<std::uint32_t>(lane)) * 16u;
 }
 
@@ -137,7 +136,7 @@ __global__ __launch_bounds__(kN) void bell_spmm_mfma(BellArgs a, const std::uint
         for (int t = 0; t < kTilesPerWave; ++t)
 #pragma unroll
             for (int kc = 0; kc < 2; ++kc)
-                f.b[t][kc] = load_frag(rbp, bo + panel_frag(kN, static_cast<std::uint32_t>(wave * kTilesPerWave + t),
+                f.b[t][kc] = load_frag(rbp, bo + panel_frag(static_cast<std::uint32_t>(wave * kTilesPerWave + t),
                                                             static_cast<std::uint32_t>(kc), lane));
     };
 
@@ -369,15 +368,16 @@ void bell_spmm_mfma_grouped(BellArgs a, const std::uint16_t *packed_rhs, std::ui
     }
 }
 
-// Grouped MFMA path by column slab (N = 128, 256). Same groups, steps and sums as above, but
-// wave w computes output columns [w N/4, (w + 1) N/4) of every member. The members' A
-// fragments (2 KB each per step) are shared through an LDS ring, loaded straight into LDS
-// (buffer loads with the lds flag), and each wave's B fragments (its slab of the step's
+// Grouped MFMA path by column slab (N = 128 with 4 waves, N = 256 with 8). Same groups, steps
+// and sums as above, but wave w computes output columns [32w, 32w + 32) of every member. The
+// members' A blocks (2 KB each per step) are shared through an LDS ring, loaded straight into
+// LDS (buffer loads with the lds flag), and each wave's B fragments (its slab of the step's
 // panel slice) come from the packed panel into registers; both run three steps ahead. Per
 // group and step the LDS carries 8 KB of A, written once and read by every wave with
 // conflict-free 16-byte reads, instead of a 16 KB slice read four times. A member without a
 // step k skips its products. Per output element the products are accumulated in the same
 // slot order as the other MFMA kernels, so the results are bitwise equal.
+
 // s_waitcnt operand: vector memory count n (6 bits, split over two fields), lgkmcnt(0),
 // expcnt unchecked
 constexpr unsigned vmcnt_wait(int n) {
@@ -502,7 +502,7 @@ void bell_spmm_mfma_slab(BellArgs a, const std::uint16_t *packed_rhs, std::uint3
         for (int t = 0; t < kSlabTiles; ++t)
 #pragma unroll
             for (int kc = 0; kc < 2; ++kc)
-                b.f[t][kc] = load_frag(rbp, panel_frag(kN, wave * kSlabTiles + static_cast<std::uint32_t>(t),
+                b.f[t][kc] = load_frag(rbp, panel_frag(wave * kSlabTiles + static_cast<std::uint32_t>(t),
                                                        static_cast<std::uint32_t>(kc), lane),
                                        bc * static_cast<std::uint32_t>(kN) * 64u);
     };
