@@ -100,10 +100,14 @@ __device__ __forceinline__ std::uint32_t select_bit32(std::uint32_t m, std::uint
     return base;
 }
 
+// One 32-bit select on the half that holds the bit, chosen by selects: a branch here would
+// be divergent across the wave and run both halves.
 __device__ __forceinline__ std::uint32_t select_bit(std::uint64_t m, std::uint32_t r) {
     const std::uint32_t lo = static_cast<std::uint32_t>(m);
     const std::uint32_t c = static_cast<std::uint32_t>(__builtin_popcount(lo));
-    return r < c ? select_bit32(lo, r) : 32u + select_bit32(static_cast<std::uint32_t>(m >> 32), r - c);
+    const bool up = r >= c;
+    return (up ? 32u : 0u)
+        + select_bit32(up ? static_cast<std::uint32_t>(m >> 32) : lo, up ? r - c : r);
 }
 
 __device__ __forceinline__ std::uint32_t select_bit(std::uint32_t m, std::uint32_t r) {
@@ -198,7 +202,7 @@ template<typename MaskT>
 __device__ __forceinline__ BatchExtent batch_extent(const BatchInput<MaskT> &b) {
     BatchExtent x;
     x.s0 = uniform(b.s_j);
-    const unsigned long long fit = __ballot(b.has_entry && b.s_next - x.s0 <= kBatchValues);
+    const std::uint64_t fit = __builtin_amdgcn_ballot_w64(b.has_entry && b.s_next - x.s0 <= kBatchValues);
     x.n = max(1u, static_cast<std::uint32_t>(__popcll(fit)));
     const std::uint32_t v_end = static_cast<std::uint32_t>(
         __builtin_amdgcn_readlane(static_cast<int>(b.s_next), static_cast<int>(x.n) - 1));
@@ -211,7 +215,7 @@ __device__ __forceinline__ BatchExtent batch_extent(const BatchInput<MaskT> &b) 
 template<typename MaskT>
 __device__ __forceinline__ std::uint32_t next_descriptor(const BatchInput<MaskT> &b, std::uint32_t d,
                                                          std::uint32_t e_next) {
-    const unsigned long long passed = __ballot(b.has_desc && b.eo_k <= e_next);
+    const std::uint64_t passed = __builtin_amdgcn_ballot_w64(b.has_desc && b.eo_k <= e_next);
     return d + max(1u, static_cast<std::uint32_t>(__popcll(passed))) - 1u;
 }
 
@@ -303,27 +307,33 @@ __global__ __launch_bounds__(kWave *kCpbpWaves) void cpbp_reduce_kernel(CpbpArgs
                 float sum = 0.0f;
                 if constexpr (kLdsPlan) {
                     const float *w = &wp[bb];
+                    // An absent bit reads weight 31 of the block (m | bit 31 is never 0, and
+                    // the weight stage is padded by one block) and at most the stage's
+                    // 4-value tail, so every read is in bounds and needs no exec mask. Its
+                    // product is dropped by one select on the sum (zeroing only one operand
+                    // would let a non-finite value or weight from outside the entry in).
+                    constexpr std::uint32_t kStop = 0x80000000u;
                     while (m != 0u) {  // four stored values per step
                         const std::uint32_t b0 = static_cast<std::uint32_t>(__builtin_ctz(m));
                         m &= m - 1u;
                         const bool h1 = m != 0u;
-                        const std::uint32_t b1 = h1 ? static_cast<std::uint32_t>(__builtin_ctz(m)) : 0u;
+                        const std::uint32_t b1 = static_cast<std::uint32_t>(__builtin_ctz(m | kStop));
                         m &= m - 1u;
                         const bool h2 = m != 0u;
-                        const std::uint32_t b2 = h2 ? static_cast<std::uint32_t>(__builtin_ctz(m)) : 0u;
+                        const std::uint32_t b2 = static_cast<std::uint32_t>(__builtin_ctz(m | kStop));
                         m &= m - 1u;
                         const bool h3 = m != 0u;
-                        const std::uint32_t b3 = h3 ? static_cast<std::uint32_t>(__builtin_ctz(m)) : 0u;
+                        const std::uint32_t b3 = static_cast<std::uint32_t>(__builtin_ctz(m | kStop));
                         m &= m - 1u;
-                        // loads first, selects after: every read is in bounds (the stage has
-                        // a 4-value tail, an absent bit reads the block's first weight), so
-                        // no read needs its own exec mask
                         const float v0 = v[0], v1 = v[1], v2 = v[2], v3 = v[3];
                         const float w0 = w[b0], w1 = w[b1], w2 = w[b2], w3 = w[b3];
+                        // keeps the reads unconditional (the compiler would otherwise sink
+                        // them under a divergent branch per select)
+                        __asm__ volatile("" ::"v"(v1), "v"(v2), "v"(v3), "v"(w1), "v"(w2), "v"(w3));
                         sum = __builtin_fmaf(v0, w0, sum);
-                        sum = __builtin_fmaf(h1 ? v1 : 0.0f, h1 ? w1 : 0.0f, sum);
-                        sum = __builtin_fmaf(h2 ? v2 : 0.0f, h2 ? w2 : 0.0f, sum);
-                        sum = __builtin_fmaf(h3 ? v3 : 0.0f, h3 ? w3 : 0.0f, sum);
+                        sum = h1 ? __builtin_fmaf(v1, w1, sum) : sum;
+                        sum = h2 ? __builtin_fmaf(v2, w2, sum) : sum;
+                        sum = h3 ? __builtin_fmaf(v3, w3, sum) : sum;
                         v += 4;
                     }
                 } else {
