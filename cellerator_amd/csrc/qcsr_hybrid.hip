@@ -6,7 +6,7 @@
 // matrix are stored in a large share of the cells: at C3, the first 4,096 of 33,538 genes
 // hold 2/3 of the nonzeros at 24% mean density (59% for the first 1,024). Those columns are
 // dense enough for the matrix cores. Y = X[:, 0:H) . W[0:H, :] + X[:, H:) . W[H:, :]: the
-// head runs here on v_mfma_f32_16x16x32_f16 over a dense copy of X[:, 0:H); the tail runs on
+// head runs here on the matrix cores over a dense copy of X[:, 0:H); the tail runs on
 // the row-group VALU kernel of qcsr_parts.hip, which starts every row at its first entry
 // >= H and adds the head's sums before its epilogue.
 //
@@ -51,6 +51,7 @@
 
 typedef _Float16 cx_half8 __attribute__((ext_vector_type(8)));
 typedef float cx_float4 __attribute__((ext_vector_type(4)));
+typedef float cx_float16 __attribute__((ext_vector_type(16)));
 typedef __fp16 cx_fp16x2 __attribute__((ext_vector_type(2)));
 
 namespace cx {
@@ -274,8 +275,9 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void qcsr_head_dense(HeadArgs h
 // lut[chunk][gene][code] = (hi, mid, lo, 0), entry 16 all zero. The head plane then holds one
 // byte per (row, gene), code * 8 or 128 when the gene is not stored (the table entry's byte
 // offset), chunk-major: bytes[chunk][rows_ld][32]. Decoding a value is one table read; the
-// parts of two genes are packed into the fragments with byte permutes. The values and their
-// order of accumulation are those of the per-value decode above, so the results are the same.
+// parts of two genes are packed into the fragments with byte permutes. The values are those
+// of the per-value decode above; the products run on v_mfma_f32_32x32x16_f16 (two 32-row
+// tiles x two 32-column tiles per wave), so they are summed in another order.
 //
 // Workgroup: 4 waves of 64 rows. Per 32-gene chunk the W^T fragments (4 KB, in fragment order),
 // the chunk's table (4,352 B) and the workgroup's code bytes (8 KB) go through an LDS double
@@ -305,40 +307,67 @@ struct LutArgs {
 };
 
 struct LutShared {
-    uint4 a[2][4][kWave];                  // W^T fragments: [buffer][column block][lane]
+    uint4 a[2][4][kWave];                  // W^T fragments: [buffer][K step * 2 + column tile][lane]
     uint4 lut[2][kLutChunkBytes / 16];     // the chunk's table
     uint4 codes[2][kCodeChunkBytes / 16];  // the workgroup's code bytes: [row][32]
 };
 
-using head_rsrc_t = __amdgpu_buffer_rsrc_t;
-using lds_void = __attribute__((address_space(3))) void *;
+typedef unsigned int head_rsrc_t __attribute__((ext_vector_type(4)));
 
+// Buffer resource over [base, base + bytes): loads past the end return 0.
 __device__ __forceinline__ head_rsrc_t head_rsrc(const void *base, std::uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
-                                             static_cast<int>(bytes), 0x00020000);
+    const std::uint64_t a = reinterpret_cast<std::uint64_t>(base);
+    head_rsrc_t r;
+    r.x = static_cast<unsigned int>(a);
+    r.y = static_cast<unsigned int>(a >> 32) & 0xffffu;  // stride 0
+    r.z = bytes;
+    r.w = 0x00020000u;
+    return r;
+}
+
+// 16 bytes per lane from the buffer at voffset straight into LDS at dst + 16 * lane (a buffer
+// load with the lds flag; the LDS address is taken from m0 when the load issues). Issued as
+// inline assembly so that the compiler sees no LDS write: as a builtin it would wait for
+// every such load before any later LDS read it cannot tell apart from the loaded buffer
+// (both buffers are one array indexed at run time), and the prefetch of the next chunk
+// would stop overlapping the current one (measured: 615 against 571 us per launch at C3).
+// The kernel waits for these loads itself (vmcnt) before the barrier that publishes a
+// buffer. m0 is saved and restored around the load, so the statement leaves every register
+// the compiler owns as it was.
+__device__ __forceinline__ void lds_load16(head_rsrc_t rsrc, const void *dst, std::uint32_t voffset) {
+    using lds_ptr = const __attribute__((address_space(3))) char *;
+    const std::uint32_t base = static_cast<std::uint32_t>(reinterpret_cast<std::uintptr_t>((lds_ptr)dst));
+    std::uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %1\n\t"
+                 "s_nop 0\n\t"
+                 "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "s"(base), "v"(voffset), "s"(rsrc)
+                 : "memory");
 }
 
 // The share of chunk c goes straight from memory into LDS buffer `buf` (buffer loads with the
 // lds flag: each wave instruction fills 1 KB, no registers): the A fragments (wave w loads
-// column block w: lane l reads row w * 16 + l % 16 of the panel, genes 8 (l / 16) .. +7),
-// table pieces w * 64 + lane (pieces 256..271 by lanes 0..15 of wave 0), and the
-// workgroup's code bytes, pieces w * 64 + lane and 256 + w * 64 + lane.
+// fragment (K step w / 2, column tile w % 2): lane l reads row 32 (w % 2) + l % 32 of the
+// panel, genes 16 (l / 32) + 8 (w / 2) .. +7), table pieces w * 64 + lane (pieces 256..271
+// by lanes 0..15 of wave 0), and the workgroup's code bytes, pieces w * 64 + lane and
+// 256 + w * 64 + lane.
 __device__ __forceinline__ void issue_share(LutShared &sh, const LutArgs &h, std::uint32_t c, int buf, int wave,
                                             int lane, std::uint32_t wg_row) {
     const head_rsrc_t pa = head_rsrc(h.panel + static_cast<std::uint64_t>(c) * h.panel_n * 32u, 64u * 64u);
-    const std::uint32_t pa_off = ((static_cast<std::uint32_t>(wave) * 16u + static_cast<std::uint32_t>(lane) % 16u) * 32u
-                                  + 8u * (static_cast<std::uint32_t>(lane) / 16u)) * 2u;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(pa, (lds_void)&sh.a[buf][wave][0], 16, pa_off, 0, 0, 0);
+    const std::uint32_t uw = static_cast<std::uint32_t>(wave), ul = static_cast<std::uint32_t>(lane);
+    const std::uint32_t pa_off = ((32u * (uw % 2u) + ul % 32u) * 32u + 16u * (ul / 32u) + 8u * (uw / 2u)) * 2u;
+    lds_load16(pa, &sh.a[buf][wave][0], pa_off);
     const head_rsrc_t lu = head_rsrc(h.lut + static_cast<std::uint64_t>(c) * (kLutChunkBytes / 16u), kLutChunkBytes);
-    const std::uint32_t piece = static_cast<std::uint32_t>(wave * kWave + lane);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(lu, (lds_void)&sh.lut[buf][wave * kWave], 16, piece * 16u, 0, 0, 0);
+    const std::uint32_t piece = uw * kWave + ul;
+    lds_load16(lu, &sh.lut[buf][wave * kWave], piece * 16u);
     const head_rsrc_t cb = head_rsrc(h.bytes + (static_cast<std::uint64_t>(c) * h.rows_ld + wg_row) * 32u, kCodeChunkBytes);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(cb, (lds_void)&sh.codes[buf][wave * kWave], 16, piece * 16u, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(cb, (lds_void)&sh.codes[buf][256 + wave * kWave], 16,
-                                             (256u + piece) * 16u, 0, 0, 0);
+    lds_load16(cb, &sh.codes[buf][wave * kWave], piece * 16u);
+    lds_load16(cb, &sh.codes[buf][256 + wave * kWave], (256u + piece) * 16u);
     if (wave == 0 && lane < static_cast<int>(kLutChunkBytes / 16u) - 256)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(lu, (lds_void)&sh.lut[buf][256], 16, (256u + static_cast<std::uint32_t>(lane)) * 16u,
-                                                 0, 0, 0);
+        lds_load16(lu, &sh.lut[buf][256], (256u + ul) * 16u);
 }
 
 static_assert(kLutWaves * kWave == 256 && kCodeChunkBytes / 16u == 512u && kLutChunkBytes / 16u == 272u, "share pieces");
@@ -349,20 +378,54 @@ __device__ __forceinline__ std::uint32_t byte_of(std::uint32_t v) {
     return kK == 3 ? v >> 24 : (v >> (8 * kK)) & 0xffu;
 }
 
+// Table entries of the 8 genes gene0 .. gene0 + 7 (from the chunk table at lb) for the code
+// bytes in w0 (genes 0..3) and w1 (genes 4..7), packed into the three B fragments.
+__device__ __forceinline__ void lut_fragments(const char *lb, std::uint32_t w0, std::uint32_t w1, cx_half8 &bh,
+                                              cx_half8 &bm, cx_half8 &bl) {
+    uint2 e[8];
+    e[0] = *reinterpret_cast<const uint2 *>(lb + 0 * kLutGeneBytes + byte_of<0>(w0));
+    e[1] = *reinterpret_cast<const uint2 *>(lb + 1 * kLutGeneBytes + byte_of<1>(w0));
+    e[2] = *reinterpret_cast<const uint2 *>(lb + 2 * kLutGeneBytes + byte_of<2>(w0));
+    e[3] = *reinterpret_cast<const uint2 *>(lb + 3 * kLutGeneBytes + byte_of<3>(w0));
+    e[4] = *reinterpret_cast<const uint2 *>(lb + 4 * kLutGeneBytes + byte_of<0>(w1));
+    e[5] = *reinterpret_cast<const uint2 *>(lb + 5 * kLutGeneBytes + byte_of<1>(w1));
+    e[6] = *reinterpret_cast<const uint2 *>(lb + 6 * kLutGeneBytes + byte_of<2>(w1));
+    e[7] = *reinterpret_cast<const uint2 *>(lb + 7 * kLutGeneBytes + byte_of<3>(w1));
+    std::uint32_t hw[4], mw[4], lw[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        // (hi | mid << 16, lo) of genes 2k and 2k + 1 -> hi pair, mid pair, lo pair
+        hw[k] = __builtin_amdgcn_perm(e[2 * k + 1].x, e[2 * k].x, 0x05040100u);
+        mw[k] = __builtin_amdgcn_perm(e[2 * k + 1].x, e[2 * k].x, 0x07060302u);
+        lw[k] = __builtin_amdgcn_perm(e[2 * k + 1].y, e[2 * k].y, 0x05040100u);
+    }
+    bh = __builtin_bit_cast(cx_half8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+    bm = __builtin_bit_cast(cx_half8, make_uint4(mw[0], mw[1], mw[2], mw[3]));
+    bl = __builtin_bit_cast(cx_half8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
+}
+
+// v_mfma_f32_32x32x16_f16 with A = W^T (32 output columns x 16 genes) and B = the decoded
+// parts (16 genes x 32 rows). The chunk's 32 genes are two K steps; lane half hf carries
+// genes 16 hf .. 16 hf + 15 (K step ks: 16 hf + 8 ks .. +7) in both operands, so its 32
+// lanes read one gene's table at a time. A wave holds 2 row tiles x 2 column tiles; each
+// part's four products are independent, so an accumulator is reused every fourth
+// instruction, which keeps the 16-pass instruction at full rate.
 __global__ __launch_bounds__(kLutWaves * kWave) __attribute__((amdgpu_waves_per_eu(4, 4))) void qcsr_head_lut(LutArgs h) {
     __shared__ LutShared sh;
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const int r16 = lane & 15;
-    const int q = lane >> 4;
+    const int r32 = lane & 31;
+    const int hf = lane >> 5;
     const std::uint32_t wg_row = blockIdx.x * kLutRows;
-    const std::uint32_t row0 = wg_row + static_cast<std::uint32_t>(wave * kRowsPerWave + r16);
-    cx_float4 acc[kTiles][4];
+    const std::uint32_t row0 = wg_row + static_cast<std::uint32_t>(wave * kRowsPerWave + r32);
+    cx_float16 acc[2][2];  // [row tile][column tile]
 #pragma unroll
-    for (int b = 0; b < kTiles; ++b)
+    for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[b][t] = cx_float4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[rt][ct][i] = 0.0f;
 
     if (h.chunks != 0u) issue_share(sh, h, 0u, 0, wave, lane, wg_row);
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's share loads are in LDS
@@ -371,57 +434,53 @@ __global__ __launch_bounds__(kLutWaves * kWave) __attribute__((amdgpu_waves_per_
         const int buf = static_cast<int>(c & 1u);
         // chunk c + 1 into the buffer chunk c - 1 used (every wave passed the barrier after it)
         if (c + 1u < h.chunks) issue_share(sh, h, c + 1u, buf ^ 1, wave, lane, wg_row);
-        cx_half8 aw[4];
+        const char *lb = reinterpret_cast<const char *>(&sh.lut[buf][0]) + 16u * hf * kLutGeneBytes;
+        const char *cbase = reinterpret_cast<const char *>(&sh.codes[buf][0]) + (wave * kRowsPerWave + r32) * 32 + 16 * hf;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) aw[t] = __builtin_bit_cast(cx_half8, sh.a[buf][t][lane]);
-        const char *lb = reinterpret_cast<const char *>(&sh.lut[buf][0]) + 8u * q * kLutGeneBytes;
-        const char *cbase = reinterpret_cast<const char *>(&sh.codes[buf][0])
-            + (wave * kRowsPerWave + r16) * 32 + 8 * q;
+        for (int ks = 0; ks < 2; ++ks) {
+            const cx_half8 a0 = __builtin_bit_cast(cx_half8, sh.a[buf][2 * ks][lane]);
+            const cx_half8 a1 = __builtin_bit_cast(cx_half8, sh.a[buf][2 * ks + 1][lane]);
+            cx_half8 bh[2], bm[2], bl[2];
 #pragma unroll
-        for (int b = 0; b < kTiles; ++b) {
-            uint2 e[8];
-            const uint2 cw = *reinterpret_cast<const uint2 *>(cbase + 16 * 32 * b);
-            const std::uint32_t w0 = cw.x, w1 = cw.y;
-            e[0] = *reinterpret_cast<const uint2 *>(lb + 0 * kLutGeneBytes + byte_of<0>(w0));
-            e[1] = *reinterpret_cast<const uint2 *>(lb + 1 * kLutGeneBytes + byte_of<1>(w0));
-            e[2] = *reinterpret_cast<const uint2 *>(lb + 2 * kLutGeneBytes + byte_of<2>(w0));
-            e[3] = *reinterpret_cast<const uint2 *>(lb + 3 * kLutGeneBytes + byte_of<3>(w0));
-            e[4] = *reinterpret_cast<const uint2 *>(lb + 4 * kLutGeneBytes + byte_of<0>(w1));
-            e[5] = *reinterpret_cast<const uint2 *>(lb + 5 * kLutGeneBytes + byte_of<1>(w1));
-            e[6] = *reinterpret_cast<const uint2 *>(lb + 6 * kLutGeneBytes + byte_of<2>(w1));
-            e[7] = *reinterpret_cast<const uint2 *>(lb + 7 * kLutGeneBytes + byte_of<3>(w1));
-            std::uint32_t hw[4], mw[4], lw[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                // (hi | mid << 16, lo) of genes 2k and 2k + 1 -> hi pair, mid pair, lo pair
-                hw[k] = __builtin_amdgcn_perm(e[2 * k + 1].x, e[2 * k].x, 0x05040100u);
-                mw[k] = __builtin_amdgcn_perm(e[2 * k + 1].x, e[2 * k].x, 0x07060302u);
-                lw[k] = __builtin_amdgcn_perm(e[2 * k + 1].y, e[2 * k].y, 0x05040100u);
+            for (int rt = 0; rt < 2; ++rt) {
+                const uint2 cw = *reinterpret_cast<const uint2 *>(cbase + 32 * 32 * rt + 8 * ks);
+                lut_fragments(lb + 8 * ks * kLutGeneBytes, cw.x, cw.y, bh[rt], bm[rt], bl[rt]);
             }
-            const cx_half8 bh = __builtin_bit_cast(cx_half8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
-            const cx_half8 bm = __builtin_bit_cast(cx_half8, make_uint4(mw[0], mw[1], mw[2], mw[3]));
-            const cx_half8 bl = __builtin_bit_cast(cx_half8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
 #pragma unroll
-            for (int t = 0; t < 4; ++t) acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[t], bh, acc[b][t], 0, 0, 0);
+            for (int rt = 0; rt < 2; ++rt) {
+                acc[rt][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bh[rt], acc[rt][0], 0, 0, 0);
+                acc[rt][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bh[rt], acc[rt][1], 0, 0, 0);
+            }
 #pragma unroll
-            for (int t = 0; t < 4; ++t) acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[t], bm, acc[b][t], 0, 0, 0);
+            for (int rt = 0; rt < 2; ++rt) {
+                acc[rt][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bm[rt], acc[rt][0], 0, 0, 0);
+                acc[rt][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bm[rt], acc[rt][1], 0, 0, 0);
+            }
 #pragma unroll
-            for (int t = 0; t < 4; ++t) acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[t], bl, acc[b][t], 0, 0, 0);
+            for (int rt = 0; rt < 2; ++rt) {
+                acc[rt][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bl[rt], acc[rt][0], 0, 0, 0);
+                acc[rt][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bl[rt], acc[rt][1], 0, 0, 0);
+            }
         }
         __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads of chunk c + 1 are in LDS
         __syncthreads();  // buffer `buf` is free again; chunk c + 1 is in place
     }
 
+    // lane l holds row l % 32 of each row tile; register 4j + i is output column
+    // 32 ct + 8j + 4 (l / 32) + i
 #pragma unroll
-    for (int b = 0; b < kTiles; ++b) {
-        const std::uint32_t row = row0 + 16u * b;
+    for (int rt = 0; rt < 2; ++rt) {
+        const std::uint32_t row = row0 + 32u * rt;
         if (row < h.rows) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                float *o = h.partial + static_cast<std::uint64_t>(row) * 64u + t * 16 + 4 * q;
-                *reinterpret_cast<float4 *>(o) = make_float4(acc[b][t][0] * h.inv_scale, acc[b][t][1] * h.inv_scale,
-                                                             acc[b][t][2] * h.inv_scale, acc[b][t][3] * h.inv_scale);
-            }
+            for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    float *o = h.partial + static_cast<std::uint64_t>(row) * 64u + ct * 32 + 8 * j + 4 * hf;
+                    *reinterpret_cast<float4 *>(o) =
+                        make_float4(acc[rt][ct][4 * j] * h.inv_scale, acc[rt][ct][4 * j + 1] * h.inv_scale,
+                                    acc[rt][ct][4 * j + 2] * h.inv_scale, acc[rt][ct][4 * j + 3] * h.inv_scale);
+                }
         }
     }
 }

@@ -1399,7 +1399,7 @@ const char *cx_exec_last_error(void);
 /* ---- execution-order quantized CSR SpMM with a dense head on the matrix cores -----------
  * For a matrix in an execution order whose first head_cols genes are the most frequently
  * stored ones (cx_popularity_order + cx_qcsr_to_execution_order), the product splits into
- * Y = X[:, 0:H) . W[0:H, :] + X[:, H:) . W[H:, :]. The head runs on v_mfma_f32_16x16x32_f16
+ * Y = X[:, 0:H) . W[0:H, :] + X[:, H:) . W[H:, :]. The head runs on the matrix cores (fp16 MFMA)
  * over a dense copy of X[:, 0:H) (codes and presence bits, built once per matrix): every
  * code is decoded exactly as the reference codec does (fma(code, scale, offset),
  * include/Cellerator/quantized/access.cuh:81-91), scaled by a power of two 2^k and split
