@@ -566,8 +566,9 @@ def main() -> int:
                     help="run only a plain copy of BYTES (rocprofv3 counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: every box in this build has one MI355X and the "
-              "projection shards by rows with no exchange (see DESIGN.md); run with --gpus 1.",
+        print("bench.py measures one GPU only: the projection shards by rows with no exchange "
+              "between GPUs, so one GPU's throughput at its share's shape is the measurement; "
+              "run with --gpus 1.",
               file=sys.stderr)
         return 2
     import torch
