@@ -91,3 +91,42 @@ def test_repeat_is_bitwise_deterministic():
     a = run_reduce(plan, t, w)
     b = run_reduce(plan, t, w)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def with_empty_descriptors(tiles, spots):
+    """Copy of host tiles with a descriptor of no cells (cell mask 0, so no entries)
+    inserted before descriptor `k` of tile `t` for each (t, k) in spots (k may be the
+    tile's descriptor count: after its last one)."""
+    import copy
+    out = copy.deepcopy(tiles)
+    for t, k in sorted(spots, reverse=True):
+        d = int(out.tile_block_offsets[t]) + k
+        assert d <= int(out.tile_block_offsets[t + 1])
+        out.tile_block_ids = np.insert(out.tile_block_ids, d, out.tile_block_ids[max(d - 1, 0)])
+        out.tile_block_cell_masks = np.insert(out.tile_block_cell_masks, d, 0)
+        out.block_row_entry_offsets = np.insert(out.block_row_entry_offsets, d, out.block_row_entry_offsets[d])
+        out.tile_block_offsets = out.tile_block_offsets.copy()
+        out.tile_block_offsets[t + 1:] += 1
+    out.req = dict(out.req, tile_block_count=int(out.tile_block_offsets[-1]))
+    return out
+
+
+@pytest.mark.parametrize("width,dtype", [(64, np.float32), (32, np.float16)])
+def test_descriptors_without_cells(oracle, width, dtype):
+    """A descriptor whose cell mask is 0 starts at the same entry as the next one and holds
+    no entries; it contributes nothing, wherever it sits in a tile (first, between two
+    descriptors, two in a row, last): the product is bitwise the one without it."""
+    rng = np.random.default_rng(width)
+    plan = random_plan(rng, 300)
+    offs, feats, vals = random_csr(rng, 6 * width, 300, 20.0, dtype)
+    w = rng.standard_normal(300).astype(np.float32)
+    t = cpbp.build_tiles(plan, offs, feats, vals, group_width=width, window_size=256)
+    counts = np.diff(t.tile_block_offsets)
+    assert len(counts) >= 4 and (counts[:4] >= 3).all()
+    spots = [(0, 0), (1, int(counts[1]) // 2), (2, 1), (2, 1), (3, int(counts[3]))]
+    e = with_empty_descriptors(t, spots)
+    assert int(e.tile_block_offsets[-1]) == int(t.tile_block_offsets[-1]) + len(spots)
+    base = run_reduce(plan, t, w)
+    got = run_reduce(plan, e, w)
+    assert np.array_equal(got.view(np.uint32), base.view(np.uint32))
+    check(oracle, offs, feats, vals, w, got)
