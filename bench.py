@@ -7,7 +7,7 @@ Zipf(1.1) gene popularity, per-gene scale/offset, fp16 W 33,538 x 64 ~ N(0, 0.02
 Inputs are generated seeded on the GPU and are resident in HBM before timing starts.
 
 One step = one launch of the prepared execution-order path over the whole matrix
-(cx_qcsr_spmm_fwd_hybrid: the 2,048 most stored genes on the matrix cores, the rest
+(cx_qcsr_spmm_fwd_hybrid: the 2,048 most stored genes on the matrix cores (6,144 for c2), the rest
 through the prepared tail stream; the structure is prepared once, untimed), with the
 canonical cx_qcsr_spmm_fwd kernel timed beside it (--canonical makes it the headline).
 Prints ONE JSON line: metric/value (nnz/s), ms_per_step, roofline of the kernels
@@ -35,6 +35,10 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+# Matrix-core head width of the prepared qCSR path per configuration, the best of a sweep in
+# steps of 1,024 genes: C3's genes past the first 2,048 are stored in at most 11% of the
+# cells, C2's (8-bit, 2,000 nnz per cell) stay above 7% up to 6,144.
+HEAD_GENES = {"c3": 2048, "c3n128": 2048, "c2": 6144}
 
 
 def log(msg: str) -> None:
@@ -557,14 +561,18 @@ def main() -> int:
                     help="qCSR: skip the column-order check (kernel keeps its per-entry check)")
     ap.add_argument("--separate-meta", action="store_true",
                     help="C2/C3: time the separate scale/offset arrays instead of interleaved pairs")
-    ap.add_argument("--head", type=int, default=2048,
+    ap.add_argument("--head", type=int, default=None,
                     help="qCSR: matrix-core head genes of the prepared execution-order path (a multiple "
-                         "of 1,024; 0: the whole matrix through the tail stream; -1 skips the path)")
+                         "of 1,024; 0: the whole matrix through the tail stream; -1 skips the path). "
+                         "Default: the measured best per configuration, 2,048 for C3 (4-bit codes, "
+                         "1M x 33,538) and 6,144 for C2 (8-bit codes, 100k x 20k, denser genes)")
     ap.add_argument("--canonical", action="store_true",
                     help="qCSR: headline the canonical row-group kernel on the unprepared CSR")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="run only a plain copy of BYTES (rocprofv3 counter calibration)")
     args = ap.parse_args()
+    if args.head is None:
+        args.head = HEAD_GENES.get(args.config, 2048)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the projection shards by rows with no exchange "
               "between GPUs, so one GPU's throughput at its share's shape is the measurement; "
