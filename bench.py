@@ -35,9 +35,9 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
-# Matrix-core head width of the prepared qCSR path per configuration, the best of a sweep in
-# steps of 1,024 genes: C3's genes past the first 2,048 are stored in at most 11% of the
-# cells, C2's (8-bit, 2,000 nnz per cell) stay above 7% up to 6,144.
+# Matrix-core head width of the prepared qCSR path per configuration, from sweeps in steps of
+# 1,024 genes: at C3, 2,048 and 3,072 measure level (2,048 keeps the smaller layout); C2's
+# genes (8-bit codes, 2,000 nnz per cell) stay above 7% density up to 6,144, its best width.
 HEAD_GENES = {"c3": 2048, "c3n128": 2048, "c2": 6144}
 
 
