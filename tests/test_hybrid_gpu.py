@@ -250,6 +250,30 @@ def test_hybrid_on_c3_rows(oracle):
     check_against_referee(oracle, ref, mag, y.cpu().numpy())
 
 
+def test_hybrid_on_c2_rows(oracle):
+    """C2-generated rows (8-bit codes, 20,000 genes, 2,000 nonzeros per cell) in popularity
+    order with the 6,144-gene head bench.py runs at C2 (the words form), several workgroups
+    of 256 rows and a ragged last one; repeats are bitwise equal."""
+    import torch
+
+    from cellerator_amd import qcsr_pack_gene_affine
+    from cellerator_amd.exec_order import hybrid_prepare, hybrid_spmm, pack_rows
+    from cellerator_amd.synth import C2, dense_normal, generate_qcsr
+    m = generate_qcsr(C2.scaled(3 * 256 + 37))
+    w = dense_normal((m.cols, 64), 0.02, torch.float16, seed=5)
+    mx, order = _exec(qcsr_pack_gene_affine(m))
+    wx = pack_rows(order, w)
+    p = hybrid_prepare(mx, 6144)
+    y = hybrid_spmm(p, wx)
+    y2 = hybrid_spmm(p, wx)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), y2.view(torch.int32))
+    h = qcsr_to_host(m)
+    ref, mag = oracle.qcsr_spmm_referee(8, 1, m.rows, m.cols, h["row_ptr"], h["packed_row_ptr"], h["col_idx"],
+                                        h["packed"], h["scales"], h["offsets"], None, w.cpu().numpy())
+    check_against_referee(oracle, ref, mag, y.cpu().numpy())
+
+
 def test_hybrid_rejects_unsorted_rows_and_bad_metadata(oracle):
     import torch
 
