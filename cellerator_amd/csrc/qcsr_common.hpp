@@ -43,9 +43,12 @@ struct QcsrArgs {
 // 8 layers of 8 rows per 1,024-row block; a fill is 16 steps of the 8 lane groups of a
 // layer, 128 entries stored group-major ([group][step]); entries are u16
 // (gene in part | code << 11) for codes of up to 4 bits and u32 (gene | code << 16) for
-// 8-bit codes. fill_index[(block * parts + part) * kStreamSlots + wave * kStreamLayers +
+// 8-bit codes. fill_index[((block * kStreamWaves + wave) * parts + part) * kStreamLayers +
 // layer] holds the layer's first fill (low 28 bits) and the step count of its last fill
-// minus one (high 4 bits); the entry after the last is the total.
+// minus one (high 4 bits); the entry after the last is the total. A wave's fills are
+// contiguous through all parts. Block rows are sets of 8 rows adjacent in the order of tail
+// lengths over the whole matrix, dealt round-robin to the blocks (slot_rows maps every slot
+// to its row).
 constexpr int kStreamWaves = 16;
 constexpr int kStreamLayers = 8;
 constexpr int kStreamSlots = kStreamWaves * kStreamLayers;        // (wave, layer) per block and part

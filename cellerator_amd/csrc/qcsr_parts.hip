@@ -63,7 +63,8 @@ __device__ __forceinline__ void load_part_weights(uint4 *w, const std::uint16_t 
 
 // The weight rows and (scale, offset) pairs of genes [lo, hi) into LDS. Interleaved pairs
 // go straight to LDS like the weights; the other decode policies build them in registers.
-template<int kPolicy, int kWaves, typename Shared>
+// kWait: wait for every load in flight (vmcnt 0) before returning; otherwise the caller waits.
+template<int kPolicy, int kWaves, typename Shared, bool kWait = true>
 __device__ __forceinline__ void load_part(Shared &sh, const QcsrArgs &a, int lo, int hi, int wave, int lane,
                                           int tid) {
     const int span = hi - lo;
@@ -85,7 +86,7 @@ __device__ __forceinline__ void load_part(Shared &sh, const QcsrArgs &a, int lo,
             sh.meta[g] = md;
         }
     }
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the LDS writes of the loads above
+    if constexpr (kWait) __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the LDS writes of the loads above
 }
 
 __device__ __forceinline__ void fma8(float (&p)[8], float x, uint4 w) {
@@ -540,6 +541,11 @@ __global__ __launch_bounds__(kStreamWaves * kWave) void qcsr_spmm_stream(QcsrArg
     const std::uint32_t blk_first = __builtin_amdgcn_readfirstlane(ix[0]) & kFillMask;
     const std::uint32_t blk_end =
         __builtin_amdgcn_readfirstlane(ix[static_cast<std::uint64_t>(parts) * kStreamSlots]) & kFillMask;
+    // This wave's index entries, (part, layer) order; entry parts * kLayers is the first fill
+    // after the wave's (the next wave's, or the next block's, first).
+    const std::uint32_t *wx = ix + static_cast<std::uint64_t>(wave) * parts * kLayers;
+    const rsrc_t rx = make_rsrc(wx, static_cast<std::uint32_t>(parts * kLayers + 1) * 4u);
+    const std::uint32_t ix_lane = static_cast<std::uint32_t>(lane <= kLayers ? lane : kLayers) * 4u;
     // the block's fills, addressed by 32-bit offsets (the builder bounds a block's bytes)
     const rsrc_t re = make_rsrc(static_cast<const char *>(a.stream_entries) + static_cast<std::uint64_t>(blk_first) * kFillBytes,
                                 (blk_end - blk_first) * kFillBytes);
@@ -571,22 +577,26 @@ __global__ __launch_bounds__(kStreamWaves * kWave) void qcsr_spmm_stream(QcsrArg
     uint4 *sp = &sh.stage[wave][grp][0];
     const int cols = static_cast<int>(a.cols);
 
+    // The wave's fills are contiguous through all its parts, so the fill words load three
+    // fills ahead without a restart at a part boundary. Each part's index entries (one per
+    // lane, lanes 0 .. kLayers) load one part ahead, under the part before.
+    std::uint32_t nb = __builtin_amdgcn_raw_buffer_load_b32(rx, ix_lane, 0, 0);
+    std::uint32_t f = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(nb, 0)) & kFillMask;
+    FillWord<kWide> q0 = load_fill<kWide>(re, (f - blk_first) * kFillBytes + lane_off);
+    FillWord<kWide> q1 = load_fill<kWide>(re, (f + 1u - blk_first) * kFillBytes + lane_off);
+    FillWord<kWide> q2 = load_fill<kWide>(re, (f + 2u - blk_first) * kFillBytes + lane_off);
     for (int p = 0; p < parts; ++p) {
         const int lo = (static_cast<int>(a.first_part) + p) * kPartGenes;
         const int hi = lo + kPartGenes < cols ? lo + kPartGenes : cols;
-        const std::uint32_t *wx = ix + static_cast<std::uint64_t>(p) * kStreamSlots + wave * kLayers;
+        __syncthreads();  // every wave is done reading part p - 1
+        load_part<kPolicy, kWaves, StreamShared, false>(sh, a, lo, hi, wave, lane, tid);
         std::uint32_t b[kLayers + 1];
 #pragma unroll
-        for (int k = 0; k <= kLayers; ++k) b[k] = __builtin_amdgcn_readfirstlane(wx[k]);
-        const std::uint32_t s_all = b[0] & kFillMask;
-        // the wave's first three fills of the part load behind the part copy
-        FillWord<kWide> q0 = load_fill<kWide>(re, (s_all - blk_first) * kFillBytes + lane_off);
-        FillWord<kWide> q1 = load_fill<kWide>(re, (s_all + 1u - blk_first) * kFillBytes + lane_off);
-        FillWord<kWide> q2 = load_fill<kWide>(re, (s_all + 2u - blk_first) * kFillBytes + lane_off);
-        __syncthreads();  // every wave is done reading part p - 1
-        load_part<kPolicy, kWaves>(sh, a, lo, hi, wave, lane, tid);
+        for (int k = 0; k <= kLayers; ++k) b[k] = __builtin_amdgcn_readlane(nb, k);
+        // the next part's entries (past the wave's last part: the entry after it, or zeros)
+        nb = __builtin_amdgcn_raw_buffer_load_b32(rx, static_cast<std::uint32_t>((p + 1) * kLayers) * 4u + ix_lane, 0, 0);
+        __builtin_amdgcn_s_waitcnt(0x0f71);  // vmcnt(1): the part copy and older loads; not the entries above
         __syncthreads();
-        std::uint32_t f = s_all;
 #pragma unroll
         for (int l = 0; l < kLayers; ++l) {
             const std::uint32_t e_l = b[l + 1] & kFillMask;

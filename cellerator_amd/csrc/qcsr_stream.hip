@@ -3,21 +3,27 @@
 // rearranged once per structure into the order the row-group walk consumes them
 // (qcsr_spmm_stream in qcsr_parts.hip), so the walk loads them instead of finding them.
 //
-// Geometry (qcsr_common.hpp): blocks of 1,024 rows; in each block the rows are ranked by
-// tail length (descending, ties by row) and ranks 8s .. 8s + 7 form row set s, dealt to the
-// 16 waves in snake order (set s -> layer s / 16), which is how the part walk balances its
-// waves. For gene part p and layer (wave w, layer l) the 8 rows' runs in the part are
-// r_0 .. r_7; the layer gets ceil(max r_g / 16) fills of 128 entries, entry k of group g's
-// run at fill k / 16, slot g * 16 + k % 16; unused slots hold the pad gene (the zero
+// Geometry (qcsr_common.hpp): the rows are sorted by tail length over the whole matrix
+// (descending, ties by row); sets of 8 consecutive rows of that order are dealt round-robin
+// to blocks of 1,024 rows, so each set's rows end their runs together and every block holds
+// the same mix of lengths. In each block the sets go, heaviest first, to the least-loaded of
+// the 16 waves with a layer left (rank_slot), which is how the part walk balances the waves
+// it synchronizes at every part. For gene part p and layer (wave w, layer l) the 8 rows' runs in
+// the part are r_0 .. r_7; the layer gets ceil(max r_g / 16) fills of 128 entries, entry k of
+// group g's run at fill k / 16, slot g * 16 + k % 16; unused slots hold the pad gene (the zero
 // weight row, value 0; of the parity opposite to the paired group's entry at that step).
 // Each group's run is stored even genes first in even groups and odd genes first in odd
-// groups (the LDS bank half of a weight row is its gene's parity).
+// groups (the LDS bank half of a weight row is its gene's parity). Fills are stored in
+// (block, wave, part, layer) order: a wave's fills are one contiguous run across all parts,
+// so the walk's fill prefetch continues through the part boundaries.
 //
-// Building: plan (slot rows and each layer's fill count and last step count), an exclusive
-// scan of the counts into the fill index, then the fill. The plan and the fill walk each
-// row the same way (a run is the entries from the cursor while the gene is below the
-// part's end), so a fill never exceeds its plan; a row whose genes are not non-decreasing
-// within [head, cols) -- which the columns-sorted flag promised -- is reported instead.
+// Building: sort the rows by tail length, plan (block rows, slot rows and each layer's fill
+// count and last step count), an exclusive scan of the counts into the fill index, then the
+// fill. The plan
+// and the fill walk each row the same way (a run is the entries from the cursor while the
+// gene is below the part's end), so a fill never exceeds its plan; a row whose genes are not
+// non-decreasing within [head, cols) -- which the columns-sorted flag promised -- is reported
+// instead.
 #include "qcsr_common.hpp"
 
 #include <algorithm>
@@ -25,52 +31,104 @@
 namespace cx {
 namespace {
 
-constexpr int kPlanChunk = 32;  // parts counted per pass of the plan kernel (LDS: 32 KB of runs)
+constexpr int kPlanChunk = 32;  // parts counted per pass of the plan kernel (LDS: 64 KB of runs)
 constexpr std::uint32_t kNoSlotRow = 0xffffffffu;
+constexpr std::uint32_t kLengthKeyBits = 24;  // tail lengths are sorted on 24 bits (longer ones tie)
 
 struct PlanArgs {
     const std::int32_t *row_ptr;
     const std::int32_t *col_idx;
     const std::int32_t *head_end;
+    const std::uint32_t *order;   // [rows]: rows by tail length, descending (ties by row)
     std::uint32_t rows;
     std::uint32_t cols;
     std::uint32_t first_part;
     std::uint32_t parts;          // parts in the stream
     std::uint32_t *slot_rows;     // [blocks][kStreamRows]
-    std::uint32_t *counts;        // [blocks * parts * kStreamSlots + 1]: fills per layer and part (last: 0)
-    std::uint8_t *lasts;          // [blocks * parts * kStreamSlots]: step count of the last fill (0: none)
+    std::uint32_t *counts;        // [blocks * kStreamWaves * parts * kStreamLayers + 1], (block, wave, part,
+                                  // layer) order: fills per layer and part (last: 0)
+    std::uint8_t *lasts;          // same order: step count of the last fill (0: none)
     std::uint32_t *error;         // [0]: a row not sorted within [head, cols); [1]: a block's fills reach 4 GiB
 };
 
-// Ranks the block's rows by tail length and records the row of every slot.
-__device__ __forceinline__ std::uint32_t rank_slot(int *len, std::uint32_t *slot_row, const PlanArgs &a,
-                                                   std::uint32_t first, int tid) {
-    const std::uint32_t row = first + static_cast<std::uint32_t>(tid);
-    len[tid] = row < a.rows ? a.row_ptr[row + 1] - a.head_end[row] : -1;
+// Position of (block, wave, part, layer) in the fill index: a wave's layers of all parts
+// are consecutive.
+__device__ __forceinline__ std::uint64_t index_pos(std::uint32_t block, int wave, std::uint32_t part,
+                                                   std::uint32_t parts, int layer) {
+    return ((static_cast<std::uint64_t>(block) * kStreamWaves + wave) * parts + part) * kStreamLayers + layer;
+}
+
+// Sort keys of the rows: 2^24 - 1 - tail length (saturated), so an ascending stable sort gives
+// descending lengths, ties by row.
+__global__ __launch_bounds__(256) void tail_length_keys_kernel(const std::int32_t *row_ptr, const std::int32_t *head_end,
+                                                               std::uint32_t rows, std::uint32_t *keys,
+                                                               std::uint32_t *ids) {
+    const std::uint32_t r = blockIdx.x * 256u + threadIdx.x;
+    if (r >= rows) return;
+    const std::int64_t len = static_cast<std::int64_t>(row_ptr[r + 1]) - head_end[r];
+    constexpr std::int64_t kMax = (std::int64_t{1} << kLengthKeyBits) - 1;
+    keys[r] = static_cast<std::uint32_t>(kMax - (len < 0 ? 0 : (len > kMax ? kMax : len)));
+    ids[r] = r;
+}
+
+// The block's rows and the row of every slot. The sorted order is cut into sets of 8
+// consecutive rows (nearly equal tail lengths, so a layer's 8 runs end together), dealt
+// round-robin to the blocks (set S -> block S % blocks, local set S / blocks): every block
+// holds the same mix of lengths. Inside the block the rows are ranked by tail length (ties by
+// local position), ranks 8s .. 8s + 7 form set s, and the sets go, heaviest first, to the
+// least-loaded wave with a layer left (ties: the lower wave), each wave's layers in the order
+// its sets arrive, so the waves carry about equal work into every part barrier.
+struct RankShared {
+    int len[kStreamRows];             // tail length by local position (-1: empty)
+    int by_rank[kStreamRows];         // tail length by rank
+    int set_slot[kStreamSlots];       // wave * kStreamLayers + layer of set s
+    std::uint32_t slot_row[kStreamRows];
+    long long wave_load[kStreamWaves];
+    int wave_used[kStreamWaves];
+};
+
+__device__ __forceinline__ std::uint32_t rank_slot(RankShared &r, const PlanArgs &a, std::uint32_t block,
+                                                   std::uint32_t blocks, int tid) {
+    const std::uint64_t at = (static_cast<std::uint64_t>(tid / 8) * blocks + block) * 8u + static_cast<std::uint64_t>(tid % 8);
+    const std::uint32_t row = at < a.rows ? a.order[at] : a.rows;
+    r.len[tid] = row < a.rows ? a.row_ptr[row + 1] - a.head_end[row] : -1;
     __syncthreads();
-    const int my = len[tid];
+    const int my = r.len[tid];
     int rank = 0;
     for (int u = 0; u < kStreamRows; ++u) {
-        const int v = len[u];
+        const int v = r.len[u];
         rank += v > my || (v == my && u < tid) ? 1 : 0;
     }
-    const int set = rank / 8, g = rank % 8;
-    const int round = set / kStreamWaves, pos = set % kStreamWaves;
-    const int w = (round & 1) != 0 ? kStreamWaves - 1 - pos : pos;
-    const int slot = (w * kStreamLayers + round) * 8 + g;
-    slot_row[slot] = row < a.rows ? row : kNoSlotRow;
+    r.by_rank[rank] = my;
     __syncthreads();
-    return slot_row[tid];  // thread tid now works for slot tid
+    if (tid == 0) {
+        for (int w = 0; w < kStreamWaves; ++w) {
+            r.wave_load[w] = 0;
+            r.wave_used[w] = 0;
+        }
+        for (int s = 0; s < kStreamSlots; ++s) {  // set loads are non-increasing in s
+            long long load = 0;
+            for (int k = 0; k < 8; ++k) load += r.by_rank[s * 8 + k] > 0 ? r.by_rank[s * 8 + k] : 0;
+            int best = -1;
+            for (int w = 0; w < kStreamWaves; ++w)
+                if (r.wave_used[w] < kStreamLayers && (best < 0 || r.wave_load[w] < r.wave_load[best])) best = w;
+            r.set_slot[s] = best * kStreamLayers + r.wave_used[best];
+            ++r.wave_used[best];
+            r.wave_load[best] += load;
+        }
+    }
+    __syncthreads();
+    r.slot_row[r.set_slot[rank / 8] * 8 + rank % 8] = row < a.rows ? row : kNoSlotRow;
+    __syncthreads();
+    return r.slot_row[tid];  // thread tid now works for slot tid
 }
 
 __global__ __launch_bounds__(kStreamRows) void stream_plan_kernel(PlanArgs a) {
-    __shared__ int len[kStreamRows];
-    __shared__ std::uint32_t slot_row[kStreamRows];
+    __shared__ RankShared rs;
     __shared__ std::uint16_t runs[kPlanChunk][kStreamRows];
     const int tid = static_cast<int>(threadIdx.x);
     const std::uint32_t block = blockIdx.x;
-    const std::uint32_t first = block * kStreamRows;
-    const std::uint32_t row = rank_slot(len, slot_row, a, first, tid);
+    const std::uint32_t row = rank_slot(rs, a, block, gridDim.x, tid);
     a.slot_rows[static_cast<std::uint64_t>(block) * kStreamRows + tid] = row;
 
     std::int64_t cur = 0, end = 0;
@@ -102,7 +160,7 @@ __global__ __launch_bounds__(kStreamRows) void stream_plan_kernel(PlanArgs a) {
             int m = 0;
 #pragma unroll
             for (int g = 0; g < 8; ++g) m = max(m, static_cast<int>(runs[c][s * 8 + g]));
-            const std::uint64_t k = (static_cast<std::uint64_t>(block) * a.parts + c0 + c) * kStreamSlots + s;
+            const std::uint64_t k = index_pos(block, s / kStreamLayers, c0 + c, a.parts, s % kStreamLayers);
             const int fills = (m + 15) / 16;
             a.counts[k] = static_cast<std::uint32_t>(fills);
             a.lasts[k] = static_cast<std::uint8_t>(fills == 0 ? 0 : m - 16 * (fills - 1));
@@ -168,7 +226,7 @@ __global__ __launch_bounds__(kStreamRows) void stream_fill_kernel(FillArgs a) {
         while (stop < end && a.col_idx[stop] < hi) ++stop;
         if (stop == cur) continue;
         const std::uint32_t fill0 =
-            a.index[(static_cast<std::uint64_t>(block) * a.parts + p) * kStreamSlots + layer_slot] & kFillMask;
+            a.index[index_pos(block, layer_slot / kStreamLayers, p, a.parts, layer_slot % kStreamLayers)] & kFillMask;
         std::uint32_t k = 0;
         for (int pass = 0; pass < 2; ++pass) {
             for (std::int64_t e = cur; e < stop; ++e) {
@@ -215,7 +273,7 @@ constexpr std::uint64_t align256(std::uint64_t b) { return (b + 255u) & ~std::ui
 
 struct PlanSizes {
     std::uint64_t n;  // fill-index entries before the sentinel
-    std::uint64_t error, slot_rows, index, counts, lasts, scan, total;
+    std::uint64_t error, slot_rows, index, counts, lasts, scan, rows4, sort, total;
     std::uint32_t blocks, parts;
 };
 
@@ -232,7 +290,9 @@ PlanSizes plan_sizes(const cx_qcsr_matrix *m, const cx_qcsr_hybrid_layout *L) {
     s.counts = align256((s.n + 1u) * 4u);
     s.lasts = align256(s.n + 1u);
     s.scan = align256(scan_workspace_bytes(s.n + 1u));
-    s.total = s.error + s.slot_rows + s.index + s.counts + s.lasts + s.scan;
+    s.rows4 = align256(static_cast<std::uint64_t>(m->rows) * 4u);  // keys, ids, sorted keys, order
+    s.sort = align256(sort_pairs_workspace_bytes(m->rows, kLengthKeyBits));
+    s.total = s.error + s.slot_rows + s.index + s.counts + s.lasts + s.scan + 4u * s.rows4 + s.sort;
     return s;
 }
 
@@ -294,8 +354,21 @@ extern "C" int cx_qcsr_tail_plan(const cx_qcsr_matrix *m, const cx_qcsr_hybrid_l
     auto *lasts = reinterpret_cast<std::uint8_t *>(base + off);
     off += sz.lasts;
     void *scan_ws = base + off;
+    off += sz.scan;
+    auto *keys = reinterpret_cast<std::uint32_t *>(base + off);
+    auto *ids = reinterpret_cast<std::uint32_t *>(base + off + sz.rows4);
+    auto *keys_sorted = reinterpret_cast<std::uint32_t *>(base + off + 2u * sz.rows4);
+    auto *order = reinterpret_cast<std::uint32_t *>(base + off + 3u * sz.rows4);
+    void *sort_ws = base + off + 4u * sz.rows4;
 
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    // rows by tail length over the whole matrix: blocks of similar rows, the longest first
+    hipLaunchKernelGGL(tail_length_keys_kernel, dim3((m->rows + 255u) / 256u), dim3(256), 0, s, m->row_ptr,
+                       layout->head_end, m->rows, keys, ids);
+    rc = check_launch("cx_qcsr_tail_plan");
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    rc = sort_pairs(keys, ids, keys_sorted, order, m->rows, kLengthKeyBits, sort_ws, sz.sort, s);
+    if (rc != CX_STATUS_SUCCESS) return rc;
     // error words, and the sentinel count that the scan turns into the total
     hipLaunchKernelGGL(fill_pattern_kernel, dim3(1), dim3(64), 0, s, error, std::uint64_t{4}, 0u);
     hipLaunchKernelGGL(fill_pattern_kernel, dim3(1), dim3(64), 0, s, counts + sz.n, std::uint64_t{1}, 0u);
@@ -303,6 +376,7 @@ extern "C" int cx_qcsr_tail_plan(const cx_qcsr_matrix *m, const cx_qcsr_hybrid_l
     pa.row_ptr = m->row_ptr;
     pa.col_idx = m->col_idx;
     pa.head_end = layout->head_end;
+    pa.order = order;
     pa.rows = m->rows;
     pa.cols = m->cols;
     pa.first_part = layout->head_cols / kStreamPartGenes;

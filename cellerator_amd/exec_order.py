@@ -185,8 +185,8 @@ def tail_prepare(p: HybridProjection, stream=None) -> N.CxQcsrTailStream:
 
 def tail_arrays(p: HybridProjection):
     """(slot_rows [blocks, block_rows] int32 (u32 bits), fill_index [blocks * parts *
-    block_rows / 8 + 1] int32, entries [fills, 128] int16 or int32) of the prepared tail
-    stream, as device views."""
+    block_rows / 8 + 1] int32 in (block, wave, part, layer) order, entries [fills, 128] int16
+    or int32) of the prepared tail stream, as device views."""
     ts = p.tail
     plan, entries = p.tail_storage
 

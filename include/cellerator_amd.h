@@ -1463,10 +1463,13 @@ int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *a, const cx_qcsr_hybrid_layout
 
 /* ---- prepared tail stream ----------------------------------------------------------------
  * The entries of every row from its first tail entry (layout.head_end) on, rearranged once
- * per structure into the order the row-group walk consumes them: blocks of 1,024 rows ranked
- * by tail length into 16 waves x 8 layers x 8 rows; per gene part of 1,024 and layer, the 8
- * rows' runs as fills of 16 steps x 8 rows (group-major), padded with the zero row, each
- * row's run even genes first in even groups and odd genes first in odd groups. With the
+ * per structure into the order the row-group walk consumes them: the rows sorted by tail
+ * length over the whole matrix (descending, ties by row), sets of 8 adjacent rows dealt
+ * round-robin to blocks of 1,024 rows, each block's sets given heaviest first to the
+ * least-loaded of 16 waves (8 layers of 8 rows each); per gene part of
+ * 1,024 and layer, the 8 rows' runs as fills of 16 steps x 8 rows (group-major), padded with
+ * the zero row, each row's run even genes first in even groups and odd genes first in odd
+ * groups; fills in (block, wave, part, layer) order, so a wave's fills are contiguous. With the
  * stream the tail kernel loads its entries instead of finding them (no per-pass run count,
  * window or reload). Built in two steps because the stream's size depends on the data:
  * cx_qcsr_tail_plan (slot rows and fill index; returns the entry bytes) and
@@ -1484,8 +1487,9 @@ typedef struct cx_qcsr_tail_stream {
     uint64_t fills;         /* fills of 128 entries */
     uint64_t nnz;           /* of the matrix it was built from */
     uint32_t *slot_rows;    /* [blocks][block_rows]: row of slot (wave * layers + layer) * 8 + group, 0xffffffff none */
-    uint32_t *fill_index;   /* [blocks * parts * (block_rows / 8) + 1]: first fill of (block, part, wave, layer)
-                               in the low 28 bits, steps of its last fill - 1 in the high 4; last entry: the total */
+    uint32_t *fill_index;   /* [blocks * parts * (block_rows / 8) + 1], (block, wave, part, layer) order: first
+                               fill of the layer's part in the low 28 bits, steps of its last fill - 1 in the
+                               high 4; last entry: the total */
     void *entries;          /* [fills + 3][128] entries (set by cx_qcsr_tail_fill) */
 } cx_qcsr_tail_stream;
 

@@ -1,12 +1,14 @@
 """GPU parity of the prepared tail stream (qcsr_stream.hip) and the walk that reads it
 (qcsr_spmm_stream in qcsr_parts.hip): the slot rows, fill index and entries are bit-exact
-against a numpy restatement of the stream's definition (rank by tail length, snake-order
-layers, per-part fills of 16 steps x 8 groups, parity order within each run, pads of the
-parity opposite to the paired group's entry), and the
-product through the stream -- every code width and decode policy, with and without a dense
-head, N = 64 and 128, fused epilogues, empty rows, rows longer than a part, ragged last
-block -- matches the float64 referee of the canonical matrix; repeats are bitwise equal.
-Rows that break the sorted-columns promise are rejected when the stream is planned."""
+against a numpy restatement of the stream's definition (rows sorted by tail length over the
+whole matrix, sets of 8 adjacent rows dealt round-robin to the blocks, each block's sets
+heaviest first to the least-loaded wave, per-part fills of 16 steps x 8 groups stored in
+(block, wave, part, layer) order, parity order within each run,
+pads of the parity opposite to the paired group's entry), and the product through the stream
+-- every code width and decode policy, with and without a dense head, N = 64 and 128, fused
+epilogues, empty rows, rows longer than a part, ragged last block -- matches the float64
+referee of the canonical matrix; repeats are bitwise equal. Rows that break the
+sorted-columns promise are rejected when the stream is planned."""
 from __future__ import annotations
 
 import numpy as np
@@ -35,19 +37,34 @@ def _stream_reference(h, head_end, head, bits, LAYERS):
     runs = {}  # (block, part, slot) -> list of (local gene, code) in stored order
     counts = np.zeros(blocks * parts * SLOTS + 1, np.int64)
     lasts = np.zeros(blocks * parts * SLOTS, np.int64)
+
+    def pos(b, p, ls):  # (block, wave, part, layer) order
+        return ((b * WAVES + ls // LAYERS) * parts + p) * LAYERS + ls % LAYERS
+
+    # rows by tail length over the whole matrix (descending; saturated at 2^24 - 1; ties by row);
+    # sets of 8 adjacent rows dealt round-robin to the blocks
+    tail_len = np.array([int(h["row_ptr"][r + 1]) - int(head_end[r]) for r in range(rows)], np.int64)
+    by_length = np.argsort((1 << 24) - 1 - np.clip(tail_len, 0, (1 << 24) - 1), kind="stable")
     for b in range(blocks):
         lens = np.full(ROWS_PER_BLOCK, -1, np.int64)
+        block_rows = np.full(ROWS_PER_BLOCK, rows, np.int64)
         for t in range(ROWS_PER_BLOCK):
-            r = b * ROWS_PER_BLOCK + t
-            if r < rows:
-                lens[t] = int(h["row_ptr"][r + 1]) - int(head_end[r])
+            at = ((t // 8) * blocks + b) * 8 + t % 8
+            if at < rows:
+                block_rows[t] = by_length[at]
+                lens[t] = tail_len[block_rows[t]]
         order = sorted(range(ROWS_PER_BLOCK), key=lambda t: (-lens[t], t))
+        # sets (ranks 8s .. 8s + 7) heaviest first to the least-loaded wave with a layer left
+        load, used, set_slot = [0] * WAVES, [0] * WAVES, []
+        for st in range(SLOTS):
+            sl = sum(max(int(lens[t]), 0) for t in order[st * 8:st * 8 + 8])
+            w = min((wv for wv in range(WAVES) if used[wv] < LAYERS), key=lambda wv: (load[wv], wv))
+            set_slot.append(w * LAYERS + used[w])
+            used[w] += 1
+            load[w] += sl
         for rank, t in enumerate(order):
-            s, g = divmod(rank, 8)
-            rnd, pos = divmod(s, WAVES)
-            w = WAVES - 1 - pos if rnd & 1 else pos
-            r = b * ROWS_PER_BLOCK + t
-            slot_rows[b, (w * LAYERS + rnd) * 8 + g] = r if r < rows else 0xFFFFFFFF
+            r = int(block_rows[t])
+            slot_rows[b, set_slot[rank // 8] * 8 + rank % 8] = r if r < rows else 0xFFFFFFFF
         for slot in range(ROWS_PER_BLOCK):
             r = int(slot_rows[b, slot])
             if r == 0xFFFFFFFF:
@@ -67,7 +84,7 @@ def _stream_reference(h, head_end, head, bits, LAYERS):
                     pref = g & 1
                     run.sort(key=lambda x: 0 if (x[0] & 1) == pref else 1)  # stable: gene order within a parity
                     m = max(m, len(run))
-                k = (b * parts + p) * SLOTS + ls
+                k = pos(b, p, ls)
                 counts[k] = (m + 15) // 16
                 lasts[k] = 0 if m == 0 else m - 16 * (counts[k] - 1)
     starts = np.zeros_like(counts)
@@ -79,7 +96,7 @@ def _stream_reference(h, head_end, head, bits, LAYERS):
     entries = np.full((total, 128), pad, np.uint32 if wide else np.uint16)
     for (b, p, slot), run in runs.items():
         ls, g = divmod(slot, 8)
-        f0 = int(starts[(b * parts + p) * SLOTS + ls])
+        f0 = int(starts[pos(b, p, ls)])
         for k, (gene, code) in enumerate(run):
             entries[f0 + k // 16, g * 16 + k % 16] = gene | (code << (16 if wide else 11))
     # a pad beside a stored entry of the paired group (2i, 2i + 1) at the same step takes the
