@@ -223,6 +223,11 @@ class CxQcsrTailStream(C.Structure):
                 ("slot_rows", p_void), ("fill_index", p_void), ("entries", p_void)]
 
 
+class CxQcsrExecInfo(C.Structure):
+    _fields_ = [("rows", u32), ("cols", u32), ("bits", u32), ("head_cols", u32), ("nnz", u64),
+                ("tail_fills", u64), ("persistent_bytes", u64), ("head_form", u32), ("reserved", u32)]
+
+
 # ---- public context ABI structs (include/Cellerator/abi.h layout) ----
 class CelleratorExecutionConfig(C.Structure):
     _fields_ = [("version", u32), ("size", C.c_size_t), ("device", i32), ("stream", p_void),
@@ -334,6 +339,14 @@ ENGINE_SIGNATURES = {
                                     C.POINTER(CxQcsrTailStream), p_void, u64, p_void]),
     "cx_qcsr_spmm_fwd_hybrid": (C.c_int, [C.POINTER(CxQcsrMatrix), C.POINTER(CxQcsrHybridLayout), p_void, i64,
                                           i64, p_void, i64, C.POINTER(CxSpmmEpilogue), p_void, u64, p_void]),
+    "cx_qcsr_exec_prepare": (C.c_int, [C.POINTER(CxQcsrMatrix), u32, C.POINTER(p_void), p_void]),
+    "cx_qcsr_exec_query": (C.c_int, [p_void, C.POINTER(CxQcsrExecInfo)]),
+    "cx_qcsr_exec_workspace_bytes": (C.c_int, [p_void, i64, C.POINTER(u64)]),
+    "cx_qcsr_exec_spmm": (C.c_int, [p_void, p_void, i64, i64, p_void, i64, C.POINTER(CxSpmmEpilogue), p_void, u64,
+                                    p_void]),
+    "cx_qcsr_exec_destroy": (C.c_int, [p_void]),
+    "cx_qcsr_exec_workspace_for": (C.c_int, [u32, u32, u32, i64, C.POINTER(u64)]),
+    "cx_cpbp_reduction_validate": (C.c_int, [C.POINTER(CxCpbpReductionView)]),
     "cx_cpbp_builder_create": (C.c_int, [C.POINTER(CxCpbpPlan), C.POINTER(CxCpbpCsr),
                                          C.POINTER(CxCpbpOrderConfig), u32, C.POINTER(p_void)]),
     "cx_cpbp_builder_requirements": (C.c_int, [p_void, C.POINTER(CxCpbpTileRequirements)]),

@@ -51,6 +51,7 @@ ENGINE_SOURCES = [
     "cpe2.cpp",
     "qcsr_hybrid.hip",
     "qcsr_stream.hip",
+    "qcsr_exec.hip",
 ]
 SYNTH_SOURCES = ["synth.hip"]
 

@@ -5,6 +5,7 @@
 #include "cpmath_backend.hh"
 
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <mutex>
 
@@ -33,6 +34,19 @@ struct qcsr_prepared {
     u64 generation = 0u;
 };
 
+// The execution-order candidate's persistent state (prepare_quantized_csr_execution_order):
+// the engine's prepared projection and what it was built from.
+struct exec_prepared {
+    cx_qcsr_exec_projection *projection = nullptr;
+    const int32_t *row_ptr = nullptr;     // structure
+    const int32_t *col_idx = nullptr;
+    const void *values = nullptr;         // codes and metadata of the value plane
+    const void *scales = nullptr;
+    const void *offsets = nullptr;
+    u64 generation = 0u;
+    u64 persistent_bytes = 0u;
+};
+
 // Physical preparations of a Blocked-ELL projection (prepare_blocked_ell_state).
 struct bell_prepared {
     const void *weights = nullptr;        // W the panel was packed from
@@ -42,11 +56,19 @@ struct bell_prepared {
     cx_bell_groups groups{};
 };
 
+// The validated reduction contract of a CP-BP projection (prepare_cpbp_state).
+struct cpbp_prepared {
+    bool validated = false;
+    cx_cpbp_tiles tiles{};  // value pointer cleared: values travel in the plane
+};
+
 struct projection_state {
     bool live = false;
     projection_declaration declaration{};
     qcsr_prepared qcsr{};
+    exec_prepared exec{};
     bell_prepared bell{};
+    cpbp_prepared cpbp{};
     execution::operand_axis_contract inputs[3]{};  // sparse, dense, bias (epilogue only)
     execution::operand_axis_contract outputs[1]{};
     execution::output_axis_contract orders[2]{};
@@ -135,6 +157,11 @@ bool supports_blocked_ell(const core::numeric_policy &n) noexcept {
     return multiply_numeric(n) && plain_storage(n.sparse_storage)
         && plain_storage(n.dense_storage)
         && n.quantization == core::quantization_granularity::none;
+}
+
+bool supports_quantized_csr_execution_order(const core::numeric_policy &n) noexcept {
+    return multiply_numeric(n) && n.dense_storage == numeric_type::f16
+        && n.sparse_storage == numeric_type::u8 && n.quantization == core::quantization_granularity::module;
 }
 
 bool supports_cpbp(const core::numeric_policy &n) noexcept {
@@ -256,14 +283,24 @@ const char *bind_epilogue(const core::prepared_operation &p, const projection_de
 
 // ---- run functions --------------------------------------------------------------------
 
-core::operation_status run_quantized_csr(const core::prepared_operation &p,
-                                         const execution::launch_bindings &l) noexcept {
-    const projection_state *s = state_of(p);
-    if (s == nullptr) return fail(code::execution_failed, "prepared operation has no live projection state");
-    const projection_declaration &d = s->declaration;
-    const void *view = physical_view(*s, l, sizeof(cx_qcsr_matrix));
+// The launch operands of either quantized CSR candidate: the sparse view completed from the
+// value plane (decode policy, codes, metadata, the prepared column order and pairs), W, Y and
+// the epilogue. Returns a failure status, or ok.
+struct qcsr_launch {
+    cx_qcsr_matrix a{};
+    const execution::value_plane *plane = nullptr;
+    execution::dense_tensor_view w{};
+    execution::dense_tensor_view y{};
+    cx_spmm_epilogue ep{};
+    bool sorted = false;
+};
+
+core::operation_status bind_quantized_csr(const projection_state &s, const core::prepared_operation &p,
+                                          const execution::launch_bindings &l, qcsr_launch *out) noexcept {
+    const projection_declaration &d = s.declaration;
+    const void *view = physical_view(s, l, sizeof(cx_qcsr_matrix));
     if (view == nullptr) return bad_launch("sparse operand does not carry the prepared quantized CSR view");
-    cx_qcsr_matrix a;
+    cx_qcsr_matrix &a = out->a;
     std::memcpy(&a, view, sizeof(a));
     if (a.rows != d.rows || a.cols != d.cols || a.bits != p.projection.variant
         || a.nnz != d.structure.logical_edge_count)
@@ -273,9 +310,10 @@ core::operation_status run_quantized_csr(const core::prepared_operation &p,
         return bad_launch("values and quantization metadata travel in the value plane");
     if (a.flags != 0u)
         return bad_launch("view flags are established by prepare_quantized_csr_state, not the caller");
-    const execution::value_plane *plane = value_plane_of(*s, p, l);
+    const execution::value_plane *plane = value_plane_of(s, p, l);
     if (plane == nullptr || plane->element_count != a.nnz)
         return bad_launch("one value plane of the structure with nnz elements is required");
+    out->plane = plane;
     const execution::quantization_descriptor &q = plane->quantization;
     if (a.bits != 0u) {
         if (q.kind != execution::quantization_kind::per_module || q.group_count != a.cols
@@ -286,7 +324,7 @@ core::operation_status run_quantized_csr(const core::prepared_operation &p,
         a.packed_values = static_cast<const uint8_t *>(plane->values);
         a.column_scales = static_cast<const float *>(q.scales);
         a.column_offsets = static_cast<const float *>(q.offsets);
-        const qcsr_prepared &pre = s->qcsr;
+        const qcsr_prepared &pre = s.qcsr;
         if (pre.pairs != nullptr && pre.generation == plane->generation.value
             && pre.scales == q.scales && pre.offsets == q.offsets) {
             a.decode_policy = CX_DECODE_PER_GENE_AFFINE_PAIRS;
@@ -299,25 +337,71 @@ core::operation_status run_quantized_csr(const core::prepared_operation &p,
         a.values = plane->values;
         a.value_dtype = engine_dtype(plane->numeric.storage);
     }
-    const execution::dense_tensor_view &w = l.inputs[1].storage.dense;
-    execution::dense_tensor_view y = l.outputs[0].storage.dense;
+    out->w = l.inputs[1].storage.dense;
+    out->y = l.outputs[0].storage.dense;
     if (l.inputs[1].kind != execution::operand_kind::dense_tensor
-        || !dense_shape(w, p.numeric.dense_storage, 2u, d.cols, d.output_columns, l))
+        || !dense_shape(out->w, p.numeric.dense_storage, 2u, d.cols, d.output_columns, l))
         return bad_launch("W must be a row-major [genes x N] tensor of the dense storage type");
-    if (!dense_shape(y, numeric_type::f32, 2u, d.rows, d.output_columns, l))
+    if (!dense_shape(out->y, numeric_type::f32, 2u, d.rows, d.output_columns, l))
         return bad_launch("Y must be a row-major f32 [cells x N] tensor");
-    cx_spmm_epilogue ep;
-    if (const char *why = bind_epilogue(p, d, l, y, &ep)) return bad_launch(why);
-    const bool sorted = s->qcsr.sorted && s->qcsr.row_ptr == a.row_ptr && s->qcsr.col_idx == a.col_idx;
-    if (sorted) a.flags = CX_QCSR_COLUMNS_SORTED;
-    const int rc = cx_qcsr_spmm_fwd_epilogue(&a, w.data, engine_dtype(w.value_type), w.stride[0],
-                                             d.output_columns, static_cast<float *>(y.data),
-                                             y.stride[0], &ep, l.stream.stream);
+    if (const char *why = bind_epilogue(p, d, l, out->y, &out->ep)) return bad_launch(why);
+    out->sorted = s.qcsr.sorted && s.qcsr.row_ptr == a.row_ptr && s.qcsr.col_idx == a.col_idx;
+    if (out->sorted) a.flags = CX_QCSR_COLUMNS_SORTED;
+    return {};
+}
+
+// The row-group (or row-wave) kernels on the bound CSR.
+core::operation_status launch_row_group(const projection_state &s, qcsr_launch &q,
+                                        const execution::launch_bindings &l) noexcept {
+    const int rc = cx_qcsr_spmm_fwd_epilogue(&q.a, q.w.data, engine_dtype(q.w.value_type), q.w.stride[0],
+                                             s.declaration.output_columns, static_cast<float *>(q.y.data),
+                                             q.y.stride[0], &q.ep, l.stream.stream);
+    return rc == CX_STATUS_SUCCESS ? core::operation_status{} : engine_failed(rc);
+}
+
+core::operation_status run_quantized_csr(const core::prepared_operation &p,
+                                         const execution::launch_bindings &l) noexcept {
+    const projection_state *s = state_of(p);
+    if (s == nullptr) return fail(code::execution_failed, "prepared operation has no live projection state");
+    qcsr_launch q;
+    const core::operation_status bound = bind_quantized_csr(*s, p, l, &q);
+    if (!bound) return bound;
+    const core::operation_status st = launch_row_group(*s, q, l);
+    if (!st) return st;
+    const bool pairs = q.a.decode_policy == CX_DECODE_PER_GENE_AFFINE_PAIRS;
+    dispatched = q.a.bits == 0u ? "qcsr:plain"
+        : pairs ? (q.sorted ? "qcsr:pairs+sorted" : "qcsr:pairs")
+                : (q.sorted ? "qcsr:gene-affine+sorted" : "qcsr:gene-affine");
+    return {};
+}
+
+// The execution-order candidate: the prepared projection when it was built from exactly the
+// bound structure, codes and metadata, else the row-group kernel on the bound operands.
+core::operation_status run_quantized_csr_execution_order(const core::prepared_operation &p,
+                                                         const execution::launch_bindings &l) noexcept {
+    const projection_state *s = state_of(p);
+    if (s == nullptr) return fail(code::execution_failed, "prepared operation has no live projection state");
+    qcsr_launch q;
+    const core::operation_status bound = bind_quantized_csr(*s, p, l, &q);
+    if (!bound) return bound;
+    const exec_prepared &x = s->exec;
+    const execution::quantization_descriptor &qd = q.plane->quantization;
+    const bool current = x.projection != nullptr && x.row_ptr == q.a.row_ptr && x.col_idx == q.a.col_idx
+        && x.values == q.plane->values && x.scales == qd.scales && x.offsets == qd.offsets
+        && x.generation == q.plane->generation.value;
+    const bool launchable = q.w.value_type == numeric_type::f16
+        && (reinterpret_cast<std::uintptr_t>(q.y.data) & 15u) == 0u && (q.y.stride[0] * 4) % 16 == 0
+        && q.y.data != q.w.data;
+    if (!current || !launchable) {
+        const core::operation_status st = launch_row_group(*s, q, l);
+        if (st) dispatched = "qcsr:execution-order->row-group";
+        return st;
+    }
+    const int rc = cx_qcsr_exec_spmm(x.projection, q.w.data, q.w.stride[0], s->declaration.output_columns,
+                                     static_cast<float *>(q.y.data), q.y.stride[0], &q.ep, l.workspace.data,
+                                     l.workspace.bytes, l.stream.stream);
     if (rc != CX_STATUS_SUCCESS) return engine_failed(rc);
-    const bool pairs = a.decode_policy == CX_DECODE_PER_GENE_AFFINE_PAIRS;
-    dispatched = a.bits == 0u ? "qcsr:plain"
-        : pairs ? (sorted ? "qcsr:pairs+sorted" : "qcsr:pairs")
-                : (sorted ? "qcsr:gene-affine+sorted" : "qcsr:gene-affine");
+    dispatched = "qcsr:execution-order";
     return {};
 }
 
@@ -335,8 +419,8 @@ core::operation_status run_blocked_ell(const core::prepared_operation &p,
     if (a.values != nullptr || a.packed_values != nullptr || a.column_scales != nullptr
         || a.column_offsets != nullptr || a.row_offsets != nullptr)
         return bad_launch("Blocked-ELL values travel in the value plane");
-    if (a.value_layout_flags != 0u || a.reserved != 0u)
-        return bad_launch("the projection-order value plane is row-major [rows x ell_cols]");
+    if ((a.value_layout_flags != 0u && a.value_layout_flags != CX_BELL_BLOCK_MAJOR_VALUES) || a.reserved != 0u)
+        return bad_launch("the projection-order value plane is row-major [rows x ell_cols] or block-major");
     const execution::value_plane *plane = value_plane_of(*s, p, l);
     if (plane == nullptr || plane->layout != execution::value_layout_kind::projection_local_order
         || plane->quantization.kind != execution::quantization_kind::none
@@ -374,8 +458,11 @@ core::operation_status run_blocked_ell(const core::prepared_operation &p,
                 : cx_bell_spmm_fwd_packed_epilogue(&a, panel, d.output_columns,
                                                    static_cast<float *>(y.data), y.stride[0], &ep,
                                                    l.stream.stream);
-        dispatched = grouped ? (prepacked ? "bell:grouped+panel" : "bell:grouped+repack")
-                             : (prepacked ? "bell:mfma+panel" : "bell:mfma+repack");
+        const bool block_major = a.value_layout_flags == CX_BELL_BLOCK_MAJOR_VALUES;
+        dispatched = grouped ? (prepacked ? (block_major ? "bell:grouped+panel+block-major" : "bell:grouped+panel")
+                                          : (block_major ? "bell:grouped+repack+block-major" : "bell:grouped+repack"))
+                             : (prepacked ? (block_major ? "bell:mfma+panel+block-major" : "bell:mfma+panel")
+                                          : (block_major ? "bell:mfma+repack+block-major" : "bell:mfma+repack"));
     } else {
         rc = cx_bell_spmm_fwd_epilogue(&a, w.data, engine_dtype(w.value_type), w.stride[0],
                                        d.output_columns, static_cast<float *>(y.data),
@@ -398,6 +485,13 @@ core::operation_status run_cpbp(const core::prepared_operation &p,
         || t.nnz_count != d.structure.logical_edge_count)
         return bad_launch("CP-BP tile view differs from the declared projection");
     if (t.values != nullptr) return bad_launch("CP-BP values travel in the value plane");
+    const bool checked = s->cpbp.validated;
+    if (checked) {
+        cx_cpbp_tiles bound = t;  // the plane supplies values and their type
+        bound.value_dtype = 0u;
+        if (std::memcmp(&bound, &s->cpbp.tiles, sizeof(bound)) != 0)
+            return bad_launch("CP-BP tile view differs from the reduction view validated by prepare_cpbp_state");
+    }
     const execution::value_plane *plane = value_plane_of(*s, p, l);
     if (plane == nullptr || plane->layout != execution::value_layout_kind::projection_local_order
         || plane->quantization.kind != execution::quantization_kind::none
@@ -415,7 +509,7 @@ core::operation_status run_cpbp(const core::prepared_operation &p,
     const int rc = cx_cpbp_reduce(&t, static_cast<const float *>(w.data), d.cols,
                                   static_cast<float *>(y.data), d.rows, l.stream.stream);
     if (rc != CX_STATUS_SUCCESS) return engine_failed(rc);
-    dispatched = "cpbp";
+    dispatched = checked ? "cpbp:checked" : "cpbp:unchecked";
     return {};
 }
 
@@ -425,6 +519,11 @@ projection_state *find_live(execution::projection_handle handle) noexcept {
     for (projection_state &s : projections)
         if (s.live && execution::same_handle(s.declaration.key.runtime, handle)) return &s;
     return nullptr;
+}
+
+// Matrix-core head width of the execution-order candidate.
+std::uint32_t head_genes_of(const projection_declaration &d) noexcept {
+    return d.head_genes != 0u ? d.head_genes : 2048u;
 }
 
 u64 mfma_panel_bytes(const projection_declaration &d) noexcept {
@@ -485,6 +584,17 @@ core::operation_status prepare(
     u64 workspace = 0u;
     if (reduce) {
         run = run_cpbp;
+    } else if (core::same_stable_id(candidate.identity, quantized_csr_execution_order_candidate_id)) {
+        if (projection.variant == 0u || numeric.dense_storage != numeric_type::f16
+            || d.output_columns % 64u != 0u || d.output_columns > 256u)
+            return fail(code::unsupported_numeric_policy,
+                "the execution-order candidate needs quantized codes, f16 W and N of 64, 128, 192 or 256");
+        if (cx_qcsr_exec_workspace_for(d.rows, d.cols, head_genes_of(d), d.output_columns, &workspace)
+            != CX_STATUS_SUCCESS)
+            return fail(code::unsupported_problem, "execution-order workspace is not defined for this shape");
+        if (policy.persistent_memory_limit != 0u && state->exec.persistent_bytes > policy.persistent_memory_limit)
+            return fail(code::capability_rejected, "candidate exceeds memory policy");
+        run = run_quantized_csr_execution_order;
     } else if (projection.kind == core::projection_kind::blocked_ell) {
         const bool mfma = mfma_eligible(d, numeric);
         kernel = mfma ? blocked_ell_mfma_kernel_id : blocked_ell_generic_kernel_id;
@@ -522,7 +632,7 @@ core::operation_candidate candidate(core::stable_id id, const char *name,
                                     core::operation_kind operation,
                                     core::projection_kind projection,
                                     core::numeric_support_function supports,
-                                    u64 transient_bytes) noexcept {
+                                    u64 transient_bytes, std::uint32_t extra_flags = 0u) noexcept {
     core::operation_candidate c{};
     c.identity = id;
     c.name = name;
@@ -531,8 +641,10 @@ core::operation_candidate candidate(core::stable_id id, const char *name,
     c.backend = core::backend_kind::native_direct;
     // Fixed per-row / per-tile summation order, and launches that neither allocate nor
     // synchronize.
-    c.capability_flags = core::candidate_deterministic | core::candidate_graph_capture;
-    c.persistent_bytes = 0u;  // no device-resident state beyond the caller's operands
+    c.capability_flags = core::candidate_deterministic | core::candidate_graph_capture | extra_flags;
+    // Device-resident state beyond the caller's operands depends on the projection: the
+    // execution-order candidate checks its prepared bytes against the policy in prepare.
+    c.persistent_bytes = 0u;
     c.transient_bytes = transient_bytes;
     c.supports_numeric = supports;
     c.prepare = prepare;
@@ -621,6 +733,8 @@ core::operation_status retire_projection(execution::projection_handle projection
     std::lock_guard<std::mutex> lock(projections_mutex);
     projection_state *s = find_live(projection);
     if (s == nullptr) return fail(code::invalid_argument, "projection is not declared");
+    if (s->exec.projection != nullptr) (void)cx_qcsr_exec_destroy(s->exec.projection);
+    s->exec = exec_prepared{};
     s->live = false;
     return {};
 }
@@ -629,6 +743,12 @@ core::operation_candidate quantized_csr_candidate() noexcept {
     return candidate(quantized_csr_candidate_id, "cellerator-amd-quantized-csr-spmm",
         core::operation_kind::sparse_dense_multiply, core::projection_kind::csr,
         supports_quantized_csr, 0u);
+}
+
+core::operation_candidate quantized_csr_execution_order_candidate() noexcept {
+    return candidate(quantized_csr_execution_order_candidate_id, "cellerator-amd-quantized-csr-execution-order",
+        core::operation_kind::sparse_dense_multiply, core::projection_kind::csr,
+        supports_quantized_csr_execution_order, 0u, core::candidate_persistent_preprocessing);
 }
 
 core::operation_candidate blocked_ell_candidate() noexcept {
@@ -686,6 +806,86 @@ core::operation_status prepare_quantized_csr_state(execution::projection_handle 
     return {};
 }
 
+core::operation_status prepare_quantized_csr_execution_order(execution::projection_handle projection,
+                                                             const cx_qcsr_matrix &structure,
+                                                             const execution::value_plane &plane,
+                                                             void *stream) noexcept {
+    std::lock_guard<std::mutex> lock(projections_mutex);
+    projection_state *s = find_live(projection);
+    if (s == nullptr) return fail(code::invalid_argument, "projection is not declared");
+    const projection_declaration &d = s->declaration;
+    if (d.key.kind != core::projection_kind::csr || d.key.variant == 0u)
+        return fail(code::unsupported_projection, "not a quantized CSR projection");
+    if (structure.rows != d.rows || structure.cols != d.cols || structure.bits != d.key.variant
+        || structure.nnz != d.structure.logical_edge_count || structure.row_ptr == nullptr
+        || structure.packed_row_ptr == nullptr || (structure.nnz != 0u && structure.col_idx == nullptr))
+        return fail(code::invalid_argument, "structure differs from the declared projection");
+    const execution::quantization_descriptor &q = plane.quantization;
+    if (!execution::same_handle(plane.structure, d.structure.identity)
+        || q.kind != execution::quantization_kind::per_module || q.group_count != d.cols
+        || q.scale_type != numeric_type::f32 || (q.offsets != nullptr && q.offset_type != numeric_type::f32)
+        || plane.values == nullptr || plane.element_count != structure.nnz)
+        return fail(code::invalid_argument, "the execution order needs the projection's codes with per-gene f32 metadata");
+    cx_qcsr_matrix a = structure;
+    a.decode_policy = CX_DECODE_PER_GENE_AFFINE;
+    a.packed_values = static_cast<const uint8_t *>(plane.values);
+    a.column_scales = static_cast<const float *>(q.scales);
+    a.column_offsets = static_cast<const float *>(q.offsets);
+    a.row_offsets = nullptr;
+    a.values = nullptr;
+    a.flags = 0u;
+    if (s->exec.projection != nullptr) (void)cx_qcsr_exec_destroy(s->exec.projection);
+    s->exec = exec_prepared{};
+    cx_qcsr_exec_projection *x = nullptr;
+    const int rc = cx_qcsr_exec_prepare(&a, head_genes_of(d), &x, stream);
+    if (rc != CX_STATUS_SUCCESS) {
+        const core::operation_status st = engine_failed(rc);
+        return {code::preparation_failed, st.binding, "execution-order preparation failed (see last_engine_error)"};
+    }
+    cx_qcsr_exec_info info{};
+    (void)cx_qcsr_exec_query(x, &info);
+    exec_prepared e{};
+    e.projection = x;
+    e.row_ptr = structure.row_ptr;
+    e.col_idx = structure.col_idx;
+    e.values = plane.values;
+    e.scales = q.scales;
+    e.offsets = q.offsets;
+    e.generation = plane.generation.value;
+    e.persistent_bytes = info.persistent_bytes;
+    s->exec = e;
+    return {};
+}
+
+std::uint64_t execution_order_persistent_bytes(execution::projection_handle projection) noexcept {
+    std::lock_guard<std::mutex> lock(projections_mutex);
+    const projection_state *s = find_live(projection);
+    return s != nullptr ? s->exec.persistent_bytes : 0u;
+}
+
+core::operation_status prepare_cpbp_state(execution::projection_handle projection,
+                                          const cx_cpbp_reduction_view &view) noexcept {
+    std::lock_guard<std::mutex> lock(projections_mutex);
+    projection_state *s = find_live(projection);
+    if (s == nullptr) return fail(code::invalid_argument, "projection is not declared");
+    const projection_declaration &d = s->declaration;
+    if (d.key.kind != core::projection_kind::native_row_masked)
+        return fail(code::unsupported_projection, "not a CP-BP projection");
+    if (view.tiles.row_count != d.rows || view.tiles.feature_count != d.cols
+        || view.tiles.nnz_count != d.structure.logical_edge_count)
+        return fail(code::invalid_argument, "reduction view differs from the declared projection");
+    const int rc = cx_cpbp_reduction_validate(&view);
+    if (rc != CX_STATUS_SUCCESS) {
+        const core::operation_status st = engine_failed(rc);
+        return {code::preparation_failed, st.binding, "reduction contract rejected (see last_engine_error)"};
+    }
+    s->cpbp.validated = true;
+    s->cpbp.tiles = view.tiles;
+    s->cpbp.tiles.values = nullptr;
+    s->cpbp.tiles.value_dtype = 0u;
+    return {};
+}
+
 core::operation_status prepare_blocked_ell_state(execution::projection_handle projection,
                                                  const cx_bell_matrix &structure,
                                                  const uint16_t *weights, int64_t weights_ld,
@@ -723,14 +923,20 @@ const char *last_dispatch() noexcept { return dispatched; }
 namespace {
 
 // Peaks of one MI355X and the fraction of them each kernel family reaches on the
-// benchmark configurations (measured: quantized CSR row-group kernel about 35% of the
-// non-packed VALU peak, Blocked-ELL grouped matrix-core kernel about 35% of HBM, CP-BP
-// about 32% of HBM).
+// benchmark configurations (measured with bench.py on one MI355X: the quantized CSR
+// row-group kernel at 35% of the non-packed fp32 VALU peak (C3: 6.99 ms for 2*nnz*N flops);
+// the execution-order path at 74% of it (C3: 3.31 ms, head on the matrix cores plus the
+// tail stream) after a preparation of about 0.074 ns per stored entry (C3: 111 ms); the
+// Blocked-ELL grouped matrix-core kernel at about 35% of HBM; CP-BP at about 32% of HBM).
 constexpr double kHbmBytesPerNs = 8000.0;         // 8 TB/s
 constexpr double kValuFlopsPerNs = 78600.0;        // fp32, non-packed
 constexpr double kMfmaFlopsPerNs = 2500000.0;      // bf16 dense
 constexpr double kQcsrEfficiency = 0.35, kBellEfficiency = 0.35, kCpbpEfficiency = 0.32;
+constexpr double kQcsrExecEfficiency = 0.74;
+constexpr double kQcsrExecPrepareNsPerEntry = 0.074;
 constexpr double kLaunchNs = 4000.0;               // launch and synchronization overhead
+
+double align256d(double bytes) { return std::ceil(bytes / 256.0) * 256.0; }
 
 bool finite_shape(const workload_shape &w) { return w.rows != 0u && w.cols != 0u; }
 
@@ -754,6 +960,24 @@ bool analytical_costs(core::stable_id candidate, const workload_shape &w,
         p.backend_prepare_ns = (nnz * 4.0 + rows * 8.0) / kHbmBytesPerNs + kLaunchNs;
         p.persistent_bytes = static_cast<std::uint64_t>(bytes - rows * n * 4.0 - cols * n * 2.0);
         p.transient_bytes = 0u;
+    } else if (core::same_stable_id(candidate, quantized_csr_execution_order_candidate_id)) {
+        if (w.out_cols == 0u || w.bits == 0u) return false;
+        const double head = static_cast<double>(std::min<std::uint64_t>(
+            w.head_genes != 0u ? w.head_genes : 2048u, w.cols / 1024u * 1024u));
+        const double flops = 2.0 * nnz * n;
+        const double code_bytes = nnz * w.bits / 8.0;
+        const double structure_bytes = (rows + 1.0) * 8.0 + nnz * 4.0 + code_bytes + cols * 8.0;
+        p.kernel_ns = flops / kValuFlopsPerNs / kQcsrExecEfficiency;
+        // popularity order, relabel, dense head, tail stream (plan and fill)
+        p.backend_prepare_ns = nnz * kQcsrExecPrepareNsPerEntry + 4.0 * kLaunchNs;
+        // head: one byte per (row, head gene) in table form (codes and presence bits in words
+        // form); tail stream: about 1.3 padded entries per tail entry, taken as half the entries
+        const double head_bytes = w.bits <= 4u ? rows * head : rows * head * (w.bits + 1.0) / 8.0;
+        const double stream_bytes = 0.5 * nnz * 1.3 * (w.bits == 8u ? 4.0 : 2.0) + rows * 28.0;
+        p.persistent_bytes = static_cast<std::uint64_t>(structure_bytes + head_bytes + stream_bytes + cols * 12.0);
+        // W in execution order, the head's partial sums, the head's weight panel
+        p.transient_bytes = static_cast<std::uint64_t>(align256d(cols * n * 2.0) + align256d(rows * 256.0)
+                                                       + align256d(head * n * 2.0));
     } else if (core::same_stable_id(candidate, blocked_ell_candidate_id)) {
         if (w.out_cols == 0u || w.block_size == 0u || w.ell_columns == 0u) return false;
         const double slots = rows * static_cast<double>(w.ell_columns);

@@ -4,9 +4,17 @@
 // prepares and runs through prepare_candidate / run_prepared_operation
 // (src/compute/math/operation_core/operation_core.cc:136-242).
 //
-//   quantized_csr_candidate   sparse_dense_multiply    x csr               x native_direct
-//   blocked_ell_candidate     sparse_dense_multiply    x blocked_ell       x native_direct
-//   cpbp_candidate            weighted_relation_reduce x native_row_masked x native_direct
+//   quantized_csr_candidate                  sparse_dense_multiply    x csr               x native_direct
+//   quantized_csr_execution_order_candidate  sparse_dense_multiply    x csr               x native_direct
+//   blocked_ell_candidate                    sparse_dense_multiply    x blocked_ell       x native_direct
+//   cpbp_candidate                           weighted_relation_reduce x native_row_masked x native_direct
+//
+// The two quantized CSR candidates compute the same product. The first runs on the CSR as
+// bound (the row-group kernel); the second on a prepared execution-order projection of it
+// (popularity order, a dense head on the matrix cores and a prepared tail stream, built once by
+// prepare_quantized_csr_execution_order and kept as persistent state), which is about twice as
+// fast per launch at the benchmark shapes but costs a one-time preparation and persistent
+// device memory; the planner weighs the two through their phase costs and the reuse it is told.
 //
 // This file compiles against the reference's public headers (types and inline validators
 // only) and links against libcellerator_amd.so, whose C-ABI (include/cellerator_amd.h)
@@ -60,6 +68,7 @@ inline constexpr std::uint16_t physical_view_schema = 1u;
 
 // Candidate identities; kernel identities of the prepared dispatch.
 inline constexpr core::stable_id quantized_csr_candidate_id{0x4358414d44514353ull, 1u};
+inline constexpr core::stable_id quantized_csr_execution_order_candidate_id{0x4358414d44514353ull, 2u};
 inline constexpr core::stable_id blocked_ell_candidate_id{0x4358414d4442454cull, 1u};
 inline constexpr core::stable_id cpbp_candidate_id{0x4358414d44435042ull, 1u};
 inline constexpr core::stable_id blocked_ell_mfma_kernel_id{0x4358414d4442454cull, 2u};
@@ -88,6 +97,8 @@ struct projection_declaration {
     std::uint32_t cols = 0u;                    // genes
     std::uint32_t output_columns = 0u;          // N (multiply); 0 for the reduction
     std::uint32_t block_size = 0u;              // Blocked-ELL block edge; 0 otherwise
+    std::uint32_t head_genes = 0u;              // execution-order candidate: genes on the matrix cores, a
+                                                // multiple of 1,024 (0: 2,048)
 };
 
 core::operation_status declare_projection(const projection_declaration &declaration) noexcept;
@@ -110,6 +121,24 @@ core::operation_status prepare_quantized_csr_state(execution::projection_handle 
                                                    const execution::value_plane *plane,
                                                    float *pairs, void *stream) noexcept;
 
+// Persistent state of the execution-order candidate for a declared quantized CSR projection:
+// the engine's prepared execution-order projection (cx_qcsr_exec_prepare) of `structure` with
+// the codes and per-gene f32 metadata of `plane`, head width from the declaration. A one-time
+// preparation: it allocates the projection's device memory (held until the projection is
+// retired or prepared again), enqueues work on `stream` and synchronizes it. Launches of the
+// execution-order candidate whose sparse view carries the same structure arrays and whose value
+// plane has the same generation, codes and metadata pointers run the prepared path
+// (last_dispatch "qcsr:execution-order"); any other launch -- new values, no preparation yet,
+// f32 W or an output the prepared path cannot write -- runs the row-group kernel on the bound
+// operands ("qcsr:execution-order->row-group"), so results stay correct. Rows may repeat no
+// gene (INVALID_ARGUMENT otherwise).
+core::operation_status prepare_quantized_csr_execution_order(execution::projection_handle projection,
+                                                             const cx_qcsr_matrix &structure,
+                                                             const execution::value_plane &plane,
+                                                             void *stream) noexcept;
+// Device bytes the execution-order state of `projection` holds (0 when none).
+std::uint64_t execution_order_persistent_bytes(execution::projection_handle projection) noexcept;
+
 // Persistent state of a declared Blocked-ELL projection for the MFMA kernels (bf16 values
 // and weights, 32 x 32 blocks). A one-time preparation that synchronizes `stream`.
 //  * `panel` (device, ceil(genes/32) * 32 * N bf16, caller-owned) is packed now from
@@ -125,12 +154,22 @@ core::operation_status prepare_blocked_ell_state(execution::projection_handle pr
                                                  uint16_t *panel, const cx_bell_groups *groups,
                                                  void *stream) noexcept;
 
+// The reduction contract of a declared CP-BP projection, checked once (host only):
+// cx_cpbp_reduction_validate -- versions, numeric contract, identities including the
+// recomputed reduction identity, and the plan / order / tile domains, the checks of the
+// reference's validate_metadata (components/CellPack/src/feature_weighted_row_reduction_cuda.cu:57-136).
+// After it, a launch runs only if its tile view equals the validated view's tiles
+// ("cpbp:checked"); without it the tile view is run as bound ("cpbp:unchecked").
+core::operation_status prepare_cpbp_state(execution::projection_handle projection,
+                                          const cx_cpbp_reduction_view &view) noexcept;
+
 // Kernel form the last successful run on this thread dispatched, e.g.
-// "qcsr:pairs+sorted", "qcsr:gene-affine", "bell:grouped+panel", "bell:mfma+repack",
-// "bell:generic", "cpbp".
+// "qcsr:pairs+sorted", "qcsr:gene-affine", "qcsr:execution-order", "bell:grouped+panel",
+// "bell:mfma+repack", "bell:generic", "cpbp:checked".
 const char *last_dispatch() noexcept;
 
 core::operation_candidate quantized_csr_candidate() noexcept;
+core::operation_candidate quantized_csr_execution_order_candidate() noexcept;
 core::operation_candidate blocked_ell_candidate() noexcept;
 core::operation_candidate cpbp_candidate() noexcept;
 
@@ -154,6 +193,8 @@ struct workload_shape {
     std::uint32_t block_size = 0u;    // Blocked-ELL block edge
     std::uint64_t ell_columns = 0u;   // Blocked-ELL padded columns per row
     std::uint64_t tile_blocks = 0u;   // CP-BP (tile, block) entries
+    std::uint32_t head_genes = 0u;    // execution-order quantized CSR: matrix-core head width (0: 2,048)
+    std::uint32_t reserved = 0u;
 };
 
 // Analytical phases of `candidate` (one of the three above) on `shape`; false for an

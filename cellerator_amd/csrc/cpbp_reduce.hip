@@ -537,12 +537,10 @@ extern "C" int cx_cpbp_reduction_view_from_cpk1(const cx_cpk1_view *image, uint6
     return CX_STATUS_SUCCESS;
 }
 
-extern "C" int cx_cpbp_reduce_checked(const cx_cpbp_reduction_view *v, const float *feature_weights,
-                                      uint64_t feature_weight_capacity, float *row_values, uint64_t row_capacity,
-                                      void *stream) {
+extern "C" int cx_cpbp_reduction_validate(const cx_cpbp_reduction_view *v) {
     using namespace cx;
     clear_error();
-    if (v == nullptr) return fail(CX_STATUS_INVALID_ARGUMENT, "cx_cpbp_reduce_checked: null view");
+    if (v == nullptr) return fail(CX_STATUS_INVALID_ARGUMENT, "cx_cpbp_reduction_validate: null view");
     const cx_cpbp_tiles &t = v->tiles;
     if (v->schema_version != kReductionSchema || v->tile_schema_version != kTileSchema
         || v->plan_schema_version != kPlanSchema || v->tiles_plan_schema_version != kPlanSchema
@@ -567,5 +565,13 @@ extern "C" int cx_cpbp_reduce_checked(const cx_cpbp_reduction_view *v, const flo
         || v->order_feature_block_count != t.feature_block_count
         || v->order_row_domain_identity != v->tiles_row_domain_identity || v->order_group_width != t.tile_row_width)
         return fail(CX_STATUS_INVALID_SHAPE, "weighted-row-reduction plan, order, and tile domains disagree");
-    return cx_cpbp_reduce(&t, feature_weights, feature_weight_capacity, row_values, row_capacity, stream);
+    return CX_STATUS_SUCCESS;
+}
+
+extern "C" int cx_cpbp_reduce_checked(const cx_cpbp_reduction_view *v, const float *feature_weights,
+                                      uint64_t feature_weight_capacity, float *row_values, uint64_t row_capacity,
+                                      void *stream) {
+    const int rc = cx_cpbp_reduction_validate(v);
+    if (rc != CX_STATUS_SUCCESS) return rc;
+    return cx_cpbp_reduce(&v->tiles, feature_weights, feature_weight_capacity, row_values, row_capacity, stream);
 }

@@ -63,6 +63,13 @@ constexpr std::uint32_t kStreamPadOdd = 1025u;
 // One 64-column block of the tail through the prepared stream (fp16 weights).
 int launch_qcsr_stream(const QcsrArgs &a, std::uint32_t bits, std::uint32_t policy, hipStream_t stream);
 
+// The launch of cx_qcsr_spmm_fwd_hybrid once its operands are checked (qcsr_hybrid.hip): reads
+// the shape, code width, decode policy, flags and metadata of `m`, its structure arrays only
+// when the layout has no tail stream.
+int launch_hybrid(const cx_qcsr_matrix &m, const cx_qcsr_hybrid_layout &layout, const void *rhs, std::int64_t rhs_ld,
+                  std::int64_t out_cols, float *out, std::int64_t out_ld, const cx_spmm_epilogue *epilogue,
+                  void *workspace, std::uint64_t workspace_bytes, hipStream_t stream, const char *who);
+
 constexpr int kWavesPerBlock = 4;
 
 // Decoded value of entry `i` (global nnz index) of row `row` whose packed codes start

@@ -948,9 +948,23 @@ extern "C" int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *m, const cx_qcsr_hy
         return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd_hybrid: rhs and output must be 16-byte aligned");
     if (static_cast<const void *>(out) == rhs)
         return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd_hybrid: output aliases the rhs");
+    return launch_hybrid(*m, L, rhs, rhs_ld, out_cols, out, out_ld, epilogue, workspace, workspace_bytes,
+                         static_cast<hipStream_t>(stream), "cx_qcsr_spmm_fwd_hybrid");
+}
+
+namespace cx {
+
+// The launch behind cx_qcsr_spmm_fwd_hybrid, after its checks of the matrix, layout and
+// operands. From `m` it reads the shape, code width, decode policy, flags and metadata; the
+// structure arrays only when the layout has no tail stream.
+int launch_hybrid(const cx_qcsr_matrix &mm, const cx_qcsr_hybrid_layout &L, const void *rhs, std::int64_t rhs_ld,
+                  std::int64_t out_cols, float *out, std::int64_t out_ld, const cx_spmm_epilogue *epilogue,
+                  void *workspace, std::uint64_t workspace_bytes, hipStream_t s, const char *who) {
+    const cx_qcsr_matrix *m = &mm;
+    int rc = CX_STATUS_SUCCESS;
     if (m->rows == 0u) return CX_STATUS_SUCCESS;
     Epilogue ep;
-    rc = make_epilogue(epilogue, m->rows, out_cols, out, out_ld, &ep, "cx_qcsr_spmm_fwd_hybrid");
+    rc = make_epilogue(epilogue, m->rows, out_cols, out, out_ld, &ep, who);
     if (rc != CX_STATUS_SUCCESS) return rc;
     std::uint64_t need = 0u;
     (void)cx_qcsr_hybrid_workspace(m, L.head_cols, out_cols, &need);
@@ -988,7 +1002,6 @@ extern "C" int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *m, const cx_qcsr_hy
         a.stream_parts = ts->parts;
         a.first_part = ts->first_part;
     }
-    const hipStream_t s = static_cast<hipStream_t>(stream);
     // one 64-column block of the tail: the prepared stream, else the row-group kernel
     auto tail = [&](const QcsrArgs &b) {
         return ts != nullptr ? launch_qcsr_stream(b, m->bits, m->decode_policy, s)
@@ -1030,3 +1043,5 @@ extern "C" int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *m, const cx_qcsr_hy
     }
     return CX_STATUS_SUCCESS;
 }
+
+} // namespace cx

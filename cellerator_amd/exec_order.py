@@ -249,3 +249,66 @@ def hybrid_spmm(p: HybridProjection, w: torch.Tensor, out: Optional[torch.Tensor
         C.byref(e) if e is not None else None, ws.data_ptr() if ws is not None else None,
         ws.numel() if ws is not None else 0, _stream(stream)))
     return out
+
+
+class ExecProjection:
+    """The prepared execution-order projection of a quantized CSR (cx_qcsr_exec_prepare): the
+    engine object that owns the popularity order, the execution-order metadata, the dense head
+    and the tail stream. Launches (spmm) take canonical W and return Y in the matrix's row
+    order. The device memory is held until close() (or garbage collection)."""
+
+    def __init__(self, m: QcsrMatrix, head_cols: int = 2048, stream=None):
+        _require_cuda(m.row_ptr)
+        self._lib = N.engine()
+        self._handle = C.c_void_p()
+        d = m.descriptor()
+        N.check("cx_qcsr_exec_prepare", self._lib.cx_qcsr_exec_prepare(C.byref(d), head_cols, C.byref(self._handle),
+                                                                        _stream(stream)))
+        self.device = m.row_ptr.device
+        self.rows, self.cols = m.rows, m.cols
+        self._workspaces: dict = {}
+
+    @property
+    def handle(self) -> int:
+        return int(self._handle.value or 0)
+
+    def info(self) -> N.CxQcsrExecInfo:
+        i = N.CxQcsrExecInfo()
+        N.check("cx_qcsr_exec_query", self._lib.cx_qcsr_exec_query(self._handle, C.byref(i)))
+        return i
+
+    def workspace(self, out_cols: int) -> torch.Tensor:
+        ws = self._workspaces.get(out_cols)
+        if ws is None:
+            nbytes = C.c_uint64()
+            N.check("cx_qcsr_exec_workspace_bytes",
+                    self._lib.cx_qcsr_exec_workspace_bytes(self._handle, out_cols, C.byref(nbytes)))
+            ws = torch.empty(max(nbytes.value, 256), dtype=torch.uint8, device=self.device)
+            self._workspaces[out_cols] = ws
+        return ws
+
+    def spmm(self, w: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None, epilogue=None) -> torch.Tensor:
+        """Y = X . W (+ epilogue) for canonical F16 W [genes, N], N in 64..256 by 64."""
+        _require_cuda(w)
+        if w.dim() != 2 or w.shape[0] != self.cols or w.dtype != torch.float16 or w.stride(1) != 1:
+            raise ValueError("w must be a row-major F16 [genes, N] tensor in canonical gene order")
+        n = int(w.shape[1])
+        if out is None:
+            out = torch.empty((self.rows, n), dtype=torch.float32, device=w.device)
+        e = epilogue.descriptor(out) if epilogue is not None else None
+        ws = self.workspace(n)
+        N.check("cx_qcsr_exec_spmm", self._lib.cx_qcsr_exec_spmm(
+            self._handle, w.data_ptr(), w.stride(0), n, out.data_ptr(), out.stride(0),
+            C.byref(e) if e is not None else None, ws.data_ptr(), ws.numel(), _stream(stream)))
+        return out
+
+    def close(self) -> None:
+        if self._handle:
+            self._lib.cx_qcsr_exec_destroy(self._handle)
+            self._handle = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

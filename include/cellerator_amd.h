@@ -1241,6 +1241,9 @@ int cx_cpbp_reduction_view_from_cpk1(const cx_cpk1_view *image, uint64_t feature
 int cx_cpbp_reduce_checked(const cx_cpbp_reduction_view *view, const float *feature_weights,
                            uint64_t feature_weight_capacity, float *row_values, uint64_t row_capacity,
                            void *stream);
+/* The checks of cx_cpbp_reduce_checked alone (host only, same statuses), for callers that
+ * validate a view once and launch cx_cpbp_reduce on its tiles many times. */
+int cx_cpbp_reduction_validate(const cx_cpbp_reduction_view *view);
 
 /* ---- execution feature order: packed dense operand and execution-order CSR ---------------
  * feature_permutation[e] = the canonical gene at execution position e (cx_cpbp_plan's
@@ -1505,6 +1508,49 @@ int cx_qcsr_tail_plan(const cx_qcsr_matrix *a, const cx_qcsr_hybrid_layout *layo
  * and sets out->entries. Stream-ordered, no synchronization. */
 int cx_qcsr_tail_fill(const cx_qcsr_matrix *a, const cx_qcsr_hybrid_layout *layout, cx_qcsr_tail_stream *stream_out,
                       void *entries, uint64_t entry_bytes, void *stream);
+
+/* ---- prepared execution-order projection ------------------------------------------------
+ * One object that owns everything the prepared path reads: the popularity order of the genes
+ * (cx_popularity_order), the per-gene metadata in that order, the dense head layout
+ * (cx_qcsr_hybrid_prepare) and the tail stream (cx_qcsr_tail_plan / cx_qcsr_tail_fill) of the
+ * matrix relabelled into that order. Built once per structure and code generation from the
+ * canonical matrix `a` (quantized codes of 1/2/4/8 bits, any decode policy, each gene at most
+ * once per row; rows need not be sorted); the relabelled column indices and codes exist only
+ * during the build. Launches take the CANONICAL operands: W [cols x out_cols] F16 in canonical
+ * gene order (row stride rhs_ld) is gathered into execution order in the workspace, then the
+ * head (matrix cores) and the tail stream run; Y rows are the matrix's rows. Same values and
+ * sums as cx_qcsr_spmm_fwd_hybrid on the relabelled matrix with the same head width.
+ * head_cols: a multiple of 1,024 (capped at cols rounded down to 1,024; 0: no head).
+ * cx_qcsr_exec_prepare allocates device memory and synchronizes `stream`; cx_qcsr_exec_spmm
+ * allocates nothing and does not synchronize (workspace: 256-byte aligned,
+ * cx_qcsr_exec_workspace_bytes). A projection may be launched from several streams at once
+ * with separate workspaces. Engine addition: the reference's quantized CSR projection has no
+ * prepared execution-order form; this is the persistent state behind the CP-Math
+ * execution-order candidate (cellerator_amd/cpmath/cpmath_backend.hh). */
+typedef struct cx_qcsr_exec_projection cx_qcsr_exec_projection;
+typedef struct cx_qcsr_exec_info {
+    uint32_t rows;
+    uint32_t cols;
+    uint32_t bits;
+    uint32_t head_cols;         /* the head width used */
+    uint64_t nnz;
+    uint64_t tail_fills;        /* fills of 128 entries in the tail stream */
+    uint64_t persistent_bytes;  /* device bytes the projection holds */
+    uint32_t head_form;         /* CX_HEAD_FORM_* */
+    uint32_t reserved;
+} cx_qcsr_exec_info;
+int cx_qcsr_exec_prepare(const cx_qcsr_matrix *a, uint32_t head_cols, cx_qcsr_exec_projection **out, void *stream);
+int cx_qcsr_exec_query(const cx_qcsr_exec_projection *p, cx_qcsr_exec_info *info);
+int cx_qcsr_exec_workspace_bytes(const cx_qcsr_exec_projection *p, int64_t out_cols, uint64_t *bytes);
+/* The same from the shape alone, before a projection exists (head_cols as passed to prepare). */
+int cx_qcsr_exec_workspace_for(uint32_t rows, uint32_t cols, uint32_t head_cols, int64_t out_cols, uint64_t *bytes);
+/* Y = act(alpha * (A . W) + beta * C + bias) with canonical W; out_cols 64..256 by 64, Y 16-byte
+ * aligned with a 16-byte multiple row stride; deterministic. */
+int cx_qcsr_exec_spmm(const cx_qcsr_exec_projection *p, const void *rhs, int64_t rhs_ld, int64_t out_cols,
+                      float *out, int64_t out_ld, const cx_spmm_epilogue *epilogue, void *workspace,
+                      uint64_t workspace_bytes, void *stream);
+/* Frees the projection's device memory (NULL is accepted). No launch on it may be in flight. */
+int cx_qcsr_exec_destroy(cx_qcsr_exec_projection *p);
 
 /* N = 1 CSR comparator: csr_spmv_fwd_f16_f32 (src/compute/sparse/ops/ops.hh:83-90);
  * y[r] = sum fp32(values) * x[col]. values F16 or F32. */

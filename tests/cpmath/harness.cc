@@ -9,6 +9,7 @@
 // the backend reports, mirroring tests/math_core/operation_core_test.cc:120-270.
 #include <cellerator_amd/cpmath/cpmath_backend.hh>
 
+#include <chrono>
 #include <cstdint>
 #include <cstring>
 
@@ -52,6 +53,13 @@ typedef struct h_case {
     uint32_t check_columns, repeats;
     uint16_t *panel;
     const void *groups;
+    // Quantized CSR through the execution-order candidate (exec_order != 0): 1 builds its
+    // persistent state (prepare_quantized_csr_execution_order) before the launch, 2 does not
+    // (the launch then runs the row-group kernel). head_genes goes into the declaration.
+    // CP-BP: a non-NULL reduction_view (cx_cpbp_reduction_view) is validated once
+    // (prepare_cpbp_state) before the launch.
+    uint32_t exec_order, head_genes;
+    const void *reduction_view;
 } h_case;
 
 typedef struct h_result {
@@ -62,6 +70,8 @@ typedef struct h_result {
     char message[160];
     char engine[256];
     char dispatch[64];
+    uint64_t persistent_bytes;  // execution-order state of the projection
+    double launch_ms;           // repeats > 1: wall time per launch (stream synchronized around them)
 } h_result;
 
 int h_case_size(void) { return (int)sizeof(h_case); }
@@ -126,15 +136,18 @@ extern "C" int h_run(const h_case *c, h_result *r) {
     d.cols = c->cols;
     d.output_columns = c->kind == 3 ? 0u : c->out_cols;
     d.block_size = c->block_size;
+    d.head_genes = c->head_genes;
     core::operation_status s = cp::declare_projection(d);
     if (!s) { note(r, s, true); return 1; }
 
     core::candidate_registry registry{};
-    const core::operation_candidate candidates[3] = {
-        cp::quantized_csr_candidate(), cp::blocked_ell_candidate(), cp::cpbp_candidate()};
+    const core::operation_candidate candidates[4] = {
+        cp::quantized_csr_candidate(), cp::quantized_csr_execution_order_candidate(), cp::blocked_ell_candidate(),
+        cp::cpbp_candidate()};
     for (const core::operation_candidate &candidate : candidates)
         if (core::register_candidate(&registry, candidate)) ++r->registered;
-    const core::stable_id wanted = c->kind == 1 ? cp::quantized_csr_candidate_id
+    const core::stable_id wanted = c->kind == 1
+        ? (c->exec_order != 0u ? cp::quantized_csr_execution_order_candidate_id : cp::quantized_csr_candidate_id)
         : c->kind == 2 ? cp::blocked_ell_candidate_id : cp::cpbp_candidate_id;
     const core::operation_candidate *candidate = core::find_candidate(registry, wanted);
     if (candidate == nullptr) { cp::retire_projection(d.key.runtime); return 2; }
@@ -309,6 +322,19 @@ extern "C" int h_run(const h_case *c, h_result *r) {
         r->state_status = static_cast<int32_t>(st.code);
         if (!st) { note(r, st, false); cp::retire_projection(d.key.runtime); return 0; }
     }
+    if (c->kind == 1 && c->exec_order == 1u) {
+        const core::operation_status st = cp::prepare_quantized_csr_execution_order(
+            d.key.runtime, *static_cast<const cx_qcsr_matrix *>(c->view), plane, c->stream);
+        r->state_status = static_cast<int32_t>(st.code);
+        r->persistent_bytes = cp::execution_order_persistent_bytes(d.key.runtime);
+        if (!st) { note(r, st, false); cp::retire_projection(d.key.runtime); return 0; }
+    }
+    if (c->kind == 3 && c->reduction_view != nullptr) {
+        const core::operation_status st = cp::prepare_cpbp_state(
+            d.key.runtime, *static_cast<const cx_cpbp_reduction_view *>(c->reduction_view));
+        r->state_status = static_cast<int32_t>(st.code);
+        if (!st) { note(r, st, false); cp::retire_projection(d.key.runtime); return 0; }
+    }
     if (c->kind == 2 && (c->panel != nullptr || c->groups != nullptr)) {
         const core::operation_status st = cp::prepare_blocked_ell_state(
             d.key.runtime, *static_cast<const cx_bell_matrix *>(c->view),
@@ -318,10 +344,19 @@ extern "C" int h_run(const h_case *c, h_result *r) {
         if (!st) { note(r, st, false); cp::retire_projection(d.key.runtime); return 0; }
     }
 
+    // Several repeats are timed (stream synchronized before and after them); a single launch
+    // is not, so it may run inside a HIP graph capture.
     const uint32_t repeats = c->repeats == 0u ? 1u : c->repeats;
+    if (repeats > 1u) (void)cx_stream_synchronize(c->stream);
+    const auto t0 = std::chrono::steady_clock::now();
     for (uint32_t i = 0; i < repeats; ++i) {
         s = core::run_prepared_operation(prepared, launch);
         if (!s) break;
+    }
+    if (repeats > 1u) {
+        (void)cx_stream_synchronize(c->stream);
+        r->launch_ms =
+            std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() / repeats;
     }
     note(r, s, false);
     std::strncpy(r->dispatch, cp::last_dispatch(), sizeof(r->dispatch) - 1u);

@@ -22,7 +22,7 @@ B_INVALID_STREAM, B_WORKSPACE, B_STRUCTURE_COUNT, B_ALIAS = 7, 8, 11, 16
 # numeric_type (include/Cellerator/execution/operands.hh:9-20)
 NT_U8, NT_F16, NT_BF16, NT_F32 = 2, 6, 7, 8
 # candidate_capability_flag
-DETERMINISTIC, GRAPH_CAPTURE = 1, 2
+DETERMINISTIC, GRAPH_CAPTURE, PERSISTENT_PREPROCESSING = 1, 2, 4
 
 KIND_QCSR, KIND_BELL, KIND_CPBP = 1, 2, 3
 MUTATIONS = dict(none=0, stale_epoch=1, structure_count=2, short_workspace=4,
@@ -50,7 +50,8 @@ class HCase(C.Structure):
                 ("fused", C.c_uint32), ("epilogue_kind", C.c_uint32), ("affine", C.c_uint32),
                 ("reserved3", C.c_uint32), ("bias", p), ("alpha", C.c_float),
                 ("beta", C.c_float), ("pairs", p), ("check_columns", C.c_uint32),
-                ("repeats", C.c_uint32), ("panel", p), ("groups", p)]
+                ("repeats", C.c_uint32), ("panel", p), ("groups", p), ("exec_order", C.c_uint32),
+                ("head_genes", C.c_uint32), ("reduction_view", p)]
 
 
 class HResult(C.Structure):
@@ -60,7 +61,7 @@ class HResult(C.Structure):
                 ("capability_flags", C.c_uint32), ("registered", C.c_uint32),
                 ("state_status", C.c_int32), ("reserved", C.c_int32),
                 ("message", C.c_char * 160), ("engine", C.c_char * 256),
-                ("dispatch", C.c_char * 64)]
+                ("dispatch", C.c_char * 64), ("persistent_bytes", C.c_uint64), ("launch_ms", C.c_double)]
 
 
 _lib = None

@@ -11,8 +11,9 @@ import pytest
 ROOT = Path(__file__).resolve().parents[2]
 HARNESS = ROOT / "oracle" / "_ref" / "libplanner_harness.so"
 
-QCSR, BELL, CPBP = 1, 2, 4  # candidate_mask bits
+QCSR, BELL, CPBP, QCSR_EXEC = 1, 2, 4, 8  # candidate_mask bits
 QCSR_ID = (0x4358414D44514353, 1)
+QCSR_EXEC_ID = (0x4358414D44514353, 2)
 BELL_ID = (0x4358414D4442454C, 1)
 CPBP_ID = (0x4358414D44435042, 1)
 # candidate_rejection / selection_source / cache_state / planner_status_code

@@ -31,7 +31,7 @@ typedef struct ph_case {
     uint32_t out_cols, bits, value_bytes, block_size;
     uint64_t ell_columns, tile_blocks;
     uint32_t problem_kind;   // 1 sparse_dense_multiply, 2 weighted_relation_reduce
-    uint32_t candidate_mask; // bit 0 quantized CSR, bit 1 Blocked-ELL, bit 2 CP-BP
+    uint32_t candidate_mask; // bit 0 quantized CSR, bit 1 Blocked-ELL, bit 2 CP-BP, bit 3 execution-order CSR
     uint32_t deterministic, graph_capture_required;
     uint64_t max_persistent, max_transient;
     uint32_t shortlist, max_measurements;
@@ -123,10 +123,11 @@ pl::planning_keys make_keys(const ph_case *c) {
 
 extern "C" int ph_plan(const ph_case *c, ph_result *r) {
     std::memset(r, 0, sizeof(*r));
-    static const core::operation_candidate ops[3] = {cp::quantized_csr_candidate(), cp::blocked_ell_candidate(),
-                                                     cp::cpbp_candidate()};
-    const core::projection_kind kinds[3] = {core::projection_kind::csr, core::projection_kind::blocked_ell,
-                                            core::projection_kind::native_row_masked};
+    static const core::operation_candidate ops[4] = {cp::quantized_csr_candidate(), cp::blocked_ell_candidate(),
+                                                     cp::cpbp_candidate(),
+                                                     cp::quantized_csr_execution_order_candidate()};
+    const core::projection_kind kinds[4] = {core::projection_kind::csr, core::projection_kind::blocked_ell,
+                                            core::projection_kind::native_row_masked, core::projection_kind::csr};
     cp::workload_shape shape{};
     shape.rows = c->rows;
     shape.cols = c->cols;
@@ -137,12 +138,12 @@ extern "C" int ph_plan(const ph_case *c, ph_result *r) {
     shape.block_size = c->block_size;
     shape.ell_columns = c->ell_columns;
     shape.tile_blocks = c->tile_blocks;
-    pl::planner_candidate candidates[3]{};
+    pl::planner_candidate candidates[4]{};
     uint32_t count = 0u;
-    for (uint32_t i = 0; i < 3u; ++i) {
+    for (uint32_t i = 0; i < 4u; ++i) {
         if ((c->candidate_mask & (1u << i)) == 0u) continue;
         const core::projection_key key{{0x100u + i, 0x200u + i}, {0x300u + i, 1u}, kinds[i], cp::physical_view_schema,
-                                       i == 0u ? c->bits : 0u};
+                                       i == 0u || i == 3u ? c->bits : 0u};
         cp::workload_shape s = shape;
         if (i != 0u) s.out_cols = i == 2u ? 0u : shape.out_cols;
         if (!cp::planner_candidate_for(ops[i], key, s, &candidates[count])) {

@@ -5,7 +5,12 @@ from __future__ import annotations
 import numpy as np
 
 REL_TOL = 1e-4  # north_star: within 1e-4 relative (fp32 accumulation, reordered sums)
-ABS_TOL_SCALED = 1e-4  # times sum |x||w| of the element (reordered-summation bound)
+# Times sum |x||w| of the element: fp32 sums of n terms in any order stay within about
+# n * 2^-24 * sum |x||w| (and typically sqrt(n) * 2^-24); 2^-20 covers the row lengths of the
+# benchmark configurations (a few thousand terms) with room, and is the bound bench.py checks
+# its timed outputs against. Losing one part of the matrix-core head's three-part split (an
+# error of about 2^-12 of every head term) fails it at these row lengths.
+ABS_TOL_SCALED = 2.0 ** -20
 
 
 def random_csr(rng: np.random.Generator, rows: int, cols: int, mean_nnz: float,

@@ -62,7 +62,7 @@ CASES = {"qcsr": qcsr_case, "bell": bell_case, "cpbp": cpbp_case}
 @pytest.mark.parametrize("kind", CASES)
 def test_registration_and_prepare(kind):
     r = H.run(CASES[kind](), "retired_projection")
-    assert r.registered == 3
+    assert r.registered == 4
     assert r.capability_flags == H.DETERMINISTIC | H.GRAPH_CAPTURE
     assert r.prepare_status == H.OK, r.message
     # the projection was retired after prepare: the borrowed state is gone, run refuses
@@ -180,3 +180,34 @@ def test_affine_effect_needs_both_scalars():
     r = H.run(_fused(bell_case(), 0, affine=True), "missing_scalars")
     assert r.prepare_status == H.OK
     assert (r.status, r.binding) == (H.INVALID_LAUNCH, H.B_MISSING_SCALAR)
+
+
+def test_execution_order_candidate_prepare():
+    """The execution-order quantized CSR candidate: registered beside the others with the
+    persistent-preprocessing capability, prepared with the engine's kernel identity and the
+    workspace its launch needs (W in execution order, the head's partial sums and panel,
+    cx_qcsr_exec_workspace_for); f32 W, plain values and widths other than 64..256 by 64
+    are numeric or shape rejections at prepare."""
+    want = C.c_uint64()
+    assert N.engine().cx_qcsr_exec_workspace_for(1000, 3000, 1024, 128, C.byref(want)) == 0
+    c = qcsr_case(rows=1000, cols=3000, n=128)
+    c.exec_order, c.head_genes = 2, 1024
+    c.workspace, c.workspace_bytes = FAKE + 0x100000, want.value
+    r = H.run(c, "retired_projection")
+    assert r.registered == 4
+    assert r.capability_flags == H.DETERMINISTIC | H.GRAPH_CAPTURE | H.PERSISTENT_PREPROCESSING
+    assert r.prepare_status == H.OK, r.message
+    assert (r.kernel_low, r.kernel_high) == (0x4358414D44514353, 2)
+    assert r.workspace_bytes == want.value
+    assert want.value >= 3000 * 128 * 2 + 1000 * 256 + 1024 * 128 * 2
+    assert r.status == H.EXECUTION_FAILED  # retired after prepare: run refuses before any launch
+    # the default head width is 2,048 genes (capped at the genes rounded down to 1,024)
+    c = qcsr_case(rows=1000, cols=3000, n=64)
+    c.exec_order = 2
+    r = H.run(c, "retired_projection")
+    assert N.engine().cx_qcsr_exec_workspace_for(1000, 3000, 2048, 64, C.byref(want)) == 0
+    assert r.workspace_bytes == want.value
+    for case in (qcsr_case(dense=H.NT_F32), qcsr_case(bits=0), qcsr_case(n=96)):
+        case.exec_order = 2
+        r = H.run(case)
+        assert r.prepare_status == H.UNSUPPORTED_NUMERIC, r.message

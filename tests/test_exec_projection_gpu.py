@@ -1,0 +1,224 @@
+"""GPU parity of the prepared execution-order projection (cx_qcsr_exec_*, qcsr_exec.hip) --
+the path bench.py times and the CP-Math execution-order candidate runs -- and of that
+candidate through the reference's own operation core.
+
+* The projection's product equals, bitwise, the step-by-step path (popularity order,
+  relabelled matrix, dense head, tail stream: exec_order.py) with the same head width, and
+  matches the float64 referee of the canonical matrix (canonical W in, canonical rows out).
+* At the benchmark configurations' shapes: C3-generated rows (4-bit codes, 33,538 genes)
+  with the 2,048-gene head and the tail stream over three full 1,024-row blocks and a ragged
+  one, N = 64 and 128; C2-generated rows (8-bit codes) with the 6,144-gene head.
+* Through register -> prepare -> run_prepared_operation: bitwise equal to the direct call,
+  with and without a fused epilogue; without its persistent state the candidate runs the
+  row-group kernel (bitwise equal to it); its launch costs no more than the direct call.
+* A row that repeats a gene is rejected when the projection is prepared."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from tests.cpmath import harness as H
+from tests.helpers import check_against_referee, qcsr_to_host, to_device_qcsr
+from tests.test_cpmath_gpu import _time_ms, qcsr_case
+from tests.test_hybrid_gpu import _exec, _referee, _skewed
+
+pytestmark = pytest.mark.gpu
+
+
+def _stepwise(m, w, head):
+    """The same product by the step-by-step path of exec_order.py."""
+    from cellerator_amd.exec_order import hybrid_prepare, hybrid_spmm, pack_rows
+    mx, order = _exec(m)
+    return hybrid_spmm(hybrid_prepare(mx, head, stream_tail=True), pack_rows(order, w))
+
+
+def _referee_of(oracle, m, w):
+    h = qcsr_to_host(m)
+    return oracle.qcsr_spmm_referee(m.bits, 1 if m.decode_policy == 3 else m.decode_policy, m.rows, m.cols,
+                                    h["row_ptr"], h["packed_row_ptr"], h["col_idx"], h["packed"],
+                                    h["scales"] if m.decode_policy != 3 else h["scales"].reshape(-1, 2)[:, 0].copy(),
+                                    h["offsets"] if m.decode_policy != 3 else h["scales"].reshape(-1, 2)[:, 1].copy(),
+                                    h["row_offsets"], w.cpu().numpy())
+
+
+@pytest.mark.parametrize("bits,policy,head", [(4, 1, 2048), (8, 1, 1024), (2, 2, 2048), (4, 3, 1024), (1, 1, 0)])
+def test_projection_equals_stepwise_path_and_referee(oracle, bits, policy, head):
+    import torch
+
+    from cellerator_amd import qcsr_pack_gene_affine
+    from cellerator_amd.exec_order import ExecProjection
+    rng = np.random.default_rng(5000 + 10 * bits + policy + head)
+    fx = _skewed(oracle, rng, 2300, 3100, bits, policy)
+    m = to_device_qcsr(fx)
+    if policy == 3:
+        m = qcsr_pack_gene_affine(m)
+    w = torch.from_numpy((rng.standard_normal((3100, 64)) * 0.02).astype(np.float16)).cuda()
+    p = ExecProjection(m, head)
+    info = p.info()
+    assert info.head_cols == head and info.rows == 2300 and info.persistent_bytes > 0
+    y = p.spmm(w)
+    y2 = p.spmm(w)
+    step = _stepwise(m, w, head)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), y2.view(torch.int32))
+    assert torch.equal(y.view(torch.int32), step.view(torch.int32))
+    ref, mag = _referee(oracle, dict(fx, policy=1 if policy == 3 else policy), w.cpu().numpy())
+    check_against_referee(oracle, ref, mag, y.cpu().numpy())
+    p.close()
+
+
+@pytest.mark.parametrize("n", [64, 128])
+def test_c3_rows_at_the_benchmark_form(oracle, n):
+    """C3-generated rows as bench.py runs them: 2,048 head genes on the matrix cores, the rest
+    through the tail stream, three full 1,024-row blocks of the stream and a ragged one."""
+    import torch
+
+    from cellerator_amd import qcsr_pack_gene_affine
+    from cellerator_amd.exec_order import ExecProjection
+    from cellerator_amd.synth import C3, dense_normal, generate_qcsr
+    m = qcsr_pack_gene_affine(generate_qcsr(C3.scaled(3 * 1024 + 500)))
+    w = dense_normal((m.cols, n), 0.02, torch.float16, seed=11 + n)
+    p = ExecProjection(m, 2048)
+    info = p.info()
+    assert info.head_cols == 2048 and info.head_form == 2 and info.tail_fills > 0
+    y = p.spmm(w)
+    step = _stepwise(m, w, 2048)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), step.view(torch.int32))
+    ref, mag = _referee_of(oracle, m, w)
+    check_against_referee(oracle, ref, mag, y.cpu().numpy())
+    p.close()
+
+
+def test_c2_rows_at_the_benchmark_form(oracle):
+    """C2-generated rows (8-bit codes, the words form of the head) with the 6,144-gene head
+    bench.py runs at C2 and the tail stream."""
+    import torch
+
+    from cellerator_amd import qcsr_pack_gene_affine
+    from cellerator_amd.exec_order import ExecProjection
+    from cellerator_amd.synth import C2, dense_normal, generate_qcsr
+    m = qcsr_pack_gene_affine(generate_qcsr(C2.scaled(2 * 1024 + 300)))
+    w = dense_normal((m.cols, 64), 0.02, torch.float16, seed=23)
+    p = ExecProjection(m, 6144)
+    assert p.info().head_form == 1
+    y = p.spmm(w)
+    step = _stepwise(m, w, 6144)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), step.view(torch.int32))
+    ref, mag = _referee_of(oracle, m, w)
+    check_against_referee(oracle, ref, mag, y.cpu().numpy())
+    p.close()
+
+
+def test_projection_rejects_repeated_genes(oracle):
+    from cellerator_amd import _native as N
+    from cellerator_amd.exec_order import ExecProjection
+    rng = np.random.default_rng(17)
+    fx = _skewed(oracle, rng, 300, 2100, 4, 1)
+    col = fx["col_idx"].copy()
+    b = int(fx["row_ptr"][7])
+    assert fx["row_ptr"][8] - b >= 2
+    col[b + 1] = col[b]
+    with pytest.raises(N.EngineError, match="repeats a gene"):
+        ExecProjection(to_device_qcsr(dict(fx, col_idx=col)), 1024)
+
+
+def _exec_case(m, w, y, head):
+    import torch
+    c = qcsr_case(m, w, y)
+    c.exec_order, c.head_genes = 1, head
+    nbytes = C.c_uint64()
+    from cellerator_amd import _native as N
+    assert N.engine().cx_qcsr_exec_workspace_for(m.rows, m.cols, head, w.shape[1], C.byref(nbytes)) == 0
+    ws = torch.empty(nbytes.value, dtype=torch.uint8, device="cuda")
+    c.workspace, c.workspace_bytes = ws.data_ptr(), nbytes.value
+    c._keep = c._keep + (ws,)
+    return c
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_execution_order_candidate_through_reference_core(oracle, bits):
+    import torch
+
+    from cellerator_amd import qcsr_spmm
+    from cellerator_amd.exec_order import ExecProjection
+    rng = np.random.default_rng(300 + bits)
+    fx = _skewed(oracle, rng, 2200, 3100, bits, 1)
+    m = to_device_qcsr(fx)
+    w = torch.from_numpy((rng.standard_normal((3100, 128)) * 0.02).astype(np.float16)).cuda()
+    y = torch.full((2200, 128), float("nan"), device="cuda")
+    r = H.run(_exec_case(m, w, y, 1024))
+    assert (r.prepare_status, r.state_status, r.status) == (H.OK, H.OK, H.OK), (r.message, r.engine)
+    assert r.dispatch == b"qcsr:execution-order"
+    assert r.persistent_bytes > 0
+    torch.cuda.synchronize()
+    direct = ExecProjection(m, 1024).spmm(w)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), direct.view(torch.int32))
+    ref, mag = _referee(oracle, fx, w.cpu().numpy())
+    check_against_referee(oracle, ref, mag, y.cpu().numpy())
+    # without the persistent state the candidate runs the row-group kernel on the bound CSR
+    y2 = torch.full_like(y, float("nan"))
+    c = _exec_case(m, w, y2, 1024)
+    c.exec_order = 2
+    r = H.run(c)
+    assert (r.prepare_status, r.status) == (H.OK, H.OK), (r.message, r.engine)
+    assert r.dispatch == b"qcsr:execution-order->row-group"
+    torch.cuda.synchronize()
+    assert torch.equal(y2.view(torch.int32), qcsr_spmm(m, w).view(torch.int32))
+
+
+def test_execution_order_candidate_epilogue(oracle):
+    """A fused epilogue (bias + ReLU, affine accumulate) through the candidate equals the
+    direct call with the same epilogue, bitwise."""
+    import torch
+
+    from cellerator_amd import Epilogue
+    from cellerator_amd.exec_order import ExecProjection
+    rng = np.random.default_rng(44)
+    fx = _skewed(oracle, rng, 1500, 2600, 4, 1)
+    m = to_device_qcsr(fx)
+    w = torch.from_numpy((rng.standard_normal((2600, 64)) * 0.02).astype(np.float16)).cuda()
+    c0 = torch.from_numpy(rng.standard_normal((1500, 64)).astype(np.float32)).cuda()
+    bias = torch.from_numpy(rng.standard_normal(64).astype(np.float32)).cuda()
+    y = c0.clone()
+    c = _exec_case(m, w, y, 1024)
+    c.fused, c.epilogue_kind, c.affine, c.alpha, c.beta = 1, 5, 1, 0.5, 2.0
+    c.bias = bias.data_ptr()
+    r = H.run(c)
+    assert (r.prepare_status, r.status) == (H.OK, H.OK), (r.message, r.engine)
+    assert r.dispatch == b"qcsr:execution-order"
+    direct = c0.clone()
+    ExecProjection(m, 1024).spmm(w, out=direct, epilogue=Epilogue(kind=5, alpha=0.5, beta=2.0, bias=bias,
+                                                                   initial=direct))
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), direct.view(torch.int32))
+
+
+def test_execution_order_candidate_launch_costs_no_more_than_direct():
+    """On C3-generated rows (131,072 cells, 2,048-gene head) the core's prepared launch takes
+    no more than the direct call: within 5% (plus 20 us of host dispatch) over 20 launches."""
+    import torch
+
+    from cellerator_amd import qcsr_pack_gene_affine
+    from cellerator_amd.exec_order import ExecProjection
+    from cellerator_amd.synth import C3, dense_normal, generate_qcsr
+    m = generate_qcsr(C3.scaled(131072))
+    w = dense_normal((m.cols, 64), 0.02, torch.float16, seed=5)
+    y = torch.empty((m.rows, 64), device="cuda")
+    c = _exec_case(m, w, y, 2048)
+    c.repeats = 20
+    r = H.run(c)  # builds the state once, then 20 timed launches
+    assert (r.state_status, r.status) == (H.OK, H.OK), (r.message, r.engine)
+    assert r.dispatch == b"qcsr:execution-order"
+    p = ExecProjection(qcsr_pack_gene_affine(m), 2048)
+    out = torch.empty_like(y)
+    direct_ms = _time_ms(lambda: p.spmm(w, out=out), 20)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), out.view(torch.int32))
+    print(f"direct {direct_ms:.4f} ms, through the core {r.launch_ms:.4f} ms per launch")
+    assert r.launch_ms <= direct_ms * 1.05 + 0.02
+    p.close()

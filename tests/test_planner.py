@@ -101,3 +101,31 @@ def test_tuning_bounds_and_failures():
     r = P.plan(P.spmm_case(**C4), lambda identity: dict(kernel_ns=1.0, samples=5, spread_percent=1.0,
                                                         correct=identity != P.BELL_ID))
     assert r.diag(P.BELL_ID).rejection == P.INCORRECT and r.winner == P.QCSR_ID
+
+
+def test_execution_order_candidate_is_chosen_for_reuse():
+    """The execution-order candidate pays a one-time preparation (about 0.074 ns per stored
+    entry: 111 ms at C3) and more persistent bytes for about half the launch time of the
+    row-group candidate. The planner amortizes the preparation over the projection reuse
+    (compute_total_cost, src/planner/end_to_end_planner.cc:184-213): a single run keeps the
+    row-group candidate, a persistent projection takes the execution order, and a persistent
+    limit below its layouts rejects it with the reference's reason."""
+    both = P.QCSR | P.QCSR_EXEC
+    single = P.plan(P.spmm_case(**C3, mask=both, structure_reuse=1, projection_reuse=1))
+    assert single.status == P.OK and single.legal == 2
+    assert single.winner == P.QCSR_ID
+    ex, rg = single.diag(P.QCSR_EXEC_ID), single.diag(P.QCSR_ID)
+    assert ex.analytical_ns > rg.analytical_ns > 0.0
+    persistent = P.plan(P.spmm_case(**C3, mask=both, structure_reuse=1000, projection_reuse=1000))
+    assert persistent.winner == P.QCSR_EXEC_ID
+    ex, rg = persistent.diag(P.QCSR_EXEC_ID), persistent.diag(P.QCSR_ID)
+    # measured launch times at C3: 3.31 ms against 6.99 ms
+    assert 0.40 < ex.analytical_ns / rg.analytical_ns < 0.60
+    # the prepared layouts add about 4 GB at C3 to the structure's 6.8 GB
+    tight = P.plan(P.spmm_case(**C3, mask=both, structure_reuse=1000, projection_reuse=1000,
+                               max_persistent=8_000_000_000))
+    assert tight.diag(P.QCSR_EXEC_ID).rejection == P.PERSISTENT
+    assert tight.winner == P.QCSR_ID
+    # plain values have no execution-order form: the candidate's shape cannot be priced
+    plain = P.plan(P.spmm_case(**C3, mask=both, bits=0, value_bytes=4, projection_reuse=1000))
+    assert plain.diag(P.QCSR_EXEC_ID).rejection == P.MALFORMED and plain.winner == P.QCSR_ID
