@@ -7,9 +7,10 @@ Zipf(1.1) gene popularity, per-gene scale/offset, fp16 W 33,538 x 64 ~ N(0, 0.02
 Inputs are generated seeded on the GPU and are resident in HBM before timing starts.
 
 One step = one launch of the prepared execution-order path over the whole matrix
-(cx_qcsr_spmm_fwd_hybrid: the 2,048 most stored genes on the matrix cores (6,144 for c2), the rest
-through the prepared tail stream; the structure is prepared once, untimed), with the
-canonical cx_qcsr_spmm_fwd kernel timed beside it (--canonical makes it the headline).
+(cx_qcsr_exec_spmm, what the CP-Math execution-order candidate runs: canonical W gathered into
+execution order, the 2,048 most stored genes on the matrix cores (6,144 for c2), the rest through
+the prepared tail stream; the projection is prepared once, untimed), with the canonical
+cx_qcsr_spmm_fwd kernel timed beside it (--canonical makes it the headline).
 Prints ONE JSON line: metric/value (nnz/s), ms_per_step, roofline of the kernels
 (achieved algorithmic GB/s from HIP events on the launch stream vs 8 TB/s), and the CPU
 baseline (the oracle's row-parallel fp32 restatement timed on this host).
@@ -232,39 +233,38 @@ def bench_qcsr(args, torch, cfg, n_out: int) -> dict:
 
 
 def bench_qcsr_prepared(args, torch, mt, w, n_out: int, stream):
-    """The same product on the prepared execution-order projection (cx_qcsr_spmm_fwd_hybrid):
-    genes relabelled by popularity (W rows gathered to match, the reference's packed dense
-    operand), the first --head genes as a dense code plane on the matrix cores, the rest
-    from the prepared tail stream on the row-group walk. Built once per structure (untimed,
-    reported as prepare_ms); output rows are the same cells in the same order."""
-    from cellerator_amd.exec_order import (hybrid_prepare, hybrid_spmm, pack_rows, popularity_order,
-                                           to_execution_order)
+    """The same product on the prepared execution-order projection (cx_qcsr_exec_prepare /
+    cx_qcsr_exec_spmm, the object behind the CP-Math execution-order candidate): genes in
+    popularity order, the first --head genes as a dense code plane on the matrix cores, the
+    rest from the prepared tail stream. Built once per structure (untimed, reported as
+    prepare_ms); each launch takes the canonical W, gathers it into execution order in its
+    workspace and runs the head and the tail; output rows are the same cells in the same
+    order."""
+    from cellerator_amd.exec_order import ExecProjection
 
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    order = popularity_order(mt)
-    mx = to_execution_order(mt, order)
-    wx = pack_rows(order, w)
-    layout = hybrid_prepare(mx, args.head, stream_tail=True)
+    proj = ExecProjection(mt, args.head)
     torch.cuda.synchronize()
     prep_ms = (time.perf_counter() - t0) * 1e3
+    info = proj.info()
     out = torch.empty((mt.rows, n_out), dtype=torch.float32, device="cuda")
 
     def launch():
-        hybrid_spmm(layout, wx, out=out, stream=stream)
+        proj.spmm(w, out=out, stream=stream)
 
     wall_ms, ev = time_launches(torch, launch, args.steps, args.warmup, stream)
-    log(f"prepared head={args.head} + tail stream: {wall_ms:.3f} ms/step (prepare {prep_ms:.0f} ms)")
-    plan, entries = layout.tail_storage
-    return {"ms_per_step": wall_ms, "value": mt.nnz / (wall_ms * 1e-3), "unit": "nnz/s",
-            "head_genes": args.head, "kernel_ms_mean": statistics.mean(ev),
-            "kernel_ms_median": statistics.median(ev),
-            "kernels": "qcsr_head_dense (matrix cores, genes < head) + qcsr_spmm_stream (tail) per 64 columns",
-            "prepare_ms": prep_ms,
-            "prepare": "popularity order, execution-order relabel, weight rows reordered, dense head layout, "
-                       "tail stream (plan + fill)",
-            "layout_bytes": int(layout.storage.numel()), "tail_stream_bytes": int(entries.numel() + plan.numel()),
-            "tail_fills": int(layout.tail.fills)}, out
+    log(f"prepared head={info.head_cols} + tail stream: {wall_ms:.3f} ms/step (prepare {prep_ms:.0f} ms)")
+    head_kernel = {1: "qcsr_head_dense", 2: "qcsr_head_lut"}.get(int(info.head_form), "qcsr_head")
+    kernels = (f"pack_dense_operand (W into execution order) + pack_rhs_kernel + {head_kernel} (matrix cores, "
+               f"genes < {info.head_cols}) + qcsr_spmm_stream (tail) per 64 columns")
+    res = {"ms_per_step": wall_ms, "value": mt.nnz / (wall_ms * 1e-3), "unit": "nnz/s",
+           "head_genes": int(info.head_cols), "kernel_ms_mean": statistics.mean(ev),
+           "kernel_ms_median": statistics.median(ev), "kernels": kernels, "prepare_ms": prep_ms,
+           "prepare": "cx_qcsr_exec_prepare: popularity order, execution-order relabel (temporary), metadata in "
+                      "execution order, dense head layout, tail stream (global sort by tail length, plan, fill)",
+           "persistent_bytes": int(info.persistent_bytes), "tail_fills": int(info.tail_fills)}
+    return res, out
 
 
 def parity_sample_qcsr(m, w, out, count: int, seed: int) -> dict:

@@ -944,8 +944,11 @@ extern "C" int cx_qcsr_spmm_fwd_hybrid(const cx_qcsr_matrix *m, const cx_qcsr_hy
         return fail(CX_STATUS_INVALID_SHAPE, "cx_qcsr_spmm_fwd_hybrid: out_cols must be 64, 128, 192 or 256");
     const bool aligned = (reinterpret_cast<std::uintptr_t>(rhs) & 15u) == 0u
         && (reinterpret_cast<std::uintptr_t>(out) & 15u) == 0u && (rhs_ld * 2) % 16 == 0 && (out_ld * 4) % 16 == 0;
-    if (!aligned || rhs_ld > (INT32_MAX / 2) / 1024)
+    if (!aligned)
         return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd_hybrid: rhs and output must be 16-byte aligned");
+    if (rhs_ld > (INT32_MAX / 2) / 1024)
+        return fail(CX_STATUS_INVALID_SHAPE,
+                    "cx_qcsr_spmm_fwd_hybrid: rhs_ld too large (a 1,024-gene part must span under 1 GiB of W)");
     if (static_cast<const void *>(out) == rhs)
         return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd_hybrid: output aliases the rhs");
     return launch_hybrid(*m, L, rhs, rhs_ld, out_cols, out, out_ld, epilogue, workspace, workspace_bytes,

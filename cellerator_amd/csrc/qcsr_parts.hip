@@ -148,12 +148,21 @@ __device__ float row_fallback(const QcsrArgs &a, std::uint32_t row, int lane) {
 
 constexpr int kPadGene = kPartGenes;  // all-zero weight row, (0, 0) metadata
 
+// Scratch of the prologue that assigns rows to (wave, layer, group) slots.
+template<int kWaves, int kLayers>
+struct GroupPrologue {
+    static constexpr int kRows = kWaves * kLayers * 8;
+    int len[kRows];                 // row lengths by position in the block (-1: no row)
+    int by_rank[kRows];             // row lengths by rank
+    int set_slot[kRows / 8];        // wave * kLayers + layer of row set s
+};
+
 template<int kWaves, int kLayers>
 struct GroupsShared {
     static constexpr int kRows = kWaves * kLayers * 8;
     union {
         uint4 stage[kWaves][8][9];  // per wave and lane group: 16 (metadata byte offset, value) pairs (+16 B pad)
-        int len[kRows];             // prologue: row lengths
+        GroupPrologue<kWaves, kLayers> pro;
     } u;
     float2 meta[kPartGenes + 2];    // (scale, offset) per gene of the part; [kPadGene] = (0, 0)
     uint4 w[(kPartGenes + 1) * 8];  // fp16 weight rows of the part; row kPadGene is zeros
@@ -163,18 +172,22 @@ struct GroupsShared {
 
 // Rank the block's rows by length (descending, ties by index); ranks 8s .. 8s + 7 form row
 // set s (similar lengths, so the 8 groups of a layer finish their runs together), and the
-// sets are dealt to the waves in snake order (set s -> layer s / kWaves), so every wave
-// carries about the same number of nonzeros.
+// sets go, heaviest first, to the least-loaded wave with a layer left (ties: the lower wave),
+// so the waves carry about the same number of nonzeros into every part barrier even when a
+// block's longest rows are several times its median.
 template<int kWaves, int kLayers>
-__device__ __forceinline__ void assign_groups(int *len, std::uint32_t *rows_out, const std::int32_t *row_ptr,
-                                              std::uint32_t rows, std::uint32_t first, int tid) {
+__device__ __forceinline__ void assign_groups(GroupPrologue<kWaves, kLayers> &pro, std::uint32_t *rows_out,
+                                              const std::int32_t *row_ptr, std::uint32_t rows, std::uint32_t first,
+                                              int tid) {
     constexpr int kRows = kWaves * kLayers * 8;
+    constexpr int kSets = kRows / 8;
+    int *len = pro.len;
     const std::uint32_t row = first + static_cast<std::uint32_t>(tid);
     if (tid < kRows) len[tid] = row < rows ? row_ptr[row + 1] - row_ptr[row] : -1;
     __syncthreads();
+    int rank = 0;
     if (tid < kRows) {
         const int my = len[tid];
-        int rank = 0;
         const int4 *l4 = reinterpret_cast<const int4 *>(len);
 #pragma unroll 4
         for (int u = 0; u < kRows / 4; ++u) {
@@ -185,11 +198,42 @@ __device__ __forceinline__ void assign_groups(int *len, std::uint32_t *rows_out,
             rank += v.z > my || (v.z == my && b + 2 < tid) ? 1 : 0;
             rank += v.w > my || (v.w == my && b + 3 < tid) ? 1 : 0;
         }
-        const int set = rank / 8, g = rank % 8;
-        const int round = set / kWaves, pos = set % kWaves;
-        const int w = (round & 1) != 0 ? kWaves - 1 - pos : pos;
-        rows_out[(w * kLayers + round) * 8 + g] = row < rows ? row : kNoRow;
+        pro.by_rank[rank] = my;
     }
+    __syncthreads();
+    if (tid < kWave) {
+        // One wave deals the sets: lane s holds set s's load, lane w (< kWaves) the load of
+        // wave w; per set, a DPP min over lanes 0..15 of (load, lane) finds the least-loaded
+        // wave with a layer left. Loads saturate at 2^27 (only the balance depends on them).
+        static_assert(kSets <= kWave && kWaves == 16, "one wave deals the sets to 16 waves");
+        const int lane = tid;
+        std::uint32_t set_load = 0u;
+        if (lane < kSets)
+            for (int k = 0; k < 8; ++k) {
+                const int v = pro.by_rank[lane * 8 + k];
+                set_load += static_cast<std::uint32_t>(v > 0 ? min(v, 1 << 20) : 0);
+            }
+        std::uint32_t wave_load = 0u;
+        int used = 0;
+        for (int st = 0; st < kSets; ++st) {
+            const std::uint32_t load = __builtin_amdgcn_readlane(set_load, st);
+            std::uint32_t key = lane < kWaves && used < kLayers ? (min(wave_load, (1u << 27) - 1u) << 4) | lane
+                                                                 : 0xffffffffu;
+            key = min(key, static_cast<std::uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(key), 0x121, 0xf, 0xf, false)));
+            key = min(key, static_cast<std::uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(key), 0x122, 0xf, 0xf, false)));
+            key = min(key, static_cast<std::uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(key), 0x124, 0xf, 0xf, false)));
+            key = min(key, static_cast<std::uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(key), 0x128, 0xf, 0xf, false)));
+            const int best = static_cast<int>(__builtin_amdgcn_readlane(key, 0) & 15u);
+            const int layer = __builtin_amdgcn_readlane(used, best);
+            if (lane == best) {
+                wave_load += load;
+                ++used;
+            }
+            if (lane == 0) pro.set_slot[st] = best * kLayers + layer;
+        }
+    }
+    __syncthreads();
+    if (tid < kRows) rows_out[pro.set_slot[rank / 8] * 8 + rank % 8] = row < rows ? row : kNoRow;
     __syncthreads();
 }
 
@@ -241,7 +285,7 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
 
     if (tid < 8) sh.w[kPadGene * 8 + tid] = make_uint4(0u, 0u, 0u, 0u);
     if (tid == 8) sh.meta[kPadGene] = make_float2(0.0f, 0.0f);
-    assign_groups<kWaves, kLayers>(sh.u.len, sh.rows, a.row_ptr, a.rows, first, tid);
+    assign_groups<kWaves, kLayers>(sh.u.pro, sh.rows, a.row_ptr, a.rows, first, tid);
 
     // The block's entries and packed bytes, addressed by 32-bit buffer offsets.
     const int wg_begin = __builtin_amdgcn_readfirstlane(a.row_ptr[first]);
@@ -500,6 +544,9 @@ struct StreamShared {
 
 static_assert(kPadGene == static_cast<int>(kStreamPad) && kPadGene + 1 == static_cast<int>(kStreamPadOdd)
               && kPartGenes == kStreamPartGenes, "the stream builder and the part walk must agree on parts and pads");
+// One workgroup per CU holds the whole part: gfx950's 160 KB of LDS per workgroup.
+static_assert(sizeof(StreamShared) <= 160u * 1024u, "the tail walk's LDS exceeds gfx950's 160 KB");
+static_assert(sizeof(GroupsShared<16, 4>) <= 160u * 1024u, "the row-group walk's LDS exceeds gfx950's 160 KB");
 
 // Entries of one lane for one fill: group g's stage slots 2j, 2j + 1.
 template<bool kWide>
@@ -696,7 +743,7 @@ struct BwdGroupsShared {
     static constexpr int kRows = kWaves * kLayers * 8;
     union {
         std::uint32_t stage[kWaves][8][20];  // per wave and lane group: 16 weight-row offsets (+16 B pad)
-        int len[kRows];                      // prologue: row lengths
+        GroupPrologue<kWaves, kLayers> pro;
     } u;
     uint4 w[(kPartGenes + 1) * 8];           // fp16 weight rows of the part; row kPadGene is zeros
     std::uint32_t rows[kRows];
@@ -729,7 +776,7 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_bwd_values_groups(BwdPart
     const std::uint32_t last = first + kRows < a.rows ? first + kRows : a.rows;
 
     if (tid < 8) sh.w[kPadGene * 8 + tid] = make_uint4(0u, 0u, 0u, 0u);
-    assign_groups<kWaves, kLayers>(sh.u.len, sh.rows, a.row_ptr, a.rows, first, tid);
+    assign_groups<kWaves, kLayers>(sh.u.pro, sh.rows, a.row_ptr, a.rows, first, tid);
 
     const int wg_begin = __builtin_amdgcn_readfirstlane(a.row_ptr[first]);
     const int wg_end = __builtin_amdgcn_readfirstlane(a.row_ptr[last]);

@@ -123,6 +123,9 @@ __device__ __forceinline__ std::uint32_t rank_slot(RankShared &r, const PlanArgs
     return r.slot_row[tid];  // thread tid now works for slot tid
 }
 
+static_assert(sizeof(RankShared) + sizeof(std::uint16_t) * kPlanChunk * kStreamRows <= 160u * 1024u,
+              "the stream plan kernel's LDS exceeds gfx950's 160 KB");
+
 __global__ __launch_bounds__(kStreamRows) void stream_plan_kernel(PlanArgs a) {
     __shared__ RankShared rs;
     __shared__ std::uint16_t runs[kPlanChunk][kStreamRows];

@@ -7,6 +7,7 @@ and execution_csr_view (include/Cellerator/compute/math/physical_csr.hh:40-215).
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes as C
 import dataclasses
 from typing import Optional
@@ -15,7 +16,22 @@ import numpy as np
 import torch
 
 from . import _native as N
-from .engine import QcsrMatrix, _require_cuda, _stream
+from .engine import QcsrMatrix, _require_cuda, _stream, _torch_stream
+
+
+def _on(stream, device):
+    """Context in which torch allocations belong to the launch stream: buffers written by
+    kernels on a caller's stream are then not handed out again before that stream is past
+    them (torch's caching allocator keys reuse on the allocating stream)."""
+    if stream is None:
+        return contextlib.nullcontext()
+    return torch.cuda.stream(_torch_stream(stream, device))
+
+
+def _record(t: torch.Tensor, stream) -> None:
+    """Marks a cached buffer as used by `stream` (see _on)."""
+    if stream is not None:
+        t.record_stream(_torch_stream(stream, t.device))
 
 
 @dataclasses.dataclass
@@ -153,7 +169,8 @@ def hybrid_prepare(m: QcsrMatrix, head_cols: int, stream=None, stream_tail: bool
     d = m.descriptor()
     nbytes = C.c_uint64()
     N.check("cx_qcsr_hybrid_layout_bytes", lib.cx_qcsr_hybrid_layout_bytes(C.byref(d), head_cols, C.byref(nbytes)))
-    storage = torch.empty(max(nbytes.value, 256), dtype=torch.uint8, device=m.row_ptr.device)
+    with _on(stream, m.row_ptr.device):
+        storage = torch.empty(max(nbytes.value, 256), dtype=torch.uint8, device=m.row_ptr.device)
     layout = N.CxQcsrHybridLayout()
     N.check("cx_qcsr_hybrid_prepare", lib.cx_qcsr_hybrid_prepare(
         C.byref(d), head_cols, storage.data_ptr(), storage.numel(), C.byref(layout), _stream(stream)))
@@ -170,12 +187,14 @@ def tail_prepare(p: HybridProjection, stream=None) -> N.CxQcsrTailStream:
     dev = p.matrix.row_ptr.device
     nbytes = C.c_uint64()
     N.check("cx_qcsr_tail_plan_bytes", lib.cx_qcsr_tail_plan_bytes(C.byref(d), C.byref(p.layout), C.byref(nbytes)))
-    plan = torch.empty(max(nbytes.value, 256), dtype=torch.uint8, device=dev)
+    with _on(stream, dev):
+        plan = torch.empty(max(nbytes.value, 256), dtype=torch.uint8, device=dev)
     ts = N.CxQcsrTailStream()
     entry_bytes = C.c_uint64()
     N.check("cx_qcsr_tail_plan", lib.cx_qcsr_tail_plan(C.byref(d), C.byref(p.layout), plan.data_ptr(), plan.numel(),
                                                         C.byref(ts), C.byref(entry_bytes), _stream(stream)))
-    entries = torch.empty(max(entry_bytes.value, 256), dtype=torch.uint8, device=dev)
+    with _on(stream, dev):
+        entries = torch.empty(max(entry_bytes.value, 256), dtype=torch.uint8, device=dev)
     N.check("cx_qcsr_tail_fill", lib.cx_qcsr_tail_fill(C.byref(d), C.byref(p.layout), C.byref(ts),
                                                         entries.data_ptr(), entries.numel(), _stream(stream)))
     p.tail, p.tail_storage = ts, (plan, entries)
@@ -244,6 +263,8 @@ def hybrid_spmm(p: HybridProjection, w: torch.Tensor, out: Optional[torch.Tensor
     d = m.descriptor()
     e = epilogue.descriptor(out) if epilogue is not None else None
     ws = p.workspace(n, w.device) if p.head_cols else None
+    if ws is not None:
+        _record(ws, stream)
     N.check("cx_qcsr_spmm_fwd_hybrid", N.engine().cx_qcsr_spmm_fwd_hybrid(
         C.byref(d), C.byref(p.layout), w.data_ptr(), w.stride(0), n, out.data_ptr(), out.stride(0),
         C.byref(e) if e is not None else None, ws.data_ptr() if ws is not None else None,
@@ -297,6 +318,7 @@ class ExecProjection:
             out = torch.empty((self.rows, n), dtype=torch.float32, device=w.device)
         e = epilogue.descriptor(out) if epilogue is not None else None
         ws = self.workspace(n)
+        _record(ws, stream)
         N.check("cx_qcsr_exec_spmm", self._lib.cx_qcsr_exec_spmm(
             self._handle, w.data_ptr(), w.stride(0), n, out.data_ptr(), out.stride(0),
             C.byref(e) if e is not None else None, ws.data_ptr(), ws.numel(), _stream(stream)))

@@ -224,3 +224,60 @@ def test_long_rows_and_unsorted_rows(oracle):
     mb = dataclasses.replace(m, col_idx=torch.from_numpy(bad).cuda())
     with pytest.raises(N.EngineError, match="not sorted"):
         hybrid_prepare(mb, 1024, stream_tail=True)
+
+
+def test_prepare_and_launch_on_a_side_stream(oracle):
+    """hybrid_prepare(..., stream=side) allocates the layouts on the side stream it fills them
+    on, and launches on that stream give the default stream's product bitwise; the prepared
+    projection object does the same."""
+    import torch
+
+    from cellerator_amd.exec_order import ExecProjection, hybrid_prepare, hybrid_spmm, pack_rows
+    rng = np.random.default_rng(515)
+    fx = _skewed(oracle, rng, 1400, 2600, 4, 1)
+    m = to_device_qcsr(fx)
+    mx, order = _exec(m)
+    w = torch.from_numpy((rng.standard_normal((2600, 64)) * 0.02).astype(np.float16)).cuda()
+    wx = pack_rows(order, w)
+    base = hybrid_spmm(hybrid_prepare(mx, 1024, stream_tail=True), wx)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    p = hybrid_prepare(mx, 1024, stream=side, stream_tail=True)
+    with torch.cuda.stream(side):
+        y = torch.empty_like(base)
+    hybrid_spmm(p, wx, out=y, stream=side)
+    proj = ExecProjection(m, 1024, stream=side)
+    with torch.cuda.stream(side):
+        y2 = torch.empty_like(base)
+    proj.spmm(w, out=y2, stream=side)
+    side.synchronize()
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), base.view(torch.int32))
+    assert torch.equal(y2.view(torch.int32), base.view(torch.int32))
+
+
+def test_stream_layout_33_parts_head_0(oracle):
+    """34,000 genes with no head: 34 gene parts, so the plan kernel counts parts in two chunks
+    (32 + 2) and every row's tail starts at its first entry; layout bit-exact, product within
+    the referee's tolerance."""
+    import torch
+
+    from cellerator_amd.exec_order import hybrid_head_arrays, hybrid_prepare, hybrid_spmm, pack_rows, tail_arrays
+    rng = np.random.default_rng(3333)
+    fx = _skewed(oracle, rng, 1100, 34_000, 4, 1)
+    mx, order = _exec(to_device_qcsr(fx))
+    p = hybrid_prepare(mx, 0, stream_tail=True)
+    torch.cuda.synchronize()
+    assert int(p.tail.parts) == 34
+    slot_rows, index, entries = tail_arrays(p)
+    h = qcsr_to_host(mx)
+    he = hybrid_head_arrays(p)[2].cpu().numpy()
+    want_rows, want_index, want_entries = _stream_reference(h, he, 0, 4, int(p.tail.layers))
+    assert np.array_equal(slot_rows.cpu().numpy().view(np.uint32), want_rows)
+    assert np.array_equal(index.cpu().numpy().view(np.uint32), want_index)
+    assert np.array_equal(entries.cpu().numpy().view(np.uint16), want_entries)
+    w = (rng.standard_normal((34_000, 64)) * 0.02).astype(np.float16)
+    y = hybrid_spmm(p, pack_rows(order, torch.from_numpy(w).cuda()))
+    torch.cuda.synchronize()
+    ref, mag = _referee(oracle, fx, w)
+    check_against_referee(oracle, ref, mag, y.cpu().numpy())
