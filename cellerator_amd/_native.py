@@ -339,6 +339,8 @@ ENGINE_SIGNATURES = {
                                     C.POINTER(CxQcsrTailStream), p_void, u64, p_void]),
     "cx_qcsr_spmm_fwd_hybrid": (C.c_int, [C.POINTER(CxQcsrMatrix), C.POINTER(CxQcsrHybridLayout), p_void, i64,
                                           i64, p_void, i64, C.POINTER(CxSpmmEpilogue), p_void, u64, p_void]),
+    "cx_qcsr_head_order": (C.c_int, [p_void, u32, u32, u32, p_void, p_void, p_void, u32, u32, p_void, p_void,
+                                     C.POINTER(u32)]),
     "cx_qcsr_exec_prepare": (C.c_int, [C.POINTER(CxQcsrMatrix), u32, C.POINTER(p_void), p_void]),
     "cx_qcsr_exec_query": (C.c_int, [p_void, C.POINTER(CxQcsrExecInfo)]),
     "cx_qcsr_exec_workspace_bytes": (C.c_int, [p_void, i64, C.POINTER(u64)]),

@@ -70,6 +70,12 @@ int launch_hybrid(const cx_qcsr_matrix &m, const cx_qcsr_hybrid_layout &layout, 
                   std::int64_t out_cols, float *out, std::int64_t out_ld, const cx_spmm_epilogue *epilogue,
                   void *workspace, std::uint64_t workspace_bytes, hipStream_t stream, const char *who);
 
+// The matrix-core head's scale exponent (qcsr_hybrid.hip): k = 14 - floor(log2 total), total =
+// the largest |decoded value| of the head's genes plus, under the row-offset policy, the
+// largest |row offset|, so every scaled value 2^k x stays below 2^15; 0 for total = 0;
+// clamped to [-100, 100]. The head layout and the head order that picks its genes share it.
+int head_scale_exp(float total);
+
 constexpr int kWavesPerBlock = 4;
 
 // Decoded value of entry `i` (global nnz index) of row `row` whose packed codes start

@@ -13,7 +13,12 @@
 // product is the referee's (src/compute/math/referee.cc:101-253) up to fp32 summation order.
 #include "qcsr_common.hpp"
 
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <cstring>
 #include <new>
+#include <numeric>
 #include <vector>
 
 struct cx_qcsr_exec_projection {
@@ -69,27 +74,98 @@ void destroy(cx_qcsr_exec_projection *p) {
 
 bool valid_out_cols(std::int64_t n) { return n > 0 && n % 64 == 0 && n <= 256; }
 
+constexpr int kNever = INT_MAX;  // no layout exponent (at most 100) carries the gene exactly
+
+// Exponent of the lowest set bit of a finite nonzero float: x = m 2^e with m odd.
+int low_bit(float x) {
+    std::uint32_t b;
+    std::memcpy(&b, &x, 4);
+    const std::uint32_t field = (b >> 23) & 0xffu;
+    std::uint32_t m = b & 0x7fffffu;
+    int e = -149;
+    if (field != 0u) {
+        m |= 0x800000u;
+        e = static_cast<int>(field) - 150;
+    }
+    return e + __builtin_ctz(m);
+}
+
+// Smallest layout exponent k under which the head carries every value of a per-gene-policy
+// gene exactly (the conditions head_exact_kernel checks, qcsr_hybrid.hip): 2^k s and 2^k o
+// stay normal floats (or zero), and every decoded value x = fma(c, s, o) is a multiple of
+// 2^(-14-k), i.e. 2^k x lies on the 2^-14 grid. Both hold for every larger k, so the
+// smallest suffices; kNever for non-finite metadata or values, or when k would exceed 100.
+int gene_min_exp(float s, float o, std::uint32_t qmax) {
+    if (!std::isfinite(s) || !std::isfinite(o)) return kNever;
+    int need = INT_MIN;
+    if (s != 0.0f) need = std::max(need, -126 - std::ilogb(s));
+    if (o != 0.0f) need = std::max(need, -126 - std::ilogb(o));
+    for (std::uint32_t c = 0; c <= qmax; ++c) {
+        const float x = std::fma(static_cast<float>(c), s, o);
+        if (!std::isfinite(x)) return kNever;
+        if (x != 0.0f) need = std::max(need, -14 - low_bit(x));
+    }
+    return need > 100 ? kNever : need;
+}
+
+// The same under the row-offset policy, for the gene's scale alone: 2^k s on the 2^-14 grid
+// (and normal). The row offsets add one condition shared by every gene (rows_min_exp).
+int scale_min_exp(float s) {
+    if (!std::isfinite(s)) return kNever;
+    if (s == 0.0f) return INT_MIN;
+    const int need = -14 - low_bit(s);
+    return need > 100 ? kNever : need;
+}
+
+// Smallest k putting every 2^k r on the 2^-14 grid; the largest |r| in *largest.
+int rows_min_exp(const float *r, std::uint32_t rows, float *largest) {
+    int need = INT_MIN;
+    float big = 0.0f;
+    for (std::uint32_t i = 0; r != nullptr && i < rows; ++i) {
+        if (!std::isfinite(r[i])) return kNever;
+        big = std::max(big, std::fabs(r[i]));
+        if (r[i] != 0.0f) need = std::max(need, -14 - low_bit(r[i]));
+    }
+    *largest = big;
+    return need > 100 ? kNever : need;
+}
+
 std::uint64_t weights_bytes(const cx_qcsr_exec_projection *p, std::int64_t out_cols) {
     return align256(static_cast<std::uint64_t>(p->shape.cols) * static_cast<std::uint64_t>(out_cols) * 2u);
 }
 
-int build(const cx_qcsr_matrix *a, std::uint32_t head, cx_qcsr_exec_projection *p, hipStream_t s) {
+int build(const cx_qcsr_matrix *a, std::uint32_t head_cols, cx_qcsr_exec_projection *p, hipStream_t s) {
     constexpr const char *who = "cx_qcsr_exec_prepare";
     const std::uint32_t rows = a->rows, cols = a->cols;
     // 1. the popularity order of the genes (stored entries per gene, descending; ties by gene)
+    //    with the genes the head cannot carry exactly moved after it (cx_qcsr_head_order)
     DeviceBuffer counts, inverse, err, col_x, packed_x, pairs_canon;
     int rc = counts.allocate(static_cast<std::uint64_t>(cols) * 4u, who);
     if (rc == CX_STATUS_SUCCESS) rc = cx_qcsr_column_counts(a, static_cast<std::uint32_t *>(counts.p), s);
     if (rc != CX_STATUS_SUCCESS) return rc;
     std::vector<std::uint32_t> host_counts(cols), perm(cols), inv(cols);
+    const bool pairs = a->decode_policy == CX_DECODE_PER_GENE_AFFINE_PAIRS;
+    const bool row_policy = a->decode_policy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET;
+    std::vector<float> scales(a->column_scales != nullptr ? static_cast<std::size_t>(cols) * (pairs ? 2u : 1u) : 0u);
+    std::vector<float> offsets(!row_policy && !pairs && a->column_offsets != nullptr ? cols : 0u);
+    std::vector<float> row_offsets(row_policy && a->row_offsets != nullptr ? rows : 0u);
     std::int32_t packed_total = 0;
     hipError_t e = hipMemcpyAsync(host_counts.data(), counts.p, static_cast<std::size_t>(cols) * 4u,
                                   hipMemcpyDeviceToHost, s);
     if (e == hipSuccess)
         e = hipMemcpyAsync(&packed_total, a->packed_row_ptr + rows, 4u, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess && !scales.empty())
+        e = hipMemcpyAsync(scales.data(), a->column_scales, scales.size() * 4u, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess && !offsets.empty())
+        e = hipMemcpyAsync(offsets.data(), a->column_offsets, offsets.size() * 4u, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess && !row_offsets.empty())
+        e = hipMemcpyAsync(row_offsets.data(), a->row_offsets, row_offsets.size() * 4u, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return hip_fail(e, who);
-    rc = cx_popularity_order(host_counts.data(), cols, perm.data(), inv.data());
+    std::uint32_t head = 0u;
+    rc = cx_qcsr_head_order(host_counts.data(), cols, a->bits, a->decode_policy, scales.empty() ? nullptr : scales.data(),
+                            offsets.empty() ? nullptr : offsets.data(), row_offsets.empty() ? nullptr : row_offsets.data(),
+                            rows, head_cols, perm.data(), inv.data(), &head);
     if (rc != CX_STATUS_SUCCESS) return rc;
     DeviceBuffer perm_d;
     rc = perm_d.allocate(static_cast<std::uint64_t>(cols) * 4u, who);
@@ -202,6 +278,95 @@ int build(const cx_qcsr_matrix *a, std::uint32_t head, cx_qcsr_exec_projection *
 
 } // namespace
 } // namespace cx
+
+extern "C" int cx_qcsr_head_order(const uint32_t *counts, uint32_t cols, uint32_t bits, uint32_t decode_policy,
+                                  const float *scales, const float *offsets, const float *row_offsets, uint32_t rows,
+                                  uint32_t head_cols, uint32_t *feature_permutation, uint32_t *inverse_permutation,
+                                  uint32_t *head_out) {
+    using namespace cx;
+    clear_error();
+    if (head_out == nullptr || (cols != 0u && (counts == nullptr || feature_permutation == nullptr
+                                               || inverse_permutation == nullptr)))
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_head_order: null argument");
+    if (bits != 1u && bits != 2u && bits != 4u && bits != 8u)
+        return fail(CX_STATUS_UNSUPPORTED, "cx_qcsr_head_order: quantized codes of 1, 2, 4 or 8 bits only");
+    if (decode_policy != CX_DECODE_PER_GENE_AFFINE && decode_policy != CX_DECODE_PER_GENE_AFFINE_PAIRS
+        && decode_policy != CX_DECODE_COLUMN_SCALE_ROW_OFFSET)
+        return fail(CX_STATUS_UNSUPPORTED, "cx_qcsr_head_order: unknown decode policy");
+    if (decode_policy == CX_DECODE_PER_GENE_AFFINE_PAIRS && scales == nullptr && cols != 0u)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_head_order: the pairs policy needs scales");
+    if (head_cols % kExecPartGenes != 0u)
+        return fail(CX_STATUS_INVALID_SHAPE, "cx_qcsr_head_order: head_cols must be a multiple of 1,024");
+    std::vector<std::uint32_t> order(cols);
+    std::iota(order.begin(), order.end(), 0u);
+    std::stable_sort(order.begin(), order.end(), [&](std::uint32_t x, std::uint32_t y) { return counts[x] > counts[y]; });
+    const std::uint32_t qmax = (1u << bits) - 1u;
+    const float qmax_f = static_cast<float>(qmax);
+    const bool row_policy = decode_policy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET;
+    float roff = 0.0f;
+    const int rows_need = row_policy ? rows_min_exp(row_offsets, rows, &roff) : INT_MIN;
+    const std::uint32_t want = std::min(head_cols, cols / kExecPartGenes * kExecPartGenes);
+    // Per gene, in popularity order: the smallest exponent carrying its values exactly (lo)
+    // and the largest its magnitude allows (hi: the bound head_range_kernel computes, plus the
+    // largest |row offset| under that policy, below 2^(15 - k)).
+    std::vector<int> lo(cols, kNever), hi(cols, INT_MIN);
+    for (std::uint32_t e = 0; e < cols && want != 0u; ++e) {
+        const std::uint32_t g = order[e];
+        float sg, og;
+        if (decode_policy == CX_DECODE_PER_GENE_AFFINE_PAIRS) {
+            sg = scales[2u * g];
+            og = scales[2u * g + 1u];
+        } else {
+            sg = scales != nullptr ? scales[g] : 1.0f;
+            og = !row_policy && offsets != nullptr ? offsets[g] : 0.0f;
+        }
+        const float b = row_policy ? std::fabs(sg) * qmax_f : std::max(std::fabs(og), std::fabs(std::fma(qmax_f, sg, og)));
+        const float total = row_policy ? b + roff : b;
+        lo[e] = row_policy ? scale_min_exp(sg) : gene_min_exp(sg, og, qmax);
+        if (!std::isfinite(total)) lo[e] = kNever;
+        hi[e] = total > 0.0f ? 14 - std::ilogb(total) : INT_MAX;
+    }
+    // The layout exponent K under which the head takes the most stored entries: the head is
+    // the most popular genes with lo <= K <= hi (whole 1,024-gene parts of them, at most
+    // `want`). The layout's own exponent (head_scale_exp of the head's largest bound) is then
+    // at least K, so every head gene stays exact under it.
+    std::uint64_t best = 0u;
+    int best_k = INT_MIN;
+    std::uint32_t head = 0u;
+    for (int K = std::max(-100, rows_need); K <= 100 && want != 0u && rows_need != kNever; ++K) {
+        std::uint32_t n = 0u;
+        for (std::uint32_t e = 0; e < cols && n < want; ++e) n += lo[e] <= K && K <= hi[e] ? 1u : 0u;
+        const std::uint32_t h = n / kExecPartGenes * kExecPartGenes;
+        std::uint64_t covered = 0u;
+        for (std::uint32_t e = 0, taken = 0u; e < cols && taken < h; ++e)
+            if (lo[e] <= K && K <= hi[e]) {
+                covered += static_cast<std::uint64_t>(counts[order[e]]) + 1u;  // + 1: of equal heads, the wider
+                ++taken;
+            }
+        if (h > 0u && covered > best) {
+            best = covered;
+            best_k = K;
+            head = h;
+        }
+    }
+    std::vector<std::uint8_t> in_head(cols, 0u);
+    for (std::uint32_t e = 0, taken = 0u; e < cols && taken < head; ++e)
+        if (lo[e] <= best_k && best_k <= hi[e]) {
+            in_head[order[e]] = 1u;
+            ++taken;
+        }
+    std::uint32_t at = 0u;
+    for (int pass = 0; pass < 2; ++pass)
+        for (std::uint32_t e = 0; e < cols; ++e) {
+            const std::uint32_t g = order[e];
+            if ((in_head[g] != 0u) == (pass == 0)) {
+                feature_permutation[at] = g;
+                inverse_permutation[g] = at++;
+            }
+        }
+    *head_out = head;
+    return CX_STATUS_SUCCESS;
+}
 
 extern "C" int cx_qcsr_exec_prepare(const cx_qcsr_matrix *a, uint32_t head_cols, cx_qcsr_exec_projection **out,
                                     void *stream) {

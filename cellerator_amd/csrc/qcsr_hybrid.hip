@@ -27,10 +27,13 @@
 // of two commutes with that rounding. x' is split into three fp16 parts with
 // round-toward-zero conversions, hi = rtz(x'), mid = rtz(x' - hi), lo = rtz(x' - hi - mid):
 // each residual is exact in fp32 (it has at most 13, then 2, significant bits), so
-// hi + mid + lo == x' whenever lo is an fp16 normal number or zero -- always for
-// |x'| >= 2^9 -- and below that only bits under 2^-14 (in x' units) can be lost: the matrix
-// cores are not relied on to keep fp16 subnormal inputs. k = 14 - floor(log2 B) for B the
-// largest |decoded value| any head code can take, so |x'| < 2^15 and hi cannot overflow.
+// hi + mid + lo == x' whenever x' is a multiple of 2^-14 below 2^15 (every nonzero part is
+// then an fp16 normal number; the matrix cores are not relied on to keep fp16 subnormal
+// inputs) -- always for 2^9 <= |x'| < 2^15. k = 14 - floor(log2 B) for B the largest
+// |decoded value| any head code can take, so |x'| < 2^15 and hi cannot overflow. The layout
+// is refused unless every value the head can decode lies on that 2^-14 grid and splits
+// exactly (head_exact_kernel, checked on the device at prepare); cx_qcsr_head_order
+// (qcsr_exec.hip) picks head genes for which it does and orders the rest after the head.
 // Each part times an fp16 weight is exact in fp32 and the matrix cores accumulate in fp32;
 // the sums are multiplied by 2^-k (exact). The result differs from an fp32 FMA chain over the
 // decoded values only in summation order.
@@ -644,6 +647,71 @@ __global__ __launch_bounds__(256) void abs_max_kernel(const float *v, std::uint3
     if ((threadIdx.x & (kWave - 1)) == 0) atomicMax(max_bits, __float_as_uint(b));
 }
 
+// Scaling by 2^k kept the value: no rounding, and the result is zero or a normal float.
+__device__ __forceinline__ bool exactly_scaled(float scaled, float value, float inv) {
+    const float a = fabsf(scaled);
+    return scaled * inv == value && a < __builtin_huge_valf() && (a == 0.0f || a >= 0x1p-126f);
+}
+
+// A scaled value the three fp16 parts can carry: a multiple of 2^-14 below 2^15.
+__device__ __forceinline__ bool on_head_grid(float x) {
+    const float t = x * 16384.0f;
+    return fabsf(x) < 32768.0f && t == truncf(t);
+}
+
+__device__ __forceinline__ bool normal_or_zero_half(std::uint32_t h) {
+    return (h & 0x7fffu) == 0u || ((h >> 10) & 0x1fu) != 0u;
+}
+
+// Exactness of the head under the layout scale 2^k (factor = 2^k, inv = 2^-k). Per-gene
+// policies, one thread per (head gene g, code c): x' = fma(c, 2^k s, 2^k o) must equal
+// 2^k fma(c, s, o), lie on the 2^-14 grid below 2^15, and split into three parts that are zero
+// or fp16 normal numbers summing to x'. Row-offset policy, one thread per head gene: 2^k s
+// exactly scaled and on the grid; with every 2^k r on the grid too (head_exact_rows_kernel),
+// each fma(c, 2^k s, 2^k r) is (the exact sum is a multiple of 2^-14 and rounding to fp32
+// keeps that), and the layout bound keeps it below 2^15. A failing gene g records g + 1.
+__global__ __launch_bounds__(256) void head_exact_kernel(const float *scales, const float *offsets, std::uint32_t policy,
+                                                         std::uint32_t head, std::uint32_t codes, float factor,
+                                                         float inv, std::uint32_t *bad) {
+    const std::uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= head * codes) return;
+    const std::uint32_t g = i / codes, c = i % codes;
+    float s, o;
+    if (policy == CX_DECODE_PER_GENE_AFFINE_PAIRS) {
+        s = scales[2 * g];
+        o = scales[2 * g + 1];
+    } else {
+        s = scales != nullptr ? scales[g] : 1.0f;
+        o = policy == CX_DECODE_PER_GENE_AFFINE && offsets != nullptr ? offsets[g] : 0.0f;
+    }
+    const float s2 = s * factor, o2 = o * factor;
+    bool ok = exactly_scaled(s2, s, inv) && exactly_scaled(o2, o, inv);
+    if (policy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET) {
+        ok = ok && on_head_grid(s2);
+    } else if (ok) {
+        const float x2 = __builtin_fmaf(static_cast<float>(c), s2, o2);
+        ok = x2 * inv == __builtin_fmaf(static_cast<float>(c), s, o) && on_head_grid(x2);
+        if (ok) {
+            std::uint32_t hw, mw, lw;
+            split_pair(x2, 0.0f, hw, mw, lw);
+            ok = normal_or_zero_half(hw) && normal_or_zero_half(mw) && normal_or_zero_half(lw)
+                 && static_cast<double>(h2f(hw & 0xffffu)) + static_cast<double>(h2f(mw & 0xffffu))
+                            + static_cast<double>(h2f(lw & 0xffffu)) == static_cast<double>(x2);
+        }
+    }
+    if (!ok) atomicMax(bad, g + 1u);
+}
+
+// Row-offset policy: every 2^k r exactly scaled and on the 2^-14 grid; a failing row records
+// row + 1.
+__global__ __launch_bounds__(256) void head_exact_rows_kernel(const float *row_offsets, std::uint32_t rows,
+                                                              float factor, float inv, std::uint32_t *bad) {
+    for (std::uint32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x) {
+        const float v = row_offsets[r], v2 = v * factor;
+        if (!(exactly_scaled(v2, v, inv) && on_head_grid(v2))) atomicMax(bad, r + 1u);
+    }
+}
+
 __global__ void zero_words(std::uint32_t *p, int n) {
     if (static_cast<int>(threadIdx.x) < n) p[threadIdx.x] = 0u;
 }
@@ -776,6 +844,17 @@ int launch_head(const cx_qcsr_hybrid_layout &L, const std::uint16_t *panel, std:
 }
 
 } // namespace
+
+int head_scale_exp(float total) {
+    int k = 0;
+    if (total > 0.0f) {
+        int ex = 0;
+        (void)std::frexp(total, &ex);  // total = f 2^ex, f in [0.5, 1): floor(log2) = ex - 1
+        k = 14 - (ex - 1);
+    }
+    return std::max(-100, std::min(100, k));
+}
+
 } // namespace cx
 
 extern "C" int cx_qcsr_hybrid_layout_bytes(const cx_qcsr_matrix *m, uint32_t head_cols, uint64_t *bytes) {
@@ -828,7 +907,7 @@ extern "C" int cx_qcsr_hybrid_prepare(const cx_qcsr_matrix *m, uint32_t head_col
 
     const hipStream_t s = static_cast<hipStream_t>(stream);
     auto *words = reinterpret_cast<std::uint32_t *>(base);  // header: range bits, row-offset bits, error
-    hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, s, words, 4);
+    hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, s, words, 6);
     if (head_cols != 0u) {
         const float qmax = static_cast<float>((1u << m->bits) - 1u);
         hipLaunchKernelGGL(head_range_kernel, dim3((head_cols + 255u) / 256u), dim3(256), 0, s, m->column_scales,
@@ -881,14 +960,9 @@ extern "C" int cx_qcsr_hybrid_prepare(const cx_qcsr_matrix *m, uint32_t head_col
     const float total = bound + roff;
     if (!(total < 3.0e38f))
         return fail(CX_STATUS_UNSUPPORTED, "cx_qcsr_hybrid_prepare: head metadata is not finite");
-    // k = 14 - floor(log2 B): every |x'| = 2^k |x| stays below 2^15
-    int k = 0;
-    if (total > 0.0f) {
-        int ex = 0;
-        (void)std::frexp(total, &ex);  // total = f 2^ex, f in [0.5, 1): floor(log2) = ex - 1
-        k = 14 - (ex - 1);
-    }
-    k = std::max(-100, std::min(100, k));
+    const int k = head_scale_exp(total);
+    if (!(std::ldexp(total, k) < 32768.0f))
+        return fail(CX_STATUS_UNSUPPORTED, "cx_qcsr_hybrid_prepare: head values of 2^115 or more");
     L.scale_exp = k;
     const std::uint32_t n = std::max(head_cols, L.row_offsets != nullptr ? m->rows : 0u);
     if (n != 0u) {
@@ -903,6 +977,35 @@ extern "C" int cx_qcsr_hybrid_prepare(const cx_qcsr_matrix *m, uint32_t head_col
                            reinterpret_cast<const float2 *>(L.meta), head_cols, (1u << m->bits) - 1u, L.lut);
         rc = check_launch("cx_qcsr_hybrid_prepare");
         if (rc != CX_STATUS_SUCCESS) return rc;
+    }
+    if (head_cols != 0u) {
+        // every value the head can decode must be carried exactly by its fp16 parts
+        const bool row_policy = m->decode_policy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET;
+        const std::uint32_t codes = row_policy ? 1u : (1u << m->bits);
+        const float factor = std::ldexp(1.0f, k), inv = std::ldexp(1.0f, -k);
+        hipLaunchKernelGGL(head_exact_kernel, dim3((head_cols * codes + 255u) / 256u), dim3(256), 0, s,
+                           m->column_scales, m->column_offsets, m->decode_policy, head_cols, codes, factor, inv,
+                           words + 4);
+        if (row_policy && m->row_offsets != nullptr)
+            hipLaunchKernelGGL(head_exact_rows_kernel, dim3(std::min<std::uint32_t>((m->rows + 255u) / 256u, 4096u)),
+                               dim3(256), 0, s, m->row_offsets, m->rows, factor, inv, words + 5);
+        rc = check_launch("cx_qcsr_hybrid_prepare");
+        if (rc != CX_STATUS_SUCCESS) return rc;
+        std::uint32_t bad[2] = {0u, 0u};
+        e = hipMemcpyAsync(bad, words + 4, sizeof(bad), hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) return hip_fail(e, "cx_qcsr_hybrid_prepare");
+        if (bad[0] != 0u) {
+            set_error("cx_qcsr_hybrid_prepare: head gene %u does not decode exactly under the layout scale 2^%d "
+                      "(cx_qcsr_head_order places such genes after the head)", bad[0] - 1u, k);
+            return CX_STATUS_UNSUPPORTED;
+        }
+        if (bad[1] != 0u) {
+            set_error("cx_qcsr_hybrid_prepare: the offset of row %u does not decode exactly under the layout scale "
+                      "2^%d (under the row-offset policy every row offset must; cx_qcsr_head_order then gives no head)",
+                      bad[1] - 1u, k);
+            return CX_STATUS_UNSUPPORTED;
+        }
     }
     *layout = L;
     return CX_STATUS_SUCCESS;

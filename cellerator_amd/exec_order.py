@@ -71,6 +71,36 @@ def popularity_order(m: QcsrMatrix, stream=None) -> ExecutionOrder:
                           torch.from_numpy(inv.view(np.int32)).to(dev))
 
 
+def head_order(m: QcsrMatrix, head_cols: int, stream=None) -> tuple[ExecutionOrder, int]:
+    """The execution order a prepared projection uses (cx_qcsr_head_order): the popularity
+    order with every gene the matrix-core head cannot carry exactly moved after the head, and
+    the head width it supports (head_cols capped at cols rounded down to 1,024, or fewer when
+    fewer genes qualify)."""
+    counts = column_counts(m, stream).cpu().numpy().view(np.uint32)
+
+    def host(t: Optional[torch.Tensor]) -> Optional[np.ndarray]:
+        return None if t is None else np.ascontiguousarray(t.detach().cpu().numpy().astype(np.float32, copy=False))
+
+    scales, offsets, row_offsets = host(m.column_scales), host(m.column_offsets), host(m.row_offsets)
+    perm = np.empty(m.cols, np.uint32)
+    inv = np.empty(m.cols, np.uint32)
+    head = C.c_uint32()
+    lib = N.engine()
+
+    def ptr(a):
+        return None if a is None else a.ctypes.data
+
+    st = lib.cx_qcsr_head_order(counts.ctypes.data, m.cols, m.bits, m.decode_policy, ptr(scales),
+                                ptr(offsets) if m.decode_policy == N.DECODE_PER_GENE_AFFINE else None,
+                                ptr(row_offsets) if m.decode_policy == N.DECODE_COLUMN_SCALE_ROW_OFFSET else None,
+                                m.rows, head_cols,
+                                perm.ctypes.data, inv.ctypes.data, C.byref(head))
+    N.check("cx_qcsr_head_order", st)
+    dev = m.col_idx.device
+    return (ExecutionOrder(torch.from_numpy(perm.view(np.int32)).to(dev),
+                           torch.from_numpy(inv.view(np.int32)).to(dev)), int(head.value))
+
+
 def pack_rows(order: ExecutionOrder, canonical: torch.Tensor, stream=None) -> torch.Tensor:
     """Rows of a feature-major device tensor [genes, ...] gathered into execution order
     (cx_pack_dense_operand): the packed dense operand for a row-major W, or the per-gene

@@ -1406,9 +1406,12 @@ const char *cx_exec_last_error(void);
  * over a dense copy of X[:, 0:H) (codes and presence bits, built once per matrix): every
  * code is decoded exactly as the reference codec does (fma(code, scale, offset),
  * include/Cellerator/quantized/access.cuh:81-91), scaled by a power of two 2^k and split
- * into three fp16 parts whose sum is the scaled value (exact for |x| >= 2^(9-k); below,
- * only bits under 2^(-14-k) can be lost), so each product is exact in fp32 and only the
- * fp32 summation order differs from the plain kernel. The tail runs on the row-group VALU
+ * into three fp16 parts whose sum is the scaled value, so each product is exact in fp32 and
+ * only the fp32 summation order differs from the plain kernel. The split is exact for a
+ * scaled value on the 2^-14 grid (every |x| >= 2^(9-k) is): cx_qcsr_hybrid_prepare checks
+ * every value the head can decode on the device and returns CX_STATUS_UNSUPPORTED naming a
+ * gene (or row offset) that is not -- order such genes after the head
+ * (cx_qcsr_head_order does). The tail runs on the row-group VALU
  * kernel from each row's first entry >= H, adds the head's sums and applies the epilogue.
  * W is F16 (the execution-order packed dense operand). Engine addition; the reference's
  * projection has no matrix-core path for CSR. */
@@ -1509,9 +1512,30 @@ int cx_qcsr_tail_plan(const cx_qcsr_matrix *a, const cx_qcsr_hybrid_layout *layo
 int cx_qcsr_tail_fill(const cx_qcsr_matrix *a, const cx_qcsr_hybrid_layout *layout, cx_qcsr_tail_stream *stream_out,
                       void *entries, uint64_t entry_bytes, void *stream);
 
+/* The execution order of a prepared projection (host arrays; counts from
+ * cx_qcsr_column_counts, metadata as the matrix holds it: scales [cols] or interleaved
+ * (scale, offset) pairs [2 * cols] for CX_DECODE_PER_GENE_AFFINE_PAIRS, offsets [cols] or
+ * NULL (0), row_offsets [rows] or NULL (0) under CX_DECODE_COLUMN_SCALE_ROW_OFFSET, scales
+ * NULL = 1). It is the popularity order (cx_popularity_order) except that genes the
+ * matrix-core head cannot carry exactly are moved after the head. A gene fits a layout
+ * exponent K when every decoded value times 2^K lies on the 2^-14 grid with its scaled
+ * metadata a normal float (under the row-offset policy: 2^K s on the grid, and 2^K r for every
+ * row offset) and its largest decoded magnitude (plus the largest |row offset| under that
+ * policy) is below 2^(15-K). The head is the most popular genes that fit the K under which
+ * they cover the most stored entries (whole 1,024-gene parts, at most head_cols); the
+ * layout's own exponent (14 - floor(log2) of the head's largest magnitude) is then at least K,
+ * so cx_qcsr_hybrid_prepare's check passes. Head genes keep their popularity order, then
+ * every other gene in popularity order. *head_out = the head width: head_cols capped at cols
+ * rounded down to 1,024, or fewer when fewer genes fit (0 when a row offset never does).
+ * Engine addition. */
+int cx_qcsr_head_order(const uint32_t *counts, uint32_t cols, uint32_t bits, uint32_t decode_policy,
+                       const float *scales, const float *offsets, const float *row_offsets, uint32_t rows,
+                       uint32_t head_cols, uint32_t *feature_permutation, uint32_t *inverse_permutation,
+                       uint32_t *head_out);
+
 /* ---- prepared execution-order projection ------------------------------------------------
- * One object that owns everything the prepared path reads: the popularity order of the genes
- * (cx_popularity_order), the per-gene metadata in that order, the dense head layout
+ * One object that owns everything the prepared path reads: the execution order of the genes
+ * (cx_qcsr_head_order), the per-gene metadata in that order, the dense head layout
  * (cx_qcsr_hybrid_prepare) and the tail stream (cx_qcsr_tail_plan / cx_qcsr_tail_fill) of the
  * matrix relabelled into that order. Built once per structure and code generation from the
  * canonical matrix `a` (quantized codes of 1/2/4/8 bits, any decode policy, each gene at most
@@ -1520,7 +1544,8 @@ int cx_qcsr_tail_fill(const cx_qcsr_matrix *a, const cx_qcsr_hybrid_layout *layo
  * gene order (row stride rhs_ld) is gathered into execution order in the workspace, then the
  * head (matrix cores) and the tail stream run; Y rows are the matrix's rows. Same values and
  * sums as cx_qcsr_spmm_fwd_hybrid on the relabelled matrix with the same head width.
- * head_cols: a multiple of 1,024 (capped at cols rounded down to 1,024; 0: no head).
+ * head_cols: a multiple of 1,024 (capped at cols rounded down to 1,024; 0: no head); the
+ * head used may be narrower when fewer genes decode exactly in it (cx_qcsr_exec_query).
  * cx_qcsr_exec_prepare allocates device memory and synchronizes `stream`; cx_qcsr_exec_spmm
  * allocates nothing and does not synchronize (workspace: 256-byte aligned,
  * cx_qcsr_exec_workspace_bytes). A projection may be launched from several streams at once

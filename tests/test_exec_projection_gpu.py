@@ -30,7 +30,7 @@ pytestmark = pytest.mark.gpu
 def _stepwise(m, w, head):
     """The same product by the step-by-step path of exec_order.py."""
     from cellerator_amd.exec_order import hybrid_prepare, hybrid_spmm, pack_rows
-    mx, order = _exec(m)
+    mx, order = _exec(m, head)
     return hybrid_spmm(hybrid_prepare(mx, head, stream_tail=True), pack_rows(order, w))
 
 
@@ -110,6 +110,50 @@ def test_c2_rows_at_the_benchmark_form(oracle):
     assert torch.equal(y.view(torch.int32), step.view(torch.int32))
     ref, mag = _referee_of(oracle, m, w)
     check_against_referee(oracle, ref, mag, y.cpu().numpy())
+    p.close()
+
+
+def test_wide_range_genes_leave_the_head(oracle):
+    """The three most stored genes get values the head cannot carry beside the others (a scale
+    of 1,000; values near zero; values crossing zero): the projection orders them after a
+    full 2,048-gene head. An identity W over those genes and 61 head genes returns every
+    decoded value bitwise (the head's split, the tail's fp32 sum), and a random W matches the
+    referee."""
+    import torch
+
+    from cellerator_amd.exec_order import ExecProjection, head_order
+    from tests.test_qcsr_parts_gpu import _rebuild
+    rng = np.random.default_rng(61)
+    fx = _skewed(oracle, rng, 900, 2600, 4, 1, hostile=0.0)
+    top = np.argsort(-np.bincount(fx["col_idx"], minlength=2600), kind="stable")[:3]
+    s_, o_ = fx["scales"].copy(), fx["offsets"].copy()
+    for g, (sg, og) in zip(top, ((1000.0, 0.5), (0.01, 0.01), (0.03, -0.2))):
+        s_[g], o_[g] = sg, og
+    fx = _rebuild(oracle, rng, dict(fx, scales=s_, offsets=o_), fx["row_ptr"], fx["col_idx"])
+    m = to_device_qcsr(fx)
+    order, h = head_order(m, 2048)
+    assert h == 2048
+    assert np.all(order.inverse_permutation.cpu().numpy()[top] >= 2048)
+    p = ExecProjection(m, 2048)
+    assert p.info().head_cols == 2048
+    genes = np.concatenate([top, order.feature_permutation.cpu().numpy()[:61]])
+    w = torch.zeros((2600, 64), dtype=torch.float16, device="cuda")
+    w[torch.from_numpy(genes.astype(np.int64)).cuda(), torch.arange(64, device="cuda")] = 1.0
+    y = p.spmm(w)
+    wr = torch.from_numpy((rng.standard_normal((2600, 64)) * 0.02).astype(np.float16)).cuda()
+    yr = p.spmm(wr)
+    torch.cuda.synchronize()
+    decoded = oracle.decode_csr(4, 1, fx["row_ptr"], fx["packed_row_ptr"], fx["col_idx"], fx["packed"],
+                                fx["scales"], fx["offsets"], None)
+    column = np.full(2600, -1)
+    column[genes] = np.arange(64)
+    rows = np.repeat(np.arange(900), np.diff(fx["row_ptr"]))
+    sel = column[fx["col_idx"]] >= 0
+    want = np.zeros((900, 64), np.float32)
+    want[rows[sel], column[fx["col_idx"][sel]]] = decoded[sel]
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    ref, mag = _referee(oracle, fx, wr.cpu().numpy())
+    check_against_referee(oracle, ref, mag, yr.cpu().numpy())
     p.close()
 
 

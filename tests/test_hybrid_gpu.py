@@ -16,16 +16,41 @@ from tests.helpers import check_against_referee, qcsr_to_host, quantized_fixture
 pytestmark = pytest.mark.gpu
 
 
-def _exec(m):
-    from cellerator_amd.exec_order import popularity_order, to_execution_order
-    order = popularity_order(m)
+def _exec(m, head):
+    """The matrix in the execution order a prepared projection with a `head`-gene head uses
+    (cx_qcsr_head_order: popularity order, genes the head cannot carry exactly after it); the
+    fixtures here have enough such genes for the full head."""
+    from cellerator_amd.exec_order import head_order, to_execution_order
+    order, h = head_order(m, head)
+    assert h == min(head, m.cols // 1024 * 1024), (h, head)
     return to_execution_order(m, order), order
 
 
-def _skewed(oracle, rng, rows, cols, bits, policy):
+def _head_metadata(rng, fx, hostile):
+    """Metadata the head carries exactly for most genes: decoded values from about 0.5 to 8.5
+    whatever the code width (offsets 0.5..1, scales 0.05..0.5 times 15 / qmax), or under the
+    row-offset policy scales and row offsets on a 2^-12 grid. A fraction `hostile` of the
+    genes gets values the head cannot always carry (offsets -0.5..1 with values crossing
+    zero at 0.05..0.5 steps; unrounded scales of 0.001..0.01 under row offsets)."""
+    cols, rows, qmax = fx["cols"], fx["rows"], (1 << fx["bits"]) - 1
+    scales = rng.uniform(0.05, 0.5, cols) * 15.0 / qmax
+    bad = rng.random(cols) < hostile
+    if fx["policy"] == 2:
+        scales = np.maximum(np.round(scales * 4096.0), 1.0) / 4096.0
+        scales[bad] = rng.uniform(0.001, 0.01, int(bad.sum()))
+        row_offsets = np.round(rng.uniform(-1.0, 1.0, rows) * 4096.0) / 4096.0
+        return dict(fx, scales=scales.astype(np.float32), row_offsets=row_offsets.astype(np.float32))
+    offsets = rng.uniform(0.5, 1.0, cols)
+    scales[bad] = rng.uniform(0.05, 0.5, int(bad.sum()))
+    offsets[bad] = rng.uniform(-0.5, 1.0, int(bad.sum()))
+    return dict(fx, scales=scales.astype(np.float32), offsets=offsets.astype(np.float32))
+
+
+def _skewed(oracle, rng, rows, cols, bits, policy, hostile=0.05):
     """Row lengths from 0 to all genes, genes drawn with a Zipf-like popularity so the
-    popularity order has a dense head."""
-    fx = quantized_fixture(oracle, rng, rows, cols, 10.0, bits, 1 if policy == 3 else policy)
+    popularity order has a dense head; metadata from _head_metadata."""
+    fx = _head_metadata(rng, quantized_fixture(oracle, rng, rows, cols, 10.0, bits, 1 if policy == 3 else policy),
+                        hostile)
     weight = 1.0 / np.arange(1, cols + 1) ** 1.1
     weight = weight[rng.permutation(cols)]
     lengths = np.minimum(rng.lognormal(np.log(250.0), 0.8, rows).astype(np.int64), cols)
@@ -59,7 +84,7 @@ def test_hybrid_matches_referee(oracle, bits, policy):
     m = to_device_qcsr(fx)
     if policy == 3:
         m = qcsr_pack_gene_affine(m)
-    mx, order = _exec(m)
+    mx, order = _exec(m, 2048)
     w = (rng.standard_normal((3100, 64)) * 0.02).astype(np.float16)
     wx = pack_rows(order, torch.from_numpy(w).cuda())
     p = hybrid_prepare(mx, 2048)
@@ -71,34 +96,35 @@ def test_hybrid_matches_referee(oracle, bits, policy):
     assert torch.equal(y.view(torch.int32), y2.view(torch.int32))
 
 
-def test_identity_panel_gives_exact_decoded_values(oracle):
-    """W = the identity on the first 64 execution genes: Y[r, c] is the decoded value of
-    (r, gene c), through the head's split and the tail's (zero) sum -- bitwise for
-    |x| >= 2^(9-k) and within 2^(-13-k) below (k = the layout's scale exponent)."""
+@pytest.mark.parametrize("bits,policy", [(4, 1), (8, 1), (2, 2)])
+def test_identity_panel_gives_exact_decoded_values(oracle, bits, policy):
+    """W = the identity on execution genes 0..31 (head) and 1024..1055 (tail): Y[r, c] is the
+    decoded value of (r, gene), through the head's three-part split or the tail's fp32 sum --
+    bitwise for every value, the head carrying only genes it decodes exactly."""
     import torch
 
     from cellerator_amd.exec_order import hybrid_prepare, hybrid_spmm
-    rng = np.random.default_rng(5)
-    fx = _skewed(oracle, rng, 600, 2100, 4, 1)
-    mx, order = _exec(to_device_qcsr(fx))
+    rng = np.random.default_rng(5 + bits)
+    fx = _skewed(oracle, rng, 600, 2100, bits, policy, hostile=0.2)
+    mx, order = _exec(to_device_qcsr(fx), 1024)
+    genes = np.concatenate([np.arange(32), 1024 + np.arange(32)])
     w = torch.zeros((2100, 64), dtype=torch.float16, device="cuda")
-    w[torch.arange(64), torch.arange(64)] = 1.0
+    w[torch.from_numpy(genes).cuda(), torch.arange(64, device="cuda")] = 1.0
     p = hybrid_prepare(mx, 1024)
     y = hybrid_spmm(p, w)
     torch.cuda.synchronize()
     h = qcsr_to_host(mx)
-    decoded = oracle.decode_csr(4, 1, h["row_ptr"], h["packed_row_ptr"], h["col_idx"], h["packed"],
-                                h["scales"], h["offsets"], None)
+    decoded = oracle.decode_csr(bits, policy, h["row_ptr"], h["packed_row_ptr"], h["col_idx"], h["packed"],
+                                h["scales"], h["offsets"], h["row_offsets"])
     want = np.zeros((600, 64), np.float32)
     rows = np.repeat(np.arange(600), np.diff(h["row_ptr"]))
-    sel = h["col_idx"] < 64
-    want[rows[sel], h["col_idx"][sel]] = decoded[sel]
+    column = np.full(2100, -1)
+    column[genes] = np.arange(64)
+    sel = column[h["col_idx"]] >= 0
+    want[rows[sel], column[h["col_idx"][sel]]] = decoded[sel]
     got = y.cpu().numpy()
-    k = p.scale_exp
-    big = np.abs(want) >= 2.0 ** (9 - k)
-    assert big.sum() > 1000
-    assert np.array_equal(got[big].view(np.uint32), want[big].view(np.uint32))
-    assert np.all(np.abs(got[~big] - want[~big]) <= 2.0 ** (-13 - k))
+    assert sel.sum() > 1000
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 def _layout_reference(h, head, rows_ld):
@@ -135,7 +161,7 @@ def test_dense_head_layout_is_bit_exact(oracle, bits, policy):
     m = to_device_qcsr(fx)
     if policy == 3:
         m = qcsr_pack_gene_affine(m)
-    mx, _ = _exec(m)
+    mx, _ = _exec(m, 2048)
     p = hybrid_prepare(mx, 2048)
     first, second, head_end, meta = hybrid_head_arrays(p)
     torch.cuda.synchronize()
@@ -198,8 +224,8 @@ def test_dense_head_layout_is_bit_exact(oracle, bits, policy):
         assert np.array_equal(lut[:, :n, 0], hi[:, :n]) and np.array_equal(lut[:, :n, 1], mid[:, :n])
         assert np.array_equal(lut[:, :n, 2], lo[:, :n])
         assert np.all(lut[:, n:, :] == 0) and np.all(lut[:, :, 3] == 0)
-        big = np.abs(x32[:, :n]) >= 2.0 ** 9
-        assert np.array_equal((hi + mid + lo)[:, :n][big], x32[:, :n][big])
+        # the head holds only genes whose every value splits exactly
+        assert np.array_equal((hi + mid + lo)[:, :n], x32[:, :n])
 
 
 @pytest.mark.parametrize("n,kind,beta", [(128, 0, 0.0), (64, 6, 0.5), (128, 2, -1.0)])
@@ -210,7 +236,7 @@ def test_hybrid_epilogue_and_wide_outputs(oracle, n, kind, beta):
     from cellerator_amd.exec_order import hybrid_prepare, hybrid_spmm, pack_rows
     rng = np.random.default_rng(3000 + n + kind)
     fx = _skewed(oracle, rng, 530, 2200, 4, 1)
-    mx, order = _exec(to_device_qcsr(fx))
+    mx, order = _exec(to_device_qcsr(fx), 2048)
     w = (rng.standard_normal((2200, n)) * 0.05).astype(np.float16)
     wx = pack_rows(order, torch.from_numpy(w).cuda())
     bias = (rng.standard_normal(n) * 0.3).astype(np.float32)
@@ -240,7 +266,7 @@ def test_hybrid_on_c3_rows(oracle):
     from cellerator_amd.synth import C3, dense_normal, generate_qcsr
     m = generate_qcsr(C3.scaled(5 * 256 + 61))
     w = dense_normal((m.cols, 64), 0.02, torch.float16, seed=3)
-    mx, order = _exec(qcsr_pack_gene_affine(m))
+    mx, order = _exec(qcsr_pack_gene_affine(m), 4096)
     wx = pack_rows(order, w)
     y = hybrid_spmm(hybrid_prepare(mx, 4096), wx)
     torch.cuda.synchronize()
@@ -261,7 +287,7 @@ def test_hybrid_on_c2_rows(oracle):
     from cellerator_amd.synth import C2, dense_normal, generate_qcsr
     m = generate_qcsr(C2.scaled(3 * 256 + 37))
     w = dense_normal((m.cols, 64), 0.02, torch.float16, seed=5)
-    mx, order = _exec(qcsr_pack_gene_affine(m))
+    mx, order = _exec(qcsr_pack_gene_affine(m), 6144)
     wx = pack_rows(order, w)
     p = hybrid_prepare(mx, 6144)
     y = hybrid_spmm(p, wx)
@@ -280,7 +306,7 @@ def test_hybrid_rejects_unsorted_rows_and_bad_metadata(oracle):
     from cellerator_amd import _native as N
     from cellerator_amd.exec_order import hybrid_prepare, hybrid_spmm
     rng = np.random.default_rng(9)
-    fx = _skewed(oracle, rng, 300, 2100, 4, 1)
+    fx = _skewed(oracle, rng, 300, 2100, 4, 1, hostile=0.0)
     m = to_device_qcsr(fx)  # canonical order, flags 0
     with pytest.raises(N.EngineError, match="sorted"):
         hybrid_prepare(m, 1024)
@@ -305,7 +331,7 @@ def test_hybrid_rejects_unsorted_rows_and_bad_metadata(oracle):
         hybrid_prepare(mn, 1024)
     # a layout used with another matrix
     p = hybrid_prepare(m, 1024)
-    other = to_device_qcsr(_skewed(oracle, np.random.default_rng(10), 301, 2100, 4, 1))
+    other = to_device_qcsr(_skewed(oracle, np.random.default_rng(10), 301, 2100, 4, 1, hostile=0.0))
     other.flags = N.QCSR_COLUMNS_SORTED
     w = torch.zeros((2100, 64), dtype=torch.float16, device="cuda")
     with pytest.raises(N.EngineError, match="not prepared for this matrix"):
@@ -315,3 +341,41 @@ def test_hybrid_rejects_unsorted_rows_and_bad_metadata(oracle):
 def dataclasses_replace(obj, **kw):
     import dataclasses
     return dataclasses.replace(obj, **kw)
+
+
+def test_head_refuses_values_it_cannot_carry(oracle):
+    """cx_qcsr_hybrid_prepare checks every value the head can decode: a head gene with a wide
+    range (scale 1,000: the layout scale drops, and the other genes' values fall off the 2^-14
+    grid) or with values near zero (offset and steps of 0.01) is refused, naming the
+    gene; under the row-offset policy a row offset off the grid is refused, naming the row.
+    The same genes placed after the head (cx_qcsr_head_order) are accepted."""
+    from cellerator_amd import _native as N
+    from cellerator_amd.exec_order import hybrid_prepare
+    from tests.test_qcsr_parts_gpu import _rebuild
+    rng = np.random.default_rng(19)
+    fx = _skewed(oracle, rng, 300, 2100, 4, 1, hostile=0.0)
+
+    def sorted_dev(f):
+        m = to_device_qcsr(f)
+        m.flags = N.QCSR_COLUMNS_SORTED
+        return m
+
+    assert hybrid_prepare(sorted_dev(fx), 1024).head_cols == 1024
+    for gene, scale, offset in ((3, 1000.0, 0.5), (700, 0.01, 0.01)):
+        s_, o_ = fx["scales"].copy(), fx["offsets"].copy()
+        s_[gene], o_[gene] = scale, offset
+        f = _rebuild(oracle, rng, dict(fx, scales=s_, offsets=o_), fx["row_ptr"], fx["col_idx"])
+        with pytest.raises(N.EngineError, match="does not decode exactly") as err:
+            hybrid_prepare(sorted_dev(f), 1024)
+        assert err.value.status == 3  # CX_STATUS_UNSUPPORTED
+        if gene == 700:
+            assert "head gene 700 " in str(err.value)
+        mx, _ = _exec(sorted_dev(f), 1024)  # the head order moves the gene behind the head
+        assert hybrid_prepare(mx, 1024).head_cols == 1024
+    fr = _skewed(oracle, rng, 300, 2100, 2, 2, hostile=0.0)
+    assert hybrid_prepare(sorted_dev(fr), 1024).head_cols == 1024
+    r_ = fr["row_offsets"].copy()
+    r_[17] = np.float32(0.01)
+    f = _rebuild(oracle, rng, dict(fr, row_offsets=r_), fr["row_ptr"], fr["col_idx"])
+    with pytest.raises(N.EngineError, match="offset of row 17 "):
+        hybrid_prepare(sorted_dev(f), 1024)

@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 from tests.helpers import check_against_referee, qcsr_to_host, to_device_qcsr
-from tests.test_hybrid_gpu import _exec, _referee, _skewed
+from tests.test_hybrid_gpu import _exec, _head_metadata, _referee, _skewed
 
 pytestmark = pytest.mark.gpu
 
@@ -119,7 +119,7 @@ def test_stream_layout_is_bit_exact(oracle, bits, head):
     from cellerator_amd.exec_order import hybrid_prepare, tail_arrays
     rng = np.random.default_rng(40 + bits + head)
     fx = _skewed(oracle, rng, 2100, 3100, bits, 1)
-    mx, _ = _exec(to_device_qcsr(fx))
+    mx, _ = _exec(to_device_qcsr(fx), head)
     p = hybrid_prepare(mx, head, stream_tail=True)
     torch.cuda.synchronize()
     slot_rows, index, entries = tail_arrays(p)
@@ -148,7 +148,7 @@ def test_stream_product_matches_referee(oracle, bits, policy, head):
     m = to_device_qcsr(fx)
     if policy == 3:
         m = qcsr_pack_gene_affine(m)
-    mx, order = _exec(m)
+    mx, order = _exec(m, head)
     w = (rng.standard_normal((3100, 64)) * 0.02).astype(np.float16)
     wx = pack_rows(order, torch.from_numpy(w).cuda())
     p = hybrid_prepare(mx, head, stream_tail=True)
@@ -167,7 +167,7 @@ def test_stream_epilogue_and_wide_outputs(oracle):
     from cellerator_amd.exec_order import hybrid_prepare, hybrid_spmm, pack_rows
     rng = np.random.default_rng(77)
     fx = _skewed(oracle, rng, 900, 2500, 4, 1)
-    mx, order = _exec(to_device_qcsr(fx))
+    mx, order = _exec(to_device_qcsr(fx), 1024)
     w = (rng.standard_normal((2500, 128)) * 0.02).astype(np.float16)
     wx = pack_rows(order, torch.from_numpy(w).cuda())
     bias = torch.from_numpy(rng.standard_normal(128).astype(np.float32)).cuda()
@@ -198,7 +198,7 @@ def test_long_rows_and_unsorted_rows(oracle):
     from tests.helpers import quantized_fixture
     rng = np.random.default_rng(91)
     rows, cols = 530, 2048 + 700
-    fx = quantized_fixture(oracle, rng, rows, cols, 5.0, 4, 1)
+    fx = _head_metadata(rng, quantized_fixture(oracle, rng, rows, cols, 5.0, 4, 1), 0.0)  # canonical order: a full head
     lengths = rng.integers(0, 40, rows)
     lengths[:20] = rng.integers(900, 1500, 20)  # dense rows: up to 1,500 entries, ~1,000 in one part
     row_ptr = np.zeros(rows + 1, np.int64)
@@ -236,7 +236,7 @@ def test_prepare_and_launch_on_a_side_stream(oracle):
     rng = np.random.default_rng(515)
     fx = _skewed(oracle, rng, 1400, 2600, 4, 1)
     m = to_device_qcsr(fx)
-    mx, order = _exec(m)
+    mx, order = _exec(m, 1024)
     w = torch.from_numpy((rng.standard_normal((2600, 64)) * 0.02).astype(np.float16)).cuda()
     wx = pack_rows(order, w)
     base = hybrid_spmm(hybrid_prepare(mx, 1024, stream_tail=True), wx)
@@ -265,7 +265,7 @@ def test_stream_layout_33_parts_head_0(oracle):
     from cellerator_amd.exec_order import hybrid_head_arrays, hybrid_prepare, hybrid_spmm, pack_rows, tail_arrays
     rng = np.random.default_rng(3333)
     fx = _skewed(oracle, rng, 1100, 34_000, 4, 1)
-    mx, order = _exec(to_device_qcsr(fx))
+    mx, order = _exec(to_device_qcsr(fx), 0)
     p = hybrid_prepare(mx, 0, stream_tail=True)
     torch.cuda.synchronize()
     assert int(p.tail.parts) == 34
