@@ -676,6 +676,10 @@ __global__ __launch_bounds__(kStreamWaves * kWave) void qcsr_spmm_stream(QcsrArg
                 // Steps in blocks of 4 stage slots; slots past a group's run hold pads (zero
                 // row, value 0), so a block may run past `cnt`. A full fill is straight-line
                 // code, which lets the weight reads of later blocks issue under earlier FMAs.
+                // Keep the steps predicated in this one form: a separate unpredicated branch
+                // for the fills before a layer's last was miscompiled by the ROCm 7.2 clang
+                // (the decode's temporaries were allocated to registers holding live
+                // accumulators, which the first step then read), giving wrong sums.
                 auto step4 = [&](int q) {
                     const uint4 ea = sp[2 * q], eb = sp[2 * q + 1];
                     const uint4 wa0 = *reinterpret_cast<const uint4 *>(wbase + (ea.x << 4));
