@@ -538,3 +538,40 @@ int or_spmm_bwd_values(uint32_t rows, const int32_t *row_ptr, const int32_t *col
     }
     return 0;
 }
+
+/* ---- digest_logical_dense (include/Cellerator/compute/math/referee.hh:219-244) ---- */
+static void or_digest_mix(uint64_t value, uint64_t d[2]) {
+    /* referee_detail::digest_mix (referee.hh:125-130) */
+    d[0] ^= value;
+    d[0] *= 1099511628211ull;
+    d[1] ^= value + 0x9e3779b97f4a7c15ull + (d[1] << 6u) + (d[1] >> 2u);
+}
+
+int or_digest_logical_dense(const void *values, uint64_t rows, uint64_t columns, uint64_t ld,
+                            int column_major, uint32_t value_type, uint64_t digest[2]) {
+    if (digest == NULL) return 1;
+    if (rows != 0u && columns != 0u) {  /* referee_detail::valid_dense (referee.hh:94-101) */
+        const uint64_t minimum = column_major ? rows : columns;
+        if (values == NULL || ld < minimum) return 1;
+    }
+    uint64_t d[2] = {1469598103934665603ull, 0x6a09e667f3bcc909ull};
+    or_digest_mix(rows, d);
+    or_digest_mix(columns, d);
+    or_digest_mix(value_type, d);
+    for (uint64_t r = 0; r < rows; ++r) {
+        for (uint64_t c = 0; c < columns; ++c) {
+            const uint64_t at = column_major ? c * ld + r : r * ld + c;  /* dense_offset */
+            double v;
+            if (value_type == OR_F16) v = (double)or_half_to_float(((const uint16_t *)values)[at]);
+            else if (value_type == OR_F32) v = (double)((const float *)values)[at];
+            else if (value_type == OR_F64) v = ((const double *)values)[at];
+            else return 3;
+            uint64_t bits;
+            memcpy(&bits, &v, sizeof bits);
+            or_digest_mix(bits, d);
+        }
+    }
+    digest[0] = d[0];
+    digest[1] = d[1];
+    return 0;
+}

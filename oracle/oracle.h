@@ -41,6 +41,13 @@
  *   or_compare
  *       - restates compare_spmm_reference (include/Cellerator/compute/math/referee.hh:143-211);
  *         pinned by planted-error tests in tests/test_oracle.py.
+ *   or_digest_logical_dense
+ *       - the reference test's property (tests/math_referee_foundation_test.cc:108-127: one
+ *         element changed by 0.25 changes the digest), layout invariance (row- and
+ *         column-major views of one logical matrix digest equally), f16/f32 views of equal
+ *         values differing only through the mixed type code. Parity of the exact digest
+ *         values is UNPINNED: no recorded digest exists in the reference, and referee.hh
+ *         needs cuda_fp16.h, so it cannot be built here.
  */
 #ifndef CELLERATOR_ORACLE_H
 #define CELLERATOR_ORACLE_H
@@ -196,6 +203,18 @@ int or_cpbp_canonical_f64(uint32_t rows, const uint32_t *row_offsets,
 /* within_tolerance rule of feature_weighted_row_reduction.cc:225-241 */
 int or_cpbp_within_tolerance(float reference, float candidate, double abs_tol,
                              double rel_tol);
+
+/* ---- determinism digest ----
+ * digest_logical_dense (include/Cellerator/compute/math/referee.hh:219-244, with
+ * referee_detail::dense_offset / valid_dense / read_dense / digest_mix at :85-130): two
+ * 64-bit lanes seeded (1469598103934665603, 0x6a09e667f3bcc909); rows, columns and the
+ * value type code are mixed in, then every element in logical row-major order as the bits
+ * of its float64 widening. Views are row-major (column_major = 0) or column-major with
+ * leading dimension ld. Returns 0 (ok), 1 (invalid_argument: NULL digest or an invalid
+ * view) or 3 (unsupported_type: a value type other than f16, f32, f64, met on the first
+ * element). */
+int or_digest_logical_dense(const void *values, uint64_t rows, uint64_t columns, uint64_t ld,
+                            int column_major, uint32_t value_type, uint64_t digest[2]);
 
 #ifdef __cplusplus
 }

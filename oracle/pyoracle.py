@@ -76,6 +76,8 @@ def lib() -> C.CDLL:
         _lib.or_build_packed_row_ptr.restype = C.c_int64
         _lib.or_compare.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_double, C.c_double,
                                     C.c_double, C.c_void_p, C.POINTER(Comparison)]
+        _lib.or_digest_logical_dense.argtypes = [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_int,
+                                                 C.c_uint32, C.POINTER(C.c_uint64 * 2)]
         _lib.or_spmm_referee.argtypes = [
             C.c_uint64, C.c_uint64, C.c_uint64, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
             C.c_void_p, C.c_int, C.c_uint64, C.c_void_p, C.c_int, C.c_int, C.c_uint64,
@@ -210,6 +212,20 @@ def compare(reference: np.ndarray, candidate: np.ndarray, abs_tol: float, rel_to
     d = out.as_dict()
     d["status"] = rc
     return d
+
+
+def digest_logical_dense(values: np.ndarray, column_major: bool = False, ld: int | None = None,
+                         shape: tuple[int, int] | None = None) -> tuple[int, tuple[int, int]]:
+    """(status, (low, high)) of digest_logical_dense over a 2-D f16/f32/f64 array (row-major
+    as given, or the array read column-major when column_major: its transpose's memory)."""
+    types = {np.dtype(np.float16): F16, np.dtype(np.float32): F32, np.dtype(np.float64): F64}
+    a = np.ascontiguousarray(values)
+    rows, cols = shape if shape is not None else (a.shape if not column_major else a.shape[::-1])
+    ld = ld if ld is not None else a.shape[1] if a.ndim == 2 else 0
+    out = (C.c_uint64 * 2)()
+    st = lib().or_digest_logical_dense(_p(a), rows, cols, ld, int(column_major),
+                                       types.get(a.dtype, 0), C.byref(out))
+    return st, (int(out[0]), int(out[1]))
 
 
 def _rhs_type(rhs: np.ndarray) -> int:

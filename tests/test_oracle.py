@@ -316,3 +316,39 @@ def test_bwd_values_adjoint_identity(oracle, rhs_dtype):
     dense = g.astype(np.float64) @ w.astype(np.float64).T
     rows_of = np.repeat(np.arange(rows), np.diff(row_ptr))
     assert np.allclose(gv, dense[rows_of, col_idx], rtol=1e-12, atol=1e-12)
+
+
+def test_digest_logical_dense_properties(oracle):
+    """digest_logical_dense (include/Cellerator/compute/math/referee.hh:219-244): the
+    reference test's property on its 2x2 fixture (one element changed by 0.25 changes the
+    digest, tests/math_referee_foundation_test.cc:108-127), equal digests for the row- and
+    column-major views of one logical matrix and for a strided view, the value type code in
+    the digest, empty views, and the invalid-argument and unsupported-type statuses. The
+    exact digest values are unpinned (no recorded value in the reference)."""
+    import numpy as np
+    view = np.array([[0.0, 30.0], [29.0, 74.0]], np.float32)
+    st, first = oracle.digest_logical_dense(view)
+    assert st == 0
+    changed = view.copy()
+    changed[1, 0] += 0.25
+    assert oracle.digest_logical_dense(changed)[1] != first
+    assert oracle.digest_logical_dense(view.copy())[1] == first
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((5, 7)).astype(np.float32)
+    st_r, d_r = oracle.digest_logical_dense(a)
+    st_c, d_c = oracle.digest_logical_dense(np.ascontiguousarray(a.T), column_major=True, ld=5, shape=(5, 7))
+    assert st_r == st_c == 0 and d_r == d_c
+    wide = np.zeros((5, 9), np.float32)
+    wide[:, :7] = a
+    assert oracle.digest_logical_dense(wide, ld=9, shape=(5, 7))[1] == d_r
+    # f16 and f32 views of the same values differ only through the type code
+    h = a.astype(np.float16)
+    assert oracle.digest_logical_dense(h)[1] != oracle.digest_logical_dense(h.astype(np.float32))[1]
+    assert oracle.digest_logical_dense(h.astype(np.float64))[1] != oracle.digest_logical_dense(h.astype(np.float32))[1]
+    # element order matters (a transposed operand is caught)
+    sq = rng.standard_normal((4, 4)).astype(np.float32)
+    assert oracle.digest_logical_dense(sq)[1] != oracle.digest_logical_dense(np.ascontiguousarray(sq.T))[1]
+    # empty views digest their shape only; invalid views and types are rejected
+    assert oracle.digest_logical_dense(np.zeros((0, 3), np.float32), shape=(0, 3))[0] == 0
+    assert oracle.digest_logical_dense(a, ld=6, shape=(5, 7))[0] == 1
+    assert oracle.digest_logical_dense(a.astype(np.int32))[0] == 3
