@@ -17,9 +17,10 @@ baseline (the oracle's row-parallel fp32 restatement timed on this host).
 
 Other configs: c2, c3n128 (the same path), c4 (Blocked-ELL on the matrix cores; block-major
 values copied once before timing, the row-major values timed beside them; --row-major for
-those alone), c5 (CP-BP warp-tile reduction).
+those alone), c4q (C4's block structure with 8-bit per-gene affine codes and f32 W, the
+reference's quantized Blocked-ELL projection), c5 (CP-BP warp-tile reduction).
 
-  python bench.py [--steps K] [--warmup W] [--config c3|c3n128|c2|c4|c5] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--config c3|c3n128|c2|c4|c4q|c5] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -36,6 +37,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+VALU_FP32_PEAK_TFLOPS = 78.6  # non-packed fp32 FMA (packed FP32 is disabled in every build)
 # Matrix-core head width of the prepared qCSR path per configuration, from sweeps in steps of
 # 1,024 genes: at C3, 2,048 and 3,072 measure level (2,048 keeps the smaller layout); C2's
 # genes (8-bit codes, 2,000 nnz per cell) stay above 7% density up to 6,144, its best width.
@@ -305,6 +307,63 @@ def parity_sample_qcsr(m, w, out, count: int, seed: int) -> dict:
             "max_relative_error": float(cmp["max_relative_error"])}
 
 
+def bench_bell_quantized(args, torch, cfg) -> dict:
+    """Config 4 with 8-bit per-gene affine codes: the reference's quantized Blocked-ELL
+    projection (quantized_blocked_ell_spmm_fwd_f32, f32 W) on C4's block structure, through
+    cx_bell_spmm_fwd (the per-element kernel), N = 256."""
+    import numpy as np
+
+    from cellerator_amd import BellMatrix, bell_spmm
+    from cellerator_amd.synth import dense_normal, generate_bell
+
+    g = generate_bell(cfg)
+    bs, n_out = g.block_size, cfg.n_out
+    gen = torch.Generator(device="cuda").manual_seed(cfg.seed)
+    codes = torch.randint(0, 256, (g.rows * g.ell_cols,), dtype=torch.uint8, device="cuda", generator=gen)
+    scales = torch.rand(g.cols, device="cuda", generator=gen) * 0.02 + 0.001
+    offsets = torch.rand(g.cols, device="cuda", generator=gen) * 0.5
+    m = BellMatrix(g.rows, g.cols, bs, g.ell_cols, g.block_col_idx, bits=8, decode_policy=1,
+                   row_stride_bytes=g.ell_cols, packed_values=codes, column_scales=scales, column_offsets=offsets)
+    del g
+    w = dense_normal((m.cols, n_out), 0.02, torch.float32, seed=cfg.seed + 7)
+    out = torch.empty((m.rows, n_out), dtype=torch.float32, device="cuda")
+    valid_blocks = int((m.block_col_idx != -1).sum().item())
+    stream = torch.cuda.current_stream()
+    wall_ms, ev = time_launches(torch, lambda: bell_spmm(m, w, out=out, stream=stream), args.steps, args.warmup,
+                                stream)
+    kern_ms = statistics.mean(ev)
+    alg_bytes = (valid_blocks * bs * bs + m.block_col_idx.numel() * 4 + m.cols * 8 + m.cols * n_out * 4
+                 + m.rows * n_out * 4)
+    flops = 2.0 * valid_blocks * bs * bs * n_out
+    achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
+    res = {
+        "metric": "quantized Blocked-ELL SpMM (8-bit codes, f32 W): effective HBM GB/s (% roofline), 500k x 20k, N=256",
+        "value": valid_blocks * bs * bs / (wall_ms * 1e-3), "unit": "stored block elements/s",
+        "ms_per_step": wall_ms, "dtype": "u8-codes/f32-W/f32-accumulate",
+        "config": {"workload": cfg.name + " 8-bit codes", "rows": m.rows, "genes": m.cols, "block_size": bs,
+                   "valid_blocks": valid_blocks, "n_out": n_out, "seed": hex(cfg.seed)},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "bell_spmm_generic<8-bit, per-gene affine> (cx_bell_spmm_fwd)",
+                     "kernel_ms_mean": kern_ms, "kernel_ms_median": statistics.median(ev),
+                     "algorithmic_bytes": alg_bytes, "fp32_fma_tflops": flops / (kern_ms * 1e-3) / 1e12,
+                     "valu_fp32_peak_tflops_nonpacked": VALU_FP32_PEAK_TFLOPS},
+    }
+    from oracle import pyoracle
+    pyoracle.build()
+    rb = min(4096 // bs, m.rows // bs)
+    rows = rb * bs
+    idx = m.block_col_idx[:rb].cpu().numpy().view(np.uint32)
+    ref, mag = pyoracle.bell_spmm_referee(rows, m.cols, bs, m.ell_cols, idx, None, w.cpu().numpy(), bits=8,
+                                          policy=1, row_stride_bytes=m.ell_cols,
+                                          packed=codes[:rows * m.ell_cols].cpu().numpy(),
+                                          scales=scales.cpu().numpy(), offsets=offsets.cpu().numpy())
+    cmp = pyoracle.compare(ref, out[:rows].cpu().numpy(), 2.0 ** -20, 1e-4, mag)
+    res["parity_sample"] = {"rows": rows, "within_tolerance": bool(cmp["within_tolerance"]),
+                            "max_relative_error": float(cmp["max_relative_error"])}
+    return res
+
+
 def bench_bell(args, torch, cfg) -> dict:
     """Config 4: Blocked-ELL bf16 SpMM on MFMA (cx_bell_spmm_fwd_packed), N = 256."""
     import numpy as np
@@ -548,7 +607,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c3", choices=["c3", "c3n128", "c2", "c4", "c5"])
+    ap.add_argument("--config", default="c3", choices=["c3", "c3n128", "c2", "c4", "c4q", "c5"])
     ap.add_argument("--rows", type=int, default=0, help="override the row count (smaller runs)")
     ap.add_argument("--cpu-rows", type=int, default=0,
                     help="rows of the CPU-baseline sample (0: the whole matrix)")
@@ -590,12 +649,12 @@ def main() -> int:
         args.cpu_rows = 1 << 31  # the whole matrix
     from cellerator_amd.synth import C2, C3
 
-    if args.config in ("c4", "c5"):
+    if args.config in ("c4", "c4q", "c5"):
         from cellerator_amd.synth import C4, C5
-        cfg = C4 if args.config == "c4" else C5
+        cfg = C5 if args.config == "c5" else C4
         if args.rows:
             cfg = cfg.scaled(args.rows)
-        res = (bench_bell if args.config == "c4" else bench_cpbp)(args, torch, cfg)
+        res = {"c4": bench_bell, "c4q": bench_bell_quantized, "c5": bench_cpbp}[args.config](args, torch, cfg)
     else:
         cfg, n_out = {"c3": (C3, 64), "c3n128": (C3, 128), "c2": (C2, 64)}[args.config]
         if args.rows:

@@ -138,6 +138,68 @@ class CxCpbpReductionView(C.Structure):
                 ("order_row_domain_identity", u64), ("tiles", CxCpbpTiles)]
 
 
+class CxFwrPlanView(C.Structure):
+    """cellpack::feature_weighted_row_reduction_plan_view (40 bytes)."""
+    _fields_ = [("semantic_plan_schema_version", u32), ("geometry_identity_version", u32),
+                ("feature_count", u32), ("feature_block_count", u32),
+                ("feature_block_geometry_identity", u64), ("feature_block_offsets", p_void),
+                ("feature_permutation", p_void)]
+
+
+class CxLocalCellOrderView(C.Structure):
+    """cellpack::local_cell_order_view (128 bytes)."""
+    _fields_ = [("order_schema_version", u32), ("signature_algorithm_version", u32), ("kind", u32),
+                ("window_size", u32), ("group_width", u32), ("reserved0", u32), ("seed", u64),
+                ("ordering_identity", u64), ("global_row_begin", u64), ("full_row_count", u32),
+                ("row_count", u32), ("feature_block_count", u32), ("reserved1", u32),
+                ("feature_block_geometry_identity", u64), ("row_domain_identity", u64),
+                ("primary_keys", p_void), ("secondary_keys", p_void), ("active_block_counts", p_void),
+                ("row_nnz_counts", p_void), ("row_permutation", p_void), ("inverse_row_permutation", p_void)]
+
+
+class CxWarpTileView(C.Structure):
+    """cellpack::warp_tile_view (176 bytes)."""
+    _fields_ = [("tile_schema_version", u32), ("record_schema_version", u32),
+                ("semantic_plan_schema_version", u32), ("geometry_identity_version", u32),
+                ("order_schema_version", u32), ("reserved0", u32), ("tile_identity", u64),
+                ("feature_block_geometry_identity", u64), ("ordering_identity", u64),
+                ("global_row_begin", u64), ("full_row_count", u32), ("row_count", u32),
+                ("feature_count", u32), ("feature_block_count", u32), ("tile_row_width", u32),
+                ("tile_count", u32), ("nnz_count", u32), ("tile_block_count", u32),
+                ("row_block_entry_count", u32), ("value_size_bytes", u32), ("feature_axis_fingerprint", u64),
+                ("feature_axis_fingerprint_version", u32), ("reserved1", u32), ("row_domain_identity", u64),
+                ("tile_block_offsets", p_void), ("tile_block_ids", p_void), ("tile_block_cell_masks", p_void),
+                ("block_row_entry_offsets", p_void), ("row_block_gene_masks", p_void),
+                ("row_block_value_offsets", p_void), ("values", p_void)]
+
+
+class CxNativeTileBlockMetrics(C.Structure):
+    _fields_ = [("active_rows", u32), ("active_features", u32), ("nnz", u32), ("dense_workload", u32),
+                ("density", C.c_double), ("feature_reuse", C.c_double)]
+
+
+class CxNativeTileRequirements(C.Structure):
+    _fields_ = [("union_mask_count", u64), ("packed_offset_count", u64), ("block_metric_count", u64),
+                ("sidecar_bytes", u64)]
+
+
+class CxNativeTileBuffers(C.Structure):
+    _fields_ = [("union_mask_capacity", u64), ("union_gene_masks", p_void), ("packed_offset_capacity", u64),
+                ("packed_value_offsets", p_void), ("block_metric_capacity", u64), ("block_metrics", p_void)]
+
+
+class CxNativeTileView(C.Structure):
+    """math::native_tile_view (384 bytes)."""
+    _fields_ = [("schema_version", u32), ("reserved", u32), ("plan", CxFwrPlanView),
+                ("order", CxLocalCellOrderView), ("tiles", CxWarpTileView), ("union_gene_masks", p_void),
+                ("packed_value_offsets", p_void), ("block_metrics", p_void), ("dense_workload", u64)]
+
+
+class CxNativeTileDecodedValue(C.Structure):
+    _fields_ = [("value_index", u32), ("execution_row", u32), ("canonical_row", u32), ("reserved0", u32),
+                ("global_row", u64), ("execution_feature", u32), ("canonical_feature", u32), ("value", p_void)]
+
+
 class CxCpk1Metadata(C.Structure):
     _fields_ = [("feature_axis_fingerprint", u64), ("feature_axis_fingerprint_version", u32),
                 ("row_domain_kind", u32), ("row_domain_identity", u64),
@@ -339,6 +401,21 @@ ENGINE_SIGNATURES = {
                                     C.POINTER(CxQcsrTailStream), p_void, u64, p_void]),
     "cx_qcsr_spmm_fwd_hybrid": (C.c_int, [C.POINTER(CxQcsrMatrix), C.POINTER(CxQcsrHybridLayout), p_void, i64,
                                           i64, p_void, i64, C.POINTER(CxSpmmEpilogue), p_void, u64, p_void]),
+    "cx_query_native_tile_requirements_host": (C.c_int, [C.POINTER(CxFwrPlanView), C.POINTER(CxLocalCellOrderView),
+                                                         C.POINTER(CxWarpTileView),
+                                                         C.POINTER(CxNativeTileRequirements)]),
+    "cx_build_native_tile_view_host": (C.c_int, [C.POINTER(CxFwrPlanView), C.POINTER(CxLocalCellOrderView),
+                                                 C.POINTER(CxWarpTileView), C.POINTER(CxNativeTileBuffers),
+                                                 C.POINTER(CxNativeTileView)]),
+    "cx_query_native_tile_requirements_from_cpk1_host": (C.c_int, [C.POINTER(CxCpk1View),
+                                                                   C.POINTER(CxNativeTileRequirements)]),
+    "cx_build_native_tile_view_from_cpk1_host": (C.c_int, [C.POINTER(CxCpk1View), C.POINTER(CxNativeTileBuffers),
+                                                           C.POINTER(CxNativeTileView)]),
+    "cx_decode_native_tile_value_host": (C.c_int, [C.POINTER(CxNativeTileView), u32,
+                                                   C.POINTER(CxNativeTileDecodedValue)]),
+    "cx_cpbp_tiles_from_native_view": (C.c_int, [C.POINTER(CxNativeTileView), C.POINTER(CxCpbpTiles)]),
+    "cx_native_tile_view_rebind": (C.c_int, [C.POINTER(CxNativeTileView), p_void, u64, p_void,
+                                             C.POINTER(CxNativeTileView)]),
     "cx_qcsr_head_order": (C.c_int, [p_void, u32, u32, u32, p_void, p_void, p_void, u32, u32, p_void, p_void,
                                      C.POINTER(u32)]),
     "cx_qcsr_exec_prepare": (C.c_int, [C.POINTER(CxQcsrMatrix), u32, C.POINTER(p_void), p_void]),

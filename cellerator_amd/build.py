@@ -44,6 +44,7 @@ ENGINE_SOURCES = [
     "cpk1.cpp",
     "bell_plan.cpp",
     "exec_order.hip",
+    "native_tile.cpp",
     "exec_csr.cpp",
     "bell_lowering.cpp",
     "spmm_request.cpp",

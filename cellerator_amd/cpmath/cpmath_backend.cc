@@ -477,17 +477,31 @@ core::operation_status run_cpbp(const core::prepared_operation &p,
     const projection_state *s = state_of(p);
     if (s == nullptr) return fail(code::execution_failed, "prepared operation has no live projection state");
     const projection_declaration &d = s->declaration;
-    const void *view = physical_view(*s, l, sizeof(cx_cpbp_tiles));
-    if (view == nullptr) return bad_launch("sparse operand does not carry the prepared CP-BP tile view");
+    // The engine's tile view, or the reference's native tile view (its math projection of
+    // the same partition, native_tile_view.hh:45-54), which aliases the compact values.
     cx_cpbp_tiles t;
-    std::memcpy(&t, view, sizeof(t));
+    bool native = false;
+    const void *view = physical_view(*s, l, sizeof(cx_cpbp_tiles));
+    if (view != nullptr) {
+        std::memcpy(&t, view, sizeof(t));
+        if (t.values != nullptr) return bad_launch("CP-BP values travel in the value plane");
+    } else if ((view = physical_view(*s, l, sizeof(cx_native_tile_view))) != nullptr) {
+        cx_native_tile_view nv;
+        std::memcpy(&nv, view, sizeof(nv));
+        if (nv.packed_value_offsets == nullptr || cx_cpbp_tiles_from_native_view(&nv, &t) != CX_STATUS_SUCCESS)
+            return bad_launch("sparse operand's native tile view is not a built v1 view");
+        native = true;
+    } else {
+        return bad_launch("sparse operand does not carry the prepared CP-BP tile view");
+    }
     if (t.row_count != d.rows || t.feature_count != d.cols
         || t.nnz_count != d.structure.logical_edge_count)
         return bad_launch("CP-BP tile view differs from the declared projection");
-    if (t.values != nullptr) return bad_launch("CP-BP values travel in the value plane");
+    const void *aliased = t.values;
     const bool checked = s->cpbp.validated;
     if (checked) {
         cx_cpbp_tiles bound = t;  // the plane supplies values and their type
+        bound.values = nullptr;
         bound.value_dtype = 0u;
         if (std::memcmp(&bound, &s->cpbp.tiles, sizeof(bound)) != 0)
             return bad_launch("CP-BP tile view differs from the reduction view validated by prepare_cpbp_state");
@@ -497,6 +511,8 @@ core::operation_status run_cpbp(const core::prepared_operation &p,
         || plane->quantization.kind != execution::quantization_kind::none
         || plane->element_count != t.nnz_count)
         return bad_launch("one projection-order value plane of nnz values is required");
+    if (native && aliased != nullptr && aliased != plane->values)
+        return bad_launch("the native tile view's values are not the bound value plane");
     t.values = plane->values;
     t.value_dtype = engine_dtype(plane->numeric.storage);
     const execution::dense_tensor_view &w = l.inputs[1].storage.dense;
@@ -509,7 +525,8 @@ core::operation_status run_cpbp(const core::prepared_operation &p,
     const int rc = cx_cpbp_reduce(&t, static_cast<const float *>(w.data), d.cols,
                                   static_cast<float *>(y.data), d.rows, l.stream.stream);
     if (rc != CX_STATUS_SUCCESS) return engine_failed(rc);
-    dispatched = checked ? "cpbp:checked" : "cpbp:unchecked";
+    dispatched = native ? (checked ? "cpbp:native-tile+checked" : "cpbp:native-tile")
+                        : (checked ? "cpbp:checked" : "cpbp:unchecked");
     return {};
 }
 

@@ -30,7 +30,10 @@
 //   inputs[0]  sparse_relation (axes cells x genes). projection_data points to the
 //              engine's typed physical view of the structure -- cx_qcsr_matrix,
 //              cx_bell_matrix or cx_cpbp_tiles -- with every value pointer NULL, and
-//              projection_bytes == sizeof of that view.
+//              projection_bytes == sizeof of that view. A CP-BP projection may instead
+//              carry the reference's native_tile_view (cx_native_tile_view, same layout,
+//              native_tile_view.hh:45-54, built with its sidecars): its compact values must
+//              then be the bound value plane's or NULL.
 //   values[0]  the value plane of that structure: quantized codes (u8 storage, per-gene
 //              affine as quantization_kind::per_module with one group per gene) or plain
 //              f16 / bf16 / f32 values.
@@ -165,7 +168,7 @@ core::operation_status prepare_cpbp_state(execution::projection_handle projectio
 
 // Kernel form the last successful run on this thread dispatched, e.g.
 // "qcsr:pairs+sorted", "qcsr:gene-affine", "qcsr:execution-order", "bell:grouped+panel",
-// "bell:mfma+repack", "bell:generic", "cpbp:checked".
+// "bell:mfma+repack", "bell:generic", "cpbp:checked", "cpbp:native-tile".
 const char *last_dispatch() noexcept;
 
 core::operation_candidate quantized_csr_candidate() noexcept;

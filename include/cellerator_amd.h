@@ -1245,6 +1245,155 @@ int cx_cpbp_reduce_checked(const cx_cpbp_reduction_view *view, const float *feat
  * validate a view once and launch cx_cpbp_reduce on its tiles many times. */
 int cx_cpbp_reduction_validate(const cx_cpbp_reduction_view *view);
 
+/* ---- native tile view: the reference's math projection of a CP-BP partition ----------------
+ * Layout-identical mirrors of cellpack::feature_weighted_row_reduction_plan_view
+ * (components/CellPack/include/CellPack/feature_weighted_row_reduction.hh:19-27, 40 bytes),
+ * cellpack::local_cell_order_view (local_cell_ordering.hh:47-67, 128 bytes),
+ * cellpack::warp_tile_view (warp_tiles.hh:49-79, 176 bytes) and
+ * cellerator::compute::math::native_tile_view with its sidecars
+ * (include/Cellerator/compute/math/native_tile_view.hh:17-64; view 384 bytes, block metrics
+ * 32 bytes), so a view the reference's own adapter built can be passed by pointer. The
+ * reserved fields name the padding the C++ layout has there. v1 tiles: u32 cell masks,
+ * tile_row_width <= 32. */
+typedef struct cx_fwr_plan_view {
+    uint32_t semantic_plan_schema_version;
+    uint32_t geometry_identity_version;
+    uint32_t feature_count;
+    uint32_t feature_block_count;
+    uint64_t feature_block_geometry_identity;
+    const uint32_t *feature_block_offsets;
+    const uint32_t *feature_permutation;
+} cx_fwr_plan_view;
+typedef struct cx_local_cell_order_view {
+    uint32_t order_schema_version;
+    uint32_t signature_algorithm_version;
+    uint32_t kind;
+    uint32_t window_size;
+    uint32_t group_width;
+    uint32_t reserved0;
+    uint64_t seed;
+    uint64_t ordering_identity;
+    uint64_t global_row_begin;
+    uint32_t full_row_count;
+    uint32_t row_count;
+    uint32_t feature_block_count;
+    uint32_t reserved1;
+    uint64_t feature_block_geometry_identity;
+    uint64_t row_domain_identity;
+    const uint64_t *primary_keys;
+    const uint32_t *secondary_keys;
+    const uint32_t *active_block_counts;
+    const uint32_t *row_nnz_counts;
+    const uint32_t *row_permutation;
+    const uint32_t *inverse_row_permutation;
+} cx_local_cell_order_view;
+typedef struct cx_warp_tile_view {
+    uint32_t tile_schema_version;
+    uint32_t record_schema_version;
+    uint32_t semantic_plan_schema_version;
+    uint32_t geometry_identity_version;
+    uint32_t order_schema_version;
+    uint32_t reserved0;
+    uint64_t tile_identity;
+    uint64_t feature_block_geometry_identity;
+    uint64_t ordering_identity;
+    uint64_t global_row_begin;
+    uint32_t full_row_count;
+    uint32_t row_count;
+    uint32_t feature_count;
+    uint32_t feature_block_count;
+    uint32_t tile_row_width;
+    uint32_t tile_count;
+    uint32_t nnz_count;
+    uint32_t tile_block_count;
+    uint32_t row_block_entry_count;
+    uint32_t value_size_bytes;
+    uint64_t feature_axis_fingerprint;
+    uint32_t feature_axis_fingerprint_version;
+    uint32_t reserved1;
+    uint64_t row_domain_identity;
+    const uint32_t *tile_block_offsets;
+    const uint32_t *tile_block_ids;
+    const uint32_t *tile_block_cell_masks;
+    const uint32_t *block_row_entry_offsets;
+    const uint32_t *row_block_gene_masks;
+    const uint32_t *row_block_value_offsets;
+    const void *values;
+} cx_warp_tile_view;
+/* native_tile_block_metrics / _requirements / _buffers (native_tile_view.hh:17-41). */
+typedef struct cx_native_tile_block_metrics {
+    uint32_t active_rows;
+    uint32_t active_features;
+    uint32_t nnz;
+    uint32_t dense_workload;
+    double density;
+    double feature_reuse;
+} cx_native_tile_block_metrics;
+typedef struct cx_native_tile_requirements {
+    uint64_t union_mask_count;
+    uint64_t packed_offset_count;
+    uint64_t block_metric_count;
+    uint64_t sidecar_bytes;
+} cx_native_tile_requirements;
+typedef struct cx_native_tile_buffers {
+    uint64_t union_mask_capacity;
+    uint32_t *union_gene_masks;
+    uint64_t packed_offset_capacity;
+    uint32_t *packed_value_offsets;
+    uint64_t block_metric_capacity;
+    cx_native_tile_block_metrics *block_metrics;
+} cx_native_tile_buffers;
+#define CX_NATIVE_TILE_VIEW_SCHEMA 1u
+typedef struct cx_native_tile_view {
+    uint32_t schema_version;  /* CX_NATIVE_TILE_VIEW_SCHEMA */
+    uint32_t reserved;
+    cx_fwr_plan_view plan;
+    cx_local_cell_order_view order;
+    cx_warp_tile_view tiles;
+    const uint32_t *union_gene_masks;
+    const uint32_t *packed_value_offsets;
+    const cx_native_tile_block_metrics *block_metrics;
+    uint64_t dense_workload;
+} cx_native_tile_view;
+/* native_tile_decoded_value (native_tile_view.hh:66-76). */
+typedef struct cx_native_tile_decoded_value {
+    uint32_t value_index;
+    uint32_t execution_row;
+    uint32_t canonical_row;
+    uint32_t reserved0;
+    uint64_t global_row;
+    uint32_t execution_feature;
+    uint32_t canonical_feature;
+    const void *value;
+} cx_native_tile_decoded_value;
+/* query_native_tile_requirements_host / build_native_tile_view_host /
+ * decode_native_tile_value_host and their CPK1 forms (native_tile_view.hh:78-136,
+ * src/compute/math/native_tile_view.cc): host only; the view aliases plan, order, tiles and
+ * values, only the sidecars are new. Statuses: INVALID_ARGUMENT (invalid argument,
+ * incompatible identity, small sidecars), INVALID_SHAPE (invalid geometry, overflow); the
+ * message is the reference's. The CPK1 forms take the engine's view of a validated (or
+ * rebound) image and fill plan, order and tiles from it. */
+int cx_query_native_tile_requirements_host(const cx_fwr_plan_view *plan, const cx_local_cell_order_view *order,
+                                           const cx_warp_tile_view *tiles, cx_native_tile_requirements *out);
+int cx_build_native_tile_view_host(const cx_fwr_plan_view *plan, const cx_local_cell_order_view *order,
+                                   const cx_warp_tile_view *tiles, const cx_native_tile_buffers *buffers,
+                                   cx_native_tile_view *out);
+int cx_query_native_tile_requirements_from_cpk1_host(const cx_cpk1_view *payload, cx_native_tile_requirements *out);
+int cx_build_native_tile_view_from_cpk1_host(const cx_cpk1_view *payload, const cx_native_tile_buffers *buffers,
+                                             cx_native_tile_view *out);
+int cx_decode_native_tile_value_host(const cx_native_tile_view *view, uint32_t value_index,
+                                     cx_native_tile_decoded_value *out);
+/* The engine's tile operand of a native view (for cx_cpbp_reduce): plan arrays, tiles,
+ * row permutation; value_dtype from value_size_bytes (2: F16, 4: F32). Host, no checks
+ * beyond the schema and the value size. */
+int cx_cpbp_tiles_from_native_view(const cx_native_tile_view *view, cx_cpbp_tiles *out);
+/* A view built on a validated host CPK1 image moved to an equal copy of the image (its
+ * device upload): plan, order and tile pointers inside [old_base, old_base + bytes) move by
+ * new_base - old_base (rebind_persistent_packing_payload's rule, persistent_packing_payload.hh:
+ * 81-86); sidecars and pointers outside the image stay. */
+int cx_native_tile_view_rebind(const cx_native_tile_view *view, const void *old_base, uint64_t bytes,
+                               const void *new_base, cx_native_tile_view *out);
+
 /* ---- execution feature order: packed dense operand and execution-order CSR ---------------
  * feature_permutation[e] = the canonical gene at execution position e (cx_cpbp_plan's
  * convention). X . W does not change when the genes of X and the rows of W are relabelled

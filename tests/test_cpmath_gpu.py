@@ -427,3 +427,56 @@ def test_blocked_ell_prepared_panel_and_groups(monkeypatch):
     torch.cuda.synchronize()
     assert torch.equal(y2.view(torch.int32), bell_spmm_grouped(m, bell_pack_rhs(w2), groups, n).view(torch.int32))
     del N
+
+
+def test_cpbp_native_tile_view_through_reference_core(oracle):
+    """The reference's native tile view (cx_native_tile_view, its layout) as the CP-BP
+    operand: built on a validated host CPK1 image with its sidecars, moved to the uploaded
+    copy (cx_native_tile_view_rebind), bound with the image's values as the value plane. The
+    core runs it (dispatch "cpbp:native-tile"), bitwise equal to the reduction on the image's
+    tiles; a view whose values are not the bound plane is rejected."""
+    import torch
+
+    from cellerator_amd import _native as N
+    from cellerator_amd import cpbp, cpbp_reduce, cpk1
+    from tests.test_cpbp_build import random_csr, random_plan
+    rng = np.random.default_rng(29)
+    plan = random_plan(rng, 600)
+    offs, feats, vals = random_csr(rng, 2100, 600, 20.0, np.float16)
+    tiles = cpbp.build_tiles(plan, offs, feats, vals, group_width=32, window_size=1024)
+    meta = cpk1.Metadata(0xA11, 0xB22, 5_000, global_row_begin=700, group_width=32, window_size=1024)
+    image, host = cpk1.write_image(plan, tiles, meta)  # host: the validated view of `image`
+    lib = N.engine()
+    req = N.CxNativeTileRequirements()
+    assert lib.cx_query_native_tile_requirements_from_cpk1_host(C.byref(host), C.byref(req)) == 0, lib.cx_last_error()
+    unions = np.zeros(req.union_mask_count, np.uint32)
+    offsets = np.zeros(req.packed_offset_count, np.uint32)
+    metrics = (N.CxNativeTileBlockMetrics * req.block_metric_count)()
+    bufs = N.CxNativeTileBuffers(unions.size, unions.ctypes.data, offsets.size, offsets.ctypes.data,
+                                 len(metrics), C.addressof(metrics))
+    view_host = N.CxNativeTileView()
+    assert lib.cx_build_native_tile_view_from_cpk1_host(C.byref(host), C.byref(bufs), C.byref(view_host)) == 0
+    dev = cpk1.upload(host, image)
+    view = N.CxNativeTileView()
+    assert lib.cx_native_tile_view_rebind(C.byref(view_host), image.ctypes.data, image.nbytes,
+                                          dev.image.data_ptr(), C.byref(view)) == 0
+    assert view.tiles.values == dev.view.tiles.values and view.union_gene_masks == unions.ctypes.data
+    nnz = int(view.tiles.nnz_count)
+    w = torch.from_numpy(rng.standard_normal(600).astype(np.float32)).cuda()
+    y = torch.full((2100,), float("nan"), device="cuda")
+
+    def case(values_ptr):
+        return H.HCase(kind=H.KIND_CPBP, view=C.addressof(view), view_bytes=C.sizeof(view), variant=0,
+                       rows=2100, cols=600, out_cols=0, block_size=0, sparse_type=H.NT_F16,
+                       dense_type=H.NT_F32, nnz=nnz, values=values_ptr, value_count=nnz, value_bytes=nnz * 2,
+                       w=w.data_ptr(), w_ld=1, y=y.data_ptr(), y_ld=1,
+                       stream=torch.cuda.current_stream().cuda_stream, device=torch.cuda.current_device())
+
+    r = H.run(case(view.tiles.values))
+    assert (r.prepare_status, r.status) == (H.OK, H.OK), (r.message, r.engine)
+    assert r.dispatch == b"cpbp:native-tile"
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), cpbp_reduce(dev, w).view(torch.int32))
+    other = torch.empty(nnz, dtype=torch.float16, device="cuda")
+    r = H.run(case(other.data_ptr()))
+    assert r.status == H.INVALID_LAUNCH
