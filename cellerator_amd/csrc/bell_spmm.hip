@@ -16,7 +16,9 @@
 //     (0xffffffff) are skipped without touching their values;
 //   * row blocks are visited in an XCD-major order so consecutive row blocks of the
 //     schedule share one XCD's L2 (the weight panel is re-read from L2, not HBM).
-// Generic path (any other dtype / block size / N, quantized BELL): one wave per row,
+// Quantized path (codes of any width, 32x32 blocks, f32 W, N a multiple of 64): fp32 matrix
+// cores, bell_spmm_quant_mfma below.
+// Generic path (any other dtype / block size / N): one wave per row,
 // lanes over output columns, slots in order, decoded with the codec exactly as
 // quantized_blocked_ell_spmm_fwd_kernel_ does
 // (src/compute/sparse/project/kernels/quantized_blocked_ell_spmm_fwd_kernel_.cuh:1-39).
@@ -721,6 +723,140 @@ __global__ __launch_bounds__(256) void bell_spmm_generic(BellArgs a, std::uint32
     }
 }
 
+// Quantized Blocked-ELL on the matrix cores (codes of 1/2/4/8 bits, either decode policy,
+// 32x32 blocks, f32 W, N a multiple of 64): the reference's quantized projection
+// (quantized_blocked_ell_spmm_fwd_f32, src/compute/sparse/project/project.cu:108-168) with
+// every value decoded exactly as its kernel does, fma(code, scale, offset) in fp32, and the
+// products on v_mfma_f32_32x32x2_f32 (fp32 operands, fp32 accumulation: only the summation
+// order differs). One workgroup of 4 waves per 32-row block; wave w takes the 64-column
+// chunks w, w + 4, ... as two 32x32 accumulator tiles. Per valid slot (block column bc),
+// lane l (row m = l % 32 of the block, K parity h = l / 32) loads its row's 32 codes of the
+// block (kBits dwords) and the (scale, offset) of gene bc * 32 + m, and per K step kk of 2
+// (genes 2kk, 2kk + 1) decodes the code of gene 2kk + h with that gene's metadata taken from
+// lanes 2kk and 2kk + 1 (readlane), so A[m][h] = x, and loads B[h][n] = W[gene][column n].
+// Genes past `cols` (a last partial block column) read as 0 in both operands. The next valid
+// slot's codes, metadata and W are loaded while the current slot's matrix instructions run.
+template<int kBits>
+struct QuantSlot {
+    std::uint32_t codes[kBits];  // this lane's row: the block's 32 codes, kBits * 32 bits
+    float meta[2];               // scale and offset of gene bc * 32 + lane % 32
+    float w[16][2];              // B operands: K step x 32-column tile
+};
+
+template<int kBits, int kPolicy>
+__global__ __launch_bounds__(256) void bell_spmm_quant_mfma(BellArgs a, std::int64_t n) {
+    constexpr int kTiles = 2;  // 64 output columns per wave and chunk
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    const std::uint32_t row_blocks = (a.rows + 31u) / 32u;
+    const std::uint32_t rb = xcd_major(blockIdx.x, gridDim.x);
+    if (rb >= row_blocks) return;
+    const std::uint32_t width = a.ell_cols / 32u;
+    const std::uint32_t *slots = a.block_col_idx + static_cast<std::uint64_t>(rb) * width;
+    const int m = lane % 32;
+    const int h = lane / 32;
+    const std::uint32_t row = rb * 32u + static_cast<std::uint32_t>(m);
+    // this row block's codes; rows past the matrix read as 0 (their sums are not stored)
+    const std::uint32_t block_rows = min(32u, a.rows - rb * 32u);
+    const rsrc_t rc = make_rsrc(a.packed + static_cast<std::uint64_t>(rb) * 32u * a.row_stride_bytes,
+                                block_rows * a.row_stride_bytes);
+    const std::uint32_t code_lane = static_cast<std::uint32_t>(m) * a.row_stride_bytes;
+    const float row_offset = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET && row < a.rows ? a.row_offsets[row] : 0.0f;
+    const float *w = static_cast<const float *>(a.rhs);
+
+    for (std::int64_t n0 = static_cast<std::int64_t>(wave) * 64; n0 < n; n0 += 256) {
+        auto load_slot = [&](QuantSlot<kBits> &f, std::uint32_t s, std::uint32_t bc) {
+            const std::uint32_t co = code_lane + s * static_cast<std::uint32_t>(kBits) * 4u;
+            if constexpr (kBits >= 4) {
+#pragma unroll
+                for (int q = 0; q < kBits / 4; ++q) {
+                    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rc, static_cast<int>(co) + 16 * q, 0, 0);
+                    f.codes[4 * q] = v[0]; f.codes[4 * q + 1] = v[1]; f.codes[4 * q + 2] = v[2]; f.codes[4 * q + 3] = v[3];
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < kBits; ++q)
+                    f.codes[q] = static_cast<std::uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rc, static_cast<int>(co) + 4 * q, 0, 0));
+            }
+            const std::uint32_t g = bc * 32u + static_cast<std::uint32_t>(m);
+            const bool in = g < a.cols;
+            f.meta[0] = in && a.scales != nullptr ? a.scales[g] : (in ? 1.0f : 0.0f);
+            f.meta[1] = kPolicy == CX_DECODE_PER_GENE_AFFINE && in && a.offsets != nullptr ? a.offsets[g] : 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < 16; ++kk) {
+                const std::uint32_t gk = bc * 32u + static_cast<std::uint32_t>(2 * kk + h);
+#pragma unroll
+                for (int t = 0; t < kTiles; ++t)
+                    f.w[kk][t] = gk < a.cols ? w[static_cast<std::int64_t>(gk) * a.rhs_ld + n0 + 32 * t + m] : 0.0f;
+            }
+        };
+
+        cx_floatx16 acc[kTiles];
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
+
+        auto mfma_slot = [&](const QuantSlot<kBits> &f, std::uint32_t bc) {
+#pragma unroll
+            for (int kk = 0; kk < 16; ++kk) {
+                // gene 2kk + h of the block: its code in this lane's row, its metadata from
+                // lane 2kk + h (the lane that loaded gene 2kk + h's pair)
+                const int bit = (2 * kk) * kBits;  // first bit of gene 2kk; gene 2kk + 1 follows
+                const std::uint32_t word = f.codes[bit / 32];
+                const std::uint32_t code = (word >> ((bit % 32) + h * kBits)) & ((1u << kBits) - 1u);
+                const float se = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f.meta[0]), 2 * kk));
+                const float so = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f.meta[0]), 2 * kk + 1));
+                const float oe = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f.meta[1]), 2 * kk));
+                const float oo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f.meta[1]), 2 * kk + 1));
+                const float scale = h != 0 ? so : se;
+                const float offset = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET ? row_offset : (h != 0 ? oo : oe);
+                const bool in = bc * 32u + static_cast<std::uint32_t>(2 * kk + h) < a.cols;
+                const float x = in ? __builtin_fmaf(static_cast<float>(code), scale, offset) : 0.0f;
+#pragma unroll
+                for (int t = 0; t < kTiles; ++t)
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(x, f.w[kk][t], acc[t], 0, 0, 0);
+            }
+        };
+
+        // valid slots in order; the next one's operands load while the current one's run
+        std::uint32_t s = 0u;
+        while (s < width && slots[s] == kInvalidBlock) ++s;
+        if (s < width) {
+            QuantSlot<kBits> f0, f1;
+            std::uint32_t bc0 = slots[s];
+            load_slot(f0, s, bc0);
+            for (;;) {
+                std::uint32_t t1 = s + 1u;
+                while (t1 < width && slots[t1] == kInvalidBlock) ++t1;
+                const bool more = t1 < width;
+                const std::uint32_t bc1 = more ? slots[t1] : bc0;
+                load_slot(f1, more ? t1 : s, bc1);
+                __builtin_amdgcn_sched_barrier(0);
+                mfma_slot(f0, bc0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (!more) break;
+                s = t1;
+                bc0 = bc1;
+                f0 = f1;
+            }
+        }
+
+        // D layout: lane holds column lane % 32; element i is row 8 (i / 4) + 4 h + i % 4
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) {
+            const std::int64_t col = n0 + 32 * t + m;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const std::uint32_t r = rb * 32u + 8u * (i / 4) + 4u * static_cast<std::uint32_t>(h) + (i % 4);
+                if (r < a.rows)
+                    a.out[static_cast<std::int64_t>(r) * a.out_ld + col] =
+                        a.ep.active ? epilogue_value(a.ep, acc[t][i], r, col) : acc[t][i];
+            }
+        }
+    }
+}
+
 int validate_bell(const cx_bell_matrix *m, const void *rhs, std::int64_t rhs_ld,
                   std::int64_t out_cols, const float *out, std::int64_t out_ld) {
     if (m == nullptr || rhs == nullptr || out == nullptr)
@@ -808,6 +944,29 @@ extern "C" int cx_bell_spmm_fwd_epilogue(const cx_bell_matrix *m, const void *rh
         return fail(CX_STATUS_UNSUPPORTED, "Blocked-ELL rhs must be F32, F16 or BF16");
     if (m->rows == 0u) return CX_STATUS_SUCCESS;
     const BellArgs a = make_args(m, rhs, rhs_ld, out, out_ld, ep);
+    if (m->bits != 0u && m->block_size == 32u && rhs_dtype == CELLERATOR_DTYPE_F32 && out_cols % 64 == 0
+        && m->row_stride_bytes % 4u == 0u && m->row_stride_bytes >= m->ell_cols * m->bits / 8u
+        && static_cast<std::uint64_t>(m->row_stride_bytes) * 32u <= 0xffffffffull) {
+        // the matrix-core form (same values, fp32 products and sums in another order)
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        const dim3 grid((m->rows + 31u) / 32u), block(256);
+#define CX_QBELL(B)                                                                                      \
+    do {                                                                                                 \
+        if (m->decode_policy == CX_DECODE_PER_GENE_AFFINE)                                               \
+            hipLaunchKernelGGL((bell_spmm_quant_mfma<B, CX_DECODE_PER_GENE_AFFINE>), grid, block, 0, s, a, out_cols); \
+        else                                                                                             \
+            hipLaunchKernelGGL((bell_spmm_quant_mfma<B, CX_DECODE_COLUMN_SCALE_ROW_OFFSET>), grid, block, 0, s, a, \
+                               out_cols);                                                                \
+    } while (0)
+        switch (m->bits) {
+        case 1: CX_QBELL(1); break;
+        case 2: CX_QBELL(2); break;
+        case 4: CX_QBELL(4); break;
+        default: CX_QBELL(8); break;
+        }
+#undef CX_QBELL
+        return check_launch("bell_spmm_quant_mfma");
+    }
     const std::uint64_t threads = static_cast<std::uint64_t>(m->rows) * kWave;
     hipLaunchKernelGGL(bell_spmm_generic, dim3(static_cast<unsigned>((threads + 255) / 256)),
                        dim3(256), 0, static_cast<hipStream_t>(stream), a, m->value_dtype,

@@ -165,3 +165,56 @@ def test_grouped_rejects_groups_that_do_not_cover():
     bad = BellGroups(0, 0, 1, torch.zeros(2, dtype=torch.int32).cuda(), torch.zeros(1, dtype=torch.int32).cuda())
     with pytest.raises(EngineError, match="INVALID_SHAPE"):
         bell_spmm_grouped(m, packed, bad, 64)
+
+
+def _quantized_bell_32(rng, rows, cols, width, bits, policy):
+    """32x32 blocks, ragged last row block and block column, invalid slots anywhere."""
+    rb, kb = (rows + 31) // 32, (cols + 31) // 32
+    idx = np.full((rb, width), 0xFFFFFFFF, np.uint32)
+    for b in range(rb):
+        c = int(rng.integers(1 if b == 0 else 0, min(width, kb) + 1))
+        picks = np.sort(rng.choice(kb, size=c, replace=False))
+        if b == 0 and kb - 1 not in picks:
+            picks[-1] = kb - 1  # the ragged block column in use (each block column once per row block)
+        where = np.sort(rng.choice(width, size=c, replace=False))
+        idx[b, where] = np.sort(picks)
+    stride = width * 32 * bits // 8
+    packed = rng.integers(0, 256, size=rows * stride).astype(np.uint8)
+    scales = rng.uniform(0.1, 0.5, cols).astype(np.float32)
+    offsets = rng.uniform(-0.5, 0.5, cols).astype(np.float32)
+    row_off = rng.uniform(-1, 1, rows).astype(np.float32)
+    return idx, stride, packed, scales, offsets, row_off
+
+
+@pytest.mark.parametrize("bits,policy,n", [(8, 1, 256), (4, 2, 64), (2, 1, 128), (1, 2, 64), (8, 2, 192)])
+def test_quantized_bell_matrix_cores(oracle, bits, policy, n):
+    """Quantized Blocked-ELL with 32x32 blocks and f32 W runs on the fp32 matrix cores
+    (bell_spmm_quant_mfma): within the bound of the float64 referee for every width and policy,
+    ragged row block and block column, invalid slots anywhere; a one-hot W returns every
+    decoded value bitwise (the codec's fma(code, scale, offset)); a fused epilogue applies."""
+    import torch
+
+    from cellerator_amd import BellMatrix, Epilogue, bell_spmm
+    rng = np.random.default_rng(100 * bits + 10 * policy + n)
+    rows, cols, width = 75, 70, 4
+    idx, stride, packed, scales, offsets, row_off = _quantized_bell_32(rng, rows, cols, width, bits, policy)
+    t = lambda a: None if a is None else torch.from_numpy(a).cuda()  # noqa: E731
+    m = BellMatrix(rows, cols, 32, width * 32, t(idx.view(np.int32)), bits=bits, decode_policy=policy,
+                   row_stride_bytes=stride, packed_values=t(packed), column_scales=t(scales),
+                   column_offsets=t(offsets) if policy == 1 else None, row_offsets=t(row_off) if policy == 2 else None)
+    kw = dict(bits=bits, policy=policy, row_stride_bytes=stride, packed=packed, scales=scales,
+              offsets=offsets if policy == 1 else None, row_offsets=row_off if policy == 2 else None)
+    rhs = rng.standard_normal((cols, n)).astype(np.float32)
+    ref, mag = oracle.bell_spmm_referee(rows, cols, 32, width * 32, idx, None, rhs, **kw)
+    out = bell_spmm(m, t(rhs))
+    # one-hot W: column c reads gene c % cols
+    onehot = np.zeros((cols, n), np.float32)
+    onehot[np.arange(n) % cols, np.arange(n)] = 1.0
+    dec, _ = oracle.bell_spmm_referee(rows, cols, 32, width * 32, idx, None, onehot, **kw)
+    hot = bell_spmm(m, t(onehot))
+    bias = rng.standard_normal(n).astype(np.float32)
+    ep_out = bell_spmm(m, t(rhs), epilogue=Epilogue(kind=1, bias=t(bias)))  # bias
+    torch.cuda.synchronize()
+    check_against_referee(oracle, ref, mag, out.cpu().numpy())
+    assert np.array_equal(hot.cpu().numpy().astype(np.float64), dec)
+    check_against_referee(oracle, ref + bias[None, :].astype(np.float64), mag, ep_out.cpu().numpy())
