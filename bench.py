@@ -627,6 +627,8 @@ def main() -> int:
                          "1M x 33,538) and 6,144 for C2 (8-bit codes, 100k x 20k, denser genes)")
     ap.add_argument("--canonical", action="store_true",
                     help="qCSR: headline the canonical row-group kernel on the unprepared CSR")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="c3: skip the secondary configurations timed after the headline")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="run only a plain copy of BYTES (rocprofv3 counter calibration)")
     args = ap.parse_args()
@@ -647,26 +649,56 @@ def main() -> int:
         return calibrate_copy(args.calibrate_copy, max(args.steps, 1))
     if args.cpu_rows <= 0:
         args.cpu_rows = 1 << 31  # the whole matrix
-    from cellerator_amd.synth import C2, C3
-
-    if args.config in ("c4", "c4q", "c5"):
-        from cellerator_amd.synth import C4, C5
-        cfg = C5 if args.config == "c5" else C4
-        if args.rows:
-            cfg = cfg.scaled(args.rows)
-        res = {"c4": bench_bell, "c4q": bench_bell_quantized, "c5": bench_cpbp}[args.config](args, torch, cfg)
-    else:
-        cfg, n_out = {"c3": (C3, 64), "c3n128": (C3, 128), "c2": (C2, 64)}[args.config]
-        if args.rows:
-            cfg = cfg.scaled(args.rows)
-        res = bench_qcsr(args, torch, cfg, n_out)
+    res = run_config(args, torch, args.config)
     line = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"),
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": res.pop("ms_per_step"), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": res.pop("dtype"), "data": "synthetic (seeded, generated on GPU)",
             **res}
+    if args.config == "c3" and not args.no_secondary and not args.rows and not args.canonical:
+        line["secondary"] = secondary_configs(args, torch)
     print(json.dumps(line), flush=True)
     return 0
+
+
+def run_config(args, torch, name: str) -> dict:
+    from cellerator_amd.synth import C2, C3
+    if name in ("c4", "c4q", "c5"):
+        from cellerator_amd.synth import C4, C5
+        cfg = C5 if name == "c5" else C4
+        if args.rows:
+            cfg = cfg.scaled(args.rows)
+        return {"c4": bench_bell, "c4q": bench_bell_quantized, "c5": bench_cpbp}[name](args, torch, cfg)
+    cfg, n_out = {"c3": (C3, 64), "c3n128": (C3, 128), "c2": (C2, 64)}[name]
+    if args.rows:
+        cfg = cfg.scaled(args.rows)
+    return bench_qcsr(args, torch, cfg, n_out)
+
+
+def secondary_configs(args, torch) -> dict:
+    """The other benchmark configurations, timed in the same run after the headline (10 steps
+    after 3 warmup, no CPU leg): C3 at N = 128, C2, C4 (Blocked-ELL bf16), C4 with 8-bit codes
+    (quantized Blocked-ELL, f32 W) and C5 (CP-BP). Each entry keeps the configuration's own
+    metric, the kernel's roofline fraction and its parity sample against the referee."""
+    import copy
+
+    out = {}
+    for name in ("c3n128", "c2", "c4", "c4q", "c5"):
+        torch.cuda.empty_cache()
+        a = copy.copy(args)
+        a.config, a.steps, a.warmup, a.no_cpu = name, 10, 3, True
+        a.head = HEAD_GENES.get(name, 2048)
+        t0 = time.perf_counter()
+        r = run_config(a, torch, name)
+        roof = r.get("roofline", {})
+        out[name] = {"workload": r.get("config", {}).get("workload"), "metric": r["metric"], "value": r["value"],
+                     "unit": r["unit"], "ms_per_step": r["ms_per_step"], "dtype": r["dtype"],
+                     "kernel": roof.get("kernel"), "kernel_ms_mean": roof.get("kernel_ms_mean"),
+                     "roofline_frac": roof.get("frac"), "roofline_unit": roof.get("unit"),
+                     "parity_sample": r.get("parity_sample"), "seconds": time.perf_counter() - t0}
+        log(f"secondary {name}: {r['ms_per_step']:.3f} ms/step")
+    torch.cuda.empty_cache()
+    return out
 
 
 if __name__ == "__main__":
