@@ -8,7 +8,7 @@ Inputs are generated seeded on the GPU and are resident in HBM before timing sta
 
 One step = one launch of the prepared execution-order path over the whole matrix
 (cx_qcsr_exec_spmm, what the CP-Math execution-order candidate runs: canonical W gathered into
-execution order, the 2,048 most stored genes on the matrix cores (6,144 for c2), the rest through
+execution order, the 2,048 most stored genes on the matrix cores (3,072 for c2), the rest through
 the prepared tail stream; the projection is prepared once, untimed), with the canonical
 cx_qcsr_spmm_fwd kernel timed beside it (--canonical makes it the headline).
 Prints ONE JSON line: metric/value (nnz/s), ms_per_step, roofline of the kernels
@@ -39,9 +39,9 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 VALU_FP32_PEAK_TFLOPS = 78.6  # non-packed fp32 FMA (packed FP32 is disabled in every build)
 # Matrix-core head width of the prepared qCSR path per configuration, from sweeps in steps of
-# 1,024 genes: at C3, 2,048 and 3,072 measure level (2,048 keeps the smaller layout); C2's
-# genes (8-bit codes, 2,000 nnz per cell) stay above 7% density up to 6,144, its best width.
-HEAD_GENES = {"c3": 2048, "c3n128": 2048, "c2": 6144}
+# 1,024 genes: at C3 2,048 (3,072 and 4,096 slower); at C2 3,072 (2,048 and 4,096 within 4%,
+# 6,144 13% slower), with C2's 100k rows spread over every compute unit in the tail walk.
+HEAD_GENES = {"c3": 2048, "c3n128": 2048, "c2": 3072}
 
 
 def log(msg: str) -> None:
@@ -624,7 +624,7 @@ def main() -> int:
                     help="qCSR: matrix-core head genes of the prepared execution-order path (a multiple "
                          "of 1,024; 0: the whole matrix through the tail stream; -1 skips the path). "
                          "Default: the measured best per configuration, 2,048 for C3 (4-bit codes, "
-                         "1M x 33,538) and 6,144 for C2 (8-bit codes, 100k x 20k, denser genes)")
+                         "1M x 33,538) and 3,072 for C2 (8-bit codes, 100k x 20k, denser genes)")
     ap.add_argument("--canonical", action="store_true",
                     help="qCSR: headline the canonical row-group kernel on the unprepared CSR")
     ap.add_argument("--no-secondary", action="store_true",

@@ -287,7 +287,7 @@ class CxQcsrTailStream(C.Structure):
 
 class CxQcsrExecInfo(C.Structure):
     _fields_ = [("rows", u32), ("cols", u32), ("bits", u32), ("head_cols", u32), ("nnz", u64),
-                ("tail_fills", u64), ("persistent_bytes", u64), ("head_form", u32), ("reserved", u32)]
+                ("tail_fills", u64), ("persistent_bytes", u64), ("head_form", u32), ("tail_blocks", u32)]
 
 
 # ---- public context ABI structs (include/Cellerator/abi.h layout) ----

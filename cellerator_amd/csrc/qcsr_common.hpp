@@ -31,12 +31,13 @@ struct QcsrArgs {
     const float *acc_init;
     std::uint32_t first_part;
     // Prepared tail stream (qcsr_spmm_stream only; built by qcsr_stream.hip): the row of
-    // every (block, wave, layer, group) slot, the fill index, the entries in fill order, and
-    // the number of gene parts the stream covers (from first_part on).
+    // every (block, wave, layer, group) slot, the fill index, the entries in fill order, the
+    // number of gene parts the stream covers (from first_part on) and its block count.
     const std::uint32_t *slot_rows;
     const std::uint32_t *fill_index;
     const void *stream_entries;
     std::uint32_t stream_parts;
+    std::uint32_t stream_blocks;
 };
 
 // Geometry of the prepared tail stream, shared by its builder and its kernel: 16 waves of
@@ -53,6 +54,29 @@ constexpr int kStreamWaves = 16;
 constexpr int kStreamLayers = 8;
 constexpr int kStreamSlots = kStreamWaves * kStreamLayers;        // (wave, layer) per block and part
 constexpr int kStreamRows = kStreamSlots * 8;
+
+// Workgroups of a row-group walk over `rows` rows, each at most `max_rows` rows and at least
+// one set of 8 (any count in [ceil(rows / max_rows), ceil(rows / 8)] is a valid geometry).
+// When ceil(rows / max_rows) full workgroups would not fill one round of `units` (one per
+// compute unit at a time), the rows are spread over `units` workgroups: 100k rows keep all
+// 256 CUs busy instead of 98. Beyond that, `whole_rounds` rounds the count up to whole
+// rounds (the canonical kernel's 1M rows: 2,048 workgroups of ~488 rows instead of 1,954
+// full ones, measured 3% faster); otherwise the fewest full workgroups are kept (the tail
+// walk's 977 blocks ran 1% faster than 1,024 smaller ones: the dispatcher balances the
+// partial last round better than equal rounds do).
+inline std::uint32_t round_block_count(std::uint32_t rows, std::uint32_t max_rows, std::uint32_t units,
+                                       bool whole_rounds) {
+    const std::uint32_t need = static_cast<std::uint32_t>((static_cast<std::uint64_t>(rows) + max_rows - 1) / max_rows);
+    const std::uint32_t sets = static_cast<std::uint32_t>((static_cast<std::uint64_t>(rows) + 7) / 8);
+    if (units == 0u || need == 0u || (need >= units && !whole_rounds)) return need;
+    const std::uint64_t blocks = (static_cast<std::uint64_t>(need) + units - 1u) / units * units;
+    return blocks < sets ? static_cast<std::uint32_t>(blocks) : sets;
+}
+
+// Workgroups per round: the environment's CX_BLOCKS_PER_ROUND when it is a positive integer
+// (1 gives the fewest full workgroups), else the current device's compute units (0 when the
+// query fails).
+std::uint32_t blocks_per_round();
 constexpr std::uint32_t kFillMask = 0x0fffffffu;
 constexpr int kStreamPartGenes = 1024;
 constexpr std::uint32_t kStreamPad = 1024u;                       // gene of a pad entry: a zero row

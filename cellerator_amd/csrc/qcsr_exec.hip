@@ -414,6 +414,7 @@ extern "C" int cx_qcsr_exec_query(const cx_qcsr_exec_projection *p, cx_qcsr_exec
     i.tail_fills = p->tail.fills;
     i.persistent_bytes = p->persistent_bytes;
     i.head_form = p->layout.head_form;
+    i.tail_blocks = p->tail.blocks;
     *info = i;
     return CX_STATUS_SUCCESS;
 }

@@ -1098,7 +1098,9 @@ int launch_hybrid(const cx_qcsr_matrix &mm, const cx_qcsr_hybrid_layout &L, cons
     if (ts != nullptr) {
         const std::uint32_t all_parts = (m->cols + kHeadAlign - 1u) / kHeadAlign;
         if (ts->rows != m->rows || ts->bits != m->bits || ts->nnz != m->nnz || ts->first_part != L.head_cols / kHeadAlign
-            || ts->parts != all_parts - ts->first_part || ts->blocks != (m->rows + kStreamRows - 1u) / kStreamRows
+            || ts->parts != all_parts - ts->first_part
+            || ts->blocks < (std::uint64_t{m->rows} + kStreamRows - 1u) / kStreamRows
+            || ts->blocks > (std::uint64_t{m->rows} + 7u) / 8u
             || ts->block_rows != kStreamRows || ts->layers != kStreamLayers
             || ts->slot_rows == nullptr || ts->fill_index == nullptr || ts->entries == nullptr)
             return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_spmm_fwd_hybrid: the tail stream was not built for this layout");
@@ -1106,6 +1108,7 @@ int launch_hybrid(const cx_qcsr_matrix &mm, const cx_qcsr_hybrid_layout &L, cons
         a.fill_index = ts->fill_index;
         a.stream_entries = ts->entries;
         a.stream_parts = ts->parts;
+        a.stream_blocks = ts->blocks;
         a.first_part = ts->first_part;
     }
     // one 64-column block of the tail: the prepared stream, else the row-group kernel

@@ -177,13 +177,13 @@ struct GroupsShared {
 // block's longest rows are several times its median.
 template<int kWaves, int kLayers>
 __device__ __forceinline__ void assign_groups(GroupPrologue<kWaves, kLayers> &pro, std::uint32_t *rows_out,
-                                              const std::int32_t *row_ptr, std::uint32_t rows, std::uint32_t first,
+                                              const std::int32_t *row_ptr, std::uint32_t end_row, std::uint32_t first,
                                               int tid) {
     constexpr int kRows = kWaves * kLayers * 8;
     constexpr int kSets = kRows / 8;
     int *len = pro.len;
-    const std::uint32_t row = first + static_cast<std::uint32_t>(tid);
-    if (tid < kRows) len[tid] = row < rows ? row_ptr[row + 1] - row_ptr[row] : -1;
+    const std::uint32_t row = first + static_cast<std::uint32_t>(tid);  // the block's rows: [first, end_row)
+    if (tid < kRows) len[tid] = row < end_row ? row_ptr[row + 1] - row_ptr[row] : -1;
     __syncthreads();
     int rank = 0;
     if (tid < kRows) {
@@ -233,7 +233,7 @@ __device__ __forceinline__ void assign_groups(GroupPrologue<kWaves, kLayers> &pr
         }
     }
     __syncthreads();
-    if (tid < kRows) rows_out[pro.set_slot[rank / 8] * 8 + rank % 8] = row < rows ? row : kNoRow;
+    if (tid < kRows) rows_out[pro.set_slot[rank / 8] * 8 + rank % 8] = row < end_row ? row : kNoRow;
     __syncthreads();
 }
 
@@ -271,7 +271,6 @@ __device__ __forceinline__ int fill_count(int run, int f) {
 template<int kBits, int kPolicy, int kWaves, int kLayers, bool kSorted>
 __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
     using Shared = GroupsShared<kWaves, kLayers>;
-    constexpr int kRows = Shared::kRows;
     constexpr int kCodeDw = kBits == 8 ? 3 : 2;
     constexpr std::uint32_t kMask = (1u << kBits) - 1u;
     __shared__ Shared sh;
@@ -280,12 +279,14 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
     const int lane = tid % kWave;
     const int grp = lane >> 3;
     const int j = lane & 7;
-    const std::uint32_t first = blockIdx.x * static_cast<std::uint32_t>(kRows);
-    const std::uint32_t last = first + kRows < a.rows ? first + kRows : a.rows;
+    // The block's rows: an even share [first, last) of the matrix, at most Shared::kRows (the
+    // launch uses at least ceil(rows / Shared::kRows) blocks).
+    const std::uint32_t first = static_cast<std::uint32_t>(std::uint64_t{blockIdx.x} * a.rows / gridDim.x);
+    const std::uint32_t last = static_cast<std::uint32_t>((std::uint64_t{blockIdx.x} + 1u) * a.rows / gridDim.x);
 
     if (tid < 8) sh.w[kPadGene * 8 + tid] = make_uint4(0u, 0u, 0u, 0u);
     if (tid == 8) sh.meta[kPadGene] = make_float2(0.0f, 0.0f);
-    assign_groups<kWaves, kLayers>(sh.u.pro, sh.rows, a.row_ptr, a.rows, first, tid);
+    assign_groups<kWaves, kLayers>(sh.u.pro, sh.rows, a.row_ptr, last, first, tid);
 
     // The block's entries and packed bytes, addressed by 32-bit buffer offsets.
     const int wg_begin = __builtin_amdgcn_readfirstlane(a.row_ptr[first]);
@@ -968,8 +969,7 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_bwd_values_groups(BwdPart
 template<int kBits, int kPolicy>
 int launch_bits_groups(const QcsrArgs &a, hipStream_t stream) {
     constexpr int kWaves = 16, kLayers = 4;
-    const unsigned rows_per_block = kWaves * kLayers * 8;
-    const dim3 grid((a.rows + rows_per_block - 1) / rows_per_block), block(kWaves * kWave);
+    const dim3 grid(round_block_count(a.rows, kWaves * kLayers * 8, blocks_per_round(), true)), block(kWaves * kWave);
     if ((a.flags & CX_QCSR_COLUMNS_SORTED) != 0u)
         hipLaunchKernelGGL((qcsr_spmm_groups<kBits, kPolicy, kWaves, kLayers, true>), grid, block, 0, stream, a);
     else
@@ -1021,8 +1021,7 @@ int launch_bwd_values_parts(const std::int32_t *row_ptr, const std::int32_t *col
 }
 
 int launch_qcsr_stream(const QcsrArgs &a, std::uint32_t bits, std::uint32_t policy, hipStream_t stream) {
-    const unsigned blocks = (a.rows + kStreamRows - 1) / kStreamRows;
-    const dim3 grid(blocks), block(kStreamWaves * kWave);
+    const dim3 grid(a.stream_blocks), block(kStreamWaves * kWave);
 #define CX_STREAM(B, P) hipLaunchKernelGGL((qcsr_spmm_stream<B, P>), grid, block, 0, stream, a)
 #define CX_STREAM_POLICY(B)                                                                         \
     do {                                                                                            \

@@ -5,8 +5,9 @@
 //
 // Geometry (qcsr_common.hpp): the rows are sorted by tail length over the whole matrix
 // (descending, ties by row); sets of 8 consecutive rows of that order are dealt round-robin
-// to blocks of 1,024 rows, so each set's rows end their runs together and every block holds
-// the same mix of lengths. In each block the sets go, heaviest first, to the least-loaded of
+// to blocks of at most 1,024 rows, so each set's rows end their runs together and every block
+// holds the same mix of lengths. The block count follows round_block_count: the fewest full
+// blocks, or one block per compute unit when those would leave CUs idle. In each block the sets go, heaviest first, to the least-loaded of
 // the 16 waves with a layer left (rank_slot), which is how the part walk balances the waves
 // it synchronizes at every part. For gene part p and layer (wave w, layer l) the 8 rows' runs in
 // the part are r_0 .. r_7; the layer gets ceil(max r_g / 16) fills of 128 entries, entry k of
@@ -27,6 +28,7 @@
 #include "qcsr_common.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace cx {
 namespace {
@@ -282,7 +284,7 @@ struct PlanSizes {
 
 PlanSizes plan_sizes(const cx_qcsr_matrix *m, const cx_qcsr_hybrid_layout *L) {
     PlanSizes s{};
-    s.blocks = (m->rows + kStreamRows - 1) / kStreamRows;
+    s.blocks = round_block_count(m->rows, kStreamRows, blocks_per_round(), false);
     const std::uint32_t all_parts = (m->cols + kStreamPartGenes - 1) / kStreamPartGenes;
     const std::uint32_t first = L->head_cols / kStreamPartGenes;
     s.parts = all_parts > first ? all_parts - first : 0u;
@@ -320,6 +322,22 @@ int validate_stream(const cx_qcsr_matrix *m, const cx_qcsr_hybrid_layout *L, con
 }
 
 } // namespace
+
+std::uint32_t blocks_per_round() {
+    if (const char *env = std::getenv("CX_BLOCKS_PER_ROUND")) {
+        char *end = nullptr;
+        const unsigned long v = std::strtoul(env, &end, 10);
+        if (end != env && *end == '\0' && v > 0ul && v <= 0xffffffffull) return static_cast<std::uint32_t>(v);
+    }
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess
+        || cus < 0) {
+        (void)hipGetLastError();
+        return 0u;
+    }
+    return static_cast<std::uint32_t>(cus);
+}
+
 } // namespace cx
 
 extern "C" int cx_qcsr_tail_plan_bytes(const cx_qcsr_matrix *m, const cx_qcsr_hybrid_layout *layout, uint64_t *bytes) {

@@ -1634,8 +1634,11 @@ typedef struct cx_qcsr_tail_stream {
     uint32_t rows;
     uint32_t first_part;    /* head_cols / 1024 */
     uint32_t parts;         /* gene parts of 1,024 in the stream: ceil(cols / 1024) - first_part */
-    uint32_t blocks;        /* ceil(rows / block_rows) */
-    uint32_t block_rows;    /* rows per block: 16 waves x layers x 8 (1,024) */
+    uint32_t blocks;        /* ceil(rows / block_rows), or, when that is below the device's compute units
+                               (the environment's CX_BLOCKS_PER_ROUND, a positive integer, replaces their
+                               count), min(compute units, ceil(rows / 8)) blocks of fewer rows; the walk
+                               launches one workgroup per block */
+    uint32_t block_rows;    /* row slots per block: 16 waves x layers x 8 (1,024) */
     uint32_t layers;        /* layers of 8 rows per wave (8) */
     uint32_t bits;
     uint32_t entry_bytes;   /* 2 (codes of up to 4 bits: gene in part | code << 11) or 4 (8-bit: gene | code << 16) */
@@ -1711,7 +1714,7 @@ typedef struct cx_qcsr_exec_info {
     uint64_t tail_fills;        /* fills of 128 entries in the tail stream */
     uint64_t persistent_bytes;  /* device bytes the projection holds */
     uint32_t head_form;         /* CX_HEAD_FORM_* */
-    uint32_t reserved;
+    uint32_t tail_blocks;       /* workgroups of the tail walk (cx_qcsr_tail_stream.blocks) */
 } cx_qcsr_exec_info;
 int cx_qcsr_exec_prepare(const cx_qcsr_matrix *a, uint32_t head_cols, cx_qcsr_exec_projection **out, void *stream);
 int cx_qcsr_exec_query(const cx_qcsr_exec_projection *p, cx_qcsr_exec_info *info);

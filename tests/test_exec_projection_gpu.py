@@ -6,8 +6,9 @@ candidate through the reference's own operation core.
   relabelled matrix, dense head, tail stream: exec_order.py) with the same head width, and
   matches the float64 referee of the canonical matrix (canonical W in, canonical rows out).
 * At the benchmark configurations' shapes: C3-generated rows (4-bit codes, 33,538 genes)
-  with the 2,048-gene head and the tail stream over three full 1,024-row blocks and a ragged
-  one, N = 64 and 128; C2-generated rows (8-bit codes) with the 6,144-gene head.
+  with the 2,048-gene head and the tail stream in three block geometries (one block per
+  compute unit; three full 1,024-row blocks and a ragged one; seven partly filled blocks),
+  N = 64 and 128; C2-generated rows (8-bit codes) with the 3,072-gene head (and 6,144).
 * Through register -> prepare -> run_prepared_operation: bitwise equal to the direct call,
   with and without a fused epilogue; without its persistent state the candidate runs the
   row-group kernel (bitwise equal to it); its launch costs no more than the direct call.
@@ -69,20 +70,30 @@ def test_projection_equals_stepwise_path_and_referee(oracle, bits, policy, head)
     p.close()
 
 
+@pytest.mark.parametrize("units", [None, 1, 7])
 @pytest.mark.parametrize("n", [64, 128])
-def test_c3_rows_at_the_benchmark_form(oracle, n):
+def test_c3_rows_at_the_benchmark_form(oracle, monkeypatch, n, units):
     """C3-generated rows as bench.py runs them: 2,048 head genes on the matrix cores, the rest
-    through the tail stream, three full 1,024-row blocks of the stream and a ragged one."""
+    through the tail stream, in each block geometry of the stream: one block per compute unit
+    of the device (blocks of ~14 rows), three full 1,024-row blocks and a ragged one (C3's own
+    geometry: the fewest full blocks), and seven partly filled blocks of ~510 rows."""
     import torch
 
     from cellerator_amd import qcsr_pack_gene_affine
     from cellerator_amd.exec_order import ExecProjection
     from cellerator_amd.synth import C3, dense_normal, generate_qcsr
-    m = qcsr_pack_gene_affine(generate_qcsr(C3.scaled(3 * 1024 + 500)))
+    if units is None:
+        monkeypatch.delenv("CX_BLOCKS_PER_ROUND", raising=False)
+    else:
+        monkeypatch.setenv("CX_BLOCKS_PER_ROUND", str(units))
+    rows = 3 * 1024 + 500
+    m = qcsr_pack_gene_affine(generate_qcsr(C3.scaled(rows)))
     w = dense_normal((m.cols, n), 0.02, torch.float16, seed=11 + n)
     p = ExecProjection(m, 2048)
     info = p.info()
     assert info.head_cols == 2048 and info.head_form == 2 and info.tail_fills > 0
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert int(info.tail_blocks) == {None: min(cus, -(-rows // 8)), 1: 4, 7: 7}[units]
     y = p.spmm(w)
     step = _stepwise(m, w, 2048)
     torch.cuda.synchronize()
@@ -92,9 +103,10 @@ def test_c3_rows_at_the_benchmark_form(oracle, n):
     p.close()
 
 
-def test_c2_rows_at_the_benchmark_form(oracle):
-    """C2-generated rows (8-bit codes, the words form of the head) with the 6,144-gene head
-    bench.py runs at C2 and the tail stream."""
+@pytest.mark.parametrize("head", [3072, 6144])
+def test_c2_rows_at_the_benchmark_form(oracle, head):
+    """C2-generated rows (8-bit codes, the words form of the head) with the 3,072-gene head
+    bench.py runs at C2 (and 6,144) and the tail stream."""
     import torch
 
     from cellerator_amd import qcsr_pack_gene_affine
@@ -102,10 +114,10 @@ def test_c2_rows_at_the_benchmark_form(oracle):
     from cellerator_amd.synth import C2, dense_normal, generate_qcsr
     m = qcsr_pack_gene_affine(generate_qcsr(C2.scaled(2 * 1024 + 300)))
     w = dense_normal((m.cols, 64), 0.02, torch.float16, seed=23)
-    p = ExecProjection(m, 6144)
+    p = ExecProjection(m, head)
     assert p.info().head_form == 1
     y = p.spmm(w)
-    step = _stepwise(m, w, 6144)
+    step = _stepwise(m, w, head)
     torch.cuda.synchronize()
     assert torch.equal(y.view(torch.int32), step.view(torch.int32))
     ref, mag = _referee_of(oracle, m, w)

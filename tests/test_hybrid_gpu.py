@@ -276,10 +276,11 @@ def test_hybrid_on_c3_rows(oracle):
     check_against_referee(oracle, ref, mag, y.cpu().numpy())
 
 
-def test_hybrid_on_c2_rows(oracle):
+@pytest.mark.parametrize("head", [3072, 6144])
+def test_hybrid_on_c2_rows(oracle, head):
     """C2-generated rows (8-bit codes, 20,000 genes, 2,000 nonzeros per cell) in popularity
-    order with the 6,144-gene head bench.py runs at C2 (the words form), several workgroups
-    of 256 rows and a ragged last one; repeats are bitwise equal."""
+    order with the 3,072-gene head bench.py runs at C2 (and 6,144; the words form), several
+    workgroups of 256 rows and a ragged last one; repeats are bitwise equal."""
     import torch
 
     from cellerator_amd import qcsr_pack_gene_affine
@@ -287,9 +288,9 @@ def test_hybrid_on_c2_rows(oracle):
     from cellerator_amd.synth import C2, dense_normal, generate_qcsr
     m = generate_qcsr(C2.scaled(3 * 256 + 37))
     w = dense_normal((m.cols, 64), 0.02, torch.float16, seed=5)
-    mx, order = _exec(qcsr_pack_gene_affine(m), 6144)
+    mx, order = _exec(qcsr_pack_gene_affine(m), head)
     wx = pack_rows(order, w)
-    p = hybrid_prepare(mx, 6144)
+    p = hybrid_prepare(mx, head)
     y = hybrid_spmm(p, wx)
     y2 = hybrid_spmm(p, wx)
     torch.cuda.synchronize()

@@ -95,15 +95,47 @@ def _long_tail_fixture(oracle, rng, bits, rows=1300, cols=2600):
     return _rebuild(oracle, rng, fx, row_ptr.astype(np.int32), col_idx)
 
 
+def _per_round(monkeypatch, units):
+    """Workgroups per round of the row-group walk: the device's compute units (None) or an
+    override (1: the fewest full workgroups of 512 rows)."""
+    if units is None:
+        monkeypatch.delenv("CX_BLOCKS_PER_ROUND", raising=False)
+    else:
+        monkeypatch.setenv("CX_BLOCKS_PER_ROUND", str(units))
+
+
+@pytest.mark.parametrize("units", [1, None])
 @pytest.mark.parametrize("bits", [4, 8])
-def test_many_workgroups_long_last_rows(oracle, bits):
-    """Three workgroups, long rows at a block boundary and at the array ends: block-end and
-    array-end window loads are both exercised."""
+def test_many_workgroups_long_last_rows(oracle, monkeypatch, bits, units):
+    """Three workgroups (one per round), long rows at a block boundary and at the array ends:
+    block-end and array-end window loads are both exercised; and the same rows spread over a
+    round of the device's compute units (workgroups of ~8 rows)."""
     rng = np.random.default_rng(971 + bits)
     fx = _long_tail_fixture(oracle, rng, bits)
     rhs = (rng.standard_normal((fx["cols"], 64)) * 0.02).astype(np.float16)
     ref, mag = _referee(oracle, fx, rhs)
+    _per_round(monkeypatch, units)
     check_against_referee(oracle, ref, mag, _run(to_device_qcsr(fx), rhs))
+
+
+def test_workgroup_geometries_agree(oracle, monkeypatch):
+    """The launch splits the rows into whole rounds of workgroups (at most 512 rows each, an
+    even share per workgroup). Every geometry gives each row the same summation order, so the
+    sums agree (as values: a pad may turn an all-zero sum's -0.0 into +0.0) and match the
+    referee: the fewest full workgroups, 3 and 7 per round, and the device's compute units."""
+    import torch
+    rng = np.random.default_rng(4242)
+    fx = _long_tail_fixture(oracle, rng, 4)
+    rhs = (rng.standard_normal((fx["cols"], 64)) * 0.02).astype(np.float16)
+    ref, mag = _referee(oracle, fx, rhs)
+    m = to_device_qcsr(fx)
+    outs = []
+    for units in (1, 3, 7, None):
+        _per_round(monkeypatch, units)
+        outs.append(_run(m, rhs))
+        check_against_referee(oracle, ref, mag, outs[-1])
+    for o in outs[1:]:
+        assert torch.equal(torch.from_numpy(o), torch.from_numpy(outs[0]))
 
 
 def test_interleaved_pairs_through_parts(oracle):

@@ -22,14 +22,31 @@ pytestmark = pytest.mark.gpu
 WAVES, PART = 16, 1024
 
 
-def _stream_reference(h, head_end, head, bits, LAYERS):
+def _round_blocks(rows, units):
+    """The planner's block count: the fewest blocks of at most 1,024 rows, or, when those would
+    not fill one round of `units` (one block per compute unit), `units` blocks capped at one
+    set of 8 rows per block."""
+    need = -(-rows // 1024)
+    return need if need >= units else min(units, -(-rows // 8))
+
+
+def _units(monkeypatch, units):
+    """Blocks per round for the next plan: the device's compute units (None) or an override."""
+    import torch
+    if units is None:
+        monkeypatch.delenv("CX_BLOCKS_PER_ROUND", raising=False)
+        return torch.cuda.get_device_properties(0).multi_processor_count
+    monkeypatch.setenv("CX_BLOCKS_PER_ROUND", str(units))
+    return units
+
+
+def _stream_reference(h, head_end, head, bits, LAYERS, blocks):
     """slot_rows, fill_index and entries of the stream by its definition (16 waves of LAYERS
-    layers of 8 rows per block)."""
+    layers of 8 rows per block, `blocks` blocks)."""
     ROWS_PER_BLOCK = WAVES * LAYERS * 8
     SLOTS = WAVES * LAYERS
     rows = len(h["row_ptr"]) - 1
     cols = int(h["cols"])
-    blocks = (rows + ROWS_PER_BLOCK - 1) // ROWS_PER_BLOCK
     first = head // PART
     parts = (cols + PART - 1) // PART - first
     wide = bits == 8
@@ -112,21 +129,27 @@ def _stream_reference(h, head_end, head, bits, LAYERS):
     return slot_rows, index.astype(np.uint32), entries
 
 
+@pytest.mark.parametrize("units", [None, 1])
 @pytest.mark.parametrize("bits,head", [(4, 1024), (8, 0), (2, 2048)])
-def test_stream_layout_is_bit_exact(oracle, bits, head):
+def test_stream_layout_is_bit_exact(oracle, monkeypatch, bits, head, units):
+    """Bit-exact layout under both block geometries: one block per compute unit of the device
+    (2,100 rows: blocks of ~8 rows) and, with one block per round, the fewest full blocks
+    (two of 1,024 rows and a ragged one)."""
     import torch
 
     from cellerator_amd.exec_order import hybrid_prepare, tail_arrays
     rng = np.random.default_rng(40 + bits + head)
     fx = _skewed(oracle, rng, 2100, 3100, bits, 1)
     mx, _ = _exec(to_device_qcsr(fx), head)
+    per_round = _units(monkeypatch, units)
     p = hybrid_prepare(mx, head, stream_tail=True)
     torch.cuda.synchronize()
+    assert int(p.tail.blocks) == _round_blocks(2100, per_round)
     slot_rows, index, entries = tail_arrays(p)
     h = qcsr_to_host(mx)
     from cellerator_amd.exec_order import hybrid_head_arrays
     he = hybrid_head_arrays(p)[2].cpu().numpy()
-    want_rows, want_index, want_entries = _stream_reference(h, he, head, bits, int(p.tail.layers))
+    want_rows, want_index, want_entries = _stream_reference(h, he, head, bits, int(p.tail.layers), int(p.tail.blocks))
     assert int(p.tail.block_rows) == WAVES * int(p.tail.layers) * 8
     assert np.array_equal(slot_rows.cpu().numpy().view(np.uint32), want_rows)
     assert np.array_equal(index.cpu().numpy().view(np.uint32), want_index)
@@ -256,23 +279,26 @@ def test_prepare_and_launch_on_a_side_stream(oracle):
     assert torch.equal(y2.view(torch.int32), base.view(torch.int32))
 
 
-def test_stream_layout_33_parts_head_0(oracle):
+@pytest.mark.parametrize("units", [None, 1])
+def test_stream_layout_33_parts_head_0(oracle, monkeypatch, units):
     """34,000 genes with no head: 34 gene parts, so the plan kernel counts parts in two chunks
-    (32 + 2) and every row's tail starts at its first entry; layout bit-exact, product within
-    the referee's tolerance."""
+    (32 + 2) and every row's tail starts at its first entry; layout bit-exact under both block
+    geometries, product within the referee's tolerance."""
     import torch
 
     from cellerator_amd.exec_order import hybrid_head_arrays, hybrid_prepare, hybrid_spmm, pack_rows, tail_arrays
     rng = np.random.default_rng(3333)
     fx = _skewed(oracle, rng, 1100, 34_000, 4, 1)
     mx, order = _exec(to_device_qcsr(fx), 0)
+    per_round = _units(monkeypatch, units)
     p = hybrid_prepare(mx, 0, stream_tail=True)
     torch.cuda.synchronize()
     assert int(p.tail.parts) == 34
+    assert int(p.tail.blocks) == _round_blocks(1100, per_round)
     slot_rows, index, entries = tail_arrays(p)
     h = qcsr_to_host(mx)
     he = hybrid_head_arrays(p)[2].cpu().numpy()
-    want_rows, want_index, want_entries = _stream_reference(h, he, 0, 4, int(p.tail.layers))
+    want_rows, want_index, want_entries = _stream_reference(h, he, 0, 4, int(p.tail.layers), int(p.tail.blocks))
     assert np.array_equal(slot_rows.cpu().numpy().view(np.uint32), want_rows)
     assert np.array_equal(index.cpu().numpy().view(np.uint32), want_index)
     assert np.array_equal(entries.cpu().numpy().view(np.uint16), want_entries)
