@@ -552,45 +552,85 @@ __global__ __launch_bounds__(256) void dense_head_build(BuildArgs a) {
     if (bad) atomicOr(a.error, 1u);
 }
 
-// Table form: one thread per row writes every chunk's 32 bytes (128: not stored), then the
-// code byte (code * 8) of each stored head gene; also the row's first tail entry.
+// Table form: one wave per row (kBytesRowsPerWave consecutive rows per wave) reads the row's
+// head entries 64 at a time, coalesced, and drops each code byte (code * 8) into an LDS copy
+// of 64 chunks x 32 bytes preset to 128 ("not stored"); lane c then stores chunk c's 32 bytes
+// as two 16-byte writes. Also the row's first tail entry. A row whose head genes are not
+// strictly increasing and non-negative keeps the bytes of the entries before the first bad
+// one, its later chunks stay "not stored", its first tail entry is its end, and the error
+// word is set.
+constexpr int kBytesWaves = 4;
+constexpr std::uint32_t kBytesRowsPerWave = 16;
+constexpr std::uint32_t kBytesRows = kBytesWaves * kBytesRowsPerWave;  // rows per workgroup
+static_assert(kLayoutRows % kBytesRows == 0u, "head plane rows");
+
 template<int kBits>
-__global__ __launch_bounds__(256) void dense_head_bytes(BuildArgs a, std::uint8_t *bytes) {
-    const std::uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
-    if (row >= a.rows_ld) return;
+__global__ __launch_bounds__(kBytesWaves * kWave) void dense_head_bytes(BuildArgs a, std::uint8_t *bytes) {
     constexpr std::uint32_t kMask = (1u << kBits) - 1u;
-    std::int64_t e = 0, end = 0, rb = 0, pbit = 0;
-    if (row < a.rows) {
-        rb = e = a.row_ptr[row];
-        end = a.row_ptr[row + 1];
-        pbit = static_cast<std::int64_t>(a.packed_row_ptr[row]) * 8;
-    }
-    std::int64_t prev = -1;
-    bool bad = false;
+    __shared__ std::uint32_t plane[kBytesWaves][kWave * 8];  // per wave: 64 chunks of 32 bytes
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    std::uint8_t *pb = reinterpret_cast<std::uint8_t *>(plane[wave]);
+    auto lds_order = [] { __asm__ volatile("" ::: "memory"); };
     const std::uint32_t chunks = a.head / 32u;
-    const uint4 absent = make_uint4(kAbsentWord, kAbsentWord, kAbsentWord, kAbsentWord);
-    for (std::uint32_t c = 0; c < chunks; ++c) {
-        std::uint8_t *dst = bytes + (static_cast<std::uint64_t>(c) * a.rows_ld + row) * 32u;
-        reinterpret_cast<uint4 *>(dst)[0] = absent;
-        reinterpret_cast<uint4 *>(dst)[1] = absent;
-        const std::int64_t g_hi = static_cast<std::int64_t>(c + 1u) * 32;
-        while (e < end) {
-            const std::int64_t g = a.col_idx[e];
-            if (g >= g_hi) break;
-            if (g <= prev) {  // repeated, decreasing or negative gene: not a sorted row
-                bad = true;
-                break;
-            }
-            const std::int64_t bit = pbit + (e - rb) * kBits;
-            const std::uint32_t code = (static_cast<std::uint32_t>(a.packed[bit >> 3]) >> (bit & 7)) & kMask;
-            dst[g - static_cast<std::int64_t>(c) * 32] = static_cast<std::uint8_t>(code * 8u);
-            prev = g;
-            ++e;
+    for (std::uint32_t r = 0; r < kBytesRowsPerWave; ++r) {
+        const std::uint32_t row = (blockIdx.x * kBytesWaves + static_cast<std::uint32_t>(wave)) * kBytesRowsPerWave + r;
+        if (row >= a.rows_ld) break;
+        std::int64_t e = 0, end = 0, rb = 0, pbit = 0;
+        if (row < a.rows) {
+            rb = e = __builtin_amdgcn_readfirstlane(a.row_ptr[row]);
+            end = __builtin_amdgcn_readfirstlane(a.row_ptr[row + 1]);
+            pbit = static_cast<std::int64_t>(__builtin_amdgcn_readfirstlane(a.packed_row_ptr[row])) * 8;
         }
-        if (bad) e = end;  // the remaining chunks of the row stay "not stored"
+        std::int64_t prev = -1;
+        bool bad = false;
+        for (std::uint32_t c0 = 0; c0 < chunks; c0 += kWave) {
+            lds_order();
+#pragma unroll
+            for (int d = 0; d < 8; ++d) plane[wave][lane * 8 + d] = kAbsentWord;
+            lds_order();
+            const std::int64_t g_lo = static_cast<std::int64_t>(c0) * 32;
+            const std::int64_t g_hi = static_cast<std::int64_t>(min(c0 + kWave, chunks)) * 32;
+            while (e < end) {
+                const std::int64_t idx = e + lane;
+                const bool valid = idx < end;
+                const std::int64_t gene = valid ? static_cast<std::int64_t>(a.col_idx[idx]) : g_hi;
+                std::int64_t before = static_cast<std::int64_t>(__shfl_up(static_cast<int>(gene), 1, kWave));
+                if (lane == 0) before = prev;
+                const bool in = valid && gene < g_hi;
+                const std::uint64_t bad_lanes = __builtin_amdgcn_ballot_w64(in && gene <= before);
+                const std::uint64_t in_lanes = __builtin_amdgcn_ballot_w64(in);
+                // sorted rows: the chunk window's entries are a prefix of the lanes
+                const int first_bad = bad_lanes != 0u ? __builtin_ctzll(bad_lanes) : kWave;
+                const std::uint64_t ok = in_lanes & (first_bad == kWave ? ~std::uint64_t{0} : (std::uint64_t{1} << first_bad) - 1u);
+                if (((ok >> lane) & 1u) != 0u) {
+                    const std::int64_t bit = pbit + (idx - rb) * kBits;
+                    const std::uint32_t code = (static_cast<std::uint32_t>(a.packed[bit >> 3]) >> (bit & 7)) & kMask;
+                    pb[gene - g_lo] = static_cast<std::uint8_t>(code * 8u);
+                }
+                if (bad_lanes != 0u) {
+                    bad = true;
+                    break;
+                }
+                const int n = __popcll(in_lanes);
+                if (n > 0) prev = static_cast<std::int64_t>(__builtin_amdgcn_readlane(static_cast<int>(gene), n - 1));
+                e += n;
+                if (n < kWave) break;
+            }
+            lds_order();
+            if (c0 + static_cast<std::uint32_t>(lane) < chunks) {
+                uint4 *dst = reinterpret_cast<uint4 *>(bytes + (static_cast<std::uint64_t>(c0 + lane) * a.rows_ld + row) * 32u);
+                const std::uint32_t *src = &plane[wave][lane * 8];
+                dst[0] = make_uint4(src[0], src[1], src[2], src[3]);
+                dst[1] = make_uint4(src[4], src[5], src[6], src[7]);
+            }
+            if (bad) e = end;  // the remaining chunks of the row stay "not stored"
+        }
+        if (lane == 0) {
+            if (row < a.rows) a.head_end[row] = static_cast<std::int32_t>(e);
+            if (bad) atomicOr(a.error, 1u);
+        }
     }
-    if (row < a.rows) a.head_end[row] = static_cast<std::int32_t>(e);
-    if (bad) atomicOr(a.error, 1u);
 }
 
 // lut[chunk][gene][code] = the three round-toward-zero fp16 parts of fma(code, 2^k s, 2^k o)
@@ -931,10 +971,11 @@ extern "C" int cx_qcsr_hybrid_prepare(const cx_qcsr_matrix *m, uint32_t head_col
         b.error = words + 2;
         const dim3 grid(L.rows_ld / 256u), block(256);
         if (sz.form == CX_HEAD_FORM_TABLE) {
+            const dim3 tgrid(L.rows_ld / kBytesRows), tblock(kBytesWaves * kWave);
             switch (m->bits) {
-            case 1: hipLaunchKernelGGL(dense_head_bytes<1>, grid, block, 0, s, b, L.code_bytes); break;
-            case 2: hipLaunchKernelGGL(dense_head_bytes<2>, grid, block, 0, s, b, L.code_bytes); break;
-            default: hipLaunchKernelGGL(dense_head_bytes<4>, grid, block, 0, s, b, L.code_bytes); break;
+            case 1: hipLaunchKernelGGL(dense_head_bytes<1>, tgrid, tblock, 0, s, b, L.code_bytes); break;
+            case 2: hipLaunchKernelGGL(dense_head_bytes<2>, tgrid, tblock, 0, s, b, L.code_bytes); break;
+            default: hipLaunchKernelGGL(dense_head_bytes<4>, tgrid, tblock, 0, s, b, L.code_bytes); break;
             }
         } else {
             switch (m->bits) {

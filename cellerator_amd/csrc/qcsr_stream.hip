@@ -125,55 +125,87 @@ __device__ __forceinline__ std::uint32_t rank_slot(RankShared &r, const PlanArgs
     return r.slot_row[tid];  // thread tid now works for slot tid
 }
 
-static_assert(sizeof(RankShared) + sizeof(std::uint16_t) * kPlanChunk * kStreamRows <= 160u * 1024u,
+static_assert(sizeof(RankShared) + sizeof(std::uint16_t) * kPlanChunk * kStreamRows + sizeof(std::int64_t) * kStreamRows
+                  <= 160u * 1024u,
               "the stream plan kernel's LDS exceeds gfx950's 160 KB");
 
+// After the ranking, wave w counts the runs of its 64 slots (stream wave w) one row at a time:
+// the row's tail is read 64 entries at a time, coalesced, each entry's part (within a window
+// of kPlanChunk parts) comes from its gene, and the first lane of each part's segment adds the
+// segment's size to the part's run. A row is reported (error word 0) when its genes go back to
+// an earlier part, fall below the window, or reach cols or past it (entries left at the end).
 __global__ __launch_bounds__(kStreamRows) void stream_plan_kernel(PlanArgs a) {
     __shared__ RankShared rs;
     __shared__ std::uint16_t runs[kPlanChunk][kStreamRows];
+    __shared__ std::int64_t cursor[kStreamRows];
     const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const std::uint32_t block = blockIdx.x;
     const std::uint32_t row = rank_slot(rs, a, block, gridDim.x, tid);
     a.slot_rows[static_cast<std::uint64_t>(block) * kStreamRows + tid] = row;
-
-    std::int64_t cur = 0, end = 0;
-    if (row != kNoSlotRow) {
-        cur = a.head_end[row];
-        end = a.row_ptr[row + 1];
-    }
-    bool bad = false;
+    cursor[tid] = row != kNoSlotRow ? a.head_end[row] : 0;
+    const std::uint64_t below = (std::uint64_t{1} << lane) - 1u;
+    bool bad = false;  // per wave (lane 0 reports)
     for (std::uint32_t c0 = 0; c0 < a.parts; c0 += kPlanChunk) {
         const std::uint32_t cn = min(static_cast<std::uint32_t>(kPlanChunk), a.parts - c0);
-        for (std::uint32_t c = 0; c < cn; ++c) {
-            const std::int64_t lo = static_cast<std::int64_t>(a.first_part + c0 + c) * kStreamPartGenes;
-            const std::int64_t hi = std::min<std::int64_t>(lo + kStreamPartGenes, a.cols);
-            int n = 0;
+        const std::int64_t lo = static_cast<std::int64_t>(a.first_part + c0) * kStreamPartGenes;
+        for (int t = tid; t < kPlanChunk * kStreamRows; t += kStreamRows) (&runs[0][0])[t] = 0;
+        __syncthreads();
+        for (int sl = 0; sl < kWave; ++sl) {
+            const int slot = wave * kWave + sl;
+            const std::uint32_t r = static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(rs.slot_row[slot])));
+            if (r == kNoSlotRow || r >= a.rows) continue;
+            const std::int64_t end = __builtin_amdgcn_readfirstlane(a.row_ptr[r + 1]);
+            std::int64_t cur = cursor[slot];
+            std::int64_t prev_pp = 0;  // part of the last entry taken
             while (cur < end) {
-                const std::int64_t g = a.col_idx[cur];
-                if (g >= hi) break;
-                if (g < lo) bad = true;  // below the part (or the head): not sorted
-                ++cur;
-                ++n;
+                const std::int64_t e = cur + lane;
+                const bool valid = e < end;
+                const std::int64_t gene = valid ? static_cast<std::int64_t>(a.col_idx[e]) : 0;
+                const std::int64_t rel = gene - lo;
+                const std::int64_t pp = rel >= 0 ? rel >> 10 : -1;
+                const bool in = valid && pp >= 0 && pp < static_cast<std::int64_t>(cn);
+                std::int64_t before = static_cast<std::int64_t>(__shfl_up(static_cast<int>(pp), 1, kWave));
+                if (lane == 0) before = prev_pp;
+                const std::uint64_t inb = __builtin_amdgcn_ballot_w64(in);
+                const int n = __popcll(inb);
+                // the window's entries must be a prefix, in non-decreasing parts, none below it
+                const bool wrong = (in && pp < before) || (valid && rel < 0);
+                if (__builtin_amdgcn_ballot_w64(wrong) != 0u || inb != (n == kWave ? ~std::uint64_t{0} : (std::uint64_t{1} << n) - 1u))
+                    bad = true;
+                const std::uint64_t heads = __builtin_amdgcn_ballot_w64(in && (lane == 0 || before != pp));
+                if (in && ((heads >> lane) & 1u) != 0u) {
+                    const std::uint64_t after = heads & ~(below | (std::uint64_t{1} << lane));
+                    const std::uint64_t stop = after != 0u ? (after & (~after + 1u)) - 1u : ~std::uint64_t{0};
+                    const int len = __popcll(inb & stop & ~below);
+                    const int total = static_cast<int>(runs[pp][slot]) + len;
+                    if (total > 0xffff) bad = true;
+                    runs[pp][slot] = static_cast<std::uint16_t>(min(total, 0xffff));
+                }
+                if (n > 0) prev_pp = __builtin_amdgcn_readlane(static_cast<int>(pp), n - 1);
+                cur += n;
+                if (n < kWave) break;
             }
-            runs[c][tid] = static_cast<std::uint16_t>(min(n, 0xffff));
-            if (n > 0xffff) bad = true;
+            if (lane == 0) cursor[slot] = cur;
         }
         __syncthreads();
         // one (part, wave, layer) per thread-iteration: the largest run of its 8 groups
         for (int t = tid; t < static_cast<int>(cn) * kStreamSlots; t += kStreamRows) {
-            const int c = t / kStreamSlots, s = t % kStreamSlots;
+            const int c = t / kStreamSlots, sl = t % kStreamSlots;
             int m = 0;
 #pragma unroll
-            for (int g = 0; g < 8; ++g) m = max(m, static_cast<int>(runs[c][s * 8 + g]));
-            const std::uint64_t k = index_pos(block, s / kStreamLayers, c0 + c, a.parts, s % kStreamLayers);
+            for (int g = 0; g < 8; ++g) m = max(m, static_cast<int>(runs[c][sl * 8 + g]));
+            const std::uint64_t k = index_pos(block, sl / kStreamLayers, c0 + c, a.parts, sl % kStreamLayers);
             const int fills = (m + 15) / 16;
             a.counts[k] = static_cast<std::uint32_t>(fills);
             a.lasts[k] = static_cast<std::uint8_t>(fills == 0 ? 0 : m - 16 * (fills - 1));
         }
         __syncthreads();
     }
-    if (cur != end) bad = true;  // genes at or past cols, or negative: the walk could not finish
-    if (bad) atomicOr(&a.error[0], 1u);
+    // genes at or past cols, or a walk stopped early: entries left over
+    if (row != kNoSlotRow && cursor[tid] != a.row_ptr[row + 1]) bad = true;
+    if (__builtin_amdgcn_ballot_w64(bad) != 0u && lane == 0) atomicOr(&a.error[0], 1u);
 }
 
 // index[k] = first fill | (last steps - 1) << 28; the scan left the first fills in index.
@@ -209,44 +241,120 @@ struct FillArgs {
     std::uint32_t parts;
 };
 
-// One thread per slot: walks its row's tail part by part (the plan's walk) and writes each
-// run in parity order at its fills.
+// One wave per slot, the 64 slots of stream wave w taken in turn by the workgroup's wave w.
+// The row's tail is read 64 entries at a time, coalesced (a thread per row read 64 unrelated
+// rows per load and missed the caches on most of them). Columns are sorted, so the entries of
+// one gene part are consecutive lanes: ballots find each part's segment, and an entry's slot
+// in its part's run is its rank among the segment's entries of its parity class plus the
+// counts of earlier chunks (LDS, per part); entries of the other parity follow all the
+// preferred ones, whose total per part a first pass counts. Parts are handled 64 at a time.
+// Every write is bounded by the fills the plan gave the layer, so a row the plan reported as
+// unsorted cannot write past them.
 template<int kBits>
 __global__ __launch_bounds__(kStreamRows) void stream_fill_kernel(FillArgs a) {
     constexpr bool kWide = kBits == 8;
     constexpr std::uint32_t kMask = (1u << kBits) - 1u;
-    const int slot = static_cast<int>(threadIdx.x);
+    __shared__ std::uint32_t part_counts[kStreamWaves][3][kWave];  // per wave and window part: preferred total, carries
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
     const std::uint32_t block = blockIdx.x;
-    const std::uint32_t row = a.slot_rows[static_cast<std::uint64_t>(block) * kStreamRows + slot];
-    if (row == kNoSlotRow) return;
-    const int layer_slot = slot / 8, g = slot % 8;
-    const std::uint32_t pref = static_cast<std::uint32_t>(g & 1);  // parity stored first
-    const std::int64_t rb = a.row_ptr[row], end = a.row_ptr[row + 1];
-    const std::int64_t pbit = static_cast<std::int64_t>(a.packed_row_ptr[row]) * 8;
-    std::int64_t cur = a.head_end[row];
-    for (std::uint32_t p = 0; p < a.parts && cur < end; ++p) {
-        const std::int64_t lo = static_cast<std::int64_t>(a.first_part + p) * kStreamPartGenes;
-        const std::int64_t hi = std::min<std::int64_t>(lo + kStreamPartGenes, a.cols);
-        std::int64_t stop = cur;
-        while (stop < end && a.col_idx[stop] < hi) ++stop;
-        if (stop == cur) continue;
-        const std::uint32_t fill0 =
-            a.index[index_pos(block, layer_slot / kStreamLayers, p, a.parts, layer_slot % kStreamLayers)] & kFillMask;
-        std::uint32_t k = 0;
-        for (int pass = 0; pass < 2; ++pass) {
-            for (std::int64_t e = cur; e < stop; ++e) {
-                const std::int64_t gene = a.col_idx[e];
-                const std::uint32_t local = gene >= lo ? static_cast<std::uint32_t>(gene - lo) : kStreamPad;
-                if (((local & 1u) == pref) != (pass == 0)) continue;
-                const std::int64_t bit = pbit + (e - rb) * kBits;
-                const std::uint32_t code = (static_cast<std::uint32_t>(a.packed[bit >> 3]) >> (bit & 7)) & kMask;
-                const std::uint64_t pos = static_cast<std::uint64_t>(fill0 + k / 16u) * 128u + g * 16u + k % 16u;
-                if constexpr (kWide) static_cast<std::uint32_t *>(a.entries)[pos] = local | code << 16;
-                else static_cast<std::uint16_t *>(a.entries)[pos] = static_cast<std::uint16_t>(local | code << 11);
-                ++k;
+    std::uint32_t *npref = part_counts[wave][0], *cpref = part_counts[wave][1], *coth = part_counts[wave][2];
+    const std::uint64_t below = (std::uint64_t{1} << lane) - 1u;  // lanes before this one
+    auto lds_order = [] { __asm__ volatile("" ::: "memory"); };
+    for (int s = 0; s < 64; ++s) {
+        const int slot = wave * 64 + s;
+        const std::uint32_t row = static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(
+            static_cast<int>(a.slot_rows[static_cast<std::uint64_t>(block) * kStreamRows + slot])));
+        if (row == kNoSlotRow) continue;
+        const int layer = (slot / 8) % kStreamLayers, g = slot % 8;
+        const std::uint32_t pref = static_cast<std::uint32_t>(g & 1);  // parity stored first
+        const std::int64_t rb = __builtin_amdgcn_readfirstlane(a.row_ptr[row]);
+        const std::int64_t end = __builtin_amdgcn_readfirstlane(a.row_ptr[row + 1]);
+        const std::int64_t pbit = static_cast<std::int64_t>(__builtin_amdgcn_readfirstlane(a.packed_row_ptr[row])) * 8;
+        std::int64_t hs = __builtin_amdgcn_readfirstlane(a.head_end[row]);
+        for (std::uint32_t p0 = 0; p0 < a.parts && hs < end; p0 += kWave) {
+            const std::int64_t lo = static_cast<std::int64_t>(a.first_part + p0) * kStreamPartGenes;
+            const std::uint32_t window = min(static_cast<std::uint32_t>(kWave), a.parts - p0);
+            lds_order();
+            npref[lane] = 0u;
+            cpref[lane] = 0u;
+            coth[lane] = 0u;
+            lds_order();
+            // An entry of the window: its part (relative to p0) and parity class; segment heads
+            // are the first lane of each part's run in the chunk.
+            struct Lane {
+                bool in, pref;
+                std::uint32_t pp, local;
+                std::uint64_t heads;
+            };
+            auto classify = [&](std::int64_t e, std::int64_t limit) {
+                Lane L{};
+                const std::int64_t gene = e < limit ? static_cast<std::int64_t>(a.col_idx[e]) : -1;
+                const std::int64_t rel = gene - lo;
+                L.in = e < limit && rel >= 0 && (rel >> 10) < static_cast<std::int64_t>(window);
+                L.pp = L.in ? static_cast<std::uint32_t>(rel >> 10) : 0u;
+                L.local = static_cast<std::uint32_t>(rel & (kStreamPartGenes - 1));
+                L.pref = L.in && (L.local & 1u) == pref;
+                const std::uint32_t prev_pp = static_cast<std::uint32_t>(__shfl_up(static_cast<int>(L.pp), 1, kWave));
+                const std::uint64_t inb = __builtin_amdgcn_ballot_w64(L.in);
+                const bool prev_in = lane > 0 && ((inb >> (lane - 1)) & 1u) != 0u;
+                L.heads = __builtin_amdgcn_ballot_w64(L.in && (!prev_in || prev_pp != L.pp));
+                return L;
+            };
+            // lanes of this lane's segment: from its head up to (not including) the next head
+            auto segment = [&](const Lane &L, std::uint64_t inb) {
+                const std::uint64_t upto = L.heads & (below | (std::uint64_t{1} << lane));
+                const int head = upto != 0u ? 63 - __builtin_clzll(upto) : 0;
+                const std::uint64_t after = L.heads & ~(below | (std::uint64_t{1} << lane));
+                const std::uint64_t stop = after != 0u ? (after & (~after + 1u)) - 1u : ~std::uint64_t{0};
+                return inb & stop & ~((std::uint64_t{1} << head) - 1u);
+            };
+            // pass 1: preferred entries per part, and the end of the window's entries
+            std::int64_t he = hs;
+            for (std::int64_t e0 = hs; e0 < end; e0 += kWave) {
+                const Lane L = classify(e0 + lane, end);
+                const std::uint64_t inb = __builtin_amdgcn_ballot_w64(L.in);
+                const std::uint64_t pb = __builtin_amdgcn_ballot_w64(L.pref);
+                if (L.in && ((L.heads >> lane) & 1u) != 0u) npref[L.pp] += static_cast<std::uint32_t>(__popcll(pb & segment(L, inb)));
+                lds_order();
+                const int n = __popcll(inb);  // sorted rows: the window's entries are a prefix
+                he = e0 + n;
+                if (n < kWave) break;
             }
+            // pass 2: each entry's slot in its part's run, and its write
+            for (std::int64_t e0 = hs; e0 < he; e0 += kWave) {
+                const std::int64_t e = e0 + lane;
+                const Lane L = classify(e, he);
+                const std::uint64_t inb = __builtin_amdgcn_ballot_w64(L.in);
+                const std::uint64_t pb = __builtin_amdgcn_ballot_w64(L.pref);
+                const std::uint64_t ob = inb & ~pb;
+                const std::uint64_t seg = segment(L, inb);
+                const std::uint64_t before = seg & below;
+                std::uint32_t k = 0u;
+                if (L.in)
+                    k = L.pref ? cpref[L.pp] + static_cast<std::uint32_t>(__popcll(pb & before))
+                               : npref[L.pp] + coth[L.pp] + static_cast<std::uint32_t>(__popcll(ob & before));
+                lds_order();
+                if (L.in) {
+                    const std::uint64_t ix = index_pos(block, wave, p0 + L.pp, a.parts, layer);
+                    const std::uint32_t fill0 = a.index[ix] & kFillMask;
+                    const std::uint32_t fills = (a.index[ix + 1u] & kFillMask) - fill0;
+                    if (k / 16u < fills) {
+                        const std::int64_t bit = pbit + (e - rb) * kBits;
+                        const std::uint32_t code = (static_cast<std::uint32_t>(a.packed[bit >> 3]) >> (bit & 7)) & kMask;
+                        const std::uint64_t pos = static_cast<std::uint64_t>(fill0 + k / 16u) * 128u + g * 16u + k % 16u;
+                        if constexpr (kWide) static_cast<std::uint32_t *>(a.entries)[pos] = L.local | code << 16;
+                        else static_cast<std::uint16_t *>(a.entries)[pos] = static_cast<std::uint16_t>(L.local | code << 11);
+                    }
+                    if (((L.heads >> lane) & 1u) != 0u) {
+                        cpref[L.pp] += static_cast<std::uint32_t>(__popcll(pb & seg));
+                        coth[L.pp] += static_cast<std::uint32_t>(__popcll(ob & seg));
+                    }
+                }
+                lds_order();
+            }
+            hs = he;
         }
-        cur = stop;
     }
 }
 
