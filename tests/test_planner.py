@@ -104,8 +104,8 @@ def test_tuning_bounds_and_failures():
 
 
 def test_execution_order_candidate_is_chosen_for_reuse():
-    """The execution-order candidate pays a one-time preparation (about 0.074 ns per stored
-    entry: 111 ms at C3) and more persistent bytes for about half the launch time of the
+    """The execution-order candidate pays a one-time preparation (about 0.028 ns per stored
+    entry: 41 ms at C3) and more persistent bytes for about half the launch time of the
     row-group candidate. The planner amortizes the preparation over the projection reuse
     (compute_total_cost, src/planner/end_to_end_planner.cc:184-213): a single run keeps the
     row-group candidate, a persistent projection takes the execution order, and a persistent
