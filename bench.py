@@ -37,7 +37,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
-VALU_FP32_PEAK_TFLOPS = 78.6  # non-packed fp32 FMA (packed FP32 is disabled in every build)
+MFMA_FP32_PEAK_TFLOPS = 157.3  # fp32 dense matrix cores
 # Matrix-core head width of the prepared qCSR path per configuration, from sweeps in steps of
 # 1,024 genes: at C3 2,048 (3,072 and 4,096 slower); at C2 3,072 (2,048 and 4,096 within 4%,
 # 6,144 13% slower), with C2's 100k rows spread over every compute unit in the tail walk.
@@ -336,18 +336,20 @@ def bench_bell_quantized(args, torch, cfg) -> dict:
                  + m.rows * n_out * 4)
     flops = 2.0 * valid_blocks * bs * bs * n_out
     achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
+    tflops = flops / (kern_ms * 1e-3) / 1e12
     res = {
-        "metric": "quantized Blocked-ELL SpMM (8-bit codes, f32 W): effective HBM GB/s (% roofline), 500k x 20k, N=256",
+        "metric": "quantized Blocked-ELL SpMM (8-bit codes, f32 W): fp32 matrix-core TFLOP/s (% roofline), 500k x 20k, N=256",
         "value": valid_blocks * bs * bs / (wall_ms * 1e-3), "unit": "stored block elements/s",
         "ms_per_step": wall_ms, "dtype": "u8-codes/f32-W/f32-accumulate",
         "config": {"workload": cfg.name + " 8-bit codes", "rows": m.rows, "genes": m.cols, "block_size": bs,
                    "valid_blocks": valid_blocks, "n_out": n_out, "seed": hex(cfg.seed)},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": "bell_spmm_generic<8-bit, per-gene affine> (cx_bell_spmm_fwd)",
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tflops / MFMA_FP32_PEAK_TFLOPS, "traffic": None,
+                     "kernel": "bell_spmm_quant_lds<8, per-gene affine> (cx_bell_spmm_fwd: fp32 matrix cores, "
+                               "W tiles and metadata through LDS)",
                      "kernel_ms_mean": kern_ms, "kernel_ms_median": statistics.median(ev),
-                     "algorithmic_bytes": alg_bytes, "fp32_fma_tflops": flops / (kern_ms * 1e-3) / 1e12,
-                     "valu_fp32_peak_tflops_nonpacked": VALU_FP32_PEAK_TFLOPS},
+                     "flops": flops, "algorithmic_bytes": alg_bytes, "hbm_gbs": achieved,
+                     "hbm_frac": achieved / HBM_PEAK_GBS},
     }
     from oracle import pyoracle
     pyoracle.build()

@@ -857,6 +857,157 @@ __global__ __launch_bounds__(256) void bell_spmm_quant_mfma(BellArgs a, std::int
     }
 }
 
+// The same product with each slot's operands staged through LDS (W 16-byte aligned with a row
+// stride of whole 16-byte units, scales present, and offsets under the per-gene policy):
+// loading a W tile as one 4-byte value per lane and product (32 vector loads per slot and
+// wave) cost 37% of the kernel above, and selecting each K step's metadata with four
+// readlanes another 10%. Per valid slot, wave w's W tile (the block column's 32 genes x its 64
+// columns, 8 KB) and the slot's 32 scales and offsets go straight from memory into a per-wave
+// LDS double buffer (8 + 2 loads per lane, no registers); the B operands are then one
+// ds_read2_b32 per K step (both column tiles) and the metadata one ds_read2_b32 (scale,
+// offset of gene 2kk + h). Genes past `cols` lie outside the loads' descriptors and read as 0
+// (their products are 0); in a block column that crosses `cols` the decoded value is also
+// set to 0 there, as above. The row block's slot ids are read once (one per lane) and the
+// valid ones walked by ballot; the next slot's loads are issued while the current one's
+// matrix instructions run. Same values and products as the kernel above, same order.
+template<int kBits, int kPolicy>
+__global__ __launch_bounds__(256) void bell_spmm_quant_lds(BellArgs a, std::int64_t n) {
+    constexpr int kTiles = 2;  // 64 output columns per wave and chunk
+    constexpr bool kOffsets = kPolicy == CX_DECODE_PER_GENE_AFFINE;
+    __shared__ __attribute__((aligned(16))) float wtile[4][2][32 * 64];
+    __shared__ __attribute__((aligned(16))) float wmeta[4][2][2 * kWave];  // scales at [0, 64), offsets at [64, 128)
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    const std::uint32_t row_blocks = (a.rows + 31u) / 32u;
+    const std::uint32_t rb = xcd_major(blockIdx.x, gridDim.x);
+    if (rb >= row_blocks) return;
+    const std::uint32_t width = a.ell_cols / 32u;
+    const std::uint32_t *slots = a.block_col_idx + static_cast<std::uint64_t>(rb) * width;
+    const int m = lane % 32;
+    const int h = lane / 32;
+    const std::uint32_t row = rb * 32u + static_cast<std::uint32_t>(m);
+    const std::uint32_t block_rows = min(32u, a.rows - rb * 32u);
+    const rsrc_t rc = make_rsrc(a.packed + static_cast<std::uint64_t>(rb) * 32u * a.row_stride_bytes,
+                                block_rows * a.row_stride_bytes);
+    const std::uint32_t code_lane = static_cast<std::uint32_t>(m) * a.row_stride_bytes;
+    const float row_offset = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET && row < a.rows ? a.row_offsets[row] : 0.0f;
+    const float *w = static_cast<const float *>(a.rhs);
+    const std::uint32_t row_bytes = static_cast<std::uint32_t>(a.rhs_ld) * 4u;
+
+    for (std::int64_t n0 = static_cast<std::int64_t>(wave) * 64; n0 < n; n0 += 256) {
+        // slot s (block column bc): this lane's codes, and the W tile and metadata into buffer buf
+        auto load_slot = [&](std::uint32_t (&codes)[kBits], std::uint32_t s, std::uint32_t bc, int buf) {
+            const std::uint32_t co = code_lane + s * static_cast<std::uint32_t>(kBits) * 4u;
+            if constexpr (kBits >= 4) {
+#pragma unroll
+                for (int q = 0; q < kBits / 4; ++q) {
+                    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rc, static_cast<int>(co) + 16 * q, 0, 0);
+                    codes[4 * q] = v[0]; codes[4 * q + 1] = v[1]; codes[4 * q + 2] = v[2]; codes[4 * q + 3] = v[3];
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < kBits; ++q)
+                    codes[q] = static_cast<std::uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rc, static_cast<int>(co) + 4 * q, 0, 0));
+            }
+            const std::uint32_t g0 = bc * 32u;
+            const std::uint32_t genes = g0 < a.cols ? min(32u, a.cols - g0) : 0u;
+            // W: load q covers genes 4q .. 4q + 3, lane l's 16 bytes at gene 4q + l / 16, columns n0 + 4 (l % 16)
+            const rsrc_t rw = make_rsrc(w + static_cast<std::int64_t>(g0) * a.rhs_ld, genes * row_bytes);
+            const std::uint32_t lane_off = static_cast<std::uint32_t>(lane / 16) * row_bytes
+                + static_cast<std::uint32_t>(n0 + 4 * (lane % 16)) * 4u;
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                load_lds16(rw, reinterpret_cast<uint4 *>(&wtile[wave][buf][q * 256]), lane_off + 4u * row_bytes * q, 0u);
+            // metadata: lane l's 4 bytes = scale (offset) of gene l % 32, the upper half repeating it
+            const rsrc_t rs = make_rsrc(a.scales + g0, genes * 4u);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void)&wmeta[wave][buf][0], 4,
+                                                     static_cast<std::uint32_t>(m) * 4u, 0, 0, 0);
+            if constexpr (kOffsets) {
+                const rsrc_t ro = make_rsrc(a.offsets + g0, genes * 4u);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ro, (lds_void)&wmeta[wave][buf][kWave], 4,
+                                                         static_cast<std::uint32_t>(m) * 4u, 0, 0, 0);
+            }
+        };
+
+        cx_floatx16 acc[kTiles];
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
+
+        auto mfma_slot = [&](const std::uint32_t (&codes)[kBits], std::uint32_t bc, int buf, auto crosses) {
+            const float *wt = &wtile[wave][buf][h * 64 + m];
+            const float *mt = &wmeta[wave][buf][h];
+#pragma unroll
+            for (int kk = 0; kk < 16; ++kk) {
+                // gene 2kk + h of the block: its code in this lane's row, its (scale, offset) and
+                // its W row (columns m and 32 + m of the wave's 64) from LDS
+                const int bit = (2 * kk) * kBits;
+                const std::uint32_t code = (codes[bit / 32] >> ((bit % 32) + h * kBits)) & ((1u << kBits) - 1u);
+                const float scale = mt[2 * kk];
+                const float offset = kOffsets ? mt[kWave + 2 * kk] : row_offset;
+                float x = __builtin_fmaf(static_cast<float>(code), scale, offset);
+                if constexpr (decltype(crosses)::value)
+                    x = bc * 32u + static_cast<std::uint32_t>(2 * kk + h) < a.cols ? x : 0.0f;
+                const float b0 = wt[kk * 128], b1 = wt[kk * 128 + 32];
+                acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(x, b0, acc[0], 0, 0, 0);
+                acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(x, b1, acc[1], 0, 0, 0);
+            }
+        };
+        auto run_slot = [&](const std::uint32_t (&codes)[kBits], std::uint32_t bc, int buf) {
+            if (bc * 32u + 32u <= a.cols) mfma_slot(codes, bc, buf, std::false_type{});
+            else mfma_slot(codes, bc, buf, std::true_type{});
+        };
+
+        int buf = 0;
+        for (std::uint32_t base = 0; base < width; base += kWave) {
+            const std::uint32_t cnt = min(static_cast<std::uint32_t>(kWave), width - base);
+            const std::uint32_t sid = static_cast<std::uint32_t>(lane) < cnt ? slots[base + lane] : kInvalidBlock;
+            unsigned long long valid = __ballot(sid != kInvalidBlock);
+            if (valid == 0ull) continue;
+            std::uint32_t s = static_cast<std::uint32_t>(__builtin_ctzll(valid));
+            std::uint32_t bc0 = static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(sid), static_cast<int>(s)));
+            std::uint32_t c0[kBits], c1[kBits];
+            load_slot(c0, base + s, bc0, buf);
+            valid &= valid - 1ull;
+            for (;;) {
+                const bool more = valid != 0ull;
+                std::uint32_t bc1 = bc0;
+                // the current slot's W tile and metadata are in LDS once every earlier load is
+                // done; the other buffer's reads were consumed by the previous slot's products
+                __builtin_amdgcn_s_waitcnt(vmcnt_wait(0));
+                if (more) {
+                    s = static_cast<std::uint32_t>(__builtin_ctzll(valid));
+                    bc1 = static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(sid), static_cast<int>(s)));
+                    load_slot(c1, base + s, bc1, buf ^ 1);
+                    valid &= valid - 1ull;
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                run_slot(c0, bc0, buf);
+                __builtin_amdgcn_sched_barrier(0);
+                buf ^= 1;
+                if (!more) break;
+                bc0 = bc1;
+#pragma unroll
+                for (int q = 0; q < kBits; ++q) c0[q] = c1[q];
+            }
+        }
+
+        // D layout: lane holds column lane % 32; element i is row 8 (i / 4) + 4 h + i % 4
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) {
+            const std::int64_t col = n0 + 32 * t + m;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const std::uint32_t r = rb * 32u + 8u * (i / 4) + 4u * static_cast<std::uint32_t>(h) + (i % 4);
+                if (r < a.rows)
+                    a.out[static_cast<std::int64_t>(r) * a.out_ld + col] =
+                        a.ep.active ? epilogue_value(a.ep, acc[t][i], r, col) : acc[t][i];
+            }
+        }
+    }
+}
+
 int validate_bell(const cx_bell_matrix *m, const void *rhs, std::int64_t rhs_ld,
                   std::int64_t out_cols, const float *out, std::int64_t out_ld) {
     if (m == nullptr || rhs == nullptr || out == nullptr)
@@ -947,16 +1098,22 @@ extern "C" int cx_bell_spmm_fwd_epilogue(const cx_bell_matrix *m, const void *rh
     if (m->bits != 0u && m->block_size == 32u && rhs_dtype == CELLERATOR_DTYPE_F32 && out_cols % 64 == 0
         && m->row_stride_bytes % 4u == 0u && m->row_stride_bytes >= m->ell_cols * m->bits / 8u
         && static_cast<std::uint64_t>(m->row_stride_bytes) * 32u <= 0xffffffffull) {
-        // the matrix-core form (same values, fp32 products and sums in another order)
+        // the matrix-core form (same values, fp32 products and sums in another order); operands
+        // through LDS when W's rows are whole 16-byte units and 32 of them span under 4 GiB
         const hipStream_t s = static_cast<hipStream_t>(stream);
         const dim3 grid((m->rows + 31u) / 32u), block(256);
+        const bool lds_w = (reinterpret_cast<std::uintptr_t>(rhs) & 15u) == 0u && rhs_ld % 4 == 0
+            && static_cast<std::uint64_t>(rhs_ld) * 4u * 32u <= 0xffffffffull && m->column_scales != nullptr
+            && (m->decode_policy != CX_DECODE_PER_GENE_AFFINE || m->column_offsets != nullptr);
+#define CX_QBELL_W(B, P)                                                                                 \
+    do {                                                                                                 \
+        if (lds_w) hipLaunchKernelGGL((bell_spmm_quant_lds<B, P>), grid, block, 0, s, a, out_cols);          \
+        else hipLaunchKernelGGL((bell_spmm_quant_mfma<B, P>), grid, block, 0, s, a, out_cols);              \
+    } while (0)
 #define CX_QBELL(B)                                                                                      \
     do {                                                                                                 \
-        if (m->decode_policy == CX_DECODE_PER_GENE_AFFINE)                                               \
-            hipLaunchKernelGGL((bell_spmm_quant_mfma<B, CX_DECODE_PER_GENE_AFFINE>), grid, block, 0, s, a, out_cols); \
-        else                                                                                             \
-            hipLaunchKernelGGL((bell_spmm_quant_mfma<B, CX_DECODE_COLUMN_SCALE_ROW_OFFSET>), grid, block, 0, s, a, \
-                               out_cols);                                                                \
+        if (m->decode_policy == CX_DECODE_PER_GENE_AFFINE) CX_QBELL_W(B, CX_DECODE_PER_GENE_AFFINE);       \
+        else CX_QBELL_W(B, CX_DECODE_COLUMN_SCALE_ROW_OFFSET);                                           \
     } while (0)
         switch (m->bits) {
         case 1: CX_QBELL(1); break;
@@ -965,6 +1122,7 @@ extern "C" int cx_bell_spmm_fwd_epilogue(const cx_bell_matrix *m, const void *rh
         default: CX_QBELL(8); break;
         }
 #undef CX_QBELL
+#undef CX_QBELL_W
         return check_launch("bell_spmm_quant_mfma");
     }
     const std::uint64_t threads = static_cast<std::uint64_t>(m->rows) * kWave;

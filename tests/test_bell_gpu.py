@@ -189,9 +189,11 @@ def _quantized_bell_32(rng, rows, cols, width, bits, policy):
 @pytest.mark.parametrize("bits,policy,n", [(8, 1, 256), (4, 2, 64), (2, 1, 128), (1, 2, 64), (8, 2, 192)])
 def test_quantized_bell_matrix_cores(oracle, bits, policy, n):
     """Quantized Blocked-ELL with 32x32 blocks and f32 W runs on the fp32 matrix cores
-    (bell_spmm_quant_mfma): within the bound of the float64 referee for every width and policy,
-    ragged row block and block column, invalid slots anywhere; a one-hot W returns every
-    decoded value bitwise (the codec's fma(code, scale, offset)); a fused epilogue applies."""
+    (bell_spmm_quant_lds, W tiles and metadata through LDS): within the bound of the float64
+    referee for every width and policy, ragged row block and block column, invalid slots
+    anywhere; a one-hot W returns every decoded value bitwise (the codec's fma(code, scale,
+    offset)); a fused epilogue applies. W at an address and row stride that are not whole
+    16-byte units takes the register form (bell_spmm_quant_mfma): bitwise the same sums."""
     import torch
 
     from cellerator_amd import BellMatrix, Epilogue, bell_spmm
@@ -214,7 +216,11 @@ def test_quantized_bell_matrix_cores(oracle, bits, policy, n):
     hot = bell_spmm(m, t(onehot))
     bias = rng.standard_normal(n).astype(np.float32)
     ep_out = bell_spmm(m, t(rhs), epilogue=Epilogue(kind=1, bias=t(bias)))  # bias
+    wide = torch.zeros((cols, n + 1), dtype=torch.float32, device="cuda")
+    wide[:, 1:] = t(rhs)
+    unaligned = bell_spmm(m, wide[:, 1:])  # 4 bytes past a 16-byte boundary, row stride n + 1
     torch.cuda.synchronize()
     check_against_referee(oracle, ref, mag, out.cpu().numpy())
+    assert torch.equal(unaligned.view(torch.int32), out.view(torch.int32))
     assert np.array_equal(hot.cpu().numpy().astype(np.float64), dec)
     check_against_referee(oracle, ref + bias[None, :].astype(np.float64), mag, ep_out.cpu().numpy())
