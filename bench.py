@@ -310,7 +310,7 @@ def parity_sample_qcsr(m, w, out, count: int, seed: int) -> dict:
 def bench_bell_quantized(args, torch, cfg) -> dict:
     """Config 4 with 8-bit per-gene affine codes: the reference's quantized Blocked-ELL
     projection (quantized_blocked_ell_spmm_fwd_f32, f32 W) on C4's block structure, through
-    cx_bell_spmm_fwd (the per-element kernel), N = 256."""
+    cx_bell_spmm_fwd (fp32 matrix cores, each slot's W tile staged in LDS), N = 256."""
     import numpy as np
 
     from cellerator_amd import BellMatrix, bell_spmm
@@ -344,7 +344,7 @@ def bench_bell_quantized(args, torch, cfg) -> dict:
         "config": {"workload": cfg.name + " 8-bit codes", "rows": m.rows, "genes": m.cols, "block_size": bs,
                    "valid_blocks": valid_blocks, "n_out": n_out, "seed": hex(cfg.seed)},
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": tflops / MFMA_FP32_PEAK_TFLOPS, "traffic": None,
+                     "frac": tflops / MFMA_FP32_PEAK_TFLOPS, "traffic": load_traffic(cfg.name + " 8-bit codes"),
                      "kernel": "bell_spmm_quant_lds<8, per-gene affine> (cx_bell_spmm_fwd: fp32 matrix cores, "
                                "W tiles and metadata through LDS)",
                      "kernel_ms_mean": kern_ms, "kernel_ms_median": statistics.median(ev),
