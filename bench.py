@@ -385,8 +385,8 @@ def bench_bell(args, torch, cfg) -> dict:
     groups = None if args.ungrouped else bell_plan_groups(m)
     torch.cuda.synchronize()
     log(f"generated {cfg.name}: {valid_blocks} valid 32x32 blocks in {time.perf_counter() - t0:.1f}s"
-        + ("" if groups is None else f"; {groups.group_count} groups cover {groups.grouped_row_blocks} "
-                                     f"row blocks, {groups.single_count} single"))
+        + ("" if groups is None else f"; {groups.planned_groups} groups of 2..4 and {groups.planned_singles} "
+                                     f"single row blocks, scheduled as {groups.group_count} units"))
     stream = torch.cuda.current_stream()
     # Headline: the values in block-major order (every 32x32 block's 2 KB contiguous, the
     # layout the CSR -> Blocked-ELL lowering emits), copied once like the packed panel; the
@@ -424,12 +424,13 @@ def bench_bell(args, torch, cfg) -> dict:
                    "seed": hex(cfg.seed),
                    "value_layout": "row-major" if mb is None else "block-major (copied once, untimed)",
                    "row_block_groups": None if groups is None else {
-                       "groups": groups.group_count, "grouped_row_blocks": groups.grouped_row_blocks,
-                       "single_row_blocks": groups.single_count}},
+                       "groups": groups.planned_groups, "single_row_blocks": groups.planned_singles,
+                       "launch_units": groups.group_count,
+                       "schedule": "XCD ranges balanced by value blocks (cx_bell_schedule_groups)"}},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
                      "traffic": load_traffic(cfg.name + ("" if mb is not None else " row-major")),
-                     "kernel": ("bell_spmm_mfma<256>" if groups is None else "bell_spmm_mfma_slab<256> (grouped, + singles)")
+                     "kernel": ("bell_spmm_mfma<256>" if groups is None else "bell_spmm_mfma_slab<256> (grouped, scheduled)")
                                + (", row-major values" if mb is None else ", block-major values"),
                      "kernel_ms_mean": kern_ms,
                      "kernel_ms_median": statistics.median(ev), "algorithmic_bytes": alg_bytes,

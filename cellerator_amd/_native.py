@@ -354,6 +354,8 @@ ENGINE_SIGNATURES = {
                                                    C.POINTER(CxSpmmEpilogue), p_void]),
     "cx_bell_plan_groups": (C.c_int, [p_void, u32, u32, u32, p_void, p_void, C.POINTER(u32),
                                       C.POINTER(u32)]),
+    "cx_bell_schedule_groups": (C.c_int, [p_void, u32, u32, p_void, p_void, u32, u32, p_void, p_void,
+                                          C.POINTER(u32)]),
     "cx_bell_plan_last_error": (C.c_char_p, []),
     "cx_bell_spmm_fwd_grouped": (C.c_int, [C.POINTER(CxBellMatrix), p_void, C.POINTER(CxBellGroups),
                                            i64, p_void, i64, p_void]),

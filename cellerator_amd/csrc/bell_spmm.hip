@@ -1261,7 +1261,7 @@ extern "C" int cx_bell_spmm_fwd_grouped_epilogue(const cx_bell_matrix *m,
     const std::uint32_t row_blocks = (m->rows + 31u) / 32u;
     if (static_cast<std::uint64_t>(groups->grouped_row_blocks) + groups->single_count != row_blocks
         || (groups->group_count != 0u
-            && (groups->group_offsets == nullptr || groups->grouped_row_blocks < 2u * groups->group_count
+            && (groups->group_offsets == nullptr || groups->grouped_row_blocks < groups->group_count
                 || groups->grouped_row_blocks > 4ull * groups->group_count))
         || (row_blocks != 0u && groups->order == nullptr))
         return fail(CX_STATUS_INVALID_SHAPE, "grouped Blocked-ELL: groups do not cover the row blocks");

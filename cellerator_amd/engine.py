@@ -439,21 +439,26 @@ def bell_spmm_packed(m: BellMatrix, packed_rhs: torch.Tensor, n: int,
 @dataclass
 class BellGroups:
     """Row-block groups of a Blocked-ELL matrix for the grouped MFMA path (host-planned once
-    per projection; see cx_bell_plan_groups)."""
+    per projection; see cx_bell_plan_groups and cx_bell_schedule_groups)."""
     group_count: int
     grouped_row_blocks: int
     single_count: int
     order: torch.Tensor          # int32 [row_blocks] (uint32 ids)
     group_offsets: torch.Tensor  # int32 [group_count + 1]
+    planned_groups: int = 0      # groups of 2..4 the planner formed (before a schedule)
+    planned_singles: int = 0     # row blocks it left single
 
     def descriptor(self) -> N.CxBellGroups:
         return N.CxBellGroups(self.group_count, self.grouped_row_blocks, self.single_count, 0,
                               _ptr(self.order), _ptr(self.group_offsets))
 
 
-def bell_plan_groups(m: BellMatrix, max_group: int = 4) -> BellGroups:
+def bell_plan_groups(m: BellMatrix, max_group: int = 4, schedule: bool = True) -> BellGroups:
     """Groups row blocks whose valid block-column lists are prefixes of one another (host
-    planner on a host copy of block_col_idx; the result is uploaded to m's device)."""
+    planner on a host copy of block_col_idx; the result is uploaded to m's device). With
+    `schedule` (the default) the plan is laid out for the launch by cx_bell_schedule_groups:
+    single row blocks become one-member groups and every XCD's range of groups carries about
+    the same number of value blocks."""
     import numpy as np
 
     rb = (m.rows + m.block_size - 1) // m.block_size
@@ -468,11 +473,25 @@ def bell_plan_groups(m: BellMatrix, max_group: int = 4) -> BellGroups:
                                  C.byref(gc), C.byref(sc))
     if st != 0:
         raise N.EngineError("cx_bell_plan_groups", st, lib.cx_bell_plan_last_error().decode())
+    planned = (gc.value, sc.value)
     grouped = int(offs[gc.value]) if gc.value else 0
+    n_groups, singles = gc.value, sc.value
+    if schedule:
+        s_order = np.zeros(rb, np.uint32)
+        s_offs = np.zeros(rb + 1, np.uint32)
+        units = C.c_uint32()
+        st = lib.cx_bell_schedule_groups(idx.ctypes.data if idx.size else None, rb, slots,
+                                         order.ctypes.data if order.size else None, offs.ctypes.data,
+                                         gc.value, sc.value, s_order.ctypes.data if s_order.size else None,
+                                         s_offs.ctypes.data, C.byref(units))
+        if st != 0:
+            raise N.EngineError("cx_bell_schedule_groups", st, lib.cx_bell_plan_last_error().decode())
+        order, offs, n_groups, grouped, singles = s_order, s_offs, units.value, rb, 0
     dev = m.block_col_idx.device
-    return BellGroups(gc.value, grouped, sc.value,
+    return BellGroups(n_groups, grouped, singles,
                       torch.from_numpy(order.view(np.int32)).to(dev),
-                      torch.from_numpy(offs[: gc.value + 1].view(np.int32).copy()).to(dev))
+                      torch.from_numpy(offs[: n_groups + 1].view(np.int32).copy()).to(dev),
+                      planned[0], planned[1])
 
 
 def bell_spmm_grouped(m: BellMatrix, packed_rhs: torch.Tensor, groups: BellGroups, n: int,

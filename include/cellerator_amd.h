@@ -567,11 +567,12 @@ int cx_bell_spmm_fwd_packed_epilogue(const cx_bell_matrix *a, const uint16_t *pa
 
 /* Row-block groups for the grouped MFMA path (engine addition, no counterpart in the
  * reference; a persistent preprocessing of the Blocked-ELL projection, like the packed
- * panel). order[0 .. grouped_row_blocks) holds group_count groups of 2..4 row blocks
+ * panel). order[0 .. grouped_row_blocks) holds group_count groups of 1..4 row blocks
  * (group g = order[group_offsets[g] .. group_offsets[g+1]), longest member last) whose valid
  * block-column lists are prefixes of the longest member's; order[grouped_row_blocks ..)
- * holds single_count row blocks run one per workgroup. order and group_offsets are device
- * arrays. */
+ * holds single_count row blocks run one per workgroup. cx_bell_plan_groups forms groups of
+ * 2..4 and leaves the rest single; cx_bell_schedule_groups folds the singles in as
+ * one-member groups. order and group_offsets are device arrays. */
 typedef struct cx_bell_groups {
     uint32_t group_count;
     uint32_t grouped_row_blocks;
@@ -587,6 +588,21 @@ typedef struct cx_bell_groups {
 int cx_bell_plan_groups(const uint32_t *block_col_idx, uint32_t row_blocks, uint32_t slots,
                         uint32_t max_group, uint32_t *order, uint32_t *group_offsets,
                         uint32_t *group_count, uint32_t *single_count);
+
+/* Launch schedule of a cx_bell_plan_groups plan (host arrays in, host arrays out): every
+ * group and every single row block becomes one unit (a group of 1..4 row blocks), and the
+ * units are ordered so that the eight contiguous ranges the grouped kernels give the eight
+ * XCDs (workgroup i runs unit (i % 8) * (units / 8) + i / 8; the last units % 8 keep their
+ * index) carry about the same number of value blocks, units of one module (same first block
+ * column) kept in one range where they fit. sched_order holds row_blocks ids, sched_offsets
+ * units + 1 entries (capacity row_blocks + 1); pass them as a cx_bell_groups with
+ * group_count = units, grouped_row_blocks = row_blocks and single_count = 0. Deterministic.
+ * No counterpart in the reference: its Blocked-ELL kernel runs one block row per thread
+ * block in matrix order. */
+int cx_bell_schedule_groups(const uint32_t *block_col_idx, uint32_t row_blocks, uint32_t slots,
+                            const uint32_t *order, const uint32_t *group_offsets,
+                            uint32_t group_count, uint32_t single_count, uint32_t *sched_order,
+                            uint32_t *sched_offsets, uint32_t *unit_count);
 const char *cx_bell_plan_last_error(void);
 
 /* Same result contract as cx_bell_spmm_fwd_packed: per group, each N x 32 panel slice is

@@ -115,10 +115,12 @@ def test_generated_c4_sample(oracle):
 
 @pytest.mark.parametrize("n", [64, 128, 256])
 @pytest.mark.parametrize("scatter", [False, True])
-def test_grouped_mfma_equals_ungrouped_and_referee(oracle, n, scatter):
-    """Grouped path (planner groups + singletons) is bitwise equal to the per-row-block MFMA
-    kernel (same slot order per output) and within tolerance of the float64 referee, with
-    valid slots contiguous or scattered among empty ones."""
+@pytest.mark.parametrize("schedule", [True, False])
+def test_grouped_mfma_equals_ungrouped_and_referee(oracle, n, scatter, schedule):
+    """Grouped path is bitwise equal to the per-row-block MFMA kernel (same slot order per
+    output) and within tolerance of the float64 referee, with valid slots contiguous or
+    scattered among empty ones: the planner's groups + singletons, and its launch schedule
+    (singles folded in as one-member groups, units dealt over the XCD ranges)."""
     import torch
 
     from cellerator_amd import (BellMatrix, bell_pack_rhs, bell_plan_groups, bell_spmm_grouped,
@@ -143,8 +145,11 @@ def test_grouped_mfma_equals_ungrouped_and_referee(oracle, n, scatter):
                    values=torch.from_numpy(vbits.view(np.int16)).view(torch.bfloat16).cuda())
     rhs = torch.from_numpy(wbits.view(np.int16)).view(torch.bfloat16).cuda()
     packed = bell_pack_rhs(rhs)
-    groups = bell_plan_groups(m)
+    groups = bell_plan_groups(m, schedule=schedule)
     assert groups.group_count > 0 and groups.grouped_row_blocks + groups.single_count == rb
+    if schedule:
+        assert groups.single_count == 0 and groups.group_count == groups.planned_groups + groups.planned_singles
+        assert groups.group_count >= 8 and groups.planned_singles > 0
     a = bell_spmm_packed(m, packed, n)
     b = bell_spmm_grouped(m, packed, groups, n)
     torch.cuda.synchronize()
