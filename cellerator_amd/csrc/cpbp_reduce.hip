@@ -235,21 +235,32 @@ __global__ __launch_bounds__(kWave *kCpbpWaves) void cpbp_reduce_kernel(CpbpArgs
     __shared__ float wp[kLdsPlan ? kWeightsLds + 32 : 1];
     __shared__ std::uint32_t block_begin[kLdsPlan ? kBlocksLds : 1];
     __shared__ WaveLds wave_lds[kCpbpWaves];
+    __shared__ std::uint32_t next_tile;  // the workgroup's tile queue (below)
     const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
     const std::uint32_t wave = uniform(threadIdx.x / kWave);
+    if (threadIdx.x == 0) next_tile = kCpbpWaves;
     if constexpr (kLdsPlan) {
         for (std::uint32_t f = threadIdx.x; f < a.feature_count + 32u; f += blockDim.x)
             wp[f] = f < a.feature_count ? a.weights[a.feature_permutation[f]] : 0.0f;
         for (std::uint32_t k = threadIdx.x; k <= a.feature_block_count; k += blockDim.x)
             block_begin[k] = a.feature_block_offsets[k];
-        __syncthreads();
     }
+    __syncthreads();
     WaveLds &L = wave_lds[wave];
     const MaskT *masks = static_cast<const MaskT *>(a.cell_masks);
     const ValT *values = static_cast<const ValT *>(a.values);
 
-    for (std::uint32_t t = blockIdx.x * kCpbpWaves + wave; t < a.tile_count;
-         t += gridDim.x * kCpbpWaves) {
+    // Workgroup b (one per CU) owns tiles b, b + gridDim.x, b + 2 gridDim.x, ...: every CU
+    // gets the same number of tiles to within one. Its waves take them first come, first
+    // served from an LDS counter (wave w starts with the w-th), so a wave that drew light
+    // tiles takes more and the CU's SIMDs end together. Each tile is still reduced by one
+    // wave in a fixed order, so results do not depend on which wave takes it. (Dealt
+    // statically wave-major, tile t to wave t % (gridDim.x * 16), the first CUs' waves all
+    // held one tile more than the last CUs', and the heaviest CU carried 5% above the mean.)
+    for (std::uint32_t k = wave;;) {
+        const std::uint64_t t64 = blockIdx.x + static_cast<std::uint64_t>(gridDim.x) * k;
+        if (t64 >= a.tile_count) break;
+        const std::uint32_t t = static_cast<std::uint32_t>(t64);
 #pragma unroll
         for (int k = 0; k < kAccSpread; ++k) L.acc[lane * kAccSpread + k] = 0.0f;
         // tile bounds are wave-uniform: keep them (and the buffer resources) in SGPRs
@@ -370,6 +381,10 @@ __global__ __launch_bounds__(kWave *kCpbpWaves) void cpbp_reduce_kernel(CpbpArgs
             a.row_values[a.row_permutation[exec_row]] = sum;
         }
         lds_order();
+        std::uint32_t nk = 0u;
+        if (lane == 0)
+            nk = __hip_atomic_fetch_add(&next_tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        k = uniform(static_cast<std::uint32_t>(__shfl(static_cast<int>(nk), 0, kWave)));
     }
 }
 
