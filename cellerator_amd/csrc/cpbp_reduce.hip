@@ -19,8 +19,9 @@
 //      wave max-scan) and its row (the rank-th set bit of the descriptor's cell mask);
 //   3. the batch's values, loaded coalesced, are staged in LDS; each entry lane sums
 //      value * wp[block start + bit] over its own values in a register (fp32 FMA) and adds
-//      the sum to its row's accumulator in LDS (one LDS atomic per entry, spread over 4
-//      slots per row; per-value LDS float atomics were measured 2x slower overall).
+//      the sum to its row's accumulator in LDS: an integer atomic numbers the batch's
+//      entries of each row, and the j-th entries of all rows are added in round j with a
+//      plain read and write (no float atomics: they are an order of magnitude slower).
 // Loads are raw buffer loads over the tile's slices (0 past the end, no branches) and run
 // one batch ahead on ping-pong registers, so a batch's waits cover only its own loads.
 // The summation order (per entry, then entries per row) differs from the reference's
@@ -53,13 +54,13 @@ struct CpbpArgs {
 
 constexpr int kCpbpWaves = 16;         // waves (tiles in flight) per workgroup
 constexpr int kCpbpGrid = 256;         // one workgroup per CU (LDS-limited)
-constexpr int kAccSpread = 4;          // accumulator slots per row
 constexpr std::uint32_t kBatchValues = 512;  // values of one entry batch (staged in LDS)
 constexpr std::uint32_t kWeightsLds = 20480;  // features whose weights fit the LDS stage
 constexpr std::uint32_t kBlocksLds = 2048;    // feature block offsets staged in LDS
 
 struct WaveLds {
-    float acc[64 * kAccSpread];
+    float acc[64];            // the tile's row sums
+    std::uint32_t occ[64];    // per batch: entries counted per row
     float stage[kBatchValues + 4];  // + one step of the 4-wide read past an entry's end
     std::int32_t slot[64];
 };
@@ -261,8 +262,7 @@ __global__ __launch_bounds__(kWave *kCpbpWaves) void cpbp_reduce_kernel(CpbpArgs
         const std::uint64_t t64 = blockIdx.x + static_cast<std::uint64_t>(gridDim.x) * k;
         if (t64 >= a.tile_count) break;
         const std::uint32_t t = static_cast<std::uint32_t>(t64);
-#pragma unroll
-        for (int k = 0; k < kAccSpread; ++k) L.acc[lane * kAccSpread + k] = 0.0f;
+        L.acc[lane] = 0.0f;
         // tile bounds are wave-uniform: keep them (and the buffer resources) in SGPRs
         const std::uint32_t d_end = uniform(a.tile_block_offsets[t + 1]);
         std::uint32_t d = uniform(a.tile_block_offsets[t]);
@@ -312,10 +312,11 @@ __global__ __launch_bounds__(kWave *kCpbpWaves) void cpbp_reduce_kernel(CpbpArgs
             for (std::uint32_t c = 0; c < kBatchValues / kWave; ++c)
                 L.stage[c * kWave + static_cast<std::uint32_t>(lane)] = x_cur[c];
             lds_order();
-            if (static_cast<std::uint32_t>(lane) < cur_x.n) {
+            const bool has = static_cast<std::uint32_t>(lane) < cur_x.n;
+            float sum = 0.0f;
+            if (has) {
                 std::uint32_t m = cur.gm;
                 const float *v = &L.stage[min(cur.s_j - cur_x.s0, kBatchValues)];
-                float sum = 0.0f;
                 if constexpr (kLdsPlan) {
                     const float *w = &wp[bb];
                     // An absent bit reads weight 31 of the block (m | bit 31 is never 0, and
@@ -356,10 +357,23 @@ __global__ __launch_bounds__(kWave *kCpbpWaves) void cpbp_reduce_kernel(CpbpArgs
                         ++v;
                     }
                 }
-                __hip_atomic_fetch_add(&L.acc[row * kAccSpread + (lane & (kAccSpread - 1))], sum,
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
             }
+            // Each entry's sum goes to its row. Rows repeat within a batch (one entry per
+            // descriptor that holds the row), and LDS float atomics cost ~190 CU cycles per
+            // wave instruction here, against ~16 for an integer atomic with return and ~10 for
+            // a plain read and write: so each entry takes its occurrence number among the
+            // batch's entries of its row from an integer atomic, and round j adds the sums of
+            // the j-th occurrences with a plain read, add and write (the rows of one round are
+            // distinct). Two or three rounds cover a batch.
+            if (has) L.occ[row] = 0u;
             lds_order();
+            std::uint32_t occ = 0u;
+            if (has) occ = __hip_atomic_fetch_add(&L.occ[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+            for (std::uint32_t j = 0u;; ++j) {
+                if (has && occ == j) L.acc[row] += sum;
+                lds_order();
+                if (__builtin_amdgcn_ballot_w64(has && occ > j) == 0ull) break;
+            }
             e = e_next;
             d = d_next;
         };
@@ -375,10 +389,7 @@ __global__ __launch_bounds__(kWave *kCpbpWaves) void cpbp_reduce_kernel(CpbpArgs
         lds_order();
         const std::uint32_t exec_row = t * a.tile_row_width + static_cast<std::uint32_t>(lane);
         if (static_cast<std::uint32_t>(lane) < a.tile_row_width && exec_row < a.row_count) {
-            float sum = 0.0f;
-#pragma unroll
-            for (int k = 0; k < kAccSpread; ++k) sum += L.acc[lane * kAccSpread + k];
-            a.row_values[a.row_permutation[exec_row]] = sum;
+            a.row_values[a.row_permutation[exec_row]] = L.acc[lane];
         }
         lds_order();
         std::uint32_t nk = 0u;
