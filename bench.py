@@ -482,7 +482,8 @@ def bench_bell(args, torch, cfg) -> dict:
 
 
 def bench_cpbp(args, torch, cfg) -> dict:
-    """Config 5: CP-BP feature-weighted row reduction on 64-row tiles (cx_cpbp_reduce)."""
+    """Config 5: CP-BP feature-weighted row reduction on 64-row tiles (cx_cpbp_reduce_rows over
+    per-entry rows made once; cx_cpbp_reduce timed beside it)."""
     import numpy as np
 
     from cellerator_amd import cpbp, cpbp_reduce
@@ -510,11 +511,28 @@ def bench_cpbp(args, torch, cfg) -> dict:
         f"in {time.perf_counter() - t0:.1f}s (device tile build {build_ms:.0f} ms)")
     stream = torch.cuda.current_stream()
 
+    # Headline: the reduction with each entry's row and block start read from a per-entry
+    # array made once per tile structure (cx_cpbp_entry_rows, untimed, like the Blocked-ELL
+    # panel); the walk that looks every entry's descriptor up per launch is timed beside it
+    # (bitwise the same output).
+    from cellerator_amd import cpbp_entry_rows, cpbp_reduce_rows
+    torch.cuda.synchronize()
+    tr = time.perf_counter()
+    entry_rows = cpbp_entry_rows(tiles, stream=stream)
+    torch.cuda.synchronize()
+    rows_ms = (time.perf_counter() - tr) * 1e3
+
     def launch():
-        cpbp_reduce(tiles, weights, out=out, stream=stream)
+        cpbp_reduce_rows(tiles, entry_rows, weights, out=out, stream=stream)
 
     wall_ms, ev = time_launches(torch, launch, args.steps, args.warmup, stream)
     kern_ms = statistics.mean(ev)
+    desc_out = torch.empty_like(out)
+    desc_wall, desc_ev = time_launches(torch, lambda: cpbp_reduce(tiles, weights, out=desc_out, stream=stream),
+                                       args.steps, args.warmup, stream)
+    torch.cuda.synchronize()
+    desc_equal = bool(torch.equal(desc_out.view(torch.int32), out.view(torch.int32)))
+    del desc_out
     alg_bytes = tiles.nbytes_algorithmic()
     achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
     # the N = 1 CSR comparator on the same canonical matrix, as the reference's reduction
@@ -536,11 +554,17 @@ def bench_cpbp(args, torch, cfg) -> dict:
                    "tile_row_width": cfg.tile_row_width, "block_width": cfg.block_width,
                    "tile_blocks": tiles.descriptor().tile_block_count,
                    "row_block_entries": tiles.descriptor().row_block_entry_count, "seed": hex(cfg.seed),
-                   "tile_build": {"where": "device", "ms": build_ms}},
+                   "tile_build": {"where": "device", "ms": build_ms},
+                   "entry_rows": {"bytes": int(entry_rows.numel()) * 4, "ms": rows_ms,
+                                  "note": "made once per tile structure (cx_cpbp_entry_rows), untimed"}},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(cfg.name),
-                     "kernel": "cpbp_reduce_kernel<u64,f32,lds-weights>", "kernel_ms_mean": kern_ms,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(cfg.name + " entry rows"),
+                     "kernel": "cpbp_reduce_kernel<u64,f32,lds-weights,with-entry-rows> (cx_cpbp_reduce_rows)",
+                     "kernel_ms_mean": kern_ms,
                      "kernel_ms_median": statistics.median(ev), "algorithmic_bytes": alg_bytes},
+        "descriptor_walk": {"kernel": "cpbp_reduce_kernel<u64,f32,lds-weights> (cx_cpbp_reduce)",
+                            "ms_per_step": desc_wall, "kernel_ms_mean": statistics.mean(desc_ev),
+                            "bitwise_equal_to_headline": desc_equal},
         "csr_spmv_comparator": {"kernel": "csr_spmv_kernel<f32>", "kernel_ms_mean": spmv_ms,
                                 "algorithmic_bytes": spmv_bytes,
                                 "achieved_gbs": spmv_bytes / (spmv_ms * 1e-3) / 1e9,

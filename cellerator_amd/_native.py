@@ -363,6 +363,8 @@ ENGINE_SIGNATURES = {
                                                     C.POINTER(CxBellGroups), i64, p_void, i64,
                                                     C.POINTER(CxSpmmEpilogue), p_void]),
     "cx_cpbp_reduce": (C.c_int, [C.POINTER(CxCpbpTiles), p_void, u64, p_void, u64, p_void]),
+    "cx_cpbp_entry_rows": (C.c_int, [C.POINTER(CxCpbpTiles), p_void, u64, p_void]),
+    "cx_cpbp_reduce_rows": (C.c_int, [C.POINTER(CxCpbpTiles), p_void, p_void, u64, p_void, u64, p_void]),
     "cx_cpbp_reduction_identity": (u64, [C.POINTER(CxCpbpReductionView)]),
     "cx_cpbp_reduction_view_from_cpk1": (C.c_int, [C.POINTER(CxCpk1View), u64, C.POINTER(CxCpbpReductionView)]),
     "cx_cpbp_reduce_checked": (C.c_int, [C.POINTER(CxCpbpReductionView), p_void, u64, p_void, u64, p_void]),

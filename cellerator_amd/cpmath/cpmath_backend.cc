@@ -60,6 +60,7 @@ struct bell_prepared {
 struct cpbp_prepared {
     bool validated = false;
     cx_cpbp_tiles tiles{};  // value pointer cleared: values travel in the plane
+    const uint32_t *entry_rows = nullptr;  // cx_cpbp_entry_rows of `tiles` (caller-owned), or none
 };
 
 struct projection_state {
@@ -522,11 +523,17 @@ core::operation_status run_cpbp(const core::prepared_operation &p,
         return bad_launch("feature weights must be a contiguous f32 [genes] tensor");
     if (!dense_shape(y, numeric_type::f32, 1u, d.rows, 0u, l))
         return bad_launch("row values must be a contiguous f32 [cells] tensor");
-    const int rc = cx_cpbp_reduce(&t, static_cast<const float *>(w.data), d.cols,
-                                  static_cast<float *>(y.data), d.rows, l.stream.stream);
+    // with the validated structure's entry rows, each entry's row and block start are read
+    // instead of looked up from its descriptor (bitwise the same sums)
+    const bool rows = checked && s->cpbp.entry_rows != nullptr;
+    const int rc = rows ? cx_cpbp_reduce_rows(&t, s->cpbp.entry_rows, static_cast<const float *>(w.data), d.cols,
+                                              static_cast<float *>(y.data), d.rows, l.stream.stream)
+                        : cx_cpbp_reduce(&t, static_cast<const float *>(w.data), d.cols,
+                                         static_cast<float *>(y.data), d.rows, l.stream.stream);
     if (rc != CX_STATUS_SUCCESS) return engine_failed(rc);
-    dispatched = native ? (checked ? "cpbp:native-tile+checked" : "cpbp:native-tile")
-                        : (checked ? "cpbp:checked" : "cpbp:unchecked");
+    dispatched = native ? (rows ? "cpbp:native-tile+checked+entry-rows"
+                                : checked ? "cpbp:native-tile+checked" : "cpbp:native-tile")
+                        : (rows ? "cpbp:checked+entry-rows" : checked ? "cpbp:checked" : "cpbp:unchecked");
     return {};
 }
 
@@ -881,7 +888,8 @@ std::uint64_t execution_order_persistent_bytes(execution::projection_handle proj
 }
 
 core::operation_status prepare_cpbp_state(execution::projection_handle projection,
-                                          const cx_cpbp_reduction_view &view) noexcept {
+                                          const cx_cpbp_reduction_view &view, uint32_t *entry_rows,
+                                          uint64_t entry_rows_capacity, void *stream) noexcept {
     std::lock_guard<std::mutex> lock(projections_mutex);
     projection_state *s = find_live(projection);
     if (s == nullptr) return fail(code::invalid_argument, "projection is not declared");
@@ -896,10 +904,18 @@ core::operation_status prepare_cpbp_state(execution::projection_handle projectio
         const core::operation_status st = engine_failed(rc);
         return {code::preparation_failed, st.binding, "reduction contract rejected (see last_engine_error)"};
     }
+    if (entry_rows != nullptr) {
+        const int er = cx_cpbp_entry_rows(&view.tiles, entry_rows, entry_rows_capacity, stream);
+        if (er != CX_STATUS_SUCCESS) {
+            const core::operation_status st = engine_failed(er);
+            return {code::preparation_failed, st.binding, "entry rows rejected (see last_engine_error)"};
+        }
+    }
     s->cpbp.validated = true;
     s->cpbp.tiles = view.tiles;
     s->cpbp.tiles.values = nullptr;
     s->cpbp.tiles.value_dtype = 0u;
+    s->cpbp.entry_rows = entry_rows;
     return {};
 }
 

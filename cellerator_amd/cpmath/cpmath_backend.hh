@@ -163,12 +163,19 @@ core::operation_status prepare_blocked_ell_state(execution::projection_handle pr
 // reference's validate_metadata (components/CellPack/src/feature_weighted_row_reduction_cuda.cu:57-136).
 // After it, a launch runs only if its tile view equals the validated view's tiles
 // ("cpbp:checked"); without it the tile view is run as bound ("cpbp:unchecked").
+// `entry_rows` (optional, caller-owned device memory of entry_rows_capacity u32, at least
+// the tiles' row_block_entry_count; kept until the projection is retired) receives
+// cx_cpbp_entry_rows of the validated tiles, enqueued on `stream`; checked launches then
+// read each entry's row and block start from it ("cpbp:checked+entry-rows"), bitwise the
+// same sums as the descriptor walk.
 core::operation_status prepare_cpbp_state(execution::projection_handle projection,
-                                          const cx_cpbp_reduction_view &view) noexcept;
+                                          const cx_cpbp_reduction_view &view, uint32_t *entry_rows = nullptr,
+                                          uint64_t entry_rows_capacity = 0u, void *stream = nullptr) noexcept;
 
 // Kernel form the last successful run on this thread dispatched, e.g.
 // "qcsr:pairs+sorted", "qcsr:gene-affine", "qcsr:execution-order", "bell:grouped+panel",
-// "bell:mfma+repack", "bell:generic", "cpbp:checked", "cpbp:native-tile".
+// "bell:mfma+repack", "bell:generic", "cpbp:checked", "cpbp:checked+entry-rows",
+// "cpbp:native-tile".
 const char *last_dispatch() noexcept;
 
 core::operation_candidate quantized_csr_candidate() noexcept;

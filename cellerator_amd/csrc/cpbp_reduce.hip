@@ -27,6 +27,8 @@
 // The summation order (per entry, then entries per row) differs from the reference's
 // (descriptor, then bit) order; results agree within the reference's tolerance
 // (feature_weighted_row_reduction.hh:13-14) widened for fp32 reordering.
+#include <cstdio>
+
 #include "cx_common.hpp"
 
 namespace cx {
@@ -45,6 +47,7 @@ struct CpbpArgs {
     const std::uint32_t *row_permutation;
     const float *weights;
     float *row_values;
+    std::uint32_t *entry_rows;  // per entry: block start << 6 | tile row (written by the rows walk)
     std::uint32_t row_count;
     std::uint32_t tile_count;
     std::uint32_t tile_row_width;
@@ -156,8 +159,13 @@ __device__ __forceinline__ float bload_value(rsrc_t r, std::uint32_t index) {
     }
 }
 
+// What one walk over the tiles does: reduce from the descriptors (the reference layout
+// alone), reduce with each entry's row and block start read from a prepared per-entry array,
+// or compute that array.
+enum class Walk { reduce, with_rows, make_rows };
+
 struct TileRsrc {
-    rsrc_t value_offsets, gene_masks, entry_offsets, masks, block_ids, values;
+    rsrc_t value_offsets, gene_masks, entry_offsets, masks, block_ids, values, rows;
     std::uint32_t e0, d0, v0;
 };
 
@@ -166,12 +174,12 @@ struct TileRsrc {
 // cell mask, block id).
 template<typename MaskT>
 struct BatchInput {
-    std::uint32_t s_j, s_next, gm, eo_k, blk_k;
+    std::uint32_t s_j, s_next, gm, eo_k, blk_k, rb;
     MaskT mask_k;
     bool has_entry, has_desc;
 };
 
-template<typename MaskT>
+template<typename MaskT, Walk kWalk>
 __device__ __forceinline__ BatchInput<MaskT> load_batch(const TileRsrc &r, std::uint32_t e,
                                                         std::uint32_t e_end, std::uint32_t d,
                                                         std::uint32_t d_end, int lane) {
@@ -187,9 +195,18 @@ __device__ __forceinline__ BatchInput<MaskT> load_batch(const TileRsrc &r, std::
     b.s_j = b.has_entry ? s_j : 0u;
     b.s_next = b.has_entry ? s_next : 0u;
     b.gm = b.has_entry ? gm : 0u;
-    b.eo_k = bload32(r.entry_offsets, di * 4u);
-    b.mask_k = bload_mask<MaskT>(r.masks, di);
-    b.blk_k = bload32(r.block_ids, di * 4u);
+    if constexpr (kWalk == Walk::with_rows) {
+        const std::uint32_t rb = bload32(r.rows, ei * 4u);
+        b.rb = b.has_entry ? rb : 0u;
+        b.eo_k = 0u;
+        b.mask_k = 0u;
+        b.blk_k = 0u;
+    } else {
+        b.eo_k = bload32(r.entry_offsets, di * 4u);
+        b.mask_k = bload_mask<MaskT>(r.masks, di);
+        b.blk_k = bload32(r.block_ids, di * 4u);
+        b.rb = 0u;
+    }
     return b;
 }
 
@@ -230,22 +247,24 @@ __device__ __forceinline__ void load_values(float (&x)[kBatchValues / kWave], co
         x[c] = bload_value<ValT>(r.values, s0 - r.v0 + c * kWave + static_cast<std::uint32_t>(lane));
 }
 
-template<typename MaskT, typename ValT, bool kLdsPlan>
+template<typename MaskT, typename ValT, bool kLdsPlan, Walk kWalk>
 __global__ __launch_bounds__(kWave *kCpbpWaves) void cpbp_reduce_kernel(CpbpArgs a) {
     // Plan staged in LDS: permuted weights (zero-padded by one block) and block starts.
-    __shared__ float wp[kLdsPlan ? kWeightsLds + 32 : 1];
-    __shared__ std::uint32_t block_begin[kLdsPlan ? kBlocksLds : 1];
+    constexpr bool kStageWeights = kLdsPlan && kWalk != Walk::make_rows;
+    constexpr bool kStageBlocks = kLdsPlan && kWalk == Walk::reduce;
+    __shared__ float wp[kStageWeights ? kWeightsLds + 32 : 1];
+    __shared__ std::uint32_t block_begin[kStageBlocks ? kBlocksLds : 1];
     __shared__ WaveLds wave_lds[kCpbpWaves];
     __shared__ std::uint32_t next_tile;  // the workgroup's tile queue (below)
     const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
     const std::uint32_t wave = uniform(threadIdx.x / kWave);
     if (threadIdx.x == 0) next_tile = kCpbpWaves;
-    if constexpr (kLdsPlan) {
+    if constexpr (kStageWeights)
         for (std::uint32_t f = threadIdx.x; f < a.feature_count + 32u; f += blockDim.x)
             wp[f] = f < a.feature_count ? a.weights[a.feature_permutation[f]] : 0.0f;
+    if constexpr (kStageBlocks)
         for (std::uint32_t k = threadIdx.x; k <= a.feature_block_count; k += blockDim.x)
             block_begin[k] = a.feature_block_offsets[k];
-    }
     __syncthreads();
     WaveLds &L = wave_lds[wave];
     const MaskT *masks = static_cast<const MaskT *>(a.cell_masks);
@@ -279,6 +298,7 @@ __global__ __launch_bounds__(kWave *kCpbpWaves) void cpbp_reduce_kernel(CpbpArgs
         r.masks = make_rsrc(masks + d, (d_end - d) * static_cast<std::uint32_t>(sizeof(MaskT)));
         r.block_ids = make_rsrc(a.tile_block_ids + d, (d_end - d) * 4u);
         r.values = make_rsrc(values + r.v0, (v_tile_end - r.v0) * static_cast<std::uint32_t>(sizeof(ValT)));
+        if constexpr (kWalk == Walk::with_rows) r.rows = make_rsrc(a.entry_rows + e, (e_end - e) * 4u);
 
         // Two-stage pipeline over ping-pong register sets (no copies, so no forced waits):
         // while batch i is reduced, the entries/descriptors of batch i+1 and the 512-value
@@ -287,10 +307,15 @@ __global__ __launch_bounds__(kWave *kCpbpWaves) void cpbp_reduce_kernel(CpbpArgs
                         BatchInput<MaskT> &nxt, float (&x_nxt)[kBatchValues / kWave]) {
             const BatchExtent cur_x = batch_extent(cur);
             const std::uint32_t e_next = e + cur_x.n;
-            const std::uint32_t d_next = next_descriptor(cur, d, e_next);
-            nxt = load_batch<MaskT>(r, e_next, e_end, d_next, d_end, lane);
-            load_values<ValT>(x_nxt, r, cur_x.s0 + cur_x.nv, lane);
+            const std::uint32_t d_next = kWalk == Walk::with_rows ? d : next_descriptor(cur, d, e_next);
+            nxt = load_batch<MaskT, kWalk>(r, e_next, e_end, d_next, d_end, lane);
+            if constexpr (kWalk != Walk::make_rows) load_values<ValT>(x_nxt, r, cur_x.s0 + cur_x.nv, lane);
 
+            std::uint32_t row, bb;
+            if constexpr (kWalk == Walk::with_rows) {
+                row = cur.rb & 63u;
+                bb = cur.rb >> 6;
+            } else {
             // entry -> descriptor (slots + max-scan) -> row and block start
             L.slot[lane] = 0;
             lds_order();
@@ -302,10 +327,13 @@ __global__ __launch_bounds__(kWave *kCpbpWaves) void cpbp_reduce_kernel(CpbpArgs
             const std::uint32_t my_eo = __shfl(cur.eo_k, kd, kWave);
             const MaskT my_mask = __shfl(cur.mask_k, kd, kWave);
             const std::uint32_t my_blk = __shfl(cur.blk_k, kd, kWave);
-            const std::uint32_t row = select_bit(my_mask, e + lane - my_eo) & 63u;
-            std::uint32_t bb;
-            if constexpr (kLdsPlan) bb = min(block_begin[min(my_blk, a.feature_block_count)], a.feature_count);
-            else bb = a.feature_block_offsets[min(my_blk, a.feature_block_count)];
+            row = select_bit(my_mask, e + lane - my_eo) & 63u;
+            if constexpr (kStageBlocks) bb = min(block_begin[min(my_blk, a.feature_block_count)], a.feature_count);
+            else bb = min(a.feature_block_offsets[min(my_blk, a.feature_block_count)], a.feature_count);
+            }
+            if constexpr (kWalk == Walk::make_rows) {
+                if (static_cast<std::uint32_t>(lane) < cur_x.n) a.entry_rows[e + static_cast<std::uint32_t>(lane)] = bb << 6 | row;
+            } else {
 
             // stage the batch's values; each entry sums its own values in a register
 #pragma unroll
@@ -374,13 +402,14 @@ __global__ __launch_bounds__(kWave *kCpbpWaves) void cpbp_reduce_kernel(CpbpArgs
                 lds_order();
                 if (__builtin_amdgcn_ballot_w64(has && occ > j) == 0ull) break;
             }
+            }
             e = e_next;
             d = d_next;
         };
 
-        BatchInput<MaskT> in_a = load_batch<MaskT>(r, e, e_end, d, d_end, lane), in_b;
+        BatchInput<MaskT> in_a = load_batch<MaskT, kWalk>(r, e, e_end, d, d_end, lane), in_b;
         float x_a[kBatchValues / kWave], x_b[kBatchValues / kWave];
-        load_values<ValT>(x_a, r, r.v0, lane);
+        if constexpr (kWalk != Walk::make_rows) load_values<ValT>(x_a, r, r.v0, lane);
         while (e < e_end) {
             step(in_a, x_a, in_b, x_b);
             if (e >= e_end) break;
@@ -388,7 +417,7 @@ __global__ __launch_bounds__(kWave *kCpbpWaves) void cpbp_reduce_kernel(CpbpArgs
         }
         lds_order();
         const std::uint32_t exec_row = t * a.tile_row_width + static_cast<std::uint32_t>(lane);
-        if (static_cast<std::uint32_t>(lane) < a.tile_row_width && exec_row < a.row_count) {
+        if (kWalk != Walk::make_rows && static_cast<std::uint32_t>(lane) < a.tile_row_width && exec_row < a.row_count) {
             a.row_values[a.row_permutation[exec_row]] = L.acc[lane];
         }
         lds_order();
@@ -402,45 +431,74 @@ __global__ __launch_bounds__(kWave *kCpbpWaves) void cpbp_reduce_kernel(CpbpArgs
 } // namespace
 } // namespace cx
 
-extern "C" int cx_cpbp_reduce(const cx_cpbp_tiles *t, const float *feature_weights,
-                              uint64_t feature_weight_capacity, float *row_values,
-                              uint64_t row_capacity, void *stream) {
-    using namespace cx;
-    clear_error();
-    if (t == nullptr) return fail(CX_STATUS_INVALID_ARGUMENT, "cx_cpbp_reduce: null tiles");
-    // Metadata checks of validate_metadata (feature_weighted_row_reduction_cuda.cu:57-136).
+namespace cx {
+namespace {
+
+// Metadata, dimension, pointer and aliasing checks of cx_cpbp_reduce (validate_metadata and
+// validate_output, feature_weighted_row_reduction_cuda.cu:57-178) for the walks over tiles
+// `t`. `weights`/`out` are checked when `reduce`; `entry_rows`/`rows_capacity` when given.
+int check_walk(const cx_cpbp_tiles *t, bool reduce, const float *feature_weights,
+               uint64_t feature_weight_capacity, const float *row_values, uint64_t row_capacity,
+               const std::uint32_t *entry_rows, uint64_t rows_capacity, const char *who) {
+    char msg[160];
+    auto bad = [&](int status, const char *what) {
+        std::snprintf(msg, sizeof(msg), "%s: %s", who, what);
+        return fail(status, msg);
+    };
+    if (t == nullptr) return bad(CX_STATUS_INVALID_ARGUMENT, "null tiles");
     if (t->value_dtype != CELLERATOR_DTYPE_F16 && t->value_dtype != CELLERATOR_DTYPE_F32)
-        return fail(CX_STATUS_UNSUPPORTED, "cx_cpbp_reduce: values must be F16 or F32");
+        return bad(CX_STATUS_UNSUPPORTED, "values must be F16 or F32");
     if (t->tile_row_width == 0u || t->tile_row_width > 64u)
-        return fail(CX_STATUS_INVALID_SHAPE, "cx_cpbp_reduce: tile_row_width must be 1..64");
+        return bad(CX_STATUS_INVALID_SHAPE, "tile_row_width must be 1..64");
     const std::uint64_t expected_tiles = (static_cast<std::uint64_t>(t->row_count) + t->tile_row_width - 1u)
         / t->tile_row_width;
     if (t->tile_count != expected_tiles || t->tile_block_count > t->row_block_entry_count
         || t->row_block_entry_count > t->nnz_count)
-        return fail(CX_STATUS_INVALID_SHAPE, "cx_cpbp_reduce: tile, descriptor or entry counts are inconsistent");
-    if (feature_weight_capacity < t->feature_count)
-        return fail(CX_STATUS_INVALID_SHAPE, "cx_cpbp_reduce: feature weight capacity is too small");
-    if (row_capacity < t->row_count)
-        return fail(CX_STATUS_INVALID_SHAPE, "cx_cpbp_reduce: output capacity is insufficient");
+        return bad(CX_STATUS_INVALID_SHAPE, "tile, descriptor or entry counts are inconsistent");
+    if (reduce && feature_weight_capacity < t->feature_count)
+        return bad(CX_STATUS_INVALID_SHAPE, "feature weight capacity is too small");
+    if (reduce && row_capacity < t->row_count)
+        return bad(CX_STATUS_INVALID_SHAPE, "output capacity is insufficient");
     if (t->feature_block_offsets == nullptr
-        || (t->feature_count != 0u && (t->feature_permutation == nullptr || feature_weights == nullptr))
+        || (reduce && t->feature_count != 0u && (t->feature_permutation == nullptr || feature_weights == nullptr))
         || t->tile_block_offsets == nullptr || t->block_row_entry_offsets == nullptr
-        || (t->row_count != 0u && (t->row_permutation == nullptr || row_values == nullptr))
+        || (reduce && t->row_count != 0u && (t->row_permutation == nullptr || row_values == nullptr))
         || (t->tile_block_count != 0u && (t->tile_block_ids == nullptr || t->tile_block_cell_masks == nullptr))
         || (t->row_block_entry_count != 0u
             && (t->row_block_gene_masks == nullptr || t->row_block_value_offsets == nullptr))
-        || (t->nnz_count != 0u && t->values == nullptr))
-        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_cpbp_reduce: device input pointer is null");
-    // Output aliasing (validate_output, :138-178).
-    const void *inputs[] = {feature_weights, t->feature_block_offsets, t->feature_permutation,
-                            t->tile_block_offsets, t->tile_block_ids, t->tile_block_cell_masks,
-                            t->block_row_entry_offsets, t->row_block_gene_masks,
-                            t->row_block_value_offsets, t->values, t->row_permutation};
-    for (const void *p : inputs)
-        if (p != nullptr && p == static_cast<const void *>(row_values))
-            return fail(CX_STATUS_INVALID_ARGUMENT, "cx_cpbp_reduce: output aliases an input");
-    if (t->row_count == 0u) return CX_STATUS_SUCCESS;
+        || (reduce && t->nnz_count != 0u && t->values == nullptr))
+        return bad(CX_STATUS_INVALID_ARGUMENT, "device input pointer is null");
+    if (rows_capacity != 0u || entry_rows != nullptr) {
+        if (entry_rows == nullptr && t->row_block_entry_count != 0u)
+            return bad(CX_STATUS_INVALID_ARGUMENT, "null entry rows");
+        if (rows_capacity < t->row_block_entry_count)
+            return bad(CX_STATUS_INVALID_SHAPE, "entry rows capacity is below the entry count");
+        // block start << 6 | row in 32 bits
+        if (t->feature_count >= (1u << 26))
+            return bad(CX_STATUS_UNSUPPORTED, "entry rows need fewer than 2^26 features");
+    }
+    if (reduce) {
+        const void *inputs[] = {feature_weights, t->feature_block_offsets, t->feature_permutation,
+                                t->tile_block_offsets, t->tile_block_ids, t->tile_block_cell_masks,
+                                t->block_row_entry_offsets, t->row_block_gene_masks,
+                                t->row_block_value_offsets, t->values, t->row_permutation, entry_rows};
+        for (const void *q : inputs)
+            if (q != nullptr && q == static_cast<const void *>(row_values))
+                return bad(CX_STATUS_INVALID_ARGUMENT, "output aliases an input");
+    } else {
+        const void *inputs[] = {t->feature_block_offsets, t->tile_block_offsets, t->tile_block_ids,
+                                t->tile_block_cell_masks, t->block_row_entry_offsets,
+                                t->row_block_gene_masks, t->row_block_value_offsets};
+        for (const void *q : inputs)
+            if (q != nullptr && q == static_cast<const void *>(entry_rows))
+                return bad(CX_STATUS_INVALID_ARGUMENT, "entry rows alias an input");
+    }
+    return CX_STATUS_SUCCESS;
+}
 
+template<Walk kWalk>
+int launch_walk(const cx_cpbp_tiles *t, const float *feature_weights, float *row_values,
+                std::uint32_t *entry_rows, void *stream, const char *who) {
     CpbpArgs a{};
     a.feature_block_offsets = t->feature_block_offsets;
     a.feature_permutation = t->feature_permutation;
@@ -454,6 +512,7 @@ extern "C" int cx_cpbp_reduce(const cx_cpbp_tiles *t, const float *feature_weigh
     a.row_permutation = t->row_permutation;
     a.weights = feature_weights;
     a.row_values = row_values;
+    a.entry_rows = entry_rows;
     a.row_count = t->row_count;
     a.tile_count = t->tile_count;
     a.tile_row_width = t->tile_row_width;
@@ -465,8 +524,12 @@ extern "C" int cx_cpbp_reduce(const cx_cpbp_tiles *t, const float *feature_weigh
     const bool wide = t->tile_row_width > 32u;
     const bool half = t->value_dtype == CELLERATOR_DTYPE_F16;
     const bool lds = t->feature_count <= kWeightsLds && t->feature_block_count < kBlocksLds;
-#define CX_CPBP_LAUNCH(M, V, W) hipLaunchKernelGGL((cpbp_reduce_kernel<M, V, W>), grid, block, 0, s, a)
-    if (lds) {
+#define CX_CPBP_LAUNCH(M, V, W) hipLaunchKernelGGL((cpbp_reduce_kernel<M, V, W, kWalk>), grid, block, 0, s, a)
+    if constexpr (kWalk == Walk::make_rows) {
+        // no weights or values read: one form per mask width
+        if (wide) CX_CPBP_LAUNCH(std::uint64_t, float, false);
+        else CX_CPBP_LAUNCH(std::uint32_t, float, false);
+    } else if (lds) {
         if (wide && half) CX_CPBP_LAUNCH(std::uint64_t, std::uint16_t, true);
         else if (wide) CX_CPBP_LAUNCH(std::uint64_t, float, true);
         else if (half) CX_CPBP_LAUNCH(std::uint32_t, std::uint16_t, true);
@@ -478,7 +541,47 @@ extern "C" int cx_cpbp_reduce(const cx_cpbp_tiles *t, const float *feature_weigh
         else CX_CPBP_LAUNCH(std::uint32_t, float, false);
     }
 #undef CX_CPBP_LAUNCH
-    return check_launch("cpbp_reduce");
+    return check_launch(who);
+}
+
+} // namespace
+} // namespace cx
+
+extern "C" int cx_cpbp_reduce(const cx_cpbp_tiles *t, const float *feature_weights,
+                              uint64_t feature_weight_capacity, float *row_values,
+                              uint64_t row_capacity, void *stream) {
+    using namespace cx;
+    clear_error();
+    const int rc = check_walk(t, true, feature_weights, feature_weight_capacity, row_values, row_capacity,
+                              nullptr, 0u, "cx_cpbp_reduce");
+    if (rc != CX_STATUS_SUCCESS || t->row_count == 0u) return rc;
+    return launch_walk<Walk::reduce>(t, feature_weights, row_values, nullptr, stream, "cpbp_reduce");
+}
+
+extern "C" int cx_cpbp_entry_rows(const cx_cpbp_tiles *t, uint32_t *entry_rows, uint64_t entry_rows_capacity,
+                                  void *stream) {
+    using namespace cx;
+    clear_error();
+    if (entry_rows == nullptr && t != nullptr && t->row_block_entry_count != 0u)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_cpbp_entry_rows: null entry rows");
+    const int rc = check_walk(t, false, nullptr, 0u, nullptr, 0u, entry_rows, entry_rows_capacity,
+                              "cx_cpbp_entry_rows");
+    if (rc != CX_STATUS_SUCCESS || t->row_count == 0u || t->row_block_entry_count == 0u) return rc;
+    return launch_walk<Walk::make_rows>(t, nullptr, nullptr, entry_rows, stream, "cpbp_entry_rows");
+}
+
+extern "C" int cx_cpbp_reduce_rows(const cx_cpbp_tiles *t, const uint32_t *entry_rows,
+                                   const float *feature_weights, uint64_t feature_weight_capacity,
+                                   float *row_values, uint64_t row_capacity, void *stream) {
+    using namespace cx;
+    clear_error();
+    if (entry_rows == nullptr && t != nullptr && t->row_block_entry_count != 0u)
+        return fail(CX_STATUS_INVALID_ARGUMENT, "cx_cpbp_reduce_rows: null entry rows");
+    const int rc = check_walk(t, true, feature_weights, feature_weight_capacity, row_values, row_capacity,
+                              entry_rows, t != nullptr ? t->row_block_entry_count : 0u, "cx_cpbp_reduce_rows");
+    if (rc != CX_STATUS_SUCCESS || t->row_count == 0u) return rc;
+    return launch_walk<Walk::with_rows>(t, feature_weights, row_values, const_cast<std::uint32_t *>(entry_rows),
+                                        stream, "cpbp_reduce_rows");
 }
 
 // ---- the reference's full direct-consumer contract --------------------------------------

@@ -574,6 +574,36 @@ def cpbp_reduce(t: CpbpTiles, weights: torch.Tensor, out: Optional[torch.Tensor]
     return out
 
 
+def cpbp_entry_rows(t: CpbpTiles, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Every entry's tile row and block start (block start << 6 | row, int32 storage of u32),
+    computed once per tile structure on the device (cx_cpbp_entry_rows): the per-entry
+    array cpbp_reduce_rows reads instead of looking the entry's descriptor up."""
+    d = t.descriptor()
+    n = int(d.row_block_entry_count)
+    if out is None:
+        out = torch.empty(max(n, 1), dtype=torch.int32, device="cuda")
+    _require_cuda(out)
+    N.check("cx_cpbp_entry_rows", N.engine().cx_cpbp_entry_rows(
+        C.byref(d), out.data_ptr(), out.numel(), _stream(stream)))
+    return out
+
+
+def cpbp_reduce_rows(t: CpbpTiles, entry_rows: torch.Tensor, weights: torch.Tensor,
+                     out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """cpbp_reduce with the entries' rows and block starts read from `entry_rows`
+    (cpbp_entry_rows of the same tiles) instead of the descriptors: same contract."""
+    _require_cuda(weights, t.values, entry_rows)
+    d = t.descriptor()
+    if entry_rows.dtype != torch.int32 or entry_rows.numel() < int(d.row_block_entry_count):
+        raise ValueError("entry_rows must be the int32 array cpbp_entry_rows made for these tiles")
+    if out is None:
+        out = torch.empty(t.row_count, dtype=torch.float32, device=weights.device)
+    N.check("cx_cpbp_reduce_rows", N.engine().cx_cpbp_reduce_rows(
+        C.byref(d), entry_rows.data_ptr(), weights.data_ptr(), weights.numel(), out.data_ptr(), out.numel(),
+        _stream(stream)))
+    return out
+
+
 def csr_spmv(row_ptr: torch.Tensor, col_idx: torch.Tensor, values: torch.Tensor,
              x: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
     _require_cuda(row_ptr, col_idx, values, x)

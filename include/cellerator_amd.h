@@ -840,6 +840,21 @@ int cx_cpbp_reduce(const cx_cpbp_tiles *tiles, const float *feature_weights,
                    uint64_t feature_weight_capacity, float *row_values,
                    uint64_t row_capacity, void *stream);
 
+/* Per-entry rows for repeated reductions over one tile structure (engine addition, no
+ * counterpart in the reference; a persistent preprocessing of the tiles, like the
+ * Blocked-ELL panel). cx_cpbp_entry_rows writes, for every row-block entry, its block's
+ * first permuted feature (clamped to feature_count) << 6 | its row in the tile: the entry's
+ * descriptor looked up once, on the device (entry_rows: row_block_entry_count u32, device;
+ * feature_count below 2^26). cx_cpbp_reduce_rows is cx_cpbp_reduce with those read per
+ * entry instead of looked up per launch: same result contract, same checks; entry_rows
+ * must be the array cx_cpbp_entry_rows made for these tiles (any change to the tile
+ * structure, not to the values or weights, needs a new one). */
+int cx_cpbp_entry_rows(const cx_cpbp_tiles *tiles, uint32_t *entry_rows, uint64_t entry_rows_capacity,
+                       void *stream);
+int cx_cpbp_reduce_rows(const cx_cpbp_tiles *tiles, const uint32_t *entry_rows,
+                        const float *feature_weights, uint64_t feature_weight_capacity,
+                        float *row_values, uint64_t row_capacity, void *stream);
+
 /* ---- CP-BP construction (host): canonical CSR -> records -> local order -> tiles ----
  * Replaces the host producers apply_frozen_plan_host + build_cell_block_records_host +
  * build_local_cell_order_host + build_warp_tiles_host

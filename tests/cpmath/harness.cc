@@ -60,6 +60,9 @@ typedef struct h_case {
     // (prepare_cpbp_state) before the launch.
     uint32_t exec_order, head_genes;
     const void *reduction_view;
+    // with reduction_view: device u32 array (entry_rows_capacity) for the entry rows
+    uint32_t *entry_rows;
+    uint64_t entry_rows_capacity;
 } h_case;
 
 typedef struct h_result {
@@ -331,7 +334,8 @@ extern "C" int h_run(const h_case *c, h_result *r) {
     }
     if (c->kind == 3 && c->reduction_view != nullptr) {
         const core::operation_status st = cp::prepare_cpbp_state(
-            d.key.runtime, *static_cast<const cx_cpbp_reduction_view *>(c->reduction_view));
+            d.key.runtime, *static_cast<const cx_cpbp_reduction_view *>(c->reduction_view), c->entry_rows,
+            c->entry_rows_capacity, c->stream);
         r->state_status = static_cast<int32_t>(st.code);
         if (!st) { note(r, st, false); cp::retire_projection(d.key.runtime); return 0; }
     }

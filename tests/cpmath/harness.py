@@ -51,7 +51,8 @@ class HCase(C.Structure):
                 ("reserved3", C.c_uint32), ("bias", p), ("alpha", C.c_float),
                 ("beta", C.c_float), ("pairs", p), ("check_columns", C.c_uint32),
                 ("repeats", C.c_uint32), ("panel", p), ("groups", p), ("exec_order", C.c_uint32),
-                ("head_genes", C.c_uint32), ("reduction_view", p)]
+                ("head_genes", C.c_uint32), ("reduction_view", p), ("entry_rows", p),
+                ("entry_rows_capacity", C.c_uint64)]
 
 
 class HResult(C.Structure):

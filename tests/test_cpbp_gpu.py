@@ -130,3 +130,100 @@ def test_descriptors_without_cells(oracle, width, dtype):
     got = run_reduce(plan, e, w)
     assert np.array_equal(got.view(np.uint32), base.view(np.uint32))
     check(oracle, offs, feats, vals, w, got)
+
+
+def host_entry_rows(plan, t):
+    """Every entry's block start << 6 | tile row, restated on the host from the descriptors:
+    the k-th entry of descriptor d sits in the tile row of the k-th set bit of d's cell mask
+    (warp_tiles.hh:49-79), its block starts at feature_block_offsets[block id]."""
+    fbo = plan.feature_block_offsets.astype(np.int64)
+    fc = int(plan.feature_permutation.size)
+    out = np.zeros(int(t.row_block_gene_masks.size), np.uint32)
+    eo = t.block_row_entry_offsets.astype(np.int64)
+    for d in range(int(t.tile_block_ids.size)):
+        m = int(t.tile_block_cell_masks[d])
+        rows = [b for b in range(64) if (m >> b) & 1]
+        bb = min(int(fbo[min(int(t.tile_block_ids[d]), fbo.size - 1)]), fc)
+        for k, e in enumerate(range(eo[d], eo[d + 1])):
+            out[e] = (bb << 6) | rows[k]
+    return out
+
+
+@pytest.mark.parametrize("width,window,dtype", [(64, 1024, np.float32), (32, 1024, np.float16),
+                                                (7, 63, np.float32), (1, 16, np.float16)])
+def test_entry_rows_and_reduce_rows(oracle, width, window, dtype):
+    """cx_cpbp_entry_rows equals the host restatement entry for entry, and cx_cpbp_reduce_rows
+    over it is bitwise the reduction from the descriptors (same batches, same order)."""
+    import torch
+
+    from cellerator_amd import cpbp_entry_rows, cpbp_reduce, cpbp_reduce_rows
+    rng = np.random.default_rng(2000 + width)
+    plan = random_plan(rng, 700)
+    offs, feats, vals = random_csr(rng, 1500, 700, 30.0, dtype)
+    w = rng.standard_normal(700).astype(np.float32)
+    t = cpbp.build_tiles(plan, offs, feats, vals, window_size=window, group_width=width, threads=4)
+    dev = cpbp.to_device(plan, t)
+    rows = cpbp_entry_rows(dev)
+    n = int(t.row_block_gene_masks.size)
+    assert np.array_equal(rows.cpu().numpy()[:n].view(np.uint32), host_entry_rows(plan, t))
+    wd = torch.from_numpy(w).cuda()
+    a = cpbp_reduce(dev, wd)
+    b = cpbp_reduce_rows(dev, rows, wd)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    check(oracle, offs, feats, vals, w, b.cpu().numpy())
+
+
+def test_reduce_rows_c5_sample(oracle):
+    """Config-5 distributions at 20,000 cells through the per-entry rows: parity with the
+    canonical referee and bitwise equal to the descriptor walk."""
+    import torch
+
+    from cellerator_amd import cpbp_entry_rows, cpbp_reduce, cpbp_reduce_rows
+    from cellerator_amd.synth import C5, generate_cpbp_host
+    cfg = C5.scaled(20_000)
+    offs, feats, vals = generate_cpbp_host(cfg)
+    plan = cpbp.contiguous_plan(cfg.genes, cfg.block_width)
+    t = cpbp.build_tiles(plan, offs, feats, vals, group_width=64, window_size=1024)
+    dev = cpbp.to_device(plan, t)
+    rows = cpbp_entry_rows(dev)
+    w = np.random.default_rng(6).standard_normal(cfg.genes).astype(np.float32)
+    wd = torch.from_numpy(w).cuda()
+    a = cpbp_reduce(dev, wd)
+    b = cpbp_reduce_rows(dev, rows, wd)
+    c = cpbp_reduce_rows(dev, rows, wd)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    assert torch.equal(b.view(torch.int32), c.view(torch.int32))
+    check(oracle, offs, feats, vals, w, b.cpu().numpy())
+
+
+def test_entry_rows_rejects_bad_arguments():
+    import ctypes
+
+    import torch
+
+    from cellerator_amd import _native as N
+    from cellerator_amd import cpbp_entry_rows, cpbp_reduce_rows
+    rng = np.random.default_rng(77)
+    plan = random_plan(rng, 100)
+    offs, feats, vals = random_csr(rng, 200, 100, 10.0, np.float32)
+    t = cpbp.build_tiles(plan, offs, feats, vals, window_size=64, group_width=32, threads=1)
+    dev = cpbp.to_device(plan, t)
+    n = int(t.row_block_gene_masks.size)
+    with pytest.raises(N.EngineError, match="capacity"):
+        cpbp_entry_rows(dev, out=torch.empty(n - 1, dtype=torch.int32, device="cuda"))
+    rows = cpbp_entry_rows(dev)
+    w = torch.ones(100, device="cuda")
+    out = torch.empty(dev.row_count, device="cuda")
+    d = dev.descriptor()
+    lib = N.engine()
+    assert lib.cx_cpbp_reduce_rows(ctypes.byref(d), None, w.data_ptr(), w.numel(), out.data_ptr(),
+                                   out.numel(), None) == 1
+    assert b"null entry rows" in lib.cx_last_error()
+    # the output may not alias the entry rows
+    assert lib.cx_cpbp_reduce_rows(ctypes.byref(d), rows.data_ptr(), w.data_ptr(), w.numel(), rows.data_ptr(),
+                                   dev.row_count, None) == 1
+    assert b"aliases" in lib.cx_last_error()
+    with pytest.raises(ValueError):
+        cpbp_reduce_rows(dev, rows[: n - 1], w)

@@ -480,3 +480,45 @@ def test_cpbp_native_tile_view_through_reference_core(oracle):
     other = torch.empty(nnz, dtype=torch.float16, device="cuda")
     r = H.run(case(other.data_ptr()))
     assert r.status == H.INVALID_LAUNCH
+
+
+def test_cpbp_checked_entry_rows_through_reference_core():
+    """prepare_cpbp_state with a validated reduction view and an entry-rows array: the core's
+    launch reads each entry's row and block start from it (dispatch
+    "cpbp:checked+entry-rows"), bitwise equal to the reduction from the descriptors; without
+    the array it keeps the descriptor walk ("cpbp:checked")."""
+    import torch
+
+    from cellerator_amd import cpbp_reduce, cpk1
+    from tests.test_cpk1 import _reduction_view, build_reference_image
+    _, _, image, view = build_reference_image()
+    dev = cpk1.upload(cpk1.validate(image, cpk1.expected_of(view)), image)
+    rv = _reduction_view(dev.view)
+    d = dev.descriptor()
+    tview = type(d).from_buffer_copy(d)
+    tview.values = None
+    half = int(d.value_dtype) == 1  # CELLERATOR_DTYPE_F16: the image's values are fp16
+    values_ptr = int(d.values)  # the values section inside the uploaded image
+    w = torch.from_numpy((0.5 + 0.125 * np.arange(int(d.feature_count))).astype(np.float32)).cuda()
+    expect = cpbp_reduce(dev, w)
+    n_entries = int(d.row_block_entry_count)
+    for with_rows in (True, False):
+        rows = torch.full((max(n_entries, 1),), -1, dtype=torch.int32, device="cuda")
+        y = torch.full((int(d.row_count),), -3.0, device="cuda")
+        c = H.HCase(kind=H.KIND_CPBP, view=C.addressof(tview), view_bytes=C.sizeof(tview), variant=0,
+                    rows=int(d.row_count), cols=int(d.feature_count), out_cols=0, block_size=0,
+                    sparse_type=H.NT_F16 if half else H.NT_F32,
+                    dense_type=H.NT_F32, nnz=int(d.nnz_count), values=values_ptr,
+                    value_count=int(d.nnz_count), value_bytes=int(d.nnz_count) * (2 if half else 4),
+                    w=w.data_ptr(), w_ld=1, y=y.data_ptr(), y_ld=1,
+                    stream=torch.cuda.current_stream().cuda_stream, device=torch.cuda.current_device(),
+                    reduction_view=C.addressof(rv),
+                    entry_rows=rows.data_ptr() if with_rows else None,
+                    entry_rows_capacity=rows.numel() if with_rows else 0)
+        r = H.run(c)
+        assert (r.prepare_status, r.state_status, r.status) == (H.OK, H.OK, H.OK), (r.message, r.engine)
+        assert r.dispatch == (b"cpbp:checked+entry-rows" if with_rows else b"cpbp:checked")
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int32), expect.view(torch.int32))
+        if with_rows:
+            assert bool((rows[:n_entries] >= 0).all())
