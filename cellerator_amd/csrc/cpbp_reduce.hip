@@ -316,92 +316,92 @@ __global__ __launch_bounds__(kWave *kCpbpWaves) void cpbp_reduce_kernel(CpbpArgs
                 row = cur.rb & 63u;
                 bb = cur.rb >> 6;
             } else {
-            // entry -> descriptor (slots + max-scan) -> row and block start
-            L.slot[lane] = 0;
-            lds_order();
-            const std::uint32_t q = cur.eo_k - e;
-            if (cur.has_desc && q < 64u)
-                __hip_atomic_fetch_max(&L.slot[q], lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
-            lds_order();
-            const int kd = wave_inclusive_max(L.slot[lane], lane);
-            const std::uint32_t my_eo = __shfl(cur.eo_k, kd, kWave);
-            const MaskT my_mask = __shfl(cur.mask_k, kd, kWave);
-            const std::uint32_t my_blk = __shfl(cur.blk_k, kd, kWave);
-            row = select_bit(my_mask, e + lane - my_eo) & 63u;
-            if constexpr (kStageBlocks) bb = min(block_begin[min(my_blk, a.feature_block_count)], a.feature_count);
-            else bb = min(a.feature_block_offsets[min(my_blk, a.feature_block_count)], a.feature_count);
+                // entry -> descriptor (slots + max-scan) -> row and block start
+                L.slot[lane] = 0;
+                lds_order();
+                const std::uint32_t q = cur.eo_k - e;
+                if (cur.has_desc && q < 64u)
+                    __hip_atomic_fetch_max(&L.slot[q], lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+                lds_order();
+                const int kd = wave_inclusive_max(L.slot[lane], lane);
+                const std::uint32_t my_eo = __shfl(cur.eo_k, kd, kWave);
+                const MaskT my_mask = __shfl(cur.mask_k, kd, kWave);
+                const std::uint32_t my_blk = __shfl(cur.blk_k, kd, kWave);
+                row = select_bit(my_mask, e + lane - my_eo) & 63u;
+                if constexpr (kStageBlocks) bb = min(block_begin[min(my_blk, a.feature_block_count)], a.feature_count);
+                else bb = min(a.feature_block_offsets[min(my_blk, a.feature_block_count)], a.feature_count);
             }
             if constexpr (kWalk == Walk::make_rows) {
                 if (static_cast<std::uint32_t>(lane) < cur_x.n) a.entry_rows[e + static_cast<std::uint32_t>(lane)] = bb << 6 | row;
             } else {
 
-            // stage the batch's values; each entry sums its own values in a register
+                // stage the batch's values; each entry sums its own values in a register
 #pragma unroll
-            for (std::uint32_t c = 0; c < kBatchValues / kWave; ++c)
-                L.stage[c * kWave + static_cast<std::uint32_t>(lane)] = x_cur[c];
-            lds_order();
-            const bool has = static_cast<std::uint32_t>(lane) < cur_x.n;
-            float sum = 0.0f;
-            if (has) {
-                std::uint32_t m = cur.gm;
-                const float *v = &L.stage[min(cur.s_j - cur_x.s0, kBatchValues)];
-                if constexpr (kLdsPlan) {
-                    const float *w = &wp[bb];
-                    // An absent bit reads weight 31 of the block (m | bit 31 is never 0, and
-                    // the weight stage is padded by one block) and at most the stage's
-                    // 4-value tail, so every read is in bounds and needs no exec mask. Its
-                    // product is dropped by one select on the sum (zeroing only one operand
-                    // would let a non-finite value or weight from outside the entry in).
-                    constexpr std::uint32_t kStop = 0x80000000u;
-                    while (m != 0u) {  // four stored values per step
-                        const std::uint32_t b0 = static_cast<std::uint32_t>(__builtin_ctz(m));
-                        m &= m - 1u;
-                        const bool h1 = m != 0u;
-                        const std::uint32_t b1 = static_cast<std::uint32_t>(__builtin_ctz(m | kStop));
-                        m &= m - 1u;
-                        const bool h2 = m != 0u;
-                        const std::uint32_t b2 = static_cast<std::uint32_t>(__builtin_ctz(m | kStop));
-                        m &= m - 1u;
-                        const bool h3 = m != 0u;
-                        const std::uint32_t b3 = static_cast<std::uint32_t>(__builtin_ctz(m | kStop));
-                        m &= m - 1u;
-                        const float v0 = v[0], v1 = v[1], v2 = v[2], v3 = v[3];
-                        const float w0 = w[b0], w1 = w[b1], w2 = w[b2], w3 = w[b3];
-                        // keeps the reads unconditional (the compiler would otherwise sink
-                        // them under a divergent branch per select)
-                        __asm__ volatile("" ::"v"(v1), "v"(v2), "v"(v3), "v"(w1), "v"(w2), "v"(w3));
-                        sum = __builtin_fmaf(v0, w0, sum);
-                        sum = h1 ? __builtin_fmaf(v1, w1, sum) : sum;
-                        sum = h2 ? __builtin_fmaf(v2, w2, sum) : sum;
-                        sum = h3 ? __builtin_fmaf(v3, w3, sum) : sum;
-                        v += 4;
-                    }
-                } else {
-                    while (m != 0u) {
-                        const std::uint32_t b = static_cast<std::uint32_t>(__builtin_ctz(m));
-                        m &= m - 1u;
-                        const std::uint32_t f = min(bb + b, a.feature_count - 1u);
-                        sum = __builtin_fmaf(*v, a.weights[a.feature_permutation[f]], sum);
-                        ++v;
+                for (std::uint32_t c = 0; c < kBatchValues / kWave; ++c)
+                    L.stage[c * kWave + static_cast<std::uint32_t>(lane)] = x_cur[c];
+                lds_order();
+                const bool has = static_cast<std::uint32_t>(lane) < cur_x.n;
+                float sum = 0.0f;
+                if (has) {
+                    std::uint32_t m = cur.gm;
+                    const float *v = &L.stage[min(cur.s_j - cur_x.s0, kBatchValues)];
+                    if constexpr (kLdsPlan) {
+                        const float *w = &wp[bb];
+                        // An absent bit reads weight 31 of the block (m | bit 31 is never 0, and
+                        // the weight stage is padded by one block) and at most the stage's
+                        // 4-value tail, so every read is in bounds and needs no exec mask. Its
+                        // product is dropped by one select on the sum (zeroing only one operand
+                        // would let a non-finite value or weight from outside the entry in).
+                        constexpr std::uint32_t kStop = 0x80000000u;
+                        while (m != 0u) {  // four stored values per step
+                            const std::uint32_t b0 = static_cast<std::uint32_t>(__builtin_ctz(m));
+                            m &= m - 1u;
+                            const bool h1 = m != 0u;
+                            const std::uint32_t b1 = static_cast<std::uint32_t>(__builtin_ctz(m | kStop));
+                            m &= m - 1u;
+                            const bool h2 = m != 0u;
+                            const std::uint32_t b2 = static_cast<std::uint32_t>(__builtin_ctz(m | kStop));
+                            m &= m - 1u;
+                            const bool h3 = m != 0u;
+                            const std::uint32_t b3 = static_cast<std::uint32_t>(__builtin_ctz(m | kStop));
+                            m &= m - 1u;
+                            const float v0 = v[0], v1 = v[1], v2 = v[2], v3 = v[3];
+                            const float w0 = w[b0], w1 = w[b1], w2 = w[b2], w3 = w[b3];
+                            // keeps the reads unconditional (the compiler would otherwise sink
+                            // them under a divergent branch per select)
+                            __asm__ volatile("" ::"v"(v1), "v"(v2), "v"(v3), "v"(w1), "v"(w2), "v"(w3));
+                            sum = __builtin_fmaf(v0, w0, sum);
+                            sum = h1 ? __builtin_fmaf(v1, w1, sum) : sum;
+                            sum = h2 ? __builtin_fmaf(v2, w2, sum) : sum;
+                            sum = h3 ? __builtin_fmaf(v3, w3, sum) : sum;
+                            v += 4;
+                        }
+                    } else {
+                        while (m != 0u) {
+                            const std::uint32_t b = static_cast<std::uint32_t>(__builtin_ctz(m));
+                            m &= m - 1u;
+                            const std::uint32_t f = min(bb + b, a.feature_count - 1u);
+                            sum = __builtin_fmaf(*v, a.weights[a.feature_permutation[f]], sum);
+                            ++v;
+                        }
                     }
                 }
-            }
-            // Each entry's sum goes to its row. Rows repeat within a batch (one entry per
-            // descriptor that holds the row), and LDS float atomics cost ~190 CU cycles per
-            // wave instruction here, against ~16 for an integer atomic with return and ~10 for
-            // a plain read and write: so each entry takes its occurrence number among the
-            // batch's entries of its row from an integer atomic, and round j adds the sums of
-            // the j-th occurrences with a plain read, add and write (the rows of one round are
-            // distinct). Two or three rounds cover a batch.
-            if (has) L.occ[row] = 0u;
-            lds_order();
-            std::uint32_t occ = 0u;
-            if (has) occ = __hip_atomic_fetch_add(&L.occ[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
-            for (std::uint32_t j = 0u;; ++j) {
-                if (has && occ == j) L.acc[row] += sum;
+                // Each entry's sum goes to its row. Rows repeat within a batch (one entry per
+                // descriptor that holds the row), and LDS float atomics cost ~190 CU cycles per
+                // wave instruction here, against ~16 for an integer atomic with return and ~10 for
+                // a plain read and write: so each entry takes its occurrence number among the
+                // batch's entries of its row from an integer atomic, and round j adds the sums of
+                // the j-th occurrences with a plain read, add and write (the rows of one round are
+                // distinct). Two or three rounds cover a batch.
+                if (has) L.occ[row] = 0u;
                 lds_order();
-                if (__builtin_amdgcn_ballot_w64(has && occ > j) == 0ull) break;
-            }
+                std::uint32_t occ = 0u;
+                if (has) occ = __hip_atomic_fetch_add(&L.occ[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+                for (std::uint32_t j = 0u;; ++j) {
+                    if (has && occ == j) L.acc[row] += sum;
+                    lds_order();
+                    if (__builtin_amdgcn_ballot_w64(has && occ > j) == 0ull) break;
+                }
             }
             e = e_next;
             d = d_next;
