@@ -345,6 +345,8 @@ ENGINE_SIGNATURES = {
     "cx_exclusive_scan_u32_workspace": (C.c_int, [u64, C.POINTER(u64)]),
     "cx_exclusive_scan_u32": (C.c_int, [p_void, p_void, u64, p_void, u64, p_void]),
     "cx_bell_spmm_fwd": (C.c_int, [C.POINTER(CxBellMatrix), p_void, u32, i64, i64, p_void, i64, p_void]),
+    "cx_bell_spmm_fwd_ordered": (C.c_int, [C.POINTER(CxBellMatrix), p_void, u32, i64, i64, p_void, i64, p_void,
+                                           p_void]),
     "cx_bell_spmm_fwd_epilogue": (C.c_int, [C.POINTER(CxBellMatrix), p_void, u32, i64, i64, p_void,
                                             i64, C.POINTER(CxSpmmEpilogue), p_void]),
     "cx_bell_pack_rhs": (C.c_int, [p_void, i64, u32, u32, p_void, p_void]),

@@ -54,6 +54,9 @@ struct BellArgs {
     std::uint32_t a_row_bytes;
     std::uint32_t a_slot_bytes;
     std::uint32_t block_major;
+    // quantized matrix-core forms: row block of workgroup slot i (an XCD-major slot), or
+    // none (the slot's own row block)
+    const std::uint32_t *rb_order;
     Epilogue ep;
 };
 
@@ -749,7 +752,8 @@ __global__ __launch_bounds__(256) void bell_spmm_quant_mfma(BellArgs a, std::int
     const int lane = static_cast<int>(threadIdx.x) % kWave;
     const int wave = static_cast<int>(threadIdx.x) / kWave;
     const std::uint32_t row_blocks = (a.rows + 31u) / 32u;
-    const std::uint32_t rb = xcd_major(blockIdx.x, gridDim.x);
+    const std::uint32_t slot = xcd_major(blockIdx.x, gridDim.x);
+    const std::uint32_t rb = a.rb_order != nullptr ? a.rb_order[slot] : slot;
     if (rb >= row_blocks) return;
     const std::uint32_t width = a.ell_cols / 32u;
     const std::uint32_t *slots = a.block_col_idx + static_cast<std::uint64_t>(rb) * width;
@@ -879,7 +883,8 @@ __global__ __launch_bounds__(256) void bell_spmm_quant_lds(BellArgs a, std::int6
     const int lane = static_cast<int>(threadIdx.x) % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
     const std::uint32_t row_blocks = (a.rows + 31u) / 32u;
-    const std::uint32_t rb = xcd_major(blockIdx.x, gridDim.x);
+    const std::uint32_t slot = xcd_major(blockIdx.x, gridDim.x);
+    const std::uint32_t rb = a.rb_order != nullptr ? a.rb_order[slot] : slot;
     if (rb >= row_blocks) return;
     const std::uint32_t width = a.ell_cols / 32u;
     const std::uint32_t *slots = a.block_col_idx + static_cast<std::uint64_t>(rb) * width;
@@ -1066,6 +1071,7 @@ BellArgs make_args(const cx_bell_matrix *m, const void *rhs, std::int64_t rhs_ld
     const std::uint32_t size = m->value_dtype == CELLERATOR_DTYPE_F32 ? 4u : 2u;
     a.a_row_bytes = (a.block_major ? m->block_size : m->ell_cols) * size;
     a.a_slot_bytes = m->block_size * (a.block_major ? m->block_size : 1u) * size;
+    a.rb_order = nullptr;
     return a;
 }
 
@@ -1079,10 +1085,35 @@ extern "C" int cx_bell_spmm_fwd(const cx_bell_matrix *m, const void *rhs, uint32
                                      stream);
 }
 
+namespace {
+
+int bell_spmm_fwd_impl(const cx_bell_matrix *m, const void *rhs, uint32_t rhs_dtype, int64_t rhs_ld,
+                       int64_t out_cols, float *out, int64_t out_ld, const cx_spmm_epilogue *epilogue,
+                       const std::uint32_t *rb_order, void *stream);
+
+} // namespace
+
 extern "C" int cx_bell_spmm_fwd_epilogue(const cx_bell_matrix *m, const void *rhs,
                                          uint32_t rhs_dtype, int64_t rhs_ld, int64_t out_cols,
                                          float *out, int64_t out_ld,
                                          const cx_spmm_epilogue *epilogue, void *stream) {
+    return bell_spmm_fwd_impl(m, rhs, rhs_dtype, rhs_ld, out_cols, out, out_ld, epilogue, nullptr, stream);
+}
+
+extern "C" int cx_bell_spmm_fwd_ordered(const cx_bell_matrix *m, const void *rhs, uint32_t rhs_dtype,
+                                        int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
+                                        const uint32_t *row_block_order, void *stream) {
+    cx::clear_error();
+    if (row_block_order == nullptr && m != nullptr && m->rows != 0u)
+        return cx::fail(CX_STATUS_INVALID_ARGUMENT, "cx_bell_spmm_fwd_ordered: null row-block order");
+    return bell_spmm_fwd_impl(m, rhs, rhs_dtype, rhs_ld, out_cols, out, out_ld, nullptr, row_block_order, stream);
+}
+
+namespace {
+
+int bell_spmm_fwd_impl(const cx_bell_matrix *m, const void *rhs, uint32_t rhs_dtype, int64_t rhs_ld,
+                       int64_t out_cols, float *out, int64_t out_ld, const cx_spmm_epilogue *epilogue,
+                       const std::uint32_t *rb_order, void *stream) {
     using namespace cx;
     clear_error();
     int rc = validate_bell(m, rhs, rhs_ld, out_cols, out, out_ld);
@@ -1094,7 +1125,8 @@ extern "C" int cx_bell_spmm_fwd_epilogue(const cx_bell_matrix *m, const void *rh
         && rhs_dtype != CELLERATOR_DTYPE_BF16)
         return fail(CX_STATUS_UNSUPPORTED, "Blocked-ELL rhs must be F32, F16 or BF16");
     if (m->rows == 0u) return CX_STATUS_SUCCESS;
-    const BellArgs a = make_args(m, rhs, rhs_ld, out, out_ld, ep);
+    BellArgs a = make_args(m, rhs, rhs_ld, out, out_ld, ep);
+    a.rb_order = rb_order;
     if (m->bits != 0u && m->block_size == 32u && rhs_dtype == CELLERATOR_DTYPE_F32 && out_cols % 64 == 0
         && m->row_stride_bytes % 4u == 0u && m->row_stride_bytes >= m->ell_cols * m->bits / 8u
         && static_cast<std::uint64_t>(m->row_stride_bytes) * 32u <= 0xffffffffull) {
@@ -1125,12 +1157,15 @@ extern "C" int cx_bell_spmm_fwd_epilogue(const cx_bell_matrix *m, const void *rh
 #undef CX_QBELL_W
         return check_launch("bell_spmm_quant_mfma");
     }
+    // the per-element kernel walks rows in matrix order (no row-block order)
     const std::uint64_t threads = static_cast<std::uint64_t>(m->rows) * kWave;
     hipLaunchKernelGGL(bell_spmm_generic, dim3(static_cast<unsigned>((threads + 255) / 256)),
                        dim3(256), 0, static_cast<hipStream_t>(stream), a, m->value_dtype,
                        rhs_dtype, m->bits, m->decode_policy, out_cols);
     return check_launch("bell_spmm_generic");
 }
+
+} // namespace
 
 extern "C" int cx_bell_pack_rhs(const uint16_t *rhs_bf16, int64_t rhs_ld, uint32_t k, uint32_t n,
                                 uint16_t *packed, void *stream) {

@@ -386,14 +386,27 @@ def bell_block_major(m: BellMatrix, stream=None) -> BellMatrix:
 
 
 def bell_spmm(m: BellMatrix, rhs: torch.Tensor, out: Optional[torch.Tensor] = None,
-              stream=None, epilogue: Optional[Epilogue] = None) -> torch.Tensor:
-    """Reference-semantics Blocked-ELL SpMM with a row-major rhs [cols, N]."""
+              stream=None, epilogue: Optional[Epilogue] = None,
+              row_block_order: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Reference-semantics Blocked-ELL SpMM with a row-major rhs [cols, N]. `row_block_order`
+    (int32 storage of a u32 permutation of the row blocks, e.g. BellGroups.order): the
+    quantized matrix-core forms take row blocks in that order (cx_bell_spmm_fwd_ordered);
+    same results."""
     _require_cuda(m.block_col_idx, rhs)
     n = rhs.shape[1]
     if out is None:
         out = torch.empty((m.rows, n), dtype=torch.float32, device=rhs.device)
     d = m.descriptor()
-    if epilogue is None:
+    if row_block_order is not None:
+        if epilogue is not None:
+            raise ValueError("a row-block order takes no epilogue")
+        _require_cuda(row_block_order)
+        if row_block_order.dtype != torch.int32 or row_block_order.numel() != (m.rows + m.block_size - 1) // m.block_size:
+            raise ValueError("row_block_order must hold one int32 entry per row block")
+        N.check("cx_bell_spmm_fwd_ordered", N.engine().cx_bell_spmm_fwd_ordered(
+            C.byref(d), rhs.data_ptr(), _DTYPE_CODE[rhs.dtype], rhs.stride(0), n, out.data_ptr(),
+            out.stride(0), row_block_order.data_ptr(), _stream(stream)))
+    elif epilogue is None:
         N.check("cx_bell_spmm_fwd", N.engine().cx_bell_spmm_fwd(
             C.byref(d), rhs.data_ptr(), _DTYPE_CODE[rhs.dtype], rhs.stride(0), n, out.data_ptr(),
             out.stride(0), _stream(stream)))

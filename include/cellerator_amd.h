@@ -537,6 +537,17 @@ int cx_bell_spmm_fwd(const cx_bell_matrix *a, const void *rhs, uint32_t rhs_dtyp
                      int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
                      void *stream);
 
+/* cx_bell_spmm_fwd with the row blocks taken in `row_block_order` (device, one u32 per row
+ * block, a permutation of them; entries past the row-block count are skipped): the
+ * quantized matrix-core forms give workgroup slot i (XCD-major) row block
+ * row_block_order[i]; other forms ignore it. Same results. An order from
+ * cx_bell_schedule_groups (every XCD's range about the same number of value blocks, a
+ * module's row blocks together) took C4's quantized projection 3.89 -> 3.80 ms. No
+ * counterpart in the reference; no epilogue. */
+int cx_bell_spmm_fwd_ordered(const cx_bell_matrix *a, const void *rhs, uint32_t rhs_dtype,
+                             int64_t rhs_ld, int64_t out_cols, float *out, int64_t out_ld,
+                             const uint32_t *row_block_order, void *stream);
+
 /* cx_bell_spmm_fwd with a fused epilogue (cx_spmm_epilogue; NULL = none), the
  * spmm_request alpha / beta / epilogue (operation.hh:136-164). */
 int cx_bell_spmm_fwd_epilogue(const cx_bell_matrix *a, const void *rhs, uint32_t rhs_dtype,

@@ -172,6 +172,25 @@ def test_grouped_rejects_groups_that_do_not_cover():
         bell_spmm_grouped(m, packed, bad, 64)
 
 
+def test_ordered_entry_rejects_a_null_order():
+    import ctypes
+
+    import torch
+
+    from cellerator_amd import BellMatrix
+    from cellerator_amd import _native as N
+    idx = torch.zeros((2, 1), dtype=torch.int32).cuda()
+    m = BellMatrix(64, 32, 32, 32, idx, bits=8, decode_policy=1, row_stride_bytes=32,
+                   packed_values=torch.zeros(64 * 32, dtype=torch.uint8).cuda(),
+                   column_scales=torch.ones(32).cuda(), column_offsets=torch.zeros(32).cuda())
+    w = torch.zeros((32, 64)).cuda()
+    out = torch.empty((64, 64)).cuda()
+    d = m.descriptor()
+    assert N.engine().cx_bell_spmm_fwd_ordered(ctypes.byref(d), w.data_ptr(), 2, 64, 64, out.data_ptr(), 64,
+                                               None, None) == 1
+    assert b"null row-block order" in N.engine().cx_last_error()
+
+
 def _quantized_bell_32(rng, rows, cols, width, bits, policy):
     """32x32 blocks, ragged last row block and block column, invalid slots anywhere."""
     rb, kb = (rows + 31) // 32, (cols + 31) // 32
@@ -224,8 +243,15 @@ def test_quantized_bell_matrix_cores(oracle, bits, policy, n):
     wide = torch.zeros((cols, n + 1), dtype=torch.float32, device="cuda")
     wide[:, 1:] = t(rhs)
     unaligned = bell_spmm(m, wide[:, 1:])  # 4 bytes past a 16-byte boundary, row stride n + 1
+    # row blocks taken in another order (cx_bell_spmm_fwd_ordered), both operand forms
+    rb = (rows + 31) // 32
+    order = t(np.random.default_rng(7).permutation(rb).astype(np.int32))
+    ordered = bell_spmm(m, t(rhs), row_block_order=order)
+    ordered_unaligned = bell_spmm(m, wide[:, 1:], row_block_order=order)
     torch.cuda.synchronize()
     check_against_referee(oracle, ref, mag, out.cpu().numpy())
     assert torch.equal(unaligned.view(torch.int32), out.view(torch.int32))
+    assert torch.equal(ordered.view(torch.int32), out.view(torch.int32))
+    assert torch.equal(ordered_unaligned.view(torch.int32), out.view(torch.int32))
     assert np.array_equal(hot.cpu().numpy().astype(np.float64), dec)
     check_against_referee(oracle, ref + bias[None, :].astype(np.float64), mag, ep_out.cpu().numpy())
