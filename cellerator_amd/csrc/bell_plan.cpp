@@ -114,8 +114,8 @@ extern "C" int cx_bell_schedule_groups(const uint32_t *block_col_idx, uint32_t r
                                        uint32_t *sched_order, uint32_t *sched_offsets,
                                        uint32_t *unit_count) {
     g_plan_error[0] = '\0';
-    if (sched_order == nullptr || sched_offsets == nullptr || unit_count == nullptr
-        || (row_blocks != 0u && (block_col_idx == nullptr || order == nullptr))
+    if (sched_offsets == nullptr || unit_count == nullptr
+        || (row_blocks != 0u && (sched_order == nullptr || block_col_idx == nullptr || order == nullptr))
         || (group_count != 0u && group_offsets == nullptr))
         return plan_fail(CX_STATUS_INVALID_ARGUMENT, "cx_bell_schedule_groups: null argument");
     const std::uint32_t grouped = group_count != 0u ? group_offsets[group_count] : 0u;

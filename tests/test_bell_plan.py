@@ -181,6 +181,13 @@ def test_schedule_balances_modules_of_unequal_length():
     assert together >= 0.8 * 8 * per
 
 
+def test_schedule_of_no_row_blocks():
+    idx = np.zeros((0, 4), np.uint32)
+    order, offs, gc, sc = plan(idx, 4)
+    s_order, s_offs, units = schedule(idx, order, offs, gc, sc)
+    assert units == 0 and s_offs[0] == 0
+
+
 def test_schedule_rejects_a_bad_plan():
     idx = patterned(np.random.default_rng(3), rb=40, slots=16)
     order, offs, gc, sc = plan(idx, 4)
