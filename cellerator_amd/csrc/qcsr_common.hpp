@@ -30,6 +30,10 @@ struct QcsrArgs {
     const std::int32_t *row_start;
     const float *acc_init;
     std::uint32_t first_part;
+    // The head may leave its sums as acc_parts partials (the genes split in order), acc_init
+    // + k * acc_part_stride floats; the row's sums start from their sum in that order.
+    std::uint32_t acc_parts;        // 0 or 1: one partial
+    std::uint64_t acc_part_stride;
     // Prepared tail stream (qcsr_spmm_stream only; built by qcsr_stream.hip): the row of
     // every (block, wave, layer, group) slot, the fill index, the entries in fill order, the
     // number of gene parts the stream covers (from first_part on) and its block count.

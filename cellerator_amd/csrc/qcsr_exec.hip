@@ -445,6 +445,7 @@ extern "C" int cx_qcsr_exec_workspace_for(uint32_t rows, uint32_t cols, uint32_t
     cx_qcsr_matrix m{};
     m.rows = rows;
     m.cols = cols;
+    m.bits = 8u;  // the code width is not known here: size for the words-form head, the larger need
     const std::uint32_t head = std::min(head_cols, cols / kExecPartGenes * kExecPartGenes);
     std::uint64_t hybrid = 0u;
     const int rc = cx_qcsr_hybrid_workspace(&m, head, out_cols, &hybrid);

@@ -77,7 +77,8 @@ struct HeadArgs {
     std::uint32_t rows_ld;
     std::uint32_t chunks;        // head / 32
     std::uint32_t panel_n;
-    float inv_scale;             // 2^-k
+    float inv_scale;
+    std::uint64_t part_stride;   // floats between the partials of two gene parts (grid.y > 1)             // 2^-k
 };
 
 template<int kBits>
@@ -249,10 +250,13 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void qcsr_head_dense(HeadArgs h
             for (int t = 0; t < 4; ++t) acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(L.aw[t], bl, acc[b][t], 0, 0, 0);
         }
     };
+    // gene part blockIdx.y of gridDim.y: chunks [c_begin, c_end), its own partial
+    const std::uint32_t c_begin = blockIdx.y * h.chunks / gridDim.y, c_end = (blockIdx.y + 1u) * h.chunks / gridDim.y;
+    float *partial = h.partial + blockIdx.y * h.part_stride;
     ChunkLoads<kBits> cur, nxt;
-    if (h.chunks != 0u) load_chunk<kBits>(cur, h, 0u, q, r16, row0);
-    for (std::uint32_t c = 0; c < h.chunks; ++c) {
-        if (c + 1u < h.chunks) load_chunk<kBits>(nxt, h, c + 1u, q, r16, row0);
+    if (c_begin < c_end) load_chunk<kBits>(cur, h, c_begin, q, r16, row0);
+    for (std::uint32_t c = c_begin; c < c_end; ++c) {
+        if (c + 1u < c_end) load_chunk<kBits>(nxt, h, c + 1u, q, r16, row0);
         chunk(cur);
         cur = nxt;
     }
@@ -263,7 +267,7 @@ __global__ __launch_bounds__(kHeadWaves * kWave) void qcsr_head_dense(HeadArgs h
         if (row < h.rows) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                float *o = h.partial + static_cast<std::uint64_t>(row) * 64u + t * 16 + 4 * q;
+                float *o = partial + static_cast<std::uint64_t>(row) * 64u + t * 16 + 4 * q;
                 *reinterpret_cast<float4 *>(o) = make_float4(acc[b][t][0] * h.inv_scale, acc[b][t][1] * h.inv_scale,
                                                              acc[b][t][2] * h.inv_scale, acc[b][t][3] * h.inv_scale);
             }
@@ -837,6 +841,23 @@ LayoutSizes layout_sizes(const cx_qcsr_matrix *m, std::uint32_t head) {
 }
 
 // Launches the dense head kernel for one 64-column block.
+// Gene parts of the words-form head: its waves cover 64 rows each, so a matrix with fewer
+// than four such waves per SIMD splits the head's genes into up to three parts, one partial
+// each (summed in order by the tail), to give every SIMD several waves. The table form, and
+// any head of larger matrices, runs in one part.
+std::uint32_t head_parts(std::uint32_t form, std::uint32_t rows_ld, std::uint32_t head_cols) {
+    if (form != CX_HEAD_FORM_WORDS || head_cols == 0u) return 1u;
+    const std::uint64_t waves = rows_ld / static_cast<std::uint64_t>(kRowsPerWave);
+    const std::uint64_t simds = 4ull * blocks_per_round();
+    if (waves == 0u || waves >= 4u * simds) return 1u;
+    const std::uint64_t want = (4u * simds + waves - 1u) / waves;
+    return static_cast<std::uint32_t>(std::min<std::uint64_t>({want, 3u, head_cols / 32u}));
+}
+
+std::uint64_t partial_stride_floats(std::uint32_t rows) {
+    return align256(static_cast<std::uint64_t>(rows) * 64u * 4u) / 4u;
+}
+
 int launch_head(const cx_qcsr_hybrid_layout &L, const std::uint16_t *panel, std::uint32_t panel_n, float *partial,
                 hipStream_t stream) {
     if (L.head_form == CX_HEAD_FORM_TABLE) {
@@ -865,7 +886,8 @@ int launch_head(const cx_qcsr_hybrid_layout &L, const std::uint16_t *panel, std:
     h.chunks = L.head_cols / 32u;
     h.panel_n = panel_n;
     h.inv_scale = std::ldexp(1.0f, -L.scale_exp);
-    const dim3 grid(L.rows_ld / kHeadRows), block(kHeadWaves * kWave);
+    h.part_stride = partial_stride_floats(L.rows);
+    const dim3 grid(L.rows_ld / kHeadRows, head_parts(L.head_form, L.rows_ld, L.head_cols)), block(kHeadWaves * kWave);
 #define CX_HEAD(B, P) hipLaunchKernelGGL((qcsr_head_dense<B, P>), grid, block, 0, stream, h)
 #define CX_HEAD_POLICY(B)                                                                        \
     do {                                                                                         \
@@ -1060,7 +1082,8 @@ extern "C" int cx_qcsr_hybrid_workspace(const cx_qcsr_matrix *m, uint32_t head_c
         return fail(CX_STATUS_INVALID_ARGUMENT, "cx_qcsr_hybrid_workspace: null argument");
     if (out_cols <= 0 || out_cols % 64 != 0 || out_cols > 256)
         return fail(CX_STATUS_INVALID_SHAPE, "cx_qcsr_hybrid_workspace: out_cols must be 64, 128, 192 or 256");
-    const std::uint64_t partial = align256(static_cast<std::uint64_t>(m->rows) * 64u * 4u);
+    const std::uint64_t partial = partial_stride_floats(m->rows) * 4u
+        * head_parts(head_form(m), layout_sizes(m, head_cols).rows_ld, head_cols);
     const std::uint64_t panel = align256(static_cast<std::uint64_t>(head_cols) * static_cast<std::uint64_t>(out_cols) * 2u);
     *bytes = partial + panel;
     return CX_STATUS_SUCCESS;
@@ -1171,8 +1194,9 @@ int launch_hybrid(const cx_qcsr_matrix &mm, const cx_qcsr_hybrid_layout &L, cons
         return CX_STATUS_SUCCESS;
     }
     auto *partial = static_cast<float *>(workspace);
+    const std::uint32_t hparts = head_parts(L.head_form, L.rows_ld, L.head_cols);
     auto *panel = reinterpret_cast<std::uint16_t *>(static_cast<unsigned char *>(workspace)
-                                                    + align256(static_cast<std::uint64_t>(m->rows) * 256u));
+                                                    + partial_stride_floats(m->rows) * 4u * hparts);
     // the head genes' weights as the matrix-core operand panel [H/32][out_cols][32]
     rc = pack_panel_columns(static_cast<const std::uint16_t *>(rhs), rhs_ld, L.head_cols,
                             static_cast<std::uint32_t>(out_cols), panel, s);
@@ -1187,6 +1211,8 @@ int launch_hybrid(const cx_qcsr_matrix &mm, const cx_qcsr_hybrid_layout &L, cons
         if (b.ep.initial != nullptr) b.ep.initial += c0;
         b.row_start = L.head_end;
         b.acc_init = partial;
+        b.acc_parts = hparts;
+        b.acc_part_stride = partial_stride_floats(m->rows);
         b.first_part = L.head_cols / kHeadAlign;
         rc = tail(b);
         if (rc != CX_STATUS_SUCCESS) return rc;

@@ -101,6 +101,20 @@ __device__ __forceinline__ void fma8(float (&p)[8], float x, uint4 w) {
 // Plain per-row path for rows the part walk could not finish: lane c accumulates column
 // c over the row's entries in storage order; columns outside [0, cols) contribute nothing.
 // In the hybrid tail the walk starts at row_start[row] from the head's partial sum.
+// The head's sums of `row`, columns 8j .. 8j + 7: its partials added in order.
+__device__ __forceinline__ void head_init8(const QcsrArgs &a, std::uint32_t row, int j, float *acc) {
+    const float *p = a.acc_init + static_cast<std::int64_t>(row) * 64 + 8 * j;
+    float4 i0 = reinterpret_cast<const float4 *>(p)[0], i1 = reinterpret_cast<const float4 *>(p)[1];
+    for (std::uint32_t k = 1; k < a.acc_parts; ++k) {
+        const float4 *q = reinterpret_cast<const float4 *>(p + k * a.acc_part_stride);
+        const float4 u0 = q[0], u1 = q[1];
+        i0.x += u0.x; i0.y += u0.y; i0.z += u0.z; i0.w += u0.w;
+        i1.x += u1.x; i1.y += u1.y; i1.z += u1.z; i1.w += u1.w;
+    }
+    acc[0] = i0.x; acc[1] = i0.y; acc[2] = i0.z; acc[3] = i0.w;
+    acc[4] = i1.x; acc[5] = i1.y; acc[6] = i1.z; acc[7] = i1.w;
+}
+
 template<int kBits, int kPolicy>
 __device__ float row_fallback(const QcsrArgs &a, std::uint32_t row, int lane) {
     const std::int64_t begin = a.row_ptr[row], end = a.row_ptr[row + 1];
@@ -108,7 +122,10 @@ __device__ float row_fallback(const QcsrArgs &a, std::uint32_t row, int lane) {
     const float row_offset = kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET && a.row_offsets != nullptr
         ? a.row_offsets[row] : 0.0f;
     const std::uint16_t *rhs = static_cast<const std::uint16_t *>(a.rhs);
-    float acc = a.acc_init != nullptr ? a.acc_init[static_cast<std::int64_t>(row) * 64 + lane] : 0.0f;
+    float acc = 0.0f;
+    if (a.acc_init != nullptr)
+        for (std::uint32_t k = 0; k < (a.acc_parts > 1u ? a.acc_parts : 1u); ++k)
+            acc += a.acc_init[static_cast<std::int64_t>(row) * 64 + lane + k * a.acc_part_stride];
     const std::int64_t start = a.row_start != nullptr ? a.row_start[row] : begin;
     for (std::int64_t i = start; i < end; ++i) {
         const std::uint32_t col = static_cast<std::uint32_t>(a.col_idx[i]);
@@ -375,10 +392,7 @@ __global__ __launch_bounds__(kWaves * kWave) void qcsr_spmm_groups(QcsrArgs a) {
                 roff[l] = a.row_offsets != nullptr ? a.row_offsets[row] : 0.0f;
         }
         if (a.acc_init != nullptr && row != kNoRow) {
-            const float4 *init = reinterpret_cast<const float4 *>(a.acc_init + static_cast<std::int64_t>(row) * 64 + 8 * j);
-            const float4 i0 = init[0], i1 = init[1];
-            acc[l][0] = i0.x; acc[l][1] = i0.y; acc[l][2] = i0.z; acc[l][3] = i0.w;
-            acc[l][4] = i1.x; acc[l][5] = i1.y; acc[l][6] = i1.z; acc[l][7] = i1.w;
+            head_init8(a, row, j, acc[l]);
         } else {
 #pragma unroll
             for (int k = 0; k < 8; ++k) acc[l][k] = 0.0f;
@@ -610,10 +624,7 @@ __global__ __launch_bounds__(kStreamWaves * kWave) void qcsr_spmm_stream(QcsrArg
         if constexpr (kPolicy == CX_DECODE_COLUMN_SCALE_ROW_OFFSET)
             roff[l] = row != kNoRow && a.row_offsets != nullptr ? a.row_offsets[row] : 0.0f;
         if (a.acc_init != nullptr && row != kNoRow) {
-            const float4 *init = reinterpret_cast<const float4 *>(a.acc_init + static_cast<std::int64_t>(row) * 64 + 8 * j);
-            const float4 i0 = init[0], i1 = init[1];
-            acc[l][0] = i0.x; acc[l][1] = i0.y; acc[l][2] = i0.z; acc[l][3] = i0.w;
-            acc[l][4] = i1.x; acc[l][5] = i1.y; acc[l][6] = i1.z; acc[l][7] = i1.w;
+            head_init8(a, row, j, acc[l]);
         } else {
 #pragma unroll
             for (int k = 0; k < 8; ++k) acc[l][k] = 0.0f;

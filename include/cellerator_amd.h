@@ -1643,8 +1643,11 @@ int cx_qcsr_hybrid_layout_bytes(const cx_qcsr_matrix *a, uint32_t head_cols, uin
  * (UNSUPPORTED). */
 int cx_qcsr_hybrid_prepare(const cx_qcsr_matrix *a, uint32_t head_cols, void *storage, uint64_t storage_bytes,
                            cx_qcsr_hybrid_layout *layout, void *stream);
-/* Workspace bytes of cx_qcsr_spmm_fwd_hybrid: the head's sums (rows x 64 fp32) and the head
- * genes' weight panel ([H/32][out_cols][32] F16), each 256-byte aligned. */
+/* Workspace bytes of cx_qcsr_spmm_fwd_hybrid: the head's sums (rows x 64 fp32, 256-byte
+ * aligned, once per gene part of the head: a words-form head over fewer rows than four
+ * 64-row waves per SIMD of the current device splits its genes into up to three parts) and
+ * the head genes' weight panel ([H/32][out_cols][32] F16, 256-byte aligned). Query it on
+ * the device that runs the product. */
 int cx_qcsr_hybrid_workspace(const cx_qcsr_matrix *a, uint32_t head_cols, int64_t out_cols, uint64_t *bytes);
 /* Y = act(alpha * (A . W) + beta * C + bias) for A in execution order with a.flags including
  * CX_QCSR_COLUMNS_SORTED, codes of 1/2/4/8 bits (any decode policy), F16 W [cols x out_cols]
@@ -1761,7 +1764,8 @@ typedef struct cx_qcsr_exec_info {
 int cx_qcsr_exec_prepare(const cx_qcsr_matrix *a, uint32_t head_cols, cx_qcsr_exec_projection **out, void *stream);
 int cx_qcsr_exec_query(const cx_qcsr_exec_projection *p, cx_qcsr_exec_info *info);
 int cx_qcsr_exec_workspace_bytes(const cx_qcsr_exec_projection *p, int64_t out_cols, uint64_t *bytes);
-/* The same from the shape alone, before a projection exists (head_cols as passed to prepare). */
+/* The same from the shape alone, before a projection exists (head_cols as passed to prepare);
+ * sized for the larger of the head forms, since the code width is not given. */
 int cx_qcsr_exec_workspace_for(uint32_t rows, uint32_t cols, uint32_t head_cols, int64_t out_cols, uint64_t *bytes);
 /* Y = act(alpha * (A . W) + beta * C + bias) with canonical W; out_cols 64..256 by 64, Y 16-byte
  * aligned with a 16-byte multiple row stride; deterministic. */
