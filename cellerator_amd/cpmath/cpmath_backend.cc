@@ -960,11 +960,13 @@ namespace {
 // row-group kernel at 35% of the non-packed fp32 VALU peak (C3: 6.99 ms for 2*nnz*N flops);
 // the execution-order path at 74% of it (C3: 3.31 ms, head on the matrix cores plus the
 // tail stream) after a preparation of about 0.028 ns per stored entry (C3: 41 ms); the
-// Blocked-ELL grouped matrix-core kernel at about 35% of HBM; CP-BP at about 32% of HBM).
+// Blocked-ELL grouped matrix-core kernel on its launch schedule at about 47% of HBM (C4:
+// 0.52 ms); the CP-BP reduction at about 48% of HBM from the descriptors (C5: 1.2 ms), 55%
+// with prepared entry rows).
 constexpr double kHbmBytesPerNs = 8000.0;         // 8 TB/s
 constexpr double kValuFlopsPerNs = 78600.0;        // fp32, non-packed
 constexpr double kMfmaFlopsPerNs = 2500000.0;      // bf16 dense
-constexpr double kQcsrEfficiency = 0.35, kBellEfficiency = 0.35, kCpbpEfficiency = 0.32;
+constexpr double kQcsrEfficiency = 0.35, kBellEfficiency = 0.47, kCpbpEfficiency = 0.48;
 constexpr double kQcsrExecEfficiency = 0.74;
 constexpr double kQcsrExecPrepareNsPerEntry = 0.028;
 constexpr double kLaunchNs = 4000.0;               // launch and synchronization overhead
