@@ -9,14 +9,17 @@
 // descriptors): with module-sparse cells a 64-row tile carries ~790 descriptors of ~6 rows
 // each, so a lane-per-row wave is ~9% busy.
 //
-// Entry-batch mapping. One wave owns one tile at a time (tiles strided over the grid); 16
-// waves share a workgroup and the plan staged once in LDS (permuted weights
-// wp[f] = w[perm[f]], block starts). A tile's row-block entries are contiguous, and so are
-// their values. The wave takes the entries in batches of up to 64 (at most 512 values):
+// Entry-batch mapping. One wave owns one tile at a time (each workgroup's tiles taken from
+// an LDS queue); 16 waves share a workgroup and the plan staged once in LDS (permuted
+// weights wp[f] = w[perm[f]], block starts). A tile's row-block entries are contiguous, and
+// so are their values. The wave takes the entries in batches of up to 64 (at most 512
+// values):
 //   1. lane j holds entry j (value offset, gene mask) and lane k descriptor k (first entry,
 //      cell mask, block id), loaded coalesced;
 //   2. each entry finds its descriptor (descriptor starts scattered into LDS slots, then a
-//      wave max-scan) and its row (the rank-th set bit of the descriptor's cell mask);
+//      wave max-scan) and its row (the rank-th set bit of the descriptor's cell mask) -- or,
+//      with entry rows prepared once per tile structure (cx_cpbp_entry_rows), reads its row
+//      and block start from one word per entry instead;
 //   3. the batch's values, loaded coalesced, are staged in LDS; each entry lane sums
 //      value * wp[block start + bit] over its own values in a register (fp32 FMA) and adds
 //      the sum to its row's accumulator in LDS: an integer atomic numbers the batch's
