@@ -348,8 +348,8 @@ def bench_bell_quantized(args, torch, cfg) -> dict:
                    "valid_blocks": valid_blocks, "n_out": n_out, "seed": hex(cfg.seed)},
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": tflops / MFMA_FP32_PEAK_TFLOPS, "traffic": load_traffic(cfg.name + " 8-bit codes"),
-                     "kernel": "bell_spmm_quant_lds<8, per-gene affine> (cx_bell_spmm_fwd_ordered: fp32 matrix "
-                               "cores, W tiles and metadata through LDS, row blocks in the launch schedule's order)",
+                     "kernel": "bell_spmm_quant_lds<8, per-gene affine, 1 buffer> (cx_bell_spmm_fwd_ordered: fp32 "
+                               "matrix cores, W tiles and metadata through LDS, row blocks in the launch schedule's order)",
                      "kernel_ms_mean": kern_ms, "kernel_ms_median": statistics.median(ev),
                      "flops": flops, "algorithmic_bytes": alg_bytes, "hbm_gbs": achieved,
                      "hbm_frac": achieved / HBM_PEAK_GBS},
