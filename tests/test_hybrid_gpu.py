@@ -380,3 +380,39 @@ def test_head_refuses_values_it_cannot_carry(oracle):
     f = _rebuild(oracle, rng, dict(fr, row_offsets=r_), fr["row_ptr"], fr["col_idx"])
     with pytest.raises(N.EngineError, match="offset of row 17 "):
         hybrid_prepare(sorted_dev(f), 1024)
+
+
+def test_words_head_gene_parts(oracle, monkeypatch):
+    """A words-form head over fewer rows than four 64-row waves per SIMD splits its genes into
+    up to three parts, one partial each (the workspace holds them all), summed in order by the
+    tail; with the device counted as one CU (CX_BLOCKS_PER_ROUND=1) the same matrix runs in
+    one part. Both agree with the referee; repeats are bitwise equal."""
+    import torch
+
+    from cellerator_amd import qcsr_pack_gene_affine
+    from cellerator_amd.exec_order import hybrid_prepare, hybrid_spmm, pack_rows
+    from cellerator_amd.synth import C2, dense_normal, generate_qcsr
+    m = generate_qcsr(C2.scaled(2 * 256 + 11))
+    w = dense_normal((m.cols, 64), 0.02, torch.float16, seed=9)
+    mx, order = _exec(qcsr_pack_gene_affine(m), 3072)
+    wx = pack_rows(order, w)
+    partial = (m.rows * 256 + 255) // 256 * 256
+    panel = (3072 * 64 * 2 + 255) // 256 * 256
+    h = qcsr_to_host(m)
+    ref, mag = oracle.qcsr_spmm_referee(8, 1, m.rows, m.cols, h["row_ptr"], h["packed_row_ptr"], h["col_idx"],
+                                        h["packed"], h["scales"], h["offsets"], None, w.cpu().numpy())
+    outs = []
+    for units, parts in ((None, 3), ("1", 1)):
+        if units is not None:
+            monkeypatch.setenv("CX_BLOCKS_PER_ROUND", units)
+        p = hybrid_prepare(mx, 3072)
+        assert p.workspace(64, "cuda").numel() == parts * partial + panel
+        y = hybrid_spmm(p, wx)
+        y2 = hybrid_spmm(p, wx)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int32), y2.view(torch.int32))
+        check_against_referee(oracle, ref, mag, y.cpu().numpy())
+        outs.append(y)
+    # the two split the head's sum differently: they differ by fp32 reordering only
+    diff = np.abs(outs[0].cpu().numpy().astype(np.float64) - outs[1].cpu().numpy())
+    assert np.all(diff <= 2.0 ** -20 * mag)
